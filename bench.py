@@ -1,0 +1,217 @@
+#!/usr/bin/env python3
+"""Decode benchmark of the MI355X GAJE path on one GPU.
+
+Workload (the metric's configuration): a random-init Qwen2-0.5B-shaped model
+(hidden 896, 24 layers, 14/2 heads, ffn 4864, vocab 151936, Q4_0 body, f32
+token_embd / lm_head, QKV bias), batch-1 greedy decode.  One step = the
+fixed-length argmax -> forward loop of benchmarks/performance/gaje_flat_benchmark.py:94-96
+for 256 tokens from the state after a 512-token prompt (KV cache 512 -> 768),
+K-WTA off as in benchmarks/performance/bench_decode.py:158-159.  The prompt is
+prefilled once before timing; every step rewinds the cache to the prompt.
+
+Also reported on the same run:
+  - per-stage device time of the exact kernels of the decode step (HIP events
+    on the model stream) and the roofline of the dominant one;
+  - the single Q4_0 matvec at K=896, N=4864 (the C0 shape), cycling 128 weight
+    copies (348 MB, beyond the 256 MB last-level cache) and hot in cache;
+  - the CPU oracle (AVX2 restatement of the reference kernels) on the host cores.
+
+Prints ONE JSON line on stdout; progress goes to stderr.
+"""
+import argparse
+import json
+import os
+import sys
+import tempfile
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(REPO, "gaje-semantic-compression_amd")
+for _p in (REPO, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import numpy as np  # noqa: E402
+
+HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, published
+METRIC = "Q4_0 GEMV HBM GB/s (% of peak); decode tok/s, Qwen2-0.5B shape, batch 1"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def model_path(preset: str, seed: int, d: str) -> str:
+    from gaje_hip import synth
+    path = os.path.join(d, f"gaje_{preset}_s{seed}.flat")
+    if not os.path.exists(path):
+        t = time.perf_counter()
+        synth.write_flat(path + ".tmp", preset=preset, seed=seed)
+        os.replace(path + ".tmp", path)
+        log(f"[bench] wrote {path} ({os.path.getsize(path) / 1e9:.2f} GB) in {time.perf_counter() - t:.1f}s")
+    return path
+
+
+def q4_gemv_c0(iters: int = 1024):
+    """The C0 matvec: Q4_0 K=896 N=4864, cold (128 copies) and hot (1 copy)."""
+    from gaje_hip import ops, synth
+    n, k = 4864, 896
+    blocks = synth.q4_0_tensor(0, "c0.gemv", n, k)
+    stride = (blocks.nbytes + 255) // 256 * 256
+    copies = 128
+    w = ops.DeviceBuffer(stride * copies)
+    host = np.zeros(stride * copies, dtype=np.uint8)
+    for c in range(copies):
+        host[c * stride:c * stride + blocks.nbytes] = blocks
+    w.write(host)
+    x = ops.DeviceBuffer.from_array(synth.normal(0, "c0.x", k))
+    y = ops.DeviceBuffer(n * 4)
+    algo = blocks.nbytes + k * 4 + n * 4  # weights + x + y
+    cold_ms = ops.bench_gemv(1, w, stride, copies, x, y, n, k, iters)
+    hot_ms = ops.bench_gemv(1, w, stride, 1, x, y, n, k, iters)
+    w.close()
+    return dict(shape="N=4864 K=896 (Q4_0Block 20 B / 32 weights)", algorithmic_bytes=algo,
+                cold_us=cold_ms * 1e3, cold_GBps=algo / (cold_ms * 1e-3) / 1e9,
+                cold_frac=algo / (cold_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
+                hot_us=hot_ms * 1e3, hot_GBps=algo / (hot_ms * 1e-3) / 1e9,
+                copies=copies, note="cold = 128 distinct copies cycled (348 MB > 256 MB LLC), "
+                                    "graph-replayed back-to-back launches; hot = one copy")
+
+
+def cpu_baseline(path: str, prompt, seconds: float, threads: int):
+    """The oracle's decode on the host cores: greedy chain from the prompt's first token."""
+    from oracle import oracle as O
+    O.set_threads(threads)
+    r = O.load_genomic(path)
+    r.set_k_wta_ratio(0.0)
+    tok = int(prompt[0])
+    r.forward_core(tok, True)  # first token also pages the weights in (untimed)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        logits = r.forward_core(tok, False)
+        tok = O.argmax_first(logits)
+        n += 1
+        el = time.perf_counter() - t0
+        if (el >= seconds and n >= 4) or n >= 512:
+            break
+    return dict(value=n / el, unit="tok/s", cores=O.get_threads(), kind="port",
+                sample=f"{n} greedy decode tokens (ctx 2..{n + 1}) of the same model on the host, "
+                       f"{O.get_threads()} threads; AVX2 restatement of the reference kernels")
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--preset", default="qwen2-0.5b")
+    ap.add_argument("--prompt", type=int, default=512)
+    ap.add_argument("--gen", type=int, default=256)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--model-dir", default=None)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-stages", action="store_true")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build runs on exactly one GPU (asked for {max(args.gpus, world)}); "
+              "the decode path is not sharded across GPUs", file=sys.stderr)
+        sys.exit(2)
+
+    import gaje_hip
+    from gaje_hip import ops
+    if ops.device_count() < 1:
+        print("bench.py: no HIP device", file=sys.stderr)
+        sys.exit(1)
+    log(f"[bench] device: {ops.device_name(0)}")
+
+    d = args.model_dir or tempfile.gettempdir()
+    path = model_path(args.preset, args.seed, d)
+    t = time.perf_counter()
+    g = gaje_hip.load_genomic_auto(path)
+    log(f"[bench] loaded {g.info['weight_bytes'] / 1e9:.2f} GB of weights into HBM in {time.perf_counter() - t:.1f}s")
+    g.set_k_wta_ratio(0.0)
+    vocab = g.vocab_size
+    prompt = np.random.default_rng(args.seed).integers(0, vocab, args.prompt).astype(np.uint32)
+    g.reserve(args.prompt + args.gen + 1)
+    g.clear_cache_py()
+    t = time.perf_counter()
+    g.prefill(prompt)
+    log(f"[bench] prefilled {args.prompt} tokens token-by-token in {time.perf_counter() - t:.2f}s")
+
+    def step():
+        g.truncate_cache(args.prompt)
+        return g.decode_greedy(int(prompt[-1]), args.gen)
+
+    for _ in range(args.warmup):
+        step()
+    ops.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        toks = step()
+    ops.synchronize()
+    el = time.perf_counter() - t0
+    tok_s = args.gen * args.steps / el
+    log(f"[bench] decode: {tok_s:.1f} tok/s ({el / args.steps * 1e3:.1f} ms per {args.gen}-token step)")
+
+    stages = {}
+    roofline = None
+    if not args.no_stages:
+        counts = {"qkv": g.info["n_blocks"], "attention": g.info["n_blocks"], "o": g.info["n_blocks"],
+                  "gate_up": g.info["n_blocks"], "down": g.info["n_blocks"], "lm_head": 1}
+        g.truncate_cache(args.prompt + args.gen - 1)  # time at the last step's context
+        for s in ("qkv", "attention", "o", "gate_up", "down", "lm_head", "token"):
+            ms, nbytes = g.time_stage(s, layer=0, iters=200 if s != "token" else 50)
+            gbps = nbytes / (ms * 1e-3) / 1e9
+            stages[s] = dict(us=round(ms * 1e3, 3), bytes=int(nbytes), GBps=round(gbps, 1),
+                             frac=round(gbps / HBM_PEAK_GBPS, 4))
+            if s in counts:
+                stages[s]["per_token_us"] = round(ms * 1e3 * counts[s], 2)
+            log(f"[bench] stage {s:9s}: {ms * 1e3:8.2f} us  {gbps:8.1f} GB/s")
+        dom = max(counts, key=lambda s: stages[s]["per_token_us"])
+        ach = stages[dom]["GBps"]
+        roofline = dict(kernel=dom, bound="hbm", achieved=ach, peak=HBM_PEAK_GBPS, unit="GB/s",
+                        frac=round(ach / HBM_PEAK_GBPS, 4), traffic=None,
+                        bytes_per_launch=stages[dom]["bytes"], us_per_launch=stages[dom]["us"])
+
+    gemv = q4_gemv_c0()
+    log(f"[bench] Q4_0 GEMV C0: cold {gemv['cold_us']:.2f} us = {gemv['cold_GBps']:.0f} GB/s "
+        f"({100 * gemv['cold_frac']:.1f}% of HBM peak); hot {gemv['hot_us']:.2f} us")
+
+    cpu = None
+    if not args.no_cpu:
+        threads = min(16, os.cpu_count() or 1)
+        cpu = cpu_baseline(path, prompt, args.cpu_seconds, threads)
+        log(f"[bench] cpu oracle: {cpu['value']:.2f} tok/s on {cpu['cores']} threads")
+    g.close()
+
+    out = {
+        "metric": METRIC,
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(el / args.steps * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (random-init weights, uniform random prompt ids)",
+        "config": {"workload": f"{args.preset}-shape batch-1 greedy decode: {args.prompt}-token prompt, "
+                               f"then {args.gen} tokens (KV cache {args.prompt}->{args.prompt + args.gen}), "
+                               "Q4_0 body, f32 embed/lm_head, K-WTA off",
+                   "prompt": args.prompt, "gen": args.gen, "batch": 1, "preset": args.preset},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "q4_0_gemv": gemv,
+        "stages": stages,
+        "last_tokens": [int(t) for t in toks[-4:]],
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,299 @@
+// C ABI: error reporting, runtime helpers and the operator entry points.
+// Model entry points live in model.cpp, the synthetic writer in synth.cpp.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "common.h"
+#include "kernels.h"
+
+namespace gaje {
+
+namespace {
+thread_local std::string g_last_error;
+}
+
+int set_error(int code, const char *fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+void clear_error() { g_last_error.clear(); }
+
+}  // namespace gaje
+
+using namespace gaje;
+
+namespace {
+
+hipStream_t as_stream(void *s) { return (hipStream_t)s; }
+
+GemvParams plain_gemv(int fmt, const void *w, const float *x, const float *bias, int64_t bias_len, float *y, int64_t n,
+                      int64_t k) {
+    GemvParams p;
+    memset(&p, 0, sizeof p);
+    p.w = (const uint8_t *)w;
+    p.fmt = fmt;
+    p.nb = (int32_t)(k / 32);
+    p.rows_valid = n;
+    p.N = n;
+    p.K = k;
+    p.x = x;
+    p.h_scale = 1.0f;
+    p.bias = bias;
+    p.bias_len = bias ? bias_len : 0;
+    p.mode = MODE_STORE;
+    p.y = y;
+    p.st_in = p.st_norm = p.st_a = p.st_b = ST_NONE;
+    return p;
+}
+
+int check_dims(int64_t n, int64_t k) {
+    if (n < 0 || k <= 0) return set_error(GAJE_ERR_INVALID_ARG, "invalid shape n=%lld k=%lld", (long long)n, (long long)k);
+    if (k > (int64_t)1 << 30 || n > (int64_t)1 << 40) return set_error(GAJE_ERR_INVALID_ARG, "shape too large");
+    return GAJE_OK;
+}
+
+}  // namespace
+
+extern "C" const char *gaje_hip_last_error(void) { return g_last_error.c_str(); }
+
+// ------------------------------------------------------------------ runtime --
+
+extern "C" int gaje_hip_device_count(int *count) {
+    if (!count) return set_error(GAJE_ERR_INVALID_ARG, "null argument");
+    *count = 0;
+    hipError_t e = hipGetDeviceCount(count);
+    if (e == hipErrorNoDevice) {
+        *count = 0;
+        return GAJE_OK;
+    }
+    GAJE_HIP_CHECK(e);
+    return GAJE_OK;
+}
+
+extern "C" int gaje_hip_set_device(int device) {
+    GAJE_HIP_CHECK(hipSetDevice(device));
+    return GAJE_OK;
+}
+
+extern "C" int gaje_hip_device_name(int device, char *buf, size_t buflen) {
+    if (!buf || buflen == 0) return set_error(GAJE_ERR_INVALID_ARG, "null buffer");
+    hipDeviceProp_t prop;
+    GAJE_HIP_CHECK(hipGetDeviceProperties(&prop, device));
+    snprintf(buf, buflen, "%s (%s, %d CUs)", prop.name, prop.gcnArchName, prop.multiProcessorCount);
+    return GAJE_OK;
+}
+
+extern "C" int gaje_hip_malloc(void **ptr, size_t bytes) {
+    if (!ptr) return set_error(GAJE_ERR_INVALID_ARG, "null argument");
+    *ptr = nullptr;
+    if (bytes == 0) return GAJE_OK;
+    GAJE_HIP_CHECK(hipMalloc(ptr, bytes));
+    return GAJE_OK;
+}
+
+extern "C" int gaje_hip_free(void *ptr) {
+    if (ptr) GAJE_HIP_CHECK(hipFree(ptr));
+    return GAJE_OK;
+}
+
+extern "C" int gaje_hip_memcpy_h2d(void *dst, const void *src, size_t bytes) {
+    if (bytes) GAJE_HIP_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+    return GAJE_OK;
+}
+
+extern "C" int gaje_hip_memcpy_d2h(void *dst, const void *src, size_t bytes) {
+    if (bytes) GAJE_HIP_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+    return GAJE_OK;
+}
+
+extern "C" int gaje_hip_memcpy_d2d(void *dst, const void *src, size_t bytes) {
+    if (bytes) GAJE_HIP_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToDevice));
+    return GAJE_OK;
+}
+
+extern "C" int gaje_hip_memset(void *dst, int value, size_t bytes) {
+    if (bytes) GAJE_HIP_CHECK(hipMemset(dst, value, bytes));
+    return GAJE_OK;
+}
+
+extern "C" int gaje_hip_device_synchronize(void) {
+    GAJE_HIP_CHECK(hipDeviceSynchronize());
+    return GAJE_OK;
+}
+
+extern "C" int gaje_hip_stream_create(void **stream) {
+    if (!stream) return set_error(GAJE_ERR_INVALID_ARG, "null argument");
+    hipStream_t s;
+    GAJE_HIP_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    *stream = (void *)s;
+    return GAJE_OK;
+}
+
+extern "C" int gaje_hip_stream_destroy(void *stream) {
+    if (stream) GAJE_HIP_CHECK(hipStreamDestroy(as_stream(stream)));
+    return GAJE_OK;
+}
+
+extern "C" int gaje_hip_stream_synchronize(void *stream) {
+    GAJE_HIP_CHECK(hipStreamSynchronize(as_stream(stream)));
+    return GAJE_OK;
+}
+
+extern "C" int gaje_hip_event_create(void **event) {
+    if (!event) return set_error(GAJE_ERR_INVALID_ARG, "null argument");
+    hipEvent_t e;
+    GAJE_HIP_CHECK(hipEventCreate(&e));
+    *event = (void *)e;
+    return GAJE_OK;
+}
+
+extern "C" int gaje_hip_event_destroy(void *event) {
+    if (event) GAJE_HIP_CHECK(hipEventDestroy((hipEvent_t)event));
+    return GAJE_OK;
+}
+
+extern "C" int gaje_hip_event_record(void *event, void *stream) {
+    GAJE_HIP_CHECK(hipEventRecord((hipEvent_t)event, as_stream(stream)));
+    return GAJE_OK;
+}
+
+extern "C" int gaje_hip_event_synchronize(void *event) {
+    GAJE_HIP_CHECK(hipEventSynchronize((hipEvent_t)event));
+    return GAJE_OK;
+}
+
+extern "C" int gaje_hip_event_elapsed_ms(void *start, void *stop, float *ms) {
+    if (!ms) return set_error(GAJE_ERR_INVALID_ARG, "null argument");
+    GAJE_HIP_CHECK(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop));
+    return GAJE_OK;
+}
+
+// ------------------------------------------------------------- operators --
+
+extern "C" int gaje_hip_q4_0_gemv(const void *blocks, const float *x, const float *bias, int64_t bias_len, float *y,
+                                  int64_t n, int64_t k, void *stream) {
+    GAJE_TRY(check_dims(n, k));
+    return launch_gemv(plain_gemv(FMT_Q4_0, blocks, x, bias, bias_len, y, n, k), as_stream(stream));
+}
+
+extern "C" int gaje_hip_q4_0_gemm(const void *blocks, const float *X, const float *bias, int64_t bias_len, float *Y,
+                                  int64_t m, int64_t n, int64_t k, void *stream) {
+    GAJE_TRY(check_dims(n, k));
+    if (m < 0 || (m > 0 && (!X || !Y))) return set_error(GAJE_ERR_INVALID_ARG, "bad gemm arguments");
+    for (int64_t r = 0; r < m; ++r)
+        GAJE_TRY(launch_gemv(plain_gemv(FMT_Q4_0, blocks, X + r * k, bias, bias_len, Y + r * n, n, k), as_stream(stream)));
+    return GAJE_OK;
+}
+
+extern "C" int gaje_hip_lut4_gemv(const uint8_t *codes, const float *lut, int64_t lut_len, const float *x,
+                                  const float *bias, int64_t bias_len, float *y, int64_t n, int64_t k, void *stream) {
+    GAJE_TRY(check_dims(n, k));
+    GemvParams p = plain_gemv(FMT_LUT4, codes, x, bias, bias_len, y, n, k);
+    const int64_t per_row = (k / 32) * 16;
+    p.lut = lut;
+    if (lut_len == 16) {
+        p.lut_block_stride = 0;
+        p.lut_rows_own = 0;
+    } else if (per_row > 0 && lut_len >= per_row) {
+        p.lut_block_stride = 16;
+        p.lut_rows_own = lut_len == per_row ? 0 : lut_len / per_row;
+    } else {
+        return set_error(GAJE_ERR_INVALID_ARG, "lut_len %lld is neither 16 nor >= k/32*16", (long long)lut_len);
+    }
+    return launch_gemv(p, as_stream(stream));
+}
+
+extern "C" int gaje_hip_f32_gemv(const float *w, const float *x, const float *bias, int64_t bias_len, float *y,
+                                 int64_t n, int64_t k, void *stream) {
+    GAJE_TRY(check_dims(n, k));
+    GemvParams p = plain_gemv(FMT_F32, w, x, bias, bias_len, y, n, k);
+    p.nontemporal = 1;
+    return launch_gemv(p, as_stream(stream));
+}
+
+extern "C" int gaje_hip_q4_0_dequant(const void *blocks, float *out, int64_t nblocks, void *stream) {
+    return launch_dequant_q4_0((const uint8_t *)blocks, out, nblocks, as_stream(stream));
+}
+
+extern "C" int gaje_hip_rmsnorm(const float *x, const float *w, float eps, float *y, int64_t n, void *stream) {
+    return launch_rmsnorm(x, w, eps, y, n, as_stream(stream));
+}
+
+extern "C" int gaje_hip_swiglu(const float *gate, const float *up, float *out, int64_t n, void *stream) {
+    return launch_swiglu(gate, up, out, n, as_stream(stream));
+}
+
+extern "C" int gaje_hip_kwta(float *scores, int64_t n, int64_t k, void *stream) {
+    return launch_kwta(scores, n, k, nullptr, as_stream(stream));
+}
+
+extern "C" int gaje_hip_argmax(const float *x, int64_t n, uint32_t *idx, void *stream) {
+    return launch_argmax(x, n, idx, as_stream(stream));
+}
+
+extern "C" int gaje_hip_bench_gemv(int format, const void *w_base, size_t copy_stride, const float *lut_base,
+                                   size_t lut_stride, int copies, const float *x, float *y, int64_t n, int64_t k,
+                                   int iters, float *avg_ms) {
+    clear_error();
+    GAJE_TRY(check_dims(n, k));
+    if (!avg_ms || copies <= 0 || iters <= 0 || !w_base || (format == FMT_LUT4 && !lut_base))
+        return set_error(GAJE_ERR_INVALID_ARG, "bad benchmark arguments");
+    if (format != FMT_F32 && format != FMT_Q4_0 && format != FMT_LUT4)
+        return set_error(GAJE_ERR_INVALID_ARG, "unknown format %d", format);
+    hipStream_t s;
+    GAJE_HIP_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    auto launch_all = [&]() -> int {
+        for (int c = 0; c < copies; ++c) {
+            GemvParams p = plain_gemv(format, (const uint8_t *)w_base + (size_t)c * copy_stride, x, nullptr, 0, y, n, k);
+            if (format == FMT_LUT4) {
+                p.lut = (const float *)((const uint8_t *)lut_base + (size_t)c * lut_stride);
+                p.lut_block_stride = 16;
+                p.lut_rows_own = n;
+            }
+            if (format == FMT_F32) p.nontemporal = 1;
+            GAJE_TRY(launch_gemv(p, s));
+        }
+        return GAJE_OK;
+    };
+    int rc = launch_all();  // warm-up, eager (validates the arguments)
+    hipGraph_t g = nullptr;
+    hipGraphExec_t ge = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    float ms = 0.0f;
+    int reps = (iters + copies - 1) / copies;
+    if (rc == GAJE_OK && hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) == hipSuccess) {
+        rc = launch_all();
+        if (hipStreamEndCapture(s, &g) != hipSuccess && rc == GAJE_OK)
+            rc = set_error(GAJE_ERR_HIP, "graph capture failed");
+    }
+    if (rc == GAJE_OK && hipGraphInstantiate(&ge, g, nullptr, nullptr, 0) != hipSuccess)
+        rc = set_error(GAJE_ERR_HIP, "graph instantiate failed");
+    if (rc == GAJE_OK) {
+        (void)hipGraphLaunch(ge, s);  // first replay uploads the graph
+        (void)hipEventCreate(&e0);
+        (void)hipEventCreate(&e1);
+        (void)hipEventRecord(e0, s);
+        for (int r = 0; r < reps; ++r) (void)hipGraphLaunch(ge, s);
+        (void)hipEventRecord(e1, s);
+        if (hipEventSynchronize(e1) != hipSuccess) rc = set_error(GAJE_ERR_HIP, "benchmark replay failed");
+        else (void)hipEventElapsedTime(&ms, e0, e1);
+    }
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (ge) (void)hipGraphExecDestroy(ge);
+    if (g) (void)hipGraphDestroy(g);
+    (void)hipStreamSynchronize(s);
+    (void)hipStreamDestroy(s);
+    GAJE_TRY(rc);
+    *avg_ms = ms / (float)(reps * copies);
+    return GAJE_OK;
+}

@@ -1,0 +1,135 @@
+// Launch interface between the host model code and the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace gaje {
+
+// Weight formats a GEMV can stream.
+enum WeightFormat : int32_t {
+    FMT_F32 = 0,   // GenomicF32 rows (lm_head / token_embd)
+    FMT_Q4_0 = 1,  // 20-byte Q4_0Block rows
+    FMT_LUT4 = 2,  // Genomic4Bit: 16-byte code blocks + 16-entry f32 tables
+};
+
+constexpr uint32_t NAN_NONE = 0xFFFFFFFFu;
+
+// Per-model device state read by the captured token graph.  Everything that
+// changes between tokens lives here so the graph itself never changes.
+struct DevState {
+    int32_t pos;               // cached positions before the current token
+    uint32_t token;            // current input token id
+    int32_t step;              // index of the next greedy output token
+    int32_t halted;            // a NaN guard fired: later graph replays do nothing
+    uint32_t nan_code;         // min(layer * 8 + stage) over failed guards
+    int32_t out_cap;           // capacity of the greedy output buffer
+    unsigned long long argmax_key;  // packed (orderable logit, ~index) maximum
+    uint32_t attn_counter[64];      // last-workgroup counters, one per KV head
+};
+
+// NaN guard stages of RustGenomicBlock::forward_core (block/forward.rs).
+enum NanStage : int32_t {
+    ST_INPUT = 0,       // "Input x is NaN"                    :11-13
+    ST_ATTN_NORM = 1,   // "NaN after attn rms_norm"           :22-24
+    ST_UP = 2,          // "NaN in up"                         :97-99
+    ST_FFN_OUT = 3,     // "NaN in ffn_out"                    :111-113
+    ST_PROJ_FFN = 4,    // "NaN in projected_ffn"              :128-130
+    ST_FINAL = 5,       // "NaN after projected_ffn addition"  :138-140
+    ST_NONE = -1,
+};
+
+enum GemvMode : int32_t {
+    MODE_STORE = 0,     // y[r] = row result
+    MODE_RESIDUAL = 1,  // y[r] += row result (y is the residual stream)
+    MODE_QKV = 2,       // fused QKV: RoPE on q/k rows, k/v appended to the cache
+    MODE_SWIGLU = 3,    // fused gate_up: y[p] = swiglu(row p, row p + ffn)
+    MODE_ARGMAX = 4,    // lm_head: y[r] = logit, running argmax into DevState
+};
+
+struct GemvParams {
+    // weights: row r of a Q4_0 tensor is blocks [r*nb, (r+1)*nb)
+    const uint8_t *w;
+    int32_t fmt;
+    int32_t nontemporal;     // stream the weights past the caches (read-once tensors)
+    const float *lut;        // FMT_LUT4 tables
+    int64_t lut_rows_own;    // rows r < lut_rows_own use table block r*nb*16
+    int32_t lut_block_stride;// 16 = one table per block column, 0 = one shared table
+    int32_t nb;              // K / 32
+    int64_t rows_valid;      // rows with a complete weight row (others read as 0)
+    int64_t N, K;
+    // input and prologue
+    const float *x;
+    const float *norm_w;     // rms_norm weight (prologue) or null
+    float eps;
+    int32_t gnorm;           // use_genomic_norm scaling of the input (block/forward.rs:115-123)
+    float h_scale;
+    float *x_out;            // if set, workgroup 0 writes the prologue output here
+    // per-row additive terms
+    const float *bias;
+    int64_t bias_len;
+    const int64_t *a_ptr;    // sparse anchors (CSR over rows) or null
+    const uint32_t *a_col;
+    const uint16_t *a_val;
+    // epilogue
+    int32_t mode;
+    float *y;
+    int32_t head_dim;
+    int32_t rope_split;
+    int64_t q_rows, kv_rows;
+    const float *rope_cos, *rope_sin;  // [max_ctx][head_dim/2]
+    float *q_out;
+    float *k_cache, *v_cache;          // this layer: [n_kv][max_ctx][head_dim]
+    int64_t kv_head_stride;            // max_ctx * head_dim
+    int64_t ffn;
+    // guards (stage < 0 disables a check)
+    DevState *st;
+    int32_t layer;
+    int32_t st_in, st_norm, st_a, st_b;
+};
+
+// Validates shapes against what the kernels assume and launches; returns a
+// GAJE_* status.
+int launch_gemv(const GemvParams &p, hipStream_t s);
+// Dynamic LDS the GEMV needs for in_features K (so callers can check limits).
+size_t gemv_lds_bytes(int64_t K, int fmt);
+
+struct AttnParams {
+    const float *q;          // roped queries [n_head * head_dim]
+    const float *k_cache, *v_cache;  // this layer: [n_kv][max_ctx][head_dim]
+    int64_t kv_head_stride;
+    int32_t n_head, n_head_kv, head_dim;
+    int32_t splits;
+    float *partial;          // [n_head][splits][head_dim + 2]
+    float *out;              // [n_head * head_dim]
+    DevState *st;
+};
+int launch_attention(const AttnParams &p, hipStream_t s);
+
+struct EmbedParams {
+    const uint8_t *w;
+    int32_t fmt;
+    const float *lut;
+    int64_t lut_rows_own;
+    int32_t lut_block_stride;
+    int64_t vocab, rows_valid, K;
+    float *h;
+    DevState *st;
+};
+int launch_embed(const EmbedParams &p, hipStream_t s);
+
+int launch_finalize(DevState *st, uint32_t *out_tokens, hipStream_t s);
+int launch_kwta(float *x, int64_t n, int64_t k, DevState *st, hipStream_t s);
+int launch_argmax(const float *x, int64_t n, uint32_t *idx, hipStream_t s);
+int launch_dequant_q4_0(const uint8_t *blocks, float *out, int64_t nblocks, hipStream_t s);
+int launch_rmsnorm(const float *x, const float *w, float eps, float *y, int64_t n, hipStream_t s);
+int launch_swiglu(const float *g, const float *u, float *out, int64_t n, hipStream_t s);
+int launch_fill_u32(uint32_t *p, uint32_t v, int64_t n, hipStream_t s);
+// Host-driven state update ordered on the stream.  Negative pos / out_cap /
+// step keep the current value; reset_guards clears halted, nan_code and the
+// argmax (and, with pos == 0, the attention counters).
+int launch_state_set(DevState *st, int32_t pos, uint32_t token, int32_t out_cap, int32_t step, int reset_guards,
+                     hipStream_t s);
+
+}  // namespace gaje

@@ -1,0 +1,254 @@
+// Small kernels of the decode step and the operator API (gfx950).
+#include "common.h"
+#include "device_util.h"
+
+namespace gaje {
+
+namespace {
+
+// Embedding row of the current token: GenomicLinear::get_row_core with
+// safe_idx = token % out_features (src/nn/linear/forward.rs:195-285).  The
+// first workgroup also resets the per-token reductions.
+__global__ __launch_bounds__(256) void embed_kernel(EmbedParams p) {
+    DevState *st = p.st;
+    if (st->halted) return;
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        st->argmax_key = 0ull;
+        st->nan_code = NAN_NONE;
+    }
+    const int64_t row = (int64_t)(st->token % (uint32_t)p.vocab);
+    const int64_t nb = p.K / 32;
+    for (int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; k < p.K; k += (int64_t)gridDim.x * blockDim.x) {
+        float v = 0.0f;
+        if (row < p.rows_valid) {
+            if (p.fmt == FMT_F32) {
+                v = ((const float *)p.w)[row * p.K + k];
+            } else if (k < nb * 32) {
+                const int64_t b = k / 32;
+                const int i = (int)(k % 32);
+                if (p.fmt == FMT_Q4_0) {
+                    const uint8_t *blk = p.w + (row * nb + b) * 20;
+                    const uint8_t byte = blk[4 + i / 2];
+                    const float q = (float)((i % 2 == 0) ? (byte & 0x0F) : (byte >> 4));
+                    const uint32_t sm = *(const uint32_t *)blk;
+                    v = __fadd_rn(__fmul_rn(q, half_lo(sm)), half_hi(sm));
+                } else {
+                    const float *t = p.lut + (row < p.lut_rows_own ? row * nb * 16 : 0) + b * p.lut_block_stride;
+                    const uint8_t byte = p.w[(row * nb + b) * 16 + i / 2];
+                    v = t[(i % 2 == 0) ? (byte >> 4) : (byte & 0x0F)];
+                }
+            }
+        }
+        p.h[k] = v;
+    }
+}
+
+// End of a token: NaN guard -> halt, else argmax -> next token, advance.
+__global__ void finalize_kernel(DevState *st, uint32_t *out_tokens) {
+    if (st->halted) return;
+    if (st->nan_code != NAN_NONE) {
+        st->halted = 1;
+        return;
+    }
+    const unsigned long long key = st->argmax_key;
+    const uint32_t idx = key ? 0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFull) : 0u;
+    st->token = idx;
+    if (out_tokens && st->step < st->out_cap) out_tokens[st->step] = idx;
+    st->step += 1;
+    st->pos += 1;
+}
+
+// Host-driven state changes (kept as a kernel so they order with the stream).
+__global__ void state_set_kernel(DevState *st, int32_t pos, uint32_t token, int32_t out_cap, int32_t step,
+                                 int reset_guards) {
+    if (pos >= 0) st->pos = pos;
+    st->token = token;
+    if (out_cap >= 0) st->out_cap = out_cap;
+    if (step >= 0) st->step = step;
+    if (reset_guards) {
+        st->halted = 0;
+        st->nan_code = NAN_NONE;
+        st->argmax_key = 0ull;
+    }
+}
+
+__global__ void state_clear_counters_kernel(DevState *st) {
+    for (int i = threadIdx.x; i < 64; i += blockDim.x) st->attn_counter[i] = 0u;
+}
+
+// lateral_inhibition_kwta (src/compute/kernels/lut.rs:45-61): the k-th largest
+// value by a 4-pass radix select over orderable keys, then x < thr -> -1e9.
+__global__ __launch_bounds__(1024) void kwta_kernel(float *x, int64_t n, int64_t k, DevState *st) {
+    if (st && st->halted) return;
+    if (n <= k || k <= 0) return;
+    __shared__ uint32_t hist[256];
+    __shared__ uint32_t prefix, mask;
+    __shared__ int64_t rank;
+    const int tid = threadIdx.x;
+    if (tid == 0) {
+        prefix = 0;
+        mask = 0;
+        rank = k;
+    }
+    for (int pass = 0; pass < 4; ++pass) {
+        const int shift = 24 - 8 * pass;
+        for (int i = tid; i < 256; i += blockDim.x) hist[i] = 0;
+        __syncthreads();
+        const uint32_t pf = prefix, mk = mask;
+        for (int64_t i = tid; i < n; i += blockDim.x) {
+            const uint32_t key = order_key(x[i]);
+            if ((key & mk) == pf) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        if (tid == 0) {
+            int64_t cum = 0;
+            int b = 255;
+            for (; b > 0; --b) {
+                if (cum + hist[b] >= rank) break;
+                cum += hist[b];
+            }
+            rank -= cum;
+            prefix |= (uint32_t)b << shift;
+            mask |= 255u << shift;
+        }
+        __syncthreads();
+    }
+    const float thr = order_key_inv(prefix);
+    for (int64_t i = tid; i < n; i += blockDim.x)
+        if (x[i] < thr) x[i] = -1e9f;
+}
+
+// First maximum with a strict '>' (llm/forward.rs:262-271).
+__global__ __launch_bounds__(1024) void argmax_kernel(const float *x, int64_t n, uint32_t *idx) {
+    __shared__ unsigned long long best;
+    if (threadIdx.x == 0) best = 0ull;
+    __syncthreads();
+    float bv = -INFINITY;
+    int64_t bi = 0;
+    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
+        const float v = x[i];
+        if (v > bv) { bv = v; bi = i; }
+    }
+    if (bv > -INFINITY)
+        atomicMax(&best, ((unsigned long long)order_key(bv) << 32) | (0xFFFFFFFFull - (uint64_t)bi));
+    __syncthreads();
+    if (threadIdx.x == 0) *idx = best ? 0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFull) : 0u;
+}
+
+// Q4_0Block::dequantize_weight (io/header/blocks.rs:18-30): q*scale then +min,
+// rounded separately (no FMA contraction).
+__global__ void dequant_q4_0_kernel(const uint8_t *blocks, float *out, int64_t nblocks) {
+    const int64_t total = nblocks * 32;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t b = e >> 5;
+        const int i = (int)(e & 31);
+        const uint8_t *blk = blocks + b * 20;
+        const uint8_t byte = blk[4 + i / 2];
+        const float q = (float)((i % 2 == 0) ? (byte & 0x0F) : (byte >> 4));
+        const uint32_t sm = (uint32_t)blk[0] | ((uint32_t)blk[1] << 8) | ((uint32_t)blk[2] << 16) |
+                            ((uint32_t)blk[3] << 24);
+        out[e] = __fadd_rn(__fmul_rn(q, half_lo(sm)), half_hi(sm));
+    }
+}
+
+__global__ __launch_bounds__(1024) void rmsnorm_kernel(const float *x, const float *w, float eps, float *y, int64_t n) {
+    __shared__ float part[16];
+    float ss = 0.0f;
+    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) ss = fmaf(x[i], x[i], ss);
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+    for (int i = 0; i < (int)(blockDim.x >> 6); ++i) tot += part[i];
+    const float inv = 1.0f / sqrtf(tot / (float)n + eps);
+    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) y[i] = (x[i] * inv) * w[i];
+}
+
+__global__ void swiglu_kernel(const float *g, const float *u, float *out, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        out[i] = swiglu1(g[i], u[i]);
+}
+
+__global__ void fill_u32_kernel(uint32_t *p, uint32_t v, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = v;
+}
+
+unsigned grid_for(int64_t n, int threads, unsigned cap = 4096) {
+    int64_t g = (n + threads - 1) / threads;
+    if (g < 1) g = 1;
+    return (unsigned)(g > cap ? cap : g);
+}
+
+}  // namespace
+
+int launch_embed(const EmbedParams &p, hipStream_t s) {
+    if (!p.st || !p.h || p.vocab <= 0 || p.K <= 0) return set_error(GAJE_ERR_INVALID_ARG, "embed: bad arguments");
+    hipLaunchKernelGGL(embed_kernel, dim3(grid_for(p.K, 256, 64)), dim3(256), 0, s, p);
+    GAJE_HIP_CHECK(hipGetLastError());
+    return GAJE_OK;
+}
+
+int launch_finalize(DevState *st, uint32_t *out_tokens, hipStream_t s) {
+    hipLaunchKernelGGL(finalize_kernel, dim3(1), dim3(1), 0, s, st, out_tokens);
+    GAJE_HIP_CHECK(hipGetLastError());
+    return GAJE_OK;
+}
+
+int launch_state_set(DevState *st, int32_t pos, uint32_t token, int32_t out_cap, int32_t step, int reset_guards,
+                     hipStream_t s) {
+    hipLaunchKernelGGL(state_set_kernel, dim3(1), dim3(1), 0, s, st, pos, token, out_cap, step, reset_guards);
+    GAJE_HIP_CHECK(hipGetLastError());
+    if (pos == 0 && reset_guards) {
+        hipLaunchKernelGGL(state_clear_counters_kernel, dim3(1), dim3(64), 0, s, st);
+        GAJE_HIP_CHECK(hipGetLastError());
+    }
+    return GAJE_OK;
+}
+
+int launch_kwta(float *x, int64_t n, int64_t k, DevState *st, hipStream_t s) {
+    if (!x || n < 0) return set_error(GAJE_ERR_INVALID_ARG, "kwta: bad arguments");
+    if (n <= k || k <= 0) return GAJE_OK;
+    hipLaunchKernelGGL(kwta_kernel, dim3(1), dim3(1024), 0, s, x, n, k, st);
+    GAJE_HIP_CHECK(hipGetLastError());
+    return GAJE_OK;
+}
+
+int launch_argmax(const float *x, int64_t n, uint32_t *idx, hipStream_t s) {
+    if (!x || !idx || n < 0) return set_error(GAJE_ERR_INVALID_ARG, "argmax: bad arguments");
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, x, n, idx);
+    GAJE_HIP_CHECK(hipGetLastError());
+    return GAJE_OK;
+}
+
+int launch_dequant_q4_0(const uint8_t *blocks, float *out, int64_t nblocks, hipStream_t s) {
+    if (nblocks < 0 || (nblocks > 0 && (!blocks || !out))) return set_error(GAJE_ERR_INVALID_ARG, "dequant: bad arguments");
+    if (nblocks == 0) return GAJE_OK;
+    hipLaunchKernelGGL(dequant_q4_0_kernel, dim3(grid_for(nblocks * 32, 256)), dim3(256), 0, s, blocks, out, nblocks);
+    GAJE_HIP_CHECK(hipGetLastError());
+    return GAJE_OK;
+}
+
+int launch_rmsnorm(const float *x, const float *w, float eps, float *y, int64_t n, hipStream_t s) {
+    if (!x || !w || !y || n <= 0) return set_error(GAJE_ERR_INVALID_ARG, "rmsnorm: bad arguments");
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(1024), 0, s, x, w, eps, y, n);
+    GAJE_HIP_CHECK(hipGetLastError());
+    return GAJE_OK;
+}
+
+int launch_swiglu(const float *g, const float *u, float *out, int64_t n, hipStream_t s) {
+    if (n < 0 || (n > 0 && (!g || !u || !out))) return set_error(GAJE_ERR_INVALID_ARG, "swiglu: bad arguments");
+    if (n == 0) return GAJE_OK;
+    hipLaunchKernelGGL(swiglu_kernel, dim3(grid_for(n, 256)), dim3(256), 0, s, g, u, out, n);
+    GAJE_HIP_CHECK(hipGetLastError());
+    return GAJE_OK;
+}
+
+int launch_fill_u32(uint32_t *p, uint32_t v, int64_t n, hipStream_t s) {
+    if (n <= 0) return GAJE_OK;
+    hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(n, 256)), dim3(256), 0, s, p, v, n);
+    GAJE_HIP_CHECK(hipGetLastError());
+    return GAJE_OK;
+}
+
+}  // namespace gaje

@@ -1,0 +1,1112 @@
+// Device-resident GAJE model: load a .gaje.flat into HBM and run the decode
+// step as one captured HIP graph.
+//
+// Reference structure mirrored here:
+//   load_genomic_auto / GajeFlatFileReader::load_genomic  src/io/flat_reader.rs:124-252
+//   GenomicLinear::new format dispatch and LUT expansion  src/nn/linear/init.rs:12-160
+//   GenomicLLM::forward_core / forward_with_hidden_core   src/nn/llm/forward.rs:7-113
+//   RustGenomicBlock::forward_core                        src/nn/block/forward.rs:10-157
+//   generate_native_core                                  src/nn/llm/forward.rs:215-330
+//   set_k_wta_ratio                                       src/nn/llm/python.rs:53-59
+//
+// HBM layout per model: every weight tensor in its file packing (20-byte Q4_0
+// blocks, 16-byte LUT code blocks + f32 tables, f32 rows), fused QKV and
+// gate_up row orders as the exporter writes them; KV cache [L][n_kv][cap][hd]
+// f32 (positions of one head contiguous for the attention kernel); a RoPE
+// cos/sin table [cap][hd/2] built on the host with the C library's powf/sinf/cosf,
+// the same functions the reference calls per head and token (attention.rs:66-68).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "common.h"
+#include "flat.h"
+#include "kernels.h"
+
+namespace gaje {
+namespace {
+
+constexpr int ATTN_SPLITS = 32;
+constexpr int64_t DEFAULT_CTX = 1024;
+
+struct HostLinear {
+    std::string name;
+    int fmt = -1;
+    int64_t N = 0, K = 0;
+    std::vector<uint8_t> w;        // weight bytes (native packing)
+    std::vector<float> lut;        // LUT-4bit tables as stored (not expanded)
+    std::vector<float> bias;
+    std::vector<int64_t> a_ptr;    // anchors CSR (empty = none)
+    std::vector<uint32_t> a_col;
+    std::vector<uint16_t> a_val;
+};
+
+struct DevLinear {
+    int fmt = -1;
+    int64_t N = 0, K = 0, rows_valid = 0, lut_rows_own = 0;
+    int lut_block_stride = 0;
+    uint8_t *w = nullptr;
+    float *lut = nullptr;
+    float *bias = nullptr;
+    int64_t bias_len = 0;
+    int64_t *a_ptr = nullptr;
+    uint32_t *a_col = nullptr;
+    uint16_t *a_val = nullptr;
+    int64_t bytes = 0;
+};
+
+struct Layer {
+    float *attn_norm = nullptr;  // null: the reference skips the norm when the tensor is empty
+    float *ffn_norm = nullptr;
+    DevLinear qkv, o, gate_up, down;
+};
+
+const char *nan_message(int stage) {
+    switch (stage) {
+        case ST_INPUT: return "Input x is NaN";
+        case ST_ATTN_NORM: return "NaN after attn rms_norm";
+        case ST_UP: return "NaN in up";
+        case ST_FFN_OUT: return "NaN in ffn_out";
+        case ST_PROJ_FFN: return "NaN in projected_ffn";
+        case ST_FINAL: return "NaN after projected_ffn addition";
+        default: return "NaN";
+    }
+}
+
+// GenomicLinear::new anchor parsing (init.rs:61-107) into CSR with the column
+// already reduced modulo in_features (compute_single_row, forward.rs:103-112).
+void parse_anchors(const uint8_t *buf, uint64_t len, HostLinear &L) {
+    if (len < 8 || memcmp(buf, "GAJE", 4) != 0) return;
+    uint32_t count;
+    memcpy(&count, buf + 4, 4);
+    const uint64_t idx_s = 8, val_s = idx_s + (uint64_t)count * 4, ptr_s = val_s + (uint64_t)count * 2;
+    if (val_s + (uint64_t)count * 2 > len) return;  // the reference would panic on the slice
+    std::vector<uint32_t> idx(count);
+    std::vector<uint16_t> val(count);
+    memcpy(idx.data(), buf + idx_s, (size_t)count * 4);
+    memcpy(val.data(), buf + val_s, (size_t)count * 2);
+    std::vector<int64_t> ptr(L.N + 1, 0);
+    if (len >= ptr_s + (uint64_t)(L.N + 1) * 8) {
+        for (int64_t i = 0; i <= L.N; ++i) {
+            uint64_t v;
+            memcpy(&v, buf + ptr_s + i * 8, 8);
+            ptr[i] = (int64_t)v;
+        }
+    } else {
+        int64_t cur = 0;
+        for (uint32_t a = 0; a < count; ++a) {
+            int64_t r = (int64_t)(idx[a] / (uint64_t)L.K);
+            while (cur < r && cur < L.N) ptr[++cur] = a;
+        }
+        while (cur < L.N) ptr[++cur] = count;
+    }
+    // Rows whose range fails the reference's a_s < a_e <= count test add nothing.
+    L.a_ptr.assign(L.N + 1, 0);
+    for (int64_t i = 0; i < L.N; ++i) {
+        int64_t a_s = ptr[i], a_e = ptr[i + 1];
+        bool ok = a_s < a_e && a_e <= (int64_t)count;
+        for (int64_t k = ok ? a_s : 0; ok && k < a_e; ++k) {
+            L.a_col.push_back((uint32_t)(idx[k] % (uint64_t)L.K));
+            L.a_val.push_back(val[k]);
+        }
+        L.a_ptr[i + 1] = (int64_t)L.a_col.size();
+    }
+    if (L.a_col.empty()) L.a_ptr.clear();
+}
+
+// GajeFlatFileReader::get_linear + GenomicLinear::new dispatch.
+int read_linear(const FlatFile &f, const std::string &name, HostLinear &L) {
+    const TensorEntry *e = f.find(name);
+    if (!e) return set_error(GAJE_ERR_NOT_FOUND, "Flat tensor entry '%s' not found", name.c_str());
+    L = HostLinear();
+    L.name = name;
+    L.N = (int64_t)e->out_features;
+    L.K = (int64_t)e->in_features;
+    const uint8_t *dna, *c, *anc, *bias;
+    GAJE_TRY(f.slice(e->dna_off, e->dna_len, &dna));
+    GAJE_TRY(f.slice(e->c_off, e->c_len, &c));
+    GAJE_TRY(f.slice(e->anc_off, e->anc_len, &anc));
+    GAJE_TRY(f.slice(e->bias_off, e->bias_len, &bias));
+    const uint8_t bit_depth = (uint8_t)e->bit_depth;  // `entry.bit_depth as u8`
+    const uint64_t n_cent = e->c_len / 4;
+    if (bit_depth == 4) L.fmt = n_cent == 0 ? FMT_Q4_0 : FMT_LUT4;
+    else if (bit_depth == 32) L.fmt = FMT_F32;
+    else if (bit_depth == 8)
+        return set_error(GAJE_ERR_UNSUPPORTED, "tensor '%s': Q8_0 (bit_depth 8) is not in this build", name.c_str());
+    else
+        return set_error(GAJE_ERR_UNSUPPORTED, "tensor '%s': 2-bit genomic format is not in this build", name.c_str());
+    if (e->dna_len) L.w.assign(dna, dna + e->dna_len);
+    if (L.fmt == FMT_LUT4) {
+        L.lut.resize(n_cent);
+        memcpy(L.lut.data(), c, n_cent * 4);
+    }
+    const uint64_t nb = e->bias_len / 4;
+    L.bias.resize(nb);
+    if (nb) memcpy(L.bias.data(), bias, nb * 4);
+    if (e->anc_len) parse_anchors(anc, e->anc_len, L);
+    return GAJE_OK;
+}
+
+int read_norm(const FlatFile &f, const std::string &name, std::vector<float> &out) {
+    const TensorEntry *e = f.find(name);
+    if (!e) return set_error(GAJE_ERR_NOT_FOUND, "Flat tensor entry '%s' not found", name.c_str());
+    const uint8_t *p;
+    GAJE_TRY(f.slice(e->dna_off, e->dna_len, &p));
+    out.resize(e->dna_len / 4);
+    if (!out.empty()) memcpy(out.data(), p, out.size() * 4);
+    return GAJE_OK;
+}
+
+int64_t rows_valid_of(const HostLinear &L) {
+    const int64_t nb = L.K / 32;
+    if (L.fmt == FMT_F32) return L.K ? std::min<int64_t>(L.N, (int64_t)(L.w.size() / 4) / L.K) : 0;
+    if (nb == 0) return 0;
+    if (L.fmt == FMT_Q4_0) return std::min<int64_t>(L.N, (int64_t)(L.w.size() / 20) / nb);
+    if (L.lut.size() < 16) return 0;  // no table: compute_single_row yields 0
+    return std::min<int64_t>(L.N, (int64_t)L.w.size() / (nb * 16));
+}
+
+// Row-concatenate split tensors into the fused order the kernels expect
+// ([q;k;v] as at export_gaje_flat.py:378-406, [gate;up] as at :413-417).
+int fuse_linears(std::vector<HostLinear> parts, const std::string &name, HostLinear &out) {
+    out = HostLinear();
+    out.name = name;
+    out.fmt = parts[0].fmt;
+    out.K = parts[0].K;
+    const int64_t nb = out.K / 32;
+    bool any_bias = false, any_anchor = false;
+    for (auto &p : parts) {
+        if (p.fmt != out.fmt || p.K != out.K)
+            return set_error(GAJE_ERR_UNSUPPORTED, "%s: split tensors differ in format or in_features", name.c_str());
+        if (rows_valid_of(p) != p.N)
+            return set_error(GAJE_ERR_UNSUPPORTED, "%s: truncated split tensor", name.c_str());
+        out.N += p.N;
+        any_bias |= !p.bias.empty();
+        any_anchor |= !p.a_ptr.empty();
+    }
+    for (auto &p : parts) {
+        size_t row_bytes = out.fmt == FMT_Q4_0 ? nb * 20 : out.fmt == FMT_LUT4 ? nb * 16 : out.K * 4;
+        out.w.insert(out.w.end(), p.w.begin(), p.w.begin() + row_bytes * p.N);
+        if (out.fmt == FMT_LUT4) {  // expand to per-row tables (init.rs:109-124)
+            const size_t per_row = nb * 16;
+            for (int64_t r = 0; r < p.N; ++r) {
+                const float *src;
+                if (p.lut.size() == 16) {
+                    for (int64_t b = 0; b < nb; ++b) out.lut.insert(out.lut.end(), p.lut.begin(), p.lut.begin() + 16);
+                    continue;
+                } else if (p.lut.size() == per_row) {
+                    src = p.lut.data();
+                } else if (p.lut.size() >= (size_t)(r + 1) * per_row) {
+                    src = p.lut.data() + r * per_row;
+                } else if (p.lut.size() >= per_row) {
+                    src = p.lut.data();
+                } else {
+                    return set_error(GAJE_ERR_INVALID_DATA, "%s: centroid table too short", p.name.c_str());
+                }
+                out.lut.insert(out.lut.end(), src, src + per_row);
+            }
+        }
+        if (any_bias) {
+            for (int64_t r = 0; r < p.N; ++r) out.bias.push_back(r < (int64_t)p.bias.size() ? p.bias[r] : 0.0f);
+        }
+        if (any_anchor) {
+            if (out.a_ptr.empty()) out.a_ptr.push_back(0);
+            for (int64_t r = 0; r < p.N; ++r) {
+                if (!p.a_ptr.empty())
+                    for (int64_t k = p.a_ptr[r]; k < p.a_ptr[r + 1]; ++k) {
+                        out.a_col.push_back(p.a_col[k]);
+                        out.a_val.push_back(p.a_val[k]);
+                    }
+                out.a_ptr.push_back((int64_t)out.a_col.size());
+            }
+        }
+    }
+    return GAJE_OK;
+}
+
+}  // namespace
+}  // namespace gaje
+
+using namespace gaje;
+
+struct gaje_hip_model {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    ModelConfig cfg;
+    int64_t n_embd = 0, n_head = 0, n_kv = 0, hd = 0, ffn = 0, vocab_embd = 0, vocab_out = 0, n_layers = 0;
+    int64_t q_rows = 0, kv_rows = 0;
+    int32_t arch_family = 0;
+    int rope_split = 1;
+    float rope_base = 10000.0f, eps = 0.0f;
+    bool use_genomic_norm = false;
+    int body_fmt = FMT_Q4_0;
+
+    DevLinear embd, lm_head;
+    float *output_norm = nullptr;
+    std::vector<Layer> layers;
+
+    // activations and scratch
+    float *h = nullptr, *q = nullptr, *attn_out = nullptr, *act = nullptr, *logits = nullptr, *hnorm = nullptr,
+          *attn_part = nullptr;
+    DevState *st = nullptr;
+    uint32_t *out_tokens = nullptr;
+    int64_t out_cap = 0;
+    // KV cache and RoPE table
+    float *k_cache = nullptr, *v_cache = nullptr, *rope_cos = nullptr, *rope_sin = nullptr;
+    int64_t cap = 0;
+
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t graph_exec = nullptr;
+    bool graph_kwta_blocks = false;
+
+    float kwta_ratio = 0.5f;        // GenomicLLM k_wta_ratio after load_genomic (flat_reader.rs:234)
+    float block_kwta_ratio = 0.0f;  // RustGenomicBlock k_wta_ratio (block/init.rs:42)
+    int64_t pos = 0;                // cached positions (k_cache_len of block 0)
+    int64_t weight_bytes = 0;
+    bool profile = false;
+    float last_blocks_ms = 0.0f, last_head_ms = 0.0f;
+
+    std::vector<void *> allocs;
+
+    ~gaje_hip_model() {
+        if (graph_exec) (void)hipGraphExecDestroy(graph_exec);
+        if (graph) (void)hipGraphDestroy(graph);
+        for (void *p : allocs) (void)hipFree(p);
+        if (stream) (void)hipStreamDestroy(stream);
+    }
+
+    template <class T>
+    int alloc(T **p, size_t count) {
+        *p = nullptr;
+        if (count == 0) return GAJE_OK;
+        void *v = nullptr;
+        GAJE_HIP_CHECK(hipMalloc(&v, count * sizeof(T)));
+        allocs.push_back(v);
+        *p = (T *)v;
+        return GAJE_OK;
+    }
+    template <class T>
+    int upload(T **p, const T *src, size_t count) {
+        GAJE_TRY(alloc(p, count));
+        if (count) GAJE_HIP_CHECK(hipMemcpy(*p, src, count * sizeof(T), hipMemcpyHostToDevice));
+        weight_bytes += (int64_t)(count * sizeof(T));
+        return GAJE_OK;
+    }
+    void release(void *p) {
+        for (auto it = allocs.begin(); it != allocs.end(); ++it)
+            if (*it == p) {
+                (void)hipFree(p);
+                allocs.erase(it);
+                return;
+            }
+    }
+};
+
+namespace {
+
+int upload_linear(gaje_hip_model *m, const HostLinear &L, DevLinear &D) {
+    D = DevLinear();
+    D.fmt = L.fmt;
+    D.N = L.N;
+    D.K = L.K;
+    D.rows_valid = rows_valid_of(L);
+    const int64_t nb = L.K / 32;
+    GAJE_TRY(m->upload(&D.w, L.w.data(), L.w.size()));
+    if (L.fmt == FMT_LUT4 && !L.lut.empty()) {
+        const size_t n = L.lut.size(), per_row = (size_t)nb * 16;
+        if (n == 16) {
+            D.lut_block_stride = 0;
+            D.lut_rows_own = 0;
+        } else if (per_row > 0 && n >= per_row) {
+            D.lut_block_stride = 16;
+            D.lut_rows_own = n == per_row ? 0 : (int64_t)(n / per_row);
+        } else {
+            return set_error(GAJE_ERR_INVALID_DATA, "tensor '%s': centroid table of %zu floats is shorter than a row",
+                             L.name.c_str(), n);
+        }
+        GAJE_TRY(m->upload(&D.lut, L.lut.data(), n));
+    }
+    D.bias_len = (int64_t)L.bias.size();
+    GAJE_TRY(m->upload(&D.bias, L.bias.data(), L.bias.size()));
+    if (!L.a_ptr.empty()) {
+        GAJE_TRY(m->upload(&D.a_ptr, L.a_ptr.data(), L.a_ptr.size()));
+        GAJE_TRY(m->upload(&D.a_col, L.a_col.data(), L.a_col.size()));
+        GAJE_TRY(m->upload(&D.a_val, L.a_val.data(), L.a_val.size()));
+    }
+    return GAJE_OK;
+}
+
+GemvParams gemv_base(const gaje_hip_model *m, const DevLinear &D, const float *x) {
+    GemvParams p;
+    memset(&p, 0, sizeof p);
+    p.w = D.w;
+    p.fmt = D.fmt;
+    p.lut = D.lut;
+    p.lut_rows_own = D.lut_rows_own;
+    p.lut_block_stride = D.lut_block_stride;
+    p.nb = (int32_t)(D.K / 32);
+    p.rows_valid = D.rows_valid;
+    p.N = D.N;
+    p.K = D.K;
+    p.x = x;
+    p.eps = m->eps;
+    p.h_scale = 1.0f;
+    p.bias = D.bias;
+    p.bias_len = D.bias_len;
+    p.a_ptr = D.a_ptr;
+    p.a_col = D.a_col;
+    p.a_val = D.a_val;
+    p.st = m->st;
+    p.st_in = p.st_norm = p.st_a = p.st_b = ST_NONE;
+    return p;
+}
+
+int build_rope(gaje_hip_model *m, int64_t cap, float **cos_out, float **sin_out) {
+    const int64_t half = m->hd / 2;
+    std::vector<float> c((size_t)(cap * half)), s((size_t)(cap * half));
+    for (int64_t i = 0; i < half; ++i) {
+        const float expo = (2.0f * (float)i) / (float)m->hd;
+        const float freq = 1.0f / powf(m->rope_base, expo);
+        for (int64_t pos = 0; pos < cap; ++pos) {
+            const float theta = (float)pos * freq;
+            c[pos * half + i] = cosf(theta);
+            s[pos * half + i] = sinf(theta);
+        }
+    }
+    GAJE_TRY(m->alloc(cos_out, c.size()));
+    GAJE_TRY(m->alloc(sin_out, s.size()));
+    GAJE_HIP_CHECK(hipMemcpy(*cos_out, c.data(), c.size() * 4, hipMemcpyHostToDevice));
+    GAJE_HIP_CHECK(hipMemcpy(*sin_out, s.data(), s.size() * 4, hipMemcpyHostToDevice));
+    return GAJE_OK;
+}
+
+void drop_graph(gaje_hip_model *m) {
+    if (m->graph_exec) (void)hipGraphExecDestroy(m->graph_exec);
+    if (m->graph) (void)hipGraphDestroy(m->graph);
+    m->graph_exec = nullptr;
+    m->graph = nullptr;
+}
+
+// Grow the KV cache and RoPE table to hold `positions` tokens.
+int reserve_ctx(gaje_hip_model *m, int64_t positions) {
+    if (positions <= m->cap) return GAJE_OK;
+    int64_t cap = std::max<int64_t>(positions, m->cap ? 2 * m->cap : DEFAULT_CTX);
+    cap = (cap + 63) / 64 * 64;
+    const int64_t L = std::max<int64_t>(m->n_layers, 1);
+    const size_t per_head_new = (size_t)cap * m->hd, per_head_old = (size_t)m->cap * m->hd;
+    float *kc, *vc, *rc, *rs;
+    GAJE_TRY(m->alloc(&kc, (size_t)L * m->n_kv * per_head_new));
+    GAJE_TRY(m->alloc(&vc, (size_t)L * m->n_kv * per_head_new));
+    if (m->k_cache && m->pos > 0) {
+        for (int64_t l = 0; l < m->n_layers; ++l)
+            for (int64_t g = 0; g < m->n_kv; ++g) {
+                const size_t src = ((size_t)l * m->n_kv + g) * per_head_old, dst = ((size_t)l * m->n_kv + g) * per_head_new;
+                const size_t bytes = (size_t)m->pos * m->hd * 4;
+                GAJE_HIP_CHECK(hipMemcpyAsync(kc + dst, m->k_cache + src, bytes, hipMemcpyDeviceToDevice, m->stream));
+                GAJE_HIP_CHECK(hipMemcpyAsync(vc + dst, m->v_cache + src, bytes, hipMemcpyDeviceToDevice, m->stream));
+            }
+        GAJE_HIP_CHECK(hipStreamSynchronize(m->stream));
+    }
+    GAJE_TRY(build_rope(m, cap, &rc, &rs));
+    if (m->k_cache) m->release(m->k_cache);
+    if (m->v_cache) m->release(m->v_cache);
+    if (m->rope_cos) m->release(m->rope_cos);
+    if (m->rope_sin) m->release(m->rope_sin);
+    m->k_cache = kc;
+    m->v_cache = vc;
+    m->rope_cos = rc;
+    m->rope_sin = rs;
+    m->cap = cap;
+    drop_graph(m);
+    return GAJE_OK;
+}
+
+// Enqueue one decode step (embedding -> blocks -> output norm -> lm_head ->
+// argmax/advance) on the model stream.
+int enqueue_token(gaje_hip_model *m, hipEvent_t ev_blocks_done) {
+    EmbedParams ep;
+    memset(&ep, 0, sizeof ep);
+    ep.w = m->embd.w;
+    ep.fmt = m->embd.fmt;
+    ep.lut = m->embd.lut;
+    ep.lut_rows_own = m->embd.lut_rows_own;
+    ep.lut_block_stride = m->embd.lut_block_stride;
+    ep.vocab = m->vocab_embd;
+    ep.rows_valid = m->embd.rows_valid;
+    ep.K = m->n_embd;
+    ep.h = m->h;
+    ep.st = m->st;
+    GAJE_TRY(launch_embed(ep, m->stream));
+
+    const size_t layer_kv = (size_t)m->n_kv * m->cap * m->hd;
+    for (int64_t l = 0; l < m->n_layers; ++l) {
+        Layer &Ly = m->layers[l];
+        GemvParams p = gemv_base(m, Ly.qkv, m->h);
+        p.norm_w = Ly.attn_norm;
+        p.layer = (int32_t)l;
+        p.st_in = ST_INPUT;
+        p.st_norm = Ly.attn_norm ? ST_ATTN_NORM : ST_NONE;
+        p.mode = MODE_QKV;
+        p.y = m->q;
+        p.q_out = m->q;
+        p.head_dim = (int32_t)m->hd;
+        p.rope_split = m->rope_split;
+        p.q_rows = m->q_rows;
+        p.kv_rows = m->kv_rows;
+        p.rope_cos = m->rope_cos;
+        p.rope_sin = m->rope_sin;
+        p.k_cache = m->k_cache + l * layer_kv;
+        p.v_cache = m->v_cache + l * layer_kv;
+        p.kv_head_stride = m->cap * m->hd;
+        GAJE_TRY(launch_gemv(p, m->stream));
+
+        AttnParams ap;
+        ap.q = m->q;
+        ap.k_cache = m->k_cache + l * layer_kv;
+        ap.v_cache = m->v_cache + l * layer_kv;
+        ap.kv_head_stride = m->cap * m->hd;
+        ap.n_head = (int32_t)m->n_head;
+        ap.n_head_kv = (int32_t)m->n_kv;
+        ap.head_dim = (int32_t)m->hd;
+        ap.splits = ATTN_SPLITS;
+        ap.partial = m->attn_part;
+        ap.out = m->attn_out;
+        ap.st = m->st;
+        GAJE_TRY(launch_attention(ap, m->stream));
+
+        p = gemv_base(m, Ly.o, m->attn_out);
+        p.layer = (int32_t)l;
+        p.mode = MODE_RESIDUAL;
+        p.y = m->h;
+        GAJE_TRY(launch_gemv(p, m->stream));
+
+        p = gemv_base(m, Ly.gate_up, m->h);
+        p.norm_w = Ly.ffn_norm;
+        p.layer = (int32_t)l;
+        p.mode = MODE_SWIGLU;
+        p.ffn = m->ffn;
+        p.y = m->act;
+        p.st_a = ST_UP;
+        p.st_b = ST_FFN_OUT;
+        GAJE_TRY(launch_gemv(p, m->stream));
+
+        p = gemv_base(m, Ly.down, m->act);
+        p.layer = (int32_t)l;
+        p.gnorm = m->use_genomic_norm;
+        p.mode = MODE_RESIDUAL;
+        p.y = m->h;
+        p.st_a = ST_PROJ_FFN;
+        p.st_b = ST_FINAL;
+        GAJE_TRY(launch_gemv(p, m->stream));
+
+        if (m->block_kwta_ratio > 0.0f && m->block_kwta_ratio < 1.0f) {
+            int64_t k = (int64_t)((float)m->n_embd * m->block_kwta_ratio);
+            if (k < 1) k = 1;
+            GAJE_TRY(launch_kwta(m->h, m->n_embd, k, m->st, m->stream));
+        }
+    }
+    if (ev_blocks_done) GAJE_HIP_CHECK(hipEventRecord(ev_blocks_done, m->stream));
+
+    GemvParams p = gemv_base(m, m->lm_head, m->h);
+    p.norm_w = m->output_norm;
+    p.mode = MODE_ARGMAX;
+    p.y = m->logits;
+    p.x_out = m->hnorm;
+    p.nontemporal = 1;
+    p.layer = (int32_t)m->n_layers;
+    GAJE_TRY(launch_gemv(p, m->stream));
+    return launch_finalize(m->st, m->out_tokens, m->stream);
+}
+
+int ensure_graph(gaje_hip_model *m) {
+    const bool kb = m->block_kwta_ratio > 0.0f && m->block_kwta_ratio < 1.0f;
+    if (m->graph_exec && m->graph_kwta_blocks == kb) return GAJE_OK;
+    drop_graph(m);
+    GAJE_HIP_CHECK(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
+    int rc = enqueue_token(m, nullptr);
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(m->stream, &g);
+    if (rc != GAJE_OK) {
+        if (g) (void)hipGraphDestroy(g);
+        return rc;
+    }
+    if (e != hipSuccess) return set_error(GAJE_ERR_HIP, "graph capture failed: %s", hipGetErrorString(e));
+    m->graph = g;
+    GAJE_HIP_CHECK(hipGraphInstantiate(&m->graph_exec, g, nullptr, nullptr, 0));
+    m->graph_kwta_blocks = kb;
+    return GAJE_OK;
+}
+
+int run_token(gaje_hip_model *m) {
+    if (m->profile) {
+        hipEvent_t e0, e1, e2;
+        GAJE_HIP_CHECK(hipEventCreate(&e0));
+        GAJE_HIP_CHECK(hipEventCreate(&e1));
+        GAJE_HIP_CHECK(hipEventCreate(&e2));
+        GAJE_HIP_CHECK(hipEventRecord(e0, m->stream));
+        int rc = enqueue_token(m, e1);
+        GAJE_HIP_CHECK(hipEventRecord(e2, m->stream));
+        GAJE_HIP_CHECK(hipEventSynchronize(e2));
+        (void)hipEventElapsedTime(&m->last_blocks_ms, e0, e1);
+        (void)hipEventElapsedTime(&m->last_head_ms, e1, e2);
+        (void)hipEventDestroy(e0);
+        (void)hipEventDestroy(e1);
+        (void)hipEventDestroy(e2);
+        return rc;
+    }
+    GAJE_TRY(ensure_graph(m));
+    GAJE_HIP_CHECK(hipGraphLaunch(m->graph_exec, m->stream));
+    return GAJE_OK;
+}
+
+int read_state(gaje_hip_model *m, DevState &s) {
+    GAJE_HIP_CHECK(hipMemcpyAsync(&s, m->st, sizeof s, hipMemcpyDeviceToHost, m->stream));
+    GAJE_HIP_CHECK(hipStreamSynchronize(m->stream));
+    return GAJE_OK;
+}
+
+int nan_error(const DevState &s) {
+    const int stage = (int)(s.nan_code % 8);
+    return set_error(GAJE_ERR_NAN, "%s", nan_message(stage));
+}
+
+int64_t kwta_k(int64_t n, float ratio) {
+    int64_t k = (int64_t)((float)n * ratio);
+    return k < 1 ? 1 : k;
+}
+
+// forward_core for one token; leaves the logits on the device (K-WTA applied
+// when `apply_kwta`), the state read back into `s`.
+int forward_device(gaje_hip_model *m, uint32_t token, bool clear, bool apply_kwta, DevState &s) {
+    if (clear) m->pos = 0;
+    GAJE_TRY(reserve_ctx(m, m->pos + 1));
+    GAJE_TRY(launch_state_set(m->st, (int32_t)m->pos, token, -1, -1, 1, m->stream));
+    GAJE_TRY(run_token(m));
+    if (apply_kwta && m->kwta_ratio > 0.0f && m->kwta_ratio < 1.0f)
+        GAJE_TRY(launch_kwta(m->logits, m->vocab_out, kwta_k(m->vocab_out, m->kwta_ratio), m->st, m->stream));
+    GAJE_TRY(read_state(m, s));
+    if (s.halted || s.nan_code != NAN_NONE) return nan_error(s);
+    m->pos += 1;
+    return GAJE_OK;
+}
+
+int check_model(gaje_hip_model *m) {
+    if (!m) return set_error(GAJE_ERR_INVALID_ARG, "null model handle");
+    GAJE_HIP_CHECK(hipSetDevice(m->device));
+    return GAJE_OK;
+}
+
+uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+}  // namespace
+
+extern "C" int gaje_hip_open(const char *path, int device, gaje_hip_model **out) {
+    clear_error();
+    if (!path || !out) return set_error(GAJE_ERR_INVALID_ARG, "gaje_hip_open: null argument");
+    *out = nullptr;
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev == 0)
+        return set_error(GAJE_ERR_NO_DEVICE, "no HIP device available");
+    if (device < 0 || device >= ndev) return set_error(GAJE_ERR_INVALID_ARG, "device %d out of range", device);
+    GAJE_HIP_CHECK(hipSetDevice(device));
+
+    FlatFile f;
+    GAJE_TRY(f.open(path));
+    std::unique_ptr<gaje_hip_model> m(new gaje_hip_model());
+    m->device = device;
+    GAJE_TRY(f.model_config(m->cfg));
+    const ModelConfig &c = m->cfg;
+    if (c.n_head == 0) return set_error(GAJE_ERR_MODEL, "n_head is 0");
+    m->n_embd = (int64_t)c.n_embd;
+    m->n_head = (int64_t)c.n_head;
+    m->n_kv = (int64_t)c.n_head_kv;
+    m->n_layers = (int64_t)c.n_blocks;
+    m->hd = m->n_embd / m->n_head;  // load_genomic: n_embd / n_head (flat_reader.rs:142)
+    m->eps = c.eps;
+    m->rope_base = c.rope_base;
+    m->rope_split = c.rope_style == "split" ? 1 : 0;
+    m->use_genomic_norm = c.use_genomic_norm;
+    m->arch_family = (int32_t)f.header().arch_family;
+    m->q_rows = m->n_head * m->hd;
+    m->kv_rows = m->n_kv * m->hd;
+    if (m->n_layers > 0 && (m->n_kv == 0 || m->n_head % m->n_kv != 0))
+        return set_error(GAJE_ERR_MODEL, "n_head %lld is not a multiple of n_head_kv %lld", (long long)m->n_head,
+                         (long long)m->n_kv);
+    if (m->n_layers > 0 && (m->hd <= 0 || m->hd > 128 || m->hd % 4 != 0))
+        return set_error(GAJE_ERR_UNSUPPORTED, "head_dim %lld not supported (need <= 128, multiple of 4)",
+                         (long long)m->hd);
+    if (m->n_kv > 64) return set_error(GAJE_ERR_UNSUPPORTED, "more than 64 KV heads");
+    m->profile = getenv("GAJE_HIP_PROFILE") != nullptr;
+
+    GAJE_HIP_CHECK(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking));
+
+    HostLinear L;
+    GAJE_TRY(read_linear(f, "token_embd", L));
+    if (L.K != m->n_embd)
+        return set_error(GAJE_ERR_MODEL, "token_embd in_features %lld != n_embd %lld", (long long)L.K,
+                         (long long)m->n_embd);
+    m->vocab_embd = L.N;
+    if (m->vocab_embd == 0) return set_error(GAJE_ERR_MODEL, "token_embd has no rows");
+    GAJE_TRY(upload_linear(m.get(), L, m->embd));
+    std::vector<float> norm;
+    GAJE_TRY(read_norm(f, "output_norm", norm));
+    if ((int64_t)norm.size() != m->n_embd) return set_error(GAJE_ERR_MODEL, "output_norm length != n_embd");
+    GAJE_TRY(m->upload(&m->output_norm, norm.data(), norm.size()));
+    GAJE_TRY(read_linear(f, "lm_head", L));
+    if (L.N == 0) return set_error(GAJE_ERR_MODEL, "LM Head out_features is 0!");
+    if (L.K != m->n_embd) return set_error(GAJE_ERR_MODEL, "lm_head in_features != n_embd");
+    m->vocab_out = L.N;
+    GAJE_TRY(upload_linear(m.get(), L, m->lm_head));
+
+    m->layers.resize((size_t)m->n_layers);
+    for (int64_t i = 0; i < m->n_layers; ++i) {
+        const std::string p = "blk." + std::to_string(i) + ".";
+        Layer &Ly = m->layers[i];
+        GAJE_TRY(read_norm(f, p + "attn_norm", norm));
+        if (!norm.empty()) {
+            if ((int64_t)norm.size() != m->n_embd) return set_error(GAJE_ERR_MODEL, "%sattn_norm length != n_embd", p.c_str());
+            GAJE_TRY(m->upload(&Ly.attn_norm, norm.data(), norm.size()));
+        }
+        GAJE_TRY(read_norm(f, p + "ffn_norm", norm));
+        if ((int64_t)norm.size() != m->n_embd) return set_error(GAJE_ERR_MODEL, "%sffn_norm length != n_embd", p.c_str());
+        GAJE_TRY(m->upload(&Ly.ffn_norm, norm.data(), norm.size()));
+
+        HostLinear qkv, gu, o, down;
+        if (f.find(p + "attn_qkv")) {
+            GAJE_TRY(read_linear(f, p + "attn_qkv", qkv));
+        } else {
+            std::vector<HostLinear> parts(3);
+            GAJE_TRY(read_linear(f, p + "attn_q", parts[0]));
+            GAJE_TRY(read_linear(f, p + "attn_k", parts[1]));
+            GAJE_TRY(read_linear(f, p + "attn_v", parts[2]));
+            GAJE_TRY(fuse_linears(std::move(parts), p + "attn_qkv", qkv));
+        }
+        GAJE_TRY(read_linear(f, p + "attn_output", o));
+        if (f.find(p + "ffn_gate_up")) {
+            GAJE_TRY(read_linear(f, p + "ffn_gate_up", gu));
+        } else {
+            std::vector<HostLinear> parts(2);
+            GAJE_TRY(read_linear(f, p + "ffn_gate", parts[0]));
+            GAJE_TRY(read_linear(f, p + "ffn_up", parts[1]));
+            GAJE_TRY(fuse_linears(std::move(parts), p + "ffn_gate_up", gu));
+        }
+        GAJE_TRY(read_linear(f, p + "ffn_down", down));
+        if (qkv.K != m->n_embd || qkv.N < m->q_rows + 2 * m->kv_rows)
+            return set_error(GAJE_ERR_MODEL, "%sattn_qkv shape %lldx%lld does not match the architecture", p.c_str(),
+                             (long long)qkv.N, (long long)qkv.K);
+        if (o.K != m->q_rows || o.N != m->n_embd)
+            return set_error(GAJE_ERR_MODEL, "%sattn_output shape does not match the architecture", p.c_str());
+        if (gu.K != m->n_embd || gu.N < 2)
+            return set_error(GAJE_ERR_MODEL, "%sffn_gate_up shape does not match the architecture", p.c_str());
+        const int64_t ffn = gu.N / 2;  // block/forward.rs:89
+        if (i == 0) m->ffn = ffn;
+        if (ffn != m->ffn) return set_error(GAJE_ERR_UNSUPPORTED, "blocks with different FFN widths");
+        if (down.K != ffn || down.N != m->n_embd)
+            return set_error(GAJE_ERR_MODEL, "%sffn_down shape does not match the architecture", p.c_str());
+        if (i == 0) m->body_fmt = qkv.fmt;
+        GAJE_TRY(upload_linear(m.get(), qkv, Ly.qkv));
+        GAJE_TRY(upload_linear(m.get(), o, Ly.o));
+        GAJE_TRY(upload_linear(m.get(), gu, Ly.gate_up));
+        GAJE_TRY(upload_linear(m.get(), down, Ly.down));
+    }
+
+    // activations, scratch, state
+    const int64_t qn = std::max<int64_t>(m->q_rows, 1);
+    GAJE_TRY(m->alloc(&m->h, (size_t)m->n_embd));
+    GAJE_TRY(m->alloc(&m->hnorm, (size_t)m->n_embd));
+    GAJE_TRY(m->alloc(&m->q, (size_t)qn));
+    GAJE_TRY(m->alloc(&m->attn_out, (size_t)qn));
+    GAJE_TRY(m->alloc(&m->act, (size_t)std::max<int64_t>(m->ffn, 1)));
+    GAJE_TRY(m->alloc(&m->logits, (size_t)m->vocab_out));
+    GAJE_TRY(m->alloc(&m->attn_part, (size_t)std::max<int64_t>(m->n_head, 1) * ATTN_SPLITS * (m->hd + 2)));
+    GAJE_TRY(m->alloc(&m->st, 1));
+    GAJE_HIP_CHECK(hipMemset(m->st, 0, sizeof(DevState)));
+    m->out_cap = 4096;
+    GAJE_TRY(m->alloc(&m->out_tokens, (size_t)m->out_cap));
+    if (m->n_layers > 0) GAJE_TRY(reserve_ctx(m.get(), DEFAULT_CTX));
+    GAJE_TRY(launch_state_set(m->st, 0, 0, (int32_t)m->out_cap, 0, 1, m->stream));
+    GAJE_HIP_CHECK(hipStreamSynchronize(m->stream));
+    *out = m.release();
+    return GAJE_OK;
+}
+
+extern "C" void gaje_hip_close(gaje_hip_model *m) {
+    if (!m) return;
+    (void)hipSetDevice(m->device);
+    if (m->stream) (void)hipStreamSynchronize(m->stream);
+    delete m;
+}
+
+extern "C" int gaje_hip_model_info_get(const gaje_hip_model *m, gaje_hip_model_info *info) {
+    if (!m || !info) return set_error(GAJE_ERR_INVALID_ARG, "null argument");
+    memset(info, 0, sizeof *info);
+    info->n_embd = m->n_embd;
+    info->n_head = m->n_head;
+    info->n_head_kv = m->n_kv;
+    info->n_blocks = m->n_layers;
+    info->head_dim = m->hd;
+    info->ffn = m->ffn;
+    info->vocab_size = m->vocab_embd;
+    info->eps = m->eps;
+    info->rope_base = m->rope_base;
+    info->rope_split = m->rope_split;
+    info->arch_family = m->arch_family;
+    info->body_format = m->body_fmt;
+    info->use_genomic_norm = m->use_genomic_norm;
+    info->max_ctx = m->cap;
+    info->weight_bytes = m->weight_bytes;
+    info->n_logits = m->vocab_out;
+    return GAJE_OK;
+}
+
+extern "C" int gaje_hip_forward(gaje_hip_model *m, uint32_t token, int clear_cache, float *logits_host) {
+    clear_error();
+    GAJE_TRY(check_model(m));
+    DevState s;
+    GAJE_TRY(forward_device(m, token, clear_cache != 0, true, s));
+    if (logits_host)
+        GAJE_HIP_CHECK(hipMemcpy(logits_host, m->logits, (size_t)m->vocab_out * 4, hipMemcpyDeviceToHost));
+    return GAJE_OK;
+}
+
+extern "C" int gaje_hip_forward_hidden(gaje_hip_model *m, uint32_t token, int clear_cache, float *logits_host,
+                                       float *h_norm_host) {
+    clear_error();
+    GAJE_TRY(check_model(m));
+    DevState s;
+    GAJE_TRY(forward_device(m, token, clear_cache != 0, false, s));
+    if (logits_host)
+        GAJE_HIP_CHECK(hipMemcpy(logits_host, m->logits, (size_t)m->vocab_out * 4, hipMemcpyDeviceToHost));
+    if (h_norm_host)
+        GAJE_HIP_CHECK(hipMemcpy(h_norm_host, m->hnorm, (size_t)m->n_embd * 4, hipMemcpyDeviceToHost));
+    return GAJE_OK;
+}
+
+extern "C" int gaje_hip_clear_cache(gaje_hip_model *m) {
+    GAJE_TRY(check_model(m));
+    m->pos = 0;
+    return GAJE_OK;
+}
+
+extern "C" int gaje_hip_cache_len(const gaje_hip_model *m, int64_t *len) {
+    if (!m || !len) return set_error(GAJE_ERR_INVALID_ARG, "null argument");
+    *len = m->pos;
+    return GAJE_OK;
+}
+
+extern "C" int gaje_hip_set_kwta(gaje_hip_model *m, float ratio) {
+    GAJE_TRY(check_model(m));
+    m->kwta_ratio = ratio;
+    m->block_kwta_ratio = ratio;  // set_k_wta_ratio also sets every block (python.rs:55-57)
+    return GAJE_OK;
+}
+
+extern "C" int gaje_hip_get_kwta(const gaje_hip_model *m, float *ratio) {
+    if (!m || !ratio) return set_error(GAJE_ERR_INVALID_ARG, "null argument");
+    *ratio = m->kwta_ratio;
+    return GAJE_OK;
+}
+
+extern "C" int gaje_hip_reserve(gaje_hip_model *m, int64_t positions) {
+    GAJE_TRY(check_model(m));
+    if (positions < 0) return set_error(GAJE_ERR_INVALID_ARG, "negative reservation");
+    return m->n_layers > 0 ? reserve_ctx(m, positions) : GAJE_OK;
+}
+
+extern "C" int gaje_hip_prefill(gaje_hip_model *m, const uint32_t *ids, int64_t n, float *last_logits_host) {
+    clear_error();
+    GAJE_TRY(check_model(m));
+    if (n < 0 || (n > 0 && !ids)) return set_error(GAJE_ERR_INVALID_ARG, "bad prefill arguments");
+    if (n == 0) return GAJE_OK;
+    GAJE_TRY(reserve_ctx(m, m->pos + n));
+    if (!m->profile) GAJE_TRY(ensure_graph(m));
+    GAJE_TRY(launch_state_set(m->st, (int32_t)m->pos, ids[0], -1, -1, 1, m->stream));
+    for (int64_t i = 0; i < n; ++i) {
+        // after the first token only the input id changes; a halted state stays halted
+        if (i > 0) GAJE_TRY(launch_state_set(m->st, -1, ids[i], -1, -1, 0, m->stream));
+        GAJE_TRY(run_token(m));
+    }
+    if (last_logits_host && m->kwta_ratio > 0.0f && m->kwta_ratio < 1.0f)
+        GAJE_TRY(launch_kwta(m->logits, m->vocab_out, kwta_k(m->vocab_out, m->kwta_ratio), m->st, m->stream));
+    DevState s;
+    GAJE_TRY(read_state(m, s));
+    const int64_t done = (int64_t)s.pos - m->pos;
+    m->pos = s.pos;
+    if (s.halted || s.nan_code != NAN_NONE) {
+        (void)done;
+        return nan_error(s);
+    }
+    if (last_logits_host)
+        GAJE_HIP_CHECK(hipMemcpy(last_logits_host, m->logits, (size_t)m->vocab_out * 4, hipMemcpyDeviceToHost));
+    return GAJE_OK;
+}
+
+extern "C" int gaje_hip_greedy_next(gaje_hip_model *m, uint32_t token, uint32_t *next) {
+    clear_error();
+    GAJE_TRY(check_model(m));
+    if (!next) return set_error(GAJE_ERR_INVALID_ARG, "null output");
+    DevState s;
+    GAJE_TRY(forward_device(m, token, false, false, s));
+    *next = s.token;
+    return GAJE_OK;
+}
+
+extern "C" int gaje_hip_decode_greedy(gaje_hip_model *m, uint32_t first_token, int64_t n, uint32_t *out_tokens) {
+    clear_error();
+    GAJE_TRY(check_model(m));
+    if (n < 0 || (n > 0 && !out_tokens)) return set_error(GAJE_ERR_INVALID_ARG, "bad decode arguments");
+    if (n == 0) return GAJE_OK;
+    GAJE_TRY(reserve_ctx(m, m->pos + n));
+    if (n > m->out_cap) {
+        m->release(m->out_tokens);
+        m->out_cap = n;
+        GAJE_TRY(m->alloc(&m->out_tokens, (size_t)n));
+        drop_graph(m);
+    }
+    if (!m->profile) GAJE_TRY(ensure_graph(m));
+    GAJE_TRY(launch_state_set(m->st, (int32_t)m->pos, first_token, (int32_t)m->out_cap, 0, 1, m->stream));
+    for (int64_t i = 0; i < n; ++i) GAJE_TRY(run_token(m));
+    DevState s;
+    GAJE_HIP_CHECK(hipMemcpyAsync(out_tokens, m->out_tokens, (size_t)n * 4, hipMemcpyDeviceToHost, m->stream));
+    GAJE_TRY(read_state(m, s));
+    m->pos = s.pos;
+    if (s.halted || s.nan_code != NAN_NONE) return nan_error(s);
+    return GAJE_OK;
+}
+
+extern "C" int gaje_hip_generate(gaje_hip_model *m, const uint32_t *prompt, int64_t n_prompt, int64_t max_new,
+                                 float temperature, float repetition_penalty, const uint32_t *eos_ids, int64_t n_eos,
+                                 uint64_t seed, uint32_t *out_tokens, int64_t *n_out) {
+    clear_error();
+    GAJE_TRY(check_model(m));
+    if (n_out) *n_out = 0;
+    if (n_prompt <= 0 || !prompt) return set_error(GAJE_ERR_MODEL, "Prompt tokens cannot be empty");
+    if (max_new < 0 || (max_new > 0 && !out_tokens) || (n_eos > 0 && !eos_ids))
+        return set_error(GAJE_ERR_INVALID_ARG, "bad generate arguments");
+    m->pos = 0;  // clear_cache_core
+    GAJE_TRY(gaje_hip_prefill(m, prompt, n_prompt, nullptr));
+    const bool kwta = m->kwta_ratio > 0.0f && m->kwta_ratio < 1.0f;
+    if (kwta) GAJE_TRY(launch_kwta(m->logits, m->vocab_out, kwta_k(m->vocab_out, m->kwta_ratio), m->st, m->stream));
+    std::vector<float> logits((size_t)m->vocab_out);
+    std::vector<uint32_t> gen;
+    uint64_t rng = seed;
+    auto is_eos = [&](uint32_t t) {
+        for (int64_t i = 0; i < n_eos; ++i)
+            if (eos_ids[i] == t) return true;
+        return false;
+    };
+    for (int64_t step = 0; step < max_new; ++step) {
+        GAJE_HIP_CHECK(hipMemcpyAsync(logits.data(), m->logits, logits.size() * 4, hipMemcpyDeviceToHost, m->stream));
+        GAJE_HIP_CHECK(hipStreamSynchronize(m->stream));
+        if (repetition_penalty > 1.0f) {
+            std::vector<uint32_t> seen;
+            for (uint32_t t : gen)
+                if (!is_eos(t) && std::find(seen.begin(), seen.end(), t) == seen.end()) seen.push_back(t);
+            for (uint32_t t : seen)
+                if (t < logits.size()) {
+                    if (logits[t] < 0.0f) logits[t] *= repetition_penalty;
+                    else logits[t] /= repetition_penalty;
+                }
+        }
+        uint32_t next = 0;
+        if (temperature <= 1e-5f) {
+            float best = -INFINITY;
+            for (size_t i = 0; i < logits.size(); ++i)
+                if (logits[i] > best) {
+                    best = logits[i];
+                    next = (uint32_t)i;
+                }
+        } else {
+            float mx = -INFINITY;
+            for (float v : logits)
+                if (v > mx) mx = v;
+            std::vector<float> probs(logits.size());
+            float sum = 0.0f;
+            for (size_t i = 0; i < logits.size(); ++i) {
+                probs[i] = expf((logits[i] - mx) / temperature);
+                sum += probs[i];
+            }
+            rng += 0x9E3779B97F4A7C15ull;
+            const float u = (float)(mix64(rng) >> 40) * 0x1.0p-24f;
+            const float r = u * sum;
+            float cum = 0.0f;
+            for (size_t i = 0; i < probs.size(); ++i) {
+                cum += probs[i];
+                if (r <= cum) {
+                    next = (uint32_t)i;
+                    break;
+                }
+            }
+        }
+        gen.push_back(next);
+        out_tokens[gen.size() - 1] = next;
+        if (n_out) *n_out = (int64_t)gen.size();
+        if (is_eos(next)) break;
+        bool repeated = false;
+        for (size_t w = 2; w <= 48 && !repeated; ++w) {
+            if (gen.size() >= w * 3) {
+                const size_t n = gen.size();
+                bool same = true;
+                for (size_t i = 0; i < w && same; ++i)
+                    same = gen[n - w + i] == gen[n - 2 * w + i] && gen[n - w + i] == gen[n - 3 * w + i];
+                repeated = same;
+            }
+        }
+        if (repeated) break;
+        DevState s;
+        GAJE_TRY(forward_device(m, next, false, true, s));
+    }
+    return GAJE_OK;
+}
+
+extern "C" int gaje_hip_truncate_cache(gaje_hip_model *m, int64_t len) {
+    GAJE_TRY(check_model(m));
+    if (len < 0 || len > m->pos)
+        return set_error(GAJE_ERR_INVALID_ARG, "cannot truncate a cache of %lld positions to %lld", (long long)m->pos,
+                         (long long)len);
+    m->pos = len;
+    return GAJE_OK;
+}
+
+extern "C" int gaje_hip_time_stage(gaje_hip_model *m, int stage, int64_t layer, int iters, float *avg_ms,
+                                   int64_t *bytes) {
+    clear_error();
+    GAJE_TRY(check_model(m));
+    if (!avg_ms || iters <= 0) return set_error(GAJE_ERR_INVALID_ARG, "bad timing arguments");
+    if (stage >= GAJE_STAGE_QKV && stage <= GAJE_STAGE_DOWN && (layer < 0 || layer >= m->n_layers))
+        return set_error(GAJE_ERR_INVALID_ARG, "layer %lld out of range", (long long)layer);
+    GAJE_TRY(reserve_ctx(m, m->pos + 1));
+    if (stage == GAJE_STAGE_TOKEN) GAJE_TRY(ensure_graph(m));
+    GAJE_TRY(launch_state_set(m->st, (int32_t)m->pos, 0, -1, -1, 1, m->stream));
+    const int64_t nb_q = m->n_embd / 32;
+    const size_t layer_kv = (size_t)m->n_kv * m->cap * m->hd;
+    auto wbytes = [](const DevLinear &D) -> int64_t {
+        const int64_t nb = D.K / 32;
+        int64_t b = D.fmt == FMT_Q4_0 ? D.N * nb * 20 : D.fmt == FMT_LUT4 ? D.N * nb * 16 : D.N * D.K * 4;
+        if (D.fmt == FMT_LUT4 && D.lut) b += (D.lut_block_stride ? (D.lut_rows_own ? D.N : 1) * nb * 16 * 4 : 64);
+        return b;
+    };
+    int64_t algo = 0;
+    auto one = [&]() -> int {
+        switch (stage) {
+            case GAJE_STAGE_QKV:
+            case GAJE_STAGE_O:
+            case GAJE_STAGE_GATE_UP:
+            case GAJE_STAGE_DOWN: {
+                Layer &Ly = m->layers[layer];
+                GemvParams p;
+                if (stage == GAJE_STAGE_QKV) {
+                    p = gemv_base(m, Ly.qkv, m->h);
+                    p.norm_w = Ly.attn_norm;
+                    p.mode = MODE_QKV;
+                    p.y = m->q;
+                    p.q_out = m->q;
+                    p.head_dim = (int32_t)m->hd;
+                    p.rope_split = m->rope_split;
+                    p.q_rows = m->q_rows;
+                    p.kv_rows = m->kv_rows;
+                    p.rope_cos = m->rope_cos;
+                    p.rope_sin = m->rope_sin;
+                    p.k_cache = m->k_cache + layer * layer_kv;
+                    p.v_cache = m->v_cache + layer * layer_kv;
+                    p.kv_head_stride = m->cap * m->hd;
+                    algo = wbytes(Ly.qkv) + (m->n_embd * 2 + m->q_rows + 2 * m->kv_rows) * 4;
+                } else if (stage == GAJE_STAGE_O) {
+                    p = gemv_base(m, Ly.o, m->attn_out);
+                    p.mode = MODE_RESIDUAL;
+                    p.y = m->h;
+                    algo = wbytes(Ly.o) + (m->q_rows + 2 * m->n_embd) * 4;
+                } else if (stage == GAJE_STAGE_GATE_UP) {
+                    p = gemv_base(m, Ly.gate_up, m->h);
+                    p.norm_w = Ly.ffn_norm;
+                    p.mode = MODE_SWIGLU;
+                    p.ffn = m->ffn;
+                    p.y = m->act;
+                    algo = wbytes(Ly.gate_up) + (2 * m->n_embd + m->ffn) * 4;
+                } else {
+                    p = gemv_base(m, Ly.down, m->act);
+                    p.mode = MODE_RESIDUAL;
+                    p.y = m->h;
+                    algo = wbytes(Ly.down) + (m->ffn + 2 * m->n_embd) * 4;
+                }
+                p.layer = (int32_t)layer;
+                return launch_gemv(p, m->stream);
+            }
+            case GAJE_STAGE_ATTENTION: {
+                AttnParams ap;
+                ap.q = m->q;
+                ap.k_cache = m->k_cache + layer * layer_kv;
+                ap.v_cache = m->v_cache + layer * layer_kv;
+                ap.kv_head_stride = m->cap * m->hd;
+                ap.n_head = (int32_t)m->n_head;
+                ap.n_head_kv = (int32_t)m->n_kv;
+                ap.head_dim = (int32_t)m->hd;
+                ap.splits = ATTN_SPLITS;
+                ap.partial = m->attn_part;
+                ap.out = m->attn_out;
+                ap.st = m->st;
+                algo = (int64_t)(m->pos + 1) * 2 * m->kv_rows * 4 + 2 * m->q_rows * 4;
+                return launch_attention(ap, m->stream);
+            }
+            case GAJE_STAGE_LM_HEAD: {
+                GemvParams p = gemv_base(m, m->lm_head, m->h);
+                p.norm_w = m->output_norm;
+                p.mode = MODE_ARGMAX;
+                p.y = m->logits;
+                p.x_out = m->hnorm;
+                p.nontemporal = 1;
+                p.layer = (int32_t)m->n_layers;
+                algo = wbytes(m->lm_head) + (2 * m->n_embd + m->vocab_out) * 4;
+                return launch_gemv(p, m->stream);
+            }
+            case GAJE_STAGE_TOKEN: {
+                int64_t a = wbytes(m->lm_head) + m->n_embd * 4;
+                for (auto &Ly : m->layers) a += wbytes(Ly.qkv) + wbytes(Ly.o) + wbytes(Ly.gate_up) + wbytes(Ly.down);
+                a += m->n_layers * (int64_t)(m->pos + 1) * 2 * m->kv_rows * 4;
+                algo = a;
+                GAJE_HIP_CHECK(hipGraphLaunch(m->graph_exec, m->stream));
+                // keep the position fixed so every replay is the same token
+                return launch_state_set(m->st, (int32_t)m->pos, 0, -1, -1, 1, m->stream);
+            }
+            default:
+                return set_error(GAJE_ERR_INVALID_ARG, "unknown stage %d", stage);
+        }
+    };
+    (void)nb_q;
+    GAJE_TRY(one());  // warm-up launch (also validates the arguments)
+    hipEvent_t e0, e1;
+    GAJE_HIP_CHECK(hipEventCreate(&e0));
+    GAJE_HIP_CHECK(hipEventCreate(&e1));
+    GAJE_HIP_CHECK(hipEventRecord(e0, m->stream));
+    int rc = GAJE_OK;
+    for (int i = 0; i < iters && rc == GAJE_OK; ++i) rc = one();
+    GAJE_HIP_CHECK(hipEventRecord(e1, m->stream));
+    GAJE_HIP_CHECK(hipEventSynchronize(e1));
+    float ms = 0.0f;
+    (void)hipEventElapsedTime(&ms, e0, e1);
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    GAJE_TRY(rc);
+    *avg_ms = ms / (float)iters;
+    if (bytes) *bytes = algo;
+    GAJE_TRY(launch_state_set(m->st, (int32_t)m->pos, 0, -1, -1, 1, m->stream));
+    GAJE_HIP_CHECK(hipStreamSynchronize(m->stream));
+    return GAJE_OK;
+}
+
+extern "C" int gaje_hip_last_timing(const gaje_hip_model *m, float *blocks_ms, float *head_ms) {
+    if (!m) return set_error(GAJE_ERR_INVALID_ARG, "null model");
+    if (blocks_ms) *blocks_ms = m->last_blocks_ms;
+    if (head_ms) *head_ms = m->last_head_ms;
+    return GAJE_OK;
+}

@@ -1,0 +1,15 @@
+"""MI355X (gfx950) implementation of the GAJE quantised decode path.
+
+The compute runs in lib/libgaje_hip.so (hand-written HIP kernels behind the C
+ABI of include/gaje_hip.h); this package is its Python binding, shaped like the
+reference's PyO3 surface (`load_genomic_auto`, `RustGenomicLLM.forward`, ...).
+"""
+from ._lib import (GajeError, GajeIOError, GajeValueError, LIB_PATH, SIGNATURES, last_error,
+                   lib)
+from .model import GenomicLLM, load_genomic_auto
+from . import ops, synth
+
+RustGenomicLLM = GenomicLLM
+
+__all__ = ["GajeError", "GajeIOError", "GajeValueError", "GenomicLLM", "RustGenomicLLM",
+           "LIB_PATH", "SIGNATURES", "last_error", "lib", "load_genomic_auto", "ops", "synth"]

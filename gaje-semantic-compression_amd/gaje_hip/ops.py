@@ -1,0 +1,162 @@
+"""Operator-level API over device buffers (mirrors the reference kernel entry
+points of src/compute/kernels/mod.rs:19-28 one level up: whole matvecs instead
+of single rows)."""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from ._lib import check, lib
+
+
+class DeviceBuffer:
+    """A device allocation made through the C ABI (freed on close / GC)."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        p = ctypes.c_void_p()
+        check(lib().gaje_hip_malloc(ctypes.byref(p), self.nbytes))
+        self.ptr = p.value
+
+    @classmethod
+    def from_array(cls, a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        b.write(a)
+        return b
+
+    def write(self, a: np.ndarray) -> None:
+        a = np.ascontiguousarray(a)
+        if a.nbytes > self.nbytes:
+            raise ValueError("array larger than the device buffer")
+        check(lib().gaje_hip_memcpy_h2d(self.ptr, a.ctypes.data, a.nbytes))
+
+    def read(self, dtype, count: int | None = None) -> np.ndarray:
+        dtype = np.dtype(dtype)
+        n = self.nbytes // dtype.itemsize if count is None else int(count)
+        out = np.empty(n, dtype=dtype)
+        check(lib().gaje_hip_memcpy_d2h(out.ctypes.data, self.ptr, out.nbytes))
+        return out
+
+    def close(self):
+        if getattr(self, "ptr", None):
+            lib().gaje_hip_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def _p(b):
+    return None if b is None else b.ptr
+
+
+def synchronize() -> None:
+    check(lib().gaje_hip_device_synchronize())
+
+
+def device_count() -> int:
+    n = ctypes.c_int()
+    check(lib().gaje_hip_device_count(ctypes.byref(n)))
+    return n.value
+
+
+def device_name(device: int = 0) -> str:
+    buf = ctypes.create_string_buffer(256)
+    check(lib().gaje_hip_device_name(device, buf, 256))
+    return buf.value.decode()
+
+
+def q4_0_gemv(blocks: DeviceBuffer, x: DeviceBuffer, y: DeviceBuffer, n: int, k: int,
+              bias: DeviceBuffer | None = None, bias_len: int = 0, stream=None) -> None:
+    check(lib().gaje_hip_q4_0_gemv(blocks.ptr, x.ptr, _p(bias), bias_len, y.ptr, n, k, stream))
+
+
+def q4_0_gemm(blocks: DeviceBuffer, X: DeviceBuffer, Y: DeviceBuffer, m: int, n: int, k: int,
+              bias: DeviceBuffer | None = None, bias_len: int = 0, stream=None) -> None:
+    check(lib().gaje_hip_q4_0_gemm(blocks.ptr, X.ptr, _p(bias), bias_len, Y.ptr, m, n, k, stream))
+
+
+def lut4_gemv(codes: DeviceBuffer, lut: DeviceBuffer, lut_len: int, x: DeviceBuffer,
+              y: DeviceBuffer, n: int, k: int, bias: DeviceBuffer | None = None,
+              bias_len: int = 0, stream=None) -> None:
+    check(lib().gaje_hip_lut4_gemv(codes.ptr, lut.ptr, lut_len, x.ptr, _p(bias), bias_len, y.ptr,
+                                   n, k, stream))
+
+
+def f32_gemv(w: DeviceBuffer, x: DeviceBuffer, y: DeviceBuffer, n: int, k: int,
+             bias: DeviceBuffer | None = None, bias_len: int = 0, stream=None) -> None:
+    check(lib().gaje_hip_f32_gemv(w.ptr, x.ptr, _p(bias), bias_len, y.ptr, n, k, stream))
+
+
+def q4_0_dequant(blocks: DeviceBuffer, out: DeviceBuffer, nblocks: int, stream=None) -> None:
+    check(lib().gaje_hip_q4_0_dequant(blocks.ptr, out.ptr, nblocks, stream))
+
+
+def rmsnorm(x: DeviceBuffer, w: DeviceBuffer, eps: float, y: DeviceBuffer, n: int, stream=None):
+    check(lib().gaje_hip_rmsnorm(x.ptr, w.ptr, float(eps), y.ptr, n, stream))
+
+
+def swiglu(gate: DeviceBuffer, up: DeviceBuffer, out: DeviceBuffer, n: int, stream=None):
+    check(lib().gaje_hip_swiglu(gate.ptr, up.ptr, out.ptr, n, stream))
+
+
+def kwta(scores: DeviceBuffer, n: int, k: int, stream=None):
+    check(lib().gaje_hip_kwta(scores.ptr, n, k, stream))
+
+
+def argmax(x: DeviceBuffer, n: int, idx: DeviceBuffer, stream=None):
+    check(lib().gaje_hip_argmax(x.ptr, n, idx.ptr, stream))
+
+
+def bench_gemv(fmt: int, w: DeviceBuffer, copy_stride: int, copies: int, x: DeviceBuffer,
+               y: DeviceBuffer, n: int, k: int, iters: int, lut: DeviceBuffer | None = None,
+               lut_stride: int = 0) -> float:
+    """Average ms per launch of the matvec over `copies` weight copies (graph replays)."""
+    ms = ctypes.c_float()
+    check(lib().gaje_hip_bench_gemv(int(fmt), w.ptr, int(copy_stride), _p(lut), int(lut_stride),
+                                    int(copies), x.ptr, y.ptr, int(n), int(k), int(iters),
+                                    ctypes.byref(ms)))
+    return ms.value
+
+
+class Stream:
+    def __init__(self):
+        s = ctypes.c_void_p()
+        check(lib().gaje_hip_stream_create(ctypes.byref(s)))
+        self.handle = s.value
+
+    def synchronize(self):
+        check(lib().gaje_hip_stream_synchronize(self.handle))
+
+    def close(self):
+        if self.handle:
+            lib().gaje_hip_stream_destroy(self.handle)
+            self.handle = None
+
+
+class Event:
+    def __init__(self):
+        e = ctypes.c_void_p()
+        check(lib().gaje_hip_event_create(ctypes.byref(e)))
+        self.handle = e.value
+
+    def record(self, stream=None):
+        check(lib().gaje_hip_event_record(self.handle, stream))
+
+    def synchronize(self):
+        check(lib().gaje_hip_event_synchronize(self.handle))
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = ctypes.c_float()
+        check(lib().gaje_hip_event_elapsed_ms(self.handle, end.handle, ctypes.byref(ms)))
+        return ms.value
+
+    def close(self):
+        if self.handle:
+            lib().gaje_hip_event_destroy(self.handle)
+            self.handle = None

@@ -1,0 +1,260 @@
+/*
+ * gaje_hip.h — C ABI of the MI355X (gfx950) GAJE quantised decode path.
+ *
+ * Each entry point names the reference interface it replaces (paths are in
+ * the erickaguilar/gaje-semantic-compression tree).  A Rust `extern "C"` shim
+ * in the upstream crate binds these from GenomicLinear::forward_core /
+ * GenomicLLM::forward_core; the ctypes mirror in gaje_hip/ binds them for
+ * Python callers.
+ *
+ * Conventions
+ *   - Status: 0 = success, negative = one of the GAJE_ERR_* codes below; the
+ *     message of the last failure on the calling thread is gaje_hip_last_error()
+ *     and carries the reference's own text where one exists.
+ *   - Ownership: host buffers are caller-owned.  Device buffers passed to the
+ *     operator API are caller-owned device pointers.  A model handle owns its
+ *     HBM weights, KV cache, stream and captured graphs.
+ *   - Threading: a model handle is not re-entrant (the reference's &mut self);
+ *     distinct handles are independent, each with its own stream.
+ *   - `stream` arguments are hipStream_t values cast to void*; NULL = the
+ *     default stream.
+ */
+#ifndef GAJE_HIP_H
+#define GAJE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- status -- */
+enum {
+    GAJE_OK = 0,
+    GAJE_ERR_INVALID_ARG = -1,   /* bad argument (null pointer, size out of range)        */
+    GAJE_ERR_IO = -2,            /* std::io::Error from open/mmap (flat_reader.rs:33-35)  */
+    GAJE_ERR_TOO_SHORT = -3,     /* HeaderError::TooShort (header/types.rs:16)            */
+    GAJE_ERR_INVALID_MAGIC = -4, /* HeaderError::InvalidMagic (header/types.rs:17)        */
+    GAJE_ERR_INVALID_DATA = -5,  /* io::ErrorKind::InvalidData: utf-8/JSON (flat_reader.rs:47-55,125-126) */
+    GAJE_ERR_NOT_FOUND = -6,     /* io::ErrorKind::NotFound: missing tensor (flat_reader.rs:93-98) */
+    GAJE_ERR_NAN = -7,           /* Err("NaN ...") guards of RustGenomicBlock::forward_core */
+    GAJE_ERR_MODEL = -8,         /* other Err(String): "LM Head out_features is 0!", "Prompt tokens cannot be empty" */
+    GAJE_ERR_UNSUPPORTED = -9,   /* a tensor format this build does not run (Q8_0, 2-bit) */
+    GAJE_ERR_HIP = -10,          /* HIP runtime failure */
+    GAJE_ERR_NO_DEVICE = -11     /* no usable gfx950 device */
+};
+
+/* Message of the last failure on this thread (thread-local copy). */
+const char *gaje_hip_last_error(void);
+
+/* --------------------------------------------------------------- runtime -- */
+/* Thin device-memory / stream / event helpers so that a foreign caller (the
+ * Rust shim, ctypes) can drive the operator API without its own HIP binding. */
+int gaje_hip_device_count(int *count);
+int gaje_hip_set_device(int device);
+int gaje_hip_device_name(int device, char *buf, size_t buflen);
+int gaje_hip_malloc(void **ptr, size_t bytes);
+int gaje_hip_free(void *ptr);
+int gaje_hip_memcpy_h2d(void *dst, const void *src, size_t bytes);
+int gaje_hip_memcpy_d2h(void *dst, const void *src, size_t bytes);
+int gaje_hip_memcpy_d2d(void *dst, const void *src, size_t bytes);
+int gaje_hip_memset(void *dst, int value, size_t bytes);
+int gaje_hip_device_synchronize(void);
+int gaje_hip_stream_create(void **stream);
+int gaje_hip_stream_destroy(void *stream);
+int gaje_hip_stream_synchronize(void *stream);
+int gaje_hip_event_create(void **event);
+int gaje_hip_event_destroy(void *event);
+int gaje_hip_event_record(void *event, void *stream);
+int gaje_hip_event_synchronize(void *event);
+int gaje_hip_event_elapsed_ms(void *start, void *stop, float *ms);
+
+/* ------------------------------------------------------ operator API ------ */
+/* All pointers are device pointers; y/out are overwritten.  k = in_features,
+ * n = out_features; row i of a Q4_0 tensor is blocks [i*(k/32), (i+1)*(k/32)).
+ * bias may be NULL; rows i < bias_len add bias[i] (compute_single_row's
+ * `self.bias.get(i)`, linear/forward.rs:113-115). */
+
+/* One Q4_0 matvec over 20-byte Q4_0Block rows: GenomicLinear::forward_core on
+ * the GenomicQ4_0 variant (linear/forward.rs:84-92,119-132) with the per-row
+ * genomic_dot_product_q4_0 (compute/kernels/genomic.rs:210-336), including its
+ * |t| < 1e-6 -> 0 flush before the bias add. */
+int gaje_hip_q4_0_gemv(const void *blocks, const float *x, const float *bias, int64_t bias_len,
+                       float *y, int64_t n, int64_t k, void *stream);
+
+/* The same Q4_0 matvec for m activation rows at once (Y[m][n] = X[m][k] W^T):
+ * m independent GenomicLinear::forward_core calls sharing one weight read.
+ * No reference function batches rows; semantics are per row as above. */
+int gaje_hip_q4_0_gemm(const void *blocks, const float *X, const float *bias, int64_t bias_len,
+                       float *Y, int64_t m, int64_t n, int64_t k, void *stream);
+
+/* LUT-4bit matvec (layout Genomic4Bit, high nibble = even element):
+ * genomic_dot_product_4bit (genomic.rs:148-204) over the row slicing of
+ * linear/forward.rs:59-83.  lut_len floats as stored in the file: 16 (one
+ * table), k/32*16 (one per block column) or >= n*k/32*16 (per row and block),
+ * i.e. the expansion of linear/init.rs:109-124. */
+int gaje_hip_lut4_gemv(const uint8_t *codes, const float *lut, int64_t lut_len, const float *x,
+                       const float *bias, int64_t bias_len, float *y, int64_t n, int64_t k,
+                       void *stream);
+
+/* FP32 matvec (lm_head, GenomicF32 rows): dot_product per row
+ * (compute/kernels/dot.rs:23-94 via linear/forward.rs:20-32). */
+int gaje_hip_f32_gemv(const float *w, const float *x, const float *bias, int64_t bias_len,
+                      float *y, int64_t n, int64_t k, void *stream);
+
+/* Bit-exact Q4_0Block::dequantize_weight (io/header/blocks.rs:18-30) of
+ * nblocks whole blocks into out[nblocks*32]. */
+int gaje_hip_q4_0_dequant(const void *blocks, float *out, int64_t nblocks, void *stream);
+
+/* rms_norm (compute/kernels/norm.rs:17-131): y = (x * inv_rms) * w. */
+int gaje_hip_rmsnorm(const float *x, const float *w, float eps, float *y, int64_t n, void *stream);
+
+/* swiglu_balanced (compute/kernels/activation.rs:35-51). */
+int gaje_hip_swiglu(const float *gate, const float *up, float *out, int64_t n, void *stream);
+
+/* lateral_inhibition_kwta (compute/kernels/lut.rs:45-61), in place. */
+int gaje_hip_kwta(float *scores, int64_t n, int64_t k, void *stream);
+
+/* Greedy argmax with the reference's strict '>' (first maximum, NaN never
+ * wins, all -inf/NaN -> 0): llm/forward.rs:262-271.  *idx is a device u32. */
+int gaje_hip_argmax(const float *x, int64_t n, uint32_t *idx, void *stream);
+
+/* --------------------------------------------------------- model API ------ */
+typedef struct gaje_hip_model gaje_hip_model;
+
+typedef struct {
+    int64_t n_embd, n_head, n_head_kv, n_blocks, head_dim, ffn, vocab_size;
+    float eps, rope_base;
+    int32_t rope_split;          /* 1 = "split" rope_style, 0 = interleaved */
+    int32_t arch_family;         /* header arch_family (0 = none)           */
+    int32_t body_format;         /* 1 = Q4_0 blocks, 2 = LUT-4bit           */
+    int32_t use_genomic_norm;
+    int64_t max_ctx;             /* KV capacity currently allocated          */
+    int64_t weight_bytes;        /* bytes of weights resident in HBM         */
+    int64_t n_logits;            /* lm_head out_features (length of logits)  */
+} gaje_hip_model_info;
+
+/* load_genomic_auto for a .gaje.flat file (io/flat_reader.rs:240-252 ->
+ * GajeFlatFileReader::open/load_genomic :33-236): mmap, header, metadata and
+ * directory, ArchitectureDescriptor-over-JSON precedence, one upload per tensor
+ * into HBM in its native packing.  k_wta_ratio starts at 0.5 (:234). */
+int gaje_hip_open(const char *flat_path, int device, gaje_hip_model **out);
+void gaje_hip_close(gaje_hip_model *m);
+int gaje_hip_model_info_get(const gaje_hip_model *m, gaje_hip_model_info *info);
+
+/* GenomicLLM::forward_core (nn/llm/forward.rs:7-64): one token through every
+ * block, output norm, lm_head and (0 < ratio < 1) K-WTA; logits_host[vocab]. */
+int gaje_hip_forward(gaje_hip_model *m, uint32_t token, int clear_cache, float *logits_host);
+
+/* GenomicLLM::forward_with_hidden_core (nn/llm/forward.rs:76-113): logits
+ * without K-WTA plus the normalised hidden state h_norm_host[n_embd]. */
+int gaje_hip_forward_hidden(gaje_hip_model *m, uint32_t token, int clear_cache, float *logits_host,
+                            float *h_norm_host);
+
+/* GenomicLLM::clear_cache_core (nn/llm/forward.rs:174-178). */
+int gaje_hip_clear_cache(gaje_hip_model *m);
+
+/* Number of cached positions (GenomicAttention::k_cache_len, attention.rs:134). */
+int gaje_hip_cache_len(const gaje_hip_model *m, int64_t *len);
+
+/* set_k_wta_ratio (nn/llm/python.rs:53-59): sets the LLM ratio and every
+ * block's ratio. */
+int gaje_hip_set_kwta(gaje_hip_model *m, float ratio);
+int gaje_hip_get_kwta(const gaje_hip_model *m, float *ratio);
+
+/* Reserve KV capacity for at least `positions` cached tokens (the reference's
+ * cache is an unbounded Vec; this only pre-sizes the device buffers). */
+int gaje_hip_reserve(gaje_hip_model *m, int64_t positions);
+
+/* Token-by-token prefill (nn/llm/forward.rs:229-232): ids[0..n) through
+ * forward_core in order; last_logits_host (may be NULL) gets the last
+ * token's K-WTA-filtered logits. */
+int gaje_hip_prefill(gaje_hip_model *m, const uint32_t *ids, int64_t n, float *last_logits_host);
+
+/* One greedy step on device: forward(token) then argmax of the logits
+ * (nn/llm/forward.rs:262-271); no logits cross PCIe. */
+int gaje_hip_greedy_next(gaje_hip_model *m, uint32_t token, uint32_t *next);
+
+/* Fixed-length greedy loop of benchmarks/performance/gaje_flat_benchmark.py:94-96:
+ * out[0] = argmax(forward(first)), out[i] = argmax(forward(out[i-1])), all on
+ * device (graph replays, no host round trip per token). */
+int gaje_hip_decode_greedy(gaje_hip_model *m, uint32_t first_token, int64_t n, uint32_t *out_tokens);
+
+/* generate_native_core (nn/llm/forward.rs:215-330): clear, prefill, then up to
+ * max_new tokens with repetition penalty, greedy (temperature <= 1e-5) or
+ * multinomial sampling (seeded here; upstream uses thread_rng), EOS stop and
+ * the repetition-loop detector.  *n_out receives the number generated. */
+int gaje_hip_generate(gaje_hip_model *m, const uint32_t *prompt, int64_t n_prompt, int64_t max_new,
+                      float temperature, float repetition_penalty, const uint32_t *eos_ids,
+                      int64_t n_eos, uint64_t seed, uint32_t *out_tokens, int64_t *n_out);
+
+/* Per-stage device times of the last forward, if GAJE_HIP_PROFILE is set
+ * (the reference's GAJE_PROFILE_VERBOSE timers, nn/llm/forward.rs:50-55). */
+int gaje_hip_last_timing(const gaje_hip_model *m, float *blocks_ms, float *head_ms);
+
+/* Benchmark helpers (no reference counterpart; the reference's benchmarks
+ * time whole forward calls from Python, benchmarks/performance/bench_decode.py). */
+
+/* Keep only the first `len` cached positions (len <= current length): lets a
+ * benchmark replay the same decode from a fixed prompt state. */
+int gaje_hip_truncate_cache(gaje_hip_model *m, int64_t len);
+
+enum {
+    GAJE_STAGE_QKV = 1,        /* rms_norm + fused QKV GEMV + RoPE + KV append */
+    GAJE_STAGE_ATTENTION = 2,  /* split-K GQA decode attention                 */
+    GAJE_STAGE_O = 3,          /* attn_output GEMV + residual                  */
+    GAJE_STAGE_GATE_UP = 4,    /* rms_norm + ffn_gate_up GEMV + SwiGLU          */
+    GAJE_STAGE_DOWN = 5,       /* ffn_down GEMV + residual                     */
+    GAJE_STAGE_LM_HEAD = 6,    /* output rms_norm + f32 lm_head GEMV + argmax  */
+    GAJE_STAGE_TOKEN = 7       /* one whole captured decode step               */
+};
+/* Average device time of `iters` back-to-back launches of one stage's kernel
+ * with the model's own arguments (layer selects the block), measured with HIP
+ * events on the model stream; *bytes gets the stage's algorithmic HBM bytes
+ * (weights + activations in/out + KV read).  Overwrites the activations and
+ * the cache slot of the next position, which the next forward rewrites. */
+int gaje_hip_time_stage(gaje_hip_model *m, int stage, int64_t layer, int iters, float *avg_ms,
+                        int64_t *bytes);
+
+/* Average device time per launch of the operator matvec for `format`
+ * (1 = Q4_0, 2 = LUT-4bit with per-row tables, 0 = f32) over `copies` weight
+ * copies laid out `copy_stride` bytes apart (copy i of the LUT tables at
+ * lut_base + i * lut_stride), cycling through the copies so that the set can
+ * exceed the caches.  The launches are captured once in a HIP graph and
+ * replayed until `iters` launches ran; timed with HIP events on a private
+ * stream. */
+int gaje_hip_bench_gemv(int format, const void *w_base, size_t copy_stride, const float *lut_base,
+                        size_t lut_stride, int copies, const float *x, float *y, int64_t n, int64_t k,
+                        int iters, float *avg_ms);
+
+/* ----------------------------------------------- synthetic .flat writer --- */
+/* Random-init model writer for the benchmark shapes (no checkpoints exist in
+ * this environment).  Writes the .gaje.flat v2 layout of
+ * scripts/export_gaje_flat.py:184-483 with a counter-based PRNG. */
+typedef struct {
+    int64_t n_embd, n_head, n_head_kv, n_blocks, ffn, vocab_size;
+    float eps, rope_base;          /* rope_base goes to the metadata JSON        */
+    int32_t arch_family;           /* header descriptor; 0 = JSON-only config    */
+    int32_t qkv_bias;              /* 1 = write an N(0,0.02) bias for attn_qkv   */
+    int32_t tied_embeddings;       /* 1 = lm_head rows equal token_embd rows     */
+    int32_t body_format;           /* 1 = Q4_0 blocks, 2 = LUT-4bit per row/block */
+    int32_t fused;                 /* 1 = attn_qkv / ffn_gate_up, 0 = split      */
+    int32_t rope_interleaved;      /* metadata rope_style "interleaved" (else "split") */
+    int32_t use_genomic_norm;      /* metadata config.use_genomic_norm           */
+    int32_t pad_;
+    uint64_t seed;
+} gaje_synth_config;
+
+int gaje_synth_write_flat(const char *path, const gaje_synth_config *cfg);
+/* Standalone tensors with the same recipe (row-major, k = in_features). */
+int gaje_synth_q4_0(uint64_t seed, const char *name, int64_t n, int64_t k, uint8_t *blocks_out);
+int gaje_synth_lut4(uint64_t seed, const char *name, int64_t n, int64_t k, uint8_t *codes_out,
+                    float *lut_out);
+int gaje_synth_normal(uint64_t seed, const char *name, int64_t count, float mean, float stddev,
+                      float *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GAJE_HIP_H */

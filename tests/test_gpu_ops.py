@@ -1,0 +1,186 @@
+"""GPU parity of the operator-level kernels against the CPU oracle.
+
+Tolerances (stated by the task for this path):
+  - dequantisation: bit-exact against Q4_0Block::dequantize_weight;
+  - matvec outputs: floored max relative error <= 1e-4 (conftest.floored_rel_err);
+  - K-WTA / argmax: exact (integer / selection results).
+"""
+import numpy as np
+import pytest
+
+from conftest import floored_rel_err
+
+pytestmark = pytest.mark.gpu
+
+GEMV_TOL = 1e-4
+
+
+@pytest.fixture(scope="module")
+def hip():
+    import gaje_hip
+    from gaje_hip import ops
+    if ops.device_count() < 1:
+        pytest.fail("no HIP device visible")
+    return gaje_hip
+
+
+@pytest.fixture(scope="module")
+def O():
+    from oracle import oracle
+    return oracle
+
+
+def _dev(hip, a):
+    return hip.ops.DeviceBuffer.from_array(a)
+
+
+def _out(hip, nbytes):
+    return hip.ops.DeviceBuffer(nbytes)
+
+
+def test_dequant_bit_exact_c0(hip, O):
+    blocks = hip.synth.q4_0_tensor(1, "c0.w", 4864, 896)
+    nb = blocks.size // 20
+    d = _dev(hip, blocks)
+    out = _out(hip, nb * 32 * 4)
+    hip.ops.q4_0_dequant(d, out, nb)
+    got = out.read(np.float32)
+    ref = O.q4_0_dequant(blocks)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_dequant_all_codes_and_f16_edges(hip, O):
+    # every code 0..15 against scale/min pairs that include subnormal, negative
+    # zero and large f16 values
+    hs = np.array([0x0000, 0x8000, 0x0001, 0x03FF, 0x3C00, 0x7BFF, 0xBC00, 0x2E66, 0x1400],
+                  dtype=np.uint16)
+    blocks = []
+    for s in hs:
+        for m in hs:
+            b = np.zeros(20, dtype=np.uint8)
+            b[0:2] = np.frombuffer(np.uint16(s).tobytes(), np.uint8)
+            b[2:4] = np.frombuffer(np.uint16(m).tobytes(), np.uint8)
+            b[4:20] = [(2 * i) % 16 | (((2 * i + 1) % 16) << 4) for i in range(16)]
+            blocks.append(b)
+    blocks = np.concatenate(blocks)
+    nb = blocks.size // 20
+    d = _dev(hip, blocks)
+    out = _out(hip, nb * 128)
+    hip.ops.q4_0_dequant(d, out, nb)
+    got = out.read(np.float32)
+    ref = O.q4_0_dequant(blocks)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def _oracle_q4_rows(O, blocks, x, n, k, bias=None):
+    L = O.GenomicLinear(blocks, b"", None, n, k, bias, 4)
+    return L.forward_core(x)
+
+
+@pytest.mark.parametrize("n,k", [(4864, 896), (1152, 896), (896, 4864), (963, 576), (17, 1536),
+                                 (64, 8960), (33, 2048), (5, 32), (3, 15360)])
+def test_q4_0_gemv(hip, O, n, k):
+    blocks = hip.synth.q4_0_tensor(11, f"gemv.{n}.{k}", n, k)
+    x = hip.synth.normal(12, f"x.{k}", k)
+    bias = hip.synth.normal(13, f"b.{n}", n // 2, 0.0, 0.02)  # shorter than n: rows >= len get none
+    y = _out(hip, n * 4)
+    hip.ops.q4_0_gemv(_dev(hip, blocks), _dev(hip, x), y, n, k, bias=_dev(hip, bias) if bias.size else None,
+                      bias_len=bias.size)
+    got = y.read(np.float32)
+    ref = _oracle_q4_rows(O, blocks, x, n, k, bias)
+    print(f"q4_0 gemv n={n} k={k} err={floored_rel_err(got, ref):.3e}")
+    assert floored_rel_err(got, ref) <= GEMV_TOL
+
+
+def test_q4_0_gemv_flush_rule(hip, O):
+    # rows built to cancel exactly: the reference flushes |t| < 1e-6 to 0 before the bias
+    k = 64
+    blk = np.zeros(20, dtype=np.uint8)
+    blk[0:2] = np.frombuffer(np.float16(0.0).tobytes(), np.uint8)
+    blk[2:4] = np.frombuffer(np.float16(1e-3).tobytes(), np.uint8)  # every weight = min = 1e-3
+    blocks = np.concatenate([blk, blk])
+    x = np.zeros(k, np.float32)
+    x[0], x[1] = 1e-4, -1e-4 + 1e-7  # dot = 1e-10: flushed
+    bias = np.array([0.5], np.float32)
+    y = _out(hip, 4)
+    hip.ops.q4_0_gemv(_dev(hip, blocks), _dev(hip, x), y, 1, k, bias=_dev(hip, bias), bias_len=1)
+    got = y.read(np.float32)
+    ref = _oracle_q4_rows(O, blocks, x, 1, k, bias)
+    assert got[0] == ref[0] == np.float32(0.5)
+
+
+@pytest.mark.parametrize("n,k,table", [(4864, 896, "row"), (300, 896, "shared16"), (300, 576, "block"),
+                                       (129, 4864, "row")])
+def test_lut4_gemv(hip, O, n, k, table):
+    codes, lut = hip.synth.lut4_tensor(21, f"lut.{n}.{k}", n, k)
+    nb = k // 32
+    if table == "shared16":
+        lut = lut[:16].copy()
+    elif table == "block":
+        lut = lut[: nb * 16].copy()
+    x = hip.synth.normal(22, f"xl.{k}", k)
+    y = _out(hip, n * 4)
+    hip.ops.lut4_gemv(_dev(hip, codes), _dev(hip, lut), lut.size, _dev(hip, x), y, n, k)
+    got = y.read(np.float32)
+    L = O.GenomicLinear(codes, b"", lut, n, k, None, 4)
+    ref = L.forward_core(x)
+    print(f"lut4 gemv n={n} k={k} table={table} err={floored_rel_err(got, ref):.3e}")
+    assert floored_rel_err(got, ref) <= GEMV_TOL
+
+
+@pytest.mark.parametrize("n,k", [(151936, 896), (49152, 576), (1001, 1536), (3, 64)])
+def test_f32_gemv(hip, O, n, k):
+    w = hip.synth.normal(31, f"w.{n}.{k}", n * k, 0.0, 0.02)
+    x = hip.synth.normal(32, f"xf.{k}", k)
+    y = _out(hip, n * 4)
+    hip.ops.f32_gemv(_dev(hip, w), _dev(hip, x), y, n, k)
+    got = y.read(np.float32)
+    L = O.GenomicLinear(w.view(np.uint8), b"", None, n, k, None, 32)
+    ref = L.forward_core(x)
+    print(f"f32 gemv n={n} k={k} err={floored_rel_err(got, ref):.3e}")
+    assert floored_rel_err(got, ref) <= GEMV_TOL
+
+
+@pytest.mark.parametrize("n", [576, 896, 1536, 7])
+def test_rmsnorm(hip, O, n):
+    x = hip.synth.normal(41, f"rx.{n}", n, 0.0, 3.0)
+    w = hip.synth.normal(42, f"rw.{n}", n, 1.0, 0.1)
+    y = _out(hip, n * 4)
+    hip.ops.rmsnorm(_dev(hip, x), _dev(hip, w), 1e-6, y, n)
+    got = y.read(np.float32)
+    ref = O.rms_norm(x, w, 1e-6)
+    assert floored_rel_err(got, ref) <= 1e-5
+
+
+def test_swiglu(hip, O):
+    n = 4864
+    g = hip.synth.normal(51, "g", n, 0.0, 30.0)
+    g[:4] = [-100.0, 100.0, -64.0, 0.0]  # the clamp boundaries of activation.rs:40
+    u = hip.synth.normal(52, "u", n)
+    out = _out(hip, n * 4)
+    hip.ops.swiglu(_dev(hip, g), _dev(hip, u), out, n)
+    got = out.read(np.float32)
+    ref = O.swiglu_balanced(g, u)
+    assert floored_rel_err(got, ref) <= 1e-5
+
+
+@pytest.mark.parametrize("n,ratio", [(151936, 0.5), (896, 0.5), (1000, 0.1), (64, 0.99)])
+def test_kwta_exact(hip, O, n, ratio):
+    x = hip.synth.normal(61, f"k.{n}", n)
+    x[::7] = x[3]  # ties at many positions
+    k = max(int(np.float32(n) * np.float32(ratio)), 1)
+    d = _dev(hip, x)
+    hip.ops.kwta(d, n, k)
+    got = d.read(np.float32)
+    ref = O.kwta(x, k)
+    assert np.array_equal(got, ref)
+
+
+def test_argmax_first_max(hip, O):
+    x = hip.synth.normal(71, "am", 151936)
+    x[[5, 90000, 120000]] = 7.5  # repeated maximum: the first index wins
+    x[10] = np.nan
+    d = _dev(hip, x)
+    idx = _out(hip, 4)
+    hip.ops.argmax(d, x.size, idx)
+    assert int(idx.read(np.uint32)[0]) == O.argmax_first(x) == 5
