@@ -232,6 +232,29 @@ extern "C" int gaje_hip_swiglu(const float *gate, const float *up, float *out, i
     return launch_swiglu(gate, up, out, n, as_stream(stream));
 }
 
+extern "C" int gaje_hip_expf(const float *x, float *y, int64_t n, void *stream) {
+    return launch_expf(x, y, n, as_stream(stream));
+}
+
+extern "C" int gaje_hip_attention(const float *q, const float *k_cache, const float *v_cache, int64_t seq_len,
+                                  int64_t capacity, int n_head, int n_head_kv, int head_dim, float *out,
+                                  void *stream) {
+    AttnParams p;
+    memset(&p, 0, sizeof p);
+    p.q = q;
+    p.k_cache = k_cache;
+    p.v_cache = v_cache;
+    p.kv_head_stride = capacity * head_dim;
+    p.n_head = n_head;
+    p.n_head_kv = n_head_kv;
+    p.head_dim = head_dim;
+    p.max_ctx = capacity;
+    p.out = out;
+    p.st = nullptr;
+    p.ctx = seq_len;
+    return launch_attention(p, as_stream(stream));
+}
+
 extern "C" int gaje_hip_kwta(float *scores, int64_t n, int64_t k, void *stream) {
     return launch_kwta(scores, n, k, nullptr, as_stream(stream));
 }

@@ -5,6 +5,7 @@
 
 #include <cstdint>
 
+#include "expf_ref.h"
 #include "kernels.h"
 
 namespace gaje {
@@ -85,19 +86,57 @@ __device__ __forceinline__ void nan_flag(DevState *st, int layer, int stage) {
     if (st && stage >= 0) atomicMin(&st->nan_code, (uint32_t)(layer * 8 + stage));
 }
 
-// swiglu_balanced for one element (activation.rs:40-49).
+// swiglu_balanced for one element (activation.rs:40-49), with the reference's
+// exponential (expf_ref) and every operation rounded as written there.
 __device__ __forceinline__ float swiglu1(float g, float u) {
     float gs = g;
     if (gs < -64.0f) gs = -64.0f;
     if (gs > 64.0f) gs = 64.0f;
     float sig;
     if (gs >= 0.0f) {
-        sig = 1.0f / (1.0f + expf(-gs));
+        const float den = 1.0f + expf_ref(-gs);
+        sig = 1.0f / den;
     } else {
-        float ex = expf(gs);
-        sig = ex / (1.0f + ex);
+        const float ex = expf_ref(gs);
+        const float den = 1.0f + ex;
+        sig = ex / den;
     }
-    return (g * sig) * u;
+    const float silu = g * sig;
+    return silu * u;
+}
+
+// rms_norm of xs[0..n) in place (norm.rs:52-88): sum of squares in eight FMA
+// chains over 8-float chunks, reduced ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7)),
+// scalar tail, inv = 1/sqrt(ss/n + eps), out = (x * inv) * w.
+// Called by every thread of the block (it contains a barrier).
+__device__ inline void rmsnorm_inplace(float *xs, int64_t n, const float *w, float eps, float *inv_slot) {
+    const int tid = threadIdx.x;
+    if (tid < 8) {
+        float acc = 0.0f;
+        const int64_t chunks = n / 8;
+        for (int64_t i = 0; i < chunks; ++i) {
+            const float v = xs[8 * i + tid];
+            acc = fmaf(v, v, acc);
+        }
+        const float u = acc + __shfl(acc, (tid + 4) & 7, 8);  // lane l<4: a_l + a_{l+4}
+        const float v = u + __shfl(u, (tid + 1) & 7, 8);      // lane 0: u0+u1, lane 2: u2+u3
+        const float tot = v + __shfl(v, (tid + 2) & 7, 8);    // lane 0: (u0+u1) + (u2+u3)
+        if (tid == 0) {
+            float ss = tot;
+            for (int64_t i = chunks * 8; i < n; ++i) {
+                const float sq = xs[i] * xs[i];
+                ss = ss + sq;
+            }
+            const float mean = ss / (float)n;
+            *inv_slot = 1.0f / sqrtf(mean + eps);
+        }
+    }
+    __syncthreads();
+    const float inv = *inv_slot;
+    for (int64_t k = tid; k < n; k += blockDim.x) {
+        const float t = xs[k] * inv;
+        xs[k] = t * w[k];
+    }
 }
 
 }  // namespace gaje

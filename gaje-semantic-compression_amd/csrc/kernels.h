@@ -26,7 +26,6 @@ struct DevState {
     uint32_t nan_code;         // min(layer * 8 + stage) over failed guards
     int32_t out_cap;           // capacity of the greedy output buffer
     unsigned long long argmax_key;  // packed (orderable logit, ~index) maximum
-    uint32_t attn_counter[64];      // last-workgroup counters, one per KV head
 };
 
 // NaN guard stages of RustGenomicBlock::forward_core (block/forward.rs).
@@ -100,12 +99,15 @@ struct AttnParams {
     const float *k_cache, *v_cache;  // this layer: [n_kv][max_ctx][head_dim]
     int64_t kv_head_stride;
     int32_t n_head, n_head_kv, head_dim;
-    int32_t splits;
-    float *partial;          // [n_head][splits][head_dim + 2]
+    int64_t max_ctx;         // KV capacity (sizes the LDS score buffer)
     float *out;              // [n_head * head_dim]
-    DevState *st;
+    DevState *st;            // positions 0..st->pos are attended; if null, 0..ctx-1
+    int64_t ctx;
 };
 int launch_attention(const AttnParams &p, hipStream_t s);
+size_t attention_lds_bytes(int head_dim, int64_t max_ctx);
+// Largest KV capacity whose scores fit the attention kernel's LDS buffer.
+constexpr int64_t MAX_CTX = 12288;
 
 struct EmbedParams {
     const uint8_t *w;
@@ -125,10 +127,11 @@ int launch_argmax(const float *x, int64_t n, uint32_t *idx, hipStream_t s);
 int launch_dequant_q4_0(const uint8_t *blocks, float *out, int64_t nblocks, hipStream_t s);
 int launch_rmsnorm(const float *x, const float *w, float eps, float *y, int64_t n, hipStream_t s);
 int launch_swiglu(const float *g, const float *u, float *out, int64_t n, hipStream_t s);
+int launch_expf(const float *x, float *y, int64_t n, hipStream_t s);
 int launch_fill_u32(uint32_t *p, uint32_t v, int64_t n, hipStream_t s);
 // Host-driven state update ordered on the stream.  Negative pos / out_cap /
 // step keep the current value; reset_guards clears halted, nan_code and the
-// argmax (and, with pos == 0, the attention counters).
+// argmax.
 int launch_state_set(DevState *st, int32_t pos, uint32_t token, int32_t out_cap, int32_t step, int reset_guards,
                      hipStream_t s);
 

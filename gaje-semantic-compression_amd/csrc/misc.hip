@@ -72,10 +72,6 @@ __global__ void state_set_kernel(DevState *st, int32_t pos, uint32_t token, int3
     }
 }
 
-__global__ void state_clear_counters_kernel(DevState *st) {
-    for (int i = threadIdx.x; i < 64; i += blockDim.x) st->attn_counter[i] = 0u;
-}
-
 // lateral_inhibition_kwta (src/compute/kernels/lut.rs:45-61): the k-th largest
 // value by a 4-pass radix select over orderable keys, then x < thr -> -1e9.
 __global__ __launch_bounds__(1024) void kwta_kernel(float *x, int64_t n, int64_t k, DevState *st) {
@@ -152,16 +148,17 @@ __global__ void dequant_q4_0_kernel(const uint8_t *blocks, float *out, int64_t n
 }
 
 __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float *x, const float *w, float eps, float *y, int64_t n) {
-    __shared__ float part[16];
-    float ss = 0.0f;
-    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) ss = fmaf(x[i], x[i], ss);
-    ss = wave_sum(ss);
-    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+    extern __shared__ __align__(16) float xs[];
+    __shared__ float inv_slot;
+    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) xs[i] = x[i];
     __syncthreads();
-    float tot = 0.0f;
-    for (int i = 0; i < (int)(blockDim.x >> 6); ++i) tot += part[i];
-    const float inv = 1.0f / sqrtf(tot / (float)n + eps);
-    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) y[i] = (x[i] * inv) * w[i];
+    rmsnorm_inplace(xs, n, w, eps, &inv_slot);
+    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) y[i] = xs[i];
+}
+
+__global__ void expf_kernel(const float *x, float *y, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        y[i] = expf_ref(x[i]);
 }
 
 __global__ void swiglu_kernel(const float *g, const float *u, float *out, int64_t n) {
@@ -199,10 +196,6 @@ int launch_state_set(DevState *st, int32_t pos, uint32_t token, int32_t out_cap,
                      hipStream_t s) {
     hipLaunchKernelGGL(state_set_kernel, dim3(1), dim3(1), 0, s, st, pos, token, out_cap, step, reset_guards);
     GAJE_HIP_CHECK(hipGetLastError());
-    if (pos == 0 && reset_guards) {
-        hipLaunchKernelGGL(state_clear_counters_kernel, dim3(1), dim3(64), 0, s, st);
-        GAJE_HIP_CHECK(hipGetLastError());
-    }
     return GAJE_OK;
 }
 
@@ -231,7 +224,16 @@ int launch_dequant_q4_0(const uint8_t *blocks, float *out, int64_t nblocks, hipS
 
 int launch_rmsnorm(const float *x, const float *w, float eps, float *y, int64_t n, hipStream_t s) {
     if (!x || !w || !y || n <= 0) return set_error(GAJE_ERR_INVALID_ARG, "rmsnorm: bad arguments");
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(1024), 0, s, x, w, eps, y, n);
+    if (n * 4 + 1024 > 64 * 1024) return set_error(GAJE_ERR_UNSUPPORTED, "rmsnorm: n = %lld too large", (long long)n);
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(1024), (size_t)n * 4, s, x, w, eps, y, n);
+    GAJE_HIP_CHECK(hipGetLastError());
+    return GAJE_OK;
+}
+
+int launch_expf(const float *x, float *y, int64_t n, hipStream_t s) {
+    if (n < 0 || (n > 0 && (!x || !y))) return set_error(GAJE_ERR_INVALID_ARG, "expf: bad arguments");
+    if (n == 0) return GAJE_OK;
+    hipLaunchKernelGGL(expf_kernel, dim3(grid_for(n, 256)), dim3(256), 0, s, x, y, n);
     GAJE_HIP_CHECK(hipGetLastError());
     return GAJE_OK;
 }

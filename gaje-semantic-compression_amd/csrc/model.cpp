@@ -32,7 +32,6 @@
 namespace gaje {
 namespace {
 
-constexpr int ATTN_SPLITS = 32;
 constexpr int64_t DEFAULT_CTX = 1024;
 
 struct HostLinear {
@@ -252,8 +251,7 @@ struct gaje_hip_model {
     std::vector<Layer> layers;
 
     // activations and scratch
-    float *h = nullptr, *q = nullptr, *attn_out = nullptr, *act = nullptr, *logits = nullptr, *hnorm = nullptr,
-          *attn_part = nullptr;
+    float *h = nullptr, *q = nullptr, *attn_out = nullptr, *act = nullptr, *logits = nullptr, *hnorm = nullptr;
     DevState *st = nullptr;
     uint32_t *out_tokens = nullptr;
     int64_t out_cap = 0;
@@ -396,8 +394,11 @@ void drop_graph(gaje_hip_model *m) {
 // Grow the KV cache and RoPE table to hold `positions` tokens.
 int reserve_ctx(gaje_hip_model *m, int64_t positions) {
     if (positions <= m->cap) return GAJE_OK;
+    if (positions > MAX_CTX)
+        return set_error(GAJE_ERR_UNSUPPORTED, "context of %lld positions exceeds this build's limit of %lld",
+                         (long long)positions, (long long)MAX_CTX);
     int64_t cap = std::max<int64_t>(positions, m->cap ? 2 * m->cap : DEFAULT_CTX);
-    cap = (cap + 63) / 64 * 64;
+    cap = std::min<int64_t>((cap + 63) / 64 * 64, MAX_CTX);
     const int64_t L = std::max<int64_t>(m->n_layers, 1);
     const size_t per_head_new = (size_t)cap * m->hd, per_head_old = (size_t)m->cap * m->hd;
     float *kc, *vc, *rc, *rs;
@@ -474,8 +475,7 @@ int enqueue_token(gaje_hip_model *m, hipEvent_t ev_blocks_done) {
         ap.n_head = (int32_t)m->n_head;
         ap.n_head_kv = (int32_t)m->n_kv;
         ap.head_dim = (int32_t)m->hd;
-        ap.splits = ATTN_SPLITS;
-        ap.partial = m->attn_part;
+        ap.max_ctx = m->cap;
         ap.out = m->attn_out;
         ap.st = m->st;
         GAJE_TRY(launch_attention(ap, m->stream));
@@ -728,7 +728,6 @@ extern "C" int gaje_hip_open(const char *path, int device, gaje_hip_model **out)
     GAJE_TRY(m->alloc(&m->attn_out, (size_t)qn));
     GAJE_TRY(m->alloc(&m->act, (size_t)std::max<int64_t>(m->ffn, 1)));
     GAJE_TRY(m->alloc(&m->logits, (size_t)m->vocab_out));
-    GAJE_TRY(m->alloc(&m->attn_part, (size_t)std::max<int64_t>(m->n_head, 1) * ATTN_SPLITS * (m->hd + 2)));
     GAJE_TRY(m->alloc(&m->st, 1));
     GAJE_HIP_CHECK(hipMemset(m->st, 0, sizeof(DevState)));
     m->out_cap = 4096;
@@ -1051,8 +1050,7 @@ extern "C" int gaje_hip_time_stage(gaje_hip_model *m, int stage, int64_t layer, 
                 ap.n_head = (int32_t)m->n_head;
                 ap.n_head_kv = (int32_t)m->n_kv;
                 ap.head_dim = (int32_t)m->hd;
-                ap.splits = ATTN_SPLITS;
-                ap.partial = m->attn_part;
+                ap.max_ctx = m->cap;
                 ap.out = m->attn_out;
                 ap.st = m->st;
                 algo = (int64_t)(m->pos + 1) * 2 * m->kv_rows * 4 + 2 * m->q_rows * 4;

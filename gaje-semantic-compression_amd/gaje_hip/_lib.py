@@ -92,6 +92,9 @@ SIGNATURES = [
     ("gaje_hip_q4_0_dequant", ctypes.c_int, [c_vp, c_vp, c_i64, c_vp]),
     ("gaje_hip_rmsnorm", ctypes.c_int, [c_vp, c_vp, ctypes.c_float, c_vp, c_i64, c_vp]),
     ("gaje_hip_swiglu", ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp]),
+    ("gaje_hip_expf", ctypes.c_int, [c_vp, c_vp, c_i64, c_vp]),
+    ("gaje_hip_attention", ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_i64, ctypes.c_int, ctypes.c_int,
+                                          ctypes.c_int, c_vp, c_vp]),
     ("gaje_hip_kwta", ctypes.c_int, [c_vp, c_i64, c_i64, c_vp]),
     ("gaje_hip_argmax", ctypes.c_int, [c_vp, c_i64, c_vp, c_vp]),
     ("gaje_hip_open", ctypes.c_int, [ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(c_vp)]),

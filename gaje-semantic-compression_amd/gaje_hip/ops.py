@@ -105,6 +105,17 @@ def swiglu(gate: DeviceBuffer, up: DeviceBuffer, out: DeviceBuffer, n: int, stre
     check(lib().gaje_hip_swiglu(gate.ptr, up.ptr, out.ptr, n, stream))
 
 
+def expf(x: DeviceBuffer, y: DeviceBuffer, n: int, stream=None):
+    check(lib().gaje_hip_expf(x.ptr, y.ptr, n, stream))
+
+
+def attention(q: DeviceBuffer, k_cache: DeviceBuffer, v_cache: DeviceBuffer, seq_len: int,
+              capacity: int, n_head: int, n_head_kv: int, head_dim: int, out: DeviceBuffer,
+              stream=None):
+    check(lib().gaje_hip_attention(q.ptr, k_cache.ptr, v_cache.ptr, seq_len, capacity, n_head,
+                                   n_head_kv, head_dim, out.ptr, stream))
+
+
 def kwta(scores: DeviceBuffer, n: int, k: int, stream=None):
     check(lib().gaje_hip_kwta(scores.ptr, n, k, stream))
 

@@ -113,6 +113,18 @@ int gaje_hip_rmsnorm(const float *x, const float *w, float eps, float *y, int64_
 /* swiglu_balanced (compute/kernels/activation.rs:35-51). */
 int gaje_hip_swiglu(const float *gate, const float *up, float *out, int64_t n, void *stream);
 
+/* f32::exp as the reference calls it (attention.rs:106, activation.rs:42-44):
+ * the host C library's expf, reproduced bit for bit on the device. */
+int gaje_hip_expf(const float *x, float *y, int64_t n, void *stream);
+
+/* The GQA softmax attention of GenomicAttention::forward_attention_core
+ * (nn/attention.rs:87-127) over seq_len cached positions, bit-exact.  q is
+ * [n_head][head_dim] (already rotated); the caches are head-major
+ * [n_head_kv][capacity][head_dim] (positions 0..seq_len-1 used); out is
+ * [n_head][head_dim]. */
+int gaje_hip_attention(const float *q, const float *k_cache, const float *v_cache, int64_t seq_len,
+                       int64_t capacity, int n_head, int n_head_kv, int head_dim, float *out, void *stream);
+
 /* lateral_inhibition_kwta (compute/kernels/lut.rs:45-61), in place. */
 int gaje_hip_kwta(float *scores, int64_t n, int64_t k, void *stream);
 

@@ -30,6 +30,12 @@
 
 #define Q4_0_BLOCK_BYTES 20 /* repr(C, packed) {f16 scale, f16 min, u8 qs[16]} */
 
+/* The exponential of attention.rs:106 and activation.rs:42-44 (f32::exp ->
+ * the C library's expf); overridable only to study sensitivity. */
+#ifndef ORC_EXPF
+#define ORC_EXPF expf
+#endif
+
 static inline float h2f(uint16_t h) { return _cvtsh_ss(h); }
 
 /* Host capability check: the restatement is only the reference's x86 path
@@ -61,6 +67,12 @@ int orc_get_threads(void) {
 /* half::f16::to_f32 / from_f32 (half 2.4.1): exact widening, RNE narrowing. */
 float orc_f16_to_f32(uint16_t h) { return h2f(h); }
 uint16_t orc_f32_to_f16(float f) { return _cvtss_sh(f, _MM_FROUND_TO_NEAREST_INT); }
+
+/* f32::exp as the reference calls it (attention.rs:106, activation.rs:42-44). */
+void orc_expf_batch(const float *x, float *y, size_t n) {
+#pragma omp parallel for schedule(static)
+    for (size_t i = 0; i < n; i++) y[i] = ORC_EXPF(x[i]);
+}
 
 /* Q4_0Block::dequantize_weight — src/io/header/blocks.rs:18-30.
  * Even index = low nibble; w = f32(q)*scale + min as a mul then an add. */
@@ -263,9 +275,9 @@ void orc_swiglu_balanced(const float *gate, const float *up, float *out, size_t 
         if (gs > 64.0f) gs = 64.0f;
         float sig;
         if (gs >= 0.0f) {
-            sig = 1.0f / (1.0f + expf(-gs));
+            sig = 1.0f / (1.0f + ORC_EXPF(-gs));
         } else {
-            float ex = expf(gs);
+            float ex = ORC_EXPF(gs);
             sig = ex / (1.0f + ex);
         }
         float silu = g * sig;
@@ -335,7 +347,7 @@ void orc_attention(const float *q_rope, const float *k_cache, const float *v_cac
         }
         float sum_e = 0.0f;
         for (size_t t = 0; t < seq_len; t++) {
-            scores[t] = expf(scores[t] - max_s);
+            scores[t] = ORC_EXPF(scores[t] - max_s);
             sum_e += scores[t];
         }
         float inv_s = 1.0f / (sum_e + 1e-12f);

@@ -82,6 +82,7 @@ def lib():
         L.orc_f16_to_f32.restype = ctypes.c_float
         L.orc_f32_to_f16.argtypes = [ctypes.c_float]
         L.orc_f32_to_f16.restype = ctypes.c_uint16
+        L.orc_expf_batch.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]
         L.orc_q4_0_dequant_weight.argtypes = [ctypes.c_void_p, ctypes.c_int]
         L.orc_q4_0_dequant_weight.restype = ctypes.c_float
         L.orc_q4_0_dequant.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
@@ -138,6 +139,23 @@ def f16_to_f32(h: int) -> float:
 
 def f32_to_f16(f: float) -> int:
     return lib().orc_f32_to_f16(f)
+
+
+def expf(x: np.ndarray) -> np.ndarray:
+    """f32::exp as the reference calls it: the host C library's expf."""
+    x = _f32(x)
+    y = np.empty_like(x)
+    lib().orc_expf_batch(_ptr(x), _ptr(y), x.size)
+    return y
+
+
+def attention(q, k_cache, v_cache, seq_len, n_head, n_head_kv, head_dim):
+    """forward_attention_core's attention over an appended cache (attention.rs:87-127);
+    caches are [seq_len][n_head_kv * head_dim]."""
+    q, k, v = _f32(q), _f32(k_cache), _f32(v_cache)
+    out = np.empty(n_head * head_dim, dtype=np.float32)
+    lib().orc_attention(_ptr(q), _ptr(k), _ptr(v), seq_len, n_head, n_head_kv, head_dim, _ptr(out))
+    return out
 
 
 def q4_0_dequant(blocks: np.ndarray) -> np.ndarray:

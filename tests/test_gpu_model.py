@@ -1,10 +1,11 @@
 """GPU parity of the whole decode path against the CPU oracle.
 
-Bars (stated by the task for this path):
-  - logits: floored max relative error <= 1e-4 per token (conftest.floored_rel_err);
-  - greedy argmax: must agree wherever the oracle's top-2 margin exceeds the
-    tolerance times |logit|; at the first step where it does not, the two runs
-    may legitimately diverge and the comparison stops there.
+The device path reproduces the reference's rounding sequence end to end
+(matvec accumulation orders, RMSNorm, RoPE table, glibc expf, the serial softmax
+sums), so logits must match the oracle bit for bit and greedy decoding must
+produce the same tokens.  That is stricter than the task's bars (floored max
+relative error <= 1e-4 on logits, argmax agreement where the top-2 margin exceeds
+the tolerance); the floored error is printed for information.
 """
 import os
 import struct
@@ -53,6 +54,12 @@ def _margin_ok(logits, tol=TOL):
     return (v[0] - v[1]) > tol * abs(v[0])
 
 
+def same_bits(a, b) -> bool:
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
 def _tokens(n, vocab, seed):
     return [int(t) for t in np.random.default_rng(seed).integers(0, vocab, n)]
 
@@ -67,11 +74,12 @@ def _compare_stream(hip, O, path, tokens, kwta=0.0, hidden=False):
         if hidden:
             gl, gh = g.forward_with_hidden(t, i == 0)
             rl, rh = r.forward_with_hidden_core(t, i == 0)
-            worst = max(worst, floored_rel_err(gh, rh))
+            assert same_bits(gh, rh), f"h_norm differs at token {i}"
         else:
             gl = g.forward(t, i == 0)
             rl = r.forward_core(t, i == 0)
         worst = max(worst, floored_rel_err(gl, rl))
+        assert same_bits(gl, rl), f"logits differ at token {i} (floored rel err {worst:.2e})"
     assert g.cache_len() == len(tokens) == r.blocks[0].attn.k_cache_len()
     g.close()
     return worst
@@ -89,23 +97,15 @@ def test_tiny_forward_with_hidden(hip, O, tiny):
 
 
 def test_tiny_kwta_logits(hip, O, tiny):
-    """K-WTA on (the flat-load default 0.5): filtered sets agree away from the threshold."""
+    """K-WTA on (the flat-load default 0.5, flat_reader.rs:234)."""
     g = hip.load_genomic_auto(tiny)
     r = O.load_genomic(tiny)
     assert abs(g.k_wta_ratio - 0.5) < 1e-7 and r.k_wta_ratio == 0.5
     for i, t in enumerate(_tokens(5, TINY["vocab_size"], 3)):
         gl = g.forward(t, i == 0)
-        r.set_k_wta_ratio(0.0)
-        raw = r.forward_core(t, i == 0)
-        n = raw.size
-        k = max(int(np.float32(n) * np.float32(0.5)), 1)
-        thr = np.sort(raw)[::-1][k - 1]
-        near = np.abs(raw - thr) <= 1e-4 * np.max(np.abs(raw))
-        kept_g = gl != np.float32(-1e9)
-        kept_r = raw >= thr
-        assert np.array_equal(kept_g[~near], kept_r[~near])
-        both = kept_g & kept_r
-        assert floored_rel_err(gl[both], raw[both]) <= TOL
+        rl = r.forward_core(t, i == 0)
+        assert (rl == np.float32(-1e9)).sum() == TINY["vocab_size"] // 2
+        assert same_bits(gl, rl)
     g.close()
 
 
@@ -115,9 +115,10 @@ def test_tiny_block_kwta(hip, O, tiny):
     r = O.load_genomic(tiny)
     g.set_k_wta_ratio(0.75)
     r.set_k_wta_ratio(0.75)
-    gl, _ = g.forward_with_hidden(7, True)
-    rl, _ = r.forward_with_hidden_core(7, True)
-    assert floored_rel_err(gl, rl) <= 1e-3
+    for i, t in enumerate([7, 11, 13]):
+        gl = g.forward(t, i == 0)
+        rl = r.forward_core(t, i == 0)
+        assert same_bits(gl, rl)
     g.close()
 
 
@@ -131,9 +132,7 @@ def _check_greedy(gen, O, path, first, n, prompt=None):
     for i in range(n):
         logits = r.forward_core(tok, prompt is None and i == 0)
         ref = O.argmax_first(logits)
-        if gen[i] != ref:
-            assert not _margin_ok(logits), f"greedy mismatch at step {i} with a clear margin"
-            return i
+        assert gen[i] == ref, f"greedy token differs at step {i} (margin ok: {_margin_ok(logits)})"
         tok = ref
     return n
 
@@ -176,22 +175,8 @@ def test_tiny_generate_greedy_matches_oracle(hip, O, tiny):
     got = g.generate_native_py(prompt, max_new_tokens=40, temperature=0.0,
                                repetition_penalty=penalty, eos_token_ids=[2])
     ref = r.generate_native_core(prompt, 40, 0.0, penalty, [2])
-    k = 0
-    while k < min(len(got), len(ref)) and got[k] == ref[k]:
-        k += 1
-    print(f"generate: {len(got)} vs {len(ref)} tokens, common prefix {k}")
-    if k == len(got) == len(ref):
-        return
-    assert k < min(len(got), len(ref)), "one run stopped early although every token agreed"
-    # first divergence: only acceptable at a near-tie of the penalised reference logits
-    r.clear_cache_core()
-    logits = None
-    for t in prompt + ref[:k]:
-        logits = r.forward_core(t, False)
-    logits = logits.copy()
-    for t in set(ref[:k]) - {2}:
-        logits[t] = logits[t] * np.float32(penalty) if logits[t] < 0 else logits[t] / np.float32(penalty)
-    assert not _margin_ok(logits), f"generate diverged at step {k} with a clear margin"
+    print(f"generate: {len(got)} vs {len(ref)} tokens")
+    assert got == ref
     g.close()
 
 
@@ -238,7 +223,7 @@ def test_nan_embedding_row_raises(hip, O, tmp_models, tiny):
     # a clean token afterwards works (the halted state is cleared per call)
     g.set_k_wta_ratio(0.0)
     r.set_k_wta_ratio(0.0)
-    assert floored_rel_err(g.forward(5, True), r.forward_core(5, True)) <= TOL
+    assert same_bits(g.forward(5, True), r.forward_core(5, True))
     g.close()
 
 
@@ -251,7 +236,7 @@ def test_kv_growth_preserves_cache(hip, O, tiny):
     for i, t in enumerate(tokens):
         if i == 6:
             g.reserve(5000)  # reallocates and copies the cache mid-sequence
-        assert floored_rel_err(g.forward(t, i == 0), r.forward_core(t, i == 0)) <= TOL
+        assert same_bits(g.forward(t, i == 0), r.forward_core(t, i == 0))
     g.close()
 
 

@@ -1,14 +1,20 @@
 """GPU parity of the operator-level kernels against the CPU oracle.
 
-Tolerances (stated by the task for this path):
-  - dequantisation: bit-exact against Q4_0Block::dequantize_weight;
-  - matvec outputs: floored max relative error <= 1e-4 (conftest.floored_rel_err);
-  - K-WTA / argmax: exact (integer / selection results).
+Every kernel reproduces the reference's rounding sequence, so the bar is
+bit-for-bit equality with the oracle (the AVX2 restatement of the reference),
+which is stricter than the task's floored 1e-4 relative-error tolerance
+(conftest.floored_rel_err, printed for information).
 """
 import numpy as np
 import pytest
 
 from conftest import floored_rel_err
+
+
+def same_bits(a, b) -> bool:
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 pytestmark = pytest.mark.gpu
 
@@ -89,7 +95,7 @@ def test_q4_0_gemv(hip, O, n, k):
     got = y.read(np.float32)
     ref = _oracle_q4_rows(O, blocks, x, n, k, bias)
     print(f"q4_0 gemv n={n} k={k} err={floored_rel_err(got, ref):.3e}")
-    assert floored_rel_err(got, ref) <= GEMV_TOL
+    assert same_bits(got, ref)
 
 
 def test_q4_0_gemv_flush_rule(hip, O):
@@ -125,10 +131,10 @@ def test_lut4_gemv(hip, O, n, k, table):
     L = O.GenomicLinear(codes, b"", lut, n, k, None, 4)
     ref = L.forward_core(x)
     print(f"lut4 gemv n={n} k={k} table={table} err={floored_rel_err(got, ref):.3e}")
-    assert floored_rel_err(got, ref) <= GEMV_TOL
+    assert same_bits(got, ref)
 
 
-@pytest.mark.parametrize("n,k", [(151936, 896), (49152, 576), (1001, 1536), (3, 64)])
+@pytest.mark.parametrize("n,k", [(151936, 896), (49152, 576), (1001, 1536), (3, 64), (5, 12), (7, 100)])
 def test_f32_gemv(hip, O, n, k):
     w = hip.synth.normal(31, f"w.{n}.{k}", n * k, 0.0, 0.02)
     x = hip.synth.normal(32, f"xf.{k}", k)
@@ -138,7 +144,7 @@ def test_f32_gemv(hip, O, n, k):
     L = O.GenomicLinear(w.view(np.uint8), b"", None, n, k, None, 32)
     ref = L.forward_core(x)
     print(f"f32 gemv n={n} k={k} err={floored_rel_err(got, ref):.3e}")
-    assert floored_rel_err(got, ref) <= GEMV_TOL
+    assert same_bits(got, ref)
 
 
 @pytest.mark.parametrize("n", [576, 896, 1536, 7])
@@ -149,7 +155,7 @@ def test_rmsnorm(hip, O, n):
     hip.ops.rmsnorm(_dev(hip, x), _dev(hip, w), 1e-6, y, n)
     got = y.read(np.float32)
     ref = O.rms_norm(x, w, 1e-6)
-    assert floored_rel_err(got, ref) <= 1e-5
+    assert same_bits(got, ref)
 
 
 def test_swiglu(hip, O):
@@ -161,7 +167,7 @@ def test_swiglu(hip, O):
     hip.ops.swiglu(_dev(hip, g), _dev(hip, u), out, n)
     got = out.read(np.float32)
     ref = O.swiglu_balanced(g, u)
-    assert floored_rel_err(got, ref) <= 1e-5
+    assert same_bits(got, ref)
 
 
 @pytest.mark.parametrize("n,ratio", [(151936, 0.5), (896, 0.5), (1000, 0.1), (64, 0.99)])
@@ -184,3 +190,37 @@ def test_argmax_first_max(hip, O):
     idx = _out(hip, 4)
     hip.ops.argmax(d, x.size, idx)
     assert int(idx.read(np.uint32)[0]) == O.argmax_first(x) == 5
+
+
+def test_expf_device_matches_host_libm(hip, O):
+    """The device exponential against the host expf on 16.7M inputs spread over
+    the whole float range, plus the special values."""
+    u = np.arange(0, 2 ** 32, 257, dtype=np.uint64).astype(np.uint32)
+    x = u.view(np.float32)
+    x = np.concatenate([x, np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 88.72283, 88.72284, -103.97208,
+                                     -103.97209, -87.33655, 1e-30, -1e-30], np.float32)])
+    d = _dev(hip, x)
+    out = _out(hip, x.nbytes)
+    hip.ops.expf(d, out, x.size)
+    got = out.read(np.float32)
+    ref = O.expf(x)
+    nan = np.isnan(ref) & np.isnan(got)
+    assert np.array_equal(got.view(np.uint32)[~nan], ref.view(np.uint32)[~nan])
+
+
+@pytest.mark.parametrize("ctx,n_head,n_kv,hd", [(1, 14, 2, 64), (768, 14, 2, 64), (384, 9, 3, 64),
+                                                 (1152, 12, 2, 128), (77, 4, 4, 16)])
+def test_attention_bit_exact(hip, O, ctx, n_head, n_kv, hd):
+    q = hip.synth.normal(81, f"aq.{ctx}.{hd}", n_head * hd)
+    k = hip.synth.normal(82, f"ak.{ctx}.{hd}", ctx * n_kv * hd)
+    v = hip.synth.normal(83, f"av.{ctx}.{hd}", ctx * n_kv * hd)
+    ref = O.attention(q, k, v, ctx, n_head, n_kv, hd)
+    cap = ctx + 5
+    kh = np.zeros((n_kv, cap, hd), np.float32)  # head-major device layout
+    vh = np.zeros((n_kv, cap, hd), np.float32)
+    kh[:, :ctx] = k.reshape(ctx, n_kv, hd).transpose(1, 0, 2)
+    vh[:, :ctx] = v.reshape(ctx, n_kv, hd).transpose(1, 0, 2)
+    out = _out(hip, n_head * hd * 4)
+    hip.ops.attention(_dev(hip, q), _dev(hip, kh), _dev(hip, vh), ctx, cap, n_head, n_kv, hd, out)
+    got = out.read(np.float32)
+    assert same_bits(got, ref)
