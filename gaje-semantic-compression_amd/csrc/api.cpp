@@ -2,6 +2,8 @@
 // Model entry points live in model.cpp, the synthetic writer in synth.cpp.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <atomic>
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -26,6 +28,22 @@ int set_error(int code, const char *fmt, ...) {
 }
 
 void clear_error() { g_last_error.clear(); }
+
+size_t max_lds_per_block() {
+    // The kernels are validated with at most 64 KiB of LDS per workgroup.
+    static std::atomic<size_t> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 64 * 1024;
+    size_t v = cache[dev].load(std::memory_order_relaxed);
+    if (!v) {
+        int a = 0;
+        if (hipDeviceGetAttribute(&a, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || a <= 0)
+            a = 64 * 1024;
+        v = std::min<size_t>((size_t)a, 64 * 1024);
+        cache[dev].store(v, std::memory_order_relaxed);
+    }
+    return v;
+}
 
 }  // namespace gaje
 
@@ -179,18 +197,28 @@ extern "C" int gaje_hip_event_elapsed_ms(void *start, void *stop, float *ms) {
 
 // ------------------------------------------------------------- operators --
 
-extern "C" int gaje_hip_q4_0_gemv(const void *blocks, const float *x, const float *bias, int64_t bias_len, float *y,
-                                  int64_t n, int64_t k, void *stream) {
-    GAJE_TRY(check_dims(n, k));
-    return launch_gemv(plain_gemv(FMT_Q4_0, blocks, x, bias, bias_len, y, n, k), as_stream(stream));
+extern "C" int64_t gaje_hip_q4_0_packed_bytes(int64_t n, int64_t k) {
+    if (n < 0 || k <= 0 || k % 32 != 0) return -1;
+    return q4_0_packed_bytes(n, k);
 }
 
-extern "C" int gaje_hip_q4_0_gemm(const void *blocks, const float *X, const float *bias, int64_t bias_len, float *Y,
+extern "C" int gaje_hip_q4_0_pack(const void *blocks, void *packed, int64_t n, int64_t k, void *stream) {
+    GAJE_TRY(check_dims(n, k));
+    return launch_pack_q4_0((const uint8_t *)blocks, (uint8_t *)packed, n, k, as_stream(stream));
+}
+
+extern "C" int gaje_hip_q4_0_gemv(const void *packed, const float *x, const float *bias, int64_t bias_len, float *y,
+                                  int64_t n, int64_t k, void *stream) {
+    GAJE_TRY(check_dims(n, k));
+    return launch_gemv(plain_gemv(FMT_Q4_0, packed, x, bias, bias_len, y, n, k), as_stream(stream));
+}
+
+extern "C" int gaje_hip_q4_0_gemm(const void *packed, const float *X, const float *bias, int64_t bias_len, float *Y,
                                   int64_t m, int64_t n, int64_t k, void *stream) {
     GAJE_TRY(check_dims(n, k));
     if (m < 0 || (m > 0 && (!X || !Y))) return set_error(GAJE_ERR_INVALID_ARG, "bad gemm arguments");
     for (int64_t r = 0; r < m; ++r)
-        GAJE_TRY(launch_gemv(plain_gemv(FMT_Q4_0, blocks, X + r * k, bias, bias_len, Y + r * n, n, k), as_stream(stream)));
+        GAJE_TRY(launch_gemv(plain_gemv(FMT_Q4_0, packed, X + r * k, bias, bias_len, Y + r * n, n, k), as_stream(stream)));
     return GAJE_OK;
 }
 
@@ -248,7 +276,7 @@ extern "C" int gaje_hip_attention(const float *q, const float *k_cache, const fl
     p.n_head = n_head;
     p.n_head_kv = n_head_kv;
     p.head_dim = head_dim;
-    p.max_ctx = capacity;
+    p.kv_cap = capacity;
     p.out = out;
     p.st = nullptr;
     p.ctx = seq_len;

@@ -60,6 +60,19 @@ __device__ __forceinline__ uint32_t ld_u32(const void *p) {
 }
 
 typedef float vf4 __attribute__((ext_vector_type(4)));
+typedef uint32_t vu2 __attribute__((ext_vector_type(2)));
+typedef uint32_t vu4 __attribute__((ext_vector_type(4)));
+
+template <bool NT>
+__device__ __forceinline__ vu2 ld_u2(const uint8_t *p) {
+    if constexpr (NT) return __builtin_nontemporal_load((const vu2 *)p);
+    else return *(const vu2 *)p;
+}
+template <bool NT>
+__device__ __forceinline__ vu4 ld_u4(const uint8_t *p) {
+    if constexpr (NT) return __builtin_nontemporal_load((const vu4 *)p);
+    else return *(const vu4 *)p;
+}
 
 template <bool NT>
 __device__ __forceinline__ float4 ld_f4(const float *p) {
@@ -114,7 +127,15 @@ __device__ inline void rmsnorm_inplace(float *xs, int64_t n, const float *w, flo
     if (tid < 8) {
         float acc = 0.0f;
         const int64_t chunks = n / 8;
-        for (int64_t i = 0; i < chunks; ++i) {
+        int64_t i = 0;
+        for (; i + 8 <= chunks; i += 8) {  // eight LDS reads in flight, then the chain
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = xs[8 * (i + u) + tid];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc = fmaf(v[u], v[u], acc);
+        }
+        for (; i < chunks; ++i) {
             const float v = xs[8 * i + tid];
             acc = fmaf(v, v, acc);
         }

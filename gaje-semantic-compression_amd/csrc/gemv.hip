@@ -20,8 +20,13 @@
 // rows and chains: LPR lanes cooperate on one row (one or more chains each) and
 // walk the row's blocks in order; 2*LPR lanes hold a row pair (the RoPE / SwiGLU
 // partners or two consecutive rows), so the pair's epilogue runs in one lane.
-// The activation vector sits in LDS; weights stream straight from HBM in their
-// file packing.
+// The time of a launch is the length of one lane's instruction stream, so the
+// Q4_0 rows use a packed layout (below) that gives each chain lane its codes in
+// one 8-byte load per four blocks, and the activations sit in LDS in chain-major
+// order so a lane reads a block's four inputs with one 16-byte LDS read.  A
+// lane's first weight loads are issued before the prologue and then run 8-16
+// groups ahead of the arithmetic; the epilogue's operands (bias, residual,
+// RoPE factors) are loaded while the row is computed.
 #include "common.h"
 #include "device_util.h"
 
@@ -31,6 +36,7 @@ namespace {
 
 constexpr int THREADS = 256;
 constexpr int MAX_GRID = 8192;
+constexpr int Q4_PREFETCH = 8;  // packed groups (4 blocks each) in flight per lane, short rows
 
 __device__ __forceinline__ void pair_rows(const GemvParams &p, int64_t pr, int64_t &r0, int64_t &r1) {
     if (p.mode == MODE_QKV) {
@@ -55,63 +61,229 @@ __device__ __forceinline__ void pair_rows(const GemvParams &p, int64_t pr, int64
 
 __device__ __forceinline__ float shfl(float v, int src) { return __shfl(v, src, WAVE); }
 
-// ---------------------------------------------------------------- Q4_0 ----
-// LPR = 8: lane s owns chain s.  LPR = 4: lane p owns chains 2p and 2p+1.
-template <int LPR, bool NT>
-__device__ __forceinline__ float row_q4_0(const GemvParams &p, const float *xs, int64_t row, int s, int base) {
-    constexpr int CH = 8 / LPR;  // chains per lane
-    float acc[CH];
+// Activation vector in LDS.  Q4_0 rows read it chain-major: element k sits at
+// (k % 8) * stride + k / 8, so chain l's inputs are one contiguous LDS row.
+struct XView {
+    float *x;
+    int stride;  // 0: plain layout
+    __device__ __forceinline__ float &at(int64_t k) const {
+        return stride ? x[(k & 7) * stride + (k >> 3)] : x[k];
+    }
+};
+
+// ------------------------------------------------------------- Q4_0 ----
+// Packed device layout of a Q4_0 row: groups of four Q4_0Blocks (128 weights,
+// 80 bytes, the file's own size), written once when the weights are uploaded:
+//   bytes [8l, 8l+8)  chain l (l = 0..7): dword h covers blocks 4g+2h (low
+//                     nibbles) and 4g+2h+1 (high nibbles); byte c holds the code
+//                     of element 8c+l of its block
+//   bytes [64, 80)    the four blocks' (scale | min << 16) words
+// Blocks past nb in a row's last group are zero and are never read.
+// Dequantises the four codes of one block for chain l: fma(q, scale, min).
+__device__ __forceinline__ void q4_dequant(float (&d)[4], uint32_t codes, uint32_t sm) {
+    const float scale = half_lo(sm), mn = half_hi(sm);
+    d[0] = fmaf(ubyte0(codes), scale, mn);
+    d[1] = fmaf(ubyte1(codes), scale, mn);
+    d[2] = fmaf(ubyte2(codes), scale, mn);
+    d[3] = fmaf(ubyte3(codes), scale, mn);
+}
+
+__device__ __forceinline__ float q4_chain(float acc, const float (&d)[4], const float4 x) {
+    acc = fmaf(d[0], x.x, acc);
+    acc = fmaf(d[1], x.y, acc);
+    acc = fmaf(d[2], x.z, acc);
+    acc = fmaf(d[3], x.w, acc);
+    return acc;
+}
+
+// One full packed group (blocks 4g .. 4g+3): the sixteen dequantised values
+// are formed before the chain consumes them, so the LDS reads of x and the
+// conversions overlap instead of alternating with the dependent FMAs.
+__device__ __forceinline__ float q4_group(float acc, const vu2 n, const vu4 s, const float *xg) {
+    const float4 x0 = *(const float4 *)(xg), x1 = *(const float4 *)(xg + 4);
+    const float4 x2 = *(const float4 *)(xg + 8), x3 = *(const float4 *)(xg + 12);
+    float d0[4], d1[4], d2[4], d3[4];
+    q4_dequant(d0, opaque_and(n.x, 0x0F0F0F0Fu), s.x);
+    q4_dequant(d1, opaque_and(n.x >> 4, 0x0F0F0F0Fu), s.y);
+    q4_dequant(d2, opaque_and(n.y, 0x0F0F0F0Fu), s.z);
+    q4_dequant(d3, opaque_and(n.y >> 4, 0x0F0F0F0Fu), s.w);
+    acc = q4_chain(acc, d0, x0);
+    acc = q4_chain(acc, d1, x1);
+    acc = q4_chain(acc, d2, x2);
+    acc = q4_chain(acc, d3, x3);
+    return acc;
+}
+
+// A row's last group with nblk (1..4) blocks.
+__device__ __forceinline__ float q4_group_tail(float acc, const vu2 n, const vu4 s, const float *xg, int nblk) {
+    float d[4];
+    q4_dequant(d, opaque_and(n.x, 0x0F0F0F0Fu), s.x);
+    acc = q4_chain(acc, d, *(const float4 *)(xg));
+    if (nblk > 1) {
+        q4_dequant(d, opaque_and(n.x >> 4, 0x0F0F0F0Fu), s.y);
+        acc = q4_chain(acc, d, *(const float4 *)(xg + 4));
+    }
+    if (nblk > 2) {
+        q4_dequant(d, opaque_and(n.y, 0x0F0F0F0Fu), s.z);
+        acc = q4_chain(acc, d, *(const float4 *)(xg + 8));
+    }
+    if (nblk > 3) {
+        q4_dequant(d, opaque_and(n.y >> 4, 0x0F0F0F0Fu), s.w);
+        acc = q4_chain(acc, d, *(const float4 *)(xg + 12));
+    }
+    return acc;
+}
+
+// Register ring of D packed groups of one row (this lane's chain bytes and
+// the group's scale/min words).
+template <int D>
+struct Q4Ring {
+    vu2 n[D];
+    vu4 s[D];
+};
+
+// Issues the loads of the row's first D groups.  A row shorter than D groups
+// reads into the next row or the tensor's tail padding (Q4_TAIL_PAD); those
+// values are never used.
+template <bool NT, int D>
+__device__ __forceinline__ void q4_prefetch(const GemvParams &p, int64_t row, int l, Q4Ring<D> &r) {
+    const int G = (p.nb + 3) >> 2;
+    const uint8_t *rp = p.w + (size_t)row * G * 80;
 #pragma unroll
-    for (int i = 0; i < CH; ++i) acc[i] = 0.0f;
-    const uint8_t *rowp = p.w + (size_t)row * p.nb * 20;
-    for (int j = 0; j < p.nb; ++j) {
-        const uint8_t *blk = rowp + (size_t)j * 20;
-        const uint32_t sm = ld_u32<NT>(blk);
-        const uint32_t qc[4] = {ld_u32<NT>(blk + 4), ld_u32<NT>(blk + 8), ld_u32<NT>(blk + 12), ld_u32<NT>(blk + 16)};
-        const float scale = half_lo(sm), mn = half_hi(sm);
-        const float *xb = xs + (size_t)j * 32;
+    for (int i = 0; i < D; ++i) {
+        r.n[i] = ld_u2<NT>(rp + i * 80 + 8 * l);
+        r.s[i] = ld_u4<NT>(rp + i * 80 + 64);
+    }
+}
+
+// Walks the row's groups in order (chain l of the row); each ring slot is
+// refilled D groups ahead right after it is consumed (past the row's end the
+// refills read the next row or the padding and are not used).  Returns the
+// flushed dot product in lane `base`.
+template <bool NT, int D>
+__device__ __forceinline__ float q4_consume(const GemvParams &p, const XView &xv, int64_t row, int l, int base,
+                                            Q4Ring<D> &r) {
+    const int nb = p.nb;
+    const int G = (nb + 3) >> 2;  // groups, the last one possibly partial
+    const int Gf = nb >> 2;       // full groups
+    const uint8_t *gp = p.w + (size_t)row * G * 80 + D * 80 + 8 * l;  // next group to load (chain bytes)
+    const float *xg = xv.x + l * xv.stride;
+    float acc = 0.0f;
+    int g = 0;
+    for (; g + D <= Gf; g += D) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
+        for (int i = 0; i < D; ++i) {
+            acc = q4_group(acc, r.n[i], r.s[i], xg + 16 * i);
+            r.n[i] = ld_u2<NT>(gp + i * 80);
+            r.s[i] = ld_u4<NT>(gp + i * 80 + 64 - 8 * l);
+        }
+        gp += D * 80;
+        xg += 16 * D;
+    }
+    // the last (< D) groups are already in the ring, in order; only a row's
+    // final group can be partial
 #pragma unroll
-            for (int i = 0; i < CH; ++i) {
-                const int chain = (LPR == 8) ? s : 2 * s + i;  // element 8c + chain of the block
-                const uint32_t nib = __builtin_amdgcn_ubfe(qc[c], 8 * (chain >> 1) + 4 * (chain & 1), 4);
-                const float d = fmaf((float)nib, scale, mn);
-                acc[i] = fmaf(d, xb[8 * c + chain], acc[i]);
+    for (int i = 0; i < D; ++i) {
+        if (g + i < Gf) acc = q4_group(acc, r.n[i], r.s[i], xg + 16 * i);
+        else if (g + i < G) acc = q4_group_tail(acc, r.n[i], r.s[i], xg + 16 * i, nb - 4 * (g + i));
+    }
+    // lanes base..base+7 hold chains 0..7
+    const float u = acc + shfl(acc, base + ((l + 4) & 7));  // lane l<4: a_l + a_{l+4}
+    const float v = u + shfl(u, base + ((l + 2) & 7));      // lane 0: u0+u2, lane 1: u1+u3
+    const float total = v + shfl(v, base + ((l + 1) & 7));  // lane 0: (u0+u2) + (u1+u3)
+    return flush_small(total);
+}
+
+// Packs Q4_0Block rows (file layout) into the layout above; one thread per
+// (row, group).
+__global__ void pack_q4_0_kernel(const uint8_t *src, uint8_t *dst, int64_t N, int nb) {
+    const int G = (nb + 3) >> 2;
+    const int64_t total = N * G;
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t row = t / G;
+        const int g = (int)(t - row * G);
+        const uint8_t *rs = src + (size_t)row * nb * 20;
+        uint32_t *out = (uint32_t *)(dst + ((size_t)row * G + g) * 80);
+        for (int l = 0; l < 8; ++l) {
+            for (int h = 0; h < 2; ++h) {
+                uint32_t word = 0;
+                for (int half = 0; half < 2; ++half) {
+                    const int b = 4 * g + 2 * h + half;
+                    if (b >= nb) continue;
+                    const uint8_t *qs = rs + (size_t)b * 20 + 4;
+                    for (int c = 0; c < 4; ++c) {
+                        const int e = 8 * c + l;  // even element = low nibble of byte e/2
+                        const uint32_t code = (qs[e >> 1] >> ((e & 1) * 4)) & 0x0Fu;
+                        word |= code << (8 * c + 4 * half);
+                    }
+                }
+                out[2 * l + h] = word;
             }
         }
+        for (int b = 0; b < 4; ++b) {
+            const int j = 4 * g + b;
+            uint32_t sm = 0;
+            if (j < nb) {
+                const uint8_t *blk = rs + (size_t)j * 20;
+                sm = (uint32_t)blk[0] | ((uint32_t)blk[1] << 8) | ((uint32_t)blk[2] << 16) | ((uint32_t)blk[3] << 24);
+            }
+            out[16 + b] = sm;
+        }
     }
-    float total;
-    if constexpr (LPR == 8) {
-        const float a = acc[0];
-        const float u = a + shfl(a, base + ((s + 4) & 7));  // lane l<4: a_l + a_{l+4}
-        const float v = u + shfl(u, base + ((s + 2) & 7));  // lane 0: u0+u2, lane 1: u1+u3
-        total = v + shfl(v, base + ((s + 1) & 7));          // lane 0: (u0+u2) + (u1+u3)
-    } else {
-        // lane p holds chains (2p, 2p+1)
-        const float u0 = acc[0] + shfl(acc[0], base + ((s + 2) & 3));  // lane 0: a0+a4, lane 1: a2+a6
-        const float u1 = acc[1] + shfl(acc[1], base + ((s + 2) & 3));  // lane 0: a1+a5, lane 1: a3+a7
-        const float v0 = u0 + shfl(u0, base + ((s + 1) & 3));          // lane 0: (a0+a4)+(a2+a6)
-        const float v1 = u1 + shfl(u1, base + ((s + 1) & 3));          // lane 0: (a1+a5)+(a3+a7)
-        total = v0 + v1;
-    }
-    return flush_small(total);
+    uint32_t *pad = (uint32_t *)(dst + (size_t)total * 80);  // the tail padding reads as zeros
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < Q4_TAIL_PAD / 4; t += (int64_t)gridDim.x * blockDim.x)
+        pad[t] = 0;
 }
 
 // ----------------------------------------------------------------- f32 ----
 // LPR = 2: lane h owns chains 4h..4h+3 (one float4 of each 8-float chunk).
+// F32_AHEAD chunks of the row are in flight per lane.
+constexpr int F32_AHEAD = 8;
+struct F32Ring {
+    float4 w[F32_AHEAD];
+};
+
 template <bool NT>
-__device__ __forceinline__ float row_f32(const GemvParams &p, const float *xs, int64_t row, int s, int base) {
+__device__ __forceinline__ void f32_prefetch(const GemvParams &p, int64_t row, int s, F32Ring &r) {
+    const int64_t chunks = p.K / 8;
+    if (chunks == 0) return;
+    const float *wl = (const float *)p.w + (size_t)row * p.K + 4 * s;
+#pragma unroll
+    for (int u = 0; u < F32_AHEAD; ++u) r.w[u] = ld_f4<NT>(wl + 8 * (u < chunks ? u : chunks - 1));
+}
+
+template <bool NT>
+__device__ __forceinline__ float f32_consume(const GemvParams &p, const float *xs, int64_t row, int s, int base,
+                                             F32Ring &r) {
     float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
     const float *wr = (const float *)p.w + (size_t)row * p.K;
+    const float *wl = wr + 4 * s;
+    const float *xl = xs + 4 * s;
     const int64_t chunks = p.K / 8;
-    for (int64_t t = 0; t < chunks; ++t) {
-        const float4 w = ld_f4<NT>(wr + 8 * t + 4 * s);
-        const float4 x = *(const float4 *)(xs + 8 * t + 4 * s);
-        a0 = fmaf(x.x, w.x, a0);
-        a1 = fmaf(x.y, w.y, a1);
-        a2 = fmaf(x.z, w.z, a2);
-        a3 = fmaf(x.w, w.w, a3);
+    int64_t t = 0;
+    for (; t + F32_AHEAD <= chunks; t += F32_AHEAD) {
+#pragma unroll
+        for (int u = 0; u < F32_AHEAD; ++u) {
+            const float4 w = r.w[u];
+            const int64_t tn = t + u + F32_AHEAD < chunks ? t + u + F32_AHEAD : chunks - 1;
+            r.w[u] = ld_f4<NT>(wl + 8 * tn);
+            const float4 x = *(const float4 *)(xl + 8 * (t + u));
+            a0 = fmaf(x.x, w.x, a0);
+            a1 = fmaf(x.y, w.y, a1);
+            a2 = fmaf(x.z, w.z, a2);
+            a3 = fmaf(x.w, w.w, a3);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < F32_AHEAD; ++u) {
+        if (t + u < chunks) {
+            const float4 w = r.w[u];
+            const float4 x = *(const float4 *)(xl + 8 * (t + u));
+            a0 = fmaf(x.x, w.x, a0);
+            a1 = fmaf(x.y, w.y, a1);
+            a2 = fmaf(x.z, w.z, a2);
+            a3 = fmaf(x.w, w.w, a3);
+        }
     }
     // lane 0 holds chains 0..3, lane 1 chains 4..7: ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7))
     const float u0 = a0 + shfl(a0, base + 1), u1 = a1 + shfl(a1, base + 1);
@@ -155,65 +327,93 @@ __device__ __forceinline__ float row_lut4(const GemvParams &p, const float *xs, 
     return flush_small(total);
 }
 
-__device__ __forceinline__ float finish_row(const GemvParams &p, const float *xs, int64_t r, float v) {
+// compute_single_row's tail: anchors, then the bias (already loaded) if the
+// row has one.
+__device__ __forceinline__ float finish_row(const GemvParams &p, const XView &xv, int64_t r, float v, float bias) {
     if (p.a_ptr) {
         for (int64_t k = p.a_ptr[r]; k < p.a_ptr[r + 1]; ++k) {
-            const float prod = xs[p.a_col[k]] * half_bits(p.a_val[k]);
+            const float prod = xv.at(p.a_col[k]) * half_bits(p.a_val[k]);
             v = v + prod;
         }
     }
-    if (r < p.bias_len) v = v + p.bias[r];
+    if (r < p.bias_len) v = v + bias;
     return v;
 }
 
-template <int FMT, int LPR, bool NT>
-__global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npairs) {
-    extern __shared__ __align__(16) float smem[];
-    __shared__ float inv_slot;
-    DevState *st = p.st;
-    if (st && st->halted) return;
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int64_t K = p.K;
-    float *xs = smem;
-
-    // ---- prologue: activation vector into LDS (normalised if requested) ----
-    int bad_in = 0;
-    for (int64_t k = tid; k < K; k += THREADS) {
-        const float v = p.x[k];
-        xs[k] = v;
-        bad_in |= isnan(v);
-    }
-    if (__syncthreads_or(bad_in) && p.st_in >= 0 && tid == 0) nan_flag(st, p.layer, p.st_in);
-    if (p.norm_w) {
-        rmsnorm_inplace(xs, K, p.norm_w, p.eps, &inv_slot);
-        int bad = 0;
-        for (int64_t k = tid; k < K; k += THREADS) bad |= isnan(xs[k]);
-        if (__syncthreads_or(bad) && p.st_norm >= 0 && tid == 0) nan_flag(st, p.layer, p.st_norm);
-    }
-    if (p.gnorm) {
-        // use_genomic_norm (block/forward.rs:115-123) sums with a rayon
-        // reduction whose order is not fixed upstream; a sequential sum here.
-        if (tid == 0) {
-            float ss = 0.0f;
-            for (int64_t k = 0; k < K; ++k) {
-                const float sq = xs[k] * xs[k];
-                ss = ss + sq;
+// rms_norm over the chain-major LDS copy: lane l < 8 walks chain l (elements
+// 8i + l), which is its own LDS row; K % 32 == 0 here so there is no tail.
+__device__ inline void rmsnorm_chain_major(const XView &xv, int64_t K, const float *w, float eps, float *inv_slot) {
+    const int tid = threadIdx.x;
+    if (tid < 8) {
+        const float *xl = xv.x + tid * xv.stride;
+        const int64_t n8 = K / 8;  // a multiple of 4
+        float acc = 0.0f;
+        int64_t i = 0;
+        for (; i + 16 <= n8; i += 16) {
+            float4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[u] = *(const float4 *)(xl + i + 4 * u);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                acc = fmaf(v[u].x, v[u].x, acc);
+                acc = fmaf(v[u].y, v[u].y, acc);
+                acc = fmaf(v[u].z, v[u].z, acc);
+                acc = fmaf(v[u].w, v[u].w, acc);
             }
-            inv_slot = sqrtf(ss / (float)K + p.eps);
         }
-        __syncthreads();
-        const float rms = inv_slot;
-        if (rms > p.h_scale) {
-            const float sc = p.h_scale / rms;
-            for (int64_t k = tid; k < K; k += THREADS) xs[k] = xs[k] * sc;
+        for (; i < n8; i += 4) {
+            const float4 v = *(const float4 *)(xl + i);
+            acc = fmaf(v.x, v.x, acc);
+            acc = fmaf(v.y, v.y, acc);
+            acc = fmaf(v.z, v.z, acc);
+            acc = fmaf(v.w, v.w, acc);
+        }
+        const float u = acc + __shfl(acc, (tid + 4) & 7, 8);  // lane l<4: a_l + a_{l+4}
+        const float v = u + __shfl(u, (tid + 1) & 7, 8);      // lane 0: u0+u1, lane 2: u2+u3
+        const float tot = v + __shfl(v, (tid + 2) & 7, 8);    // lane 0: (u0+u1) + (u2+u3)
+        if (tid == 0) {
+            const float mean = tot / (float)K;
+            *inv_slot = 1.0f / sqrtf(mean + eps);
         }
     }
     __syncthreads();
-    if (p.x_out && blockIdx.x == 0)
-        for (int64_t k = tid; k < K; k += THREADS) p.x_out[k] = xs[k];
+    const float inv = *inv_slot;
+    for (int64_t k = tid; k < K; k += blockDim.x) {
+        float &x = xv.at(k);
+        const float t = x * inv;
+        x = t * w[k];
+    }
+}
 
-    // ---- row pairs ----
+// Row pair -> its rows (r1 = -1 if none) and this lane's row.
+struct PairRows {
+    int64_t r0, r1, row;
+    bool pair_ok, row_ok;
+};
+
+template <int FMT>
+__device__ __forceinline__ PairRows locate(const GemvParams &p, int64_t pr, int64_t npairs, int half) {
+    PairRows q;
+    q.pair_ok = pr < npairs;
+    q.r0 = 0;
+    q.r1 = -1;
+    if (q.pair_ok) pair_rows(p, pr, q.r0, q.r1);
+    q.row = half ? q.r1 : q.r0;
+    const bool has_work = (FMT == FMT_F32) ? p.K > 0 : p.nb > 0;
+    q.row_ok = q.pair_ok && q.row >= 0 && q.row < p.rows_valid && has_work;
+    return q;
+}
+
+template <int FMT, int LPR, bool NT, int D>
+__global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npairs, int xstride, int nw_off) {
+    extern __shared__ __align__(16) float smem[];
+    __shared__ float inv_slot;
+    DevState *st = p.st;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t K = p.K;
+    const XView xv{smem, FMT == FMT_Q4_0 ? xstride : 0};
+
     constexpr int PAIR_LANES = 2 * LPR;
     constexpr int PAIRS_PER_WAVE = WAVE / PAIR_LANES;
     const int pslot = lane / PAIR_LANES;
@@ -224,31 +424,147 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
     const int pairs_per_block = PAIRS_PER_WAVE * (THREADS / WAVE);
     float *tbl = smem + ((K + 3) & ~(int64_t)3) + (size_t)(tid / LPR) * 16;  // LUT slot of this row group
 
+    // ---- the first row pair's weights start streaming before anything else ----
+    int64_t pr0 = (int64_t)blockIdx.x * pairs_per_block;
+    PairRows q = locate<FMT>(p, pr0 + wave * PAIRS_PER_WAVE + pslot, npairs, half);
+    Q4Ring<D> q4r;
+    F32Ring f32r;
+    if (q.row_ok) {
+        if constexpr (FMT == FMT_Q4_0) q4_prefetch<NT, D>(p, q.row, s, q4r);
+        else if constexpr (FMT == FMT_F32) f32_prefetch<NT>(p, q.row, s, f32r);
+    }
+    const int halted = st ? st->halted : 0;
+
+    // ---- prologue: activation vector (and the norm weights) into LDS, one
+    // batch of loads in flight per thread; normalised if requested ----
+    float *nw = smem + nw_off;  // plain copy of norm_w when there is one
+    int bad_in = 0;
+    if constexpr (FMT == FMT_LUT4) {
+        constexpr int XB = 8;
+        for (int64_t k0 = 0; k0 < K; k0 += XB * THREADS) {
+            float xr[XB], wr[XB];
+#pragma unroll
+            for (int u = 0; u < XB; ++u) {
+                const int64_t k = k0 + u * THREADS + tid;
+                xr[u] = k < K ? p.x[k] : 0.0f;
+                wr[u] = (p.norm_w && k < K) ? p.norm_w[k] : 0.0f;
+            }
+            if (k0 == 0 && halted) return;  // uniform; checked once the first loads are in flight
+#pragma unroll
+            for (int u = 0; u < XB; ++u) {
+                const int64_t k = k0 + u * THREADS + tid;
+                if (k < K) {
+                    xv.at(k) = xr[u];
+                    if (p.norm_w) nw[k] = wr[u];
+                    bad_in |= isnan(xr[u]);
+                }
+            }
+        }
+    } else {
+        // K % 4 == 0 and 16-byte aligned x / norm_w (checked at launch)
+        constexpr int XB4 = 6;
+        const int64_t K4 = K >> 2;
+        for (int64_t m0 = 0; m0 < K4; m0 += XB4 * THREADS) {
+            float4 xr[XB4], wr[XB4];
+#pragma unroll
+            for (int u = 0; u < XB4; ++u) {
+                const int64_t m = m0 + u * THREADS + tid;
+                xr[u] = m < K4 ? ((const float4 *)p.x)[m] : make_float4(0.f, 0.f, 0.f, 0.f);
+                wr[u] = (p.norm_w && m < K4) ? ((const float4 *)p.norm_w)[m] : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+            if (m0 == 0 && halted) return;  // uniform; checked once the first loads are in flight
+#pragma unroll
+            for (int u = 0; u < XB4; ++u) {
+                const int64_t m = m0 + u * THREADS + tid;
+                if (m < K4) {
+                    const float4 v = xr[u];
+                    xv.at(4 * m) = v.x;
+                    xv.at(4 * m + 1) = v.y;
+                    xv.at(4 * m + 2) = v.z;
+                    xv.at(4 * m + 3) = v.w;
+                    if (p.norm_w) *(float4 *)(nw + 4 * m) = wr[u];
+                    bad_in |= isnan(v.x) | isnan(v.y) | isnan(v.z) | isnan(v.w);
+                }
+            }
+        }
+    }
+    if (__syncthreads_or(bad_in) && p.st_in >= 0 && tid == 0) nan_flag(st, p.layer, p.st_in);
+    if (p.norm_w) {
+        if constexpr (FMT == FMT_Q4_0) rmsnorm_chain_major(xv, K, nw, p.eps, &inv_slot);
+        else rmsnorm_inplace(smem, K, nw, p.eps, &inv_slot);
+        int bad = 0;
+        for (int64_t k = tid; k < K; k += THREADS) bad |= isnan(xv.at(k));
+        if (__syncthreads_or(bad) && p.st_norm >= 0 && tid == 0) nan_flag(st, p.layer, p.st_norm);
+    }
+    if (p.gnorm) {
+        // use_genomic_norm (block/forward.rs:115-123) sums with a rayon
+        // reduction whose order is not fixed upstream; a sequential sum here.
+        if (tid == 0) {
+            float ss = 0.0f;
+            for (int64_t k = 0; k < K; ++k) {
+                const float xk = xv.at(k);
+                const float sq = xk * xk;
+                ss = ss + sq;
+            }
+            inv_slot = sqrtf(ss / (float)K + p.eps);
+        }
+        __syncthreads();
+        const float rms = inv_slot;
+        if (rms > p.h_scale) {
+            const float sc = p.h_scale / rms;
+            for (int64_t k = tid; k < K; k += THREADS) xv.at(k) = xv.at(k) * sc;
+        }
+    }
+    __syncthreads();
+    if (p.x_out && blockIdx.x == 0)
+        for (int64_t k = tid; k < K; k += THREADS) p.x_out[k] = xv.at(k);
+
+    // ---- row pairs ----
     float best_v = -INFINITY;
     int64_t best_i = 0;
+    const int hh = p.head_dim >> 1;
 
-    for (int64_t pr0 = (int64_t)blockIdx.x * pairs_per_block; pr0 < npairs; pr0 += (int64_t)gridDim.x * pairs_per_block) {
+    for (bool first = true; pr0 < npairs; pr0 += (int64_t)gridDim.x * pairs_per_block, first = false) {
         const int64_t pr = pr0 + wave * PAIRS_PER_WAVE + pslot;
-        const bool pair_ok = pr < npairs;
-        int64_t r0 = 0, r1 = -1;
-        if (pair_ok) pair_rows(p, pr, r0, r1);
-        const int64_t row = half ? r1 : r0;
-        const bool has_work = (FMT == FMT_F32) ? p.K > 0 : p.nb > 0;
-        const bool row_ok = pair_ok && row >= 0 && row < p.rows_valid && has_work;
+        if (!first) {
+            q = locate<FMT>(p, pr, npairs, half);
+            if (q.row_ok) {
+                if constexpr (FMT == FMT_Q4_0) q4_prefetch<NT, D>(p, q.row, s, q4r);
+                else if constexpr (FMT == FMT_F32) f32_prefetch<NT>(p, q.row, s, f32r);
+            }
+        }
+        const int64_t r0 = q.r0, r1 = q.r1;
+        const bool leader = q.pair_ok && lane == pair_base;
+        // epilogue operands, loaded while the rows are computed
+        float b0 = 0.0f, b1 = 0.0f, old0 = 0.0f, old1 = 0.0f, cs = 0.0f, sn = 0.0f;
+        int pos = 0;
+        if (leader) {
+            if (r0 < p.bias_len) b0 = p.bias[r0];
+            if (r1 >= 0 && r1 < p.bias_len) b1 = p.bias[r1];
+            if (p.mode == MODE_RESIDUAL) {
+                old0 = p.y[r0];
+                if (r1 >= 0) old1 = p.y[r1];
+            } else if (p.mode == MODE_QKV) {
+                pos = st->pos;
+                const int i = (int)(pr % hh);
+                cs = p.rope_cos[(size_t)pos * hh + i];
+                sn = p.rope_sin[(size_t)pos * hh + i];
+            }
+        }
         float v = 0.0f;
         // all lanes of a row group share row_ok, so each row function's
         // shuffles only read lanes that execute it
-        if (row_ok) {
-            if constexpr (FMT == FMT_Q4_0) v = row_q4_0<LPR, NT>(p, xs, row, s, row_base);
-            else if constexpr (FMT == FMT_F32) v = row_f32<NT>(p, xs, row, s, row_base);
-            else v = row_lut4<NT>(p, xs, row, s, row_base, tbl);
+        if (q.row_ok) {
+            if constexpr (FMT == FMT_Q4_0) v = q4_consume<NT, D>(p, xv, q.row, s, row_base, q4r);
+            else if constexpr (FMT == FMT_F32) v = f32_consume<NT>(p, smem, q.row, s, row_base, f32r);
+            else v = row_lut4<NT>(p, smem, q.row, s, row_base, tbl);
         }
         const float v1 = shfl(v, pair_base + LPR);  // r1's result (lane 0 of its group)
-        if (!pair_ok || lane != pair_base) continue;
+        if (!leader) continue;
 
         // ---- epilogue (one lane per row pair) ----
-        const float y0 = finish_row(p, xs, r0, v);
-        const float y1 = r1 >= 0 ? finish_row(p, xs, r1, v1) : 0.0f;
+        const float y0 = finish_row(p, xv, r0, v, b0);
+        const float y1 = r1 >= 0 ? finish_row(p, xv, r1, v1, b1) : 0.0f;
         switch (p.mode) {
             case MODE_STORE:
                 p.y[r0] = y0;
@@ -256,11 +572,11 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
                 break;
             case MODE_RESIDUAL: {
                 if (isnan(y0) || (r1 >= 0 && isnan(y1))) nan_flag(st, p.layer, p.st_a);
-                const float h0 = p.y[r0] + y0;
+                const float h0 = old0 + y0;
                 p.y[r0] = h0;
                 bool bad = isnan(h0);
                 if (r1 >= 0) {
-                    const float h1 = p.y[r1] + y1;
+                    const float h1 = old1 + y1;
                     p.y[r1] = h1;
                     bad |= isnan(h1);
                 }
@@ -270,27 +586,25 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
             case MODE_QKV: {
                 // attention.rs:62-82 with the host-built cos/sin table:
                 // (v0*cos - v1*sin, v0*sin + v1*cos), every product rounded.
-                const int hh = p.head_dim >> 1;
-                const int pos = st->pos;
-                const int i = (int)(pr % hh);
-                const float cs = p.rope_cos[(size_t)pos * hh + i], sn = p.rope_sin[(size_t)pos * hh + i];
                 const float t0 = y0 * cs, t1 = y1 * sn, t2 = y0 * sn, t3 = y1 * cs;
                 const float o0 = t0 - t1, o1 = t2 + t3;
                 if (r0 < p.q_rows) {
                     p.q_out[r0] = o0;
                     p.q_out[r1] = o1;
                 } else if (r0 < p.q_rows + p.kv_rows) {
+                    // K cache: [kv head][position][dim]
                     const int64_t kh = (r0 - p.q_rows) / p.head_dim;
                     const int64_t b = p.q_rows + kh * p.head_dim;
                     float *kc = p.k_cache + kh * p.kv_head_stride + (size_t)pos * p.head_dim;
                     kc[r0 - b] = o0;
                     kc[r1 - b] = o1;
                 } else {
+                    // V cache: [kv head][dim][position]
                     const int64_t vh = (r0 - p.q_rows - p.kv_rows) / p.head_dim;
                     const int64_t b = p.q_rows + p.kv_rows + vh * p.head_dim;
-                    float *vc = p.v_cache + vh * p.kv_head_stride + (size_t)pos * p.head_dim;
-                    vc[r0 - b] = y0;
-                    vc[r1 - b] = y1;
+                    float *vc = p.v_cache + vh * p.kv_head_stride + pos;
+                    vc[(r0 - b) * p.kv_cap] = y0;
+                    vc[(r1 - b) * p.kv_cap] = y1;
                 }
                 break;
             }
@@ -326,14 +640,44 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
     }
 }
 
-using KernelFn = void (*)(GemvParams, int64_t);
+using KernelFn = void (*)(GemvParams, int64_t, int, int);
+
+// LDS row stride (floats) of the chain-major activation copy: room for every
+// packed group's 16 inputs, padded so that stride / 4 is odd (the eight chain
+// rows' 16-byte reads then fall in distinct banks).
+int q4_xstride(int64_t K) {
+    const int64_t G = (K / 32 + 3) / 4;
+    return (int)(16 * G + 4);
+}
 
 }  // namespace
 
-size_t gemv_lds_bytes(int64_t K, int fmt) {
-    size_t b = (size_t)((K + 3) & ~(int64_t)3) * 4;
-    if (fmt == FMT_LUT4) b += (size_t)(THREADS / 4) * 16 * 4;  // one 16-entry table per row group
-    return b;
+int64_t q4_0_packed_bytes(int64_t N, int64_t K) { return N * ((K / 32 + 3) / 4) * 80 + Q4_TAIL_PAD; }
+
+int launch_pack_q4_0(const uint8_t *src, uint8_t *dst, int64_t N, int64_t K, hipStream_t s) {
+    if (N < 0 || K <= 0 || K % 32 != 0) return set_error(GAJE_ERR_INVALID_ARG, "pack: K must be a positive multiple of 32");
+    if (N == 0) return GAJE_OK;
+    if (!src || !dst) return set_error(GAJE_ERR_INVALID_ARG, "pack: null buffer");
+    const int nb = (int)(K / 32);
+    const int64_t total = N * ((nb + 3) / 4);
+    int64_t grid = (total + 255) / 256;
+    if (grid > 65536) grid = 65536;
+    hipLaunchKernelGGL(pack_q4_0_kernel, dim3((unsigned)grid), dim3(256), 0, s, src, dst, N, nb);
+    GAJE_HIP_CHECK(hipGetLastError());
+    return GAJE_OK;
+}
+
+// LDS floats before the norm-weight copy: the activation vector (chain-major
+// for Q4_0, plain otherwise) and, for LUT rows, one 16-entry table per row group.
+static int64_t gemv_x_floats(int64_t K, int fmt) {
+    if (fmt == FMT_Q4_0) return (int64_t)8 * q4_xstride(K);
+    int64_t f = (K + 3) & ~(int64_t)3;
+    if (fmt == FMT_LUT4) f += (int64_t)(THREADS / 4) * 16;
+    return f;
+}
+
+size_t gemv_lds_bytes(int64_t K, int fmt, bool norm) {
+    return (size_t)(gemv_x_floats(K, fmt) + (norm ? ((K + 3) & ~(int64_t)3) : 0)) * 4;
 }
 
 int launch_gemv(const GemvParams &p, hipStream_t s) {
@@ -343,17 +687,23 @@ int launch_gemv(const GemvParams &p, hipStream_t s) {
     if (p.fmt == FMT_F32 && p.K % 4 != 0)
         return set_error(GAJE_ERR_UNSUPPORTED, "gemv: f32 rows need in_features %% 4 == 0 (got %lld)",
                          (long long)p.K);
+    if (p.fmt == FMT_Q4_0 && p.K % 32 != 0)
+        return set_error(GAJE_ERR_UNSUPPORTED, "gemv: Q4_0 rows need in_features %% 32 == 0 (got %lld)",
+                         (long long)p.K);
+    if (p.fmt != FMT_LUT4 && (((uintptr_t)p.x | (uintptr_t)p.norm_w) & 15))
+        return set_error(GAJE_ERR_INVALID_ARG, "gemv: x and norm_w must be 16-byte aligned");
     if (p.rows_valid > 0 && !p.w) return set_error(GAJE_ERR_INVALID_ARG, "gemv: null weights");
     if (p.fmt == FMT_LUT4 && p.nb > 0 && p.rows_valid > 0 && !p.lut)
         return set_error(GAJE_ERR_INVALID_ARG, "gemv: null LUT");
-    const size_t lds = gemv_lds_bytes(p.K, p.fmt);
-    if (lds + 1024 > 64 * 1024)  // dynamic + the kernel's static LDS within 64 KiB
+    const size_t lds = gemv_lds_bytes(p.K, p.fmt, p.norm_w != nullptr);
+    if (lds + 1024 > max_lds_per_block())  // dynamic + the kernel's static LDS
         return set_error(GAJE_ERR_UNSUPPORTED, "gemv: in_features %lld exceeds the LDS budget", (long long)p.K);
     int64_t npairs;
     switch (p.mode) {
         case MODE_QKV:
             if (!p.st || p.head_dim <= 0 || p.head_dim % 2 || p.q_rows % p.head_dim || p.kv_rows % p.head_dim ||
-                p.N < p.q_rows + 2 * p.kv_rows || !p.q_out || !p.k_cache || !p.v_cache || !p.rope_cos || !p.rope_sin)
+                p.N < p.q_rows + 2 * p.kv_rows || !p.q_out || !p.k_cache || !p.v_cache || !p.rope_cos ||
+                !p.rope_sin || p.kv_cap <= 0 || p.kv_head_stride != p.kv_cap * p.head_dim)
                 return set_error(GAJE_ERR_INVALID_ARG, "gemv: bad fused-QKV arguments");
             npairs = (p.q_rows + 2 * p.kv_rows) / 2;
             break;
@@ -376,21 +726,28 @@ int launch_gemv(const GemvParams &p, hipStream_t s) {
     KernelFn fn;
     int lpr;
     if (p.fmt == FMT_Q4_0) {
-        // one chain per lane when rows are few (more lanes in flight), two otherwise
-        const bool few_rows = npairs < 2048;
-        lpr = few_rows ? 8 : 4;
-        fn = few_rows ? gemv_kernel<FMT_Q4_0, 8, false> : gemv_kernel<FMT_Q4_0, 4, false>;
+        // ring depth: a short row's groups are all in flight at once; long rows
+        // keep 16 groups (64 blocks) ahead of the arithmetic
+        const bool long_rows = (p.nb + 3) / 4 > Q4_PREFETCH;
+        lpr = 8;
+        if (long_rows)
+            fn = p.nontemporal ? gemv_kernel<FMT_Q4_0, 8, true, 2 * Q4_PREFETCH>
+                               : gemv_kernel<FMT_Q4_0, 8, false, 2 * Q4_PREFETCH>;
+        else
+            fn = p.nontemporal ? gemv_kernel<FMT_Q4_0, 8, true, Q4_PREFETCH> : gemv_kernel<FMT_Q4_0, 8, false, Q4_PREFETCH>;
     } else if (p.fmt == FMT_LUT4) {
         lpr = 4;
-        fn = gemv_kernel<FMT_LUT4, 4, false>;
+        fn = gemv_kernel<FMT_LUT4, 4, false, 1>;
     } else {
         lpr = 2;
-        fn = p.nontemporal ? gemv_kernel<FMT_F32, 2, true> : gemv_kernel<FMT_F32, 2, false>;
+        fn = p.nontemporal ? gemv_kernel<FMT_F32, 2, true, 1> : gemv_kernel<FMT_F32, 2, false, 1>;
     }
     const int64_t pairs_per_block = (WAVE / (2 * lpr)) * (THREADS / WAVE);
     int64_t grid = (npairs + pairs_per_block - 1) / pairs_per_block;
     if (grid > MAX_GRID) grid = MAX_GRID;
-    hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(THREADS), lds, s, p, npairs);
+    const int xstride = p.fmt == FMT_Q4_0 ? q4_xstride(p.K) : 0;
+    const int nw_off = (int)gemv_x_floats(p.K, p.fmt);
+    hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(THREADS), lds, s, p, npairs, xstride, nw_off);
     GAJE_HIP_CHECK(hipGetLastError());
     return GAJE_OK;
 }

@@ -48,7 +48,7 @@ enum GemvMode : int32_t {
 };
 
 struct GemvParams {
-    // weights: row r of a Q4_0 tensor is blocks [r*nb, (r+1)*nb)
+    // weights: FMT_Q4_0 rows in the packed layout of launch_pack_q4_0
     const uint8_t *w;
     int32_t fmt;
     int32_t nontemporal;     // stream the weights past the caches (read-once tensors)
@@ -79,8 +79,10 @@ struct GemvParams {
     int64_t q_rows, kv_rows;
     const float *rope_cos, *rope_sin;  // [max_ctx][head_dim/2]
     float *q_out;
-    float *k_cache, *v_cache;          // this layer: [n_kv][max_ctx][head_dim]
-    int64_t kv_head_stride;            // max_ctx * head_dim
+    float *k_cache;                    // this layer: [n_kv][kv_cap][head_dim]
+    float *v_cache;                    // this layer: [n_kv][head_dim][kv_cap]
+    int64_t kv_head_stride;            // kv_cap * head_dim
+    int64_t kv_cap;                    // positions per cache row
     int64_t ffn;
     // guards (stage < 0 disables a check)
     DevState *st;
@@ -91,15 +93,24 @@ struct GemvParams {
 // Validates shapes against what the kernels assume and launches; returns a
 // GAJE_* status.
 int launch_gemv(const GemvParams &p, hipStream_t s);
+// Q4_0Block rows (file layout, K % 32 == 0) -> the GEMV's packed row layout.
+// A packed tensor is followed by Q4_TAIL_PAD bytes that the GEMV's prefetch
+// may read (and never uses); q4_0_packed_bytes includes them.
+constexpr int64_t Q4_TAIL_PAD = 2048;
+int launch_pack_q4_0(const uint8_t *src, uint8_t *dst, int64_t N, int64_t K, hipStream_t s);
+int64_t q4_0_packed_bytes(int64_t N, int64_t K);
+// Dynamic LDS a workgroup may use on the current device.
+size_t max_lds_per_block();
 // Dynamic LDS the GEMV needs for in_features K (so callers can check limits).
-size_t gemv_lds_bytes(int64_t K, int fmt);
+size_t gemv_lds_bytes(int64_t K, int fmt, bool norm);
 
 struct AttnParams {
     const float *q;          // roped queries [n_head * head_dim]
-    const float *k_cache, *v_cache;  // this layer: [n_kv][max_ctx][head_dim]
-    int64_t kv_head_stride;
+    const float *k_cache;    // this layer: [n_kv][kv_cap][head_dim]
+    const float *v_cache;    // this layer: [n_kv][head_dim][kv_cap]
+    int64_t kv_head_stride;  // kv_cap * head_dim
     int32_t n_head, n_head_kv, head_dim;
-    int64_t max_ctx;         // KV capacity (sizes the LDS score buffer)
+    int64_t kv_cap;          // KV capacity (sizes the LDS score buffer)
     float *out;              // [n_head * head_dim]
     DevState *st;            // positions 0..st->pos are attended; if null, 0..ctx-1
     int64_t ctx;
@@ -110,7 +121,7 @@ size_t attention_lds_bytes(int head_dim, int64_t max_ctx);
 constexpr int64_t MAX_CTX = 12288;
 
 struct EmbedParams {
-    const uint8_t *w;
+    const uint8_t *w;        // FMT_Q4_0: packed rows
     int32_t fmt;
     const float *lut;
     int64_t lut_rows_own;

@@ -27,10 +27,14 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedParams p) {
                 const int64_t b = k / 32;
                 const int i = (int)(k % 32);
                 if (p.fmt == FMT_Q4_0) {
-                    const uint8_t *blk = p.w + (row * nb + b) * 20;
-                    const uint8_t byte = blk[4 + i / 2];
-                    const float q = (float)((i % 2 == 0) ? (byte & 0x0F) : (byte >> 4));
-                    const uint32_t sm = *(const uint32_t *)blk;
+                    // packed rows (launch_pack_q4_0): element i of block b is
+                    // chain i % 8, chunk i / 8 of group b / 4
+                    const int64_t G = (nb + 3) / 4;
+                    const uint8_t *grp = p.w + (row * G + b / 4) * 80;
+                    const int bb = (int)(b & 3), l = i & 7, c = i >> 3;
+                    const uint32_t word = *(const uint32_t *)(grp + 8 * l + 4 * (bb >> 1));
+                    const float q = (float)((word >> (8 * c + 4 * (bb & 1))) & 0x0Fu);
+                    const uint32_t sm = *(const uint32_t *)(grp + 64 + 4 * bb);
                     v = __fadd_rn(__fmul_rn(q, half_lo(sm)), half_hi(sm));
                 } else {
                     const float *t = p.lut + (row < p.lut_rows_own ? row * nb * 16 : 0) + b * p.lut_block_stride;

@@ -315,7 +315,23 @@ int upload_linear(gaje_hip_model *m, const HostLinear &L, DevLinear &D) {
     D.K = L.K;
     D.rows_valid = rows_valid_of(L);
     const int64_t nb = L.K / 32;
-    GAJE_TRY(m->upload(&D.w, L.w.data(), L.w.size()));
+    if (L.fmt == FMT_Q4_0) {
+        // stage the file's Q4_0Block rows and pack them into the GEMV layout
+        const size_t raw = (size_t)D.rows_valid * nb * 20;
+        const int64_t packed = q4_0_packed_bytes(D.rows_valid, L.K);
+        uint8_t *tmp = nullptr;
+        GAJE_TRY(m->upload(&tmp, L.w.data(), raw));
+        m->weight_bytes -= (int64_t)raw;
+        int rc = m->alloc(&D.w, (size_t)packed);
+        if (rc == GAJE_OK && packed > 0) rc = launch_pack_q4_0(tmp, D.w, D.rows_valid, L.K, m->stream);
+        if (rc == GAJE_OK) rc = hipStreamSynchronize(m->stream) == hipSuccess ? GAJE_OK
+                                                                               : set_error(GAJE_ERR_HIP, "Q4_0 pack failed");
+        m->release(tmp);
+        GAJE_TRY(rc);
+        m->weight_bytes += packed;
+    } else {
+        GAJE_TRY(m->upload(&D.w, L.w.data(), L.w.size()));
+    }
     if (L.fmt == FMT_LUT4 && !L.lut.empty()) {
         const size_t n = L.lut.size(), per_row = (size_t)nb * 16;
         if (n == 16) {
@@ -408,9 +424,12 @@ int reserve_ctx(gaje_hip_model *m, int64_t positions) {
         for (int64_t l = 0; l < m->n_layers; ++l)
             for (int64_t g = 0; g < m->n_kv; ++g) {
                 const size_t src = ((size_t)l * m->n_kv + g) * per_head_old, dst = ((size_t)l * m->n_kv + g) * per_head_new;
+                // K rows are [position][dim]: one contiguous prefix;
+                // V rows are [dim][position]: a prefix of every dimension's row
                 const size_t bytes = (size_t)m->pos * m->hd * 4;
                 GAJE_HIP_CHECK(hipMemcpyAsync(kc + dst, m->k_cache + src, bytes, hipMemcpyDeviceToDevice, m->stream));
-                GAJE_HIP_CHECK(hipMemcpyAsync(vc + dst, m->v_cache + src, bytes, hipMemcpyDeviceToDevice, m->stream));
+                GAJE_HIP_CHECK(hipMemcpy2DAsync(vc + dst, (size_t)cap * 4, m->v_cache + src, (size_t)m->cap * 4,
+                                                (size_t)m->pos * 4, (size_t)m->hd, hipMemcpyDeviceToDevice, m->stream));
             }
         GAJE_HIP_CHECK(hipStreamSynchronize(m->stream));
     }
@@ -465,6 +484,7 @@ int enqueue_token(gaje_hip_model *m, hipEvent_t ev_blocks_done) {
         p.k_cache = m->k_cache + l * layer_kv;
         p.v_cache = m->v_cache + l * layer_kv;
         p.kv_head_stride = m->cap * m->hd;
+        p.kv_cap = m->cap;
         GAJE_TRY(launch_gemv(p, m->stream));
 
         AttnParams ap;
@@ -475,7 +495,7 @@ int enqueue_token(gaje_hip_model *m, hipEvent_t ev_blocks_done) {
         ap.n_head = (int32_t)m->n_head;
         ap.n_head_kv = (int32_t)m->n_kv;
         ap.head_dim = (int32_t)m->hd;
-        ap.max_ctx = m->cap;
+        ap.kv_cap = m->cap;
         ap.out = m->attn_out;
         ap.st = m->st;
         GAJE_TRY(launch_attention(ap, m->stream));
@@ -1019,6 +1039,7 @@ extern "C" int gaje_hip_time_stage(gaje_hip_model *m, int stage, int64_t layer, 
                     p.k_cache = m->k_cache + layer * layer_kv;
                     p.v_cache = m->v_cache + layer * layer_kv;
                     p.kv_head_stride = m->cap * m->hd;
+                    p.kv_cap = m->cap;
                     algo = wbytes(Ly.qkv) + (m->n_embd * 2 + m->q_rows + 2 * m->kv_rows) * 4;
                 } else if (stage == GAJE_STAGE_O) {
                     p = gemv_base(m, Ly.o, m->attn_out);
@@ -1050,7 +1071,7 @@ extern "C" int gaje_hip_time_stage(gaje_hip_model *m, int stage, int64_t layer, 
                 ap.n_head = (int32_t)m->n_head;
                 ap.n_head_kv = (int32_t)m->n_kv;
                 ap.head_dim = (int32_t)m->hd;
-                ap.max_ctx = m->cap;
+                ap.kv_cap = m->cap;
                 ap.out = m->attn_out;
                 ap.st = m->st;
                 algo = (int64_t)(m->pos + 1) * 2 * m->kv_rows * 4 + 2 * m->q_rows * 4;

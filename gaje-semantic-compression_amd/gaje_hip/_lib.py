@@ -85,6 +85,8 @@ SIGNATURES = [
     ("gaje_hip_event_record", ctypes.c_int, [c_vp, c_vp]),
     ("gaje_hip_event_synchronize", ctypes.c_int, [c_vp]),
     ("gaje_hip_event_elapsed_ms", ctypes.c_int, [c_vp, c_vp, ctypes.POINTER(ctypes.c_float)]),
+    ("gaje_hip_q4_0_packed_bytes", c_i64, [c_i64, c_i64]),
+    ("gaje_hip_q4_0_pack", ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, c_vp]),
     ("gaje_hip_q4_0_gemv", ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_vp]),
     ("gaje_hip_q4_0_gemm", ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_vp]),
     ("gaje_hip_lut4_gemv", ctypes.c_int, [c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_vp]),

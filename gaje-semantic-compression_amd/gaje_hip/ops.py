@@ -71,14 +71,36 @@ def device_name(device: int = 0) -> str:
     return buf.value.decode()
 
 
-def q4_0_gemv(blocks: DeviceBuffer, x: DeviceBuffer, y: DeviceBuffer, n: int, k: int,
-              bias: DeviceBuffer | None = None, bias_len: int = 0, stream=None) -> None:
-    check(lib().gaje_hip_q4_0_gemv(blocks.ptr, x.ptr, _p(bias), bias_len, y.ptr, n, k, stream))
+def q4_0_packed_bytes(n: int, k: int) -> int:
+    v = lib().gaje_hip_q4_0_packed_bytes(int(n), int(k))
+    if v < 0:
+        raise ValueError(f"Q4_0 needs k to be a positive multiple of 32 (got {k})")
+    return v
 
 
-def q4_0_gemm(blocks: DeviceBuffer, X: DeviceBuffer, Y: DeviceBuffer, m: int, n: int, k: int,
+def q4_0_pack(blocks: DeviceBuffer, packed: DeviceBuffer, n: int, k: int, stream=None) -> None:
+    """Q4_0Block rows (file layout) -> the matvec's packed layout, on the device."""
+    check(lib().gaje_hip_q4_0_pack(blocks.ptr, packed.ptr, n, k, stream))
+
+
+def q4_0_upload(blocks: np.ndarray, n: int, k: int) -> DeviceBuffer:
+    """Uploads n rows of Q4_0Blocks and returns them packed for q4_0_gemv."""
+    raw = DeviceBuffer.from_array(np.ascontiguousarray(blocks, dtype=np.uint8))
+    packed = DeviceBuffer(max(q4_0_packed_bytes(n, k), 1))
+    q4_0_pack(raw, packed, n, k)
+    synchronize()
+    raw.close()
+    return packed
+
+
+def q4_0_gemv(packed: DeviceBuffer, x: DeviceBuffer, y: DeviceBuffer, n: int, k: int,
               bias: DeviceBuffer | None = None, bias_len: int = 0, stream=None) -> None:
-    check(lib().gaje_hip_q4_0_gemm(blocks.ptr, X.ptr, _p(bias), bias_len, Y.ptr, m, n, k, stream))
+    check(lib().gaje_hip_q4_0_gemv(packed.ptr, x.ptr, _p(bias), bias_len, y.ptr, n, k, stream))
+
+
+def q4_0_gemm(packed: DeviceBuffer, X: DeviceBuffer, Y: DeviceBuffer, m: int, n: int, k: int,
+              bias: DeviceBuffer | None = None, bias_len: int = 0, stream=None) -> None:
+    check(lib().gaje_hip_q4_0_gemm(packed.ptr, X.ptr, _p(bias), bias_len, Y.ptr, m, n, k, stream))
 
 
 def lut4_gemv(codes: DeviceBuffer, lut: DeviceBuffer, lut_len: int, x: DeviceBuffer,
@@ -112,6 +134,7 @@ def expf(x: DeviceBuffer, y: DeviceBuffer, n: int, stream=None):
 def attention(q: DeviceBuffer, k_cache: DeviceBuffer, v_cache: DeviceBuffer, seq_len: int,
               capacity: int, n_head: int, n_head_kv: int, head_dim: int, out: DeviceBuffer,
               stream=None):
+    """k_cache is [n_head_kv][capacity][head_dim], v_cache [n_head_kv][head_dim][capacity]."""
     check(lib().gaje_hip_attention(q.ptr, k_cache.ptr, v_cache.ptr, seq_len, capacity, n_head,
                                    n_head_kv, head_dim, out.ptr, stream))
 

@@ -76,17 +76,28 @@ int gaje_hip_event_elapsed_ms(void *start, void *stop, float *ms);
  * bias may be NULL; rows i < bias_len add bias[i] (compute_single_row's
  * `self.bias.get(i)`, linear/forward.rs:113-115). */
 
-/* One Q4_0 matvec over 20-byte Q4_0Block rows: GenomicLinear::forward_core on
- * the GenomicQ4_0 variant (linear/forward.rs:84-92,119-132) with the per-row
+/* Q4_0 weights are packed once on the device before the matvec reads them,
+ * as the reference builds its GenomicQ4_0 weights once from the mmap'd file
+ * (GenomicLinear::new, linear/init.rs:12-40).  The packed layout permutes the
+ * nibbles and scale/min words inside each group of four Q4_0Blocks (80 bytes)
+ * so that every accumulation chain reads its codes with one load; it holds the
+ * same bits.  gaje_hip_q4_0_packed_bytes gives its size for an n x k tensor
+ * (n * ceil(k/128) * 80; equal to the file's n * k/32 * 20 when k % 128 == 0)
+ * or -1 if k is not a positive multiple of 32. */
+int64_t gaje_hip_q4_0_packed_bytes(int64_t n, int64_t k);
+int gaje_hip_q4_0_pack(const void *blocks, void *packed, int64_t n, int64_t k, void *stream);
+
+/* One Q4_0 matvec over packed rows: GenomicLinear::forward_core on the
+ * GenomicQ4_0 variant (linear/forward.rs:84-92,119-132) with the per-row
  * genomic_dot_product_q4_0 (compute/kernels/genomic.rs:210-336), including its
  * |t| < 1e-6 -> 0 flush before the bias add. */
-int gaje_hip_q4_0_gemv(const void *blocks, const float *x, const float *bias, int64_t bias_len,
+int gaje_hip_q4_0_gemv(const void *packed, const float *x, const float *bias, int64_t bias_len,
                        float *y, int64_t n, int64_t k, void *stream);
 
 /* The same Q4_0 matvec for m activation rows at once (Y[m][n] = X[m][k] W^T):
  * m independent GenomicLinear::forward_core calls sharing one weight read.
  * No reference function batches rows; semantics are per row as above. */
-int gaje_hip_q4_0_gemm(const void *blocks, const float *X, const float *bias, int64_t bias_len,
+int gaje_hip_q4_0_gemm(const void *packed, const float *X, const float *bias, int64_t bias_len,
                        float *Y, int64_t m, int64_t n, int64_t k, void *stream);
 
 /* LUT-4bit matvec (layout Genomic4Bit, high nibble = even element):
@@ -119,9 +130,9 @@ int gaje_hip_expf(const float *x, float *y, int64_t n, void *stream);
 
 /* The GQA softmax attention of GenomicAttention::forward_attention_core
  * (nn/attention.rs:87-127) over seq_len cached positions, bit-exact.  q is
- * [n_head][head_dim] (already rotated); the caches are head-major
- * [n_head_kv][capacity][head_dim] (positions 0..seq_len-1 used); out is
- * [n_head][head_dim]. */
+ * [n_head][head_dim] (already rotated); k_cache is [n_head_kv][capacity]
+ * [head_dim] and v_cache is [n_head_kv][head_dim][capacity] (positions
+ * 0..seq_len-1 used); out is [n_head][head_dim]. */
 int gaje_hip_attention(const float *q, const float *k_cache, const float *v_cache, int64_t seq_len,
                        int64_t capacity, int n_head, int n_head_kv, int head_dim, float *out, void *stream);
 

@@ -19,6 +19,7 @@ def same_bits(a, b) -> bool:
 pytestmark = pytest.mark.gpu
 
 GEMV_TOL = 1e-4
+Q4_TAIL_PAD = 2048  # bytes after a packed Q4_0 tensor (kernels.h)
 
 
 @pytest.fixture(scope="module")
@@ -83,15 +84,46 @@ def _oracle_q4_rows(O, blocks, x, n, k, bias=None):
     return L.forward_core(x)
 
 
+def pack_q4_0_numpy(blocks, n, k):
+    """The packed row layout, restated with numpy: per group of four blocks,
+    chain l's 8 bytes (dword h = blocks 4g+2h | 4g+2h+1 << 4, byte c = element
+    8c+l), then the four scale|min words; missing blocks are zero."""
+    nb = k // 32
+    G = (nb + 3) // 4
+    b = np.asarray(blocks, np.uint8).reshape(n, nb, 20)
+    codes = np.zeros((n, 4 * G, 32), np.uint8)
+    codes[:, :nb, 0::2] = b[:, :, 4:] & 0x0F
+    codes[:, :nb, 1::2] = b[:, :, 4:] >> 4
+    sm = np.zeros((n, 4 * G, 4), np.uint8)
+    sm[:, :nb] = b[:, :, :4]
+    c = codes.reshape(n, G, 4, 4, 8)                  # [row][g][block][c][l]
+    byte = c[:, :, 0::2] | (c[:, :, 1::2] << 4)       # [row][g][h][c][l]
+    chains = byte.transpose(0, 1, 4, 2, 3).reshape(n, G, 64)
+    return np.concatenate([chains, sm.reshape(n, G, 16)], axis=2).reshape(-1)
+
+
+@pytest.mark.parametrize("n,k", [(3, 896), (2, 4864), (5, 32), (4, 96), (7, 160)])
+def test_q4_0_pack_layout(hip, n, k):
+    blocks = hip.synth.q4_0_tensor(15, f"pack.{n}.{k}", n, k)
+    packed = hip.ops.q4_0_upload(blocks, n, k)
+    ref = pack_q4_0_numpy(blocks, n, k)
+    got = packed.read(np.uint8)
+    # the packed rows, then a zeroed tail the matvec's prefetch may read past the last row
+    assert packed.nbytes == hip.ops.q4_0_packed_bytes(n, k) == ref.size + Q4_TAIL_PAD
+    assert np.array_equal(got[:ref.size], ref)
+    assert not got[ref.size:].any()
+
+
 @pytest.mark.parametrize("n,k", [(4864, 896), (1152, 896), (896, 4864), (963, 576), (17, 1536),
-                                 (64, 8960), (33, 2048), (5, 32), (3, 15360)])
+                                 (64, 8960), (33, 2048), (5, 32), (3, 15360), (9, 96), (11, 160),
+                                 (6, 1056), (300, 8192)])
 def test_q4_0_gemv(hip, O, n, k):
     blocks = hip.synth.q4_0_tensor(11, f"gemv.{n}.{k}", n, k)
     x = hip.synth.normal(12, f"x.{k}", k)
     bias = hip.synth.normal(13, f"b.{n}", n // 2, 0.0, 0.02)  # shorter than n: rows >= len get none
     y = _out(hip, n * 4)
-    hip.ops.q4_0_gemv(_dev(hip, blocks), _dev(hip, x), y, n, k, bias=_dev(hip, bias) if bias.size else None,
-                      bias_len=bias.size)
+    hip.ops.q4_0_gemv(hip.ops.q4_0_upload(blocks, n, k), _dev(hip, x), y, n, k,
+                      bias=_dev(hip, bias) if bias.size else None, bias_len=bias.size)
     got = y.read(np.float32)
     ref = _oracle_q4_rows(O, blocks, x, n, k, bias)
     print(f"q4_0 gemv n={n} k={k} err={floored_rel_err(got, ref):.3e}")
@@ -109,7 +141,7 @@ def test_q4_0_gemv_flush_rule(hip, O):
     x[0], x[1] = 1e-4, -1e-4 + 1e-7  # dot = 1e-10: flushed
     bias = np.array([0.5], np.float32)
     y = _out(hip, 4)
-    hip.ops.q4_0_gemv(_dev(hip, blocks), _dev(hip, x), y, 1, k, bias=_dev(hip, bias), bias_len=1)
+    hip.ops.q4_0_gemv(hip.ops.q4_0_upload(blocks, 1, k), _dev(hip, x), y, 1, k, bias=_dev(hip, bias), bias_len=1)
     got = y.read(np.float32)
     ref = _oracle_q4_rows(O, blocks, x, 1, k, bias)
     assert got[0] == ref[0] == np.float32(0.5)
@@ -208,18 +240,22 @@ def test_expf_device_matches_host_libm(hip, O):
     assert np.array_equal(got.view(np.uint32)[~nan], ref.view(np.uint32)[~nan])
 
 
-@pytest.mark.parametrize("ctx,n_head,n_kv,hd", [(1, 14, 2, 64), (768, 14, 2, 64), (384, 9, 3, 64),
-                                                 (1152, 12, 2, 128), (77, 4, 4, 16)])
-def test_attention_bit_exact(hip, O, ctx, n_head, n_kv, hd):
+# cap % 4 == 0 with head_dim 64 or 128 takes the streaming kernel, the rest the
+# generic one; ctx % 4 != 0 exercises the streaming kernel's scalar tail
+@pytest.mark.parametrize("ctx,n_head,n_kv,hd,cap", [(1, 14, 2, 64, 4), (768, 14, 2, 64, 768), (384, 9, 3, 64, 388),
+                                                     (1152, 12, 2, 128, 1152), (77, 4, 4, 16, 82),
+                                                     (771, 14, 2, 64, 772), (130, 12, 2, 128, 132),
+                                                     (5, 14, 2, 64, 8), (66, 14, 2, 64, 69),
+                                                     (2048, 14, 2, 64, 2112), (100, 6, 2, 96, 100)])
+def test_attention_bit_exact(hip, O, ctx, n_head, n_kv, hd, cap):
     q = hip.synth.normal(81, f"aq.{ctx}.{hd}", n_head * hd)
     k = hip.synth.normal(82, f"ak.{ctx}.{hd}", ctx * n_kv * hd)
     v = hip.synth.normal(83, f"av.{ctx}.{hd}", ctx * n_kv * hd)
     ref = O.attention(q, k, v, ctx, n_head, n_kv, hd)
-    cap = ctx + 5
-    kh = np.zeros((n_kv, cap, hd), np.float32)  # head-major device layout
-    vh = np.zeros((n_kv, cap, hd), np.float32)
+    kh = np.zeros((n_kv, cap, hd), np.float32)  # device layouts: K [head][pos][dim],
+    vh = np.zeros((n_kv, hd, cap), np.float32)  # V [head][dim][pos]
     kh[:, :ctx] = k.reshape(ctx, n_kv, hd).transpose(1, 0, 2)
-    vh[:, :ctx] = v.reshape(ctx, n_kv, hd).transpose(1, 0, 2)
+    vh[:, :, :ctx] = v.reshape(ctx, n_kv, hd).transpose(1, 2, 0)
     out = _out(hip, n_head * hd * 4)
     hip.ops.attention(_dev(hip, q), _dev(hip, kh), _dev(hip, vh), ctx, cap, n_head, n_kv, hd, out)
     got = out.read(np.float32)
