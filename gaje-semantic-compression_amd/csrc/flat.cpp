@@ -241,3 +241,87 @@ int FlatFile::model_config(ModelConfig &c) const {
 }
 
 }  // namespace gaje
+
+// ------------------------------------------------------------- C ABI ----
+
+namespace {
+
+void fill_header(const gaje::FlatHeaderV2 &h, gaje_flat_header *o) {
+    memset(o, 0, sizeof *o);
+    o->version = h.version;
+    o->flags = h.flags;
+    o->num_tensors = h.num_tensors;
+    o->group_size = h.group_size;
+    o->quant_format = h.quant_format;
+    o->arch_family = h.arch_family;
+    o->arch_n_embd = h.arch_n_embd;
+    o->arch_n_head = h.arch_n_head;
+    o->arch_n_head_kv = h.arch_n_head_kv;
+    o->arch_n_blocks = h.arch_n_blocks;
+    o->arch_qk_permute = h.arch_qk_permute;
+    o->quant_type = (int32_t)gaje::quantization_type(h);
+    o->effective_group_size = gaje::effective_group_size(h);
+    o->meta_len = h.meta_len;
+    o->dir_len = h.dir_len;
+    o->weights_offset = h.weights_offset;
+    o->weights_len = h.weights_len;
+}
+
+}  // namespace
+
+extern "C" int gaje_flat_header_from_bytes(const uint8_t *bytes, size_t len, gaje_flat_header *out) {
+    gaje::clear_error();
+    if (!out || (len > 0 && !bytes)) return gaje::set_error(GAJE_ERR_INVALID_ARG, "null argument");
+    if (len < sizeof(gaje::FlatHeaderV2))
+        return gaje::set_error(GAJE_ERR_TOO_SHORT, "Header buffer is less than 4096 bytes");
+    gaje::FlatHeaderV2 h;
+    memcpy(&h, bytes, sizeof h);
+    if (memcmp(h.magic, "GAJE", 4) != 0)
+        return gaje::set_error(GAJE_ERR_INVALID_MAGIC, "Invalid magic bytes (expected 'GAJE')");
+    fill_header(h, out);
+    return GAJE_OK;
+}
+
+extern "C" int gaje_flat_inspect(const char *path, gaje_flat_info *out) {
+    gaje::clear_error();
+    if (!path || !out) return gaje::set_error(GAJE_ERR_INVALID_ARG, "null argument");
+    gaje::FlatFile f;
+    GAJE_TRY(f.open(path));
+    gaje::ModelConfig c;
+    GAJE_TRY(f.model_config(c));
+    memset(out, 0, sizeof *out);
+    fill_header(f.header(), &out->header);
+    out->n_embd = (int64_t)c.n_embd;
+    out->n_head = (int64_t)c.n_head;
+    out->n_head_kv = (int64_t)c.n_head_kv;
+    out->n_blocks = (int64_t)c.n_blocks;
+    out->vocab_size = c.has_vocab_size ? (int64_t)c.vocab_size : -1;
+    out->eps = c.eps;
+    out->rope_base = c.rope_base;
+    out->rope_split = c.rope_style == "split" ? 1 : 0;
+    out->use_genomic_norm = c.use_genomic_norm ? 1 : 0;
+    out->has_descriptor = f.header().arch_family != 0 ? 1 : 0;
+    out->n_tensors = (int32_t)f.entry_count();
+    return GAJE_OK;
+}
+
+extern "C" int gaje_flat_tensor_entry(const char *path, const char *name, gaje_flat_tensor *out) {
+    gaje::clear_error();
+    if (!path || !name || !out) return gaje::set_error(GAJE_ERR_INVALID_ARG, "null argument");
+    gaje::FlatFile f;
+    GAJE_TRY(f.open(path));
+    const gaje::TensorEntry *e = f.find(name);
+    if (!e) return gaje::set_error(GAJE_ERR_NOT_FOUND, "Flat tensor entry '%s' not found", name);
+    out->bit_depth = e->bit_depth;
+    out->out_features = e->out_features;
+    out->in_features = e->in_features;
+    out->dna_off = e->dna_off;
+    out->dna_len = e->dna_len;
+    out->c_off = e->c_off;
+    out->c_len = e->c_len;
+    out->anc_off = e->anc_off;
+    out->anc_len = e->anc_len;
+    out->bias_off = e->bias_off;
+    out->bias_len = e->bias_len;
+    return GAJE_OK;
+}

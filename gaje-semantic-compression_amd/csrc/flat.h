@@ -103,6 +103,7 @@ public:
     // (src/io/flat_reader.rs:125-139).
     int model_config(ModelConfig &out) const;
     size_t size() const { return size_; }
+    size_t entry_count() const { return tensors_.size(); }
 
 private:
     const uint8_t *base_ = nullptr;

@@ -7,9 +7,9 @@ reference's PyO3 surface (`load_genomic_auto`, `RustGenomicLLM.forward`, ...).
 from ._lib import (GajeError, GajeIOError, GajeValueError, LIB_PATH, SIGNATURES, last_error,
                    lib)
 from .model import GenomicLLM, load_genomic_auto
-from . import ops, synth
+from . import flat, ops, synth
 
 RustGenomicLLM = GenomicLLM
 
 __all__ = ["GajeError", "GajeIOError", "GajeValueError", "GenomicLLM", "RustGenomicLLM",
-           "LIB_PATH", "SIGNATURES", "last_error", "lib", "load_genomic_auto", "ops", "synth"]
+           "LIB_PATH", "SIGNATURES", "flat", "last_error", "lib", "load_genomic_auto", "ops", "synth"]

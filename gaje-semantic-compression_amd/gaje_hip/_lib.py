@@ -53,6 +53,31 @@ class ModelInfo(ctypes.Structure):
                 ("n_logits", c_i64)]
 
 
+class FlatHeader(ctypes.Structure):
+    _fields_ = [("version", ctypes.c_uint32), ("flags", ctypes.c_uint32), ("num_tensors", ctypes.c_uint32),
+                ("group_size", ctypes.c_uint32), ("quant_format", ctypes.c_uint32),
+                ("arch_family", ctypes.c_uint32), ("arch_n_embd", ctypes.c_uint32),
+                ("arch_n_head", ctypes.c_uint32), ("arch_n_head_kv", ctypes.c_uint32),
+                ("arch_n_blocks", ctypes.c_uint32), ("arch_qk_permute", ctypes.c_uint32),
+                ("quant_type", ctypes.c_int32), ("effective_group_size", ctypes.c_uint32),
+                ("pad_", ctypes.c_uint32), ("meta_len", ctypes.c_uint64), ("dir_len", ctypes.c_uint64),
+                ("weights_offset", ctypes.c_uint64), ("weights_len", ctypes.c_uint64)]
+
+
+class FlatInfo(ctypes.Structure):
+    _fields_ = [("header", FlatHeader), ("n_embd", c_i64), ("n_head", c_i64), ("n_head_kv", c_i64),
+                ("n_blocks", c_i64), ("vocab_size", c_i64), ("eps", ctypes.c_float),
+                ("rope_base", ctypes.c_float), ("rope_split", ctypes.c_int32),
+                ("use_genomic_norm", ctypes.c_int32), ("has_descriptor", ctypes.c_int32),
+                ("n_tensors", ctypes.c_int32)]
+
+
+class FlatTensor(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint64) for n in ("bit_depth", "out_features", "in_features", "dna_off",
+                                               "dna_len", "c_off", "c_len", "anc_off", "anc_len",
+                                               "bias_off", "bias_len")]
+
+
 class SynthConfig(ctypes.Structure):
     _fields_ = [("n_embd", c_i64), ("n_head", c_i64), ("n_head_kv", c_i64), ("n_blocks", c_i64),
                 ("ffn", c_i64), ("vocab_size", c_i64), ("eps", ctypes.c_float),
@@ -122,6 +147,9 @@ SIGNATURES = [
     ("gaje_hip_bench_gemv", ctypes.c_int, [ctypes.c_int, c_vp, ctypes.c_size_t, c_vp, ctypes.c_size_t,
                                            ctypes.c_int, c_vp, c_vp, c_i64, c_i64, ctypes.c_int,
                                            ctypes.POINTER(ctypes.c_float)]),
+    ("gaje_flat_header_from_bytes", ctypes.c_int, [c_vp, ctypes.c_size_t, ctypes.POINTER(FlatHeader)]),
+    ("gaje_flat_inspect", ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(FlatInfo)]),
+    ("gaje_flat_tensor_entry", ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(FlatTensor)]),
     ("gaje_synth_write_flat", ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(SynthConfig)]),
     ("gaje_synth_q4_0", ctypes.c_int, [ctypes.c_uint64, ctypes.c_char_p, c_i64, c_i64, c_vp]),
     ("gaje_synth_lut4", ctypes.c_int, [ctypes.c_uint64, ctypes.c_char_p, c_i64, c_i64, c_vp, c_vp]),

@@ -161,7 +161,8 @@ typedef struct {
 /* load_genomic_auto for a .gaje.flat file (io/flat_reader.rs:240-252 ->
  * GajeFlatFileReader::open/load_genomic :33-236): mmap, header, metadata and
  * directory, ArchitectureDescriptor-over-JSON precedence, one upload per tensor
- * into HBM in its native packing.  k_wta_ratio starts at 0.5 (:234). */
+ * into HBM (Q4_0 tensors packed as for gaje_hip_q4_0_pack, the rest as stored).
+ * k_wta_ratio starts at 0.5 (:234). */
 int gaje_hip_open(const char *flat_path, int device, gaje_hip_model **out);
 void gaje_hip_close(gaje_hip_model *m);
 int gaje_hip_model_info_get(const gaje_hip_model *m, gaje_hip_model_info *info);
@@ -250,6 +251,49 @@ int gaje_hip_time_stage(gaje_hip_model *m, int stage, int64_t layer, int iters, 
 int gaje_hip_bench_gemv(int format, const void *w_base, size_t copy_stride, const float *lut_base,
                         size_t lut_stride, int copies, const float *x, float *y, int64_t n, int64_t k,
                         int iters, float *avg_ms);
+
+/* ------------------------------------------------- .gaje.flat reader --- */
+/* Host-only entry points over the reader that gaje_hip_open uses, so a
+ * file can be inspected (and the reader tested) without a GPU. */
+typedef struct {
+    uint32_t version, flags, num_tensors;
+    uint32_t group_size, quant_format;
+    uint32_t arch_family, arch_n_embd, arch_n_head, arch_n_head_kv, arch_n_blocks, arch_qk_permute;
+    int32_t quant_type;             /* quantization_type(): 0 legacy centroids, 1 Q4_0, 2 Q8_0, 3 unknown */
+    uint32_t effective_group_size;  /* effective_group_size(): group_size, or 16 when 0 */
+    uint32_t pad_;
+    uint64_t meta_len, dir_len, weights_offset, weights_len;
+} gaje_flat_header;
+
+/* FlatHeaderV2::from_bytes (io/header/flat.rs:46-59) with quantization_type
+ * and effective_group_size (:63-79): GAJE_ERR_TOO_SHORT if len < 4096, then
+ * GAJE_ERR_INVALID_MAGIC unless the bytes start with "GAJE". */
+int gaje_flat_header_from_bytes(const uint8_t *bytes, size_t len, gaje_flat_header *out);
+
+typedef struct {
+    gaje_flat_header header;
+    int64_t n_embd, n_head, n_head_kv, n_blocks;
+    int64_t vocab_size;          /* metadata config.vocab_size, -1 if absent */
+    float eps, rope_base;
+    int32_t rope_split;          /* rope_style == "split" */
+    int32_t use_genomic_norm;
+    int32_t has_descriptor;      /* arch_family != 0: the header overrides the JSON */
+    int32_t n_tensors;           /* entries in the tensor directory */
+} gaje_flat_info;
+
+/* GajeFlatFileReader::open (io/flat_reader.rs:33-69) and load_genomic's
+ * config resolution, JSON then header descriptor (:124-139).  Errors as
+ * gaje_hip_open reports them for a bad file. */
+int gaje_flat_inspect(const char *path, gaje_flat_info *out);
+
+typedef struct {
+    uint64_t bit_depth, out_features, in_features;
+    uint64_t dna_off, dna_len, c_off, c_len, anc_off, anc_len, bias_off, bias_len;
+} gaje_flat_tensor;
+
+/* The FlatTensorEntry named `name` (io/flat_reader.rs:9-22);
+ * GAJE_ERR_NOT_FOUND if the directory has none. */
+int gaje_flat_tensor_entry(const char *path, const char *name, gaje_flat_tensor *out);
 
 /* ----------------------------------------------- synthetic .flat writer --- */
 /* Random-init model writer for the benchmark shapes (no checkpoints exist in

@@ -175,8 +175,16 @@ def dot_q4_0(blocks: np.ndarray, x: np.ndarray, scalar: bool = False) -> float:
 
 
 def dot_4bit(codes: np.ndarray, x: np.ndarray, centroids: np.ndarray) -> float:
+    """genomic_dot_product_4bit over one row: centroids are per block ([n_blocks][16]);
+    a single 16-entry table is shared by every block, as init.rs:109-124 expands it."""
     c = np.ascontiguousarray(codes, dtype=np.uint8).reshape(-1)
-    return lib().orc_dot_4bit(_ptr(c), _ptr(_f32(x)), _ptr(_f32(centroids)), 16, c.size // 16)
+    nb = c.size // 16
+    t = _f32(centroids)
+    if t.size == 16:
+        t = np.ascontiguousarray(np.tile(t, nb))
+    if t.size < nb * 16:
+        raise ValueError("dot_4bit needs 16 centroids per block")
+    return lib().orc_dot_4bit(_ptr(c), _ptr(_f32(x)), _ptr(t), 16, nb)
 
 
 def dot_f32(a: np.ndarray, b: np.ndarray) -> float:
