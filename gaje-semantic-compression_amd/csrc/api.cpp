@@ -5,6 +5,7 @@
 #include <algorithm>
 #include <atomic>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 
@@ -302,8 +303,12 @@ extern "C" int gaje_hip_bench_gemv(int format, const void *w_base, size_t copy_s
         return set_error(GAJE_ERR_INVALID_ARG, "unknown format %d", format);
     hipStream_t s;
     GAJE_HIP_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    // one pass launches `per_pass` matvecs cycling through the copies (at least
+    // 128, so that a replayed graph is not dominated by its own launch cost)
+    const int per_pass = copies < 128 ? ((128 + copies - 1) / copies) * copies : copies;
     auto launch_all = [&]() -> int {
-        for (int c = 0; c < copies; ++c) {
+        for (int i = 0; i < per_pass; ++i) {
+            const int c = i % copies;
             GemvParams p = plain_gemv(format, (const uint8_t *)w_base + (size_t)c * copy_stride, x, nullptr, 0, y, n, k);
             if (format == FMT_LUT4) {
                 p.lut = (const float *)((const uint8_t *)lut_base + (size_t)c * lut_stride);
@@ -316,11 +321,30 @@ extern "C" int gaje_hip_bench_gemv(int format, const void *w_base, size_t copy_s
         return GAJE_OK;
     };
     int rc = launch_all();  // warm-up, eager (validates the arguments)
+    if (rc == GAJE_OK && getenv("GAJE_HIP_PROFILE")) {
+        // eager launches only, so that a kernel tracer sees every dispatch
+        int reps = (iters + per_pass - 1) / per_pass;
+        hipEvent_t a = nullptr, b = nullptr;
+        float ms = 0.0f;
+        (void)hipEventCreate(&a);
+        (void)hipEventCreate(&b);
+        (void)hipEventRecord(a, s);
+        for (int r = 0; r < reps && rc == GAJE_OK; ++r) rc = launch_all();
+        (void)hipEventRecord(b, s);
+        if (rc == GAJE_OK && hipEventSynchronize(b) == hipSuccess) (void)hipEventElapsedTime(&ms, a, b);
+        (void)hipEventDestroy(a);
+        (void)hipEventDestroy(b);
+        (void)hipStreamSynchronize(s);
+        (void)hipStreamDestroy(s);
+        GAJE_TRY(rc);
+        *avg_ms = ms / (float)(reps * per_pass);
+        return GAJE_OK;
+    }
     hipGraph_t g = nullptr;
     hipGraphExec_t ge = nullptr;
     hipEvent_t e0 = nullptr, e1 = nullptr;
     float ms = 0.0f;
-    int reps = (iters + copies - 1) / copies;
+    int reps = (iters + per_pass - 1) / per_pass;
     if (rc == GAJE_OK && hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) == hipSuccess) {
         rc = launch_all();
         if (hipStreamEndCapture(s, &g) != hipSuccess && rc == GAJE_OK)
@@ -345,6 +369,6 @@ extern "C" int gaje_hip_bench_gemv(int format, const void *w_base, size_t copy_s
     (void)hipStreamSynchronize(s);
     (void)hipStreamDestroy(s);
     GAJE_TRY(rc);
-    *avg_ms = ms / (float)(reps * copies);
+    *avg_ms = ms / (float)(reps * per_pass);
     return GAJE_OK;
 }

@@ -55,6 +55,12 @@ def _p(b):
     return None if b is None else b.ptr
 
 
+def memcpy_d2d(dst: DeviceBuffer, src: DeviceBuffer, nbytes: int) -> None:
+    if nbytes > min(dst.nbytes, src.nbytes):
+        raise ValueError("copy larger than a buffer")
+    check(lib().gaje_hip_memcpy_d2d(dst.ptr, src.ptr, int(nbytes)))
+
+
 def synchronize() -> None:
     check(lib().gaje_hip_device_synchronize())
 

@@ -247,7 +247,9 @@ int gaje_hip_time_stage(gaje_hip_model *m, int stage, int64_t layer, int iters, 
  * lut_base + i * lut_stride), cycling through the copies so that the set can
  * exceed the caches.  The launches are captured once in a HIP graph and
  * replayed until `iters` launches ran; timed with HIP events on a private
- * stream. */
+ * stream.  With GAJE_HIP_PROFILE set in the environment the launches are
+ * issued one by one instead (no graph), so that a kernel tracer records each;
+ * the model's token step is likewise launched kernel by kernel then. */
 int gaje_hip_bench_gemv(int format, const void *w_base, size_t copy_stride, const float *lut_base,
                         size_t lut_stride, int copies, const float *x, float *y, int64_t n, int64_t k,
                         int iters, float *avg_ms);
