@@ -118,43 +118,48 @@ __device__ __forceinline__ float swiglu1(float g, float u) {
     return silu * u;
 }
 
-// rms_norm of xs[0..n) in place (norm.rs:52-88): sum of squares in eight FMA
+// rms_norm's 1/rms of xs[0..n) (norm.rs:52-88): sum of squares in eight FMA
 // chains over 8-float chunks, reduced ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7)),
-// scalar tail, inv = 1/sqrt(ss/n + eps), out = (x * inv) * w.
+// scalar tail, inv = 1/sqrt(ss/n + eps), stored by thread 0 in *inv_slot.
+// Threads 0..7 of the block compute it; the caller synchronises.
+__device__ inline void rms_inv_plain(const float *xs, int64_t n, float eps, float *inv_slot) {
+    const int tid = threadIdx.x;
+    if (tid >= 8) return;
+    float acc = 0.0f;
+    const int64_t chunks = n / 8;
+    int64_t i = 0;
+    for (; i + 8 <= chunks; i += 8) {  // eight LDS reads in flight, then the chain
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = xs[8 * (i + u) + tid];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc = fmaf(v[u], v[u], acc);
+    }
+    for (; i < chunks; ++i) {
+        const float v = xs[8 * i + tid];
+        acc = fmaf(v, v, acc);
+    }
+    const float u = acc + __shfl(acc, (tid + 4) & 7, 8);  // lane l<4: a_l + a_{l+4}
+    const float v = u + __shfl(u, (tid + 1) & 7, 8);      // lane 0: u0+u1, lane 2: u2+u3
+    const float tot = v + __shfl(v, (tid + 2) & 7, 8);    // lane 0: (u0+u1) + (u2+u3)
+    if (tid == 0) {
+        float ss = tot;
+        for (int64_t k = chunks * 8; k < n; ++k) {
+            const float sq = xs[k] * xs[k];
+            ss = ss + sq;
+        }
+        const float mean = ss / (float)n;
+        *inv_slot = 1.0f / sqrtf(mean + eps);
+    }
+}
+
+// rms_norm of xs[0..n) in place: out = (x * inv) * w, each product rounded.
 // Called by every thread of the block (it contains a barrier).
 __device__ inline void rmsnorm_inplace(float *xs, int64_t n, const float *w, float eps, float *inv_slot) {
-    const int tid = threadIdx.x;
-    if (tid < 8) {
-        float acc = 0.0f;
-        const int64_t chunks = n / 8;
-        int64_t i = 0;
-        for (; i + 8 <= chunks; i += 8) {  // eight LDS reads in flight, then the chain
-            float v[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = xs[8 * (i + u) + tid];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) acc = fmaf(v[u], v[u], acc);
-        }
-        for (; i < chunks; ++i) {
-            const float v = xs[8 * i + tid];
-            acc = fmaf(v, v, acc);
-        }
-        const float u = acc + __shfl(acc, (tid + 4) & 7, 8);  // lane l<4: a_l + a_{l+4}
-        const float v = u + __shfl(u, (tid + 1) & 7, 8);      // lane 0: u0+u1, lane 2: u2+u3
-        const float tot = v + __shfl(v, (tid + 2) & 7, 8);    // lane 0: (u0+u1) + (u2+u3)
-        if (tid == 0) {
-            float ss = tot;
-            for (int64_t i = chunks * 8; i < n; ++i) {
-                const float sq = xs[i] * xs[i];
-                ss = ss + sq;
-            }
-            const float mean = ss / (float)n;
-            *inv_slot = 1.0f / sqrtf(mean + eps);
-        }
-    }
+    rms_inv_plain(xs, n, eps, inv_slot);
     __syncthreads();
     const float inv = *inv_slot;
-    for (int64_t k = tid; k < n; k += blockDim.x) {
+    for (int64_t k = threadIdx.x; k < n; k += blockDim.x) {
         const float t = xs[k] * inv;
         xs[k] = t * w[k];
     }

@@ -96,40 +96,58 @@ __device__ __forceinline__ float q4_chain(float acc, const float (&d)[4], const 
     return acc;
 }
 
+// x of one packed group for chain l: its four blocks' four inputs.
+struct X4 {
+    float4 b0, b1, b2, b3;
+};
+__device__ __forceinline__ X4 read_x4(const float *xg) {
+    return X4{*(const float4 *)(xg), *(const float4 *)(xg + 4), *(const float4 *)(xg + 8), *(const float4 *)(xg + 12)};
+}
+
 // One full packed group (blocks 4g .. 4g+3): the sixteen dequantised values
-// are formed before the chain consumes them, so the LDS reads of x and the
-// conversions overlap instead of alternating with the dependent FMAs.
-__device__ __forceinline__ float q4_group(float acc, const vu2 n, const vu4 s, const float *xg) {
-    const float4 x0 = *(const float4 *)(xg), x1 = *(const float4 *)(xg + 4);
-    const float4 x2 = *(const float4 *)(xg + 8), x3 = *(const float4 *)(xg + 12);
+// are formed before the chain consumes them, so the conversions overlap the
+// LDS reads instead of alternating with the dependent FMAs.
+__device__ __forceinline__ float q4_group(float acc, const vu2 n, const vu4 s, const X4 &x) {
     float d0[4], d1[4], d2[4], d3[4];
     q4_dequant(d0, opaque_and(n.x, 0x0F0F0F0Fu), s.x);
     q4_dequant(d1, opaque_and(n.x >> 4, 0x0F0F0F0Fu), s.y);
     q4_dequant(d2, opaque_and(n.y, 0x0F0F0F0Fu), s.z);
     q4_dequant(d3, opaque_and(n.y >> 4, 0x0F0F0F0Fu), s.w);
-    acc = q4_chain(acc, d0, x0);
-    acc = q4_chain(acc, d1, x1);
-    acc = q4_chain(acc, d2, x2);
-    acc = q4_chain(acc, d3, x3);
+    acc = q4_chain(acc, d0, x.b0);
+    acc = q4_chain(acc, d1, x.b1);
+    acc = q4_chain(acc, d2, x.b2);
+    acc = q4_chain(acc, d3, x.b3);
     return acc;
 }
+__device__ __forceinline__ float q4_group(float acc, const vu2 n, const vu4 s, const float *xg) {
+    return q4_group(acc, n, s, read_x4(xg));
+}
 
-// A row's last group with nblk (1..4) blocks.
-__device__ __forceinline__ float q4_group_tail(float acc, const vu2 n, const vu4 s, const float *xg, int nblk) {
-    float d[4];
-    q4_dequant(d, opaque_and(n.x, 0x0F0F0F0Fu), s.x);
-    acc = q4_chain(acc, d, *(const float4 *)(xg));
-    if (nblk > 1) {
-        q4_dequant(d, opaque_and(n.x >> 4, 0x0F0F0F0Fu), s.y);
-        acc = q4_chain(acc, d, *(const float4 *)(xg + 4));
-    }
-    if (nblk > 2) {
-        q4_dequant(d, opaque_and(n.y, 0x0F0F0F0Fu), s.z);
-        acc = q4_chain(acc, d, *(const float4 *)(xg + 8));
-    }
-    if (nblk > 3) {
-        q4_dequant(d, opaque_and(n.y >> 4, 0x0F0F0F0Fu), s.w);
-        acc = q4_chain(acc, d, *(const float4 *)(xg + 12));
+// The row's last groups from ring slots 0..T-1, branch-free: `left` blocks
+// remain, and a block's four chain steps are kept only if it exists (the
+// condition is uniform, so the select costs one instruction per block).  Slots
+// past the row hold finite bytes of the following rows or of the tensor's
+// padding; their results are discarded.
+template <int T, int D>
+__device__ __forceinline__ float q4_tail_pass(float acc, const vu2 (&n)[D], const vu4 (&s)[D], const float *xg,
+                                              int left) {
+#pragma unroll
+    for (int i = 0; i < T; ++i) {
+        const X4 x = read_x4(xg + 16 * i);
+        float d0[4], d1[4], d2[4], d3[4];
+        q4_dequant(d0, opaque_and(n[i].x, 0x0F0F0F0Fu), s[i].x);
+        q4_dequant(d1, opaque_and(n[i].x >> 4, 0x0F0F0F0Fu), s[i].y);
+        q4_dequant(d2, opaque_and(n[i].y, 0x0F0F0F0Fu), s[i].z);
+        q4_dequant(d3, opaque_and(n[i].y >> 4, 0x0F0F0F0Fu), s[i].w);
+        const int b = left - 4 * i;  // blocks of this group that exist (<= 0: none)
+        float t = q4_chain(acc, d0, x.b0);
+        acc = b > 0 ? t : acc;
+        t = q4_chain(acc, d1, x.b1);
+        acc = b > 1 ? t : acc;
+        t = q4_chain(acc, d2, x.b2);
+        acc = b > 2 ? t : acc;
+        t = q4_chain(acc, d3, x.b3);
+        acc = b > 3 ? t : acc;
     }
     return acc;
 }
@@ -141,6 +159,11 @@ struct Q4Ring {
     vu2 n[D];
     vu4 s[D];
 };
+
+template <int T, int D>
+__device__ __forceinline__ float q4_tail(float acc, const Q4Ring<D> &r, const float *xg, int left) {
+    return q4_tail_pass<T, D>(acc, r.n, r.s, xg, left);
+}
 
 // Issues the loads of the row's first D groups.  A row shorter than D groups
 // reads into the next row or the tensor's tail padding (Q4_TAIL_PAD); those
@@ -180,13 +203,10 @@ __device__ __forceinline__ float q4_consume(const GemvParams &p, const XView &xv
         gp += D * 80;
         xg += 16 * D;
     }
-    // the last (< D) groups are already in the ring, in order; only a row's
-    // final group can be partial
-#pragma unroll
-    for (int i = 0; i < D; ++i) {
-        if (g + i < Gf) acc = q4_group(acc, r.n[i], r.s[i], xg + 16 * i);
-        else if (g + i < G) acc = q4_group_tail(acc, r.n[i], r.s[i], xg + 16 * i, nb - 4 * (g + i));
-    }
+    // the last <= D groups are already in the ring, in order: one branch-free
+    // pass over T slots (T = D or D/2)
+    if (G - g > D / 2) acc = q4_tail<D>(acc, r, xg, nb - 4 * g);
+    else if (G > g) acc = q4_tail<D / 2>(acc, r, xg, nb - 4 * g);
     // lanes base..base+7 hold chains 0..7
     const float u = acc + shfl(acc, base + ((l + 4) & 7));  // lane l<4: a_l + a_{l+4}
     const float v = u + shfl(u, base + ((l + 2) & 7));      // lane 0: u0+u2, lane 1: u1+u3
@@ -340,48 +360,42 @@ __device__ __forceinline__ float finish_row(const GemvParams &p, const XView &xv
     return v;
 }
 
-// rms_norm over the chain-major LDS copy: lane l < 8 walks chain l (elements
-// 8i + l), which is its own LDS row; K % 32 == 0 here so there is no tail.
-__device__ inline void rmsnorm_chain_major(const XView &xv, int64_t K, const float *w, float eps, float *inv_slot) {
+// rms_norm's 1/rms over the chain-major LDS copy (norm.rs:52-88): lane l < 8
+// walks chain l (elements 8i + l), which is its own LDS row, reduces the eight
+// chains, and lane 0 stores 1/sqrt(ss/n + eps) in *inv_slot.  K % 32 == 0 here,
+// so there is no tail.  The caller synchronises before reading the slot.
+__device__ inline void rms_inv_chain_major(const XView &xv, int64_t K, float eps, float *inv_slot) {
     const int tid = threadIdx.x;
-    if (tid < 8) {
-        const float *xl = xv.x + tid * xv.stride;
-        const int64_t n8 = K / 8;  // a multiple of 4
-        float acc = 0.0f;
-        int64_t i = 0;
-        for (; i + 16 <= n8; i += 16) {
-            float4 v[4];
+    if (tid >= 8) return;
+    const float *xl = xv.x + tid * xv.stride;
+    const int64_t n8 = K / 8;  // a multiple of 4
+    float acc = 0.0f;
+    int64_t i = 0;
+    for (; i + 16 <= n8; i += 16) {
+        float4 v[4];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) v[u] = *(const float4 *)(xl + i + 4 * u);
+        for (int u = 0; u < 4; ++u) v[u] = *(const float4 *)(xl + i + 4 * u);
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                acc = fmaf(v[u].x, v[u].x, acc);
-                acc = fmaf(v[u].y, v[u].y, acc);
-                acc = fmaf(v[u].z, v[u].z, acc);
-                acc = fmaf(v[u].w, v[u].w, acc);
-            }
-        }
-        for (; i < n8; i += 4) {
-            const float4 v = *(const float4 *)(xl + i);
-            acc = fmaf(v.x, v.x, acc);
-            acc = fmaf(v.y, v.y, acc);
-            acc = fmaf(v.z, v.z, acc);
-            acc = fmaf(v.w, v.w, acc);
-        }
-        const float u = acc + __shfl(acc, (tid + 4) & 7, 8);  // lane l<4: a_l + a_{l+4}
-        const float v = u + __shfl(u, (tid + 1) & 7, 8);      // lane 0: u0+u1, lane 2: u2+u3
-        const float tot = v + __shfl(v, (tid + 2) & 7, 8);    // lane 0: (u0+u1) + (u2+u3)
-        if (tid == 0) {
-            const float mean = tot / (float)K;
-            *inv_slot = 1.0f / sqrtf(mean + eps);
+        for (int u = 0; u < 4; ++u) {
+            acc = fmaf(v[u].x, v[u].x, acc);
+            acc = fmaf(v[u].y, v[u].y, acc);
+            acc = fmaf(v[u].z, v[u].z, acc);
+            acc = fmaf(v[u].w, v[u].w, acc);
         }
     }
-    __syncthreads();
-    const float inv = *inv_slot;
-    for (int64_t k = tid; k < K; k += blockDim.x) {
-        float &x = xv.at(k);
-        const float t = x * inv;
-        x = t * w[k];
+    for (; i < n8; i += 4) {
+        const float4 v = *(const float4 *)(xl + i);
+        acc = fmaf(v.x, v.x, acc);
+        acc = fmaf(v.y, v.y, acc);
+        acc = fmaf(v.z, v.z, acc);
+        acc = fmaf(v.w, v.w, acc);
+    }
+    const float u = acc + __shfl(acc, (tid + 4) & 7, 8);  // lane l<4: a_l + a_{l+4}
+    const float v = u + __shfl(u, (tid + 1) & 7, 8);      // lane 0: u0+u1, lane 2: u2+u3
+    const float tot = v + __shfl(v, (tid + 2) & 7, 8);    // lane 0: (u0+u1) + (u2+u3)
+    if (tid == 0) {
+        const float mean = tot / (float)K;
+        *inv_slot = 1.0f / sqrtf(mean + eps);
     }
 }
 
@@ -437,8 +451,10 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
 
     // ---- prologue: activation vector (and the norm weights) into LDS, one
     // batch of loads in flight per thread; normalised if requested ----
-    float *nw = smem + nw_off;  // plain copy of norm_w when there is one
+    float *nw = smem + nw_off;  // plain copy of norm_w when the vector spans several batches
     int bad_in = 0;
+    constexpr int XB4 = 6;
+    float4 xr[XB4], wr[XB4];
     if constexpr (FMT == FMT_LUT4) {
         constexpr int XB = 8;
         for (int64_t k0 = 0; k0 < K; k0 += XB * THREADS) {
@@ -461,11 +477,11 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
             }
         }
     } else {
-        // K % 4 == 0 and 16-byte aligned x / norm_w (checked at launch)
-        constexpr int XB4 = 6;
+        // K % 4 == 0 and 16-byte aligned x / norm_w (checked at launch).  When
+        // the vector fits one batch its values stay in registers for the norm.
         const int64_t K4 = K >> 2;
+        const bool one_batch = K4 <= XB4 * THREADS;
         for (int64_t m0 = 0; m0 < K4; m0 += XB4 * THREADS) {
-            float4 xr[XB4], wr[XB4];
 #pragma unroll
             for (int u = 0; u < XB4; ++u) {
                 const int64_t m = m0 + u * THREADS + tid;
@@ -482,19 +498,52 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
                     xv.at(4 * m + 1) = v.y;
                     xv.at(4 * m + 2) = v.z;
                     xv.at(4 * m + 3) = v.w;
-                    if (p.norm_w) *(float4 *)(nw + 4 * m) = wr[u];
+                    if (p.norm_w && !one_batch) *(float4 *)(nw + 4 * m) = wr[u];
                     bad_in |= isnan(v.x) | isnan(v.y) | isnan(v.z) | isnan(v.w);
                 }
             }
         }
+        if (__syncthreads_or(bad_in) && p.st_in >= 0 && tid == 0) nan_flag(st, p.layer, p.st_in);
+        if (p.norm_w) {
+            if constexpr (FMT == FMT_Q4_0) rms_inv_chain_major(xv, K, p.eps, &inv_slot);
+            else rms_inv_plain(smem, K, p.eps, &inv_slot);
+            __syncthreads();
+            const float inv = inv_slot;
+            int bad = 0;
+            if (one_batch) {
+#pragma unroll
+                for (int u = 0; u < XB4; ++u) {
+                    const int64_t m = u * THREADS + tid;
+                    if (m < K4) {
+                        float t[4] = {xr[u].x * inv, xr[u].y * inv, xr[u].z * inv, xr[u].w * inv};
+                        const float w4[4] = {wr[u].x, wr[u].y, wr[u].z, wr[u].w};
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) {
+                            t[c] = t[c] * w4[c];  // (x * inv) * w, each product rounded
+                            xv.at(4 * m + c) = t[c];
+                            bad |= isnan(t[c]);
+                        }
+                    }
+                }
+            } else {
+                for (int64_t k = tid; k < K; k += THREADS) {
+                    float &x = xv.at(k);
+                    const float t = x * inv;
+                    x = t * nw[k];
+                    bad |= isnan(x);
+                }
+            }
+            if (__syncthreads_or(bad) && p.st_norm >= 0 && tid == 0) nan_flag(st, p.layer, p.st_norm);
+        }
     }
-    if (__syncthreads_or(bad_in) && p.st_in >= 0 && tid == 0) nan_flag(st, p.layer, p.st_in);
-    if (p.norm_w) {
-        if constexpr (FMT == FMT_Q4_0) rmsnorm_chain_major(xv, K, nw, p.eps, &inv_slot);
-        else rmsnorm_inplace(smem, K, nw, p.eps, &inv_slot);
-        int bad = 0;
-        for (int64_t k = tid; k < K; k += THREADS) bad |= isnan(xv.at(k));
-        if (__syncthreads_or(bad) && p.st_norm >= 0 && tid == 0) nan_flag(st, p.layer, p.st_norm);
+    if constexpr (FMT == FMT_LUT4) {
+        if (__syncthreads_or(bad_in) && p.st_in >= 0 && tid == 0) nan_flag(st, p.layer, p.st_in);
+        if (p.norm_w) {
+            rmsnorm_inplace(smem, K, nw, p.eps, &inv_slot);
+            int bad = 0;
+            for (int64_t k = tid; k < K; k += THREADS) bad |= isnan(xv.at(k));
+            if (__syncthreads_or(bad) && p.st_norm >= 0 && tid == 0) nan_flag(st, p.layer, p.st_norm);
+        }
     }
     if (p.gnorm) {
         // use_genomic_norm (block/forward.rs:115-123) sums with a rayon
@@ -514,8 +563,8 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
             const float sc = p.h_scale / rms;
             for (int64_t k = tid; k < K; k += THREADS) xv.at(k) = xv.at(k) * sc;
         }
+        __syncthreads();
     }
-    __syncthreads();
     if (p.x_out && blockIdx.x == 0)
         for (int64_t k = tid; k < K; k += THREADS) p.x_out[k] = xv.at(k);
 
@@ -677,7 +726,10 @@ static int64_t gemv_x_floats(int64_t K, int fmt) {
 }
 
 size_t gemv_lds_bytes(int64_t K, int fmt, bool norm) {
-    return (size_t)(gemv_x_floats(K, fmt) + (norm ? ((K + 3) & ~(int64_t)3) : 0)) * 4;
+    // Q4_0: + one ring's worth of groups (16 x 16 floats) that the branch-free
+    // tail may read past the last chain row
+    const int64_t slack = fmt == FMT_Q4_0 ? 16 * 2 * Q4_PREFETCH : 0;
+    return (size_t)(gemv_x_floats(K, fmt) + (norm ? ((K + 3) & ~(int64_t)3) : 0) + slack) * 4;
 }
 
 int launch_gemv(const GemvParams &p, hipStream_t s) {
