@@ -31,7 +31,7 @@ int set_error(int code, const char *fmt, ...) {
 void clear_error() { g_last_error.clear(); }
 
 size_t max_lds_per_block() {
-    // The kernels are validated with at most 64 KiB of LDS per workgroup.
+    // The device's own limit (160 KiB per workgroup on gfx950).
     static std::atomic<size_t> cache[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 64 * 1024;
@@ -40,7 +40,7 @@ size_t max_lds_per_block() {
         int a = 0;
         if (hipDeviceGetAttribute(&a, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || a <= 0)
             a = 64 * 1024;
-        v = std::min<size_t>((size_t)a, 64 * 1024);
+        v = std::min<size_t>((size_t)a, 160 * 1024);
         cache[dev].store(v, std::memory_order_relaxed);
     }
     return v;

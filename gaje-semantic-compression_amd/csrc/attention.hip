@@ -12,9 +12,10 @@
 // The current token's k/v were appended by the fused QKV kernel, so the range
 // 0..pos is the causal window.
 //
-// Cache layout: K is [kv head][position][dim] (a score reads one contiguous
-// row); V is [kv head][dim][position] (an output dimension's chain reads one
-// contiguous row).
+// Cache layout: K and V are both [kv head][dim][position].  A thread scoring
+// four consecutive positions reads one 16-byte quad of each key dimension's
+// row, so a wave's key loads are contiguous 1 KiB runs; an output dimension's
+// chain reads one contiguous V row.
 //
 // Scores, exponentials and products are computed in parallel over positions;
 // the two serial chains (the softmax sum, and each output dimension's
@@ -25,61 +26,36 @@
 #include "common.h"
 #include "device_util.h"
 
+#include <cstddef>
+
 namespace gaje {
+
+static_assert(offsetof(DevState, pos) == 0 && offsetof(DevState, halted) == 12,
+              "the attention kernel reads pos and halted with one 16-byte load");
 
 namespace {
 
 constexpr int THREADS = 256;
 
-// dot_product(a, b) of dot.rs:43-67 for one thread: chains l = 0..7 over the
-// 8-float chunks, ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7)), then the scalar tail.
-__device__ __forceinline__ float dot_ref(const float *a, const float *b, int n) {
+// dot_product(a, b) of dot.rs:43-67 for one thread, b read with a stride:
+// chains l = 0..7 over the 8-float chunks, ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7)),
+// then the scalar tail.
+__device__ __forceinline__ float dot_ref(const float *a, const float *b, int64_t bstride, int n) {
     float acc[8];
 #pragma unroll
     for (int l = 0; l < 8; ++l) acc[l] = 0.0f;
     const int chunks = n / 8;
     for (int i = 0; i < chunks; ++i) {
-        const float4 a0 = *(const float4 *)(a + 8 * i), a1 = *(const float4 *)(a + 8 * i + 4);
-        const float4 b0 = *(const float4 *)(b + 8 * i), b1 = *(const float4 *)(b + 8 * i + 4);
-        acc[0] = fmaf(a0.x, b0.x, acc[0]);
-        acc[1] = fmaf(a0.y, b0.y, acc[1]);
-        acc[2] = fmaf(a0.z, b0.z, acc[2]);
-        acc[3] = fmaf(a0.w, b0.w, acc[3]);
-        acc[4] = fmaf(a1.x, b1.x, acc[4]);
-        acc[5] = fmaf(a1.y, b1.y, acc[5]);
-        acc[6] = fmaf(a1.z, b1.z, acc[6]);
-        acc[7] = fmaf(a1.w, b1.w, acc[7]);
+#pragma unroll
+        for (int l = 0; l < 8; ++l) acc[l] = fmaf(a[8 * i + l], b[(8 * i + l) * bstride], acc[l]);
     }
     const float u0 = acc[0] + acc[4], u1 = acc[1] + acc[5], u2 = acc[2] + acc[6], u3 = acc[3] + acc[7];
     float sum = (u0 + u1) + (u2 + u3);
     for (int i = chunks * 8; i < n; ++i) {
-        const float prod = a[i] * b[i];
+        const float prod = a[i] * b[i * bstride];
         sum = sum + prod;
     }
     return sum;
-}
-
-// The same dot product with the key row already in registers (HD % 8 == 0).
-template <int HD>
-__device__ __forceinline__ float dot_regs(const float *q, const float4 (&k)[HD / 4]) {
-    float acc[8];
-#pragma unroll
-    for (int l = 0; l < 8; ++l) acc[l] = 0.0f;
-#pragma unroll
-    for (int c = 0; c < HD / 8; ++c) {
-        const float4 a0 = *(const float4 *)(q + 8 * c), a1 = *(const float4 *)(q + 8 * c + 4);
-        const float4 b0 = k[2 * c], b1 = k[2 * c + 1];
-        acc[0] = fmaf(a0.x, b0.x, acc[0]);
-        acc[1] = fmaf(a0.y, b0.y, acc[1]);
-        acc[2] = fmaf(a0.z, b0.z, acc[2]);
-        acc[3] = fmaf(a0.w, b0.w, acc[3]);
-        acc[4] = fmaf(a1.x, b1.x, acc[4]);
-        acc[5] = fmaf(a1.y, b1.y, acc[5]);
-        acc[6] = fmaf(a1.z, b1.z, acc[6]);
-        acc[7] = fmaf(a1.w, b1.w, acc[7]);
-    }
-    const float u0 = acc[0] + acc[4], u1 = acc[1] + acc[5], u2 = acc[2] + acc[6], u3 = acc[3] + acc[7];
-    return (u0 + u1) + (u2 + u3);
 }
 
 // Largest score over the block (every thread passes its own running max).
@@ -94,41 +70,10 @@ __device__ __forceinline__ float block_max(float mx, float *red) {
 }
 
 // e[0] + e[1] + ... + e[n-1] in order, one chain (called by one thread): the
-// softmax denominator and every output dimension's accumulation.  LDS reads
-// run one 32-float batch ahead of the adds.
-__device__ __forceinline__ void add8(float &sum, const float4 (&v)[8]) {
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-        sum = sum + v[u].x;
-        sum = sum + v[u].y;
-        sum = sum + v[u].z;
-        sum = sum + v[u].w;
-    }
-}
-__device__ __forceinline__ void read8(float4 (&v)[8], const float *e) {
-#pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = *(const float4 *)(e + 4 * u);
-}
-
+// softmax denominator and every output dimension's accumulation.
 __device__ __forceinline__ float serial_sum(const float *e, int n) {
     float sum = 0.0f;
     int t = 0;
-    if (n >= 32) {
-        float4 a[8], b[8];
-        read8(a, e);
-        while (true) {
-            const bool more_b = t + 64 <= n;
-            if (more_b) read8(b, e + t + 32);
-            add8(sum, a);
-            t += 32;
-            if (!more_b) break;
-            const bool more_a = t + 64 <= n;
-            if (more_a) read8(a, e + t + 32);
-            add8(sum, b);
-            t += 32;
-            if (!more_a) break;
-        }
-    }
     for (; t + 4 <= n; t += 4) {
         const float4 v = *(const float4 *)(e + t);
         sum = sum + v.x;
@@ -140,13 +85,48 @@ __device__ __forceinline__ float serial_sum(const float *e, int n) {
     return sum;
 }
 
+// The same chain over n values, n % 128 == 0, where the values past the
+// caller's count are +0.  The chain starts at +0 and a rounded sum is -0 only
+// when both addends are, so it is never -0 and adding +0 leaves it unchanged:
+// the padded chain equals the unpadded one.  Branch-free, with the LDS reads
+// issued 64 values ahead; it reads 64 floats past e[n - 1] (never used).
+__device__ __forceinline__ void add64(float &sum, const float4 (&v)[16]) {
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+        sum = sum + v[u].x;
+        sum = sum + v[u].y;
+        sum = sum + v[u].z;
+        sum = sum + v[u].w;
+    }
+}
+__device__ __forceinline__ void read64(float4 (&v)[16], const float *e) {
+#pragma unroll
+    for (int u = 0; u < 16; ++u) v[u] = *(const float4 *)(e + 4 * u);
+}
+__device__ __forceinline__ float serial_sum_padded(const float *e, int n) {
+    float sum = 0.0f;
+    float4 a[16], b[16];
+    read64(a, e);
+    for (int t = 0; t < n; t += 128) {
+        read64(b, e + t + 64);
+        add64(sum, a);
+        read64(a, e + t + 128);
+        add64(sum, b);
+    }
+    return sum;
+}
+
+// Padded chain length for ctx positions, and the LDS row length that holds it
+// plus the chain's read-ahead.
+__host__ __device__ constexpr int chain_len(int64_t ctx) { return (int)((ctx + 127) / 128 * 128); }
+__host__ __device__ constexpr int chain_row(int64_t cap) { return chain_len(cap) + 64; }
+
 // Streaming kernel: head dimension HD known at compile time (64 or 128),
 // capacity % 4 == 0.  Workgroup (h, slice) owns output dimensions
 // [slice*ds, slice*ds + ds) of query head h: it computes all of the head's
-// scores (parallel, one round of key loads per thread for contexts up to
-// PPR * 256), and copies only its ds rows of V into LDS with LDS-direct loads
-// issued first, so they land while the scores are computed and both serial
-// chains read LDS only.
+// scores (one quad of positions per thread and round), and copies only its ds
+// rows of V into LDS with LDS-direct loads issued first, so they land while the
+// scores are computed and both serial chains read LDS only.
 typedef __attribute__((address_space(3))) void lds_void;
 
 template <int HD>
@@ -154,90 +134,136 @@ __global__ __launch_bounds__(THREADS) void attn_decode_fast(AttnParams p, int ds
     extern __shared__ __align__(16) float smem[];
     __shared__ float red[THREADS / WAVE];
     __shared__ float inv_slot;
-    DevState *st = p.st;
-    if (st && st->halted) return;  // before any LDS-direct copy is in flight
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int h = blockIdx.x;
-    const int d0 = blockIdx.y * ds;
-    const int g = h / (p.n_head / p.n_head_kv);
-    const int ctx = st ? st->pos + 1 : (int)p.ctx;
-    const float scale = 1.0f / sqrtf((float)HD);
-    const int vstride = (int)p.kv_cap + 4;  // LDS row stride of the V slice (bank spread)
-
-    float *qh = smem;           // HD floats
-    float *sc = smem + HD;      // kv_cap scores, then exponentials
-    float *vs = sc + p.kv_cap;  // ds rows of vstride: V, then the products
-    const float *Kh = p.k_cache + (size_t)g * p.kv_head_stride;
-    const float *Vh = p.v_cache + (size_t)g * p.kv_head_stride + (size_t)d0 * p.kv_cap;
-
-    // ---- V slice -> LDS: one wave instruction copies 256 positions of a row
-    // (lane i its quad i); quads at or past ctx are not copied, and a copied
-    // quad ends before the row's capacity (kv_cap % 4 == 0) ----
-    const int nchunk = (ctx + 255) >> 8;
-    for (int c = wave; c < ds * nchunk; c += THREADS / WAVE) {
-        const int j = c / nchunk, ch = c - j * nchunk;
-        const int t = ch * 256 + lane * 4;
-        if (t < ctx)
-            __builtin_amdgcn_global_load_lds((const void *)(Vh + (size_t)j * p.kv_cap + t),
-                                             (lds_void *)(vs + j * vstride + ch * 256), 16, 0, 0);
+    int ctx = (int)p.ctx;
+    if (p.st) {
+        typedef int vi4 __attribute__((ext_vector_type(4)));
+        const vi4 s4 = *(const volatile vi4 *)p.st;  // pos, token, step, halted: one load
+        if (s4.w) return;                            // before any LDS-direct copy is in flight
+        ctx = s4.x + 1;
     }
 
-    if (tid < HD) qh[tid] = p.q[(size_t)h * HD + tid];
-    __syncthreads();
+    const int d0 = blockIdx.y * ds;
+    const int g = h / (p.n_head / p.n_head_kv);
+    const float scale = 1.0f / sqrtf((float)HD);
+    const int64_t cap = p.kv_cap;
+    const int n = chain_len(ctx);
+    const int vstride = chain_row(cap) + 4;  // LDS row stride of the V slice (bank spread)
 
-    // ---- scores: PPR positions per thread per round, key rows loaded first ----
-    constexpr int PPR = HD <= 64 ? 3 : 1;
+    float *sc = smem;                   // chain_row(cap) scores, then exponentials
+    float *vs = sc + chain_row(cap);    // ds rows of vstride: V, then the products
+    const float *qg = p.q + (size_t)h * HD;
+    const float *Kh = p.k_cache + (size_t)g * p.kv_head_stride;
+    const float *Vh = p.v_cache + (size_t)g * p.kv_head_stride + (size_t)d0 * cap;
+
+    // ---- scores: thread j takes positions 4j..4j+3 of each round; key
+    // dimension d of those positions is one quad of row d (a 32-bit byte
+    // offset walks the rows).  RING 8-dimension chunks of the quads are in
+    // flight ahead of the FMAs.  A quad that runs past ctx stays inside the row
+    // (kv_cap % 4 == 0); its extra lanes are dropped.  q is read with uniform
+    // loads ----
+    constexpr int NCH = HD / 8, RING = 4;
+    const char *kb = (const char *)Kh;
+    const uint32_t rowb = (uint32_t)cap * 4;
     float mx = -INFINITY;
-    for (int t0 = tid; t0 < ctx; t0 += PPR * THREADS) {
-        float4 k[PPR][HD / 4];
+    for (int t4 = 4 * tid; t4 < ctx; t4 += 4 * THREADS) {
+        uint32_t off = (uint32_t)t4 * 4;
+        float4 kr[RING][8];
 #pragma unroll
-        for (int j = 0; j < PPR; ++j) {
-            const int t = t0 + j * THREADS < ctx ? t0 + j * THREADS : t0;
-            const float4 *kr = (const float4 *)(Kh + (size_t)t * HD);
+        for (int c = 0; c < RING; ++c)
 #pragma unroll
-            for (int u = 0; u < HD / 4; ++u) k[j][u] = kr[u];
+            for (int l = 0; l < 8; ++l) {
+                kr[c][l] = *(const float4 *)(kb + off);
+                off += rowb;
+            }
+        float acc[4][8];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int l = 0; l < 8; ++l) acc[u][l] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            const float4 qa = *(const float4 *)(qg + 8 * c), qb = *(const float4 *)(qg + 8 * c + 4);
+            const float qc[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+            for (int l = 0; l < 8; ++l) {
+                const float4 k = kr[c % RING][l];
+                acc[0][l] = fmaf(qc[l], k.x, acc[0][l]);
+                acc[1][l] = fmaf(qc[l], k.y, acc[1][l]);
+                acc[2][l] = fmaf(qc[l], k.z, acc[2][l]);
+                acc[3][l] = fmaf(qc[l], k.w, acc[3][l]);
+            }
+            if (c + RING < NCH) {
+#pragma unroll
+                for (int l = 0; l < 8; ++l) {
+                    kr[c % RING][l] = *(const float4 *)(kb + off);
+                    off += rowb;
+                }
+            }
         }
 #pragma unroll
-        for (int j = 0; j < PPR; ++j) {
-            const int t = t0 + j * THREADS;
-            if (t < ctx) {
-                const float s = dot_regs<HD>(qh, k[j]) * scale;
-                sc[t] = s;
+        for (int u = 0; u < 4; ++u) {
+            const float u0 = acc[u][0] + acc[u][4], u1 = acc[u][1] + acc[u][5];
+            const float u2 = acc[u][2] + acc[u][6], u3 = acc[u][3] + acc[u][7];
+            const float s = ((u0 + u1) + (u2 + u3)) * scale;
+            if (t4 + u < ctx) {
+                sc[t4 + u] = s;
                 mx = fmaxf(mx, s);  // NaN never wins, as with the reference's '>'
             }
         }
     }
+    // ---- V slice -> LDS, issued by the last wave once its scores are done
+    // (the first 768 positions leave it none), so the other waves' key loads
+    // never wait behind the copies (loads complete in order).  One wave
+    // instruction copies 256 positions of a row (lane i its quad i); quads at or
+    // past ctx are not copied, and a copied quad ends before the row's capacity
+    // (kv_cap % 4 == 0) ----
+    if (wave == THREADS / WAVE - 1) {
+        const int nchunk = (ctx + 255) >> 8;
+        for (int j = 0; j < ds; ++j)
+            for (int ch = 0; ch < nchunk; ++ch) {
+                const int t = ch * 256 + lane * 4;
+                if (t < ctx)
+                    __builtin_amdgcn_global_load_lds((const void *)(Vh + (size_t)j * cap + t),
+                                                     (lds_void *)(vs + j * vstride + ch * 256), 16, 0, 0);
+            }
+    }
     __builtin_amdgcn_s_waitcnt(0);  // this thread's LDS-direct copies have landed
     const float max_s = block_max(mx, red);  // (its barrier publishes them to the block)
 
-    for (int t = tid; t < ctx; t += THREADS) sc[t] = expf_ref(sc[t] - max_s);
+    // exponentials, +0 up to the padded chain length
+    for (int t = tid; t < n; t += THREADS) sc[t] = t < ctx ? expf_ref(sc[t] - max_s) : 0.0f;
     __syncthreads();
-    if (tid == 0) inv_slot = 1.0f / (serial_sum(sc, ctx) + 1e-12f);
+    if (tid == 0) inv_slot = 1.0f / (serial_sum_padded(sc, n) + 1e-12f);
     __syncthreads();
     const float inv = inv_slot;
 
-    // products w_t * v_t[i] in place, w_t = e_t * inv rounded first
-    for (int t = tid; t < ctx; t += THREADS) {
-        const float w = sc[t] * inv;
+    // products w_t * v_t[i] in place, w_t = e_t * inv rounded first; +0 past ctx
+    for (int t = 4 * tid; t < n; t += 4 * THREADS) {
+        const float4 e = *(const float4 *)(sc + t);
+        const float w[4] = {e.x * inv, e.y * inv, e.z * inv, e.w * inv};
         for (int j = 0; j < ds; ++j) {
-            float &v = vs[j * vstride + t];
-            v = w * v;
+            float4 &v4 = *(float4 *)(vs + j * vstride + t);
+            const float4 v = v4;
+            v4 = make_float4(t < ctx ? w[0] * v.x : 0.0f, t + 1 < ctx ? w[1] * v.y : 0.0f,
+                             t + 2 < ctx ? w[2] * v.z : 0.0f, t + 3 < ctx ? w[3] * v.w : 0.0f);
         }
     }
     __syncthreads();
 
     // ---- out_i = sum_t products, one chain per output dimension ----
-    if (tid < ds) p.out[(size_t)h * HD + d0 + tid] = serial_sum(vs + tid * vstride, ctx);
+    if (tid < ds) p.out[(size_t)h * HD + d0 + tid] = serial_sum_padded(vs + tid * vstride, n);
 }
 
 // Output dimensions per workgroup of the streaming kernel for this capacity,
 // or 0 if even one V row does not fit.
+size_t fast_lds_bytes(int64_t cap, int ds) { return (size_t)(chain_row(cap) + (size_t)ds * (chain_row(cap) + 4)) * 4; }
 int fast_slice(int head_dim, int64_t cap) {
-    for (int ds = 16; ds >= 1; ds >>= 1) {
+    for (int ds = 8; ds >= 1; ds >>= 1) {
         if (head_dim % ds) continue;
-        const size_t lds = (size_t)(head_dim + cap + (size_t)ds * (cap + 4)) * 4;
-        if (lds + 1024 <= max_lds_per_block()) return ds;
+        if (fast_lds_bytes(cap, ds) + 1024 <= max_lds_per_block()) return ds;
     }
     return 0;
 }
@@ -267,7 +293,7 @@ __global__ __launch_bounds__(THREADS) void attn_decode_generic(AttnParams p) {
 
     float mx = -INFINITY;
     for (int t = tid; t < ctx; t += THREADS) {
-        const float d = dot_ref(qh, Kh + (size_t)t * hd, hd);
+        const float d = dot_ref(qh, Kh + t, p.kv_cap, hd);
         const float s = d * scale;
         sc[t] = s;
         mx = fmaxf(mx, s);
@@ -319,7 +345,7 @@ int launch_attention(const AttnParams &p, hipStream_t s) {
                          (long long)p.kv_cap);
     const int ds = (p.kv_cap % 4 == 0 && (p.head_dim == 64 || p.head_dim == 128)) ? fast_slice(p.head_dim, p.kv_cap) : 0;
     if (ds > 0) {
-        const size_t flds = (size_t)(p.head_dim + p.kv_cap + (size_t)ds * (p.kv_cap + 4)) * 4;
+        const size_t flds = fast_lds_bytes(p.kv_cap, ds);
         auto fn = p.head_dim == 64 ? attn_decode_fast<64> : attn_decode_fast<128>;
         hipLaunchKernelGGL(fn, dim3(p.n_head, p.head_dim / ds), dim3(THREADS), flds, s, p, ds);
     } else {

@@ -123,35 +123,6 @@ __device__ __forceinline__ float q4_group(float acc, const vu2 n, const vu4 s, c
     return q4_group(acc, n, s, read_x4(xg));
 }
 
-// The row's last groups from ring slots 0..T-1, branch-free: `left` blocks
-// remain, and a block's four chain steps are kept only if it exists (the
-// condition is uniform, so the select costs one instruction per block).  Slots
-// past the row hold finite bytes of the following rows or of the tensor's
-// padding; their results are discarded.
-template <int T, int D>
-__device__ __forceinline__ float q4_tail_pass(float acc, const vu2 (&n)[D], const vu4 (&s)[D], const float *xg,
-                                              int left) {
-#pragma unroll
-    for (int i = 0; i < T; ++i) {
-        const X4 x = read_x4(xg + 16 * i);
-        float d0[4], d1[4], d2[4], d3[4];
-        q4_dequant(d0, opaque_and(n[i].x, 0x0F0F0F0Fu), s[i].x);
-        q4_dequant(d1, opaque_and(n[i].x >> 4, 0x0F0F0F0Fu), s[i].y);
-        q4_dequant(d2, opaque_and(n[i].y, 0x0F0F0F0Fu), s[i].z);
-        q4_dequant(d3, opaque_and(n[i].y >> 4, 0x0F0F0F0Fu), s[i].w);
-        const int b = left - 4 * i;  // blocks of this group that exist (<= 0: none)
-        float t = q4_chain(acc, d0, x.b0);
-        acc = b > 0 ? t : acc;
-        t = q4_chain(acc, d1, x.b1);
-        acc = b > 1 ? t : acc;
-        t = q4_chain(acc, d2, x.b2);
-        acc = b > 2 ? t : acc;
-        t = q4_chain(acc, d3, x.b3);
-        acc = b > 3 ? t : acc;
-    }
-    return acc;
-}
-
 // Register ring of D packed groups of one row (this lane's chain bytes and
 // the group's scale/min words).
 template <int D>
@@ -160,9 +131,29 @@ struct Q4Ring {
     vu4 s[D];
 };
 
+// The row's last groups from ring slots 0..T-1, branch-free: `left` blocks
+// remain.  A slot past the row holds finite or non-finite bytes of the
+// following rows or of the tensor's padding, so the scale/min word of every
+// block that does not exist is replaced by zero (its four values dequantise to
+// +0), and the chain-major activation rows are zero past their last block
+// (q4_zero_x_pad).  The step fma(+0, +0, acc) returns acc unchanged (acc starts
+// at +0 and is never -0), so the chain's rounding sequence is the row's own and
+// the selects stay off the dependent chain.  xc holds slot 0's inputs.
 template <int T, int D>
-__device__ __forceinline__ float q4_tail(float acc, const Q4Ring<D> &r, const float *xg, int left) {
-    return q4_tail_pass<T, D>(acc, r.n, r.s, xg, left);
+__device__ __forceinline__ float q4_tail(float acc, const Q4Ring<D> &r, const float *xg, X4 xc, int left) {
+#pragma unroll
+    for (int i = 0; i < T; ++i) {
+        const X4 xn = read_x4(xg + 16 * (i + 1));
+        const int b = left - 4 * i;  // blocks of this group that exist (<= 0: none)
+        vu4 s = r.s[i];
+        s.x = b > 0 ? s.x : 0u;
+        s.y = b > 1 ? s.y : 0u;
+        s.z = b > 2 ? s.z : 0u;
+        s.w = b > 3 ? s.w : 0u;
+        acc = q4_group(acc, r.n[i], s, xc);
+        xc = xn;
+    }
+    return acc;
 }
 
 // Issues the loads of the row's first D groups.  A row shorter than D groups
@@ -181,8 +172,9 @@ __device__ __forceinline__ void q4_prefetch(const GemvParams &p, int64_t row, in
 
 // Walks the row's groups in order (chain l of the row); each ring slot is
 // refilled D groups ahead right after it is consumed (past the row's end the
-// refills read the next row or the padding and are not used).  Returns the
-// flushed dot product in lane `base`.
+// refills read the next row or the padding and are not used).  The LDS reads
+// of a group's inputs are issued one group ahead of its arithmetic.  Returns
+// the flushed dot product in lane `base`.
 template <bool NT, int D>
 __device__ __forceinline__ float q4_consume(const GemvParams &p, const XView &xv, int64_t row, int l, int base,
                                             Q4Ring<D> &r) {
@@ -192,26 +184,49 @@ __device__ __forceinline__ float q4_consume(const GemvParams &p, const XView &xv
     const uint8_t *gp = p.w + (size_t)row * G * 80 + D * 80 + 8 * l;  // next group to load (chain bytes)
     const float *xg = xv.x + l * xv.stride;
     float acc = 0.0f;
+    X4 xc = read_x4(xg);
     int g = 0;
     for (; g + D <= Gf; g += D) {
 #pragma unroll
         for (int i = 0; i < D; ++i) {
-            acc = q4_group(acc, r.n[i], r.s[i], xg + 16 * i);
+            const X4 xn = read_x4(xg + 16 * (i + 1));
+            acc = q4_group(acc, r.n[i], r.s[i], xc);
             r.n[i] = ld_u2<NT>(gp + i * 80);
             r.s[i] = ld_u4<NT>(gp + i * 80 + 64 - 8 * l);
+            xc = xn;
         }
         gp += D * 80;
         xg += 16 * D;
     }
     // the last <= D groups are already in the ring, in order: one branch-free
-    // pass over T slots (T = D or D/2)
-    if (G - g > D / 2) acc = q4_tail<D>(acc, r, xg, nb - 4 * g);
-    else if (G > g) acc = q4_tail<D / 2>(acc, r, xg, nb - 4 * g);
+    // pass over T slots (T = D - 1, D or D/2)
+    const int rem = G - g;
+    if (rem == D - 1) acc = q4_tail<D - 1, D>(acc, r, xg, xc, nb - 4 * g);
+    else if (rem > D / 2) acc = q4_tail<D, D>(acc, r, xg, xc, nb - 4 * g);
+    else if (rem > 0) acc = q4_tail<D / 2, D>(acc, r, xg, xc, nb - 4 * g);
     // lanes base..base+7 hold chains 0..7
     const float u = acc + shfl(acc, base + ((l + 4) & 7));  // lane l<4: a_l + a_{l+4}
     const float v = u + shfl(u, base + ((l + 2) & 7));      // lane 0: u0+u2, lane 1: u1+u3
     const float total = v + shfl(v, base + ((l + 1) & 7));  // lane 0: (u0+u2) + (u1+u3)
     return flush_small(total);
+}
+
+// Ring depth of the Q4_0 row walk for rows of nb blocks: a short row's groups
+// are all in flight at once; long rows keep 16 groups (64 blocks) ahead.
+__host__ __device__ constexpr int q4_depth(int nb) { return (nb + 3) / 4 > Q4_PREFETCH ? 2 * Q4_PREFETCH : Q4_PREFETCH; }
+
+// Floats of a chain-major activation row that the row walk may read: every
+// group's 16 inputs, plus the slots a tail pass reads past the last group.
+__host__ __device__ constexpr int q4_xrow(int nb) { return 16 * ((nb + 3) / 4 + q4_depth(nb) / 2); }
+
+// Zeroes chain-major positions [4 nb, q4_xrow(nb)) of the eight activation rows
+// (inputs of blocks that do not exist, read by the tail pass).
+__device__ __forceinline__ void q4_zero_x_pad(const XView &xv, int nb) {
+    const int from = 4 * nb, per_row = (q4_xrow(nb) - from) >> 2;  // float4s per row (from % 4 == 0)
+    for (int t = threadIdx.x; t < 8 * per_row; t += blockDim.x) {
+        const int l = t / per_row, c = t - l * per_row;
+        *(float4 *)(xv.x + l * xv.stride + from + 4 * c) = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
 }
 
 // Packs Q4_0Block rows (file layout) into the layout above; one thread per
@@ -503,6 +518,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
                 }
             }
         }
+        if constexpr (FMT == FMT_Q4_0) q4_zero_x_pad(xv, p.nb);
         if (__syncthreads_or(bad_in) && p.st_in >= 0 && tid == 0) nan_flag(st, p.layer, p.st_in);
         if (p.norm_w) {
             if constexpr (FMT == FMT_Q4_0) rms_inv_chain_major(xv, K, p.eps, &inv_slot);
@@ -641,12 +657,12 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
                     p.q_out[r0] = o0;
                     p.q_out[r1] = o1;
                 } else if (r0 < p.q_rows + p.kv_rows) {
-                    // K cache: [kv head][position][dim]
+                    // K cache: [kv head][dim][position]
                     const int64_t kh = (r0 - p.q_rows) / p.head_dim;
                     const int64_t b = p.q_rows + kh * p.head_dim;
-                    float *kc = p.k_cache + kh * p.kv_head_stride + (size_t)pos * p.head_dim;
-                    kc[r0 - b] = o0;
-                    kc[r1 - b] = o1;
+                    float *kc = p.k_cache + kh * p.kv_head_stride + pos;
+                    kc[(r0 - b) * p.kv_cap] = o0;
+                    kc[(r1 - b) * p.kv_cap] = o1;
                 } else {
                     // V cache: [kv head][dim][position]
                     const int64_t vh = (r0 - p.q_rows - p.kv_rows) / p.head_dim;
@@ -691,13 +707,10 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
 
 using KernelFn = void (*)(GemvParams, int64_t, int, int);
 
-// LDS row stride (floats) of the chain-major activation copy: room for every
-// packed group's 16 inputs, padded so that stride / 4 is odd (the eight chain
+// LDS row stride (floats) of the chain-major activation copy: the floats the
+// row walk reads (q4_xrow), padded so that stride / 4 is odd (the eight chain
 // rows' 16-byte reads then fall in distinct banks).
-int q4_xstride(int64_t K) {
-    const int64_t G = (K / 32 + 3) / 4;
-    return (int)(16 * G + 4);
-}
+int q4_xstride(int64_t K) { return q4_xrow((int)(K / 32)) + 4; }
 
 }  // namespace
 
@@ -726,9 +739,9 @@ static int64_t gemv_x_floats(int64_t K, int fmt) {
 }
 
 size_t gemv_lds_bytes(int64_t K, int fmt, bool norm) {
-    // Q4_0: + one ring's worth of groups (16 x 16 floats) that the branch-free
-    // tail may read past the last chain row
-    const int64_t slack = fmt == FMT_Q4_0 ? 16 * 2 * Q4_PREFETCH : 0;
+    // Q4_0: + the one group of inputs that the row walk reads ahead past the
+    // last chain row (never used)
+    const int64_t slack = fmt == FMT_Q4_0 ? 16 : 0;
     return (size_t)(gemv_x_floats(K, fmt) + (norm ? ((K + 3) & ~(int64_t)3) : 0) + slack) * 4;
 }
 
@@ -778,9 +791,7 @@ int launch_gemv(const GemvParams &p, hipStream_t s) {
     KernelFn fn;
     int lpr;
     if (p.fmt == FMT_Q4_0) {
-        // ring depth: a short row's groups are all in flight at once; long rows
-        // keep 16 groups (64 blocks) ahead of the arithmetic
-        const bool long_rows = (p.nb + 3) / 4 > Q4_PREFETCH;
+        const bool long_rows = q4_depth(p.nb) == 2 * Q4_PREFETCH;
         lpr = 8;
         if (long_rows)
             fn = p.nontemporal ? gemv_kernel<FMT_Q4_0, 8, true, 2 * Q4_PREFETCH>

@@ -79,7 +79,7 @@ struct GemvParams {
     int64_t q_rows, kv_rows;
     const float *rope_cos, *rope_sin;  // [max_ctx][head_dim/2]
     float *q_out;
-    float *k_cache;                    // this layer: [n_kv][kv_cap][head_dim]
+    float *k_cache;                    // this layer: [n_kv][head_dim][kv_cap]
     float *v_cache;                    // this layer: [n_kv][head_dim][kv_cap]
     int64_t kv_head_stride;            // kv_cap * head_dim
     int64_t kv_cap;                    // positions per cache row
@@ -106,7 +106,7 @@ size_t gemv_lds_bytes(int64_t K, int fmt, bool norm);
 
 struct AttnParams {
     const float *q;          // roped queries [n_head * head_dim]
-    const float *k_cache;    // this layer: [n_kv][kv_cap][head_dim]
+    const float *k_cache;    // this layer: [n_kv][head_dim][kv_cap]
     const float *v_cache;    // this layer: [n_kv][head_dim][kv_cap]
     int64_t kv_head_stride;  // kv_cap * head_dim
     int32_t n_head, n_head_kv, head_dim;

@@ -424,10 +424,9 @@ int reserve_ctx(gaje_hip_model *m, int64_t positions) {
         for (int64_t l = 0; l < m->n_layers; ++l)
             for (int64_t g = 0; g < m->n_kv; ++g) {
                 const size_t src = ((size_t)l * m->n_kv + g) * per_head_old, dst = ((size_t)l * m->n_kv + g) * per_head_new;
-                // K rows are [position][dim]: one contiguous prefix;
-                // V rows are [dim][position]: a prefix of every dimension's row
-                const size_t bytes = (size_t)m->pos * m->hd * 4;
-                GAJE_HIP_CHECK(hipMemcpyAsync(kc + dst, m->k_cache + src, bytes, hipMemcpyDeviceToDevice, m->stream));
+                // K and V rows are [dim][position]: a prefix of every dimension's row
+                GAJE_HIP_CHECK(hipMemcpy2DAsync(kc + dst, (size_t)cap * 4, m->k_cache + src, (size_t)m->cap * 4,
+                                                (size_t)m->pos * 4, (size_t)m->hd, hipMemcpyDeviceToDevice, m->stream));
                 GAJE_HIP_CHECK(hipMemcpy2DAsync(vc + dst, (size_t)cap * 4, m->v_cache + src, (size_t)m->cap * 4,
                                                 (size_t)m->pos * 4, (size_t)m->hd, hipMemcpyDeviceToDevice, m->stream));
             }

@@ -140,7 +140,7 @@ def expf(x: DeviceBuffer, y: DeviceBuffer, n: int, stream=None):
 def attention(q: DeviceBuffer, k_cache: DeviceBuffer, v_cache: DeviceBuffer, seq_len: int,
               capacity: int, n_head: int, n_head_kv: int, head_dim: int, out: DeviceBuffer,
               stream=None):
-    """k_cache is [n_head_kv][capacity][head_dim], v_cache [n_head_kv][head_dim][capacity]."""
+    """k_cache and v_cache are both [n_head_kv][head_dim][capacity]."""
     check(lib().gaje_hip_attention(q.ptr, k_cache.ptr, v_cache.ptr, seq_len, capacity, n_head,
                                    n_head_kv, head_dim, out.ptr, stream))
 

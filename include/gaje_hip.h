@@ -130,9 +130,9 @@ int gaje_hip_expf(const float *x, float *y, int64_t n, void *stream);
 
 /* The GQA softmax attention of GenomicAttention::forward_attention_core
  * (nn/attention.rs:87-127) over seq_len cached positions, bit-exact.  q is
- * [n_head][head_dim] (already rotated); k_cache is [n_head_kv][capacity]
- * [head_dim] and v_cache is [n_head_kv][head_dim][capacity] (positions
- * 0..seq_len-1 used); out is [n_head][head_dim]. */
+ * [n_head][head_dim] (already rotated); k_cache and v_cache are both
+ * [n_head_kv][head_dim][capacity] (positions 0..seq_len-1 used); out is
+ * [n_head][head_dim]. */
 int gaje_hip_attention(const float *q, const float *k_cache, const float *v_cache, int64_t seq_len,
                        int64_t capacity, int n_head, int n_head_kv, int head_dim, float *out, void *stream);
 

@@ -75,9 +75,9 @@ def test_elementwise_golden(hip, g):
 def test_attention_golden(hip, g, cap_pad):
     ctx, nh, nkv, hd = (int(v) for v in g["att.shape"])
     cap = (ctx + 3) // 4 * 4 + cap_pad
-    kh = np.zeros((nkv, cap, hd), np.float32)
+    kh = np.zeros((nkv, hd, cap), np.float32)  # K and V: [head][dim][pos]
     vh = np.zeros((nkv, hd, cap), np.float32)
-    kh[:, :ctx] = g["att.k"].reshape(ctx, nkv, hd).transpose(1, 0, 2)
+    kh[:, :, :ctx] = g["att.k"].reshape(ctx, nkv, hd).transpose(1, 2, 0)
     vh[:, :, :ctx] = g["att.v"].reshape(ctx, nkv, hd).transpose(1, 2, 0)
     out = hip.ops.DeviceBuffer(nh * hd * 4)
     hip.ops.attention(dev(hip, g["att.q"]), dev(hip, kh), dev(hip, vh), ctx, cap, nh, nkv, hd, out)

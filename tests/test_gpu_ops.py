@@ -252,9 +252,9 @@ def test_attention_bit_exact(hip, O, ctx, n_head, n_kv, hd, cap):
     k = hip.synth.normal(82, f"ak.{ctx}.{hd}", ctx * n_kv * hd)
     v = hip.synth.normal(83, f"av.{ctx}.{hd}", ctx * n_kv * hd)
     ref = O.attention(q, k, v, ctx, n_head, n_kv, hd)
-    kh = np.zeros((n_kv, cap, hd), np.float32)  # device layouts: K [head][pos][dim],
-    vh = np.zeros((n_kv, hd, cap), np.float32)  # V [head][dim][pos]
-    kh[:, :ctx] = k.reshape(ctx, n_kv, hd).transpose(1, 0, 2)
+    kh = np.zeros((n_kv, hd, cap), np.float32)  # device layout of K and V: [head][dim][pos]
+    vh = np.zeros((n_kv, hd, cap), np.float32)
+    kh[:, :, :ctx] = k.reshape(ctx, n_kv, hd).transpose(1, 2, 0)
     vh[:, :, :ctx] = v.reshape(ctx, n_kv, hd).transpose(1, 2, 0)
     out = _out(hip, n_head * hd * 4)
     hip.ops.attention(_dev(hip, q), _dev(hip, kh), _dev(hip, vh), ctx, cap, n_head, n_kv, hd, out)
