@@ -85,58 +85,34 @@ __device__ __forceinline__ float serial_sum(const float *e, int n) {
     return sum;
 }
 
-// The same chain over n values, n % 128 == 0, where the values past the
-// caller's count are +0.  The chain starts at +0 and a rounded sum is -0 only
-// when both addends are, so it is never -0 and adding +0 leaves it unchanged:
-// the padded chain equals the unpadded one.  Branch-free, with the LDS reads
-// issued 64 values ahead; it reads 64 floats past e[n - 1] (never used).
-__device__ __forceinline__ void add64(float &sum, const float4 (&v)[16]) {
-#pragma unroll
-    for (int u = 0; u < 16; ++u) {
-        sum = sum + v[u].x;
-        sum = sum + v[u].y;
-        sum = sum + v[u].z;
-        sum = sum + v[u].w;
-    }
-}
-__device__ __forceinline__ void read64(float4 (&v)[16], const float *e) {
-#pragma unroll
-    for (int u = 0; u < 16; ++u) v[u] = *(const float4 *)(e + 4 * u);
-}
-__device__ __forceinline__ float serial_sum_padded(const float *e, int n) {
-    float sum = 0.0f;
-    float4 a[16], b[16];
-    read64(a, e);
-    for (int t = 0; t < n; t += 128) {
-        read64(b, e + t + 64);
-        add64(sum, a);
-        read64(a, e + t + 128);
-        add64(sum, b);
-    }
-    return sum;
-}
+// The chains run over chain_len(ctx) values: the values past ctx are +0.  A
+// chain starts at +0 and a rounded sum is -0 only when both addends are, so it
+// is never -0 and adding +0 leaves it unchanged: the padded chain equals the
+// unpadded one.
 
 // Padded chain length for ctx positions, and the LDS row length that holds it
-// plus the chain's read-ahead.
+// plus the chain's read-ahead (chain_lds reads 32 floats past the end).
 __host__ __device__ constexpr int chain_len(int64_t ctx) { return (int)((ctx + 127) / 128 * 128); }
 __host__ __device__ constexpr int chain_row(int64_t cap) { return chain_len(cap) + 64; }
 
 // Streaming kernel: head dimension HD known at compile time (64 or 128),
 // capacity % 4 == 0.  Workgroup (h, slice) owns output dimensions
-// [slice*ds, slice*ds + ds) of query head h: it computes all of the head's
-// scores (one quad of positions per thread and round), and copies only its ds
-// rows of V into LDS with LDS-direct loads issued first, so they land while the
-// scores are computed and both serial chains read LDS only.
+// [slice*DS, slice*DS + DS) of query head h: it computes all of the head's
+// scores (one quad of positions per thread and round), and copies only its DS
+// rows of V into LDS with LDS-direct loads, so they land while the scores are
+// computed and both serial chains read LDS only.
 typedef __attribute__((address_space(3))) void lds_void;
 
-template <int HD>
-__global__ __launch_bounds__(THREADS) void attn_decode_fast(AttnParams p, int ds) {
+template <int HD, int DS>
+__global__ __launch_bounds__(THREADS) void attn_decode_fast(AttnParams p) {
     extern __shared__ __align__(16) float smem[];
     __shared__ float red[THREADS / WAVE];
     __shared__ float inv_slot;
+    __shared__ uint64_t tab[32];  // the exponential's table, read from LDS
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int h = blockIdx.x;
+    const uint64_t tabv = tid < 32 ? kExp2Tab[tid] : 0;
     int ctx = (int)p.ctx;
     if (p.st) {
         typedef int vi4 __attribute__((ext_vector_type(4)));
@@ -145,7 +121,7 @@ __global__ __launch_bounds__(THREADS) void attn_decode_fast(AttnParams p, int ds
         ctx = s4.x + 1;
     }
 
-    const int d0 = blockIdx.y * ds;
+    const int d0 = blockIdx.y * DS;
     const int g = h / (p.n_head / p.n_head_kv);
     const float scale = 1.0f / sqrtf((float)HD);
     const int64_t cap = p.kv_cap;
@@ -153,7 +129,7 @@ __global__ __launch_bounds__(THREADS) void attn_decode_fast(AttnParams p, int ds
     const int vstride = chain_row(cap) + 4;  // LDS row stride of the V slice (bank spread)
 
     float *sc = smem;                   // chain_row(cap) scores, then exponentials
-    float *vs = sc + chain_row(cap);    // ds rows of vstride: V, then the products
+    float *vs = sc + chain_row(cap);    // DS rows of vstride: V, then the products
     const float *qg = p.q + (size_t)h * HD;
     const float *Kh = p.k_cache + (size_t)g * p.kv_head_stride;
     const float *Vh = p.v_cache + (size_t)g * p.kv_head_stride + (size_t)d0 * cap;
@@ -222,7 +198,7 @@ __global__ __launch_bounds__(THREADS) void attn_decode_fast(AttnParams p, int ds
     // (kv_cap % 4 == 0) ----
     if (wave == THREADS / WAVE - 1) {
         const int nchunk = (ctx + 255) >> 8;
-        for (int j = 0; j < ds; ++j)
+        for (int j = 0; j < DS; ++j)
             for (int ch = 0; ch < nchunk; ++ch) {
                 const int t = ch * 256 + lane * 4;
                 if (t < ctx)
@@ -230,13 +206,14 @@ __global__ __launch_bounds__(THREADS) void attn_decode_fast(AttnParams p, int ds
                                                      (lds_void *)(vs + j * vstride + ch * 256), 16, 0, 0);
             }
     }
+    if (tid < 32) tab[tid] = tabv;
     __builtin_amdgcn_s_waitcnt(0);  // this thread's LDS-direct copies have landed
     const float max_s = block_max(mx, red);  // (its barrier publishes them to the block)
 
     // exponentials, +0 up to the padded chain length
-    for (int t = tid; t < n; t += THREADS) sc[t] = t < ctx ? expf_ref(sc[t] - max_s) : 0.0f;
+    for (int t = tid; t < n; t += THREADS) sc[t] = t < ctx ? expf_ref_t(sc[t] - max_s, tab) : 0.0f;
     __syncthreads();
-    if (tid == 0) inv_slot = 1.0f / (serial_sum_padded(sc, n) + 1e-12f);
+    if (tid == 0) inv_slot = 1.0f / (chain_lds(0.0f, sc, n) + 1e-12f);
     __syncthreads();
     const float inv = inv_slot;
 
@@ -244,7 +221,8 @@ __global__ __launch_bounds__(THREADS) void attn_decode_fast(AttnParams p, int ds
     for (int t = 4 * tid; t < n; t += 4 * THREADS) {
         const float4 e = *(const float4 *)(sc + t);
         const float w[4] = {e.x * inv, e.y * inv, e.z * inv, e.w * inv};
-        for (int j = 0; j < ds; ++j) {
+#pragma unroll
+        for (int j = 0; j < DS; ++j) {
             float4 &v4 = *(float4 *)(vs + j * vstride + t);
             const float4 v = v4;
             v4 = make_float4(t < ctx ? w[0] * v.x : 0.0f, t + 1 < ctx ? w[1] * v.y : 0.0f,
@@ -254,7 +232,7 @@ __global__ __launch_bounds__(THREADS) void attn_decode_fast(AttnParams p, int ds
     __syncthreads();
 
     // ---- out_i = sum_t products, one chain per output dimension ----
-    if (tid < ds) p.out[(size_t)h * HD + d0 + tid] = serial_sum_padded(vs + tid * vstride, n);
+    if (tid < DS) p.out[(size_t)h * HD + d0 + tid] = chain_lds(0.0f, vs + tid * vstride, n);
 }
 
 // Output dimensions per workgroup of the streaming kernel for this capacity,
@@ -346,8 +324,12 @@ int launch_attention(const AttnParams &p, hipStream_t s) {
     const int ds = (p.kv_cap % 4 == 0 && (p.head_dim == 64 || p.head_dim == 128)) ? fast_slice(p.head_dim, p.kv_cap) : 0;
     if (ds > 0) {
         const size_t flds = fast_lds_bytes(p.kv_cap, ds);
-        auto fn = p.head_dim == 64 ? attn_decode_fast<64> : attn_decode_fast<128>;
-        hipLaunchKernelGGL(fn, dim3(p.n_head, p.head_dim / ds), dim3(THREADS), flds, s, p, ds);
+        void (*fn)(AttnParams);
+        if (p.head_dim == 64)
+            fn = ds == 8 ? attn_decode_fast<64, 8> : ds == 4 ? attn_decode_fast<64, 4> : ds == 2 ? attn_decode_fast<64, 2> : attn_decode_fast<64, 1>;
+        else
+            fn = ds == 8 ? attn_decode_fast<128, 8> : ds == 4 ? attn_decode_fast<128, 4> : ds == 2 ? attn_decode_fast<128, 2> : attn_decode_fast<128, 1>;
+        hipLaunchKernelGGL(fn, dim3(p.n_head, p.head_dim / ds), dim3(THREADS), flds, s, p);
     } else {
         hipLaunchKernelGGL(attn_decode_generic, dim3(p.n_head), dim3(THREADS), lds, s, p);
     }

@@ -100,22 +100,138 @@ __device__ __forceinline__ void nan_flag(DevState *st, int layer, int stage) {
 }
 
 // swiglu_balanced for one element (activation.rs:40-49), with the reference's
-// exponential (expf_ref) and every operation rounded as written there.
-__device__ __forceinline__ float swiglu1(float g, float u) {
+// exponential (expf_ref; tab is its table, kExp2Tab or an LDS copy) and every
+// operation rounded as written there.
+__device__ __forceinline__ float swiglu1(float g, float u, const uint64_t *tab = kExp2Tab) {
     float gs = g;
     if (gs < -64.0f) gs = -64.0f;
     if (gs > 64.0f) gs = 64.0f;
     float sig;
     if (gs >= 0.0f) {
-        const float den = 1.0f + expf_ref(-gs);
+        const float den = 1.0f + expf_ref_t(-gs, tab);
         sig = 1.0f / den;
     } else {
-        const float ex = expf_ref(gs);
+        const float ex = expf_ref_t(gs, tab);
         const float den = 1.0f + ex;
         sig = ex / den;
     }
     const float silu = g * sig;
     return silu * u;
+}
+
+// sum + e[0] + e[1] + ... + e[n - 1] in order in this lane (the reference's
+// serial accumulation loops), n % 64 == 0 and n >= 64; e is an LDS array that
+// is read 32 floats past its end (the values are not used).  The loop is
+// written out because the compiler's schedule waits for every LDS read before
+// each block of adds: here the reads run one block of 32 values ahead, with one
+// wait per block, and v100..v163 hold the two blocks.  Uniform n.
+__device__ __forceinline__ float chain_lds(float sum, const float *e, int n) {
+    uint32_t p = (uint32_t)(uintptr_t)e;
+    int c = __builtin_amdgcn_readfirstlane(n >> 6);  // uniform: lives in an SGPR
+    asm volatile(
+        "ds_read_b128 v[100:103], %[p] offset:0\n"
+        "ds_read_b128 v[104:107], %[p] offset:16\n"
+        "ds_read_b128 v[108:111], %[p] offset:32\n"
+        "ds_read_b128 v[112:115], %[p] offset:48\n"
+        "ds_read_b128 v[116:119], %[p] offset:64\n"
+        "ds_read_b128 v[120:123], %[p] offset:80\n"
+        "ds_read_b128 v[124:127], %[p] offset:96\n"
+        "ds_read_b128 v[128:131], %[p] offset:112\n"
+        "1:\n"
+        "ds_read_b128 v[132:135], %[p] offset:128\n"
+        "ds_read_b128 v[136:139], %[p] offset:144\n"
+        "ds_read_b128 v[140:143], %[p] offset:160\n"
+        "ds_read_b128 v[144:147], %[p] offset:176\n"
+        "ds_read_b128 v[148:151], %[p] offset:192\n"
+        "ds_read_b128 v[152:155], %[p] offset:208\n"
+        "ds_read_b128 v[156:159], %[p] offset:224\n"
+        "ds_read_b128 v[160:163], %[p] offset:240\n"
+        "s_waitcnt lgkmcnt(8)\n"
+        "v_add_f32 %[s], %[s], v100\n"
+        "v_add_f32 %[s], %[s], v101\n"
+        "v_add_f32 %[s], %[s], v102\n"
+        "v_add_f32 %[s], %[s], v103\n"
+        "v_add_f32 %[s], %[s], v104\n"
+        "v_add_f32 %[s], %[s], v105\n"
+        "v_add_f32 %[s], %[s], v106\n"
+        "v_add_f32 %[s], %[s], v107\n"
+        "v_add_f32 %[s], %[s], v108\n"
+        "v_add_f32 %[s], %[s], v109\n"
+        "v_add_f32 %[s], %[s], v110\n"
+        "v_add_f32 %[s], %[s], v111\n"
+        "v_add_f32 %[s], %[s], v112\n"
+        "v_add_f32 %[s], %[s], v113\n"
+        "v_add_f32 %[s], %[s], v114\n"
+        "v_add_f32 %[s], %[s], v115\n"
+        "v_add_f32 %[s], %[s], v116\n"
+        "v_add_f32 %[s], %[s], v117\n"
+        "v_add_f32 %[s], %[s], v118\n"
+        "v_add_f32 %[s], %[s], v119\n"
+        "v_add_f32 %[s], %[s], v120\n"
+        "v_add_f32 %[s], %[s], v121\n"
+        "v_add_f32 %[s], %[s], v122\n"
+        "v_add_f32 %[s], %[s], v123\n"
+        "v_add_f32 %[s], %[s], v124\n"
+        "v_add_f32 %[s], %[s], v125\n"
+        "v_add_f32 %[s], %[s], v126\n"
+        "v_add_f32 %[s], %[s], v127\n"
+        "v_add_f32 %[s], %[s], v128\n"
+        "v_add_f32 %[s], %[s], v129\n"
+        "v_add_f32 %[s], %[s], v130\n"
+        "v_add_f32 %[s], %[s], v131\n"
+        "ds_read_b128 v[100:103], %[p] offset:256\n"
+        "ds_read_b128 v[104:107], %[p] offset:272\n"
+        "ds_read_b128 v[108:111], %[p] offset:288\n"
+        "ds_read_b128 v[112:115], %[p] offset:304\n"
+        "ds_read_b128 v[116:119], %[p] offset:320\n"
+        "ds_read_b128 v[120:123], %[p] offset:336\n"
+        "ds_read_b128 v[124:127], %[p] offset:352\n"
+        "ds_read_b128 v[128:131], %[p] offset:368\n"
+        "s_waitcnt lgkmcnt(8)\n"
+        "v_add_f32 %[s], %[s], v132\n"
+        "v_add_f32 %[s], %[s], v133\n"
+        "v_add_f32 %[s], %[s], v134\n"
+        "v_add_f32 %[s], %[s], v135\n"
+        "v_add_f32 %[s], %[s], v136\n"
+        "v_add_f32 %[s], %[s], v137\n"
+        "v_add_f32 %[s], %[s], v138\n"
+        "v_add_f32 %[s], %[s], v139\n"
+        "v_add_f32 %[s], %[s], v140\n"
+        "v_add_f32 %[s], %[s], v141\n"
+        "v_add_f32 %[s], %[s], v142\n"
+        "v_add_f32 %[s], %[s], v143\n"
+        "v_add_f32 %[s], %[s], v144\n"
+        "v_add_f32 %[s], %[s], v145\n"
+        "v_add_f32 %[s], %[s], v146\n"
+        "v_add_f32 %[s], %[s], v147\n"
+        "v_add_f32 %[s], %[s], v148\n"
+        "v_add_f32 %[s], %[s], v149\n"
+        "v_add_f32 %[s], %[s], v150\n"
+        "v_add_f32 %[s], %[s], v151\n"
+        "v_add_f32 %[s], %[s], v152\n"
+        "v_add_f32 %[s], %[s], v153\n"
+        "v_add_f32 %[s], %[s], v154\n"
+        "v_add_f32 %[s], %[s], v155\n"
+        "v_add_f32 %[s], %[s], v156\n"
+        "v_add_f32 %[s], %[s], v157\n"
+        "v_add_f32 %[s], %[s], v158\n"
+        "v_add_f32 %[s], %[s], v159\n"
+        "v_add_f32 %[s], %[s], v160\n"
+        "v_add_f32 %[s], %[s], v161\n"
+        "v_add_f32 %[s], %[s], v162\n"
+        "v_add_f32 %[s], %[s], v163\n"
+        "v_add_u32 %[p], 256, %[p]\n"
+        "s_sub_i32 %[c], %[c], 1\n"
+        "s_cmp_gt_i32 %[c], 0\n"
+        "s_cbranch_scc1 1b\n"
+        "s_waitcnt lgkmcnt(0)\n"
+        : [s] "+v"(sum), [p] "+v"(p), [c] "+s"(c)
+        :
+        : "v100", "v101", "v102", "v103", "v104", "v105", "v106", "v107", "v108", "v109", "v110", "v111", "v112", "v113", "v114", "v115",
+          "v116", "v117", "v118", "v119", "v120", "v121", "v122", "v123", "v124", "v125", "v126", "v127", "v128", "v129", "v130", "v131",
+          "v132", "v133", "v134", "v135", "v136", "v137", "v138", "v139", "v140", "v141", "v142", "v143", "v144", "v145", "v146", "v147",
+          "v148", "v149", "v150", "v151", "v152", "v153", "v154", "v155", "v156", "v157", "v158", "v159", "v160", "v161", "v162", "v163", "scc", "memory");
+    return sum;
 }
 
 // rms_norm's 1/rms of xs[0..n) (norm.rs:52-88): sum of squares in eight FMA

@@ -49,7 +49,8 @@ GAJE_HD inline uint32_t ref_f32_bits(float f) {
     return u;
 }
 
-GAJE_HD inline float expf_ref(float x) {
+// tab: the 32 table words above (kExp2Tab, or a copy of it in LDS).
+GAJE_HD inline float expf_ref_t(float x, const uint64_t *tab) {
     const double InvLn2N = 0x1.71547652b82fep+0 * 32.0;
     const double Shift = 0x1.8p+52;
     const double C0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
@@ -69,7 +70,7 @@ GAJE_HD inline float expf_ref(float x) {
     memcpy(&ki, &kd, 8);
     kd -= Shift;
     const double r = __builtin_fma(InvLn2N, xd, -kd);
-    uint64_t t = kExp2Tab[ki % 32] + (ki << 47);
+    uint64_t t = tab[ki % 32] + (ki << 47);
     double s;
     memcpy(&s, &t, 8);
     const double z = __builtin_fma(C0, r, C1);
@@ -79,5 +80,7 @@ GAJE_HD inline float expf_ref(float x) {
     y = y * s;
     return (float)y;
 }
+
+GAJE_HD inline float expf_ref(float x) { return expf_ref_t(x, kExp2Tab); }
 
 }  // namespace gaje

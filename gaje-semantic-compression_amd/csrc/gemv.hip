@@ -437,6 +437,7 @@ template <int FMT, int LPR, bool NT, int D>
 __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npairs, int xstride, int nw_off) {
     extern __shared__ __align__(16) float smem[];
     __shared__ float inv_slot;
+    __shared__ uint64_t etab[32];  // SwiGLU: the exponential's table, read from LDS
     DevState *st = p.st;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -463,6 +464,8 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
         else if constexpr (FMT == FMT_F32) f32_prefetch<NT>(p, q.row, s, f32r);
     }
     const int halted = st ? st->halted : 0;
+    const bool swiglu = p.mode == MODE_SWIGLU;
+    const uint64_t tabv = swiglu && tid < 32 ? kExp2Tab[tid] : 0;
 
     // ---- prologue: activation vector (and the norm weights) into LDS, one
     // batch of loads in flight per thread; normalised if requested ----
@@ -519,6 +522,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
             }
         }
         if constexpr (FMT == FMT_Q4_0) q4_zero_x_pad(xv, p.nb);
+        if (swiglu && tid < 32) etab[tid] = tabv;
         if (__syncthreads_or(bad_in) && p.st_in >= 0 && tid == 0) nan_flag(st, p.layer, p.st_in);
         if (p.norm_w) {
             if constexpr (FMT == FMT_Q4_0) rms_inv_chain_major(xv, K, p.eps, &inv_slot);
@@ -553,6 +557,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
         }
     }
     if constexpr (FMT == FMT_LUT4) {
+        if (swiglu && tid < 32) etab[tid] = tabv;
         if (__syncthreads_or(bad_in) && p.st_in >= 0 && tid == 0) nan_flag(st, p.layer, p.st_in);
         if (p.norm_w) {
             rmsnorm_inplace(smem, K, nw, p.eps, &inv_slot);
@@ -675,7 +680,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
             }
             case MODE_SWIGLU: {
                 if (isnan(y1)) nan_flag(st, p.layer, p.st_a);
-                const float o = swiglu1(y0, y1);
+                const float o = swiglu1(y0, y1, etab);
                 if (isnan(o)) nan_flag(st, p.layer, p.st_b);
                 p.y[pr] = o;
                 break;
