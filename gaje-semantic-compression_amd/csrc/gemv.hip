@@ -270,29 +270,61 @@ __global__ void pack_q4_0_kernel(const uint8_t *src, uint8_t *dst, int64_t N, in
         pad[t] = 0;
 }
 
+// Row-major f32 rows -> tiled layout; one thread per 8-float chunk slot.
+__global__ void pack_f32_tiled_kernel(const float *src, float *dst, int64_t N, int64_t K) {
+    const int64_t C = K / 8;
+    const int64_t total = (N + 31) / 32 * 32 * C;  // chunk slots
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = t & 31, tc = t >> 5;  // row in tile, (tile, chunk)
+        const int64_t tile = tc / C, c = tc - tile * C;
+        const int64_t row = tile * 32 + r;
+        float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+        if (row < N) {
+            a = *(const float4 *)(src + row * K + 8 * c);
+            b = *(const float4 *)(src + row * K + 8 * c + 4);
+        }
+        *(float4 *)(dst + 8 * t) = a;
+        *(float4 *)(dst + 8 * t + 4) = b;
+    }
+}
+
 // ----------------------------------------------------------------- f32 ----
 // LPR = 2: lane h owns chains 4h..4h+3 (one float4 of each 8-float chunk).
-// F32_AHEAD chunks of the row are in flight per lane.
+// F32_AHEAD chunks of the row are in flight per lane.  Row-major rows step 8
+// floats from chunk to chunk; tiled rows (a wave's 32 rows are one tile) step
+// one KiB, and each of the wave's chunk loads is one contiguous KiB.
 constexpr int F32_AHEAD = 8;
 struct F32Ring {
     float4 w[F32_AHEAD];
 };
 
+// This lane's first weight quad of `row` and the float stride between its chunks.
+__device__ __forceinline__ const float *f32_lane_ptr(const GemvParams &p, int64_t row, int s, int64_t &cstride) {
+    if (p.f32_tiled) {
+        cstride = 256;
+        return (const float *)p.w + (size_t)(row >> 5) * (size_t)p.K * 32 + (row & 31) * 8 + 4 * s;
+    }
+    cstride = 8;
+    return (const float *)p.w + (size_t)row * p.K + 4 * s;
+}
+
 template <bool NT>
 __device__ __forceinline__ void f32_prefetch(const GemvParams &p, int64_t row, int s, F32Ring &r) {
     const int64_t chunks = p.K / 8;
     if (chunks == 0) return;
-    const float *wl = (const float *)p.w + (size_t)row * p.K + 4 * s;
+    int64_t cs;
+    const float *wl = f32_lane_ptr(p, row, s, cs);
 #pragma unroll
-    for (int u = 0; u < F32_AHEAD; ++u) r.w[u] = ld_f4<NT>(wl + 8 * (u < chunks ? u : chunks - 1));
+    for (int u = 0; u < F32_AHEAD; ++u) r.w[u] = ld_f4<NT>(wl + cs * (u < chunks ? u : chunks - 1));
 }
 
 template <bool NT>
 __device__ __forceinline__ float f32_consume(const GemvParams &p, const float *xs, int64_t row, int s, int base,
                                              F32Ring &r) {
     float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-    const float *wr = (const float *)p.w + (size_t)row * p.K;
-    const float *wl = wr + 4 * s;
+    const float *wr = (const float *)p.w + (size_t)row * p.K;  // row-major only (scalar tail)
+    int64_t cs;
+    const float *wl = f32_lane_ptr(p, row, s, cs);
     const float *xl = xs + 4 * s;
     const int64_t chunks = p.K / 8;
     int64_t t = 0;
@@ -301,7 +333,7 @@ __device__ __forceinline__ float f32_consume(const GemvParams &p, const float *x
         for (int u = 0; u < F32_AHEAD; ++u) {
             const float4 w = r.w[u];
             const int64_t tn = t + u + F32_AHEAD < chunks ? t + u + F32_AHEAD : chunks - 1;
-            r.w[u] = ld_f4<NT>(wl + 8 * tn);
+            r.w[u] = ld_f4<NT>(wl + cs * tn);
             const float4 x = *(const float4 *)(xl + 8 * (t + u));
             a0 = fmaf(x.x, w.x, a0);
             a1 = fmaf(x.y, w.y, a1);
@@ -324,7 +356,7 @@ __device__ __forceinline__ float f32_consume(const GemvParams &p, const float *x
     const float u0 = a0 + shfl(a0, base + 1), u1 = a1 + shfl(a1, base + 1);
     const float u2 = a2 + shfl(a2, base + 1), u3 = a3 + shfl(a3, base + 1);
     float sum = (u0 + u1) + (u2 + u3);
-    for (int64_t i = chunks * 8; i < p.K; ++i) {  // scalar tail, mul then add
+    for (int64_t i = chunks * 8; i < p.K; ++i) {  // scalar tail (row-major rows), mul then add
         const float prod = xs[i] * wr[i];
         sum = sum + prod;
     }
@@ -734,6 +766,20 @@ int launch_pack_q4_0(const uint8_t *src, uint8_t *dst, int64_t N, int64_t K, hip
     return GAJE_OK;
 }
 
+int64_t f32_tiled_bytes(int64_t N, int64_t K) { return (N + 31) / 32 * 32 * K * 4; }
+
+int launch_pack_f32_tiled(const float *src, float *dst, int64_t N, int64_t K, hipStream_t s) {
+    if (N < 0 || K <= 0 || K % 8 != 0) return set_error(GAJE_ERR_INVALID_ARG, "f32 tiling: K must be a positive multiple of 8");
+    if (N == 0) return GAJE_OK;
+    if (!src || !dst || (((uintptr_t)src | (uintptr_t)dst) & 15)) return set_error(GAJE_ERR_INVALID_ARG, "f32 tiling: null or unaligned buffer");
+    const int64_t total = (N + 31) / 32 * 32 * (K / 8);
+    int64_t grid = (total + 255) / 256;
+    if (grid > 65536) grid = 65536;
+    hipLaunchKernelGGL(pack_f32_tiled_kernel, dim3((unsigned)grid), dim3(256), 0, s, src, dst, N, K);
+    GAJE_HIP_CHECK(hipGetLastError());
+    return GAJE_OK;
+}
+
 // LDS floats before the norm-weight copy: the activation vector (chain-major
 // for Q4_0, plain otherwise) and, for LUT rows, one 16-entry table per row group.
 static int64_t gemv_x_floats(int64_t K, int fmt) {
@@ -757,6 +803,8 @@ int launch_gemv(const GemvParams &p, hipStream_t s) {
     if (p.fmt == FMT_F32 && p.K % 4 != 0)
         return set_error(GAJE_ERR_UNSUPPORTED, "gemv: f32 rows need in_features %% 4 == 0 (got %lld)",
                          (long long)p.K);
+    if (p.fmt == FMT_F32 && p.f32_tiled && p.K % 8 != 0)
+        return set_error(GAJE_ERR_INVALID_ARG, "gemv: tiled f32 rows need in_features %% 8 == 0");
     if (p.fmt == FMT_Q4_0 && p.K % 32 != 0)
         return set_error(GAJE_ERR_UNSUPPORTED, "gemv: Q4_0 rows need in_features %% 32 == 0 (got %lld)",
                          (long long)p.K);

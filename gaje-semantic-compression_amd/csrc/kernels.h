@@ -48,9 +48,11 @@ enum GemvMode : int32_t {
 };
 
 struct GemvParams {
-    // weights: FMT_Q4_0 rows in the packed layout of launch_pack_q4_0
+    // weights: FMT_Q4_0 rows in the packed layout of launch_pack_q4_0; FMT_F32
+    // rows row-major, or in the tiled layout of launch_pack_f32_tiled
     const uint8_t *w;
     int32_t fmt;
+    int32_t f32_tiled;       // FMT_F32 weights in the tiled layout (K % 8 == 0)
     int32_t nontemporal;     // stream the weights past the caches (read-once tensors)
     const float *lut;        // FMT_LUT4 tables
     int64_t lut_rows_own;    // rows r < lut_rows_own use table block r*nb*16
@@ -99,6 +101,12 @@ int launch_gemv(const GemvParams &p, hipStream_t s);
 constexpr int64_t Q4_TAIL_PAD = 2048;
 int launch_pack_q4_0(const uint8_t *src, uint8_t *dst, int64_t N, int64_t K, hipStream_t s);
 int64_t q4_0_packed_bytes(int64_t N, int64_t K);
+// Row-major f32 rows (K % 8 == 0) -> the tiled layout: tiles of 32 rows, and in
+// a tile the 8-float chunk c of rows 0..31 is one contiguous KiB, so a wave
+// holding the tile's rows reads each chunk with one coalesced load.  Rows past
+// N in the last tile are zero.
+int launch_pack_f32_tiled(const float *src, float *dst, int64_t N, int64_t K, hipStream_t s);
+int64_t f32_tiled_bytes(int64_t N, int64_t K);
 // Dynamic LDS a workgroup may use on the current device.
 size_t max_lds_per_block();
 // Dynamic LDS the GEMV needs for in_features K (so callers can check limits).

@@ -48,6 +48,7 @@ struct HostLinear {
 
 struct DevLinear {
     int fmt = -1;
+    int f32_tiled = 0;  // FMT_F32 rows in the GEMV's tiled layout
     int64_t N = 0, K = 0, rows_valid = 0, lut_rows_own = 0;
     int lut_block_stride = 0;
     uint8_t *w = nullptr;
@@ -308,7 +309,9 @@ struct gaje_hip_model {
 
 namespace {
 
-int upload_linear(gaje_hip_model *m, const HostLinear &L, DevLinear &D) {
+// tile_f32: store FMT_F32 rows in the GEMV's tiled layout (not for the
+// embedding, whose rows are looked up one at a time).
+int upload_linear(gaje_hip_model *m, const HostLinear &L, DevLinear &D, bool tile_f32 = true) {
     D = DevLinear();
     D.fmt = L.fmt;
     D.N = L.N;
@@ -329,6 +332,21 @@ int upload_linear(gaje_hip_model *m, const HostLinear &L, DevLinear &D) {
         m->release(tmp);
         GAJE_TRY(rc);
         m->weight_bytes += packed;
+    } else if (L.fmt == FMT_F32 && tile_f32 && L.K % 8 == 0 && D.rows_valid > 0) {
+        // stage the row-major rows and tile them (32-row tiles, KiB chunks)
+        const size_t raw = (size_t)D.rows_valid * L.K * 4;
+        const int64_t tiled = f32_tiled_bytes(D.rows_valid, L.K);
+        uint8_t *tmp = nullptr;
+        GAJE_TRY(m->upload(&tmp, L.w.data(), raw));
+        m->weight_bytes -= (int64_t)raw;
+        int rc = m->alloc(&D.w, (size_t)tiled);
+        if (rc == GAJE_OK) rc = launch_pack_f32_tiled((const float *)tmp, (float *)D.w, D.rows_valid, L.K, m->stream);
+        if (rc == GAJE_OK) rc = hipStreamSynchronize(m->stream) == hipSuccess ? GAJE_OK
+                                                                               : set_error(GAJE_ERR_HIP, "f32 tiling failed");
+        m->release(tmp);
+        GAJE_TRY(rc);
+        m->weight_bytes += tiled;
+        D.f32_tiled = 1;
     } else {
         GAJE_TRY(m->upload(&D.w, L.w.data(), L.w.size()));
     }
@@ -361,6 +379,7 @@ GemvParams gemv_base(const gaje_hip_model *m, const DevLinear &D, const float *x
     memset(&p, 0, sizeof p);
     p.w = D.w;
     p.fmt = D.fmt;
+    p.f32_tiled = D.f32_tiled;
     p.lut = D.lut;
     p.lut_rows_own = D.lut_rows_own;
     p.lut_block_stride = D.lut_block_stride;
@@ -676,7 +695,7 @@ extern "C" int gaje_hip_open(const char *path, int device, gaje_hip_model **out)
                          (long long)m->n_embd);
     m->vocab_embd = L.N;
     if (m->vocab_embd == 0) return set_error(GAJE_ERR_MODEL, "token_embd has no rows");
-    GAJE_TRY(upload_linear(m.get(), L, m->embd));
+    GAJE_TRY(upload_linear(m.get(), L, m->embd, false));
     std::vector<float> norm;
     GAJE_TRY(read_norm(f, "output_norm", norm));
     if ((int64_t)norm.size() != m->n_embd) return set_error(GAJE_ERR_MODEL, "output_norm length != n_embd");
