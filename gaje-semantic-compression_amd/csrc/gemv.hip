@@ -293,7 +293,7 @@ __global__ void pack_f32_tiled_kernel(const float *src, float *dst, int64_t N, i
 // F32_AHEAD chunks of the row are in flight per lane.  Row-major rows step 8
 // floats from chunk to chunk; tiled rows (a wave's 32 rows are one tile) step
 // one KiB, and each of the wave's chunk loads is one contiguous KiB.
-constexpr int F32_AHEAD = 8;
+constexpr int F32_AHEAD = 16;
 struct F32Ring {
     float4 w[F32_AHEAD];
 };
@@ -861,6 +861,9 @@ int launch_gemv(const GemvParams &p, hipStream_t s) {
     const int64_t pairs_per_block = (WAVE / (2 * lpr)) * (THREADS / WAVE);
     int64_t grid = (npairs + pairs_per_block - 1) / pairs_per_block;
     if (grid > MAX_GRID) grid = MAX_GRID;
+    // tiled f32 rows stream at the best rate with one workgroup per compute
+    // unit walking its share of the tiles (measured on a 151936 x 896 matrix)
+    if (p.fmt == FMT_F32 && p.f32_tiled && grid > device_cu_count()) grid = device_cu_count();
     const int xstride = p.fmt == FMT_Q4_0 ? q4_xstride(p.K) : 0;
     const int nw_off = (int)gemv_x_floats(p.K, p.fmt);
     hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(THREADS), lds, s, p, npairs, xstride, nw_off);

@@ -109,6 +109,8 @@ int launch_pack_f32_tiled(const float *src, float *dst, int64_t N, int64_t K, hi
 int64_t f32_tiled_bytes(int64_t N, int64_t K);
 // Dynamic LDS a workgroup may use on the current device.
 size_t max_lds_per_block();
+// Compute units of the current device.
+int device_cu_count();
 // Dynamic LDS the GEMV needs for in_features K (so callers can check limits).
 size_t gemv_lds_bytes(int64_t K, int fmt, bool norm);
 
