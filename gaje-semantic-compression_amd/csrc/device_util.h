@@ -12,6 +12,28 @@ namespace gaje {
 
 constexpr int WAVE = 64;
 
+// Workgroup barrier that orders LDS only: unlike __syncthreads it does not wait
+// for the wave's outstanding global loads (s_waitcnt lgkmcnt(0); s_barrier),
+// so weight loads issued earlier stay in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// lds_barrier that also returns whether pred held in any thread of the block;
+// slots: one int per wave in LDS, used by no other barrier_or in flight.
+template <int NWAVES>
+__device__ __forceinline__ bool barrier_or(int pred, int *slots) {
+    const bool any = __any(pred);
+    if ((threadIdx.x & 63) == 0) slots[threadIdx.x >> 6] = any;
+    lds_barrier();
+    bool r = false;
+#pragma unroll
+    for (int w = 0; w < NWAVES; ++w) r |= slots[w] != 0;
+    return r;
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);

@@ -36,6 +36,10 @@ namespace {
 
 constexpr int THREADS = 256;
 constexpr int MAX_GRID = 8192;
+
+// Stands in for the weights of a tensor with no complete row, so that the
+// weight ring's first loads never need a branch (they are not used).
+__device__ __align__(256) uint8_t kZeroRows[65536];
 constexpr int Q4_PREFETCH = 8;  // packed groups (4 blocks each) in flight per lane, short rows
 
 __device__ __forceinline__ void pair_rows(const GemvParams &p, int64_t pr, int64_t &r0, int64_t &r1) {
@@ -160,9 +164,9 @@ __device__ __forceinline__ float q4_tail(float acc, const Q4Ring<D> &r, const fl
 // reads into the next row or the tensor's tail padding (Q4_TAIL_PAD); those
 // values are never used.
 template <bool NT, int D>
-__device__ __forceinline__ void q4_prefetch(const GemvParams &p, int64_t row, int l, Q4Ring<D> &r) {
+__device__ __forceinline__ void q4_prefetch(const uint8_t *w, const GemvParams &p, int64_t row, int l, Q4Ring<D> &r) {
     const int G = (p.nb + 3) >> 2;
-    const uint8_t *rp = p.w + (size_t)row * G * 80;
+    const uint8_t *rp = w + (size_t)row * G * 80;
 #pragma unroll
     for (int i = 0; i < D; ++i) {
         r.n[i] = ld_u2<NT>(rp + i * 80 + 8 * l);
@@ -299,23 +303,23 @@ struct F32Ring {
 };
 
 // This lane's first weight quad of `row` and the float stride between its chunks.
-__device__ __forceinline__ const float *f32_lane_ptr(const GemvParams &p, int64_t row, int s, int64_t &cstride) {
+__device__ __forceinline__ const float *f32_lane_ptr(const uint8_t *w, const GemvParams &p, int64_t row, int s,
+                                                     int64_t &cstride) {
     if (p.f32_tiled) {
         cstride = 256;
-        return (const float *)p.w + (size_t)(row >> 5) * (size_t)p.K * 32 + (row & 31) * 8 + 4 * s;
+        return (const float *)w + (size_t)(row >> 5) * (size_t)p.K * 32 + (row & 31) * 8 + 4 * s;
     }
     cstride = 8;
-    return (const float *)p.w + (size_t)row * p.K + 4 * s;
+    return (const float *)w + (size_t)row * p.K + 4 * s;
 }
 
 template <bool NT>
-__device__ __forceinline__ void f32_prefetch(const GemvParams &p, int64_t row, int s, F32Ring &r) {
+__device__ __forceinline__ void f32_prefetch(const uint8_t *w, const GemvParams &p, int64_t row, int s, F32Ring &r) {
     const int64_t chunks = p.K / 8;
-    if (chunks == 0) return;
     int64_t cs;
-    const float *wl = f32_lane_ptr(p, row, s, cs);
+    const float *wl = f32_lane_ptr(w, p, row, s, cs);
 #pragma unroll
-    for (int u = 0; u < F32_AHEAD; ++u) r.w[u] = ld_f4<NT>(wl + cs * (u < chunks ? u : chunks - 1));
+    for (int u = 0; u < F32_AHEAD; ++u) r.w[u] = ld_f4<NT>(wl + cs * (u < chunks ? u : (chunks > 0 ? chunks - 1 : 0)));
 }
 
 template <bool NT>
@@ -324,7 +328,7 @@ __device__ __forceinline__ float f32_consume(const GemvParams &p, const float *x
     float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
     const float *wr = (const float *)p.w + (size_t)row * p.K;  // row-major only (scalar tail)
     int64_t cs;
-    const float *wl = f32_lane_ptr(p, row, s, cs);
+    const float *wl = f32_lane_ptr(p.w, p, row, s, cs);
     const float *xl = xs + 4 * s;
     const int64_t chunks = p.K / 8;
     int64_t t = 0;
@@ -470,6 +474,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
     extern __shared__ __align__(16) float smem[];
     __shared__ float inv_slot;
     __shared__ uint64_t etab[32];  // SwiGLU: the exponential's table, read from LDS
+    __shared__ int or_in[THREADS / WAVE], or_norm[THREADS / WAVE];  // barrier_or slots
     DevState *st = p.st;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -486,15 +491,10 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
     const int pairs_per_block = PAIRS_PER_WAVE * (THREADS / WAVE);
     float *tbl = smem + ((K + 3) & ~(int64_t)3) + (size_t)(tid / LPR) * 16;  // LUT slot of this row group
 
-    // ---- the first row pair's weights start streaming before anything else ----
     int64_t pr0 = (int64_t)blockIdx.x * pairs_per_block;
     PairRows q = locate<FMT>(p, pr0 + wave * PAIRS_PER_WAVE + pslot, npairs, half);
     Q4Ring<D> q4r;
     F32Ring f32r;
-    if (q.row_ok) {
-        if constexpr (FMT == FMT_Q4_0) q4_prefetch<NT, D>(p, q.row, s, q4r);
-        else if constexpr (FMT == FMT_F32) f32_prefetch<NT>(p, q.row, s, f32r);
-    }
     const int halted = st ? st->halted : 0;
     const bool swiglu = p.mode == MODE_SWIGLU;
     const uint64_t tabv = swiglu && tid < 32 ? kExp2Tab[tid] : 0;
@@ -529,16 +529,31 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
     } else {
         // K % 4 == 0 and 16-byte aligned x / norm_w (checked at launch).  When
         // the vector fits one batch its values stay in registers for the norm.
+        // The first batch of activation loads is issued first, then the first
+        // row pair's weight ring, with no branch in between: the loads complete
+        // in order, so the first use of the activations waits for them alone and
+        // the weights stream in while the prologue runs.  Rows without work
+        // prefetch row 0 (never used).
         const int64_t K4 = K >> 2;
         const bool one_batch = K4 <= XB4 * THREADS;
-        for (int64_t m0 = 0; m0 < K4; m0 += XB4 * THREADS) {
+        const float4 *x4 = (const float4 *)p.x;
+        const float4 *w4 = (const float4 *)(p.norm_w ? p.norm_w : p.x);
 #pragma unroll
-            for (int u = 0; u < XB4; ++u) {
-                const int64_t m = m0 + u * THREADS + tid;
-                xr[u] = m < K4 ? ((const float4 *)p.x)[m] : make_float4(0.f, 0.f, 0.f, 0.f);
-                wr[u] = (p.norm_w && m < K4) ? ((const float4 *)p.norm_w)[m] : make_float4(0.f, 0.f, 0.f, 0.f);
-            }
-            if (m0 == 0 && halted) return;  // uniform; checked once the first loads are in flight
+        for (int u = 0; u < XB4; ++u) {
+            const int64_t m = u * THREADS + tid;
+            const int64_t mc = m < K4 ? m : K4 - 1;
+            xr[u] = x4[mc];
+            wr[u] = w4[mc];
+        }
+        __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the ring
+        {
+            const uint8_t *wbase = p.rows_valid > 0 ? p.w : kZeroRows;
+            const int64_t prow = q.row_ok ? q.row : 0;
+            if constexpr (FMT == FMT_Q4_0) q4_prefetch<NT, D>(wbase, p, prow, s, q4r);
+            else f32_prefetch<NT>(wbase, p, prow, s, f32r);
+        }
+        if (halted) return;  // uniform; checked once the first loads are in flight
+        auto store_batch = [&](int64_t m0) {
 #pragma unroll
             for (int u = 0; u < XB4; ++u) {
                 const int64_t m = m0 + u * THREADS + tid;
@@ -552,14 +567,26 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
                     bad_in |= isnan(v.x) | isnan(v.y) | isnan(v.z) | isnan(v.w);
                 }
             }
+        };
+        store_batch(0);  // (peeled: no join between the loads above and this use)
+        for (int64_t m0 = XB4 * THREADS; m0 < K4; m0 += XB4 * THREADS) {
+#pragma unroll
+            for (int u = 0; u < XB4; ++u) {
+                const int64_t m = m0 + u * THREADS + tid;
+                const int64_t mc = m < K4 ? m : K4 - 1;
+                xr[u] = x4[mc];
+                wr[u] = w4[mc];
+            }
+            store_batch(m0);
         }
         if constexpr (FMT == FMT_Q4_0) q4_zero_x_pad(xv, p.nb);
         if (swiglu && tid < 32) etab[tid] = tabv;
-        if (__syncthreads_or(bad_in) && p.st_in >= 0 && tid == 0) nan_flag(st, p.layer, p.st_in);
+        // barriers from here on order LDS only: the weight ring stays in flight
+        if (barrier_or<THREADS / WAVE>(bad_in, or_in) && p.st_in >= 0 && tid == 0) nan_flag(st, p.layer, p.st_in);
         if (p.norm_w) {
             if constexpr (FMT == FMT_Q4_0) rms_inv_chain_major(xv, K, p.eps, &inv_slot);
             else rms_inv_plain(smem, K, p.eps, &inv_slot);
-            __syncthreads();
+            lds_barrier();
             const float inv = inv_slot;
             int bad = 0;
             if (one_batch) {
@@ -585,7 +612,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
                     bad |= isnan(x);
                 }
             }
-            if (__syncthreads_or(bad) && p.st_norm >= 0 && tid == 0) nan_flag(st, p.layer, p.st_norm);
+            if (barrier_or<THREADS / WAVE>(bad, or_norm) && p.st_norm >= 0 && tid == 0) nan_flag(st, p.layer, p.st_norm);
         }
     }
     if constexpr (FMT == FMT_LUT4) {
@@ -610,13 +637,13 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
             }
             inv_slot = sqrtf(ss / (float)K + p.eps);
         }
-        __syncthreads();
+        lds_barrier();
         const float rms = inv_slot;
         if (rms > p.h_scale) {
             const float sc = p.h_scale / rms;
             for (int64_t k = tid; k < K; k += THREADS) xv.at(k) = xv.at(k) * sc;
         }
-        __syncthreads();
+        lds_barrier();
     }
     if (p.x_out && blockIdx.x == 0)
         for (int64_t k = tid; k < K; k += THREADS) p.x_out[k] = xv.at(k);
@@ -631,8 +658,8 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
         if (!first) {
             q = locate<FMT>(p, pr, npairs, half);
             if (q.row_ok) {
-                if constexpr (FMT == FMT_Q4_0) q4_prefetch<NT, D>(p, q.row, s, q4r);
-                else if constexpr (FMT == FMT_F32) f32_prefetch<NT>(p, q.row, s, f32r);
+                if constexpr (FMT == FMT_Q4_0) q4_prefetch<NT, D>(p.w, p, q.row, s, q4r);
+                else if constexpr (FMT == FMT_F32) f32_prefetch<NT>(p.w, p, q.row, s, f32r);
             }
         }
         const int64_t r0 = q.r0, r1 = q.r1;
