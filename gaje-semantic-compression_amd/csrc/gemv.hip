@@ -503,7 +503,9 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
     // batch of loads in flight per thread; normalised if requested ----
     float *nw = smem + nw_off;  // plain copy of norm_w when the vector spans several batches
     int bad_in = 0;
-    constexpr int XB4 = 6;
+    // float4s of the activation vector per thread and batch: Q4_0 rows with
+    // the short ring have K <= 1024, which one float4 per thread covers
+    constexpr int XB4 = (FMT == FMT_Q4_0 && D == Q4_PREFETCH) ? 1 : 6;
     float4 xr[XB4], wr[XB4];
     if constexpr (FMT == FMT_LUT4) {
         constexpr int XB = 8;
@@ -537,13 +539,18 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
         const int64_t K4 = K >> 2;
         const bool one_batch = K4 <= XB4 * THREADS;
         const float4 *x4 = (const float4 *)p.x;
-        const float4 *w4 = (const float4 *)(p.norm_w ? p.norm_w : p.x);
+        const float4 *w4 = (const float4 *)p.norm_w;
 #pragma unroll
         for (int u = 0; u < XB4; ++u) {
             const int64_t m = u * THREADS + tid;
-            const int64_t mc = m < K4 ? m : K4 - 1;
-            xr[u] = x4[mc];
-            wr[u] = w4[mc];
+            xr[u] = x4[m < K4 ? m : K4 - 1];
+        }
+        if (w4) {
+#pragma unroll
+            for (int u = 0; u < XB4; ++u) {
+                const int64_t m = u * THREADS + tid;
+                wr[u] = w4[m < K4 ? m : K4 - 1];
+            }
         }
         __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the ring
         {
@@ -575,7 +582,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
                 const int64_t m = m0 + u * THREADS + tid;
                 const int64_t mc = m < K4 ? m : K4 - 1;
                 xr[u] = x4[mc];
-                wr[u] = w4[mc];
+                if (w4) wr[u] = w4[mc];
             }
             store_batch(m0);
         }
