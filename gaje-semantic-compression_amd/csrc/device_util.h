@@ -256,6 +256,117 @@ __device__ __forceinline__ float chain_lds(float sum, const float *e, int n) {
     return sum;
 }
 
+// fma(e[i], e[i], acc) for i = 0..n-1 in order in this lane (the sum-of-squares
+// chain of rms_norm), with the same loop, limits and read-ahead as chain_lds.
+__device__ __forceinline__ float chain_lds_sq(float acc, const float *e, int n) {
+    uint32_t p = (uint32_t)(uintptr_t)e;
+    int c = __builtin_amdgcn_readfirstlane(n >> 6);  // uniform: lives in an SGPR
+    asm volatile(
+        "ds_read_b128 v[100:103], %[p] offset:0\n"
+        "ds_read_b128 v[104:107], %[p] offset:16\n"
+        "ds_read_b128 v[108:111], %[p] offset:32\n"
+        "ds_read_b128 v[112:115], %[p] offset:48\n"
+        "ds_read_b128 v[116:119], %[p] offset:64\n"
+        "ds_read_b128 v[120:123], %[p] offset:80\n"
+        "ds_read_b128 v[124:127], %[p] offset:96\n"
+        "ds_read_b128 v[128:131], %[p] offset:112\n"
+        "1:\n"
+        "ds_read_b128 v[132:135], %[p] offset:128\n"
+        "ds_read_b128 v[136:139], %[p] offset:144\n"
+        "ds_read_b128 v[140:143], %[p] offset:160\n"
+        "ds_read_b128 v[144:147], %[p] offset:176\n"
+        "ds_read_b128 v[148:151], %[p] offset:192\n"
+        "ds_read_b128 v[152:155], %[p] offset:208\n"
+        "ds_read_b128 v[156:159], %[p] offset:224\n"
+        "ds_read_b128 v[160:163], %[p] offset:240\n"
+        "s_waitcnt lgkmcnt(8)\n"
+        "v_fmac_f32 %[s], v100, v100\n"
+        "v_fmac_f32 %[s], v101, v101\n"
+        "v_fmac_f32 %[s], v102, v102\n"
+        "v_fmac_f32 %[s], v103, v103\n"
+        "v_fmac_f32 %[s], v104, v104\n"
+        "v_fmac_f32 %[s], v105, v105\n"
+        "v_fmac_f32 %[s], v106, v106\n"
+        "v_fmac_f32 %[s], v107, v107\n"
+        "v_fmac_f32 %[s], v108, v108\n"
+        "v_fmac_f32 %[s], v109, v109\n"
+        "v_fmac_f32 %[s], v110, v110\n"
+        "v_fmac_f32 %[s], v111, v111\n"
+        "v_fmac_f32 %[s], v112, v112\n"
+        "v_fmac_f32 %[s], v113, v113\n"
+        "v_fmac_f32 %[s], v114, v114\n"
+        "v_fmac_f32 %[s], v115, v115\n"
+        "v_fmac_f32 %[s], v116, v116\n"
+        "v_fmac_f32 %[s], v117, v117\n"
+        "v_fmac_f32 %[s], v118, v118\n"
+        "v_fmac_f32 %[s], v119, v119\n"
+        "v_fmac_f32 %[s], v120, v120\n"
+        "v_fmac_f32 %[s], v121, v121\n"
+        "v_fmac_f32 %[s], v122, v122\n"
+        "v_fmac_f32 %[s], v123, v123\n"
+        "v_fmac_f32 %[s], v124, v124\n"
+        "v_fmac_f32 %[s], v125, v125\n"
+        "v_fmac_f32 %[s], v126, v126\n"
+        "v_fmac_f32 %[s], v127, v127\n"
+        "v_fmac_f32 %[s], v128, v128\n"
+        "v_fmac_f32 %[s], v129, v129\n"
+        "v_fmac_f32 %[s], v130, v130\n"
+        "v_fmac_f32 %[s], v131, v131\n"
+        "ds_read_b128 v[100:103], %[p] offset:256\n"
+        "ds_read_b128 v[104:107], %[p] offset:272\n"
+        "ds_read_b128 v[108:111], %[p] offset:288\n"
+        "ds_read_b128 v[112:115], %[p] offset:304\n"
+        "ds_read_b128 v[116:119], %[p] offset:320\n"
+        "ds_read_b128 v[120:123], %[p] offset:336\n"
+        "ds_read_b128 v[124:127], %[p] offset:352\n"
+        "ds_read_b128 v[128:131], %[p] offset:368\n"
+        "s_waitcnt lgkmcnt(8)\n"
+        "v_fmac_f32 %[s], v132, v132\n"
+        "v_fmac_f32 %[s], v133, v133\n"
+        "v_fmac_f32 %[s], v134, v134\n"
+        "v_fmac_f32 %[s], v135, v135\n"
+        "v_fmac_f32 %[s], v136, v136\n"
+        "v_fmac_f32 %[s], v137, v137\n"
+        "v_fmac_f32 %[s], v138, v138\n"
+        "v_fmac_f32 %[s], v139, v139\n"
+        "v_fmac_f32 %[s], v140, v140\n"
+        "v_fmac_f32 %[s], v141, v141\n"
+        "v_fmac_f32 %[s], v142, v142\n"
+        "v_fmac_f32 %[s], v143, v143\n"
+        "v_fmac_f32 %[s], v144, v144\n"
+        "v_fmac_f32 %[s], v145, v145\n"
+        "v_fmac_f32 %[s], v146, v146\n"
+        "v_fmac_f32 %[s], v147, v147\n"
+        "v_fmac_f32 %[s], v148, v148\n"
+        "v_fmac_f32 %[s], v149, v149\n"
+        "v_fmac_f32 %[s], v150, v150\n"
+        "v_fmac_f32 %[s], v151, v151\n"
+        "v_fmac_f32 %[s], v152, v152\n"
+        "v_fmac_f32 %[s], v153, v153\n"
+        "v_fmac_f32 %[s], v154, v154\n"
+        "v_fmac_f32 %[s], v155, v155\n"
+        "v_fmac_f32 %[s], v156, v156\n"
+        "v_fmac_f32 %[s], v157, v157\n"
+        "v_fmac_f32 %[s], v158, v158\n"
+        "v_fmac_f32 %[s], v159, v159\n"
+        "v_fmac_f32 %[s], v160, v160\n"
+        "v_fmac_f32 %[s], v161, v161\n"
+        "v_fmac_f32 %[s], v162, v162\n"
+        "v_fmac_f32 %[s], v163, v163\n"
+        "v_add_u32 %[p], 256, %[p]\n"
+        "s_sub_i32 %[c], %[c], 1\n"
+        "s_cmp_gt_i32 %[c], 0\n"
+        "s_cbranch_scc1 1b\n"
+        "s_waitcnt lgkmcnt(0)\n"
+        : [s] "+v"(acc), [p] "+v"(p), [c] "+s"(c)
+        :
+        : "v100", "v101", "v102", "v103", "v104", "v105", "v106", "v107", "v108", "v109", "v110", "v111", "v112", "v113", "v114", "v115",
+          "v116", "v117", "v118", "v119", "v120", "v121", "v122", "v123", "v124", "v125", "v126", "v127", "v128", "v129", "v130", "v131",
+          "v132", "v133", "v134", "v135", "v136", "v137", "v138", "v139", "v140", "v141", "v142", "v143", "v144", "v145", "v146", "v147",
+          "v148", "v149", "v150", "v151", "v152", "v153", "v154", "v155", "v156", "v157", "v158", "v159", "v160", "v161", "v162", "v163", "scc", "memory");
+    return acc;
+}
+
 // rms_norm's 1/rms of xs[0..n) (norm.rs:52-88): sum of squares in eight FMA
 // chains over 8-float chunks, reduced ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7)),
 // scalar tail, inv = 1/sqrt(ss/n + eps), stored by thread 0 in *inv_slot.

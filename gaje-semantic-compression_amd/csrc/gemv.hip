@@ -75,6 +75,22 @@ struct XView {
     }
 };
 
+// Stores elements 4m..4m+3 of the activation vector.  Chain-major: they sit
+// in chain rows 4(m&1)..4(m&1)+3 at column m/2, one 32-bit base and three
+// row-stride steps; plain: one float4.
+template <bool CHAIN_MAJOR>
+__device__ __forceinline__ void store_quad(const XView &xv, int m, const float (&v)[4]) {
+    if constexpr (CHAIN_MAJOR) {
+        float *xp = xv.x + (m & 1) * 4 * xv.stride + (m >> 1);
+        xp[0] = v[0];
+        xp[xv.stride] = v[1];
+        xp[2 * xv.stride] = v[2];
+        xp[3 * xv.stride] = v[3];
+    } else {
+        *(float4 *)(xv.x + 4 * m) = make_float4(v[0], v[1], v[2], v[3]);
+    }
+}
+
 // ------------------------------------------------------------- Q4_0 ----
 // Packed device layout of a Q4_0 row: groups of four Q4_0Blocks (128 weights,
 // 80 bytes, the file's own size), written once when the weights are uploaded:
@@ -414,33 +430,15 @@ __device__ __forceinline__ float finish_row(const GemvParams &p, const XView &xv
 // rms_norm's 1/rms over the chain-major LDS copy (norm.rs:52-88): lane l < 8
 // walks chain l (elements 8i + l), which is its own LDS row, reduces the eight
 // chains, and lane 0 stores 1/sqrt(ss/n + eps) in *inv_slot.  K % 32 == 0 here,
-// so there is no tail.  The caller synchronises before reading the slot.
+// so there is no tail.  The rows are zero past their K/8 values
+// (q4_zero_x_pad) for at least the rounding to 64 plus the chain's read-ahead,
+// and fma(0, 0, acc) leaves the chain unchanged (acc >= +0), so it runs over
+// the rounded length.  The caller synchronises before reading the slot.
 __device__ inline void rms_inv_chain_major(const XView &xv, int64_t K, float eps, float *inv_slot) {
     const int tid = threadIdx.x;
     if (tid >= 8) return;
-    const float *xl = xv.x + tid * xv.stride;
-    const int64_t n8 = K / 8;  // a multiple of 4
-    float acc = 0.0f;
-    int64_t i = 0;
-    for (; i + 16 <= n8; i += 16) {
-        float4 v[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] = *(const float4 *)(xl + i + 4 * u);
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            acc = fmaf(v[u].x, v[u].x, acc);
-            acc = fmaf(v[u].y, v[u].y, acc);
-            acc = fmaf(v[u].z, v[u].z, acc);
-            acc = fmaf(v[u].w, v[u].w, acc);
-        }
-    }
-    for (; i < n8; i += 4) {
-        const float4 v = *(const float4 *)(xl + i);
-        acc = fmaf(v.x, v.x, acc);
-        acc = fmaf(v.y, v.y, acc);
-        acc = fmaf(v.z, v.z, acc);
-        acc = fmaf(v.w, v.w, acc);
-    }
+    const int n8 = (int)(K / 8);
+    const float acc = chain_lds_sq(0.0f, xv.x + tid * xv.stride, (n8 + 63) & ~63);
     const float u = acc + __shfl(acc, (tid + 4) & 7, 8);  // lane l<4: a_l + a_{l+4}
     const float v = u + __shfl(u, (tid + 1) & 7, 8);      // lane 0: u0+u1, lane 2: u2+u3
     const float tot = v + __shfl(v, (tid + 2) & 7, 8);    // lane 0: (u0+u1) + (u2+u3)
@@ -566,10 +564,8 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
                 const int64_t m = m0 + u * THREADS + tid;
                 if (m < K4) {
                     const float4 v = xr[u];
-                    xv.at(4 * m) = v.x;
-                    xv.at(4 * m + 1) = v.y;
-                    xv.at(4 * m + 2) = v.z;
-                    xv.at(4 * m + 3) = v.w;
+                    const float q[4] = {v.x, v.y, v.z, v.w};
+                    store_quad<FMT == FMT_Q4_0>(xv, (int)m, q);
                     if (p.norm_w && !one_batch) *(float4 *)(nw + 4 * m) = wr[u];
                     bad_in |= isnan(v.x) | isnan(v.y) | isnan(v.z) | isnan(v.w);
                 }
@@ -606,9 +602,9 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
 #pragma unroll
                         for (int c = 0; c < 4; ++c) {
                             t[c] = t[c] * w4[c];  // (x * inv) * w, each product rounded
-                            xv.at(4 * m + c) = t[c];
                             bad |= isnan(t[c]);
                         }
+                        store_quad<FMT == FMT_Q4_0>(xv, (int)m, t);
                     }
                 }
             } else {
@@ -824,9 +820,10 @@ static int64_t gemv_x_floats(int64_t K, int fmt) {
 }
 
 size_t gemv_lds_bytes(int64_t K, int fmt, bool norm) {
-    // Q4_0: + the one group of inputs that the row walk reads ahead past the
-    // last chain row (never used)
-    const int64_t slack = fmt == FMT_Q4_0 ? 16 : 0;
+    // Q4_0: + what the reads ahead may touch past the last chain row: the row
+    // walk's next group (16 floats) and the sum-of-squares chain's read-ahead
+    // (up to 28 floats with the short ring); never used
+    const int64_t slack = fmt == FMT_Q4_0 ? 32 : 0;
     return (size_t)(gemv_x_floats(K, fmt) + (norm ? ((K + 3) & ~(int64_t)3) : 0) + slack) * 4;
 }
 
