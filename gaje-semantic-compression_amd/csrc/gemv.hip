@@ -772,6 +772,182 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
     }
 }
 
+// ------------------------------------------------- Q4_0, split waves ----
+// A matvec with too few rows to fill the chip is bound by the length of one
+// lane's instruction stream, and per element that stream is a byte-to-float
+// conversion, the dequantising fma and the chain's fma.  Here a workgroup
+// takes 8 rows and splits the work: wave 0 walks their 64 chains (lane 8r + l:
+// row r, chain l), reading the dequantised values from LDS, while waves 1..3
+// load and dequantise the weights one stage (SPLIT_SQ packed groups) ahead
+// into a double-buffered LDS ring, one barrier per stage.  The values and the
+// chain order are those of q4_consume, so the result is the same bit for bit.
+constexpr int SPLIT_ROWS = 8;                     // rows per workgroup
+constexpr int64_t SPLIT_MAX_ROWS = 4096;          // beyond this the row-per-lane kernel fills the chip
+constexpr int SPLIT_PQ = 2;                       // groups per producer wave and stage
+constexpr int SPLIT_SQ = 3 * SPLIT_PQ;            // groups per stage
+constexpr int SPLIT_DSTRIDE = 16 * SPLIT_SQ + 4;  // ring floats per chain lane (stride / 4 odd: no bank conflicts)
+
+__device__ __forceinline__ float q4_chain4(float acc, const float4 d, const float4 x) {
+    acc = fmaf(d.x, x.x, acc);
+    acc = fmaf(d.y, x.y, acc);
+    acc = fmaf(d.z, x.z, acc);
+    acc = fmaf(d.w, x.w, acc);
+    return acc;
+}
+
+// Epilogue of a STORE / RESIDUAL row pair (r1 = -1 if none), in its leader lane.
+__device__ __forceinline__ void store_pair(const GemvParams &p, const XView &xv, int64_t r0, int64_t r1, float v0,
+                                           float v1) {
+    DevState *st = p.st;
+    const float b0 = r0 < p.bias_len ? p.bias[r0] : 0.0f;
+    const float b1 = (r1 >= 0 && r1 < p.bias_len) ? p.bias[r1] : 0.0f;
+    const float y0 = finish_row(p, xv, r0, v0, b0);
+    const float y1 = r1 >= 0 ? finish_row(p, xv, r1, v1, b1) : 0.0f;
+    if (p.mode == MODE_STORE) {
+        p.y[r0] = y0;
+        if (r1 >= 0) p.y[r1] = y1;
+        return;
+    }
+    if (isnan(y0) || (r1 >= 0 && isnan(y1))) nan_flag(st, p.layer, p.st_a);
+    const float h0 = p.y[r0] + y0;
+    p.y[r0] = h0;
+    bool bad = isnan(h0);
+    if (r1 >= 0) {
+        const float h1 = p.y[r1] + y1;
+        p.y[r1] = h1;
+        bad |= isnan(h1);
+    }
+    if (bad) nan_flag(st, p.layer, p.st_b);
+}
+
+__global__ __launch_bounds__(THREADS) void gemv_q4_split_kernel(GemvParams p, int xstride) {
+    extern __shared__ __align__(16) float smem[];
+    __shared__ int or_in[THREADS / WAVE];
+    DevState *st = p.st;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t K4 = p.K >> 2;
+    const int nb = p.nb, G = (nb + 3) >> 2, nstage = (G + SPLIT_SQ - 1) / SPLIT_SQ;
+    const XView xv{smem, xstride};
+    float *ring = smem + 8 * xstride;  // [2][64 chain lanes][SPLIT_DSTRIDE]
+    const int r = lane >> 3, l = lane & 7;
+    const int64_t row = (int64_t)blockIdx.x * SPLIT_ROWS + r;
+    const bool row_ok = row < p.rows_valid;
+    const int halted = st ? st->halted : 0;
+
+    if (wave > 0) {
+        // ---- producers: wave 1 + pw dequantises groups pw*PQ .. pw*PQ + PQ-1
+        // of every stage for the 64 chain lanes; loads run two stages ahead ----
+        const int pw = wave - 1;
+        const uint8_t *wrow = (p.rows_valid > 0 ? p.w : kZeroRows) + (size_t)(row_ok ? row : 0) * G * 80;
+        vu2 an[SPLIT_PQ], bn[SPLIT_PQ];
+        vu4 as[SPLIT_PQ], bs[SPLIT_PQ];
+        auto load = [&](int stg, vu2(&n)[SPLIT_PQ], vu4(&sw)[SPLIT_PQ]) {
+#pragma unroll
+            for (int j = 0; j < SPLIT_PQ; ++j) {
+                int g = stg * SPLIT_SQ + pw * SPLIT_PQ + j;
+                g = g < G ? g : G - 1;  // groups past the row are never read by the chain
+                n[j] = ld_u2<false>(wrow + (size_t)g * 80 + 8 * l);
+                sw[j] = ld_u4<false>(wrow + (size_t)g * 80 + 64);
+            }
+        };
+        auto produce = [&](int buf, const vu2(&n)[SPLIT_PQ], const vu4(&sw)[SPLIT_PQ]) {
+            float *dst = ring + (buf * 64 + lane) * SPLIT_DSTRIDE + 16 * pw * SPLIT_PQ;
+#pragma unroll
+            for (int j = 0; j < SPLIT_PQ; ++j) {
+                float d[4][4];
+                q4_dequant(d[0], opaque_and(n[j].x, 0x0F0F0F0Fu), sw[j].x);
+                q4_dequant(d[1], opaque_and(n[j].x >> 4, 0x0F0F0F0Fu), sw[j].y);
+                q4_dequant(d[2], opaque_and(n[j].y, 0x0F0F0F0Fu), sw[j].z);
+                q4_dequant(d[3], opaque_and(n[j].y >> 4, 0x0F0F0F0Fu), sw[j].w);
+#pragma unroll
+                for (int b = 0; b < 4; ++b) *(float4 *)(dst + 16 * j + 4 * b) = make_float4(d[b][0], d[b][1], d[b][2], d[b][3]);
+            }
+        };
+        // Stages are produced in pairs with no branch around the loads (past
+        // the row they re-read its last group), so each wait is for the stage
+        // being dequantised alone; an odd stage count ends with one unused
+        // stage, matched by one extra barrier in wave 0.
+        load(0, an, as);
+        load(1, bn, bs);
+        if (halted) return;  // uniform
+        produce(0, an, as);
+        load(2, an, as);
+        barrier_or<THREADS / WAVE>(0, or_in);  // stage 0 ready (wave 0 reports the input's NaN)
+        produce(1, bn, bs);
+        load(3, bn, bs);
+        lds_barrier();
+        for (int s = 2; s < nstage; s += 2) {
+            produce(0, an, as);
+            load(s + 2, an, as);
+            lds_barrier();
+            produce(1, bn, bs);
+            load(s + 3, bn, bs);
+            lds_barrier();
+        }
+        return;  // wave 0 passes no further barrier
+    }
+
+    // ---- wave 0: activations -> chain-major LDS, then the 64 chains ----
+    if (halted) return;
+    const float4 *x4 = (const float4 *)p.x;
+    int bad_in = 0;
+    for (int64_t m0 = 0; m0 < K4; m0 += 8 * 64) {
+        float4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int64_t m = m0 + u * 64 + lane;
+            v[u] = x4[m < K4 ? m : K4 - 1];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int64_t m = m0 + u * 64 + lane;
+            if (m < K4) {
+                const float q[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+                store_quad<true>(xv, (int)m, q);
+                bad_in |= isnan(v[u].x) | isnan(v[u].y) | isnan(v[u].z) | isnan(v[u].w);
+            }
+        }
+    }
+    {  // inputs of the blocks past nb in the last group are zero (their values are)
+        const int pad = 16 * G - 4 * nb;
+        for (int t = lane; t < 8 * pad; t += 64) xv.x[(t / pad) * xstride + 4 * nb + t % pad] = 0.0f;
+    }
+    float acc = 0.0f;
+    const float *xg = xv.x + l * xstride;
+    const int nbar = (nstage + 1) & ~1;  // the producers' barriers (stages in pairs)
+    for (int s = 0; s < nbar; ++s) {
+        if (s == 0) {
+            if (barrier_or<THREADS / WAVE>(bad_in, or_in) && p.st_in >= 0 && lane == 0) nan_flag(st, p.layer, p.st_in);
+        } else {
+            lds_barrier();
+        }
+        if (s >= nstage) break;  // (the producers' unused last stage)
+        const float *dl = ring + ((s & 1) * 64 + lane) * SPLIT_DSTRIDE;
+#pragma unroll
+        for (int j = 0; j < SPLIT_SQ; ++j) {
+            const int g = s * SPLIT_SQ + j;
+            if (g < G) {
+                const X4 x = read_x4(xg + 16 * g);
+                const X4 d = read_x4(dl + 16 * j);
+                acc = q4_chain4(acc, d.b0, x.b0);
+                acc = q4_chain4(acc, d.b1, x.b1);
+                acc = q4_chain4(acc, d.b2, x.b2);
+                acc = q4_chain4(acc, d.b3, x.b3);
+            }
+        }
+    }
+    // lanes 8r..8r+7 hold row r's chains 0..7: the reduction of q4_consume
+    const int base = lane & ~7;
+    const float u = acc + shfl(acc, base + ((l + 4) & 7));
+    const float v = u + shfl(u, base + ((l + 2) & 7));
+    const float total = row_ok ? flush_small(v + shfl(v, base + ((l + 1) & 7))) : 0.0f;
+    const float v1 = shfl(total, (lane & ~15) + 8);  // the pair's second row (lane 16i + 8)
+    if ((lane & 15) == 0) {
+        const int64_t r0 = (int64_t)blockIdx.x * SPLIT_ROWS + (lane >> 3);
+        if (r0 < p.N) store_pair(p, xv, r0, r0 + 1 < p.N ? r0 + 1 : -1, total, v1);
+    }
+}
+
 using KernelFn = void (*)(GemvParams, int64_t, int, int);
 
 // LDS row stride (floats) of the chain-major activation copy: the floats the
@@ -817,6 +993,13 @@ static int64_t gemv_x_floats(int64_t K, int fmt) {
     int64_t f = (K + 3) & ~(int64_t)3;
     if (fmt == FMT_LUT4) f += (int64_t)(THREADS / 4) * 16;
     return f;
+}
+
+// LDS floats of the split-wave Q4_0 kernel: the chain-major activation rows
+// (every group's 16 inputs) and the two ring buffers.
+static int64_t split_lds_floats(int64_t K) {
+    const int64_t G = (K / 32 + 3) / 4;
+    return 8 * (16 * G + 4) + 2 * 64 * SPLIT_DSTRIDE;
 }
 
 size_t gemv_lds_bytes(int64_t K, int fmt, bool norm) {
@@ -872,6 +1055,18 @@ int launch_gemv(const GemvParams &p, hipStream_t s) {
             return set_error(GAJE_ERR_INVALID_ARG, "gemv: unknown mode %d", p.mode);
     }
     if (npairs == 0) return GAJE_OK;
+    // latency-bound Q4_0 matvecs (few rows) without a prologue: split waves
+    if (p.fmt == FMT_Q4_0 && (p.mode == MODE_STORE || p.mode == MODE_RESIDUAL) && !p.norm_w && !p.gnorm && !p.x_out &&
+        p.N <= SPLIT_MAX_ROWS && p.nb > 0) {
+        const size_t slds = (size_t)split_lds_floats(p.K) * 4;
+        if (slds + 1024 <= max_lds_per_block()) {
+            const int64_t grid = (p.N + SPLIT_ROWS - 1) / SPLIT_ROWS;
+            const int xs = (int)(16 * ((p.nb + 3) / 4) + 4);
+            hipLaunchKernelGGL(gemv_q4_split_kernel, dim3((unsigned)grid), dim3(THREADS), slds, s, p, xs);
+            GAJE_HIP_CHECK(hipGetLastError());
+            return GAJE_OK;
+        }
+    }
     KernelFn fn;
     int lpr;
     if (p.fmt == FMT_Q4_0) {
