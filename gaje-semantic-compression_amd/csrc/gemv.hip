@@ -139,9 +139,6 @@ __device__ __forceinline__ float q4_group(float acc, const vu2 n, const vu4 s, c
     acc = q4_chain(acc, d3, x.b3);
     return acc;
 }
-__device__ __forceinline__ float q4_group(float acc, const vu2 n, const vu4 s, const float *xg) {
-    return q4_group(acc, n, s, read_x4(xg));
-}
 
 // Register ring of D packed groups of one row (this lane's chain bytes and
 // the group's scale/min words).
@@ -448,6 +445,33 @@ __device__ inline void rms_inv_chain_major(const XView &xv, int64_t K, float eps
     }
 }
 
+// The fused QKV epilogue of a RoPE pair (attention.rs:62-82 with the
+// host-built cos/sin table): q and k get (v0*cos - v1*sin, v0*sin + v1*cos),
+// every product rounded; q goes to q_out, k and v to the cache at position pos.
+__device__ __forceinline__ void qkv_store(const GemvParams &p, int64_t r0, int64_t r1, float y0, float y1, float cs,
+                                          float sn, int pos) {
+    const float t0 = y0 * cs, t1 = y1 * sn, t2 = y0 * sn, t3 = y1 * cs;
+    const float o0 = t0 - t1, o1 = t2 + t3;
+    if (r0 < p.q_rows) {
+        p.q_out[r0] = o0;
+        p.q_out[r1] = o1;
+    } else if (r0 < p.q_rows + p.kv_rows) {
+        // K cache: [kv head][dim][position]
+        const int64_t kh = (r0 - p.q_rows) / p.head_dim;
+        const int64_t b = p.q_rows + kh * p.head_dim;
+        float *kc = p.k_cache + kh * p.kv_head_stride + pos;
+        kc[(r0 - b) * p.kv_cap] = o0;
+        kc[(r1 - b) * p.kv_cap] = o1;
+    } else {
+        // V cache: [kv head][dim][position]
+        const int64_t vh = (r0 - p.q_rows - p.kv_rows) / p.head_dim;
+        const int64_t b = p.q_rows + p.kv_rows + vh * p.head_dim;
+        float *vc = p.v_cache + vh * p.kv_head_stride + pos;
+        vc[(r0 - b) * p.kv_cap] = y0;
+        vc[(r1 - b) * p.kv_cap] = y1;
+    }
+}
+
 // Row pair -> its rows (r1 = -1 if none) and this lane's row.
 struct PairRows {
     int64_t r0, r1, row;
@@ -715,31 +739,9 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
                 if (bad) nan_flag(st, p.layer, p.st_b);
                 break;
             }
-            case MODE_QKV: {
-                // attention.rs:62-82 with the host-built cos/sin table:
-                // (v0*cos - v1*sin, v0*sin + v1*cos), every product rounded.
-                const float t0 = y0 * cs, t1 = y1 * sn, t2 = y0 * sn, t3 = y1 * cs;
-                const float o0 = t0 - t1, o1 = t2 + t3;
-                if (r0 < p.q_rows) {
-                    p.q_out[r0] = o0;
-                    p.q_out[r1] = o1;
-                } else if (r0 < p.q_rows + p.kv_rows) {
-                    // K cache: [kv head][dim][position]
-                    const int64_t kh = (r0 - p.q_rows) / p.head_dim;
-                    const int64_t b = p.q_rows + kh * p.head_dim;
-                    float *kc = p.k_cache + kh * p.kv_head_stride + pos;
-                    kc[(r0 - b) * p.kv_cap] = o0;
-                    kc[(r1 - b) * p.kv_cap] = o1;
-                } else {
-                    // V cache: [kv head][dim][position]
-                    const int64_t vh = (r0 - p.q_rows - p.kv_rows) / p.head_dim;
-                    const int64_t b = p.q_rows + p.kv_rows + vh * p.head_dim;
-                    float *vc = p.v_cache + vh * p.kv_head_stride + pos;
-                    vc[(r0 - b) * p.kv_cap] = y0;
-                    vc[(r1 - b) * p.kv_cap] = y1;
-                }
+            case MODE_QKV:
+                qkv_store(p, r0, r1, y0, y1, cs, sn, pos);
                 break;
-            }
             case MODE_SWIGLU: {
                 if (isnan(y1)) nan_flag(st, p.layer, p.st_a);
                 const float o = swiglu1(y0, y1, etab);
@@ -776,16 +778,30 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
 // A matvec with too few rows to fill the chip is bound by the length of one
 // lane's instruction stream, and per element that stream is a byte-to-float
 // conversion, the dequantising fma and the chain's fma.  Here a workgroup
-// takes 8 rows and splits the work: wave 0 walks their 64 chains (lane 8r + l:
-// row r, chain l), reading the dequantised values from LDS, while waves 1..3
+// takes 4 row pairs (8 rows) and splits the work: wave 0 walks their 64
+// chains (lanes 16i..16i+7: pair i's first row, 16i+8..16i+15 its second;
+// chain = lane % 8), reading the dequantised values from LDS, while waves 1..3
 // load and dequantise the weights one stage (SPLIT_SQ packed groups) ahead
-// into a double-buffered LDS ring, one barrier per stage.  The values and the
-// chain order are those of q4_consume, so the result is the same bit for bit.
-constexpr int SPLIT_ROWS = 8;                     // rows per workgroup
+// into a double-buffered LDS ring, one barrier per stage.  Wave 0 also runs
+// the prologue (the activations, their RMSNorm) and the epilogue.  The values
+// and the chain order are those of q4_consume, so the result is the same bit
+// for bit.
+constexpr int SPLIT_PAIRS = 4;                    // row pairs per workgroup
 constexpr int64_t SPLIT_MAX_ROWS = 4096;          // beyond this the row-per-lane kernel fills the chip
 constexpr int SPLIT_PQ = 2;                       // groups per producer wave and stage
 constexpr int SPLIT_SQ = 3 * SPLIT_PQ;            // groups per stage
 constexpr int SPLIT_DSTRIDE = 16 * SPLIT_SQ + 4;  // ring floats per chain lane (stride / 4 odd: no bank conflicts)
+constexpr int64_t SPLIT_NORM_MAX_K4 = 8 * 64;     // RMSNorm from wave 0's registers: one batch of 8 float4 per lane
+
+// Floats of a chain-major activation row in the split kernel: every group's 16
+// inputs and, for the RMSNorm's sum-of-squares chain, the rounding to 64 plus
+// its read-ahead of 32, all zero past the 4 nb values; a multiple of 8 (the
+// row stride, 4 more, is then an odd number of float4s).
+__host__ __device__ constexpr int split_xrow(int nb) {
+    const int g16 = 16 * ((nb + 3) / 4), sq = (4 * nb + 63) / 64 * 64 + 32;
+    const int m = g16 > sq ? g16 : sq;
+    return (m + 7) / 8 * 8;
+}
 
 __device__ __forceinline__ float q4_chain4(float acc, const float4 d, const float4 x) {
     acc = fmaf(d.x, x.x, acc);
@@ -795,50 +811,42 @@ __device__ __forceinline__ float q4_chain4(float acc, const float4 d, const floa
     return acc;
 }
 
-// Epilogue of a STORE / RESIDUAL row pair (r1 = -1 if none), in its leader lane.
-__device__ __forceinline__ void store_pair(const GemvParams &p, const XView &xv, int64_t r0, int64_t r1, float v0,
-                                           float v1) {
-    DevState *st = p.st;
-    const float b0 = r0 < p.bias_len ? p.bias[r0] : 0.0f;
-    const float b1 = (r1 >= 0 && r1 < p.bias_len) ? p.bias[r1] : 0.0f;
-    const float y0 = finish_row(p, xv, r0, v0, b0);
-    const float y1 = r1 >= 0 ? finish_row(p, xv, r1, v1, b1) : 0.0f;
-    if (p.mode == MODE_STORE) {
-        p.y[r0] = y0;
-        if (r1 >= 0) p.y[r1] = y1;
-        return;
-    }
-    if (isnan(y0) || (r1 >= 0 && isnan(y1))) nan_flag(st, p.layer, p.st_a);
-    const float h0 = p.y[r0] + y0;
-    p.y[r0] = h0;
-    bool bad = isnan(h0);
-    if (r1 >= 0) {
-        const float h1 = p.y[r1] + y1;
-        p.y[r1] = h1;
-        bad |= isnan(h1);
-    }
-    if (bad) nan_flag(st, p.layer, p.st_b);
-}
-
-__global__ __launch_bounds__(THREADS) void gemv_q4_split_kernel(GemvParams p, int xstride) {
+template <int MODE, bool NORM>
+__global__ __launch_bounds__(THREADS) void gemv_q4_split_kernel(GemvParams p, int64_t npairs, int xstride) {
     extern __shared__ __align__(16) float smem[];
-    __shared__ int or_in[THREADS / WAVE];
     DevState *st = p.st;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int64_t K4 = p.K >> 2;
+    const int64_t K = p.K, K4 = K >> 2;
     const int nb = p.nb, G = (nb + 3) >> 2, nstage = (G + SPLIT_SQ - 1) / SPLIT_SQ;
     const XView xv{smem, xstride};
     float *ring = smem + 8 * xstride;  // [2][64 chain lanes][SPLIT_DSTRIDE]
-    const int r = lane >> 3, l = lane & 7;
-    const int64_t row = (int64_t)blockIdx.x * SPLIT_ROWS + r;
-    const bool row_ok = row < p.rows_valid;
+    const int l = lane & 7;
+    const int64_t pr = (int64_t)blockIdx.x * SPLIT_PAIRS + (lane >> 4);
+    PairRows q;  // (locate, with the pairing of this kernel's mode only)
+    q.pair_ok = pr < npairs;
+    q.r0 = 0;
+    q.r1 = -1;
+    if (q.pair_ok) {
+        if constexpr (MODE == MODE_QKV) {
+            pair_rows(p, pr, q.r0, q.r1);
+        } else {
+            q.r0 = 2 * pr;
+            q.r1 = 2 * pr + 1 < p.N ? 2 * pr + 1 : -1;
+        }
+    }
+    q.row = ((lane >> 3) & 1) ? q.r1 : q.r0;
+    q.row_ok = q.pair_ok && q.row >= 0 && q.row < p.rows_valid;
     const int halted = st ? st->halted : 0;
 
     if (wave > 0) {
         // ---- producers: wave 1 + pw dequantises groups pw*PQ .. pw*PQ + PQ-1
-        // of every stage for the 64 chain lanes; loads run two stages ahead ----
+        // of every stage for the 64 chain lanes; loads run two stages ahead.
+        // Stages are produced in pairs with no branch around the loads (past
+        // the row they re-read its last group), so each wait is for the stage
+        // being dequantised alone; an odd stage count ends with one unused
+        // stage, matched by one extra barrier in wave 0 ----
         const int pw = wave - 1;
-        const uint8_t *wrow = (p.rows_valid > 0 ? p.w : kZeroRows) + (size_t)(row_ok ? row : 0) * G * 80;
+        const uint8_t *wrow = (p.rows_valid > 0 ? p.w : kZeroRows) + (size_t)(q.row_ok ? q.row : 0) * G * 80;
         vu2 an[SPLIT_PQ], bn[SPLIT_PQ];
         vu4 as[SPLIT_PQ], bs[SPLIT_PQ];
         auto load = [&](int stg, vu2(&n)[SPLIT_PQ], vu4(&sw)[SPLIT_PQ]) {
@@ -863,20 +871,10 @@ __global__ __launch_bounds__(THREADS) void gemv_q4_split_kernel(GemvParams p, in
                 for (int b = 0; b < 4; ++b) *(float4 *)(dst + 16 * j + 4 * b) = make_float4(d[b][0], d[b][1], d[b][2], d[b][3]);
             }
         };
-        // Stages are produced in pairs with no branch around the loads (past
-        // the row they re-read its last group), so each wait is for the stage
-        // being dequantised alone; an odd stage count ends with one unused
-        // stage, matched by one extra barrier in wave 0.
         load(0, an, as);
         load(1, bn, bs);
         if (halted) return;  // uniform
-        produce(0, an, as);
-        load(2, an, as);
-        barrier_or<THREADS / WAVE>(0, or_in);  // stage 0 ready (wave 0 reports the input's NaN)
-        produce(1, bn, bs);
-        load(3, bn, bs);
-        lds_barrier();
-        for (int s = 2; s < nstage; s += 2) {
+        for (int s = 0; s < nstage; s += 2) {
             produce(0, an, as);
             load(s + 2, an, as);
             lds_barrier();
@@ -887,40 +885,95 @@ __global__ __launch_bounds__(THREADS) void gemv_q4_split_kernel(GemvParams p, in
         return;  // wave 0 passes no further barrier
     }
 
-    // ---- wave 0: activations -> chain-major LDS, then the 64 chains ----
+    // ---- wave 0 ----
     if (halted) return;
+    // activations -> chain-major LDS (batches of 8 float4 per lane); with a
+    // norm the vector is one batch and stays in registers for the normalising
+    const bool leader = q.pair_ok && (lane & 15) == 0;
+    float b0 = 0.0f, b1 = 0.0f, old0 = 0.0f, old1 = 0.0f, cs = 0.0f, sn = 0.0f;
+    int pos = 0;
     const float4 *x4 = (const float4 *)p.x;
+    const float4 *w4 = (const float4 *)p.norm_w;  // non-null exactly when NORM
     int bad_in = 0;
+    float4 v[8], w[NORM ? 8 : 1];
     for (int64_t m0 = 0; m0 < K4; m0 += 8 * 64) {
-        float4 v[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
             const int64_t m = m0 + u * 64 + lane;
             v[u] = x4[m < K4 ? m : K4 - 1];
         }
+        if constexpr (NORM) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int64_t m = m0 + u * 64 + lane;
+                w[u] = w4[m < K4 ? m : K4 - 1];
+            }
+        }
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
             const int64_t m = m0 + u * 64 + lane;
             if (m < K4) {
-                const float q[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
-                store_quad<true>(xv, (int)m, q);
+                const float qd[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+                store_quad<true>(xv, (int)m, qd);
                 bad_in |= isnan(v[u].x) | isnan(v[u].y) | isnan(v[u].z) | isnan(v[u].w);
             }
         }
     }
-    {  // inputs of the blocks past nb in the last group are zero (their values are)
-        const int pad = 16 * G - 4 * nb;
-        for (int t = lane; t < 8 * pad; t += 64) xv.x[(t / pad) * xstride + 4 * nb + t % pad] = 0.0f;
+    // the epilogue operands, loaded while the chains run (once the
+    // activations are in: a load issued before them would hold up their use)
+    if (leader) {
+        if (q.r0 < p.bias_len) b0 = p.bias[q.r0];
+        if (q.r1 >= 0 && q.r1 < p.bias_len) b1 = p.bias[q.r1];
+        if constexpr (MODE == MODE_RESIDUAL) {
+            old0 = p.y[q.r0];
+            if (q.r1 >= 0) old1 = p.y[q.r1];
+        } else if constexpr (MODE == MODE_QKV) {
+            pos = st->pos;
+            const int hh = p.head_dim >> 1;
+            const int i = (int)(pr % hh);
+            cs = p.rope_cos[(size_t)pos * hh + i];
+            sn = p.rope_sin[(size_t)pos * hh + i];
+        }
     }
+    {  // zero past the 4 nb values of each chain row: the partial last group's
+       // inputs and, with a norm, the sum-of-squares chain's range (split_xrow)
+        const int from = 4 * nb, to = NORM ? xstride - 4 : 16 * G;  // from and to are multiples of 4
+        for (int c = from + 4 * (lane & 7); c < to; c += 32)
+            *(float4 *)(xv.x + (lane >> 3) * xstride + c) = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    if (__any(bad_in) && p.st_in >= 0 && lane == 0) nan_flag(st, p.layer, p.st_in);
+    if constexpr (NORM) {
+        // rms_norm (norm.rs:52-88): the eight chains of the chain-major rows,
+        // then (x * inv) * w from the registers, each product rounded
+        float ss = 0.0f;
+        if (lane < 8) ss = chain_lds_sq(0.0f, xv.x + lane * xstride, (4 * nb + 63) & ~63);
+        const float u1 = ss + __shfl(ss, (lane + 4) & 7, 8);
+        const float u2 = u1 + __shfl(u1, (lane + 1) & 7, 8);
+        const float tot = u2 + __shfl(u2, (lane + 2) & 7, 8);
+        const float inv = __shfl(1.0f / sqrtf(tot / (float)K + p.eps), 0, WAVE);
+        int bad = 0;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int64_t m = u * 64 + lane;
+            if (m < K4) {
+                float t[4] = {v[u].x * inv, v[u].y * inv, v[u].z * inv, v[u].w * inv};
+                const float wn[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    t[c] = t[c] * wn[c];
+                    bad |= isnan(t[c]);
+                }
+                store_quad<true>(xv, (int)m, t);
+            }
+        }
+        if (__any(bad) && p.st_norm >= 0 && lane == 0) nan_flag(st, p.layer, p.st_norm);
+    }
+    // the 64 chains, one stage per barrier
     float acc = 0.0f;
     const float *xg = xv.x + l * xstride;
     const int nbar = (nstage + 1) & ~1;  // the producers' barriers (stages in pairs)
     for (int s = 0; s < nbar; ++s) {
-        if (s == 0) {
-            if (barrier_or<THREADS / WAVE>(bad_in, or_in) && p.st_in >= 0 && lane == 0) nan_flag(st, p.layer, p.st_in);
-        } else {
-            lds_barrier();
-        }
+        lds_barrier();
         if (s >= nstage) break;  // (the producers' unused last stage)
         const float *dl = ring + ((s & 1) * 64 + lane) * SPLIT_DSTRIDE;
 #pragma unroll
@@ -936,15 +989,32 @@ __global__ __launch_bounds__(THREADS) void gemv_q4_split_kernel(GemvParams p, in
             }
         }
     }
-    // lanes 8r..8r+7 hold row r's chains 0..7: the reduction of q4_consume
+    // lanes 8r..8r+7 hold a row's chains 0..7: the reduction of q4_consume
     const int base = lane & ~7;
     const float u = acc + shfl(acc, base + ((l + 4) & 7));
-    const float v = u + shfl(u, base + ((l + 2) & 7));
-    const float total = row_ok ? flush_small(v + shfl(v, base + ((l + 1) & 7))) : 0.0f;
-    const float v1 = shfl(total, (lane & ~15) + 8);  // the pair's second row (lane 16i + 8)
-    if ((lane & 15) == 0) {
-        const int64_t r0 = (int64_t)blockIdx.x * SPLIT_ROWS + (lane >> 3);
-        if (r0 < p.N) store_pair(p, xv, r0, r0 + 1 < p.N ? r0 + 1 : -1, total, v1);
+    const float vv = u + shfl(u, base + ((l + 2) & 7));
+    const float total = q.row_ok ? flush_small(vv + shfl(vv, base + ((l + 1) & 7))) : 0.0f;
+    const float v1 = shfl(total, (lane & ~15) + 8);  // the pair's second row
+    if (!leader) return;
+    const int64_t r0 = q.r0, r1 = q.r1;
+    const float y0 = finish_row(p, xv, r0, total, b0);
+    const float y1 = r1 >= 0 ? finish_row(p, xv, r1, v1, b1) : 0.0f;
+    if constexpr (MODE == MODE_STORE) {
+        p.y[r0] = y0;
+        if (r1 >= 0) p.y[r1] = y1;
+    } else if constexpr (MODE == MODE_RESIDUAL) {
+        if (isnan(y0) || (r1 >= 0 && isnan(y1))) nan_flag(st, p.layer, p.st_a);
+        const float h0 = old0 + y0;
+        p.y[r0] = h0;
+        bool bad = isnan(h0);
+        if (r1 >= 0) {
+            const float h1 = old1 + y1;
+            p.y[r1] = h1;
+            bad |= isnan(h1);
+        }
+        if (bad) nan_flag(st, p.layer, p.st_b);
+    } else {
+        qkv_store(p, r0, r1, y0, y1, cs, sn, pos);
     }
 }
 
@@ -996,11 +1066,9 @@ static int64_t gemv_x_floats(int64_t K, int fmt) {
 }
 
 // LDS floats of the split-wave Q4_0 kernel: the chain-major activation rows
-// (every group's 16 inputs) and the two ring buffers.
-static int64_t split_lds_floats(int64_t K) {
-    const int64_t G = (K / 32 + 3) / 4;
-    return 8 * (16 * G + 4) + 2 * 64 * SPLIT_DSTRIDE;
-}
+// (split_xrow + 4 floats each; the sum-of-squares chain's read-ahead ends in
+// the row) and the two ring buffers.
+static int64_t split_lds_floats(int64_t K) { return 8 * ((int64_t)split_xrow((int)(K / 32)) + 4) + 2 * 64 * SPLIT_DSTRIDE; }
 
 size_t gemv_lds_bytes(int64_t K, int fmt, bool norm) {
     // Q4_0: + what the reads ahead may touch past the last chain row: the row
@@ -1055,14 +1123,18 @@ int launch_gemv(const GemvParams &p, hipStream_t s) {
             return set_error(GAJE_ERR_INVALID_ARG, "gemv: unknown mode %d", p.mode);
     }
     if (npairs == 0) return GAJE_OK;
-    // latency-bound Q4_0 matvecs (few rows) without a prologue: split waves
-    if (p.fmt == FMT_Q4_0 && (p.mode == MODE_STORE || p.mode == MODE_RESIDUAL) && !p.norm_w && !p.gnorm && !p.x_out &&
-        p.N <= SPLIT_MAX_ROWS && p.nb > 0) {
+    // latency-bound Q4_0 matvecs (few rows): split waves
+    if (p.fmt == FMT_Q4_0 && (p.mode == MODE_STORE || p.mode == MODE_RESIDUAL || p.mode == MODE_QKV) && !p.gnorm &&
+        !p.x_out && 2 * npairs <= SPLIT_MAX_ROWS && p.nb > 0 && (!p.norm_w || p.K / 4 <= SPLIT_NORM_MAX_K4)) {
         const size_t slds = (size_t)split_lds_floats(p.K) * 4;
         if (slds + 1024 <= max_lds_per_block()) {
-            const int64_t grid = (p.N + SPLIT_ROWS - 1) / SPLIT_ROWS;
-            const int xs = (int)(16 * ((p.nb + 3) / 4) + 4);
-            hipLaunchKernelGGL(gemv_q4_split_kernel, dim3((unsigned)grid), dim3(THREADS), slds, s, p, xs);
+            const int64_t grid = (npairs + SPLIT_PAIRS - 1) / SPLIT_PAIRS;
+            const int xs = split_xrow(p.nb) + 4;
+            void (*fn)(GemvParams, int64_t, int);
+            if (p.mode == MODE_QKV) fn = p.norm_w ? gemv_q4_split_kernel<MODE_QKV, true> : gemv_q4_split_kernel<MODE_QKV, false>;
+            else if (p.mode == MODE_RESIDUAL) fn = p.norm_w ? gemv_q4_split_kernel<MODE_RESIDUAL, true> : gemv_q4_split_kernel<MODE_RESIDUAL, false>;
+            else fn = p.norm_w ? gemv_q4_split_kernel<MODE_STORE, true> : gemv_q4_split_kernel<MODE_STORE, false>;
+            hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(THREADS), slds, s, p, npairs, xs);
             GAJE_HIP_CHECK(hipGetLastError());
             return GAJE_OK;
         }
