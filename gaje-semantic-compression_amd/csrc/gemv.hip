@@ -42,8 +42,8 @@ constexpr int MAX_GRID = 8192;
 __device__ __align__(256) uint8_t kZeroRows[65536];
 constexpr int Q4_PREFETCH = 8;  // packed groups (4 blocks each) in flight per lane, short rows
 
-__device__ __forceinline__ void pair_rows(const GemvParams &p, int64_t pr, int64_t &r0, int64_t &r1) {
-    if (p.mode == MODE_QKV) {
+__device__ __forceinline__ void pair_rows(const GemvParams &p, int mode, int64_t pr, int64_t &r0, int64_t &r1) {
+    if (mode == MODE_QKV) {
         const int half = p.head_dim >> 1;
         const int64_t head = pr / half;
         const int64_t i = pr - head * half;
@@ -54,7 +54,7 @@ __device__ __forceinline__ void pair_rows(const GemvParams &p, int64_t pr, int64
             r0 = head * p.head_dim + 2 * i;
             r1 = r0 + 1;
         }
-    } else if (p.mode == MODE_SWIGLU) {
+    } else if (mode == MODE_SWIGLU) {
         r0 = pr;
         r1 = pr + p.ffn;
     } else {
@@ -479,25 +479,28 @@ struct PairRows {
 };
 
 template <int FMT>
-__device__ __forceinline__ PairRows locate(const GemvParams &p, int64_t pr, int64_t npairs, int half) {
+__device__ __forceinline__ PairRows locate(const GemvParams &p, int mode, int64_t pr, int64_t npairs, int half) {
     PairRows q;
     q.pair_ok = pr < npairs;
     q.r0 = 0;
     q.r1 = -1;
-    if (q.pair_ok) pair_rows(p, pr, q.r0, q.r1);
+    if (q.pair_ok) pair_rows(p, mode, pr, q.r0, q.r1);
     q.row = half ? q.r1 : q.r0;
     const bool has_work = (FMT == FMT_F32) ? p.K > 0 : p.nb > 0;
     q.row_ok = q.pair_ok && q.row >= 0 && q.row < p.rows_valid && has_work;
     return q;
 }
 
-template <int FMT, int LPR, bool NT, int D>
+// MODE >= 0 specialises the kernel to one epilogue (a smaller kernel, whose
+// instructions are fetched cold at every launch); -1 reads p.mode.
+template <int FMT, int LPR, bool NT, int D, int MODE = -1>
 __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npairs, int xstride, int nw_off) {
     extern __shared__ __align__(16) float smem[];
     __shared__ float inv_slot;
     __shared__ uint64_t etab[32];  // SwiGLU: the exponential's table, read from LDS
     __shared__ int or_in[THREADS / WAVE], or_norm[THREADS / WAVE];  // barrier_or slots
     DevState *st = p.st;
+    const int mode = MODE >= 0 ? MODE : p.mode;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t K = p.K;
@@ -514,11 +517,11 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
     float *tbl = smem + ((K + 3) & ~(int64_t)3) + (size_t)(tid / LPR) * 16;  // LUT slot of this row group
 
     int64_t pr0 = (int64_t)blockIdx.x * pairs_per_block;
-    PairRows q = locate<FMT>(p, pr0 + wave * PAIRS_PER_WAVE + pslot, npairs, half);
+    PairRows q = locate<FMT>(p, mode, pr0 + wave * PAIRS_PER_WAVE + pslot, npairs, half);
     Q4Ring<D> q4r;
     F32Ring f32r;
     const int halted = st ? st->halted : 0;
-    const bool swiglu = p.mode == MODE_SWIGLU;
+    const bool swiglu = mode == MODE_SWIGLU;
     const uint64_t tabv = swiglu && tid < 32 ? kExp2Tab[tid] : 0;
 
     // ---- prologue: activation vector (and the norm weights) into LDS, one
@@ -683,7 +686,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
     for (bool first = true; pr0 < npairs; pr0 += (int64_t)gridDim.x * pairs_per_block, first = false) {
         const int64_t pr = pr0 + wave * PAIRS_PER_WAVE + pslot;
         if (!first) {
-            q = locate<FMT>(p, pr, npairs, half);
+            q = locate<FMT>(p, mode, pr, npairs, half);
             if (q.row_ok) {
                 if constexpr (FMT == FMT_Q4_0) q4_prefetch<NT, D>(p.w, p, q.row, s, q4r);
                 else if constexpr (FMT == FMT_F32) f32_prefetch<NT>(p.w, p, q.row, s, f32r);
@@ -697,10 +700,10 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
         if (leader) {
             if (r0 < p.bias_len) b0 = p.bias[r0];
             if (r1 >= 0 && r1 < p.bias_len) b1 = p.bias[r1];
-            if (p.mode == MODE_RESIDUAL) {
+            if (mode == MODE_RESIDUAL) {
                 old0 = p.y[r0];
                 if (r1 >= 0) old1 = p.y[r1];
-            } else if (p.mode == MODE_QKV) {
+            } else if (mode == MODE_QKV) {
                 pos = st->pos;
                 const int i = (int)(pr % hh);
                 cs = p.rope_cos[(size_t)pos * hh + i];
@@ -721,7 +724,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
         // ---- epilogue (one lane per row pair) ----
         const float y0 = finish_row(p, xv, r0, v, b0);
         const float y1 = r1 >= 0 ? finish_row(p, xv, r1, v1, b1) : 0.0f;
-        switch (p.mode) {
+        switch (mode) {
             case MODE_STORE:
                 p.y[r0] = y0;
                 if (r1 >= 0) p.y[r1] = y1;
@@ -760,7 +763,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
             }
         }
     }
-    if (p.mode == MODE_ARGMAX && st) {
+    if (mode == MODE_ARGMAX && st) {
         unsigned long long key =
             best_v > -INFINITY
                 ? ((unsigned long long)order_key(best_v) << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)best_i)
@@ -828,7 +831,7 @@ __global__ __launch_bounds__(THREADS) void gemv_q4_split_kernel(GemvParams p, in
     q.r1 = -1;
     if (q.pair_ok) {
         if constexpr (MODE == MODE_QKV) {
-            pair_rows(p, pr, q.r0, q.r1);
+            pair_rows(p, MODE_QKV, pr, q.r0, q.r1);
         } else {
             q.r0 = 2 * pr;
             q.r1 = 2 * pr + 1 < p.N ? 2 * pr + 1 : -1;
@@ -1147,6 +1150,8 @@ int launch_gemv(const GemvParams &p, hipStream_t s) {
         if (long_rows)
             fn = p.nontemporal ? gemv_kernel<FMT_Q4_0, 8, true, 2 * Q4_PREFETCH>
                                : gemv_kernel<FMT_Q4_0, 8, false, 2 * Q4_PREFETCH>;
+        else if (p.mode == MODE_SWIGLU && !p.nontemporal)
+            fn = gemv_kernel<FMT_Q4_0, 8, false, Q4_PREFETCH, MODE_SWIGLU>;
         else
             fn = p.nontemporal ? gemv_kernel<FMT_Q4_0, 8, true, Q4_PREFETCH> : gemv_kernel<FMT_Q4_0, 8, false, Q4_PREFETCH>;
     } else if (p.fmt == FMT_LUT4) {
@@ -1154,7 +1159,8 @@ int launch_gemv(const GemvParams &p, hipStream_t s) {
         fn = gemv_kernel<FMT_LUT4, 4, false, 1>;
     } else {
         lpr = 2;
-        fn = p.nontemporal ? gemv_kernel<FMT_F32, 2, true, 1> : gemv_kernel<FMT_F32, 2, false, 1>;
+        if (p.mode == MODE_ARGMAX && p.nontemporal) fn = gemv_kernel<FMT_F32, 2, true, 1, MODE_ARGMAX>;
+        else fn = p.nontemporal ? gemv_kernel<FMT_F32, 2, true, 1> : gemv_kernel<FMT_F32, 2, false, 1>;
     }
     const int64_t pairs_per_block = (WAVE / (2 * lpr)) * (THREADS / WAVE);
     int64_t grid = (npairs + pairs_per_block - 1) / pairs_per_block;
