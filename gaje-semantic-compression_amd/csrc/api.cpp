@@ -235,6 +235,86 @@ extern "C" int gaje_hip_q4_0_gemm(const void *packed, const float *X, const floa
     return GAJE_OK;
 }
 
+namespace {
+
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// Workspace of gaje_hip_q4_0_gemm_mfma: weight row exponents, activation row
+// exponents, the two f16 activation planes, split-K partials.
+struct GemmWorkspace {
+    int *ew, *ex;
+    uint16_t *xh, *xl;
+    float *part;
+    size_t bytes;
+};
+
+GemmWorkspace gemm_workspace(char *base, int64_t m, int64_t n, int64_t k, const GemmPlan &pl) {
+    GemmWorkspace w{};
+    size_t off = 0;
+    w.ew = (int *)(base + off);
+    off = align256(off + (size_t)n * 4);
+    w.ex = (int *)(base + off);
+    off = align256(off + (size_t)m * 4);
+    w.xh = (uint16_t *)(base + off);
+    off = align256(off + (size_t)m * k * 2);
+    w.xl = (uint16_t *)(base + off);
+    off = align256(off + (size_t)m * k * 2);
+    w.part = (float *)(base + off);
+    off = align256(off + (size_t)pl.part_floats * 4);
+    w.bytes = off;
+    return w;
+}
+
+}  // namespace
+
+extern "C" int64_t gaje_hip_q4_0_gemm_mfma_workspace(int64_t m, int64_t n, int64_t k) {
+    if (m < 0 || n <= 0 || k <= 0 || k % 32 != 0) return -1;
+    if (m == 0) return 0;
+    return (int64_t)gemm_workspace(nullptr, m, n, k, plan_gemm_q4(m, n, k)).bytes;
+}
+
+extern "C" int gaje_hip_q4_0_gemm_mfma(const void *packed, const float *X, const float *bias, int64_t bias_len,
+                                       float *Y, int64_t m, int64_t n, int64_t k, void *workspace,
+                                       int64_t workspace_bytes, void *stream) {
+    GAJE_TRY(check_dims(n, k));
+    if (k % 32 || m < 0 || (m > 0 && (!X || !Y || !packed || !workspace)) || bias_len < 0 || (bias_len > 0 && !bias))
+        return set_error(GAJE_ERR_INVALID_ARG, "bad gemm arguments");
+    if (m == 0 || n == 0) return GAJE_OK;
+    const GemmPlan pl = plan_gemm_q4(m, n, k);
+    const GemmWorkspace w = gemm_workspace((char *)workspace, m, n, k, pl);
+    if ((int64_t)w.bytes > workspace_bytes)
+        return set_error(GAJE_ERR_INVALID_ARG, "gemm workspace of %lld bytes is smaller than the %zu needed",
+                         (long long)workspace_bytes, w.bytes);
+    hipStream_t s = as_stream(stream);
+    GAJE_TRY(launch_q4_row_exponents((const uint8_t *)packed, n, k, w.ew, s));
+    SplitParams sp{};
+    sp.x = X;
+    sp.ldx = k;
+    sp.xh = w.xh;
+    sp.xl = w.xl;
+    sp.ldh = k;
+    sp.ex = w.ex;
+    sp.M = m;
+    sp.K = k;
+    GAJE_TRY(launch_split_rows(sp, s));
+    GemmQ4Params p{};
+    p.w = (const uint8_t *)packed;
+    p.ew = w.ew;
+    p.xh = w.xh;
+    p.xl = w.xl;
+    p.ex = w.ex;
+    p.ldh = k;
+    p.bias = bias;
+    p.bias_len = bias_len;
+    p.y = Y;
+    p.ldy = n;
+    p.part = w.part;
+    p.M = m;
+    p.N = n;
+    p.nb = (int32_t)(k / 32);
+    return launch_gemm_q4(p, pl, s);
+}
+
 extern "C" int gaje_hip_lut4_gemv(const uint8_t *codes, const float *lut, int64_t lut_len, const float *x,
                                   const float *bias, int64_t bias_len, float *y, int64_t n, int64_t k, void *stream) {
     GAJE_TRY(check_dims(n, k));

@@ -1,0 +1,373 @@
+// Q4_0 x FP32 matrix products on the MFMA units (prompt prefill, expert FFNs).
+//
+// Y[m][n] = sum_k X[m][k] W[n][k] with W the Q4_0 rows of GenomicLinear
+// (d = fma(q, scale, min), blocks.rs:18-30 / genomic.rs:298-316) and X fp32.
+// The reference has no matrix product: it runs compute_single_row
+// (linear/forward.rs:11-117) once per activation row.  The result here is the
+// same dot product to fp32 accuracy, not the same bits.
+//
+// Precision.  One f16 MFMA operand carries 11 significant bits, which puts a
+// matvec 0.1 away from the reference under the floored relative metric; so
+// both operands are split into an f16 pair, v = hi + lo with
+// hi = f16(v') and lo = f16(v' - hi), v' = v * 2^e (e a power-of-two scale
+// per activation row and per weight row that puts the row's largest magnitude
+// in [2^14, 2^15), away from f16 overflow and from subnormal lo parts).  Three
+// products hi*hi + hi*lo + lo*hi, accumulated in fp32 by the MFMA, carry
+// about 22 bits per term; the dropped lo*lo term is 2^-22 relative.  The
+// epilogue multiplies by 2^-(e_x + e_w) (exact).
+//
+// Tiling (gfx950, wave64).  A workgroup owns MT activation rows x 128 weight
+// rows; its waves are (MT/64) x 2, each holding a 64 x 64 tile as 4 x 4
+// accumulators of v_mfma_f32_16x16x32_f16 (K = 32 = one Q4_0 block per
+// step).  Per block the workgroup stages both activation planes and the
+// dequantised weight planes into LDS (double-buffered, one barrier per block);
+// weights are dequantised once per workgroup and shared by all its waves.
+// Rows of a tile in LDS are 80 bytes apart (32 halves + 8 pad), so the
+// 16-byte fragment reads of 16 consecutive rows fall in distinct banks.
+// Split-K over blocks fills the device when there are few output tiles; the
+// partial products are summed in a fixed order by gemm_reduce_kernel.
+#include <hip/hip_runtime.h>
+
+#include "common.h"
+#include "device_util.h"
+#include "kernels.h"
+
+namespace gaje {
+namespace {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+constexpr int GM_NT = 128;   // weight rows per workgroup
+constexpr int GM_ROW = 40;   // halves per LDS tile row (32 + 8 pad)
+
+// e such that maxabs * 2^e lies in [2^14, 2^15); 0 when maxabs is 0 or not finite.
+__device__ __forceinline__ int split_exponent(float maxabs) {
+    if (!(maxabs > 0.0f) || !(maxabs <= 3.402823466e38f)) return 0;
+    int e;
+    (void)frexpf(maxabs, &e);  // maxabs = f * 2^e, f in [0.5, 1)
+    return 15 - e;
+}
+
+// Per weight row: the exponent of its largest |d| = max(|min|, |fma(15, scale, min)|)
+// over its blocks (d is affine in the code, so the extremes are codes 0 and 15).
+// One wave per row.
+__global__ __launch_bounds__(256) void q4_row_exp_kernel(const uint8_t *w, int64_t N, int nb, int *ew) {
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= N) return;
+    const int lane = threadIdx.x & 63;
+    const int G = (nb + 3) >> 2;
+    const uint8_t *rp = w + (size_t)row * G * 80;
+    float mx = 0.0f;
+    for (int b = lane; b < nb; b += 64) {
+        const uint32_t sm = *(const uint32_t *)(rp + (size_t)(b >> 2) * 80 + 64 + 4 * (b & 3));
+        const float s = half_lo(sm), m = half_hi(sm);
+        mx = fmaxf(mx, fmaxf(fabsf(m), fabsf(fmaf(15.0f, s, m))));
+    }
+    mx = wave_max(mx);
+    if (lane == 0) ew[row] = split_exponent(mx);
+}
+
+// One activation row per workgroup: optional rms_norm (norm.rs:52-88, the
+// reference's chain order), then the row's exponent and its f16 hi/lo planes.
+template <bool NORM>
+__global__ __launch_bounds__(256) void split_rows_kernel(SplitParams p) {
+    extern __shared__ __align__(16) float xs[];
+    __shared__ float red[4];
+    __shared__ float inv_slot;
+    const int64_t m = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int64_t K = p.K, K4 = K >> 2;
+    const float *xr = p.x + m * p.ldx;
+    for (int64_t i = tid; i < K4; i += 256) *(float4 *)(xs + 4 * i) = *(const float4 *)(xr + 4 * i);
+    __syncthreads();
+    if constexpr (NORM) {
+        rms_inv_plain(xs, K, p.eps, &inv_slot);
+        __syncthreads();
+        const float inv = inv_slot;
+        for (int64_t i = tid; i < K4; i += 256) {
+            float4 v = *(float4 *)(xs + 4 * i);
+            const float4 g = *(const float4 *)(p.norm_w + 4 * i);
+            v.x = (v.x * inv) * g.x;
+            v.y = (v.y * inv) * g.y;
+            v.z = (v.z * inv) * g.z;
+            v.w = (v.w * inv) * g.w;
+            *(float4 *)(xs + 4 * i) = v;
+        }
+        if (p.x_out) {  // the normalised row itself, for callers that keep it
+            for (int64_t i = tid; i < K4; i += 256) *(float4 *)(p.x_out + m * p.ldo + 4 * i) = *(float4 *)(xs + 4 * i);
+        }
+    }
+    float mx = 0.0f;
+    for (int64_t i = tid; i < K4; i += 256) {
+        const float4 v = *(const float4 *)(xs + 4 * i);
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+    mx = wave_max(mx);
+    if ((tid & 63) == 0) red[tid >> 6] = mx;
+    __syncthreads();
+    const int e = split_exponent(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+    if (tid == 0) p.ex[m] = e;
+    for (int64_t i = tid; i < K4; i += 256) {
+        const float4 v = *(const float4 *)(xs + 4 * i);
+        const float a[4] = {ldexpf(v.x, e), ldexpf(v.y, e), ldexpf(v.z, e), ldexpf(v.w, e)};
+        h4 hi, lo;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            hi[j] = (_Float16)a[j];
+            lo[j] = (_Float16)(a[j] - (float)hi[j]);
+        }
+        *(h4 *)((_Float16 *)p.xh + m * p.ldh + 4 * i) = hi;
+        *(h4 *)((_Float16 *)p.xl + m * p.ldh + 4 * i) = lo;
+    }
+}
+
+__device__ __forceinline__ uint32_t word_of(const vu4 (&wq)[4], int j) { return wq[j >> 2][j & 3]; }
+
+template <int MT>
+__global__ __launch_bounds__(MT * 2) void gemm_q4_mfma_kernel(GemmQ4Params p) {
+    constexpr int NTH = MT * 2;
+    constexpr int TPR = NTH / GM_NT;  // staging threads per weight row: 2 or 4
+    constexpr int CPT = 4 / TPR;      // 8-element chunks of a block per staging thread
+    constexpr int APL = MT * GM_ROW;  // halves per activation plane
+    constexpr int BPL = GM_NT * GM_ROW;
+    extern __shared__ __align__(16) _Float16 lds[];
+    _Float16 *As = lds;                // [buf][plane][MT][GM_ROW]
+    _Float16 *Bs = lds + 4 * APL;      // [buf][plane][GM_NT][GM_ROW]
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int64_t m0 = (int64_t)blockIdx.y * MT, n0 = (int64_t)blockIdx.x * GM_NT;
+    const int z = blockIdx.z;
+    const int b0 = z * p.kb_per;
+    const int b1 = min(p.nb, b0 + p.kb_per);
+    const int G = (p.nb + 3) >> 2;
+
+    // activation staging: row ar, 16 halves at column 16*ah of each plane
+    const int ar = tid >> 1, ah = tid & 1;
+    int64_t am = m0 + ar;
+    if (am >= p.M) am = p.M - 1;
+    const _Float16 *xhp = (const _Float16 *)p.xh + am * p.ldh + 16 * ah;
+    const _Float16 *xlp = (const _Float16 *)p.xl + am * p.ldh + 16 * ah;
+    // weight staging: row br, chunks c = bq*CPT .. of each block
+    const int br = tid / TPR, bq = tid % TPR;
+    int64_t bn = n0 + br;
+    if (bn >= p.N) bn = p.N - 1;
+    const uint8_t *wrow = p.w + (size_t)bn * G * 80;
+    const float wsc = ldexpf(1.0f, p.ew[bn]);
+
+    f4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = (f4){0.f, 0.f, 0.f, 0.f};
+
+    // two activation blocks and two weight groups in flight
+    vu4 xa[2][4];
+    vu4 wq[2][4], ws[2];
+    auto load_x = [&](int b, vu4 (&r)[4]) {
+        const int bb = b < b1 ? b : b1 - 1;  // clamped, so every load is in bounds
+        r[0] = *(const vu4 *)(xhp + 32 * bb);
+        r[1] = *(const vu4 *)(xhp + 32 * bb + 8);
+        r[2] = *(const vu4 *)(xlp + 32 * bb);
+        r[3] = *(const vu4 *)(xlp + 32 * bb + 8);
+    };
+    auto load_w = [&](int g, vu4 (&q)[4], vu4 &s) {
+        const int gg = g < G ? g : G - 1;
+        const uint8_t *gp = wrow + (size_t)gg * 80;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) q[i] = *(const vu4 *)(gp + 16 * i);
+        s = *(const vu4 *)(gp + 64);
+    };
+
+    const int g0 = b0 >> 2;  // b0 is a multiple of 4
+    const int g1 = (b1 + 3) >> 2;
+    load_w(g0, wq[0], ws[0]);
+    load_x(b0, xa[0]);
+    load_x(b0 + 1, xa[1]);
+    load_w(g0 + 1, wq[1], ws[1]);
+
+    const int fr = lane & 15, fk = 8 * (lane >> 4);
+    int buf = 0;
+    for (int g = g0; g < g1; ++g) {
+        const int wi = (g - g0) & 1;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            // Every group runs all four blocks, branch-free (a branch here makes
+            // the compiler wait for every load in flight).  Blocks past nb only
+            // occur in the last group: their packed codes, scales and mins are
+            // zero, and their activations are masked to zero here.
+            const int b = 4 * g + u;
+            const int xi = u & 1;
+            const uint32_t live = b < b1 ? 0xFFFFFFFFu : 0u;
+            // stage block b into LDS buffer buf
+            {
+                _Float16 *ad = As + buf * 2 * APL + ar * GM_ROW + 16 * ah;
+                *(vu4 *)ad = xa[xi][0] & live;
+                *(vu4 *)(ad + 8) = xa[xi][1] & live;
+                *(vu4 *)(ad + APL) = xa[xi][2] & live;
+                *(vu4 *)(ad + APL + 8) = xa[xi][3] & live;
+                const uint32_t smw = ws[wi][u];
+                const float s = half_lo(smw), mn = half_hi(smw);
+                const int hb = u >> 1;
+                const int sh = 4 * (u & 1);
+#pragma unroll
+                for (int cc = 0; cc < CPT; ++cc) {
+                    const int c = bq * CPT + cc;
+                    h8 hi, lo;
+#pragma unroll
+                    for (int l = 0; l < 8; ++l) {
+                        const uint32_t code = (word_of(wq[wi], 2 * l + hb) >> (8 * c + sh)) & 0xFu;
+                        const float d = fmaf((float)code, s, mn) * wsc;
+                        hi[l] = (_Float16)d;
+                        lo[l] = (_Float16)(d - (float)hi[l]);
+                    }
+                    _Float16 *bd = Bs + buf * 2 * BPL + br * GM_ROW + 8 * c;
+                    *(h8 *)bd = hi;
+                    *(h8 *)(bd + BPL) = lo;
+                }
+            }
+            // refill: activations two blocks ahead; the next-but-one weight group
+            load_x(b + 2, xa[xi]);
+            if (u == 3) load_w(g + 2, wq[wi], ws[wi]);
+            lds_barrier();
+            // 4 x 4 tiles x 3 products from buffer buf
+            const _Float16 *Ab = As + buf * 2 * APL + (wm * 64 + fr) * GM_ROW + fk;
+            const _Float16 *Bb = Bs + buf * 2 * BPL + (wn * 64 + fr) * GM_ROW + fk;
+            h8 ahi[4], alo[4], bhi[4], blo[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                ahi[i] = *(const h8 *)(Ab + 16 * i * GM_ROW);
+                alo[i] = *(const h8 *)(Ab + 16 * i * GM_ROW + APL);
+                bhi[i] = *(const h8 *)(Bb + 16 * i * GM_ROW);
+                blo[i] = *(const h8 *)(Bb + 16 * i * GM_ROW + BPL);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[i], bhi[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[i], blo[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[i], bhi[j], acc[i][j], 0, 0, 0);
+            buf ^= 1;
+        }
+    }
+
+    // epilogue: lane holds rows 4*(lane>>4)+r, column lane&15 of each 16x16 tile
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t n = n0 + wn * 64 + 16 * j + fr;
+        if (n >= p.N) continue;
+        const int en = p.ew[n];
+        const float bias = (!p.part && n < p.bias_len) ? p.bias[n] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t m = m0 + wm * 64 + 16 * i + 4 * (lane >> 4) + r;
+                if (m >= p.M) continue;
+                float v = ldexpf(acc[i][j][r], -(p.ex[m] + en));
+                if (p.part) {
+                    p.part[((int64_t)z * p.M + m) * p.N + n] = v;
+                } else {
+                    v = flush_small(v);
+                    if (n < p.bias_len) v = v + bias;
+                    if (p.resid) v = p.resid[m * p.ldr + n] + v;
+                    p.y[m * p.ldy + n] = v;
+                }
+            }
+        }
+    }
+}
+
+// Sums the split-K partials in split order, then the row epilogue of
+// compute_single_row: flush, + bias; + residual (block/forward.rs:70-72,131-133).
+__global__ void gemm_reduce_kernel(GemmQ4Params p, int S) {
+    const int64_t total = p.M * p.N;
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t m = t / p.N, n = t - m * p.N;
+        float v = p.part[t];
+        for (int z = 1; z < S; ++z) v += p.part[(int64_t)z * total + t];
+        v = flush_small(v);
+        if (n < p.bias_len) v = v + p.bias[n];
+        if (p.resid) v = p.resid[m * p.ldr + n] + v;
+        p.y[m * p.ldy + n] = v;
+    }
+}
+
+template <int MT>
+size_t gemm_lds() { return (size_t)(4 * MT * GM_ROW + 4 * GM_NT * GM_ROW) * sizeof(_Float16); }
+
+}  // namespace
+
+int launch_q4_row_exponents(const uint8_t *packed, int64_t N, int64_t K, int *ew, hipStream_t s) {
+    if (!packed || !ew || N <= 0 || K <= 0 || K % 32) return set_error(GAJE_ERR_INVALID_ARG, "row exponents: bad arguments");
+    hipLaunchKernelGGL(q4_row_exp_kernel, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, s, packed, N, (int)(K / 32), ew);
+    GAJE_HIP_CHECK(hipGetLastError());
+    return GAJE_OK;
+}
+
+int launch_split_rows(const SplitParams &p, hipStream_t s) {
+    if (p.M < 0 || p.K <= 0 || p.K % 32 || (p.M > 0 && (!p.x || !p.xh || !p.xl || !p.ex)) || p.ldx < p.K || p.ldh < p.K)
+        return set_error(GAJE_ERR_INVALID_ARG, "split rows: bad arguments");
+    if (p.M == 0) return GAJE_OK;
+    const size_t lds = (size_t)p.K * 4;
+    if (lds + 1024 > max_lds_per_block())
+        return set_error(GAJE_ERR_UNSUPPORTED, "split rows: K = %lld does not fit LDS", (long long)p.K);
+    if (p.norm_w) hipLaunchKernelGGL(split_rows_kernel<true>, dim3((unsigned)p.M), dim3(256), lds, s, p);
+    else hipLaunchKernelGGL(split_rows_kernel<false>, dim3((unsigned)p.M), dim3(256), lds, s, p);
+    GAJE_HIP_CHECK(hipGetLastError());
+    return GAJE_OK;
+}
+
+GemmPlan plan_gemm_q4(int64_t M, int64_t N, int64_t K) {
+    GemmPlan pl{};
+    pl.mt = M > 128 ? 256 : 128;
+    const int64_t tiles = ((M + pl.mt - 1) / pl.mt) * ((N + GM_NT - 1) / GM_NT);
+    const int64_t nb = K / 32;
+    const int64_t cu = device_cu_count();
+    int64_t S = 1;
+    if (tiles < cu) S = (cu + tiles - 1) / tiles;
+    int64_t kb = (nb + S - 1) / S;
+    if (kb < 8) kb = 8;          // at least two weight groups per split
+    kb = (kb + 3) / 4 * 4;       // splits start on group boundaries
+    pl.kb_per = (int)kb;
+    pl.splits = (int)((nb + kb - 1) / kb);
+    pl.part_floats = pl.splits > 1 ? pl.splits * M * N : 0;
+    return pl;
+}
+
+int launch_gemm_q4(const GemmQ4Params &p0, const GemmPlan &pl, hipStream_t s) {
+    GemmQ4Params p = p0;
+    if (p.M < 0 || p.N <= 0 || p.nb <= 0 || !p.w || !p.ew || (p.M > 0 && (!p.xh || !p.xl || !p.ex || !p.y)))
+        return set_error(GAJE_ERR_INVALID_ARG, "q4 gemm: bad arguments");
+    if (p.M == 0) return GAJE_OK;
+    if (pl.kb_per % 4 || pl.kb_per <= 0 || (int64_t)pl.splits * pl.kb_per < p.nb || (pl.splits > 1 && !p.part))
+        return set_error(GAJE_ERR_INVALID_ARG, "q4 gemm: bad plan");
+    p.kb_per = pl.kb_per;
+    if (pl.splits == 1) p.part = nullptr;
+    const dim3 grid((unsigned)((p.N + GM_NT - 1) / GM_NT), (unsigned)((p.M + pl.mt - 1) / pl.mt), (unsigned)pl.splits);
+    if (pl.mt == 256) {
+        if (gemm_lds<256>() + 1024 > max_lds_per_block()) return set_error(GAJE_ERR_UNSUPPORTED, "q4 gemm: LDS");
+        hipLaunchKernelGGL(gemm_q4_mfma_kernel<256>, grid, dim3(512), gemm_lds<256>(), s, p);
+    } else {
+        hipLaunchKernelGGL(gemm_q4_mfma_kernel<128>, grid, dim3(256), gemm_lds<128>(), s, p);
+    }
+    GAJE_HIP_CHECK(hipGetLastError());
+    if (pl.splits > 1) {
+        const int64_t total = p.M * p.N;
+        int64_t g = (total + 255) / 256;
+        if (g > 4096) g = 4096;
+        hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)g), dim3(256), 0, s, p, pl.splits);
+        GAJE_HIP_CHECK(hipGetLastError());
+    }
+    return GAJE_OK;
+}
+
+}  // namespace gaje

@@ -142,6 +142,54 @@ struct EmbedParams {
 };
 int launch_embed(const EmbedParams &p, hipStream_t s);
 
+// Activation rows -> the f16 hi/lo planes of the MFMA matrix product (optional
+// rms_norm first).  Row m of the planes holds x' = x * 2^ex[m] split as
+// hi = f16(x'), lo = f16(x' - hi).
+struct SplitParams {
+    const float *x;          // [M][ldx] fp32 rows
+    int64_t ldx;
+    const float *norm_w;     // rms_norm weight [K] or null
+    float eps;
+    float *x_out;            // with norm_w: the normalised rows [M][ldo], or null
+    int64_t ldo;
+    uint16_t *xh, *xl;       // f16 planes [M][ldh]
+    int64_t ldh;
+    int *ex;                 // [M] row exponents
+    int64_t M, K;
+};
+int launch_split_rows(const SplitParams &p, hipStream_t s);
+// Per packed Q4_0 row: the exponent that scales its largest |d| into [2^14, 2^15).
+int launch_q4_row_exponents(const uint8_t *packed, int64_t N, int64_t K, int *ew, hipStream_t s);
+
+// Y = X W^T over packed Q4_0 rows on the MFMA units (f16 hi/lo operand pairs,
+// fp32 accumulation): per row, the dot flushed like the reference's, + bias,
+// + residual.
+struct GemmQ4Params {
+    const uint8_t *w;        // packed rows (launch_pack_q4_0)
+    const int *ew;           // [N] weight row exponents
+    const uint16_t *xh, *xl; // activation planes (launch_split_rows)
+    const int *ex;
+    int64_t ldh;
+    const float *bias;
+    int64_t bias_len;
+    const float *resid;      // Y = resid + row result, or null (may alias y)
+    int64_t ldr;
+    float *y;
+    int64_t ldy;
+    float *part;             // split-K partials [splits][M][N] (plan.part_floats)
+    int64_t M, N;
+    int32_t nb;              // K / 32
+    int32_t kb_per;          // set by launch_gemm_q4 from the plan
+};
+struct GemmPlan {
+    int mt;                  // activation rows per workgroup (128 or 256)
+    int splits;              // K splits
+    int kb_per;              // blocks per split (multiple of 4)
+    int64_t part_floats;     // partial buffer the splits need (0 if one split)
+};
+GemmPlan plan_gemm_q4(int64_t M, int64_t N, int64_t K);
+int launch_gemm_q4(const GemmQ4Params &p, const GemmPlan &plan, hipStream_t s);
+
 int launch_finalize(DevState *st, uint32_t *out_tokens, hipStream_t s);
 int launch_kwta(float *x, int64_t n, int64_t k, DevState *st, hipStream_t s);
 int launch_argmax(const float *x, int64_t n, uint32_t *idx, hipStream_t s);

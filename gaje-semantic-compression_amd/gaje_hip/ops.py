@@ -109,6 +109,19 @@ def q4_0_gemm(packed: DeviceBuffer, X: DeviceBuffer, Y: DeviceBuffer, m: int, n:
     check(lib().gaje_hip_q4_0_gemm(packed.ptr, X.ptr, _p(bias), bias_len, Y.ptr, m, n, k, stream))
 
 
+def q4_0_gemm_mfma_workspace(m: int, n: int, k: int) -> int:
+    return int(lib().gaje_hip_q4_0_gemm_mfma_workspace(m, n, k))
+
+
+def q4_0_gemm_mfma(packed: DeviceBuffer, X: DeviceBuffer, Y: DeviceBuffer, m: int, n: int, k: int,
+                   workspace: DeviceBuffer, bias: DeviceBuffer | None = None, bias_len: int = 0,
+                   stream=None) -> None:
+    """Y = X W^T (+ bias) on the MFMA units: the reference dot product to fp32
+    accuracy (f16 hi/lo operand pairs), not bit-exact; see gaje_hip.h."""
+    check(lib().gaje_hip_q4_0_gemm_mfma(packed.ptr, X.ptr, _p(bias), bias_len, Y.ptr, m, n, k,
+                                        workspace.ptr, workspace.nbytes, stream))
+
+
 def lut4_gemv(codes: DeviceBuffer, lut: DeviceBuffer, lut_len: int, x: DeviceBuffer,
               y: DeviceBuffer, n: int, k: int, bias: DeviceBuffer | None = None,
               bias_len: int = 0, stream=None) -> None:
