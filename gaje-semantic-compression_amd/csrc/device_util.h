@@ -117,6 +117,39 @@ __device__ __forceinline__ float order_key_inv(uint32_t k) {
 // The reference's |t| < 1e-6 -> 0 flush of the 4-bit dots (genomic.rs:198-203,331-335).
 __device__ __forceinline__ float flush_small(float t) { return fabsf(t) < 1e-6f ? 0.0f : t; }
 
+// GenomicLinear::get_row_core (linear/forward.rs:195-285) element k of `row`
+// for the embedding formats: F32 copy, Q4_0 dequantize_weight (a product then
+// a sum, blocks.rs:18-30) from the packed rows, LUT-4bit table lookup (high
+// nibble first); rows past rows_valid read as zeros.
+__device__ __forceinline__ float embed_value(const EmbedParams &p, int64_t row, int64_t k) {
+    const int64_t nb = p.K / 32;
+    float v = 0.0f;
+    if (row < p.rows_valid) {
+        if (p.fmt == FMT_F32) {
+            v = ((const float *)p.w)[row * p.K + k];
+        } else if (k < nb * 32) {
+            const int64_t b = k / 32;
+            const int i = (int)(k % 32);
+            if (p.fmt == FMT_Q4_0) {
+                // packed rows (launch_pack_q4_0): element i of block b is
+                // chain i % 8, chunk i / 8 of group b / 4
+                const int64_t G = (nb + 3) / 4;
+                const uint8_t *grp = p.w + (row * G + b / 4) * 80;
+                const int bb = (int)(b & 3), l = i & 7, c = i >> 3;
+                const uint32_t word = *(const uint32_t *)(grp + 8 * l + 4 * (bb >> 1));
+                const float q = (float)((word >> (8 * c + 4 * (bb & 1))) & 0x0Fu);
+                const uint32_t sm = *(const uint32_t *)(grp + 64 + 4 * bb);
+                v = __fadd_rn(__fmul_rn(q, half_lo(sm)), half_hi(sm));
+            } else {
+                const float *t = p.lut + (row < p.lut_rows_own ? row * nb * 16 : 0) + b * p.lut_block_stride;
+                const uint8_t byte = p.w[(row * nb + b) * 16 + i / 2];
+                v = t[(i % 2 == 0) ? (byte >> 4) : (byte & 0x0F)];
+            }
+        }
+    }
+    return v;
+}
+
 __device__ __forceinline__ void nan_flag(DevState *st, int layer, int stage) {
     if (st && stage >= 0) atomicMin(&st->nan_code, (uint32_t)(layer * 8 + stage));
 }

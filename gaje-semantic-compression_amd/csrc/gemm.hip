@@ -39,6 +39,8 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
+enum SplitPrologue { SPLIT_PLAIN = 0, SPLIT_NORM = 1, SPLIT_SWIGLU = 2 };
+
 constexpr int GM_NT = 128;   // weight rows per workgroup
 constexpr int GM_ROW = 40;   // halves per LDS tile row (32 + 8 pad)
 
@@ -69,9 +71,13 @@ __global__ __launch_bounds__(256) void q4_row_exp_kernel(const uint8_t *w, int64
     if (lane == 0) ew[row] = split_exponent(mx);
 }
 
-// One activation row per workgroup: optional rms_norm (norm.rs:52-88, the
-// reference's chain order), then the row's exponent and its f16 hi/lo planes.
-template <bool NORM>
+// One activation row per workgroup: a prologue (none, rms_norm in the
+// reference's chain order (norm.rs:52-88), or swiglu_balanced of a gate/up pair
+// (activation.rs:35-51) with the optional use_genomic_norm scaling of
+// block/forward.rs:115-123), the NaN guards of RustGenomicBlock::forward_core
+// that the prologue's values decide, then the row's exponent and its f16
+// hi/lo planes.
+template <int PRO>
 __global__ __launch_bounds__(256) void split_rows_kernel(SplitParams p) {
     extern __shared__ __align__(16) float xs[];
     __shared__ float red[4];
@@ -80,9 +86,30 @@ __global__ __launch_bounds__(256) void split_rows_kernel(SplitParams p) {
     const int tid = threadIdx.x;
     const int64_t K = p.K, K4 = K >> 2;
     const float *xr = p.x + m * p.ldx;
-    for (int64_t i = tid; i < K4; i += 256) *(float4 *)(xs + 4 * i) = *(const float4 *)(xr + 4 * i);
-    __syncthreads();
-    if constexpr (NORM) {
+    int bad_a = 0, bad_b = 0;
+    if constexpr (PRO == SPLIT_SWIGLU) {
+        const float *ur = p.up + m * p.ldx;
+        for (int64_t i = tid; i < K4; i += 256) {
+            const float4 g = *(const float4 *)(xr + 4 * i), u = *(const float4 *)(ur + 4 * i);
+            bad_a |= isnan(u.x) | isnan(u.y) | isnan(u.z) | isnan(u.w);
+            float4 o;
+            o.x = swiglu1(g.x, u.x);
+            o.y = swiglu1(g.y, u.y);
+            o.z = swiglu1(g.z, u.z);
+            o.w = swiglu1(g.w, u.w);
+            bad_b |= isnan(o.x) | isnan(o.y) | isnan(o.z) | isnan(o.w);
+            *(float4 *)(xs + 4 * i) = o;
+        }
+    } else {
+        for (int64_t i = tid; i < K4; i += 256) {
+            const float4 v = *(const float4 *)(xr + 4 * i);
+            bad_a |= isnan(v.x) | isnan(v.y) | isnan(v.z) | isnan(v.w);
+            *(float4 *)(xs + 4 * i) = v;
+        }
+    }
+    const bool any_a = __syncthreads_or(bad_a);
+    if (any_a && tid == 0) nan_flag(p.st, p.layer, p.st_a);
+    if constexpr (PRO == SPLIT_NORM) {
         rms_inv_plain(xs, K, p.eps, &inv_slot);
         __syncthreads();
         const float inv = inv_slot;
@@ -93,11 +120,35 @@ __global__ __launch_bounds__(256) void split_rows_kernel(SplitParams p) {
             v.y = (v.y * inv) * g.y;
             v.z = (v.z * inv) * g.z;
             v.w = (v.w * inv) * g.w;
+            bad_b |= isnan(v.x) | isnan(v.y) | isnan(v.z) | isnan(v.w);
             *(float4 *)(xs + 4 * i) = v;
         }
-        if (p.x_out) {  // the normalised row itself, for callers that keep it
-            for (int64_t i = tid; i < K4; i += 256) *(float4 *)(p.x_out + m * p.ldo + 4 * i) = *(float4 *)(xs + 4 * i);
+    }
+    if constexpr (PRO != SPLIT_PLAIN) {
+        if (__syncthreads_or(bad_b) && tid == 0) nan_flag(p.st, p.layer, p.st_b);
+    }
+    if constexpr (PRO == SPLIT_SWIGLU) {
+        if (p.gnorm) {
+            // the reference's rayon sum has no fixed order; a sequential one here
+            if (tid == 0) {
+                float ss = 0.0f;
+                for (int64_t k = 0; k < K; ++k) {
+                    const float sq = xs[k] * xs[k];
+                    ss = ss + sq;
+                }
+                inv_slot = sqrtf(ss / (float)K + p.eps);
+            }
+            __syncthreads();
+            const float rms = inv_slot;
+            if (rms > p.h_scale) {
+                const float sc = p.h_scale / rms;
+                for (int64_t k = tid; k < K; k += 256) xs[k] = xs[k] * sc;
+            }
+            __syncthreads();
         }
+    }
+    if (p.x_out) {  // the prologue's output row itself, for callers that keep it
+        for (int64_t i = tid; i < K4; i += 256) *(float4 *)(p.x_out + m * p.ldo + 4 * i) = *(float4 *)(xs + 4 * i);
     }
     float mx = 0.0f;
     for (int64_t i = tid; i < K4; i += 256) {
@@ -260,6 +311,7 @@ __global__ __launch_bounds__(MT * 2) void gemm_q4_mfma_kernel(GemmQ4Params p) {
     }
 
     // epilogue: lane holds rows 4*(lane>>4)+r, column lane&15 of each 16x16 tile
+    int bad_a = 0, bad_b = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int64_t n = n0 + wn * 64 + 16 * j + fr;
@@ -278,11 +330,17 @@ __global__ __launch_bounds__(MT * 2) void gemm_q4_mfma_kernel(GemmQ4Params p) {
                 } else {
                     v = flush_small(v);
                     if (n < p.bias_len) v = v + bias;
+                    bad_a |= isnan(v);
                     if (p.resid) v = p.resid[m * p.ldr + n] + v;
+                    bad_b |= isnan(v);
                     p.y[m * p.ldy + n] = v;
                 }
             }
         }
+    }
+    if (p.st) {
+        if (__any(bad_a) && lane == 0) nan_flag(p.st, p.layer, p.st_a);
+        if (__any(bad_b) && lane == 0) nan_flag(p.st, p.layer, p.st_b);
     }
 }
 
@@ -296,7 +354,9 @@ __global__ void gemm_reduce_kernel(GemmQ4Params p, int S) {
         for (int z = 1; z < S; ++z) v += p.part[(int64_t)z * total + t];
         v = flush_small(v);
         if (n < p.bias_len) v = v + p.bias[n];
+        if (isnan(v)) nan_flag(p.st, p.layer, p.st_a);
         if (p.resid) v = p.resid[m * p.ldr + n] + v;
+        if (isnan(v)) nan_flag(p.st, p.layer, p.st_b);
         p.y[m * p.ldy + n] = v;
     }
 }
@@ -320,8 +380,10 @@ int launch_split_rows(const SplitParams &p, hipStream_t s) {
     const size_t lds = (size_t)p.K * 4;
     if (lds + 1024 > max_lds_per_block())
         return set_error(GAJE_ERR_UNSUPPORTED, "split rows: K = %lld does not fit LDS", (long long)p.K);
-    if (p.norm_w) hipLaunchKernelGGL(split_rows_kernel<true>, dim3((unsigned)p.M), dim3(256), lds, s, p);
-    else hipLaunchKernelGGL(split_rows_kernel<false>, dim3((unsigned)p.M), dim3(256), lds, s, p);
+    if (p.up && p.norm_w) return set_error(GAJE_ERR_INVALID_ARG, "split rows: norm and swiglu prologues are exclusive");
+    if (p.up) hipLaunchKernelGGL(split_rows_kernel<SPLIT_SWIGLU>, dim3((unsigned)p.M), dim3(256), lds, s, p);
+    else if (p.norm_w) hipLaunchKernelGGL(split_rows_kernel<SPLIT_NORM>, dim3((unsigned)p.M), dim3(256), lds, s, p);
+    else hipLaunchKernelGGL(split_rows_kernel<SPLIT_PLAIN>, dim3((unsigned)p.M), dim3(256), lds, s, p);
     GAJE_HIP_CHECK(hipGetLastError());
     return GAJE_OK;
 }

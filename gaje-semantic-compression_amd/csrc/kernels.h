@@ -141,17 +141,25 @@ struct EmbedParams {
     DevState *st;
 };
 int launch_embed(const EmbedParams &p, hipStream_t s);
+// Embedding rows of ids[0..n) into p.h [n][K] (p.st unused).
+int launch_embed_rows(const EmbedParams &p, const uint32_t *ids, int64_t n, hipStream_t s);
 
 // Activation rows -> the f16 hi/lo planes of the MFMA matrix product (optional
 // rms_norm first).  Row m of the planes holds x' = x * 2^ex[m] split as
 // hi = f16(x'), lo = f16(x' - hi).
 struct SplitParams {
-    const float *x;          // [M][ldx] fp32 rows
+    const float *x;          // [M][ldx] fp32 rows (with `up`: the gate rows)
     int64_t ldx;
     const float *norm_w;     // rms_norm weight [K] or null
     float eps;
-    float *x_out;            // with norm_w: the normalised rows [M][ldo], or null
+    const float *up;         // swiglu prologue: up rows [M][ldx], or null
+    int32_t gnorm;           // with `up`: use_genomic_norm scaling (h_scale)
+    float h_scale;
+    float *x_out;            // the prologue's output rows [M][ldo], or null
     int64_t ldo;
+    DevState *st;            // NaN guards (stage < 0 or st null: none): st_a on the
+    int32_t layer;           // input (or the up rows), st_b on the norm / swiglu output
+    int32_t st_a, st_b;
     uint16_t *xh, *xl;       // f16 planes [M][ldh]
     int64_t ldh;
     int *ex;                 // [M] row exponents
@@ -180,6 +188,9 @@ struct GemmQ4Params {
     int64_t M, N;
     int32_t nb;              // K / 32
     int32_t kb_per;          // set by launch_gemm_q4 from the plan
+    DevState *st;            // NaN guards (or null): st_a on the row result,
+    int32_t layer;           // st_b after the residual add
+    int32_t st_a, st_b;
 };
 struct GemmPlan {
     int mt;                  // activation rows per workgroup (128 or 256)
@@ -189,6 +200,27 @@ struct GemmPlan {
 };
 GemmPlan plan_gemm_q4(int64_t M, int64_t N, int64_t K);
 int launch_gemm_q4(const GemmQ4Params &p, const GemmPlan &plan, hipStream_t s);
+
+// Prompt prefill: RoPE + KV append for P tokens at positions pos0.. of one layer.
+struct PrefillRopeParams {
+    const float *qkv;        // [P][ldq] rows q | k | v (bias added)
+    int64_t ldq;
+    float *q_out;            // [P][n_head * head_dim] roped queries
+    float *k_cache, *v_cache;// this layer: [n_kv][head_dim][cap]
+    int64_t cap, pos0, P;
+    int32_t n_head, n_kv, head_dim, rope_split;
+    const float *rope_cos, *rope_sin;  // [cap][head_dim / 2]
+};
+int launch_rope_kv(const PrefillRopeParams &p, hipStream_t s);
+// Causal GQA attention of P queries (positions pos0..) over the cache.
+struct PrefillAttnParams {
+    const float *q;          // [P][n_head * head_dim] roped
+    const float *k_cache, *v_cache;  // this layer: [n_kv][head_dim][cap]
+    int64_t cap, pos0, P;
+    int32_t n_head, n_kv, head_dim;
+    float *out;              // [P][n_head * head_dim]
+};
+int launch_prefill_attention(const PrefillAttnParams &p, hipStream_t s);
 
 int launch_finalize(DevState *st, uint32_t *out_tokens, hipStream_t s);
 int launch_kwta(float *x, int64_t n, int64_t k, DevState *st, hipStream_t s);

@@ -17,34 +17,16 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedParams p) {
         st->nan_code = NAN_NONE;
     }
     const int64_t row = (int64_t)(st->token % (uint32_t)p.vocab);
-    const int64_t nb = p.K / 32;
-    for (int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; k < p.K; k += (int64_t)gridDim.x * blockDim.x) {
-        float v = 0.0f;
-        if (row < p.rows_valid) {
-            if (p.fmt == FMT_F32) {
-                v = ((const float *)p.w)[row * p.K + k];
-            } else if (k < nb * 32) {
-                const int64_t b = k / 32;
-                const int i = (int)(k % 32);
-                if (p.fmt == FMT_Q4_0) {
-                    // packed rows (launch_pack_q4_0): element i of block b is
-                    // chain i % 8, chunk i / 8 of group b / 4
-                    const int64_t G = (nb + 3) / 4;
-                    const uint8_t *grp = p.w + (row * G + b / 4) * 80;
-                    const int bb = (int)(b & 3), l = i & 7, c = i >> 3;
-                    const uint32_t word = *(const uint32_t *)(grp + 8 * l + 4 * (bb >> 1));
-                    const float q = (float)((word >> (8 * c + 4 * (bb & 1))) & 0x0Fu);
-                    const uint32_t sm = *(const uint32_t *)(grp + 64 + 4 * bb);
-                    v = __fadd_rn(__fmul_rn(q, half_lo(sm)), half_hi(sm));
-                } else {
-                    const float *t = p.lut + (row < p.lut_rows_own ? row * nb * 16 : 0) + b * p.lut_block_stride;
-                    const uint8_t byte = p.w[(row * nb + b) * 16 + i / 2];
-                    v = t[(i % 2 == 0) ? (byte >> 4) : (byte & 0x0F)];
-                }
-            }
-        }
-        p.h[k] = v;
-    }
+    for (int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; k < p.K; k += (int64_t)gridDim.x * blockDim.x)
+        p.h[k] = embed_value(p, row, k);
+}
+
+// get_row_core for a batch of token ids: rows [n][K] of h (prompt prefill).
+__global__ __launch_bounds__(256) void embed_rows_kernel(EmbedParams p, const uint32_t *ids, int64_t n) {
+    const int64_t t = blockIdx.y;
+    const int64_t row = (int64_t)(ids[t] % (uint32_t)p.vocab);
+    for (int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; k < p.K; k += (int64_t)gridDim.x * blockDim.x)
+        p.h[t * p.K + k] = embed_value(p, row, k);
 }
 
 // End of a token: NaN guard -> halt, else argmax -> next token, advance.
@@ -186,6 +168,14 @@ unsigned grid_for(int64_t n, int threads, unsigned cap = 4096) {
 int launch_embed(const EmbedParams &p, hipStream_t s) {
     if (!p.st || !p.h || p.vocab <= 0 || p.K <= 0) return set_error(GAJE_ERR_INVALID_ARG, "embed: bad arguments");
     hipLaunchKernelGGL(embed_kernel, dim3(grid_for(p.K, 256, 64)), dim3(256), 0, s, p);
+    GAJE_HIP_CHECK(hipGetLastError());
+    return GAJE_OK;
+}
+
+int launch_embed_rows(const EmbedParams &p, const uint32_t *ids, int64_t n, hipStream_t s) {
+    if (!p.h || !ids || p.vocab <= 0 || p.K <= 0 || n <= 0 || n > 65535)
+        return set_error(GAJE_ERR_INVALID_ARG, "embed rows: bad arguments");
+    hipLaunchKernelGGL(embed_rows_kernel, dim3(grid_for(p.K, 256, 16), (unsigned)n), dim3(256), 0, s, p, ids, n);
     GAJE_HIP_CHECK(hipGetLastError());
     return GAJE_OK;
 }

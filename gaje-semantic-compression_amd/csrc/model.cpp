@@ -58,6 +58,7 @@ struct DevLinear {
     int64_t *a_ptr = nullptr;
     uint32_t *a_col = nullptr;
     uint16_t *a_val = nullptr;
+    int *ew = nullptr;  // FMT_Q4_0: per-row exponents of the MFMA matrix product
     int64_t bytes = 0;
 };
 
@@ -271,6 +272,16 @@ struct gaje_hip_model {
     bool profile = false;
     float last_blocks_ms = 0.0f, last_head_ms = 0.0f;
 
+    // prompt prefill on the MFMA units: per-chunk activations, grown on demand
+    struct Prefill {
+        int64_t rows = 0;        // chunk rows the buffers hold
+        int64_t part_floats = 0; // split-K partials they hold
+        float *H = nullptr, *QKV = nullptr, *Q = nullptr, *ATT = nullptr, *GU = nullptr, *part = nullptr;
+        uint16_t *xh = nullptr, *xl = nullptr;
+        int *ex = nullptr;
+        uint32_t *ids = nullptr;
+    } pf;
+
     std::vector<void *> allocs;
 
     ~gaje_hip_model() {
@@ -332,6 +343,10 @@ int upload_linear(gaje_hip_model *m, const HostLinear &L, DevLinear &D, bool til
         m->release(tmp);
         GAJE_TRY(rc);
         m->weight_bytes += packed;
+        if (D.rows_valid > 0) {
+            GAJE_TRY(m->alloc(&D.ew, (size_t)D.rows_valid));
+            GAJE_TRY(launch_q4_row_exponents(D.w, D.rows_valid, L.K, D.ew, m->stream));
+        }
     } else if (L.fmt == FMT_F32 && tile_f32 && L.K % 8 == 0 && D.rows_valid > 0) {
         // stage the row-major rows and tile them (32-row tiles, KiB chunks)
         const size_t raw = (size_t)D.rows_valid * L.K * 4;
@@ -465,6 +480,20 @@ int reserve_ctx(gaje_hip_model *m, int64_t positions) {
     return GAJE_OK;
 }
 
+// Output norm -> lm_head logits with the running argmax -> next token, advance
+// (llm/forward.rs:38-46) for the hidden state in m->h.
+int enqueue_head(gaje_hip_model *m) {
+    GemvParams p = gemv_base(m, m->lm_head, m->h);
+    p.norm_w = m->output_norm;
+    p.mode = MODE_ARGMAX;
+    p.y = m->logits;
+    p.x_out = m->hnorm;
+    p.nontemporal = 1;
+    p.layer = (int32_t)m->n_layers;
+    GAJE_TRY(launch_gemv(p, m->stream));
+    return launch_finalize(m->st, m->out_tokens, m->stream);
+}
+
 // Enqueue one decode step (embedding -> blocks -> output norm -> lm_head ->
 // argmax/advance) on the model stream.
 int enqueue_token(gaje_hip_model *m, hipEvent_t ev_blocks_done) {
@@ -550,16 +579,7 @@ int enqueue_token(gaje_hip_model *m, hipEvent_t ev_blocks_done) {
         }
     }
     if (ev_blocks_done) GAJE_HIP_CHECK(hipEventRecord(ev_blocks_done, m->stream));
-
-    GemvParams p = gemv_base(m, m->lm_head, m->h);
-    p.norm_w = m->output_norm;
-    p.mode = MODE_ARGMAX;
-    p.y = m->logits;
-    p.x_out = m->hnorm;
-    p.nontemporal = 1;
-    p.layer = (int32_t)m->n_layers;
-    GAJE_TRY(launch_gemv(p, m->stream));
-    return launch_finalize(m->st, m->out_tokens, m->stream);
+    return enqueue_head(m);
 }
 
 int ensure_graph(gaje_hip_model *m) {
@@ -883,6 +903,237 @@ extern "C" int gaje_hip_prefill(gaje_hip_model *m, const uint32_t *ids, int64_t 
         (void)done;
         return nan_error(s);
     }
+    if (last_logits_host)
+        GAJE_HIP_CHECK(hipMemcpy(last_logits_host, m->logits, (size_t)m->vocab_out * 4, hipMemcpyDeviceToHost));
+    return GAJE_OK;
+}
+
+namespace {
+
+// Tokens per MFMA prefill pass (the activation buffers hold one chunk).
+constexpr int64_t PREFILL_CHUNK = 1024;
+
+int prefill_mfma_supported(const gaje_hip_model *m) {
+    if (m->n_layers == 0) return GAJE_OK;
+    if (m->hd != 64 && m->hd != 128)
+        return set_error(GAJE_ERR_UNSUPPORTED, "MFMA prefill: head_dim %lld (64 or 128 only)", (long long)m->hd);
+    for (const Layer &Ly : m->layers)
+        for (const DevLinear *D : {&Ly.qkv, &Ly.o, &Ly.gate_up, &Ly.down})
+            if (D->fmt != FMT_Q4_0 || D->a_ptr || D->rows_valid != D->N || !D->ew)
+                return set_error(GAJE_ERR_UNSUPPORTED,
+                                 "MFMA prefill needs complete Q4_0 body tensors without anchors (use gaje_hip_prefill)");
+    return GAJE_OK;
+}
+
+int64_t prefill_kmax(const gaje_hip_model *m) { return std::max({m->n_embd, m->q_rows, m->ffn}); }
+
+// Grow the prefill buffers to `rows` tokens (and the split-K partials their
+// products need).
+int prefill_reserve(gaje_hip_model *m, int64_t rows) {
+    auto &f = m->pf;
+    const Layer &L0 = m->layers[0];
+    int64_t part = 0;
+    for (const DevLinear *D : {&L0.qkv, &L0.o, &L0.gate_up, &L0.down})
+        part = std::max(part, plan_gemm_q4(rows, D->N, D->K).part_floats);
+    if (rows <= f.rows && part <= f.part_floats) return GAJE_OK;
+    rows = std::max(rows, f.rows);
+    part = std::max(part, f.part_floats);
+    GAJE_HIP_CHECK(hipStreamSynchronize(m->stream));
+    for (void *p : {(void *)f.H, (void *)f.QKV, (void *)f.Q, (void *)f.ATT, (void *)f.GU, (void *)f.part, (void *)f.xh,
+                    (void *)f.xl, (void *)f.ex, (void *)f.ids})
+        if (p) m->release(p);
+    f = gaje_hip_model::Prefill();
+    const int64_t kmax = prefill_kmax(m);
+    GAJE_TRY(m->alloc(&f.H, (size_t)(rows * m->n_embd)));
+    GAJE_TRY(m->alloc(&f.QKV, (size_t)(rows * L0.qkv.N)));
+    GAJE_TRY(m->alloc(&f.Q, (size_t)(rows * m->q_rows)));
+    GAJE_TRY(m->alloc(&f.ATT, (size_t)(rows * m->q_rows)));
+    GAJE_TRY(m->alloc(&f.GU, (size_t)(rows * L0.gate_up.N)));
+    GAJE_TRY(m->alloc(&f.xh, (size_t)(rows * kmax)));
+    GAJE_TRY(m->alloc(&f.xl, (size_t)(rows * kmax)));
+    GAJE_TRY(m->alloc(&f.ex, (size_t)rows));
+    GAJE_TRY(m->alloc(&f.ids, (size_t)rows));
+    GAJE_TRY(m->alloc(&f.part, (size_t)part));
+    f.rows = rows;
+    f.part_floats = part;
+    return GAJE_OK;
+}
+
+SplitParams prefill_split(const gaje_hip_model *m, const float *x, int64_t ldx, int64_t P, int64_t K) {
+    SplitParams sp{};
+    sp.x = x;
+    sp.ldx = ldx;
+    sp.eps = m->eps;
+    sp.h_scale = 1.0f;
+    sp.xh = m->pf.xh;
+    sp.xl = m->pf.xl;
+    sp.ldh = K;
+    sp.ex = m->pf.ex;
+    sp.M = P;
+    sp.K = K;
+    sp.st = m->st;
+    sp.st_a = sp.st_b = ST_NONE;
+    return sp;
+}
+
+// Y[P][D.N] = rows of the current activation planes x D (+ bias) (+ resid).
+int prefill_gemm(gaje_hip_model *m, const DevLinear &D, int64_t P, float *y, const float *resid, int32_t layer,
+                 int32_t st_a, int32_t st_b) {
+    const auto &f = m->pf;
+    const GemmPlan pl = plan_gemm_q4(P, D.N, D.K);
+    if (pl.part_floats > f.part_floats) return set_error(GAJE_ERR_INVALID_ARG, "prefill: split-K buffer too small");
+    GemmQ4Params p{};
+    p.w = D.w;
+    p.ew = D.ew;
+    p.xh = f.xh;
+    p.xl = f.xl;
+    p.ex = f.ex;
+    p.ldh = D.K;
+    p.bias = D.bias;
+    p.bias_len = D.bias_len;
+    p.resid = resid;
+    p.ldr = D.N;
+    p.y = y;
+    p.ldy = D.N;
+    p.part = f.part;
+    p.M = P;
+    p.N = D.N;
+    p.nb = (int32_t)(D.K / 32);
+    p.st = m->st;
+    p.layer = layer;
+    p.st_a = st_a;
+    p.st_b = st_b;
+    return launch_gemm_q4(p, pl, m->stream);
+}
+
+// One block (RustGenomicBlock::forward_core, block/forward.rs:10-157) for the
+// P tokens of the current chunk at positions pos..pos+P-1, in place on pf.H.
+int prefill_layer(gaje_hip_model *m, int64_t l, int64_t pos, int64_t P) {
+    Layer &Ly = m->layers[l];
+    auto &f = m->pf;
+    hipStream_t s = m->stream;
+    const int32_t li = (int32_t)l;
+    const size_t layer_kv = (size_t)m->n_kv * m->cap * m->hd;
+
+    SplitParams sp = prefill_split(m, f.H, m->n_embd, P, m->n_embd);
+    sp.norm_w = Ly.attn_norm;
+    sp.layer = li;
+    sp.st_a = ST_INPUT;
+    sp.st_b = Ly.attn_norm ? ST_ATTN_NORM : ST_NONE;
+    GAJE_TRY(launch_split_rows(sp, s));
+    GAJE_TRY(prefill_gemm(m, Ly.qkv, P, f.QKV, nullptr, li, ST_NONE, ST_NONE));
+
+    PrefillRopeParams rp{};
+    rp.qkv = f.QKV;
+    rp.ldq = Ly.qkv.N;
+    rp.q_out = f.Q;
+    rp.k_cache = m->k_cache + l * layer_kv;
+    rp.v_cache = m->v_cache + l * layer_kv;
+    rp.cap = m->cap;
+    rp.pos0 = pos;
+    rp.P = P;
+    rp.n_head = (int32_t)m->n_head;
+    rp.n_kv = (int32_t)m->n_kv;
+    rp.head_dim = (int32_t)m->hd;
+    rp.rope_split = m->rope_split;
+    rp.rope_cos = m->rope_cos;
+    rp.rope_sin = m->rope_sin;
+    GAJE_TRY(launch_rope_kv(rp, s));
+
+    PrefillAttnParams ap{};
+    ap.q = f.Q;
+    ap.k_cache = rp.k_cache;
+    ap.v_cache = rp.v_cache;
+    ap.cap = m->cap;
+    ap.pos0 = pos;
+    ap.P = P;
+    ap.n_head = (int32_t)m->n_head;
+    ap.n_kv = (int32_t)m->n_kv;
+    ap.head_dim = (int32_t)m->hd;
+    ap.out = f.ATT;
+    GAJE_TRY(launch_prefill_attention(ap, s));
+
+    sp = prefill_split(m, f.ATT, m->q_rows, P, m->q_rows);
+    GAJE_TRY(launch_split_rows(sp, s));
+    GAJE_TRY(prefill_gemm(m, Ly.o, P, f.H, f.H, li, ST_NONE, ST_NONE));
+
+    sp = prefill_split(m, f.H, m->n_embd, P, m->n_embd);
+    sp.norm_w = Ly.ffn_norm;
+    GAJE_TRY(launch_split_rows(sp, s));
+    GAJE_TRY(prefill_gemm(m, Ly.gate_up, P, f.GU, nullptr, li, ST_NONE, ST_NONE));
+
+    sp = prefill_split(m, f.GU, Ly.gate_up.N, P, m->ffn);
+    sp.up = f.GU + m->ffn;
+    sp.gnorm = m->use_genomic_norm;
+    sp.layer = li;
+    sp.st_a = ST_UP;
+    sp.st_b = ST_FFN_OUT;
+    GAJE_TRY(launch_split_rows(sp, s));
+    GAJE_TRY(prefill_gemm(m, Ly.down, P, f.H, f.H, li, ST_PROJ_FFN, ST_FINAL));
+
+    if (m->block_kwta_ratio > 0.0f && m->block_kwta_ratio < 1.0f) {
+        const int64_t k = kwta_k(m->n_embd, m->block_kwta_ratio);
+        for (int64_t t = 0; t < P; ++t) GAJE_TRY(launch_kwta(f.H + t * m->n_embd, m->n_embd, k, m->st, s));
+    }
+    return GAJE_OK;
+}
+
+}  // namespace
+
+extern "C" int gaje_hip_prefill_mfma(gaje_hip_model *m, const uint32_t *ids, int64_t n, float *last_logits_host) {
+    clear_error();
+    GAJE_TRY(check_model(m));
+    if (n < 0 || (n > 0 && !ids)) return set_error(GAJE_ERR_INVALID_ARG, "bad prefill arguments");
+    if (n == 0) return GAJE_OK;
+    GAJE_TRY(prefill_mfma_supported(m));
+    const int64_t pos0 = m->pos;
+    GAJE_TRY(reserve_ctx(m, pos0 + n));
+    hipStream_t s = m->stream;
+    GAJE_TRY(launch_state_set(m->st, (int32_t)pos0, ids[n - 1], -1, -1, 1, s));
+    int64_t last_rows = 0;
+    for (int64_t c0 = 0; c0 < n; c0 += PREFILL_CHUNK) {
+        const int64_t P = std::min(PREFILL_CHUNK, n - c0);
+        if (m->n_layers > 0) GAJE_TRY(prefill_reserve(m, P));
+        else if (m->pf.rows < P) {
+            if (m->pf.H) m->release(m->pf.H);
+            if (m->pf.ids) m->release(m->pf.ids);
+            GAJE_TRY(m->alloc(&m->pf.H, (size_t)(P * m->n_embd)));
+            GAJE_TRY(m->alloc(&m->pf.ids, (size_t)P));
+            m->pf.rows = P;
+        }
+        auto &f = m->pf;
+        GAJE_HIP_CHECK(hipMemcpyAsync(f.ids, ids + c0, (size_t)P * 4, hipMemcpyHostToDevice, s));
+        EmbedParams ep;
+        memset(&ep, 0, sizeof ep);
+        ep.w = m->embd.w;
+        ep.fmt = m->embd.fmt;
+        ep.lut = m->embd.lut;
+        ep.lut_rows_own = m->embd.lut_rows_own;
+        ep.lut_block_stride = m->embd.lut_block_stride;
+        ep.vocab = m->vocab_embd;
+        ep.rows_valid = m->embd.rows_valid;
+        ep.K = m->n_embd;
+        ep.h = f.H;
+        GAJE_TRY(launch_embed_rows(ep, f.ids, P, s));
+        for (int64_t l = 0; l < m->n_layers; ++l) GAJE_TRY(prefill_layer(m, l, pos0 + c0, P));
+        last_rows = P;
+        // the ids copy reads host memory the caller owns only for this call
+        GAJE_HIP_CHECK(hipStreamSynchronize(s));
+    }
+    DevState st;
+    GAJE_TRY(read_state(m, st));
+    if (st.nan_code != NAN_NONE) return nan_error(st);  // nothing is committed: the cache length stays pos0
+
+    // the last token's logits, argmax and position advance, as the decode step ends
+    GAJE_HIP_CHECK(hipMemcpyAsync(m->h, m->pf.H + (last_rows - 1) * m->n_embd, (size_t)m->n_embd * 4,
+                                  hipMemcpyDeviceToDevice, s));
+    GAJE_TRY(launch_state_set(m->st, (int32_t)(pos0 + n - 1), ids[n - 1], -1, -1, 1, s));
+    GAJE_TRY(enqueue_head(m));
+    if (last_logits_host && m->kwta_ratio > 0.0f && m->kwta_ratio < 1.0f)
+        GAJE_TRY(launch_kwta(m->logits, m->vocab_out, kwta_k(m->vocab_out, m->kwta_ratio), m->st, s));
+    GAJE_TRY(read_state(m, st));
+    if (st.halted || st.nan_code != NAN_NONE) return nan_error(st);
+    m->pos = st.pos;
     if (last_logits_host)
         GAJE_HIP_CHECK(hipMemcpy(last_logits_host, m->logits, (size_t)m->vocab_out * 4, hipMemcpyDeviceToHost));
     return GAJE_OK;

@@ -138,6 +138,7 @@ SIGNATURES = [
     ("gaje_hip_get_kwta", ctypes.c_int, [c_vp, ctypes.POINTER(ctypes.c_float)]),
     ("gaje_hip_reserve", ctypes.c_int, [c_vp, c_i64]),
     ("gaje_hip_prefill", ctypes.c_int, [c_vp, c_vp, c_i64, c_vp]),
+    ("gaje_hip_prefill_mfma", ctypes.c_int, [c_vp, c_vp, c_i64, c_vp]),
     ("gaje_hip_greedy_next", ctypes.c_int, [c_vp, ctypes.c_uint32, ctypes.POINTER(ctypes.c_uint32)]),
     ("gaje_hip_decode_greedy", ctypes.c_int, [c_vp, ctypes.c_uint32, c_i64, c_vp]),
     ("gaje_hip_generate", ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, ctypes.c_float, ctypes.c_float,

@@ -111,6 +111,15 @@ class GenomicLLM:
                                      out.ctypes.data if out is not None else None))
         return out
 
+    def prefill_mfma(self, ids, want_logits: bool = False):
+        """prefill() with the prompt processed as MFMA matrix products: fp32
+        accuracy, not the reference's bits (gaje_hip_prefill_mfma)."""
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        out = np.empty(self.n_logits, dtype=np.float32) if want_logits else None
+        check(lib().gaje_hip_prefill_mfma(self._h, ids.ctypes.data if ids.size else None, ids.size,
+                                          out.ctypes.data if out is not None else None))
+        return out
+
     def greedy_next(self, token: int) -> int:
         nxt = ctypes.c_uint32()
         check(lib().gaje_hip_greedy_next(self._h, int(token), ctypes.byref(nxt)))

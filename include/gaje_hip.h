@@ -209,6 +209,17 @@ int gaje_hip_reserve(gaje_hip_model *m, int64_t positions);
  * token's K-WTA-filtered logits. */
 int gaje_hip_prefill(gaje_hip_model *m, const uint32_t *ids, int64_t n, float *last_logits_host);
 
+/* Prompt prefill on the MFMA units: the same result as gaje_hip_prefill
+ * (ids[0..n) appended to the cache, last_logits_host (may be NULL) = the last
+ * token's K-WTA-filtered logits, the next greedy token kept on device) with
+ * the n tokens processed in chunks of up to 1024 as matrix products.  Not
+ * bit-exact: the body products carry fp32 accuracy in another summation order
+ * (see gaje_hip_q4_0_gemm_mfma), attention sums in another order.  The
+ * reference has no batched prefill (it loops forward_core, llm/forward.rs:229-232).
+ * Needs Q4_0 body tensors without anchors and head_dim 64 or 128, else
+ * GAJE_ERR_UNSUPPORTED.  On a NaN guard the cache length is left unchanged. */
+int gaje_hip_prefill_mfma(gaje_hip_model *m, const uint32_t *ids, int64_t n, float *last_logits_host);
+
 /* One greedy step on device: forward(token) then argmax of the logits
  * (nn/llm/forward.rs:262-271); no logits cross PCIe. */
 int gaje_hip_greedy_next(gaje_hip_model *m, uint32_t token, uint32_t *next);
