@@ -360,7 +360,7 @@ extern "C" int gaje_hip_expf(const float *x, float *y, int64_t n, void *stream) 
 extern "C" int gaje_hip_attention(const float *q, const float *k_cache, const float *v_cache, int64_t seq_len,
                                   int64_t capacity, int n_head, int n_head_kv, int head_dim, float *out,
                                   void *stream) {
-    AttnParams p;
+    AttnParams p{};
     memset(&p, 0, sizeof p);
     p.q = q;
     p.k_cache = k_cache;

@@ -114,7 +114,16 @@ __global__ __launch_bounds__(THREADS) void attn_decode_fast(AttnParams p) {
     const int h = blockIdx.x;
     const uint64_t tabv = tid < 32 ? kExp2Tab[tid] : 0;
     int ctx = (int)p.ctx;
-    if (p.st) {
+    if (p.seq_pos) {  // batched decode: this block's sequence
+        const int z = blockIdx.z;
+        const int pos = p.seq_pos[z];
+        if (pos < 0) return;
+        ctx = pos + 1;
+        p.q += z * p.seq_q_stride;
+        p.out += z * p.seq_q_stride;
+        p.k_cache += z * p.seq_kv_stride;
+        p.v_cache += z * p.seq_kv_stride;
+    } else if (p.st) {
         typedef int vi4 __attribute__((ext_vector_type(4)));
         const vi4 s4 = *(const volatile vi4 *)p.st;  // pos, token, step, halted: one load
         if (s4.w) return;                            // before any LDS-direct copy is in flight
@@ -258,7 +267,16 @@ __global__ __launch_bounds__(THREADS) void attn_decode_generic(AttnParams p) {
     const int h = blockIdx.x;
     const int hd = p.head_dim;
     const int g = h / (p.n_head / p.n_head_kv);
-    const int ctx = st ? st->pos + 1 : (int)p.ctx;
+    int ctx = st ? st->pos + 1 : (int)p.ctx;
+    if (p.seq_pos) {  // batched decode: this block's sequence
+        const int z = blockIdx.z;
+        if (p.seq_pos[z] < 0) return;
+        ctx = p.seq_pos[z] + 1;
+        p.q += z * p.seq_q_stride;
+        p.out += z * p.seq_q_stride;
+        p.k_cache += z * p.seq_kv_stride;
+        p.v_cache += z * p.seq_kv_stride;
+    }
     const float scale = 1.0f / sqrtf((float)hd);
 
     float *qh = smem;                            // hd floats (hd % 4 == 0)
@@ -308,7 +326,7 @@ int launch_attention(const AttnParams &p, hipStream_t s) {
         return set_error(GAJE_ERR_INVALID_ARG, "attention: null buffer");
     if (p.kv_cap <= 0 || p.kv_head_stride != p.kv_cap * p.head_dim)
         return set_error(GAJE_ERR_INVALID_ARG, "attention: bad cache geometry");
-    if (!p.st && (p.ctx <= 0 || p.ctx > p.kv_cap))
+    if (!p.st && !p.seq_pos && (p.ctx <= 0 || p.ctx > p.kv_cap))
         return set_error(GAJE_ERR_INVALID_ARG, "attention: context %lld outside 1..%lld", (long long)p.ctx,
                          (long long)p.kv_cap);
     if (p.n_head_kv <= 0 || p.n_head % p.n_head_kv != 0)
@@ -321,6 +339,8 @@ int launch_attention(const AttnParams &p, hipStream_t s) {
     if (lds + 1024 > max_lds_per_block())
         return set_error(GAJE_ERR_UNSUPPORTED, "attention: context capacity %lld exceeds the LDS score buffer",
                          (long long)p.kv_cap);
+    if (p.seq_pos && (p.n_seq <= 0 || p.n_seq > 65535)) return set_error(GAJE_ERR_INVALID_ARG, "attention: bad batch");
+    const unsigned nz = p.seq_pos ? (unsigned)p.n_seq : 1u;
     const int ds = (p.kv_cap % 4 == 0 && (p.head_dim == 64 || p.head_dim == 128)) ? fast_slice(p.head_dim, p.kv_cap) : 0;
     if (ds > 0) {
         const size_t flds = fast_lds_bytes(p.kv_cap, ds);
@@ -329,9 +349,9 @@ int launch_attention(const AttnParams &p, hipStream_t s) {
             fn = ds == 8 ? attn_decode_fast<64, 8> : ds == 4 ? attn_decode_fast<64, 4> : ds == 2 ? attn_decode_fast<64, 2> : attn_decode_fast<64, 1>;
         else
             fn = ds == 8 ? attn_decode_fast<128, 8> : ds == 4 ? attn_decode_fast<128, 4> : ds == 2 ? attn_decode_fast<128, 2> : attn_decode_fast<128, 1>;
-        hipLaunchKernelGGL(fn, dim3(p.n_head, p.head_dim / ds), dim3(THREADS), flds, s, p);
+        hipLaunchKernelGGL(fn, dim3(p.n_head, p.head_dim / ds, nz), dim3(THREADS), flds, s, p);
     } else {
-        hipLaunchKernelGGL(attn_decode_generic, dim3(p.n_head), dim3(THREADS), lds, s, p);
+        hipLaunchKernelGGL(attn_decode_generic, dim3(p.n_head, 1, nz), dim3(THREADS), lds, s, p);
     }
     GAJE_HIP_CHECK(hipGetLastError());
     return GAJE_OK;

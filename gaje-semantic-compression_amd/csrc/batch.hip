@@ -1,0 +1,450 @@
+// Batched decode: one token for each of up to 16 independent sequences per
+// step, as if as many GenomicLLM instances (llm/forward.rs:7-64) stepped
+// together over shared weights.  Every product and reduction follows the
+// batch-1 decode kernels' order, so each sequence's values are bit-identical
+// to its own forward_core: the weight rows are read and dequantised once per
+// step and consumed by every sequence's chains.
+#include <hip/hip_runtime.h>
+
+#include "common.h"
+#include "device_util.h"
+#include "kernels.h"
+
+namespace gaje {
+namespace {
+
+constexpr int BQ_CHUNK = 512;              // activation elements per staged chunk (4 packed groups)
+constexpr int BQ_CROW = BQ_CHUNK / 8 + 4;  // LDS floats per (vector, chain) row of a chunk
+
+__device__ __forceinline__ void seq_flag(uint32_t *codes, int s, int layer, int stage) {
+    if (codes && stage >= 0) atomicMin(&codes[s], (uint32_t)(layer * 8 + stage));
+}
+
+// dequantised values of one packed group for chain l (genomic.rs:298-316): d = fma(q, scale, min)
+__device__ __forceinline__ void group_dequant(float (&d)[16], vu2 n, vu4 s) {
+    const uint32_t c[4] = {opaque_and(n.x, 0x0F0F0F0Fu), opaque_and(n.x >> 4, 0x0F0F0F0Fu),
+                           opaque_and(n.y, 0x0F0F0F0Fu), opaque_and(n.y >> 4, 0x0F0F0F0Fu)};
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        const float scale = half_lo(s[b]), mn = half_hi(s[b]);
+        d[4 * b + 0] = fmaf(ubyte0(c[b]), scale, mn);
+        d[4 * b + 1] = fmaf(ubyte1(c[b]), scale, mn);
+        d[4 * b + 2] = fmaf(ubyte2(c[b]), scale, mn);
+        d[4 * b + 3] = fmaf(ubyte3(c[b]), scale, mn);
+    }
+}
+
+// Packed Q4_0 rows x NV activation vectors (genomic_dot_product_q4_0_avx2,
+// genomic.rs:263-336, per vector).  Lane = (row lane>>3 of the workgroup's
+// eight, chain l = lane&7); wave w owns vectors w*VPW.. (their accumulators);
+// the waves share the rows and the staged chunk of all vectors, kept
+// chain-major in LDS (element k of a chunk at chain k%8, column k/8).  The
+// chunks are double-buffered through registers; groups past the row's end
+// read as zero codes/scales against zero activations, and fma(0, 0, acc) =
+// acc (acc is never -0), so whole chunks run branch-free.
+template <int NV, int VPW>
+__global__ __launch_bounds__(NV / VPW * 64) void gemv_batch_q4_kernel(BatchGemvParams p) {
+    constexpr int NTH = NV / VPW * 64;
+    constexpr int BUF = NV * 8 * BQ_CROW;
+    constexpr int UPT = NV * (BQ_CHUNK / 8) / NTH;  // 8-element runs staged per thread per chunk
+    extern __shared__ __align__(16) float xs[];       // [2][NV][8][BQ_CROW]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l = lane & 7, base = lane & ~7;
+    const int64_t row = (int64_t)blockIdx.x * 8 + (lane >> 3);
+    const bool row_ok = row < p.N;
+    const int nb = p.nb, G = (nb + 3) >> 2;
+    const int64_t K = (int64_t)nb * 32;
+    const int nch = (int)((K + BQ_CHUNK - 1) / BQ_CHUNK);
+    const uint8_t *wr = p.w + (size_t)(row_ok ? row : p.N - 1) * G * 80;
+    const int v0 = wave * VPW;
+
+    float4 st[UPT][2];
+    auto load_chunk = [&](int c) {
+#pragma unroll
+        for (int i = 0; i < UPT; ++i) {
+            const int u = tid + i * NTH, v = u / (BQ_CHUNK / 8), m = u % (BQ_CHUNK / 8);
+            const int64_t k = (int64_t)c * BQ_CHUNK + 8 * m;
+            const bool in = k < K;
+            const float *src = p.x + (size_t)v * p.ldx + (in ? k : K - 8);
+            const float4 a = *(const float4 *)src, b = *(const float4 *)(src + 4);
+            const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+            st[i][0] = in ? a : z;
+            st[i][1] = in ? b : z;
+        }
+    };
+    auto store_chunk = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < UPT; ++i) {
+            const int u = tid + i * NTH, v = u / (BQ_CHUNK / 8), m = u % (BQ_CHUNK / 8);
+            float *dst = xs + buf * BUF + v * 8 * BQ_CROW + m;
+            dst[0 * BQ_CROW] = st[i][0].x;
+            dst[1 * BQ_CROW] = st[i][0].y;
+            dst[2 * BQ_CROW] = st[i][0].z;
+            dst[3 * BQ_CROW] = st[i][0].w;
+            dst[4 * BQ_CROW] = st[i][1].x;
+            dst[5 * BQ_CROW] = st[i][1].y;
+            dst[6 * BQ_CROW] = st[i][1].z;
+            dst[7 * BQ_CROW] = st[i][1].w;
+        }
+    };
+    vu2 wn[2][4];
+    vu4 ws[2][4];
+    auto load_w = [&](int c, int slot) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int g = 4 * c + i;
+            const bool in = g < G;
+            const uint8_t *gp = wr + (size_t)(in ? g : G - 1) * 80;
+            const vu2 n = *(const vu2 *)(gp + 8 * l);
+            const vu4 s = *(const vu4 *)(gp + 64);
+            const uint32_t keep = in ? 0xFFFFFFFFu : 0u;
+            wn[slot][i] = n & keep;
+            ws[slot][i] = s & keep;
+        }
+    };
+
+    float acc[VPW];
+#pragma unroll
+    for (int v = 0; v < VPW; ++v) acc[v] = 0.0f;
+
+    load_w(0, 0);
+    load_chunk(0);
+    store_chunk(0);
+    __syncthreads();
+    // one chunk from buffer `cur` (a constant at each call: the register rings
+    // are indexed statically)
+    auto chunk = [&](int c, int cur) {
+        const bool more = c + 1 < nch;
+        if (more) {
+            load_w(c + 1, cur ^ 1);
+            load_chunk(c + 1);
+        }
+        const float *xb = xs + cur * BUF + (v0 * 8 + l) * BQ_CROW;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float d[16];
+            group_dequant(d, wn[cur][i], ws[cur][i]);
+#pragma unroll
+            for (int v = 0; v < VPW; ++v) {
+                const float *xv = xb + v * 8 * BQ_CROW + 16 * i;
+                const float4 x0 = *(const float4 *)xv, x1 = *(const float4 *)(xv + 4);
+                const float4 x2 = *(const float4 *)(xv + 8), x3 = *(const float4 *)(xv + 12);
+                float a = acc[v];
+                a = fmaf(d[0], x0.x, a);
+                a = fmaf(d[1], x0.y, a);
+                a = fmaf(d[2], x0.z, a);
+                a = fmaf(d[3], x0.w, a);
+                a = fmaf(d[4], x1.x, a);
+                a = fmaf(d[5], x1.y, a);
+                a = fmaf(d[6], x1.z, a);
+                a = fmaf(d[7], x1.w, a);
+                a = fmaf(d[8], x2.x, a);
+                a = fmaf(d[9], x2.y, a);
+                a = fmaf(d[10], x2.z, a);
+                a = fmaf(d[11], x2.w, a);
+                a = fmaf(d[12], x3.x, a);
+                a = fmaf(d[13], x3.y, a);
+                a = fmaf(d[14], x3.z, a);
+                a = fmaf(d[15], x3.w, a);
+                acc[v] = a;
+            }
+            __builtin_amdgcn_sched_barrier(0);  // one group's LDS reads in flight at a time
+        }
+        if (more) store_chunk(cur ^ 1);
+        __syncthreads();
+    };
+    for (int c = 0; c < nch; c += 2) {
+        chunk(c, 0);
+        if (c + 1 < nch) chunk(c + 1, 1);
+    }
+
+    // per vector: ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) in lane l = 0, then the row epilogue
+#pragma unroll
+    for (int v = 0; v < VPW; ++v) {
+        const float a = acc[v];
+        const float u = a + __shfl(a, base + ((l + 4) & 7), WAVE);
+        const float w = u + __shfl(u, base + ((l + 2) & 7), WAVE);
+        const float t = w + __shfl(w, base + ((l + 1) & 7), WAVE);
+        const int s = v0 + v;
+        if (l != 0 || !row_ok || s >= p.nv) continue;
+        float y = flush_small(t);
+        if (p.a_ptr) {  // sparse anchors, then the bias (forward.rs:103-115)
+            for (int64_t k = p.a_ptr[row]; k < p.a_ptr[row + 1]; ++k) {
+                const float prod = p.x[(size_t)s * p.ldx + p.a_col[k]] * half_bits(p.a_val[k]);
+                y = y + prod;
+            }
+        }
+        if (row < p.bias_len) y = y + p.bias[row];
+        float *dst = p.y + (size_t)s * p.ldy + row;
+        if (p.mode == MODE_RESIDUAL) {
+            if (isnan(y)) seq_flag(p.nan_codes, s, p.layer, p.st_a);
+            const float h = *dst + y;
+            *dst = h;
+            if (isnan(h)) seq_flag(p.nan_codes, s, p.layer, p.st_b);
+        } else {
+            *dst = y;
+        }
+    }
+}
+
+// F32 rows in the tiled layout x NV vectors (dot_product, dot.rs:23-94, per
+// vector): lanes 2r, 2r+1 of a wave own row r of the wave's 32-row tile,
+// chains 0..3 and 4..7; each chunk of the tile is one coalesced KiB.  All NV
+// vectors sit in LDS in plain layout.
+template <int NV>
+__global__ __launch_bounds__(256) void gemv_batch_f32_kernel(BatchGemvParams p) {
+    extern __shared__ __align__(16) float xs[];  // [NV][K]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t K = p.K, K4 = K / 4;
+    for (int64_t i = tid; i < NV * K4; i += 256) {
+        const int64_t v = i / K4, q = i - v * K4;
+        *(float4 *)(xs + v * K + 4 * q) = *(const float4 *)(p.x + (size_t)v * p.ldx + 4 * q);
+    }
+    __syncthreads();
+    const int s = lane & 1;
+    const int64_t row = (int64_t)blockIdx.x * 128 + wave * 32 + (lane >> 1);
+    const bool row_ok = row < p.N;
+    const int64_t lrow = row_ok ? row : p.N - 1;
+    const float *wl = (const float *)p.w + (size_t)(lrow >> 5) * (size_t)K * 32 + (lrow & 31) * 8 + 4 * s;
+    const int64_t chunks = K / 8;
+    float acc[NV][4];
+#pragma unroll
+    for (int v = 0; v < NV; ++v) acc[v][0] = acc[v][1] = acc[v][2] = acc[v][3] = 0.0f;
+    constexpr int AHEAD = 8;
+    float4 ring[AHEAD];
+#pragma unroll
+    for (int u = 0; u < AHEAD; ++u) ring[u] = ld_f4<true>(wl + 256 * (u < chunks ? u : chunks - 1));
+    for (int64_t c0 = 0; c0 < chunks; c0 += AHEAD) {
+#pragma unroll
+        for (int u = 0; u < AHEAD; ++u) {
+            const int64_t c = c0 + u;
+            if (c >= chunks) break;
+            const float4 w = ring[u];
+            const int64_t cn = c + AHEAD < chunks ? c + AHEAD : chunks - 1;
+            ring[u] = ld_f4<true>(wl + 256 * cn);
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+                const float4 x = *(const float4 *)(xs + v * K + 8 * c + 4 * s);
+                acc[v][0] = fmaf(x.x, w.x, acc[v][0]);
+                acc[v][1] = fmaf(x.y, w.y, acc[v][1]);
+                acc[v][2] = fmaf(x.z, w.z, acc[v][2]);
+                acc[v][3] = fmaf(x.w, w.w, acc[v][3]);
+            }
+        }
+    }
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+        // lane 2r: chains 0..3, lane 2r+1: 4..7 -> ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7))
+        const float u0 = acc[v][0] + __shfl_xor(acc[v][0], 1, WAVE);
+        const float u1 = acc[v][1] + __shfl_xor(acc[v][1], 1, WAVE);
+        const float u2 = acc[v][2] + __shfl_xor(acc[v][2], 1, WAVE);
+        const float u3 = acc[v][3] + __shfl_xor(acc[v][3], 1, WAVE);
+        if (s != 0 || !row_ok || v >= p.nv) continue;
+        float y = (u0 + u1) + (u2 + u3);
+        if (row < p.bias_len) y = y + p.bias[row];
+        p.y[(size_t)v * p.ldy + row] = y;
+    }
+}
+
+// rms_norm per sequence row (norm.rs:52-88): threads 0..7 run the chains,
+// out = (x * inv) * w.  Guards: st_a on the input, st_b on the output.
+__global__ __launch_bounds__(256) void rmsnorm_rows_kernel(BatchRowParams p) {
+    extern __shared__ __align__(16) float xs[];
+    __shared__ float inv_slot;
+    const int s = blockIdx.x;
+    const int tid = threadIdx.x;
+    const float *x = p.x + (size_t)s * p.ldx;
+    int bad = 0;
+    for (int64_t k = tid; k < p.K; k += 256) {
+        const float v = x[k];
+        bad |= isnan(v);
+        xs[k] = v;
+    }
+    if (__syncthreads_or(bad) && tid == 0) seq_flag(p.nan_codes, s, p.layer, p.st_a);
+    rms_inv_plain(xs, p.K, p.eps, &inv_slot);
+    __syncthreads();
+    const float inv = inv_slot;
+    bad = 0;
+    for (int64_t k = tid; k < p.K; k += 256) {
+        const float t = xs[k] * inv;
+        const float o = t * p.w[k];
+        bad |= isnan(o);
+        p.y[(size_t)s * p.ldy + k] = o;
+    }
+    if (__syncthreads_or(bad) && tid == 0) seq_flag(p.nan_codes, s, p.layer, p.st_b);
+}
+
+// swiglu_balanced per element of each sequence's gate/up row pair
+// (block/forward.rs:87-113), with use_genomic_norm (:115-123) when set.
+__global__ __launch_bounds__(256) void swiglu_rows_kernel(BatchRowParams p) {
+    extern __shared__ __align__(16) float xs[];
+    __shared__ float rms_slot;
+    const int s = blockIdx.x;
+    const int tid = threadIdx.x;
+    const float *g = p.x + (size_t)s * p.ldx, *u = g + p.K;
+    int bad_u = 0, bad_o = 0;
+    for (int64_t k = tid; k < p.K; k += 256) {
+        const float uv = u[k];
+        bad_u |= isnan(uv);
+        const float o = swiglu1(g[k], uv);
+        bad_o |= isnan(o);
+        xs[k] = o;
+    }
+    const bool any_u = __syncthreads_or(bad_u);
+    const bool any_o = __syncthreads_or(bad_o);
+    if (tid == 0) {
+        if (any_u) seq_flag(p.nan_codes, s, p.layer, p.st_a);
+        if (any_o) seq_flag(p.nan_codes, s, p.layer, p.st_b);
+    }
+    float sc = 1.0f;
+    if (p.gnorm) {
+        if (tid == 0) {
+            float ss = 0.0f;
+            for (int64_t k = 0; k < p.K; ++k) {
+                const float sq = xs[k] * xs[k];
+                ss = ss + sq;
+            }
+            rms_slot = sqrtf(ss / (float)p.K + p.eps);
+        }
+        __syncthreads();
+        const float rms = rms_slot;
+        if (rms > p.h_scale) sc = p.h_scale / rms;
+    }
+    for (int64_t k = tid; k < p.K; k += 256) p.y[(size_t)s * p.ldy + k] = p.gnorm ? xs[k] * sc : xs[k];
+}
+
+// Greedy argmax per sequence (llm/forward.rs:262-271: strict '>', so the first
+// maximum; NaN never wins; all-NaN gives 0).
+__global__ __launch_bounds__(1024) void argmax_rows_kernel(const float *x, int64_t n, int64_t ld, uint32_t *out) {
+    __shared__ unsigned long long best[16];
+    const int s = blockIdx.x;
+    const int tid = threadIdx.x;
+    unsigned long long key = 0ull;
+    for (int64_t i = tid; i < n; i += 1024) {
+        const float v = x[(size_t)s * ld + i];
+        if (isnan(v)) continue;
+        const unsigned long long k = ((unsigned long long)order_key(v) << 32) | (0xFFFFFFFFu - (uint32_t)i);
+        key = k > key ? k : key;
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        const unsigned long long other = __shfl_xor(key, o, WAVE);
+        key = other > key ? other : key;
+    }
+    if ((tid & 63) == 0) best[tid >> 6] = key;
+    __syncthreads();
+    if (tid == 0) {
+        unsigned long long k = best[0];
+        for (int w = 1; w < 16; ++w) k = best[w] > k ? best[w] : k;
+        out[s] = k ? 0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull) : 0u;
+    }
+}
+
+// Start of a step: sequence s takes token ids[s * n + i] (forced tokens) or
+// keeps tok[s] (its previous greedy output); it runs at its cached length
+// unless it is past nseq, halted, or fed the inactive id.
+__global__ void batch_begin_kernel(BatchState b, const uint32_t *ids, int64_t n, int64_t i) {
+    const int s = threadIdx.x;
+    if (s >= b.lanes) return;
+    uint32_t t = b.tok[s];
+    if (ids && s < b.nseq) t = ids[(size_t)s * n + i];
+    b.tok[s] = t;
+    const bool run = s < b.nseq && !b.halted[s] && t != BATCH_INACTIVE;
+    b.cur_pos[s] = run ? b.pos[s] : -1;
+    b.nan_codes[s] = NAN_NONE;
+    b.embed_ids[s] = run ? t : 0u;
+}
+
+// End of a step: a sequence whose guards held advances and (greedy) feeds its
+// argmax back; one whose guard fired halts with the stage code.
+__global__ void batch_end_kernel(BatchState b, uint32_t *out, int64_t n, int64_t i, int greedy) {
+    const int s = threadIdx.x;
+    if (s >= b.nseq || b.cur_pos[s] < 0) return;
+    if (b.nan_codes[s] != NAN_NONE) {
+        b.halted[s] = 1;
+        b.err[s] = b.nan_codes[s];
+        return;
+    }
+    b.pos[s] += 1;
+    const uint32_t nx = b.next[s];
+    if (greedy) b.tok[s] = nx;
+    if (out) out[(size_t)s * n + i] = nx;
+}
+
+template <int NV, int VPW>
+int launch_q4(const BatchGemvParams &p, hipStream_t s) {
+    const size_t lds = (size_t)2 * NV * 8 * BQ_CROW * 4;
+    hipLaunchKernelGGL((gemv_batch_q4_kernel<NV, VPW>), dim3((unsigned)((p.N + 7) / 8)), dim3(NV / VPW * 64), lds, s, p);
+    GAJE_HIP_CHECK(hipGetLastError());
+    return GAJE_OK;
+}
+
+template <int NV>
+int launch_f32(const BatchGemvParams &p, hipStream_t s) {
+    const size_t lds = (size_t)NV * p.K * 4;
+    if (lds + 1024 > max_lds_per_block())
+        return set_error(GAJE_ERR_UNSUPPORTED, "batched f32 matvec: %d x %lld activations exceed LDS", NV, (long long)p.K);
+    hipLaunchKernelGGL((gemv_batch_f32_kernel<NV>), dim3((unsigned)((p.N + 127) / 128)), dim3(256), lds, s, p);
+    GAJE_HIP_CHECK(hipGetLastError());
+    return GAJE_OK;
+}
+
+}  // namespace
+
+int batch_lanes(int64_t n) { return n <= 4 ? 4 : n <= 8 ? 8 : 16; }
+
+int launch_gemv_batch(const BatchGemvParams &p, hipStream_t s) {
+    if (!p.w || !p.x || !p.y || p.N <= 0 || p.nv <= 0 || p.nv > 16 || p.ldx < p.K || p.ldy < p.N)
+        return set_error(GAJE_ERR_INVALID_ARG, "batched matvec: bad arguments");
+    const int nv = batch_lanes(p.nv);
+    if (p.fmt == FMT_Q4_0) {
+        if (p.nb <= 0 || (int64_t)p.nb * 32 != p.K) return set_error(GAJE_ERR_INVALID_ARG, "batched matvec: bad K");
+        if (nv == 4) return launch_q4<4, 4>(p, s);
+        if (nv == 8) return launch_q4<8, 4>(p, s);
+        return launch_q4<16, 4>(p, s);
+    }
+    if (p.fmt == FMT_F32) {
+        if (!p.f32_tiled || p.K % 8) return set_error(GAJE_ERR_UNSUPPORTED, "batched matvec: f32 rows must be tiled");
+        if (p.mode != MODE_STORE) return set_error(GAJE_ERR_UNSUPPORTED, "batched matvec: f32 rows store only");
+        if (nv == 4) return launch_f32<4>(p, s);
+        if (nv == 8) return launch_f32<8>(p, s);
+        return launch_f32<16>(p, s);
+    }
+    return set_error(GAJE_ERR_UNSUPPORTED, "batched matvec: weight format %d", p.fmt);
+}
+
+int launch_rmsnorm_rows(const BatchRowParams &p, hipStream_t s) {
+    if (!p.x || !p.y || !p.w || p.K <= 0 || p.nv <= 0) return set_error(GAJE_ERR_INVALID_ARG, "rmsnorm rows: bad arguments");
+    if ((size_t)p.K * 4 + 1024 > max_lds_per_block()) return set_error(GAJE_ERR_UNSUPPORTED, "rmsnorm rows: K too large");
+    hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3((unsigned)p.nv), dim3(256), (size_t)p.K * 4, s, p);
+    GAJE_HIP_CHECK(hipGetLastError());
+    return GAJE_OK;
+}
+
+int launch_swiglu_rows(const BatchRowParams &p, hipStream_t s) {
+    if (!p.x || !p.y || p.K <= 0 || p.nv <= 0) return set_error(GAJE_ERR_INVALID_ARG, "swiglu rows: bad arguments");
+    if ((size_t)p.K * 4 + 1024 > max_lds_per_block()) return set_error(GAJE_ERR_UNSUPPORTED, "swiglu rows: K too large");
+    hipLaunchKernelGGL(swiglu_rows_kernel, dim3((unsigned)p.nv), dim3(256), (size_t)p.K * 4, s, p);
+    GAJE_HIP_CHECK(hipGetLastError());
+    return GAJE_OK;
+}
+
+int launch_batch_begin(const BatchState &b, const uint32_t *ids, int64_t n, int64_t i, hipStream_t s) {
+    hipLaunchKernelGGL(batch_begin_kernel, dim3(1), dim3(64), 0, s, b, ids, n, i);
+    GAJE_HIP_CHECK(hipGetLastError());
+    return GAJE_OK;
+}
+
+int launch_batch_end(const BatchState &b, uint32_t *out, int64_t n, int64_t i, int greedy, hipStream_t s) {
+    hipLaunchKernelGGL(batch_end_kernel, dim3(1), dim3(64), 0, s, b, out, n, i, greedy);
+    GAJE_HIP_CHECK(hipGetLastError());
+    return GAJE_OK;
+}
+
+int launch_argmax_rows(const float *x, int64_t n, int64_t ld, int64_t rows, uint32_t *out, hipStream_t s) {
+    if (!x || !out || n <= 0 || rows <= 0 || n > 0xFFFFFFFFll) return set_error(GAJE_ERR_INVALID_ARG, "argmax rows: bad arguments");
+    hipLaunchKernelGGL(argmax_rows_kernel, dim3((unsigned)rows), dim3(1024), 0, s, x, n, ld, out);
+    GAJE_HIP_CHECK(hipGetLastError());
+    return GAJE_OK;
+}
+
+}  // namespace gaje

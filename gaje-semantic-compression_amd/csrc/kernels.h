@@ -124,6 +124,12 @@ struct AttnParams {
     float *out;              // [n_head * head_dim]
     DevState *st;            // positions 0..st->pos are attended; if null, 0..ctx-1
     int64_t ctx;
+    // batched decode (seq_pos non-null): blockIdx.z = sequence z attends to
+    // positions 0..seq_pos[z] of its own cache (k/v_cache + z * seq_kv_stride);
+    // its q and out rows are z * seq_q_stride floats on; seq_pos[z] < 0 skips it
+    const int32_t *seq_pos;
+    int64_t seq_kv_stride, seq_q_stride;
+    int32_t n_seq;
 };
 int launch_attention(const AttnParams &p, hipStream_t s);
 size_t attention_lds_bytes(int head_dim, int64_t max_ctx);
@@ -210,6 +216,10 @@ struct PrefillRopeParams {
     int64_t cap, pos0, P;
     int32_t n_head, n_kv, head_dim, rope_split;
     const float *rope_cos, *rope_sin;  // [cap][head_dim / 2]
+    // batched decode: row t is sequence t at position seq_pos[t] (< 0: skipped)
+    // of its own cache (k/v_cache + t * seq_kv_stride); pos0 unused
+    const int32_t *seq_pos;
+    int64_t seq_kv_stride;
 };
 int launch_rope_kv(const PrefillRopeParams &p, hipStream_t s);
 // Causal GQA attention of P queries (positions pos0..) over the cache.
@@ -221,6 +231,64 @@ struct PrefillAttnParams {
     float *out;              // [P][n_head * head_dim]
 };
 int launch_prefill_attention(const PrefillAttnParams &p, hipStream_t s);
+
+// Batched decode: NV (<= 16) activation vectors per matvec, each product in
+// the batch-1 order (bit-identical per vector).
+struct BatchGemvParams {
+    const uint8_t *w;        // FMT_Q4_0 packed rows, or FMT_F32 tiled rows
+    int32_t fmt;
+    int32_t f32_tiled;
+    int32_t nb;              // K / 32 (Q4_0)
+    int64_t N, K;
+    const float *x;          // [nv][ldx]
+    int64_t ldx;
+    int32_t nv;              // vectors (sequences)
+    const float *bias;
+    int64_t bias_len;
+    const int64_t *a_ptr;    // sparse anchors (Q4_0 only) or null
+    const uint32_t *a_col;
+    const uint16_t *a_val;
+    int32_t mode;            // MODE_STORE or MODE_RESIDUAL (y += row result)
+    float *y;                // [nv][ldy]
+    int64_t ldy;
+    uint32_t *nan_codes;     // [nv] min(layer * 8 + stage) of failed guards, or null
+    int32_t layer, st_a, st_b;
+};
+int launch_gemv_batch(const BatchGemvParams &p, hipStream_t s);
+// Activation lanes a batch of n sequences is padded to (4, 8 or 16).
+int batch_lanes(int64_t n);
+// Per-sequence row passes of the batched step.
+struct BatchRowParams {
+    const float *x;          // [nv][ldx] (swiglu: gate | up rows of K each)
+    int64_t ldx;
+    float *y;                // [nv][ldy]
+    int64_t ldy;
+    const float *w;          // rms_norm weight [K]
+    int64_t K;
+    int32_t nv;
+    float eps, h_scale;
+    int32_t gnorm;
+    uint32_t *nan_codes;
+    int32_t layer, st_a, st_b;
+};
+int launch_rmsnorm_rows(const BatchRowParams &p, hipStream_t s);
+int launch_swiglu_rows(const BatchRowParams &p, hipStream_t s);
+int launch_argmax_rows(const float *x, int64_t n, int64_t ld, int64_t rows, uint32_t *out, hipStream_t s);
+// Device-side per-sequence state of a batched decode (arrays of `lanes`).
+constexpr uint32_t BATCH_INACTIVE = 0xFFFFFFFFu;
+struct BatchState {
+    int32_t nseq, lanes;
+    int32_t *pos;            // cached length per sequence
+    int32_t *cur_pos;        // this step's position, -1 = not stepping
+    int32_t *halted;         // a guard fired: the sequence stops
+    uint32_t *err;           // the stage code that halted it
+    uint32_t *tok;           // this step's token (greedy: the previous argmax)
+    uint32_t *embed_ids;     // embedding row ids of this step (0 for idle lanes)
+    uint32_t *next;          // argmax of this step's logits
+    uint32_t *nan_codes;     // guards of this step
+};
+int launch_batch_begin(const BatchState &b, const uint32_t *ids, int64_t n, int64_t i, hipStream_t s);
+int launch_batch_end(const BatchState &b, uint32_t *out, int64_t n, int64_t i, int greedy, hipStream_t s);
 
 int launch_finalize(DevState *st, uint32_t *out_tokens, hipStream_t s);
 int launch_kwta(float *x, int64_t n, int64_t k, DevState *st, hipStream_t s);

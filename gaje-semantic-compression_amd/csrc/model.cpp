@@ -534,7 +534,7 @@ int enqueue_token(gaje_hip_model *m, hipEvent_t ev_blocks_done) {
         p.kv_cap = m->cap;
         GAJE_TRY(launch_gemv(p, m->stream));
 
-        AttnParams ap;
+        AttnParams ap{};
         ap.q = m->q;
         ap.k_cache = m->k_cache + l * layer_kv;
         ap.v_cache = m->v_cache + l * layer_kv;
@@ -1139,6 +1139,376 @@ extern "C" int gaje_hip_prefill_mfma(gaje_hip_model *m, const uint32_t *ids, int
     return GAJE_OK;
 }
 
+// ------------------------------------------------------------ batched decode --
+
+struct gaje_hip_batch {
+    gaje_hip_model *m = nullptr;
+    int64_t nseq = 0, lanes = 0, cap = 0;
+    float *k_cache = nullptr, *v_cache = nullptr;  // [layer][seq][n_kv][head_dim][cap]
+    float *rope_cos = nullptr, *rope_sin = nullptr;
+    float *H = nullptr, *XN = nullptr, *QKV = nullptr, *Q = nullptr, *ATT = nullptr, *GU = nullptr, *ACT = nullptr,
+          *LOG = nullptr;
+    uint32_t *ids = nullptr, *out = nullptr;  // fed tokens / greedy outputs [seq][n]
+    int64_t ids_cap = 0, out_cap = 0;
+    BatchState st{};
+    std::vector<int32_t> pos;  // host mirror of st.pos
+    std::vector<void *> allocs;
+
+    ~gaje_hip_batch() {
+        for (void *p : allocs) (void)hipFree(p);
+    }
+    template <class T>
+    int alloc(T **p, size_t count) {
+        *p = nullptr;
+        if (count == 0) return GAJE_OK;
+        void *v = nullptr;
+        GAJE_HIP_CHECK(hipMalloc(&v, count * sizeof(T)));
+        allocs.push_back(v);
+        *p = (T *)v;
+        return GAJE_OK;
+    }
+    void release(void *p) {
+        for (auto it = allocs.begin(); it != allocs.end(); ++it)
+            if (*it == p) {
+                (void)hipFree(p);
+                allocs.erase(it);
+                return;
+            }
+    }
+};
+
+namespace {
+
+int batch_supported(const gaje_hip_model *m) {
+    for (const Layer &Ly : m->layers)
+        for (const DevLinear *D : {&Ly.qkv, &Ly.o, &Ly.gate_up, &Ly.down})
+            if (D->fmt != FMT_Q4_0 || D->rows_valid != D->N)
+                return set_error(GAJE_ERR_UNSUPPORTED, "batched decode needs complete Q4_0 body tensors");
+    const DevLinear &H = m->lm_head;
+    if (H.fmt != FMT_F32 || !H.f32_tiled || H.rows_valid != H.N || H.a_ptr)
+        return set_error(GAJE_ERR_UNSUPPORTED, "batched decode needs an f32 lm_head (K %% 8 == 0) without anchors");
+    return GAJE_OK;
+}
+
+BatchGemvParams batch_gemv(const gaje_hip_batch *b, const DevLinear &D, const float *x, int64_t ldx, float *y,
+                           int64_t ldy) {
+    BatchGemvParams p{};
+    p.w = D.w;
+    p.fmt = D.fmt;
+    p.f32_tiled = D.f32_tiled;
+    p.nb = (int32_t)(D.K / 32);
+    p.N = D.N;
+    p.K = D.K;
+    p.x = x;
+    p.ldx = ldx;
+    p.nv = (int32_t)b->lanes;
+    p.bias = D.bias;
+    p.bias_len = D.bias_len;
+    p.a_ptr = D.a_ptr;
+    p.a_col = D.a_col;
+    p.a_val = D.a_val;
+    p.mode = MODE_STORE;
+    p.y = y;
+    p.ldy = ldy;
+    p.nan_codes = b->st.nan_codes;
+    p.st_a = p.st_b = ST_NONE;
+    return p;
+}
+
+BatchRowParams batch_rows(const gaje_hip_batch *b, const float *x, int64_t ldx, float *y, int64_t ldy, int64_t K) {
+    BatchRowParams r{};
+    r.x = x;
+    r.ldx = ldx;
+    r.y = y;
+    r.ldy = ldy;
+    r.K = K;
+    r.nv = (int32_t)b->lanes;
+    r.eps = b->m->eps;
+    r.h_scale = 1.0f;
+    r.nan_codes = b->st.nan_codes;
+    r.st_a = r.st_b = ST_NONE;
+    return r;
+}
+
+// One step of every running sequence (the batched counterpart of enqueue_token).
+int batch_enqueue_step(gaje_hip_batch *b, const uint32_t *ids, int64_t n, int64_t i, uint32_t *out, bool greedy) {
+    gaje_hip_model *m = b->m;
+    hipStream_t s = m->stream;
+    const int64_t L = b->lanes, E = m->n_embd;
+    GAJE_TRY(launch_batch_begin(b->st, ids, n, i, s));
+    EmbedParams ep;
+    memset(&ep, 0, sizeof ep);
+    ep.w = m->embd.w;
+    ep.fmt = m->embd.fmt;
+    ep.lut = m->embd.lut;
+    ep.lut_rows_own = m->embd.lut_rows_own;
+    ep.lut_block_stride = m->embd.lut_block_stride;
+    ep.vocab = m->vocab_embd;
+    ep.rows_valid = m->embd.rows_valid;
+    ep.K = E;
+    ep.h = b->H;
+    GAJE_TRY(launch_embed_rows(ep, b->st.embed_ids, L, s));
+    const int64_t seq_kv = m->n_kv * m->hd * b->cap;
+    const int64_t qkvN = m->layers.empty() ? 0 : m->layers[0].qkv.N, guN = m->layers.empty() ? 0 : m->layers[0].gate_up.N;
+    for (int64_t l = 0; l < m->n_layers; ++l) {
+        Layer &Ly = m->layers[l];
+        const int32_t li = (int32_t)l;
+        float *kc = b->k_cache + l * b->nseq * seq_kv, *vc = b->v_cache + l * b->nseq * seq_kv;
+        if (Ly.attn_norm) {
+            BatchRowParams r = batch_rows(b, b->H, E, b->XN, E, E);
+            r.w = Ly.attn_norm;
+            r.layer = li;
+            r.st_a = ST_INPUT;
+            r.st_b = ST_ATTN_NORM;
+            GAJE_TRY(launch_rmsnorm_rows(r, s));
+        } else {
+            GAJE_HIP_CHECK(hipMemcpyAsync(b->XN, b->H, (size_t)(L * E) * 4, hipMemcpyDeviceToDevice, s));
+        }
+        GAJE_TRY(launch_gemv_batch(batch_gemv(b, Ly.qkv, b->XN, E, b->QKV, qkvN), s));
+        PrefillRopeParams rp{};
+        rp.qkv = b->QKV;
+        rp.ldq = qkvN;
+        rp.q_out = b->Q;
+        rp.k_cache = kc;
+        rp.v_cache = vc;
+        rp.cap = b->cap;
+        rp.P = L;
+        rp.n_head = (int32_t)m->n_head;
+        rp.n_kv = (int32_t)m->n_kv;
+        rp.head_dim = (int32_t)m->hd;
+        rp.rope_split = m->rope_split;
+        rp.rope_cos = b->rope_cos;
+        rp.rope_sin = b->rope_sin;
+        rp.seq_pos = b->st.cur_pos;
+        rp.seq_kv_stride = seq_kv;
+        GAJE_TRY(launch_rope_kv(rp, s));
+        AttnParams ap{};
+        ap.q = b->Q;
+        ap.k_cache = kc;
+        ap.v_cache = vc;
+        ap.kv_head_stride = b->cap * m->hd;
+        ap.n_head = (int32_t)m->n_head;
+        ap.n_head_kv = (int32_t)m->n_kv;
+        ap.head_dim = (int32_t)m->hd;
+        ap.kv_cap = b->cap;
+        ap.out = b->ATT;
+        ap.seq_pos = b->st.cur_pos;
+        ap.seq_kv_stride = seq_kv;
+        ap.seq_q_stride = m->q_rows;
+        ap.n_seq = (int32_t)b->nseq;
+        GAJE_TRY(launch_attention(ap, s));
+        BatchGemvParams g = batch_gemv(b, Ly.o, b->ATT, m->q_rows, b->H, E);
+        g.mode = MODE_RESIDUAL;
+        GAJE_TRY(launch_gemv_batch(g, s));
+        BatchRowParams r = batch_rows(b, b->H, E, b->XN, E, E);
+        r.w = Ly.ffn_norm;
+        GAJE_TRY(launch_rmsnorm_rows(r, s));
+        GAJE_TRY(launch_gemv_batch(batch_gemv(b, Ly.gate_up, b->XN, E, b->GU, guN), s));
+        r = batch_rows(b, b->GU, guN, b->ACT, m->ffn, m->ffn);
+        r.gnorm = m->use_genomic_norm;
+        r.layer = li;
+        r.st_a = ST_UP;
+        r.st_b = ST_FFN_OUT;
+        GAJE_TRY(launch_swiglu_rows(r, s));
+        g = batch_gemv(b, Ly.down, b->ACT, m->ffn, b->H, E);
+        g.mode = MODE_RESIDUAL;
+        g.layer = li;
+        g.st_a = ST_PROJ_FFN;
+        g.st_b = ST_FINAL;
+        GAJE_TRY(launch_gemv_batch(g, s));
+        if (m->block_kwta_ratio > 0.0f && m->block_kwta_ratio < 1.0f) {
+            const int64_t k = kwta_k(E, m->block_kwta_ratio);
+            for (int64_t q = 0; q < b->nseq; ++q) GAJE_TRY(launch_kwta(b->H + q * E, E, k, nullptr, s));
+        }
+    }
+    BatchRowParams r = batch_rows(b, b->H, E, b->XN, E, E);
+    r.w = m->output_norm;
+    GAJE_TRY(launch_rmsnorm_rows(r, s));
+    GAJE_TRY(launch_gemv_batch(batch_gemv(b, m->lm_head, b->XN, E, b->LOG, m->vocab_out), s));
+    GAJE_TRY(launch_argmax_rows(b->LOG, m->vocab_out, m->vocab_out, b->nseq, b->st.next, s));
+    return launch_batch_end(b->st, out, n, i, greedy ? 1 : 0, s);
+}
+
+// Reads the device state back; a sequence halted by a guard reports the
+// reference's message (the first such sequence's).
+int batch_sync(gaje_hip_batch *b, int32_t *status) {
+    std::vector<int32_t> halted((size_t)b->lanes);
+    std::vector<uint32_t> err((size_t)b->lanes);
+    hipStream_t s = b->m->stream;
+    GAJE_HIP_CHECK(hipMemcpyAsync(b->pos.data(), b->st.pos, (size_t)b->lanes * 4, hipMemcpyDeviceToHost, s));
+    GAJE_HIP_CHECK(hipMemcpyAsync(halted.data(), b->st.halted, (size_t)b->lanes * 4, hipMemcpyDeviceToHost, s));
+    GAJE_HIP_CHECK(hipMemcpyAsync(err.data(), b->st.err, (size_t)b->lanes * 4, hipMemcpyDeviceToHost, s));
+    GAJE_HIP_CHECK(hipStreamSynchronize(s));
+    int first = -1;
+    for (int64_t q = 0; q < b->nseq; ++q) {
+        if (status) status[q] = halted[q] ? (int32_t)(err[q] % 8) + 1 : 0;
+        if (halted[q] && first < 0) first = (int)q;
+    }
+    if (first >= 0) return set_error(GAJE_ERR_NAN, "%s", nan_message((int)(err[first] % 8)));
+    return GAJE_OK;
+}
+
+int batch_check(gaje_hip_batch *b, int64_t steps) {
+    if (!b || !b->m) return set_error(GAJE_ERR_INVALID_ARG, "null batch handle");
+    GAJE_HIP_CHECK(hipSetDevice(b->m->device));
+    for (int64_t q = 0; q < b->nseq; ++q)
+        if (b->pos[q] + steps > b->cap)
+            return set_error(GAJE_ERR_INVALID_ARG, "sequence %lld: %lld cached + %lld steps exceed the capacity %lld",
+                             (long long)q, (long long)b->pos[q], (long long)steps, (long long)b->cap);
+    return GAJE_OK;
+}
+
+}  // namespace
+
+extern "C" int gaje_hip_batch_open(gaje_hip_model *m, int64_t n_seq, int64_t capacity, gaje_hip_batch **out) {
+    clear_error();
+    GAJE_TRY(check_model(m));
+    if (!out) return set_error(GAJE_ERR_INVALID_ARG, "null output");
+    *out = nullptr;
+    if (n_seq < 1 || n_seq > 16) return set_error(GAJE_ERR_INVALID_ARG, "batch of %lld sequences (1..16)", (long long)n_seq);
+    if (capacity < 1 || capacity > MAX_CTX)
+        return set_error(GAJE_ERR_INVALID_ARG, "capacity %lld outside 1..%lld", (long long)capacity, (long long)MAX_CTX);
+    GAJE_TRY(batch_supported(m));
+    std::unique_ptr<gaje_hip_batch> b(new gaje_hip_batch());
+    b->m = m;
+    b->nseq = n_seq;
+    b->lanes = batch_lanes(n_seq);
+    b->cap = (capacity + 63) / 64 * 64;
+    b->cap = std::min<int64_t>(b->cap, MAX_CTX);
+    const int64_t L = b->lanes, E = m->n_embd;
+    const size_t kv = (size_t)std::max<int64_t>(m->n_layers, 1) * n_seq * m->n_kv * m->hd * b->cap;
+    GAJE_TRY(b->alloc(&b->k_cache, kv));
+    GAJE_TRY(b->alloc(&b->v_cache, kv));
+    {
+        // the decode path's RoPE table (build_rope) at this capacity
+        const int64_t half = m->hd / 2;
+        std::vector<float> c((size_t)(b->cap * half)), sn((size_t)(b->cap * half));
+        for (int64_t i = 0; i < half; ++i) {
+            const float expo = (2.0f * (float)i) / (float)m->hd;
+            const float freq = 1.0f / powf(m->rope_base, expo);
+            for (int64_t p = 0; p < b->cap; ++p) {
+                const float theta = (float)p * freq;
+                c[p * half + i] = cosf(theta);
+                sn[p * half + i] = sinf(theta);
+            }
+        }
+        GAJE_TRY(b->alloc(&b->rope_cos, c.size()));
+        GAJE_TRY(b->alloc(&b->rope_sin, sn.size()));
+        GAJE_HIP_CHECK(hipMemcpy(b->rope_cos, c.data(), c.size() * 4, hipMemcpyHostToDevice));
+        GAJE_HIP_CHECK(hipMemcpy(b->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
+    }
+    const int64_t qkvN = m->layers.empty() ? 1 : m->layers[0].qkv.N, guN = m->layers.empty() ? 2 : m->layers[0].gate_up.N;
+    const int64_t qn = std::max<int64_t>(m->q_rows, 1), ffn = std::max<int64_t>(m->ffn, 1);
+    GAJE_TRY(b->alloc(&b->H, (size_t)(L * E)));
+    GAJE_TRY(b->alloc(&b->XN, (size_t)(L * E)));
+    GAJE_TRY(b->alloc(&b->QKV, (size_t)(L * qkvN)));
+    GAJE_TRY(b->alloc(&b->Q, (size_t)(L * qn)));
+    GAJE_TRY(b->alloc(&b->ATT, (size_t)(L * qn)));
+    GAJE_TRY(b->alloc(&b->GU, (size_t)(L * guN)));
+    GAJE_TRY(b->alloc(&b->ACT, (size_t)(L * ffn)));
+    GAJE_TRY(b->alloc(&b->LOG, (size_t)(L * m->vocab_out)));
+    // rows of idle lanes are computed and discarded; zeroed, they stay finite
+    GAJE_HIP_CHECK(hipMemset(b->H, 0, (size_t)(L * E) * 4));
+    GAJE_HIP_CHECK(hipMemset(b->XN, 0, (size_t)(L * E) * 4));
+    GAJE_HIP_CHECK(hipMemset(b->QKV, 0, (size_t)(L * qkvN) * 4));
+    GAJE_HIP_CHECK(hipMemset(b->Q, 0, (size_t)(L * qn) * 4));
+    GAJE_HIP_CHECK(hipMemset(b->ATT, 0, (size_t)(L * qn) * 4));
+    GAJE_HIP_CHECK(hipMemset(b->GU, 0, (size_t)(L * guN) * 4));
+    GAJE_HIP_CHECK(hipMemset(b->ACT, 0, (size_t)(L * ffn) * 4));
+    BatchState &st = b->st;
+    st.nseq = (int32_t)n_seq;
+    st.lanes = (int32_t)L;
+    GAJE_TRY(b->alloc(&st.pos, (size_t)L));
+    GAJE_TRY(b->alloc(&st.cur_pos, (size_t)L));
+    GAJE_TRY(b->alloc(&st.halted, (size_t)L));
+    GAJE_TRY(b->alloc(&st.err, (size_t)L));
+    GAJE_TRY(b->alloc(&st.tok, (size_t)L));
+    GAJE_TRY(b->alloc(&st.embed_ids, (size_t)L));
+    GAJE_TRY(b->alloc(&st.next, (size_t)L));
+    GAJE_TRY(b->alloc(&st.nan_codes, (size_t)L));
+    for (void *p : {(void *)st.pos, (void *)st.cur_pos, (void *)st.halted, (void *)st.err, (void *)st.tok,
+                    (void *)st.embed_ids, (void *)st.next})
+        GAJE_HIP_CHECK(hipMemset(p, 0, (size_t)L * 4));
+    b->pos.assign((size_t)L, 0);
+    *out = b.release();
+    return GAJE_OK;
+}
+
+extern "C" void gaje_hip_batch_close(gaje_hip_batch *b) {
+    if (!b) return;
+    (void)hipSetDevice(b->m->device);
+    (void)hipStreamSynchronize(b->m->stream);
+    delete b;
+}
+
+extern "C" int gaje_hip_batch_reset(gaje_hip_batch *b, int64_t seq) {
+    clear_error();
+    GAJE_TRY(batch_check(b, 0));
+    if (seq < -1 || seq >= b->nseq) return set_error(GAJE_ERR_INVALID_ARG, "sequence %lld out of range", (long long)seq);
+    for (int64_t q = 0; q < b->nseq; ++q)
+        if (seq < 0 || q == seq) {
+            const int32_t zero = 0;
+            GAJE_HIP_CHECK(hipMemcpyAsync(b->st.pos + q, &zero, 4, hipMemcpyHostToDevice, b->m->stream));
+            GAJE_HIP_CHECK(hipMemcpyAsync(b->st.halted + q, &zero, 4, hipMemcpyHostToDevice, b->m->stream));
+            GAJE_HIP_CHECK(hipStreamSynchronize(b->m->stream));
+            b->pos[q] = 0;
+        }
+    return GAJE_OK;
+}
+
+extern "C" int gaje_hip_batch_cache_len(const gaje_hip_batch *b, int64_t seq, int64_t *len) {
+    if (!b || !len || seq < 0 || seq >= b->nseq) return set_error(GAJE_ERR_INVALID_ARG, "bad arguments");
+    *len = b->pos[seq];
+    return GAJE_OK;
+}
+
+extern "C" int gaje_hip_batch_feed(gaje_hip_batch *b, const uint32_t *ids, int64_t n, float *last_logits_host,
+                                   int32_t *status) {
+    clear_error();
+    GAJE_TRY(batch_check(b, n));
+    if (n < 0 || (n > 0 && !ids)) return set_error(GAJE_ERR_INVALID_ARG, "bad feed arguments");
+    if (n == 0) return GAJE_OK;
+    gaje_hip_model *m = b->m;
+    hipStream_t s = m->stream;
+    const size_t need = (size_t)(b->nseq * n);
+    if ((int64_t)need > b->ids_cap) {
+        if (b->ids) b->release(b->ids);
+        GAJE_TRY(b->alloc(&b->ids, need));
+        b->ids_cap = (int64_t)need;
+    }
+    GAJE_HIP_CHECK(hipMemcpyAsync(b->ids, ids, need * 4, hipMemcpyHostToDevice, s));
+    for (int64_t i = 0; i < n; ++i) GAJE_TRY(batch_enqueue_step(b, b->ids, n, i, nullptr, false));
+    if (last_logits_host && m->kwta_ratio > 0.0f && m->kwta_ratio < 1.0f)
+        for (int64_t q = 0; q < b->nseq; ++q)
+            GAJE_TRY(launch_kwta(b->LOG + q * m->vocab_out, m->vocab_out, kwta_k(m->vocab_out, m->kwta_ratio), nullptr, s));
+    const int rc = batch_sync(b, status);
+    if (last_logits_host)
+        GAJE_HIP_CHECK(hipMemcpy(last_logits_host, b->LOG, (size_t)(b->nseq * m->vocab_out) * 4, hipMemcpyDeviceToHost));
+    return rc;
+}
+
+extern "C" int gaje_hip_batch_decode_greedy(gaje_hip_batch *b, const uint32_t *first, int64_t n, uint32_t *out_tokens,
+                                            int32_t *status) {
+    clear_error();
+    GAJE_TRY(batch_check(b, n));
+    if (n < 0 || (n > 0 && (!first || !out_tokens))) return set_error(GAJE_ERR_INVALID_ARG, "bad decode arguments");
+    if (n == 0) return GAJE_OK;
+    gaje_hip_model *m = b->m;
+    hipStream_t s = m->stream;
+    const size_t need = (size_t)(b->nseq * n);
+    if ((int64_t)need > b->out_cap) {
+        if (b->out) b->release(b->out);
+        GAJE_TRY(b->alloc(&b->out, need));
+        b->out_cap = (int64_t)need;
+    }
+    GAJE_HIP_CHECK(hipMemcpyAsync(b->st.tok, first, (size_t)b->nseq * 4, hipMemcpyHostToDevice, s));
+    GAJE_TRY(launch_fill_u32(b->out, 0u, (int64_t)need, s));
+    for (int64_t i = 0; i < n; ++i) GAJE_TRY(batch_enqueue_step(b, nullptr, n, i, b->out, true));
+    const int rc = batch_sync(b, status);
+    GAJE_HIP_CHECK(hipMemcpy(out_tokens, b->out, need * 4, hipMemcpyDeviceToHost));
+    return rc;
+}
+
 extern "C" int gaje_hip_greedy_next(gaje_hip_model *m, uint32_t token, uint32_t *next) {
     clear_error();
     GAJE_TRY(check_model(m));
@@ -1332,7 +1702,7 @@ extern "C" int gaje_hip_time_stage(gaje_hip_model *m, int stage, int64_t layer, 
                 return launch_gemv(p, m->stream);
             }
             case GAJE_STAGE_ATTENTION: {
-                AttnParams ap;
+                AttnParams ap{};
                 ap.q = m->q;
                 ap.k_cache = m->k_cache + layer * layer_kv;
                 ap.v_cache = m->v_cache + layer * layer_kv;

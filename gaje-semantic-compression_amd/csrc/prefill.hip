@@ -21,7 +21,13 @@ namespace {
 // cache at the token's position.  One workgroup per token.
 __global__ __launch_bounds__(256) void rope_kv_kernel(PrefillRopeParams p) {
     const int64_t t = blockIdx.x;
-    const int64_t pos = p.pos0 + t;
+    int64_t pos = p.pos0 + t;
+    if (p.seq_pos) {
+        pos = p.seq_pos[t];
+        if (pos < 0) return;
+        p.k_cache += t * p.seq_kv_stride;
+        p.v_cache += t * p.seq_kv_stride;
+    }
     const float *row = p.qkv + t * p.ldq;
     const int hd = p.head_dim, half = hd >> 1;
     const int64_t q_rows = (int64_t)p.n_head * hd, kv_rows = (int64_t)p.n_kv * hd;
@@ -186,7 +192,7 @@ int launch_attn_hd(const PrefillAttnParams &p, hipStream_t s) {
 
 int launch_rope_kv(const PrefillRopeParams &p, hipStream_t s) {
     if (p.P <= 0 || !p.qkv || !p.q_out || !p.k_cache || !p.v_cache || p.head_dim <= 0 || p.head_dim % 2 ||
-        p.pos0 < 0 || p.pos0 + p.P > p.cap)
+        (!p.seq_pos && (p.pos0 < 0 || p.pos0 + p.P > p.cap)))
         return set_error(GAJE_ERR_INVALID_ARG, "rope/kv: bad arguments");
     hipLaunchKernelGGL(rope_kv_kernel, dim3((unsigned)p.P), dim3(256), 0, s, p);
     GAJE_HIP_CHECK(hipGetLastError());

@@ -139,6 +139,12 @@ SIGNATURES = [
     ("gaje_hip_reserve", ctypes.c_int, [c_vp, c_i64]),
     ("gaje_hip_prefill", ctypes.c_int, [c_vp, c_vp, c_i64, c_vp]),
     ("gaje_hip_prefill_mfma", ctypes.c_int, [c_vp, c_vp, c_i64, c_vp]),
+    ("gaje_hip_batch_open", ctypes.c_int, [c_vp, c_i64, c_i64, ctypes.POINTER(c_vp)]),
+    ("gaje_hip_batch_close", None, [c_vp]),
+    ("gaje_hip_batch_reset", ctypes.c_int, [c_vp, c_i64]),
+    ("gaje_hip_batch_cache_len", ctypes.c_int, [c_vp, c_i64, ctypes.POINTER(c_i64)]),
+    ("gaje_hip_batch_feed", ctypes.c_int, [c_vp, c_vp, c_i64, c_vp, c_vp]),
+    ("gaje_hip_batch_decode_greedy", ctypes.c_int, [c_vp, c_vp, c_i64, c_vp, c_vp]),
     ("gaje_hip_greedy_next", ctypes.c_int, [c_vp, ctypes.c_uint32, ctypes.POINTER(ctypes.c_uint32)]),
     ("gaje_hip_decode_greedy", ctypes.c_int, [c_vp, ctypes.c_uint32, c_i64, c_vp]),
     ("gaje_hip_generate", ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, ctypes.c_float, ctypes.c_float,

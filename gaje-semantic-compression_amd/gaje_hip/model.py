@@ -151,3 +151,63 @@ class GenomicLLM:
 def load_genomic_auto(path: str, device: int = 0) -> GenomicLLM:
     """load_genomic_auto for .gaje.flat files (src/io/flat_reader.rs:240-252)."""
     return GenomicLLM(path, device)
+
+
+BATCH_INACTIVE = 0xFFFFFFFF
+
+
+class GenomicBatch:
+    """n_seq independent sequences over one GenomicLLM's weights, stepped
+    together (gaje_hip_batch_*): each sequence's logits are bit-identical to its
+    own GenomicLLM.forward_core."""
+
+    def __init__(self, model: GenomicLLM, n_seq: int, capacity: int):
+        h = ctypes.c_void_p()
+        check(lib().gaje_hip_batch_open(model._h, int(n_seq), int(capacity), ctypes.byref(h)))
+        self._h = h
+        self.model = model
+        self.n_seq = int(n_seq)
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().gaje_hip_batch_close(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def reset(self, seq: int = -1) -> None:
+        check(lib().gaje_hip_batch_reset(self._h, int(seq)))
+
+    def cache_len(self, seq: int) -> int:
+        n = ctypes.c_int64()
+        check(lib().gaje_hip_batch_cache_len(self._h, int(seq), ctypes.byref(n)))
+        return n.value
+
+    def feed(self, ids, want_logits: bool = False, status: bool = False):
+        """ids: [n_seq][n] token ids (BATCH_INACTIVE skips a sequence's step).
+        Returns the last step's logits [n_seq][n_logits] (or None), and the
+        per-sequence status when asked."""
+        ids = np.ascontiguousarray(ids, dtype=np.uint32).reshape(self.n_seq, -1)
+        out = np.empty((self.n_seq, self.model.n_logits), np.float32) if want_logits else None
+        st = np.zeros(self.n_seq, np.int32)
+        rc = lib().gaje_hip_batch_feed(self._h, ids.ctypes.data, ids.shape[1],
+                                       out.ctypes.data if out is not None else None, st.ctypes.data)
+        if status:
+            return out, st, rc
+        check(rc)
+        return out
+
+    def decode_greedy(self, first, n: int, status: bool = False):
+        first = np.ascontiguousarray(first, dtype=np.uint32).reshape(self.n_seq)
+        out = np.zeros((self.n_seq, int(n)), np.uint32)
+        st = np.zeros(self.n_seq, np.int32)
+        rc = lib().gaje_hip_batch_decode_greedy(self._h, first.ctypes.data, int(n), out.ctypes.data,
+                                                st.ctypes.data)
+        if status:
+            return out, st, rc
+        check(rc)
+        return out

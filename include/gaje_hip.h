@@ -220,6 +220,32 @@ int gaje_hip_prefill(gaje_hip_model *m, const uint32_t *ids, int64_t n, float *l
  * GAJE_ERR_UNSUPPORTED.  On a NaN guard the cache length is left unchanged. */
 int gaje_hip_prefill_mfma(gaje_hip_model *m, const uint32_t *ids, int64_t n, float *last_logits_host);
 
+/* Batched decode: n_seq (1..16) independent sequences over one model's
+ * weights, each with its own KV cache of `capacity` positions, as n_seq
+ * GenomicLLM instances (llm/forward.rs:7-64) stepping together.  Every
+ * sequence's logits are bit-identical to its own forward_core: the matvecs
+ * read each weight row once per step and run every sequence's accumulation
+ * chains in the reference order.  Needs Q4_0 body tensors and an f32 lm_head
+ * (GAJE_ERR_UNSUPPORTED otherwise).  No reference function batches
+ * sequences. */
+typedef struct gaje_hip_batch gaje_hip_batch;
+#define GAJE_BATCH_INACTIVE 0xFFFFFFFFu /* a fed id that skips its sequence for that step */
+int gaje_hip_batch_open(gaje_hip_model *m, int64_t n_seq, int64_t capacity, gaje_hip_batch **out);
+void gaje_hip_batch_close(gaje_hip_batch *b);
+/* clear_cache_core of one sequence (seq = -1: all); also clears a NaN halt */
+int gaje_hip_batch_reset(gaje_hip_batch *b, int64_t seq);
+int gaje_hip_batch_cache_len(const gaje_hip_batch *b, int64_t seq, int64_t *len);
+/* n steps with given ids (ids[s * n + i] for sequence s, step i; prompt
+ * prefill): last_logits_host (NULL or [n_seq][n_logits]) gets the last step's
+ * K-WTA-filtered logits; status (NULL or [n_seq]) gets 0, or 1 + the NaN
+ * stage of a sequence a guard halted (the call then fails with its message). */
+int gaje_hip_batch_feed(gaje_hip_batch *b, const uint32_t *ids, int64_t n, float *last_logits_host,
+                        int32_t *status);
+/* n greedy steps on device from first[s]: out_tokens[s * n + i] = argmax of
+ * step i's logits (llm/forward.rs:262-271), fed back as step i+1's token. */
+int gaje_hip_batch_decode_greedy(gaje_hip_batch *b, const uint32_t *first, int64_t n, uint32_t *out_tokens,
+                                 int32_t *status);
+
 /* One greedy step on device: forward(token) then argmax of the logits
  * (nn/llm/forward.rs:262-271); no logits cross PCIe. */
 int gaje_hip_greedy_next(gaje_hip_model *m, uint32_t token, uint32_t *next);
