@@ -244,6 +244,124 @@ __global__ __launch_bounds__(THREADS) void attn_decode_fast(AttnParams p) {
     if (tid < DS) p.out[(size_t)h * HD + d0 + tid] = chain_lds(0.0f, vs + tid * vstride, n);
 }
 
+// Batched decode (several sequences per launch): one workgroup per (query
+// head, sequence) computes the head's scores once; after the softmax each
+// output dimension's chain runs in its own thread (threads 0..HD-1), reading
+// its V row straight from memory (the row is contiguous and the loads run
+// ahead of the adds).  Same rounding sequence as attn_decode_fast.
+template <int HD>
+__global__ __launch_bounds__(THREADS) void attn_decode_batch(AttnParams p) {
+    extern __shared__ __align__(16) float smem[];  // chain_row(cap): scores, exponentials, weights
+    __shared__ float red[THREADS / WAVE];
+    __shared__ float inv_slot;
+    __shared__ uint64_t tab[32];
+    const int tid = threadIdx.x;
+    const int h = blockIdx.x, z = blockIdx.z;
+    const int pos = p.seq_pos[z];
+    if (pos < 0) return;
+    const int ctx = pos + 1;
+    if (tid < 32) tab[tid] = kExp2Tab[tid];
+    const int g = h / (p.n_head / p.n_head_kv);
+    const float scale = 1.0f / sqrtf((float)HD);
+    const int64_t cap = p.kv_cap;
+    const int n = chain_len(ctx);
+    float *sc = smem;
+    const float *qg = p.q + z * p.seq_q_stride + (size_t)h * HD;
+    const float *Kh = p.k_cache + z * p.seq_kv_stride + (size_t)g * p.kv_head_stride;
+    const float *Vh = p.v_cache + z * p.seq_kv_stride + (size_t)g * p.kv_head_stride;
+
+    // scores: thread j takes positions 4j..4j+3 of each round (as attn_decode_fast)
+    constexpr int NCH = HD / 8, RING = 4;
+    const char *kb = (const char *)Kh;
+    const uint32_t rowb = (uint32_t)cap * 4;
+    float mx = -INFINITY;
+    for (int t4 = 4 * tid; t4 < ctx; t4 += 4 * THREADS) {
+        uint32_t off = (uint32_t)t4 * 4;
+        float4 kr[RING][8];
+#pragma unroll
+        for (int c = 0; c < RING; ++c)
+#pragma unroll
+            for (int l = 0; l < 8; ++l) {
+                kr[c][l] = *(const float4 *)(kb + off);
+                off += rowb;
+            }
+        float acc[4][8];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int l = 0; l < 8; ++l) acc[u][l] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            const float4 qa = *(const float4 *)(qg + 8 * c), qb = *(const float4 *)(qg + 8 * c + 4);
+            const float qc[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+            for (int l = 0; l < 8; ++l) {
+                const float4 k = kr[c % RING][l];
+                acc[0][l] = fmaf(qc[l], k.x, acc[0][l]);
+                acc[1][l] = fmaf(qc[l], k.y, acc[1][l]);
+                acc[2][l] = fmaf(qc[l], k.z, acc[2][l]);
+                acc[3][l] = fmaf(qc[l], k.w, acc[3][l]);
+            }
+            if (c + RING < NCH) {
+#pragma unroll
+                for (int l = 0; l < 8; ++l) {
+                    kr[c % RING][l] = *(const float4 *)(kb + off);
+                    off += rowb;
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const float u0 = acc[u][0] + acc[u][4], u1 = acc[u][1] + acc[u][5];
+            const float u2 = acc[u][2] + acc[u][6], u3 = acc[u][3] + acc[u][7];
+            const float s = ((u0 + u1) + (u2 + u3)) * scale;
+            if (t4 + u < ctx) {
+                sc[t4 + u] = s;
+                mx = fmaxf(mx, s);
+            }
+        }
+    }
+    const float max_s = block_max(mx, red);
+    for (int t = tid; t < n; t += THREADS) sc[t] = t < ctx ? expf_ref_t(sc[t] - max_s, tab) : 0.0f;
+    __syncthreads();
+    if (tid == 0) inv_slot = 1.0f / (chain_lds(0.0f, sc, n) + 1e-12f);
+    __syncthreads();
+    const float inv = inv_slot;
+    for (int t = tid; t < ctx; t += THREADS) sc[t] = sc[t] * inv;
+    __syncthreads();
+
+    // out_i = ((w_0 v_0[i]) + (w_1 v_1[i])) + ..., products and sums rounded in t order
+    if (tid < HD) {
+        const float *v = Vh + (size_t)tid * cap;
+        float acc = 0.0f;
+        constexpr int AH = 8;  // quads loaded ahead of the chain
+        float4 vq[AH];
+#pragma unroll
+        for (int a = 0; a < AH; ++a) vq[a] = *(const float4 *)(v + (4 * a < ctx ? 4 * a : 0));
+        for (int t0 = 0; t0 < ctx; t0 += 4 * AH) {
+#pragma unroll
+            for (int a = 0; a < AH; ++a) {
+                const int t = t0 + 4 * a;
+                if (t >= ctx) break;
+                const float4 vv = vq[a];
+                const int tn = t + 4 * AH;
+                vq[a] = *(const float4 *)(v + (tn < ctx ? tn : 0));
+                const float4 w = *(const float4 *)(sc + t);
+                const float vals[4] = {vv.x, vv.y, vv.z, vv.w}, ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if (t + j < ctx) {
+                        const float prod = ws[j] * vals[j];
+                        acc = acc + prod;
+                    }
+                }
+            }
+        }
+        const int64_t i = (int64_t)h * HD + tid, rows = (int64_t)p.n_head * HD;
+        p.out[z * p.seq_q_stride + (p.out_chain_major ? (i & 7) * (rows / 8) + (i >> 3) : i)] = acc;
+    }
+}
+
 // Output dimensions per workgroup of the streaming kernel for this capacity,
 // or 0 if even one V row does not fit.
 size_t fast_lds_bytes(int64_t cap, int ds) { return (size_t)(chain_row(cap) + (size_t)ds * (chain_row(cap) + 4)) * 4; }
@@ -311,7 +429,8 @@ __global__ __launch_bounds__(THREADS) void attn_decode_generic(AttnParams p) {
             const float prod = sc[t] * v[t];
             acc = acc + prod;
         }
-        p.out[(size_t)h * hd + i] = acc;
+        const int64_t o = (int64_t)h * hd + i, rows = (int64_t)p.n_head * hd;
+        p.out[p.out_chain_major ? (o & 7) * (rows / 8) + (o >> 3) : o] = acc;
     }
 }
 
@@ -341,7 +460,19 @@ int launch_attention(const AttnParams &p, hipStream_t s) {
                          (long long)p.kv_cap);
     if (p.seq_pos && (p.n_seq <= 0 || p.n_seq > 65535)) return set_error(GAJE_ERR_INVALID_ARG, "attention: bad batch");
     const unsigned nz = p.seq_pos ? (unsigned)p.n_seq : 1u;
-    const int ds = (p.kv_cap % 4 == 0 && (p.head_dim == 64 || p.head_dim == 128)) ? fast_slice(p.head_dim, p.kv_cap) : 0;
+    if (p.out_chain_major && (!p.seq_pos || ((int64_t)p.n_head * p.head_dim) % 8))
+        return set_error(GAJE_ERR_INVALID_ARG, "attention: chain-major output needs a batch and n_head*head_dim %% 8 == 0");
+    const bool batch_kernel = p.seq_pos && p.kv_cap % 4 == 0 && (p.head_dim == 64 || p.head_dim == 128) &&
+                              (size_t)chain_row(p.kv_cap) * 4 + 1024 <= max_lds_per_block();
+    if (batch_kernel) {
+        const size_t blds = (size_t)chain_row(p.kv_cap) * 4;
+        if (p.head_dim == 64) hipLaunchKernelGGL(attn_decode_batch<64>, dim3(p.n_head, 1, nz), dim3(THREADS), blds, s, p);
+        else hipLaunchKernelGGL(attn_decode_batch<128>, dim3(p.n_head, 1, nz), dim3(THREADS), blds, s, p);
+        GAJE_HIP_CHECK(hipGetLastError());
+        return GAJE_OK;
+    }
+    // the batched generic path (any head_dim) or batch 1
+    const int ds = (!p.seq_pos && p.kv_cap % 4 == 0 && (p.head_dim == 64 || p.head_dim == 128)) ? fast_slice(p.head_dim, p.kv_cap) : 0;
     if (ds > 0) {
         const size_t flds = fast_lds_bytes(p.kv_cap, ds);
         void (*fn)(AttnParams);

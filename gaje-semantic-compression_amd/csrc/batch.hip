@@ -35,122 +35,113 @@ __device__ __forceinline__ void group_dequant(float (&d)[16], vu2 n, vu4 s) {
 }
 
 // Packed Q4_0 rows x NV activation vectors (genomic_dot_product_q4_0_avx2,
-// genomic.rs:263-336, per vector).  Lane = (row lane>>3 of the workgroup's
-// eight, chain l = lane&7); wave w owns vectors w*VPW.. (their accumulators);
-// the waves share the rows and the staged chunk of all vectors, kept
-// chain-major in LDS (element k of a chunk at chain k%8, column k/8).  The
-// chunks are double-buffered through registers; groups past the row's end
-// read as zero codes/scales against zero activations, and fma(0, 0, acc) =
-// acc (acc is never -0), so whole chunks run branch-free.
-template <int NV, int VPW>
+// genomic.rs:263-336, per vector).  Lane = (row slot lane>>3, chain l =
+// lane&7); a slot holds R rows (rows slot + 8j of the workgroup's 8R), so
+// each activation value read from LDS feeds R rows' chains; wave w owns
+// vectors w*VPW.. (their accumulators); the waves share the rows and the
+// staged chunk of all vectors.  Activations arrive chain-major
+// ([vector][chain l][K/8]: element k at chain k%8, column k/8), so a chunk is
+// 8 contiguous runs per vector, copied to LDS through registers
+// (double-buffered, loads always issued, clamped at the end).  Groups past the
+// row's end read as zero codes/scales against zero activations, and
+// fma(0, 0, acc) = acc (acc is never -0), so every chunk runs branch-free.
+template <int NV, int VPW, int R>
 __global__ __launch_bounds__(NV / VPW * 64) void gemv_batch_q4_kernel(BatchGemvParams p) {
     constexpr int NTH = NV / VPW * 64;
+    constexpr int RUN = BQ_CHUNK / 8;                 // floats of one chain per chunk
     constexpr int BUF = NV * 8 * BQ_CROW;
-    constexpr int UPT = NV * (BQ_CHUNK / 8) / NTH;  // 8-element runs staged per thread per chunk
+    constexpr int UPT = NV * 8 * (RUN / 4) / NTH;     // float4s staged per thread per chunk
     extern __shared__ __align__(16) float xs[];       // [2][NV][8][BQ_CROW]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l = lane & 7, base = lane & ~7;
-    const int64_t row = (int64_t)blockIdx.x * 8 + (lane >> 3);
-    const bool row_ok = row < p.N;
     const int nb = p.nb, G = (nb + 3) >> 2;
-    const int64_t K = (int64_t)nb * 32;
-    const int nch = (int)((K + BQ_CHUNK - 1) / BQ_CHUNK);
-    const uint8_t *wr = p.w + (size_t)(row_ok ? row : p.N - 1) * G * 80;
+    const int64_t K8 = (int64_t)nb * 4;               // column count of a chain row
+    const int nch = (int)((K8 + RUN - 1) / RUN);
+    int64_t row[R];
+    const uint8_t *wr[R];
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+        row[j] = (int64_t)blockIdx.x * 8 * R + 8 * j + (lane >> 3);
+        wr[j] = p.w + (size_t)(row[j] < p.N ? row[j] : p.N - 1) * G * 80;
+    }
     const int v0 = wave * VPW;
 
-    float4 st[UPT][2];
+    vf4 st[UPT];
     auto load_chunk = [&](int c) {
 #pragma unroll
         for (int i = 0; i < UPT; ++i) {
-            const int u = tid + i * NTH, v = u / (BQ_CHUNK / 8), m = u % (BQ_CHUNK / 8);
-            const int64_t k = (int64_t)c * BQ_CHUNK + 8 * m;
-            const bool in = k < K;
-            const float *src = p.x + (size_t)v * p.ldx + (in ? k : K - 8);
-            const float4 a = *(const float4 *)src, b = *(const float4 *)(src + 4);
-            const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-            st[i][0] = in ? a : z;
-            st[i][1] = in ? b : z;
+            const int u = tid + i * NTH, vl = u / (RUN / 4), q = u % (RUN / 4);  // vl = v * 8 + l
+            const int64_t col = (int64_t)c * RUN + 4 * q;
+            const bool in = col < K8;
+            const float *src = p.x + (size_t)(vl >> 3) * p.ldx + (size_t)(vl & 7) * K8 + (in ? col : 0);
+            const vf4 a = *(const vf4 *)src;
+            st[i] = in ? a : (vf4){0.f, 0.f, 0.f, 0.f};
         }
     };
     auto store_chunk = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < UPT; ++i) {
-            const int u = tid + i * NTH, v = u / (BQ_CHUNK / 8), m = u % (BQ_CHUNK / 8);
-            float *dst = xs + buf * BUF + v * 8 * BQ_CROW + m;
-            dst[0 * BQ_CROW] = st[i][0].x;
-            dst[1 * BQ_CROW] = st[i][0].y;
-            dst[2 * BQ_CROW] = st[i][0].z;
-            dst[3 * BQ_CROW] = st[i][0].w;
-            dst[4 * BQ_CROW] = st[i][1].x;
-            dst[5 * BQ_CROW] = st[i][1].y;
-            dst[6 * BQ_CROW] = st[i][1].z;
-            dst[7 * BQ_CROW] = st[i][1].w;
+            const int u = tid + i * NTH, vl = u / (RUN / 4), q = u % (RUN / 4);
+            *(vf4 *)(xs + buf * BUF + vl * BQ_CROW + 4 * q) = st[i];
         }
     };
-    vu2 wn[2][4];
-    vu4 ws[2][4];
+    vu2 wn[2][R][4];
+    vu4 ws[2][R][4];
     auto load_w = [&](int c, int slot) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int g = 4 * c + i;
-            const bool in = g < G;
-            const uint8_t *gp = wr + (size_t)(in ? g : G - 1) * 80;
-            const vu2 n = *(const vu2 *)(gp + 8 * l);
-            const vu4 s = *(const vu4 *)(gp + 64);
-            const uint32_t keep = in ? 0xFFFFFFFFu : 0u;
-            wn[slot][i] = n & keep;
-            ws[slot][i] = s & keep;
-        }
+        for (int j = 0; j < R; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int g = 4 * c + i;
+                const bool in = g < G;
+                const uint8_t *gp = wr[j] + (size_t)(in ? g : G - 1) * 80;
+                const vu2 n = *(const vu2 *)(gp + 8 * l);
+                const vu4 s = *(const vu4 *)(gp + 64);
+                const uint32_t keep = in ? 0xFFFFFFFFu : 0u;
+                wn[slot][j][i] = n & keep;
+                ws[slot][j][i] = s & keep;
+            }
     };
 
-    float acc[VPW];
+    float acc[R][VPW];
 #pragma unroll
-    for (int v = 0; v < VPW; ++v) acc[v] = 0.0f;
+    for (int j = 0; j < R; ++j)
+#pragma unroll
+        for (int v = 0; v < VPW; ++v) acc[j][v] = 0.0f;
 
     load_w(0, 0);
     load_chunk(0);
     store_chunk(0);
     __syncthreads();
-    // one chunk from buffer `cur` (a constant at each call: the register rings
-    // are indexed statically)
+    // one chunk from buffer `cur` (a constant at each call: the rings are
+    // indexed statically); the next chunk's loads are in flight meanwhile
     auto chunk = [&](int c, int cur) {
-        const bool more = c + 1 < nch;
-        if (more) {
-            load_w(c + 1, cur ^ 1);
-            load_chunk(c + 1);
-        }
+        const int cn = c + 1 < nch ? c + 1 : c;
+        load_w(cn, cur ^ 1);
+        load_chunk(cn);
         const float *xb = xs + cur * BUF + (v0 * 8 + l) * BQ_CROW;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            float d[16];
-            group_dequant(d, wn[cur][i], ws[cur][i]);
+            float d[R][16];
+#pragma unroll
+            for (int j = 0; j < R; ++j) group_dequant(d[j], wn[cur][j][i], ws[cur][j][i]);
 #pragma unroll
             for (int v = 0; v < VPW; ++v) {
                 const float *xv = xb + v * 8 * BQ_CROW + 16 * i;
                 const float4 x0 = *(const float4 *)xv, x1 = *(const float4 *)(xv + 4);
                 const float4 x2 = *(const float4 *)(xv + 8), x3 = *(const float4 *)(xv + 12);
-                float a = acc[v];
-                a = fmaf(d[0], x0.x, a);
-                a = fmaf(d[1], x0.y, a);
-                a = fmaf(d[2], x0.z, a);
-                a = fmaf(d[3], x0.w, a);
-                a = fmaf(d[4], x1.x, a);
-                a = fmaf(d[5], x1.y, a);
-                a = fmaf(d[6], x1.z, a);
-                a = fmaf(d[7], x1.w, a);
-                a = fmaf(d[8], x2.x, a);
-                a = fmaf(d[9], x2.y, a);
-                a = fmaf(d[10], x2.z, a);
-                a = fmaf(d[11], x2.w, a);
-                a = fmaf(d[12], x3.x, a);
-                a = fmaf(d[13], x3.y, a);
-                a = fmaf(d[14], x3.z, a);
-                a = fmaf(d[15], x3.w, a);
-                acc[v] = a;
+                const float xx[16] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w,
+                                      x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
+#pragma unroll
+                for (int j = 0; j < R; ++j) {
+                    float a = acc[j][v];
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) a = fmaf(d[j][e], xx[e], a);
+                    acc[j][v] = a;
+                }
             }
-            __builtin_amdgcn_sched_barrier(0);  // one group's LDS reads in flight at a time
         }
-        if (more) store_chunk(cur ^ 1);
+        store_chunk(cur ^ 1);
         __syncthreads();
     };
     for (int c = 0; c < nch; c += 2) {
@@ -158,33 +149,37 @@ __global__ __launch_bounds__(NV / VPW * 64) void gemv_batch_q4_kernel(BatchGemvP
         if (c + 1 < nch) chunk(c + 1, 1);
     }
 
-    // per vector: ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) in lane l = 0, then the row epilogue
+    // per (row, vector): ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) in lane l = 0, then the row epilogue
 #pragma unroll
-    for (int v = 0; v < VPW; ++v) {
-        const float a = acc[v];
-        const float u = a + __shfl(a, base + ((l + 4) & 7), WAVE);
-        const float w = u + __shfl(u, base + ((l + 2) & 7), WAVE);
-        const float t = w + __shfl(w, base + ((l + 1) & 7), WAVE);
-        const int s = v0 + v;
-        if (l != 0 || !row_ok || s >= p.nv) continue;
-        float y = flush_small(t);
-        if (p.a_ptr) {  // sparse anchors, then the bias (forward.rs:103-115)
-            for (int64_t k = p.a_ptr[row]; k < p.a_ptr[row + 1]; ++k) {
-                const float prod = p.x[(size_t)s * p.ldx + p.a_col[k]] * half_bits(p.a_val[k]);
-                y = y + prod;
+    for (int j = 0; j < R; ++j)
+#pragma unroll
+        for (int v = 0; v < VPW; ++v) {
+            const float a = acc[j][v];
+            const float u = a + __shfl(a, base + ((l + 4) & 7), WAVE);
+            const float w = u + __shfl(u, base + ((l + 2) & 7), WAVE);
+            const float t = w + __shfl(w, base + ((l + 1) & 7), WAVE);
+            const int s = v0 + v;
+            const int64_t r = row[j];
+            if (l != 0 || r >= p.N || s >= p.nv) continue;
+            float y = flush_small(t);
+            if (p.a_ptr) {  // sparse anchors, then the bias (forward.rs:103-115)
+                for (int64_t k = p.a_ptr[r]; k < p.a_ptr[r + 1]; ++k) {
+                    const uint32_t col = p.a_col[k];
+                    const float prod = p.x[(size_t)s * p.ldx + (col & 7) * K8 + (col >> 3)] * half_bits(p.a_val[k]);
+                    y = y + prod;
+                }
+            }
+            if (r < p.bias_len) y = y + p.bias[r];
+            float *dst = p.y + (size_t)s * p.ldy + r;
+            if (p.mode == MODE_RESIDUAL) {
+                if (isnan(y)) seq_flag(p.nan_codes, s, p.layer, p.st_a);
+                const float h = *dst + y;
+                *dst = h;
+                if (isnan(h)) seq_flag(p.nan_codes, s, p.layer, p.st_b);
+            } else {
+                *dst = y;
             }
         }
-        if (row < p.bias_len) y = y + p.bias[row];
-        float *dst = p.y + (size_t)s * p.ldy + row;
-        if (p.mode == MODE_RESIDUAL) {
-            if (isnan(y)) seq_flag(p.nan_codes, s, p.layer, p.st_a);
-            const float h = *dst + y;
-            *dst = h;
-            if (isnan(h)) seq_flag(p.nan_codes, s, p.layer, p.st_b);
-        } else {
-            *dst = y;
-        }
-    }
 }
 
 // F32 rows in the tiled layout x NV vectors (dot_product, dot.rs:23-94, per
@@ -261,17 +256,42 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(BatchRowParams p) {
         xs[k] = v;
     }
     if (__syncthreads_or(bad) && tid == 0) seq_flag(p.nan_codes, s, p.layer, p.st_a);
-    rms_inv_plain(xs, p.K, p.eps, &inv_slot);
-    __syncthreads();
-    const float inv = inv_slot;
+    float inv = 1.0f;
+    if (p.w) {
+        rms_inv_plain(xs, p.K, p.eps, &inv_slot);
+        __syncthreads();
+        inv = inv_slot;
+    }
     bad = 0;
+    const int64_t K8 = p.K / 8;
     for (int64_t k = tid; k < p.K; k += 256) {
-        const float t = xs[k] * inv;
-        const float o = t * p.w[k];
+        float o = xs[k];  // no weight: the plain rows (an empty norm tensor is skipped, block/forward.rs:18-28)
+        if (p.w) {
+            const float t = o * inv;
+            o = t * p.w[k];
+        }
         bad |= isnan(o);
-        p.y[(size_t)s * p.ldy + k] = o;
+        p.y[(size_t)s * p.ldy + (p.chain_major ? (k & 7) * K8 + (k >> 3) : k)] = o;
     }
     if (__syncthreads_or(bad) && tid == 0) seq_flag(p.nan_codes, s, p.layer, p.st_b);
+}
+
+// swiglu_balanced per element (block/forward.rs:87-113) without the genomic
+// norm: a grid over (sequence, 256-element slices).
+__global__ __launch_bounds__(256) void swiglu_elems_kernel(BatchRowParams p) {
+    const int s = blockIdx.y;
+    const int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const float *g = p.x + (size_t)s * p.ldx, *u = g + p.K;
+    int bad_u = 0, bad_o = 0;
+    if (k < p.K) {
+        const float uv = u[k];
+        bad_u = isnan(uv);
+        const float o = swiglu1(g[k], uv);
+        bad_o = isnan(o);
+        p.y[(size_t)s * p.ldy + (p.chain_major ? (k & 7) * (p.K / 8) + (k >> 3) : k)] = o;
+    }
+    if (__any(bad_u) && (threadIdx.x & 63) == 0) seq_flag(p.nan_codes, s, p.layer, p.st_a);
+    if (__any(bad_o) && (threadIdx.x & 63) == 0) seq_flag(p.nan_codes, s, p.layer, p.st_b);
 }
 
 // swiglu_balanced per element of each sequence's gate/up row pair
@@ -310,7 +330,8 @@ __global__ __launch_bounds__(256) void swiglu_rows_kernel(BatchRowParams p) {
         const float rms = rms_slot;
         if (rms > p.h_scale) sc = p.h_scale / rms;
     }
-    for (int64_t k = tid; k < p.K; k += 256) p.y[(size_t)s * p.ldy + k] = p.gnorm ? xs[k] * sc : xs[k];
+    for (int64_t k = tid; k < p.K; k += 256)
+        p.y[(size_t)s * p.ldy + (p.chain_major ? (k & 7) * (p.K / 8) + (k >> 3) : k)] = p.gnorm ? xs[k] * sc : xs[k];
 }
 
 // Greedy argmax per sequence (llm/forward.rs:262-271: strict '>', so the first
@@ -373,7 +394,11 @@ __global__ void batch_end_kernel(BatchState b, uint32_t *out, int64_t n, int64_t
 template <int NV, int VPW>
 int launch_q4(const BatchGemvParams &p, hipStream_t s) {
     const size_t lds = (size_t)2 * NV * 8 * BQ_CROW * 4;
-    hipLaunchKernelGGL((gemv_batch_q4_kernel<NV, VPW>), dim3((unsigned)((p.N + 7) / 8)), dim3(NV / VPW * 64), lds, s, p);
+    // two rows per lane halve the LDS reads per FMA; one when that leaves too few workgroups
+    if (p.N >= 16 * 1024)
+        hipLaunchKernelGGL((gemv_batch_q4_kernel<NV, VPW, 2>), dim3((unsigned)((p.N + 15) / 16)), dim3(NV / VPW * 64), lds, s, p);
+    else
+        hipLaunchKernelGGL((gemv_batch_q4_kernel<NV, VPW, 1>), dim3((unsigned)((p.N + 7) / 8)), dim3(NV / VPW * 64), lds, s, p);
     GAJE_HIP_CHECK(hipGetLastError());
     return GAJE_OK;
 }
@@ -413,7 +438,8 @@ int launch_gemv_batch(const BatchGemvParams &p, hipStream_t s) {
 }
 
 int launch_rmsnorm_rows(const BatchRowParams &p, hipStream_t s) {
-    if (!p.x || !p.y || !p.w || p.K <= 0 || p.nv <= 0) return set_error(GAJE_ERR_INVALID_ARG, "rmsnorm rows: bad arguments");
+    if (!p.x || !p.y || p.K <= 0 || p.nv <= 0 || (p.chain_major && p.K % 8))
+        return set_error(GAJE_ERR_INVALID_ARG, "rmsnorm rows: bad arguments");
     if ((size_t)p.K * 4 + 1024 > max_lds_per_block()) return set_error(GAJE_ERR_UNSUPPORTED, "rmsnorm rows: K too large");
     hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3((unsigned)p.nv), dim3(256), (size_t)p.K * 4, s, p);
     GAJE_HIP_CHECK(hipGetLastError());
@@ -422,6 +448,11 @@ int launch_rmsnorm_rows(const BatchRowParams &p, hipStream_t s) {
 
 int launch_swiglu_rows(const BatchRowParams &p, hipStream_t s) {
     if (!p.x || !p.y || p.K <= 0 || p.nv <= 0) return set_error(GAJE_ERR_INVALID_ARG, "swiglu rows: bad arguments");
+    if (!p.gnorm) {
+        hipLaunchKernelGGL(swiglu_elems_kernel, dim3((unsigned)((p.K + 255) / 256), (unsigned)p.nv), dim3(256), 0, s, p);
+        GAJE_HIP_CHECK(hipGetLastError());
+        return GAJE_OK;
+    }
     if ((size_t)p.K * 4 + 1024 > max_lds_per_block()) return set_error(GAJE_ERR_UNSUPPORTED, "swiglu rows: K too large");
     hipLaunchKernelGGL(swiglu_rows_kernel, dim3((unsigned)p.nv), dim3(256), (size_t)p.K * 4, s, p);
     GAJE_HIP_CHECK(hipGetLastError());

@@ -126,10 +126,12 @@ struct AttnParams {
     int64_t ctx;
     // batched decode (seq_pos non-null): blockIdx.z = sequence z attends to
     // positions 0..seq_pos[z] of its own cache (k/v_cache + z * seq_kv_stride);
-    // its q and out rows are z * seq_q_stride floats on; seq_pos[z] < 0 skips it
+    // its q and out rows are z * seq_q_stride floats on; seq_pos[z] < 0 skips
+    // it; out_chain_major writes each out row chain-major over n_head*head_dim
     const int32_t *seq_pos;
     int64_t seq_kv_stride, seq_q_stride;
     int32_t n_seq;
+    int32_t out_chain_major;
 };
 int launch_attention(const AttnParams &p, hipStream_t s);
 size_t attention_lds_bytes(int head_dim, int64_t max_ctx);
@@ -240,7 +242,7 @@ struct BatchGemvParams {
     int32_t f32_tiled;
     int32_t nb;              // K / 32 (Q4_0)
     int64_t N, K;
-    const float *x;          // [nv][ldx]
+    const float *x;          // [nv][ldx]; FMT_Q4_0: each row chain-major (element k at (k%8)*K/8 + k/8)
     int64_t ldx;
     int32_t nv;              // vectors (sequences)
     const float *bias;
@@ -268,6 +270,7 @@ struct BatchRowParams {
     int32_t nv;
     float eps, h_scale;
     int32_t gnorm;
+    int32_t chain_major;     // write y rows chain-major (input of a batched Q4_0 matvec)
     uint32_t *nan_codes;
     int32_t layer, st_a, st_b;
 };

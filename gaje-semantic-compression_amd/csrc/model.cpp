@@ -283,6 +283,7 @@ struct gaje_hip_model {
     } pf;
 
     std::vector<void *> allocs;
+    std::vector<gaje_hip_batch *> batches;  // open batches over these weights
 
     ~gaje_hip_model() {
         if (graph_exec) (void)hipGraphExecDestroy(graph_exec);
@@ -797,10 +798,14 @@ extern "C" int gaje_hip_open(const char *path, int device, gaje_hip_model **out)
     return GAJE_OK;
 }
 
+void batch_detach(gaje_hip_batch *b);
+
 extern "C" void gaje_hip_close(gaje_hip_model *m) {
     if (!m) return;
     (void)hipSetDevice(m->device);
     if (m->stream) (void)hipStreamSynchronize(m->stream);
+    // a batch outliving its model keeps only its handle (its close then frees it)
+    for (gaje_hip_batch *b : m->batches) batch_detach(b);
     delete m;
 }
 
@@ -1254,16 +1259,13 @@ int batch_enqueue_step(gaje_hip_batch *b, const uint32_t *ids, int64_t n, int64_
         Layer &Ly = m->layers[l];
         const int32_t li = (int32_t)l;
         float *kc = b->k_cache + l * b->nseq * seq_kv, *vc = b->v_cache + l * b->nseq * seq_kv;
-        if (Ly.attn_norm) {
-            BatchRowParams r = batch_rows(b, b->H, E, b->XN, E, E);
-            r.w = Ly.attn_norm;
-            r.layer = li;
-            r.st_a = ST_INPUT;
-            r.st_b = ST_ATTN_NORM;
-            GAJE_TRY(launch_rmsnorm_rows(r, s));
-        } else {
-            GAJE_HIP_CHECK(hipMemcpyAsync(b->XN, b->H, (size_t)(L * E) * 4, hipMemcpyDeviceToDevice, s));
-        }
+        BatchRowParams r = batch_rows(b, b->H, E, b->XN, E, E);
+        r.w = Ly.attn_norm;  // null: the rows as they are
+        r.chain_major = 1;
+        r.layer = li;
+        r.st_a = ST_INPUT;
+        r.st_b = Ly.attn_norm ? ST_ATTN_NORM : ST_NONE;
+        GAJE_TRY(launch_rmsnorm_rows(r, s));
         GAJE_TRY(launch_gemv_batch(batch_gemv(b, Ly.qkv, b->XN, E, b->QKV, qkvN), s));
         PrefillRopeParams rp{};
         rp.qkv = b->QKV;
@@ -1296,16 +1298,19 @@ int batch_enqueue_step(gaje_hip_batch *b, const uint32_t *ids, int64_t n, int64_
         ap.seq_kv_stride = seq_kv;
         ap.seq_q_stride = m->q_rows;
         ap.n_seq = (int32_t)b->nseq;
+        ap.out_chain_major = 1;
         GAJE_TRY(launch_attention(ap, s));
         BatchGemvParams g = batch_gemv(b, Ly.o, b->ATT, m->q_rows, b->H, E);
         g.mode = MODE_RESIDUAL;
         GAJE_TRY(launch_gemv_batch(g, s));
-        BatchRowParams r = batch_rows(b, b->H, E, b->XN, E, E);
+        r = batch_rows(b, b->H, E, b->XN, E, E);
         r.w = Ly.ffn_norm;
+        r.chain_major = 1;
         GAJE_TRY(launch_rmsnorm_rows(r, s));
         GAJE_TRY(launch_gemv_batch(batch_gemv(b, Ly.gate_up, b->XN, E, b->GU, guN), s));
         r = batch_rows(b, b->GU, guN, b->ACT, m->ffn, m->ffn);
         r.gnorm = m->use_genomic_norm;
+        r.chain_major = 1;
         r.layer = li;
         r.st_a = ST_UP;
         r.st_b = ST_FFN_OUT;
@@ -1349,7 +1354,8 @@ int batch_sync(gaje_hip_batch *b, int32_t *status) {
 }
 
 int batch_check(gaje_hip_batch *b, int64_t steps) {
-    if (!b || !b->m) return set_error(GAJE_ERR_INVALID_ARG, "null batch handle");
+    if (!b) return set_error(GAJE_ERR_INVALID_ARG, "null batch handle");
+    if (!b->m) return set_error(GAJE_ERR_INVALID_ARG, "the batch's model was closed");
     GAJE_HIP_CHECK(hipSetDevice(b->m->device));
     for (int64_t q = 0; q < b->nseq; ++q)
         if (b->pos[q] + steps > b->cap)
@@ -1430,14 +1436,25 @@ extern "C" int gaje_hip_batch_open(gaje_hip_model *m, int64_t n_seq, int64_t cap
                     (void *)st.embed_ids, (void *)st.next})
         GAJE_HIP_CHECK(hipMemset(p, 0, (size_t)L * 4));
     b->pos.assign((size_t)L, 0);
+    m->batches.push_back(b.get());
     *out = b.release();
     return GAJE_OK;
 }
 
+void batch_detach(gaje_hip_batch *b) {
+    for (void *p : b->allocs) (void)hipFree(p);
+    b->allocs.clear();
+    b->m = nullptr;
+}
+
 extern "C" void gaje_hip_batch_close(gaje_hip_batch *b) {
     if (!b) return;
-    (void)hipSetDevice(b->m->device);
-    (void)hipStreamSynchronize(b->m->stream);
+    if (b->m) {
+        (void)hipSetDevice(b->m->device);
+        (void)hipStreamSynchronize(b->m->stream);
+        auto &v = b->m->batches;
+        v.erase(std::remove(v.begin(), v.end(), b), v.end());
+    }
     delete b;
 }
 
@@ -1457,7 +1474,7 @@ extern "C" int gaje_hip_batch_reset(gaje_hip_batch *b, int64_t seq) {
 }
 
 extern "C" int gaje_hip_batch_cache_len(const gaje_hip_batch *b, int64_t seq, int64_t *len) {
-    if (!b || !len || seq < 0 || seq >= b->nseq) return set_error(GAJE_ERR_INVALID_ARG, "bad arguments");
+    if (!b || !b->m || !len || seq < 0 || seq >= b->nseq) return set_error(GAJE_ERR_INVALID_ARG, "bad arguments");
     *len = b->pos[seq];
     return GAJE_OK;
 }
