@@ -315,6 +315,156 @@ extern "C" int gaje_hip_q4_0_gemm_mfma(const void *packed, const float *X, const
     return launch_gemm_q4(p, pl, s);
 }
 
+namespace {
+
+// Workspace of gaje_hip_moe_ffn.
+struct MoeWorkspace {
+    int *ew_gu, *ew_dn;              // [E][2 ffn], [E][h] weight row exponents
+    int32_t *top_idx, *rows, *slot, *counts, *offsets;
+    float *top_w;
+    uint16_t *xh, *xl;               // [2T][max(h, ffn)] planes
+    int *ex;                         // [2T]
+    float *GU, *Y, *part;            // [2T][2 ffn], [2T][h], split-K partials
+    int64_t part_floats;
+    size_t bytes;
+};
+
+MoeWorkspace moe_workspace(char *base, int64_t T, int64_t h, int64_t ffn, int64_t E) {
+    MoeWorkspace w{};
+    const int64_t R = 2 * T, kmax = std::max(h, ffn);
+    int64_t part = 0;
+    for (int64_t m = 1; m <= R; ++m)
+        part = std::max({part, plan_gemm_q4(m, 2 * ffn, h).part_floats, plan_gemm_q4(m, h, ffn).part_floats});
+    w.part_floats = part;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        char *p = base + off;
+        off = align256(off + bytes);
+        return p;
+    };
+    w.ew_gu = (int *)take((size_t)(E * 2 * ffn) * 4);
+    w.ew_dn = (int *)take((size_t)(E * h) * 4);
+    w.top_idx = (int32_t *)take((size_t)R * 4);
+    w.top_w = (float *)take((size_t)R * 4);
+    w.rows = (int32_t *)take((size_t)R * 4);
+    w.slot = (int32_t *)take((size_t)R * 4);
+    w.counts = (int32_t *)take((size_t)E * 4);
+    w.offsets = (int32_t *)take((size_t)E * 4);
+    w.xh = (uint16_t *)take((size_t)(R * kmax) * 2);
+    w.xl = (uint16_t *)take((size_t)(R * kmax) * 2);
+    w.ex = (int *)take((size_t)R * 4);
+    w.GU = (float *)take((size_t)(R * 2 * ffn) * 4);
+    w.Y = (float *)take((size_t)(R * h) * 4);
+    w.part = (float *)take((size_t)part * 4);
+    w.bytes = off;
+    return w;
+}
+
+int check_moe(int64_t T, int64_t h, int64_t ffn, int64_t E) {
+    if (T <= 0 || T > 65535 || h <= 0 || h % 32 || ffn <= 0 || ffn % 32 || E < 2 || E > MOE_MAX_EXPERTS)
+        return set_error(GAJE_ERR_INVALID_ARG, "moe: T %lld (1..65535), h %lld and ffn %lld (multiples of 32), %lld experts (2..%d)",
+                         (long long)T, (long long)h, (long long)ffn, (long long)E, MOE_MAX_EXPERTS);
+    return GAJE_OK;
+}
+
+}  // namespace
+
+extern "C" int64_t gaje_hip_moe_ffn_workspace(int64_t T, int64_t h, int64_t ffn, int64_t n_expert) {
+    if (check_moe(T, h, ffn, n_expert) != GAJE_OK) return -1;
+    return (int64_t)moe_workspace(nullptr, T, h, ffn, n_expert).bytes;
+}
+
+extern "C" int gaje_hip_moe_ffn(const float *x, int64_t T, int64_t h, const float *router, int64_t n_expert,
+                                const void *const *gate_up, const void *const *down, int64_t ffn, float *y,
+                                int32_t *top_idx, float *top_w, void *workspace, int64_t workspace_bytes,
+                                void *stream) {
+    GAJE_TRY(check_moe(T, h, ffn, n_expert));
+    if (!x || !router || !gate_up || !down || !y || !workspace) return set_error(GAJE_ERR_INVALID_ARG, "moe: null argument");
+    for (int64_t e = 0; e < n_expert; ++e)
+        if (!gate_up[e] || !down[e]) return set_error(GAJE_ERR_INVALID_ARG, "moe: expert %lld has no weights", (long long)e);
+    const MoeWorkspace w = moe_workspace((char *)workspace, T, h, ffn, n_expert);
+    if ((int64_t)w.bytes > workspace_bytes)
+        return set_error(GAJE_ERR_INVALID_ARG, "moe workspace of %lld bytes is smaller than the %zu needed",
+                         (long long)workspace_bytes, w.bytes);
+    hipStream_t s = as_stream(stream);
+    const int64_t R = 2 * T;
+    for (int64_t e = 0; e < n_expert; ++e) {
+        GAJE_TRY(launch_q4_row_exponents((const uint8_t *)gate_up[e], 2 * ffn, h, w.ew_gu + e * 2 * ffn, s));
+        GAJE_TRY(launch_q4_row_exponents((const uint8_t *)down[e], h, ffn, w.ew_dn + e * h, s));
+    }
+    MoeParams mp{};
+    mp.x = x;
+    mp.ldx = h;
+    mp.T = T;
+    mp.h = h;
+    mp.router = router;
+    mp.n_expert = (int32_t)n_expert;
+    mp.top_idx = w.top_idx;
+    mp.top_w = w.top_w;
+    mp.rows = w.rows;
+    mp.slot = w.slot;
+    mp.counts = w.counts;
+    mp.offsets = w.offsets;
+    mp.y = y;
+    mp.ldy = h;
+    GAJE_TRY(launch_moe_route(mp, s));
+    int32_t counts[MOE_MAX_EXPERTS], offsets[MOE_MAX_EXPERTS];
+    GAJE_HIP_CHECK(hipMemcpyAsync(counts, w.counts, (size_t)n_expert * 4, hipMemcpyDeviceToHost, s));
+    GAJE_HIP_CHECK(hipMemcpyAsync(offsets, w.offsets, (size_t)n_expert * 4, hipMemcpyDeviceToHost, s));
+    GAJE_HIP_CHECK(hipStreamSynchronize(s));
+
+    // gate_up of every expert over its gathered tokens
+    SplitParams sp{};
+    sp.x = x;
+    sp.ldx = h;
+    sp.xh = w.xh;
+    sp.xl = w.xl;
+    sp.ldh = h;
+    sp.ex = w.ex;
+    sp.M = R;
+    sp.K = h;
+    sp.rows = w.rows;
+    GAJE_TRY(launch_split_rows(sp, s));
+    auto gemm = [&](const void *wt, const int *ew, int64_t m0, int64_t M, int64_t N, int64_t K, float *Y) {
+        GemmQ4Params p{};
+        p.w = (const uint8_t *)wt;
+        p.ew = ew;
+        p.xh = w.xh + m0 * K;
+        p.xl = w.xl + m0 * K;
+        p.ex = w.ex + m0;
+        p.ldh = K;
+        p.y = Y + m0 * N;
+        p.ldy = N;
+        p.part = w.part;
+        p.M = M;
+        p.N = N;
+        p.nb = (int32_t)(K / 32);
+        return launch_gemm_q4(p, plan_gemm_q4(M, N, K), s);
+    };
+    for (int64_t e = 0; e < n_expert; ++e)
+        if (counts[e] > 0) GAJE_TRY(gemm(gate_up[e], w.ew_gu + e * 2 * ffn, offsets[e], counts[e], 2 * ffn, h, w.GU));
+    // swiglu of every dispatched row, then down
+    sp = SplitParams{};
+    sp.x = w.GU;
+    sp.up = w.GU + ffn;
+    sp.ldx = 2 * ffn;
+    sp.h_scale = 1.0f;
+    sp.xh = w.xh;
+    sp.xl = w.xl;
+    sp.ldh = ffn;
+    sp.ex = w.ex;
+    sp.M = R;
+    sp.K = ffn;
+    sp.st_a = sp.st_b = -1;
+    GAJE_TRY(launch_split_rows(sp, s));
+    for (int64_t e = 0; e < n_expert; ++e)
+        if (counts[e] > 0) GAJE_TRY(gemm(down[e], w.ew_dn + e * h, offsets[e], counts[e], h, ffn, w.Y));
+    GAJE_TRY(launch_moe_combine(mp, w.Y, s));
+    if (top_idx) GAJE_HIP_CHECK(hipMemcpyAsync(top_idx, w.top_idx, (size_t)R * 4, hipMemcpyDeviceToDevice, s));
+    if (top_w) GAJE_HIP_CHECK(hipMemcpyAsync(top_w, w.top_w, (size_t)R * 4, hipMemcpyDeviceToDevice, s));
+    return GAJE_OK;
+}
+
 extern "C" int gaje_hip_lut4_gemv(const uint8_t *codes, const float *lut, int64_t lut_len, const float *x,
                                   const float *bias, int64_t bias_len, float *y, int64_t n, int64_t k, void *stream) {
     GAJE_TRY(check_dims(n, k));

@@ -85,10 +85,10 @@ __global__ __launch_bounds__(256) void split_rows_kernel(SplitParams p) {
     const int64_t m = blockIdx.x;
     const int tid = threadIdx.x;
     const int64_t K = p.K, K4 = K >> 2;
-    const float *xr = p.x + m * p.ldx;
+    const float *xr = p.x + (p.rows ? (int64_t)p.rows[m] : m) * p.ldx;
     int bad_a = 0, bad_b = 0;
     if constexpr (PRO == SPLIT_SWIGLU) {
-        const float *ur = p.up + m * p.ldx;
+        const float *ur = p.up + (p.rows ? (int64_t)p.rows[m] : m) * p.ldx;
         for (int64_t i = tid; i < K4; i += 256) {
             const float4 g = *(const float4 *)(xr + 4 * i), u = *(const float4 *)(ur + 4 * i);
             bad_a |= isnan(u.x) | isnan(u.y) | isnan(u.z) | isnan(u.w);

@@ -172,6 +172,7 @@ struct SplitParams {
     int64_t ldh;
     int *ex;                 // [M] row exponents
     int64_t M, K;
+    const int32_t *rows;     // plane row m takes input row rows[m] (a gather), or null
 };
 int launch_split_rows(const SplitParams &p, hipStream_t s);
 // Per packed Q4_0 row: the exponent that scales its largest |d| into [2^14, 2^15).
@@ -292,6 +293,24 @@ struct BatchState {
 };
 int launch_batch_begin(const BatchState &b, const uint32_t *ids, int64_t n, int64_t i, hipStream_t s);
 int launch_batch_end(const BatchState &b, uint32_t *out, int64_t n, int64_t i, int greedy, hipStream_t s);
+
+// Mixture-of-experts FFN (top-2 routing over Q4_0 SwiGLU experts).
+constexpr int MOE_MAX_EXPERTS = 16;
+struct MoeParams {
+    const float *x;          // [T][ldx] token activations
+    int64_t ldx, T, h;
+    const float *router;     // [n_expert][h] f32 router rows
+    int32_t n_expert;
+    int32_t *top_idx;        // [T][2] chosen experts (top-1, top-2)
+    float *top_w;            // [T][2] renormalised weights
+    int32_t *rows;           // [2T] token of each dispatched row (experts in id order)
+    int32_t *slot;           // [T][2] dispatched row of each (token, choice)
+    int32_t *counts, *offsets;  // [n_expert]
+    float *y;                // [T][ldy] output
+    int64_t ldy;
+};
+int launch_moe_route(const MoeParams &p, hipStream_t s);
+int launch_moe_combine(const MoeParams &p, const float *Y, hipStream_t s);
 
 int launch_finalize(DevState *st, uint32_t *out_tokens, hipStream_t s);
 int launch_kwta(float *x, int64_t n, int64_t k, DevState *st, hipStream_t s);

@@ -117,6 +117,9 @@ SIGNATURES = [
     ("gaje_hip_q4_0_gemm_mfma_workspace", c_i64, [c_i64, c_i64, c_i64]),
     ("gaje_hip_q4_0_gemm_mfma", ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_vp,
                                                c_i64, c_vp]),
+    ("gaje_hip_moe_ffn_workspace", c_i64, [c_i64, c_i64, c_i64, c_i64]),
+    ("gaje_hip_moe_ffn", ctypes.c_int, [c_vp, c_i64, c_i64, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp,
+                                        c_vp, c_i64, c_vp]),
     ("gaje_hip_lut4_gemv", ctypes.c_int, [c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_vp]),
     ("gaje_hip_f32_gemv", ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_vp]),
     ("gaje_hip_q4_0_dequant", ctypes.c_int, [c_vp, c_vp, c_i64, c_vp]),

@@ -122,6 +122,21 @@ def q4_0_gemm_mfma(packed: DeviceBuffer, X: DeviceBuffer, Y: DeviceBuffer, m: in
                                         workspace.ptr, workspace.nbytes, stream))
 
 
+def moe_ffn_workspace(T: int, h: int, ffn: int, n_expert: int) -> int:
+    return int(lib().gaje_hip_moe_ffn_workspace(T, h, ffn, n_expert))
+
+
+def moe_ffn(x: DeviceBuffer, T: int, h: int, router: DeviceBuffer, gate_up, down, ffn: int,
+            y: DeviceBuffer, workspace: DeviceBuffer, top_idx: DeviceBuffer | None = None,
+            top_w: DeviceBuffer | None = None, stream=None) -> None:
+    """Top-2 MoE SwiGLU FFN over packed Q4_0 experts (gaje_hip_moe_ffn)."""
+    E = len(gate_up)
+    gu = (ctypes.c_void_p * E)(*[b.ptr for b in gate_up])
+    dn = (ctypes.c_void_p * E)(*[b.ptr for b in down])
+    check(lib().gaje_hip_moe_ffn(x.ptr, T, h, router.ptr, E, gu, dn, ffn, y.ptr, _p(top_idx), _p(top_w),
+                                 workspace.ptr, workspace.nbytes, stream))
+
+
 def lut4_gemv(codes: DeviceBuffer, lut: DeviceBuffer, lut_len: int, x: DeviceBuffer,
               y: DeviceBuffer, n: int, k: int, bias: DeviceBuffer | None = None,
               bias_len: int = 0, stream=None) -> None:

@@ -113,6 +113,25 @@ int gaje_hip_q4_0_gemm_mfma(const void *packed, const float *X, const float *bia
                             float *Y, int64_t m, int64_t n, int64_t k, void *workspace,
                             int64_t workspace_bytes, void *stream);
 
+/* Mixture-of-experts SwiGLU FFN layer with top-2 routing over Q4_0 experts.
+ * No reference counterpart (the reference has no MoE); a composition of its
+ * primitives: router logits l_e = dot_product(x_t, router_e) (dot.rs:23-94,
+ * bit-exact), p = softmax(l) with expf(l_e - max) and a serial sum in expert
+ * order, the two largest p (ties to the lower expert id) with weights
+ * renormalised to w/(p_a + p_b), expert FFN_e(x) = down_e(swiglu_balanced(
+ * gate_e(x), up_e(x))) (linear/forward.rs:84-92, activation.rs:35-51), and
+ * y_t = (w_a FFN_a(x_t)) + (w_b FFN_b(x_t)).  Routing is exact; the expert
+ * products run on the MFMA units (fp32 accuracy, as gaje_hip_q4_0_gemm_mfma).
+ * x, y: [T][h] device f32; router: [n_expert][h] device f32; gate_up[e] and
+ * down[e] (host arrays of device pointers): packed Q4_0 rows (gaje_hip_q4_0_pack)
+ * of [2 ffn][h] (gate rows then up rows) and [h][ffn]; top_idx, top_w
+ * (optional, device [T][2]) receive the routing.  h and ffn multiples of 32,
+ * 2..16 experts, T <= 65535. */
+int64_t gaje_hip_moe_ffn_workspace(int64_t T, int64_t h, int64_t ffn, int64_t n_expert);
+int gaje_hip_moe_ffn(const float *x, int64_t T, int64_t h, const float *router, int64_t n_expert,
+                     const void *const *gate_up, const void *const *down, int64_t ffn, float *y,
+                     int32_t *top_idx, float *top_w, void *workspace, int64_t workspace_bytes, void *stream);
+
 /* LUT-4bit matvec (layout Genomic4Bit, high nibble = even element):
  * genomic_dot_product_4bit (genomic.rs:148-204) over the row slicing of
  * linear/forward.rs:59-83.  lut_len floats as stored in the file: 16 (one

@@ -492,6 +492,62 @@ class GenomicLLM:
         return generated
 
 
+def moe_route(x: np.ndarray, router: np.ndarray):
+    """Top-2 routing of the MoE layer (no reference function; the composition the
+    device layer defines): logits by dot_product (dot.rs:23-94), softmax with
+    expf(l - max) and a serial sum in expert order, p_e = e_e / sum, the two
+    largest p (ties to the lower id), weights p / (p_a + p_b).  Parity of the
+    routing semantics themselves is unpinned (nothing in the reference fixes
+    them); the arithmetic is float32 throughout."""
+    x = _f32(x)
+    router = _f32(router)
+    T, E = x.shape[0], router.shape[0]
+    idx = np.zeros((T, 2), np.int32)
+    w = np.zeros((T, 2), np.float32)
+    for t in range(T):
+        l = np.array([dot_f32(x[t], router[e]) for e in range(E)], np.float32)
+        mx = l[0]
+        for e in range(1, E):
+            mx = l[e] if l[e] > mx else mx
+        ex = expf((l - mx).astype(np.float32))
+        s = np.float32(0.0)
+        for e in range(E):
+            s = np.float32(s + ex[e])
+        p = (ex / s).astype(np.float32)
+        a = 0
+        for e in range(1, E):
+            if p[e] > p[a]:
+                a = e
+        b = 1 if a == 0 else 0
+        for e in range(E):
+            if e != a and p[e] > p[b]:
+                b = e
+        den = np.float32(p[a] + p[b])
+        idx[t] = (a, b)
+        w[t] = (np.float32(p[a] / den), np.float32(p[b] / den))
+    return idx, w
+
+
+def moe_ffn(x: np.ndarray, router: np.ndarray, gate_up, down, ffn: int):
+    """The MoE layer through the oracle's GenomicLinear rows: expert e is
+    down_e(swiglu_balanced(gate_e(x), up_e(x))) with Q4_0 blocks gate_up[e]
+    ([2 ffn][h]) and down[e] ([h][ffn]); y = (w_a f_a) + (w_b f_b)."""
+    x = _f32(x)
+    T, h = x.shape
+    idx, w = moe_route(x, router)
+    gu = [GenomicLinear(b, b"", None, 2 * ffn, h, None, 4) for b in gate_up]
+    dn = [GenomicLinear(b, b"", None, h, ffn, None, 4) for b in down]
+    y = np.zeros((T, h), np.float32)
+    for t in range(T):
+        f = []
+        for k in range(2):
+            e = int(idx[t, k])
+            g = gu[e].forward_core(x[t])
+            f.append(dn[e].forward_core(swiglu_balanced(g[:ffn], g[ffn:])))
+        y[t] = (w[t, 0] * f[0]).astype(np.float32) + (w[t, 1] * f[1]).astype(np.float32)
+    return y, idx, w
+
+
 def argmax_first(logits: np.ndarray) -> int:
     """Greedy argmax with the reference's strict '>' (llm/forward.rs:262-271)."""
     v = np.where(np.isnan(logits), -np.inf, np.asarray(logits, dtype=np.float32))
