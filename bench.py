@@ -16,6 +16,14 @@ Also reported on the same run:
     copies (348 MB, beyond the 256 MB last-level cache) and hot in cache;
   - the CPU oracle (AVX2 restatement of the reference kernels) on the host cores.
 
+Secondary workloads (same JSON line, under "workloads"):
+  - Qwen2.5-1.5B-shaped (hidden 1536, 28 layers, 12/2 heads, ffn 8960,
+    vocab 151936) 512-token prompt prefill on the MFMA units, and batch-16
+    greedy decode (each sequence fed a 1024-token random context, then 128
+    steps, bit-exact per sequence);
+  - a Q4_0 MoE SwiGLU FFN layer: hidden 1536, 8 experts of ffn 4096, top-2,
+    256 tokens.
+
 Prints ONE JSON line on stdout; progress goes to stderr.
 """
 import argparse
@@ -115,6 +123,82 @@ def cpu_baseline(path: str, prompt, seconds: float, threads: int):
                        f"{O.get_threads()} threads; AVX2 restatement of the reference kernels")
 
 
+def c3_workloads(d: str, seed: int, prefill_tokens: int = 512, batch: int = 16, ctx: int = 1024, gen: int = 128):
+    """Qwen2.5-1.5B-shaped MFMA prefill and batch-16 decode."""
+    import gaje_hip
+    from gaje_hip import ops
+    path = model_path("qwen2.5-1.5b", seed, d)
+    g = gaje_hip.load_genomic_auto(path)
+    g.set_k_wta_ratio(0.0)
+    rng = np.random.default_rng(seed + 1)
+    ids = rng.integers(0, g.vocab_size, prefill_tokens).astype(np.uint32)
+    g.reserve(prefill_tokens + 1)
+    times = []
+    for _ in range(4):
+        g.clear_cache_py()
+        ops.synchronize()
+        t = time.perf_counter()
+        g.prefill_mfma(ids)
+        ops.synchronize()
+        times.append(time.perf_counter() - t)
+    pf = min(times[1:])
+    body_flop = 2.0 * prefill_tokens * sum(
+        n * k for n, k in ((2048, 1536), (1536, 1536), (17920, 1536), (1536, 8960))) * g.info["n_blocks"]
+    prefill = dict(tokens=prefill_tokens, ms=round(pf * 1e3, 3), tok_s=round(prefill_tokens / pf, 1),
+                   body_TFLOPs=round(body_flop / pf / 1e12, 2), body_flop=body_flop,
+                   precision="f16 hi/lo operand pairs, fp32 accumulation (fp32-level accuracy)")
+    log(f"[bench] C3 prefill {prefill_tokens}: {pf * 1e3:.2f} ms = {prefill_tokens / pf:.0f} tok/s, "
+        f"body {body_flop / pf / 1e12:.1f} TFLOP/s")
+    b = gaje_hip.GenomicBatch(g, batch, ctx + 2 * gen + 1)
+    ctx_ids = rng.integers(0, g.vocab_size, (batch, ctx)).astype(np.uint32)
+    t = time.perf_counter()
+    logits = b.feed(ctx_ids, want_logits=True)
+    ops.synchronize()
+    feed_s = time.perf_counter() - t
+    first = logits.argmax(axis=1).astype(np.uint32)
+    b.decode_greedy(first, 8)  # warm-up steps
+    ops.synchronize()
+    t = time.perf_counter()
+    out = b.decode_greedy(first, gen)
+    ops.synchronize()
+    el = time.perf_counter() - t
+    decode = dict(batch=batch, context=ctx, steps=gen, ms_per_step=round(el / gen * 1e3, 3),
+                  tok_s=round(batch * gen / el, 1), feed_s=round(feed_s, 2),
+                  note="each sequence bit-exact with its own forward_core; contexts fed through batched steps")
+    log(f"[bench] C3 batch-{batch} decode: {el / gen * 1e3:.2f} ms/step = {batch * gen / el:.0f} tok/s "
+        f"(context {ctx}+, fed in {feed_s:.1f}s)")
+    b.close()
+    g.close()
+    return prefill, decode, [int(v) for v in out[0, :4]]
+
+
+def moe_workload(seed: int, T: int = 256, h: int = 1536, ffn: int = 4096, E: int = 8, iters: int = 50):
+    from gaje_hip import ops, synth
+    x = synth.normal(seed + 51, "moe.x", T * h).reshape(T, h)
+    router = synth.normal(seed + 52, "moe.r", E * h, 0.0, 0.02).reshape(E, h)
+    gu = [ops.q4_0_upload(synth.q4_0_tensor(seed + 53, f"moe.gu.{e}", 2 * ffn, h), 2 * ffn, h) for e in range(E)]
+    dn = [ops.q4_0_upload(synth.q4_0_tensor(seed + 53, f"moe.dn.{e}", h, ffn), h, ffn) for e in range(E)]
+    xd, rd = ops.DeviceBuffer.from_array(x), ops.DeviceBuffer.from_array(router)
+    y = ops.DeviceBuffer(T * h * 4)
+    ws = ops.DeviceBuffer(ops.moe_ffn_workspace(T, h, ffn, E))
+    for _ in range(3):
+        ops.moe_ffn(xd, T, h, rd, gu, dn, ffn, y, ws)
+    ops.synchronize()
+    e0, e1 = ops.Event(), ops.Event()
+    e0.record()
+    for _ in range(iters):
+        ops.moe_ffn(xd, T, h, rd, gu, dn, ffn, y, ws)
+    e1.record()
+    e1.synchronize()
+    ms = e0.elapsed_ms(e1) / iters
+    flop = 2.0 * T * 2 * (2 * ffn * h + h * ffn)
+    wbytes = E * (2 * ffn * h + h * ffn) * 20 // 32
+    log(f"[bench] C4 MoE layer: {ms * 1e3:.1f} us, {flop / ms / 1e9:.1f} TFLOP/s (expert products)")
+    return dict(tokens=T, hidden=h, ffn=ffn, experts=E, top_k=2, us_per_layer=round(ms * 1e3, 2),
+                expert_TFLOPs=round(flop / ms / 1e9, 2), expert_flop=flop, expert_weight_bytes=wbytes,
+                tokens_per_s=round(T / ms * 1e3, 1))
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -128,6 +212,12 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-stages", action="store_true")
+    ap.add_argument("--no-c3", action="store_true", help="skip the Qwen2.5-1.5B prefill and batched decode")
+    ap.add_argument("--c3-ctx", type=int, default=1024, help="context fed to each batched sequence")
+    ap.add_argument("--c3-gen", type=int, default=128, help="batched greedy steps timed")
+    ap.add_argument("--no-decode", action="store_true",
+                    help="skip the Qwen2-0.5B decode, its stages and the C0 matvec (profiling runs of the other workloads)")
+    ap.add_argument("--no-moe", action="store_true", help="skip the MoE layer")
     ap.add_argument("--gemv-only", action="store_true",
                     help="only the C0 Q4_0 matvec (cold) and a 256 MiB device copy, for counter runs")
     args = ap.parse_args()
@@ -156,73 +246,85 @@ def main():
         return
 
     d = args.model_dir or tempfile.gettempdir()
-    path = model_path(args.preset, args.seed, d)
-    t = time.perf_counter()
-    g = gaje_hip.load_genomic_auto(path)
-    log(f"[bench] loaded {g.info['weight_bytes'] / 1e9:.2f} GB of weights into HBM in {time.perf_counter() - t:.1f}s")
-    g.set_k_wta_ratio(0.0)
-    vocab = g.vocab_size
-    prompt = np.random.default_rng(args.seed).integers(0, vocab, args.prompt).astype(np.uint32)
-    g.reserve(args.prompt + args.gen + 1)
-    g.clear_cache_py()
-    t = time.perf_counter()
-    g.prefill(prompt)
-    log(f"[bench] prefilled {args.prompt} tokens token-by-token in {time.perf_counter() - t:.2f}s")
+    tok_s = el = None
+    toks = []
+    stages, gemv, roofline, path, prompt = {}, None, None, None, None
+    if not args.no_decode:
+        path = model_path(args.preset, args.seed, d)
+        t = time.perf_counter()
+        g = gaje_hip.load_genomic_auto(path)
+        log(f"[bench] loaded {g.info['weight_bytes'] / 1e9:.2f} GB of weights into HBM in {time.perf_counter() - t:.1f}s")
+        g.set_k_wta_ratio(0.0)
+        vocab = g.vocab_size
+        prompt = np.random.default_rng(args.seed).integers(0, vocab, args.prompt).astype(np.uint32)
+        g.reserve(args.prompt + args.gen + 1)
+        g.clear_cache_py()
+        t = time.perf_counter()
+        g.prefill(prompt)
+        log(f"[bench] prefilled {args.prompt} tokens token-by-token in {time.perf_counter() - t:.2f}s")
 
-    def step():
-        g.truncate_cache(args.prompt)
-        return g.decode_greedy(int(prompt[-1]), args.gen)
+        def step():
+            g.truncate_cache(args.prompt)
+            return g.decode_greedy(int(prompt[-1]), args.gen)
 
-    for _ in range(args.warmup):
-        step()
-    ops.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        toks = step()
-    ops.synchronize()
-    el = time.perf_counter() - t0
-    tok_s = args.gen * args.steps / el
-    log(f"[bench] decode: {tok_s:.1f} tok/s ({el / args.steps * 1e3:.1f} ms per {args.gen}-token step)")
+        for _ in range(args.warmup):
+            step()
+        ops.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            toks = step()
+        ops.synchronize()
+        el = time.perf_counter() - t0
+        tok_s = args.gen * args.steps / el
+        log(f"[bench] decode: {tok_s:.1f} tok/s ({el / args.steps * 1e3:.1f} ms per {args.gen}-token step)")
 
-    stages = {}
-    roofline = None
-    if not args.no_stages:
-        counts = {"qkv": g.info["n_blocks"], "attention": g.info["n_blocks"], "o": g.info["n_blocks"],
-                  "gate_up": g.info["n_blocks"], "down": g.info["n_blocks"], "lm_head": 1}
-        g.truncate_cache(args.prompt + args.gen - 1)  # time at the last step's context
-        for s in ("qkv", "attention", "o", "gate_up", "down", "lm_head", "token"):
-            ms, nbytes = g.time_stage(s, layer=0, iters=200 if s != "token" else 50)
-            gbps = nbytes / (ms * 1e-3) / 1e9
-            stages[s] = dict(us=round(ms * 1e3, 3), bytes=int(nbytes), GBps=round(gbps, 1),
-                             frac=round(gbps / HBM_PEAK_GBPS, 4))
-            if s in counts:
-                stages[s]["per_token_us"] = round(ms * 1e3 * counts[s], 2)
-            log(f"[bench] stage {s:9s}: {ms * 1e3:8.2f} us  {gbps:8.1f} GB/s")
+        stages = {}
+        roofline = None
+        if not args.no_stages:
+            counts = {"qkv": g.info["n_blocks"], "attention": g.info["n_blocks"], "o": g.info["n_blocks"],
+                      "gate_up": g.info["n_blocks"], "down": g.info["n_blocks"], "lm_head": 1}
+            g.truncate_cache(args.prompt + args.gen - 1)  # time at the last step's context
+            for s in ("qkv", "attention", "o", "gate_up", "down", "lm_head", "token"):
+                ms, nbytes = g.time_stage(s, layer=0, iters=200 if s != "token" else 50)
+                gbps = nbytes / (ms * 1e-3) / 1e9
+                stages[s] = dict(us=round(ms * 1e3, 3), bytes=int(nbytes), GBps=round(gbps, 1),
+                                 frac=round(gbps / HBM_PEAK_GBPS, 4))
+                if s in counts:
+                    stages[s]["per_token_us"] = round(ms * 1e3 * counts[s], 2)
+                log(f"[bench] stage {s:9s}: {ms * 1e3:8.2f} us  {gbps:8.1f} GB/s")
 
-    gemv = q4_gemv_c0()
-    log(f"[bench] Q4_0 GEMV C0: cold {gemv['cold_us']:.2f} us = {gemv['cold_GBps']:.0f} GB/s "
-        f"({100 * gemv['cold_frac']:.1f}% of HBM peak); hot {gemv['hot_us']:.2f} us")
-    # the metric's kernel: the C0 Q4_0 matvec, cold, timed with HIP events on its own stream
-    roofline = dict(kernel="gemv_kernel<Q4_0> (C0: K=896, N=4864, 128 cold weight copies)", bound="hbm",
-                    achieved=round(gemv["cold_GBps"], 1), peak=HBM_PEAK_GBPS, unit="GB/s",
-                    frac=round(gemv["cold_frac"], 4), traffic=read_traffic(),
-                    bytes_per_launch=gemv["algorithmic_bytes"], us_per_launch=round(gemv["cold_us"], 3))
+        gemv = q4_gemv_c0()
+        log(f"[bench] Q4_0 GEMV C0: cold {gemv['cold_us']:.2f} us = {gemv['cold_GBps']:.0f} GB/s "
+            f"({100 * gemv['cold_frac']:.1f}% of HBM peak); hot {gemv['hot_us']:.2f} us")
+        # the metric's kernel: the C0 Q4_0 matvec, cold, timed with HIP events on its own stream
+        roofline = dict(kernel="gemv_kernel<Q4_0> (C0: K=896, N=4864, 128 cold weight copies)", bound="hbm",
+                        achieved=round(gemv["cold_GBps"], 1), peak=HBM_PEAK_GBPS, unit="GB/s",
+                        frac=round(gemv["cold_frac"], 4), traffic=read_traffic(),
+                        bytes_per_launch=gemv["algorithmic_bytes"], us_per_launch=round(gemv["cold_us"], 3))
+
+        g.close()
+    workloads = {}
+    if not args.no_c3:
+        prefill, decode, c3_tokens = c3_workloads(d, args.seed, ctx=args.c3_ctx, gen=args.c3_gen)
+        workloads["qwen2.5-1.5b_prefill_512"] = prefill
+        workloads["qwen2.5-1.5b_batch16_decode"] = decode
+    if not args.no_moe:
+        workloads["moe_ffn_256x1536_8x4096_top2"] = moe_workload(args.seed)
 
     cpu = None
-    if not args.no_cpu:
+    if not args.no_cpu and path is not None:
         threads = min(16, os.cpu_count() or 1)
         cpu = cpu_baseline(path, prompt, args.cpu_seconds, threads)
         log(f"[bench] cpu oracle: {cpu['value']:.2f} tok/s on {cpu['cores']} threads")
-    g.close()
 
     out = {
         "metric": METRIC,
-        "value": round(tok_s, 2),
+        "value": round(tok_s, 2) if tok_s else None,
         "unit": "tok/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(el / args.steps * 1e3, 3),
+        "ms_per_step": round(el / args.steps * 1e3, 3) if el else None,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -236,6 +338,7 @@ def main():
         "cpu_baseline": cpu,
         "q4_0_gemv": gemv,
         "stages": stages,
+        "workloads": workloads,
         "last_tokens": [int(t) for t in toks[-4:]],
     }
     print(json.dumps(out), flush=True)
