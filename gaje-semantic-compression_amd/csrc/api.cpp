@@ -495,6 +495,26 @@ extern "C" int gaje_hip_q4_0_dequant(const void *blocks, float *out, int64_t nbl
     return launch_dequant_q4_0((const uint8_t *)blocks, out, nblocks, as_stream(stream));
 }
 
+extern "C" int gaje_hip_q8_0_dequant(const void *blocks, float *out, int64_t nblocks, void *stream) {
+    return launch_dequant_q8_0((const uint8_t *)blocks, out, nblocks, as_stream(stream));
+}
+
+extern "C" int64_t gaje_hip_q8_0_packed_bytes(int64_t n, int64_t k) {
+    if (n < 0 || k <= 0 || k % 32 != 0) return -1;
+    return q8_0_packed_bytes(n, k);
+}
+
+extern "C" int gaje_hip_q8_0_pack(const void *blocks, void *packed, int64_t n, int64_t k, void *stream) {
+    GAJE_TRY(check_dims(n, k));
+    return launch_pack_q8_0((const uint8_t *)blocks, (uint8_t *)packed, n, k, as_stream(stream));
+}
+
+extern "C" int gaje_hip_q8_0_gemv(const void *packed, const float *x, const float *bias, int64_t bias_len, float *y,
+                                  int64_t n, int64_t k, void *stream) {
+    GAJE_TRY(check_dims(n, k));
+    return launch_gemv(plain_gemv(FMT_Q8_0, packed, x, bias, bias_len, y, n, k), as_stream(stream));
+}
+
 extern "C" int gaje_hip_rmsnorm(const float *x, const float *w, float eps, float *y, int64_t n, void *stream) {
     return launch_rmsnorm(x, w, eps, y, n, as_stream(stream));
 }

@@ -246,6 +246,136 @@ __device__ __forceinline__ void q4_zero_x_pad(const XView &xv, int nb) {
     }
 }
 
+// ---------------------------------------------------------------- Q8_0 ----
+// Packed Q8_0 rows (genomic_dot_product_q8_0_avx2, genomic.rs:377-448, has
+// the Q4_0 kernel's chain structure: lane l owns element 8c+l of every block).
+// Per group of four Q8_0Blocks (128 weights): chain l's 16 bytes at
+// [16l, 16l+16), dword b = block 4g+b, byte c = element 8c+l (signed); the four
+// f16 scales at [128, 136); 8 zero bytes.  144 bytes per group (the file's
+// 136 plus alignment for the 16-byte chain loads).
+constexpr int Q8_GROUP = 144;
+
+template <int D>
+struct Q8Ring {
+    vu4 n[D];
+    vu2 s[D];
+};
+
+// dq = f32(q) * scale (genomic.rs:425-428): an exact product
+__device__ __forceinline__ void q8_dequant(float (&d)[4], uint32_t codes, float scale) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) d[c] = (float)(int32_t)(int8_t)(codes >> (8 * c)) * scale;
+}
+
+__device__ __forceinline__ float q8_group(float acc, const vu4 n, const vu2 s, const X4 &x) {
+    float d0[4], d1[4], d2[4], d3[4];
+    q8_dequant(d0, n.x, half_lo(s.x));
+    q8_dequant(d1, n.y, half_hi(s.x));
+    q8_dequant(d2, n.z, half_lo(s.y));
+    q8_dequant(d3, n.w, half_hi(s.y));
+    acc = q4_chain(acc, d0, x.b0);
+    acc = q4_chain(acc, d1, x.b1);
+    acc = q4_chain(acc, d2, x.b2);
+    acc = q4_chain(acc, d3, x.b3);
+    return acc;
+}
+
+// The row's last groups, as q4_tail: the scales of blocks that do not exist
+// become +0 (their values dequantise to +-0 against zero activations).
+template <int T, int D>
+__device__ __forceinline__ float q8_tail(float acc, const Q8Ring<D> &r, const float *xg, X4 xc, int left) {
+#pragma unroll
+    for (int i = 0; i < T; ++i) {
+        const X4 xn = read_x4(xg + 16 * (i + 1));
+        const int b = left - 4 * i;
+        vu2 s = r.s[i];
+        s.x = (b > 0 ? s.x & 0xFFFFu : 0u) | (b > 1 ? s.x & 0xFFFF0000u : 0u);
+        s.y = (b > 2 ? s.y & 0xFFFFu : 0u) | (b > 3 ? s.y & 0xFFFF0000u : 0u);
+        acc = q8_group(acc, r.n[i], s, xc);
+        xc = xn;
+    }
+    return acc;
+}
+
+template <bool NT, int D>
+__device__ __forceinline__ void q8_prefetch(const uint8_t *w, const GemvParams &p, int64_t row, int l, Q8Ring<D> &r) {
+    const int G = (p.nb + 3) >> 2;
+    const uint8_t *rp = w + (size_t)row * G * Q8_GROUP;
+#pragma unroll
+    for (int i = 0; i < D; ++i) {
+        r.n[i] = ld_u4<NT>(rp + i * Q8_GROUP + 16 * l);
+        r.s[i] = ld_u2<NT>(rp + i * Q8_GROUP + 128);
+    }
+}
+
+// q4_consume for packed Q8_0 rows: the same walk, ring and reduction.
+template <bool NT, int D>
+__device__ __forceinline__ float q8_consume(const GemvParams &p, const XView &xv, int64_t row, int l, int base,
+                                            Q8Ring<D> &r) {
+    const int nb = p.nb;
+    const int G = (nb + 3) >> 2;
+    const int Gf = nb >> 2;
+    const uint8_t *gp = p.w + (size_t)row * G * Q8_GROUP + D * Q8_GROUP;  // next group to load
+    const float *xg = xv.x + l * xv.stride;
+    float acc = 0.0f;
+    X4 xc = read_x4(xg);
+    int g = 0;
+    for (; g + D <= Gf; g += D) {
+#pragma unroll
+        for (int i = 0; i < D; ++i) {
+            const X4 xn = read_x4(xg + 16 * (i + 1));
+            acc = q8_group(acc, r.n[i], r.s[i], xc);
+            r.n[i] = ld_u4<NT>(gp + i * Q8_GROUP + 16 * l);
+            r.s[i] = ld_u2<NT>(gp + i * Q8_GROUP + 128);
+            xc = xn;
+        }
+        gp += D * Q8_GROUP;
+        xg += 16 * D;
+    }
+    const int rem = G - g;
+    if (rem == D - 1) acc = q8_tail<D - 1, D>(acc, r, xg, xc, nb - 4 * g);
+    else if (rem > D / 2) acc = q8_tail<D, D>(acc, r, xg, xc, nb - 4 * g);
+    else if (rem > 0) acc = q8_tail<D / 2, D>(acc, r, xg, xc, nb - 4 * g);
+    const float u = acc + shfl(acc, base + ((l + 4) & 7));
+    const float v = u + shfl(u, base + ((l + 2) & 7));
+    const float total = v + shfl(v, base + ((l + 1) & 7));
+    return flush_small(total);
+}
+
+// Q8_0Block rows (file layout, 34 bytes per block) -> the packed layout; one
+// thread per (row, group); blocks past nb are zero.
+__global__ void pack_q8_0_kernel(const uint8_t *src, uint8_t *dst, int64_t N, int nb) {
+    const int G = (nb + 3) >> 2;
+    const int64_t total = N * G;
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t row = t / G;
+        const int g = (int)(t - row * G);
+        const uint8_t *rs = src + (size_t)row * nb * 34;
+        uint32_t *out = (uint32_t *)(dst + ((size_t)row * G + g) * Q8_GROUP);
+        for (int l = 0; l < 8; ++l)
+            for (int b = 0; b < 4; ++b) {
+                const int j = 4 * g + b;
+                uint32_t word = 0;
+                if (j < nb)
+                    for (int c = 0; c < 4; ++c) word |= (uint32_t)rs[(size_t)j * 34 + 2 + 8 * c + l] << (8 * c);
+                out[4 * l + b] = word;
+            }
+        for (int h = 0; h < 2; ++h) {
+            uint32_t w2 = 0;
+            for (int half = 0; half < 2; ++half) {
+                const int j = 4 * g + 2 * h + half;
+                if (j < nb) w2 |= ((uint32_t)rs[(size_t)j * 34] | ((uint32_t)rs[(size_t)j * 34 + 1] << 8)) << (16 * half);
+            }
+            out[32 + h] = w2;
+        }
+        out[34] = 0;
+        out[35] = 0;
+    }
+    uint32_t *pad = (uint32_t *)(dst + (size_t)total * Q8_GROUP);
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < Q8_TAIL_PAD / 4; t += (int64_t)gridDim.x * blockDim.x)
+        pad[t] = 0;
+}
+
 // Packs Q4_0Block rows (file layout) into the layout above; one thread per
 // (row, group).
 __global__ void pack_q4_0_kernel(const uint8_t *src, uint8_t *dst, int64_t N, int nb) {
@@ -504,7 +634,8 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t K = p.K;
-    const XView xv{smem, FMT == FMT_Q4_0 ? xstride : 0};
+    constexpr bool CHAIN_X = FMT == FMT_Q4_0 || FMT == FMT_Q8_0;  // chain-major activations
+    const XView xv{smem, CHAIN_X ? xstride : 0};
 
     constexpr int PAIR_LANES = 2 * LPR;
     constexpr int PAIRS_PER_WAVE = WAVE / PAIR_LANES;
@@ -519,6 +650,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
     int64_t pr0 = (int64_t)blockIdx.x * pairs_per_block;
     PairRows q = locate<FMT>(p, mode, pr0 + wave * PAIRS_PER_WAVE + pslot, npairs, half);
     Q4Ring<D> q4r;
+    Q8Ring<FMT == FMT_Q8_0 ? D : 1> q8r;
     F32Ring f32r;
     const int halted = st ? st->halted : 0;
     const bool swiglu = mode == MODE_SWIGLU;
@@ -530,7 +662,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
     int bad_in = 0;
     // float4s of the activation vector per thread and batch: Q4_0 rows with
     // the short ring have K <= 1024, which one float4 per thread covers
-    constexpr int XB4 = (FMT == FMT_Q4_0 && D == Q4_PREFETCH) ? 1 : 6;
+    constexpr int XB4 = (CHAIN_X && D == Q4_PREFETCH) ? 1 : 6;
     float4 xr[XB4], wr[XB4];
     if constexpr (FMT == FMT_LUT4) {
         constexpr int XB = 8;
@@ -582,6 +714,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
             const uint8_t *wbase = p.rows_valid > 0 ? p.w : kZeroRows;
             const int64_t prow = q.row_ok ? q.row : 0;
             if constexpr (FMT == FMT_Q4_0) q4_prefetch<NT, D>(wbase, p, prow, s, q4r);
+            else if constexpr (FMT == FMT_Q8_0) q8_prefetch<NT, D>(wbase, p, prow, s, q8r);
             else f32_prefetch<NT>(wbase, p, prow, s, f32r);
         }
         if (halted) return;  // uniform; checked once the first loads are in flight
@@ -592,7 +725,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
                 if (m < K4) {
                     const float4 v = xr[u];
                     const float q[4] = {v.x, v.y, v.z, v.w};
-                    store_quad<FMT == FMT_Q4_0>(xv, (int)m, q);
+                    store_quad<CHAIN_X>(xv, (int)m, q);
                     if (p.norm_w && !one_batch) *(float4 *)(nw + 4 * m) = wr[u];
                     bad_in |= isnan(v.x) | isnan(v.y) | isnan(v.z) | isnan(v.w);
                 }
@@ -609,12 +742,12 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
             }
             store_batch(m0);
         }
-        if constexpr (FMT == FMT_Q4_0) q4_zero_x_pad(xv, p.nb);
+        if constexpr (CHAIN_X) q4_zero_x_pad(xv, p.nb);
         if (swiglu && tid < 32) etab[tid] = tabv;
         // barriers from here on order LDS only: the weight ring stays in flight
         if (barrier_or<THREADS / WAVE>(bad_in, or_in) && p.st_in >= 0 && tid == 0) nan_flag(st, p.layer, p.st_in);
         if (p.norm_w) {
-            if constexpr (FMT == FMT_Q4_0) rms_inv_chain_major(xv, K, p.eps, &inv_slot);
+            if constexpr (CHAIN_X) rms_inv_chain_major(xv, K, p.eps, &inv_slot);
             else rms_inv_plain(smem, K, p.eps, &inv_slot);
             lds_barrier();
             const float inv = inv_slot;
@@ -631,7 +764,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
                             t[c] = t[c] * w4[c];  // (x * inv) * w, each product rounded
                             bad |= isnan(t[c]);
                         }
-                        store_quad<FMT == FMT_Q4_0>(xv, (int)m, t);
+                        store_quad<CHAIN_X>(xv, (int)m, t);
                     }
                 }
             } else {
@@ -689,6 +822,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
             q = locate<FMT>(p, mode, pr, npairs, half);
             if (q.row_ok) {
                 if constexpr (FMT == FMT_Q4_0) q4_prefetch<NT, D>(p.w, p, q.row, s, q4r);
+                else if constexpr (FMT == FMT_Q8_0) q8_prefetch<NT, D>(p.w, p, q.row, s, q8r);
                 else if constexpr (FMT == FMT_F32) f32_prefetch<NT>(p.w, p, q.row, s, f32r);
             }
         }
@@ -715,6 +849,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
         // shuffles only read lanes that execute it
         if (q.row_ok) {
             if constexpr (FMT == FMT_Q4_0) v = q4_consume<NT, D>(p, xv, q.row, s, row_base, q4r);
+            else if constexpr (FMT == FMT_Q8_0) v = q8_consume<NT, D>(p, xv, q.row, s, row_base, q8r);
             else if constexpr (FMT == FMT_F32) v = f32_consume<NT>(p, smem, q.row, s, row_base, f32r);
             else v = row_lut4<NT>(p, smem, q.row, s, row_base, tbl);
         }
@@ -1031,6 +1166,19 @@ int q4_xstride(int64_t K) { return q4_xrow((int)(K / 32)) + 4; }
 }  // namespace
 
 int64_t q4_0_packed_bytes(int64_t N, int64_t K) { return N * ((K / 32 + 3) / 4) * 80 + Q4_TAIL_PAD; }
+int64_t q8_0_packed_bytes(int64_t N, int64_t K) { return N * ((K / 32 + 3) / 4) * Q8_GROUP + Q8_TAIL_PAD; }
+
+int launch_pack_q8_0(const uint8_t *src, uint8_t *dst, int64_t N, int64_t K, hipStream_t s) {
+    if (N < 0 || K <= 0 || K % 32 != 0 || (N > 0 && (!src || !dst)))
+        return set_error(GAJE_ERR_INVALID_ARG, "pack_q8_0: bad arguments");
+    const int64_t G = (K / 32 + 3) / 4;
+    int64_t grid = (N * G + 255) / 256;
+    if (grid < 1) grid = 1;
+    if (grid > 65535) grid = 65535;
+    hipLaunchKernelGGL(pack_q8_0_kernel, dim3((unsigned)grid), dim3(256), 0, s, src, dst, N, (int)(K / 32));
+    GAJE_HIP_CHECK(hipGetLastError());
+    return GAJE_OK;
+}
 
 int launch_pack_q4_0(const uint8_t *src, uint8_t *dst, int64_t N, int64_t K, hipStream_t s) {
     if (N < 0 || K <= 0 || K % 32 != 0) return set_error(GAJE_ERR_INVALID_ARG, "pack: K must be a positive multiple of 32");
@@ -1062,7 +1210,7 @@ int launch_pack_f32_tiled(const float *src, float *dst, int64_t N, int64_t K, hi
 // LDS floats before the norm-weight copy: the activation vector (chain-major
 // for Q4_0, plain otherwise) and, for LUT rows, one 16-entry table per row group.
 static int64_t gemv_x_floats(int64_t K, int fmt) {
-    if (fmt == FMT_Q4_0) return (int64_t)8 * q4_xstride(K);
+    if (fmt == FMT_Q4_0 || fmt == FMT_Q8_0) return (int64_t)8 * q4_xstride(K);
     int64_t f = (K + 3) & ~(int64_t)3;
     if (fmt == FMT_LUT4) f += (int64_t)(THREADS / 4) * 16;
     return f;
@@ -1077,7 +1225,7 @@ size_t gemv_lds_bytes(int64_t K, int fmt, bool norm) {
     // Q4_0: + what the reads ahead may touch past the last chain row: the row
     // walk's next group (16 floats) and the sum-of-squares chain's read-ahead
     // (up to 28 floats with the short ring); never used
-    const int64_t slack = fmt == FMT_Q4_0 ? 32 : 0;
+    const int64_t slack = (fmt == FMT_Q4_0 || fmt == FMT_Q8_0) ? 32 : 0;
     return (size_t)(gemv_x_floats(K, fmt) + (norm ? ((K + 3) & ~(int64_t)3) : 0) + slack) * 4;
 }
 
@@ -1090,9 +1238,10 @@ int launch_gemv(const GemvParams &p, hipStream_t s) {
                          (long long)p.K);
     if (p.fmt == FMT_F32 && p.f32_tiled && p.K % 8 != 0)
         return set_error(GAJE_ERR_INVALID_ARG, "gemv: tiled f32 rows need in_features %% 8 == 0");
-    if (p.fmt == FMT_Q4_0 && p.K % 32 != 0)
-        return set_error(GAJE_ERR_UNSUPPORTED, "gemv: Q4_0 rows need in_features %% 32 == 0 (got %lld)",
+    if ((p.fmt == FMT_Q4_0 || p.fmt == FMT_Q8_0) && p.K % 32 != 0)
+        return set_error(GAJE_ERR_UNSUPPORTED, "gemv: Q4_0/Q8_0 rows need in_features %% 32 == 0 (got %lld)",
                          (long long)p.K);
+    if (p.fmt < FMT_F32 || p.fmt > FMT_Q8_0) return set_error(GAJE_ERR_INVALID_ARG, "gemv: unknown format %d", p.fmt);
     if (p.fmt != FMT_LUT4 && (((uintptr_t)p.x | (uintptr_t)p.norm_w) & 15))
         return set_error(GAJE_ERR_INVALID_ARG, "gemv: x and norm_w must be 16-byte aligned");
     if (p.rows_valid > 0 && !p.w) return set_error(GAJE_ERR_INVALID_ARG, "gemv: null weights");
@@ -1154,6 +1303,14 @@ int launch_gemv(const GemvParams &p, hipStream_t s) {
             fn = gemv_kernel<FMT_Q4_0, 8, false, Q4_PREFETCH, MODE_SWIGLU>;
         else
             fn = p.nontemporal ? gemv_kernel<FMT_Q4_0, 8, true, Q4_PREFETCH> : gemv_kernel<FMT_Q4_0, 8, false, Q4_PREFETCH>;
+    } else if (p.fmt == FMT_Q8_0) {
+        const bool long_rows = q4_depth(p.nb) == 2 * Q4_PREFETCH;
+        lpr = 8;
+        if (long_rows)
+            fn = p.nontemporal ? gemv_kernel<FMT_Q8_0, 8, true, 2 * Q4_PREFETCH>
+                               : gemv_kernel<FMT_Q8_0, 8, false, 2 * Q4_PREFETCH>;
+        else
+            fn = p.nontemporal ? gemv_kernel<FMT_Q8_0, 8, true, Q4_PREFETCH> : gemv_kernel<FMT_Q8_0, 8, false, Q4_PREFETCH>;
     } else if (p.fmt == FMT_LUT4) {
         lpr = 4;
         fn = gemv_kernel<FMT_LUT4, 4, false, 1>;
@@ -1168,7 +1325,7 @@ int launch_gemv(const GemvParams &p, hipStream_t s) {
     // tiled f32 rows stream at the best rate with one workgroup per compute
     // unit walking its share of the tiles (measured on a 151936 x 896 matrix)
     if (p.fmt == FMT_F32 && p.f32_tiled && grid > device_cu_count()) grid = device_cu_count();
-    const int xstride = p.fmt == FMT_Q4_0 ? q4_xstride(p.K) : 0;
+    const int xstride = (p.fmt == FMT_Q4_0 || p.fmt == FMT_Q8_0) ? q4_xstride(p.K) : 0;
     const int nw_off = (int)gemv_x_floats(p.K, p.fmt);
     hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(THREADS), lds, s, p, npairs, xstride, nw_off);
     GAJE_HIP_CHECK(hipGetLastError());

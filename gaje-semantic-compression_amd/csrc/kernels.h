@@ -12,6 +12,7 @@ enum WeightFormat : int32_t {
     FMT_F32 = 0,   // GenomicF32 rows (lm_head / token_embd)
     FMT_Q4_0 = 1,  // 20-byte Q4_0Block rows
     FMT_LUT4 = 2,  // Genomic4Bit: 16-byte code blocks + 16-entry f32 tables
+    FMT_Q8_0 = 3,  // 34-byte Q8_0Block rows
 };
 
 constexpr uint32_t NAN_NONE = 0xFFFFFFFFu;
@@ -101,6 +102,12 @@ int launch_gemv(const GemvParams &p, hipStream_t s);
 constexpr int64_t Q4_TAIL_PAD = 2048;
 int launch_pack_q4_0(const uint8_t *src, uint8_t *dst, int64_t N, int64_t K, hipStream_t s);
 int64_t q4_0_packed_bytes(int64_t N, int64_t K);
+// Q8_0Block rows (K % 32 == 0) -> 144-byte groups of four blocks (chain l's
+// codes at [16l, 16l+16), the four f16 scales at [128, 136)), followed by
+// Q8_TAIL_PAD bytes the matvec's prefetch may read.
+constexpr int64_t Q8_TAIL_PAD = 4096;
+int launch_pack_q8_0(const uint8_t *src, uint8_t *dst, int64_t N, int64_t K, hipStream_t s);
+int64_t q8_0_packed_bytes(int64_t N, int64_t K);
 // Row-major f32 rows (K % 8 == 0) -> the tiled layout: tiles of 32 rows, and in
 // a tile the 8-float chunk c of rows 0..31 is one contiguous KiB, so a wave
 // holding the tile's rows reads each chunk with one coalesced load.  Rows past
@@ -139,7 +146,7 @@ size_t attention_lds_bytes(int head_dim, int64_t max_ctx);
 constexpr int64_t MAX_CTX = 12288;
 
 struct EmbedParams {
-    const uint8_t *w;        // FMT_Q4_0: packed rows
+    const uint8_t *w;        // FMT_Q4_0 / FMT_Q8_0: packed rows
     int32_t fmt;
     const float *lut;
     int64_t lut_rows_own;
@@ -316,6 +323,7 @@ int launch_finalize(DevState *st, uint32_t *out_tokens, hipStream_t s);
 int launch_kwta(float *x, int64_t n, int64_t k, DevState *st, hipStream_t s);
 int launch_argmax(const float *x, int64_t n, uint32_t *idx, hipStream_t s);
 int launch_dequant_q4_0(const uint8_t *blocks, float *out, int64_t nblocks, hipStream_t s);
+int launch_dequant_q8_0(const uint8_t *blocks, float *out, int64_t nblocks, hipStream_t s);
 int launch_rmsnorm(const float *x, const float *w, float eps, float *y, int64_t n, hipStream_t s);
 int launch_swiglu(const float *g, const float *u, float *out, int64_t n, hipStream_t s);
 int launch_expf(const float *x, float *y, int64_t n, hipStream_t s);

@@ -133,6 +133,16 @@ __global__ void dequant_q4_0_kernel(const uint8_t *blocks, float *out, int64_t n
     }
 }
 
+// Q8_0Block::dequantize_weight (blocks.rs:43-49): f32(q) * scale, file layout.
+__global__ void dequant_q8_0_kernel(const uint8_t *blocks, float *out, int64_t nblocks) {
+    const int64_t total = nblocks * 32;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+        const uint8_t *blk = blocks + (e >> 5) * 34;
+        const float q = (float)(int32_t)(int8_t)blk[2 + (e & 31)];
+        out[e] = __fmul_rn(q, half_bits((uint16_t)blk[0] | ((uint16_t)blk[1] << 8)));
+    }
+}
+
 __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float *x, const float *w, float eps, float *y, int64_t n) {
     extern __shared__ __align__(16) float xs[];
     __shared__ float inv_slot;
@@ -212,6 +222,14 @@ int launch_dequant_q4_0(const uint8_t *blocks, float *out, int64_t nblocks, hipS
     if (nblocks < 0 || (nblocks > 0 && (!blocks || !out))) return set_error(GAJE_ERR_INVALID_ARG, "dequant: bad arguments");
     if (nblocks == 0) return GAJE_OK;
     hipLaunchKernelGGL(dequant_q4_0_kernel, dim3(grid_for(nblocks * 32, 256)), dim3(256), 0, s, blocks, out, nblocks);
+    GAJE_HIP_CHECK(hipGetLastError());
+    return GAJE_OK;
+}
+
+int launch_dequant_q8_0(const uint8_t *blocks, float *out, int64_t nblocks, hipStream_t s) {
+    if (nblocks < 0 || (nblocks > 0 && (!blocks || !out))) return set_error(GAJE_ERR_INVALID_ARG, "dequant: bad arguments");
+    if (nblocks == 0) return GAJE_OK;
+    hipLaunchKernelGGL(dequant_q8_0_kernel, dim3(grid_for(nblocks * 32, 256)), dim3(256), 0, s, blocks, out, nblocks);
     GAJE_HIP_CHECK(hipGetLastError());
     return GAJE_OK;
 }

@@ -138,8 +138,7 @@ int read_linear(const FlatFile &f, const std::string &name, HostLinear &L) {
     const uint64_t n_cent = e->c_len / 4;
     if (bit_depth == 4) L.fmt = n_cent == 0 ? FMT_Q4_0 : FMT_LUT4;
     else if (bit_depth == 32) L.fmt = FMT_F32;
-    else if (bit_depth == 8)
-        return set_error(GAJE_ERR_UNSUPPORTED, "tensor '%s': Q8_0 (bit_depth 8) is not in this build", name.c_str());
+    else if (bit_depth == 8) L.fmt = FMT_Q8_0;  // init.rs:40-45
     else
         return set_error(GAJE_ERR_UNSUPPORTED, "tensor '%s': 2-bit genomic format is not in this build", name.c_str());
     if (e->dna_len) L.w.assign(dna, dna + e->dna_len);
@@ -169,6 +168,7 @@ int64_t rows_valid_of(const HostLinear &L) {
     if (L.fmt == FMT_F32) return L.K ? std::min<int64_t>(L.N, (int64_t)(L.w.size() / 4) / L.K) : 0;
     if (nb == 0) return 0;
     if (L.fmt == FMT_Q4_0) return std::min<int64_t>(L.N, (int64_t)(L.w.size() / 20) / nb);
+    if (L.fmt == FMT_Q8_0) return std::min<int64_t>(L.N, (int64_t)(L.w.size() / 34) / nb);
     if (L.lut.size() < 16) return 0;  // no table: compute_single_row yields 0
     return std::min<int64_t>(L.N, (int64_t)L.w.size() / (nb * 16));
 }
@@ -192,7 +192,7 @@ int fuse_linears(std::vector<HostLinear> parts, const std::string &name, HostLin
         any_anchor |= !p.a_ptr.empty();
     }
     for (auto &p : parts) {
-        size_t row_bytes = out.fmt == FMT_Q4_0 ? nb * 20 : out.fmt == FMT_LUT4 ? nb * 16 : out.K * 4;
+        size_t row_bytes = out.fmt == FMT_Q4_0 ? nb * 20 : out.fmt == FMT_Q8_0 ? nb * 34 : out.fmt == FMT_LUT4 ? nb * 16 : out.K * 4;
         out.w.insert(out.w.end(), p.w.begin(), p.w.begin() + row_bytes * p.N);
         if (out.fmt == FMT_LUT4) {  // expand to per-row tables (init.rs:109-124)
             const size_t per_row = nb * 16;
@@ -348,6 +348,20 @@ int upload_linear(gaje_hip_model *m, const HostLinear &L, DevLinear &D, bool til
             GAJE_TRY(m->alloc(&D.ew, (size_t)D.rows_valid));
             GAJE_TRY(launch_q4_row_exponents(D.w, D.rows_valid, L.K, D.ew, m->stream));
         }
+    } else if (L.fmt == FMT_Q8_0) {
+        // stage the file's Q8_0Block rows and pack them into 144-byte groups
+        const size_t raw = (size_t)D.rows_valid * nb * 34;
+        const int64_t packed = q8_0_packed_bytes(D.rows_valid, L.K);
+        uint8_t *tmp = nullptr;
+        GAJE_TRY(m->upload(&tmp, L.w.data(), raw));
+        m->weight_bytes -= (int64_t)raw;
+        int rc = m->alloc(&D.w, (size_t)packed);
+        if (rc == GAJE_OK && packed > 0) rc = launch_pack_q8_0(tmp, D.w, D.rows_valid, L.K, m->stream);
+        if (rc == GAJE_OK) rc = hipStreamSynchronize(m->stream) == hipSuccess ? GAJE_OK
+                                                                               : set_error(GAJE_ERR_HIP, "Q8_0 pack failed");
+        m->release(tmp);
+        GAJE_TRY(rc);
+        m->weight_bytes += packed;
     } else if (L.fmt == FMT_F32 && tile_f32 && L.K % 8 == 0 && D.rows_valid > 0) {
         // stage the row-major rows and tile them (32-row tiles, KiB chunks)
         const size_t raw = (size_t)D.rows_valid * L.K * 4;

@@ -166,13 +166,41 @@ void gen_normal(uint64_t seed, const std::string &name, int64_t count, double me
     });
 }
 
+// quantize_q8_0_native's block loop (compute/quantize/python.rs:235-300):
+// scale = max|w| / 127, inv = 1/scale when scale > 1e-7 (else every code 0),
+// q = round(w * inv) half away from zero, clamped to [-128, 127]; the scale
+// stored as f16 rounded to nearest even (half::f16::from_f32).
+void quantize_q8_0(const float *w, int64_t nblocks, uint8_t *out) {
+    parallel_rows(nblocks, [&](int64_t a, int64_t b) {
+        for (int64_t j = a; j < b; ++j) {
+            const float *blk = w + j * 32;
+            uint8_t *o = out + j * 34;
+            float max_abs = 0.0f;
+            for (int k = 0; k < 32; ++k) max_abs = std::fabs(blk[k]) > max_abs ? std::fabs(blk[k]) : max_abs;
+            const float scale = max_abs / 127.0f;
+            const float inv = scale > 1e-7f ? 1.0f / scale : 0.0f;
+            for (int k = 0; k < 32; ++k) {
+                int8_t q = 0;
+                if (scale > 1e-7f) {
+                    float r = std::round(blk[k] * inv);
+                    r = r < -128.0f ? -128.0f : r > 127.0f ? 127.0f : r;
+                    q = (int8_t)r;
+                }
+                o[2 + k] = (uint8_t)q;
+            }
+            const _Float16 hs = (_Float16)scale;
+            memcpy(o, &hs, 2);
+        }
+    });
+}
+
 // One directory entry plus the generator of its bytes.
 struct Blob {
     std::string name;
     uint64_t bit_depth, out_f, in_f;
     uint64_t dna_len, c_len, bias_len;  // bytes
     uint64_t dna_off = 0, c_off = 0, anc_off = 0, bias_off = 0;
-    // generators: 0 normal f32, 1 q4_0, 2 lut4, 3 norm weights
+    // generators: 0 normal f32, 1 q4_0, 2 lut4, 3 norm weights, 4 normal f32 quantised to Q8_0
     int kind;
     std::string stream;  // PRNG stream name of the dna values
     bool has_bias = false;
@@ -249,9 +277,21 @@ extern "C" int gaje_synth_write_flat(const char *path, const gaje_synth_config *
         return b;
     };
 
-    blobs.push_back(dense("token_embd", c.vocab_size, h, "token_embd"));
+    // --quant-embed (export_gaje_flat.py:25-32): token_embd and lm_head as Q8_0 (bit_depth 8)
+    auto embed = [&](const std::string &name, const std::string &stream) {
+        Blob b = dense(name, c.vocab_size, h, stream);
+        if (c.quant_embed) {
+            b.bit_depth = 8;
+            b.kind = 4;
+            b.dna_len = (uint64_t)(c.vocab_size * (h / 32) * 34);
+        }
+        return b;
+    };
+    if (c.quant_embed && h % 32)
+        return set_error(GAJE_ERR_INVALID_ARG, "gaje_synth_write_flat: Q8_0 embeddings need n_embd %% 32 == 0");
+    blobs.push_back(embed("token_embd", "token_embd"));
     blobs.push_back(norm("output_norm"));
-    blobs.push_back(dense("lm_head", c.vocab_size, h, c.tied_embeddings ? "token_embd" : "lm_head"));
+    blobs.push_back(embed("lm_head", c.tied_embeddings ? "token_embd" : "lm_head"));
     for (int64_t i = 0; i < c.n_blocks; ++i) {
         std::string p = "blk." + std::to_string(i) + ".";
         blobs.push_back(norm(p + "attn_norm"));
@@ -388,6 +428,12 @@ extern "C" int gaje_synth_write_flat(const char *path, const gaje_synth_config *
                 lut.resize(b.c_len / 4);
                 gen_lut4(c.seed, b.stream, (int64_t)b.out_f, (int64_t)b.in_f, dna.data(), lut.data());
                 break;
+            case 4: {
+                std::vector<float> w((size_t)(b.out_f * b.in_f));
+                gen_normal(c.seed, b.stream, (int64_t)w.size(), 0.0, 0.02, w.data());
+                quantize_q8_0(w.data(), (int64_t)(w.size() / 32), dna.data());
+                break;
+            }
         }
         put(dna.data(), b.dna_off, b.dna_len);
         if (b.c_len) put(lut.data(), b.c_off, b.c_len);

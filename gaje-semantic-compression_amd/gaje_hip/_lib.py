@@ -85,7 +85,7 @@ class SynthConfig(ctypes.Structure):
                 ("qkv_bias", ctypes.c_int32), ("tied_embeddings", ctypes.c_int32),
                 ("body_format", ctypes.c_int32), ("fused", ctypes.c_int32),
                 ("rope_interleaved", ctypes.c_int32), ("use_genomic_norm", ctypes.c_int32),
-                ("pad_", ctypes.c_int32),
+                ("quant_embed", ctypes.c_int32),
                 ("seed", ctypes.c_uint64)]
 
 
@@ -120,6 +120,10 @@ SIGNATURES = [
     ("gaje_hip_moe_ffn_workspace", c_i64, [c_i64, c_i64, c_i64, c_i64]),
     ("gaje_hip_moe_ffn", ctypes.c_int, [c_vp, c_i64, c_i64, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp,
                                         c_vp, c_i64, c_vp]),
+    ("gaje_hip_q8_0_packed_bytes", c_i64, [c_i64, c_i64]),
+    ("gaje_hip_q8_0_pack", ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, c_vp]),
+    ("gaje_hip_q8_0_gemv", ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_vp]),
+    ("gaje_hip_q8_0_dequant", ctypes.c_int, [c_vp, c_vp, c_i64, c_vp]),
     ("gaje_hip_lut4_gemv", ctypes.c_int, [c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_vp]),
     ("gaje_hip_f32_gemv", ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_vp]),
     ("gaje_hip_q4_0_dequant", ctypes.c_int, [c_vp, c_vp, c_i64, c_vp]),

@@ -137,6 +137,29 @@ def moe_ffn(x: DeviceBuffer, T: int, h: int, router: DeviceBuffer, gate_up, down
                                  workspace.ptr, workspace.nbytes, stream))
 
 
+def q8_0_packed_bytes(n: int, k: int) -> int:
+    return int(lib().gaje_hip_q8_0_packed_bytes(n, k))
+
+
+def q8_0_upload(blocks: np.ndarray, n: int, k: int) -> DeviceBuffer:
+    """Q8_0Block rows (34 bytes per block) -> packed device rows."""
+    raw = DeviceBuffer.from_array(np.ascontiguousarray(blocks, np.uint8))
+    packed = DeviceBuffer(max(q8_0_packed_bytes(n, k), 1))
+    check(lib().gaje_hip_q8_0_pack(raw.ptr, packed.ptr, n, k, None))
+    synchronize()
+    raw.close()
+    return packed
+
+
+def q8_0_gemv(packed: DeviceBuffer, x: DeviceBuffer, y: DeviceBuffer, n: int, k: int,
+              bias: DeviceBuffer | None = None, bias_len: int = 0, stream=None) -> None:
+    check(lib().gaje_hip_q8_0_gemv(packed.ptr, x.ptr, _p(bias), bias_len, y.ptr, n, k, stream))
+
+
+def q8_0_dequant(blocks: DeviceBuffer, out: DeviceBuffer, nblocks: int, stream=None) -> None:
+    check(lib().gaje_hip_q8_0_dequant(blocks.ptr, out.ptr, nblocks, stream))
+
+
 def lut4_gemv(codes: DeviceBuffer, lut: DeviceBuffer, lut_len: int, x: DeviceBuffer,
               y: DeviceBuffer, n: int, k: int, bias: DeviceBuffer | None = None,
               bias_len: int = 0, stream=None) -> None:

@@ -132,6 +132,18 @@ int gaje_hip_moe_ffn(const float *x, int64_t T, int64_t h, const float *router, 
                      const void *const *gate_up, const void *const *down, int64_t ffn, float *y,
                      int32_t *top_idx, float *top_w, void *workspace, int64_t workspace_bytes, void *stream);
 
+/* Q8_0 rows (Q8_0Block {f16 scale; i8 qs[32]}, blocks.rs:36-49; the
+ * --quant-embed format of token_embd / lm_head): packing into 144-byte groups
+ * of four blocks (n * ceil(k/128) * 144 + 4 KiB of tail padding), the matvec
+ * of GenomicLinear::forward_core on GenomicQ8_0 (linear/forward.rs:93-101) with
+ * genomic_dot_product_q8_0_avx2's order (genomic.rs:377-448) and flush, and
+ * dequantize_weight over file-layout blocks, all bit-exact. */
+int64_t gaje_hip_q8_0_packed_bytes(int64_t n, int64_t k);
+int gaje_hip_q8_0_pack(const void *blocks, void *packed, int64_t n, int64_t k, void *stream);
+int gaje_hip_q8_0_gemv(const void *packed, const float *x, const float *bias, int64_t bias_len,
+                       float *y, int64_t n, int64_t k, void *stream);
+int gaje_hip_q8_0_dequant(const void *blocks, float *out, int64_t nblocks, void *stream);
+
 /* LUT-4bit matvec (layout Genomic4Bit, high nibble = even element):
  * genomic_dot_product_4bit (genomic.rs:148-204) over the row slicing of
  * linear/forward.rs:59-83.  lut_len floats as stored in the file: 16 (one
@@ -380,7 +392,7 @@ typedef struct {
     int32_t fused;                 /* 1 = attn_qkv / ffn_gate_up, 0 = split      */
     int32_t rope_interleaved;      /* metadata rope_style "interleaved" (else "split") */
     int32_t use_genomic_norm;      /* metadata config.use_genomic_norm           */
-    int32_t pad_;
+    int32_t quant_embed;           /* 1 = token_embd / lm_head as Q8_0 (bit_depth 8, --quant-embed) */
     uint64_t seed;
 } gaje_synth_config;
 

@@ -29,6 +29,7 @@
 #endif
 
 #define Q4_0_BLOCK_BYTES 20 /* repr(C, packed) {f16 scale, f16 min, u8 qs[16]} */
+#define Q8_0_BLOCK_BYTES 34 /* repr(C, packed) {f16 scale, i8 qs[32]} (blocks.rs:36-41) */
 
 /* The exponential of attention.rs:106 and activation.rs:42-44 (f32::exp ->
  * the C library's expf); overridable only to study sensitivity. */
@@ -138,6 +139,111 @@ float orc_dot_q4_0_avx2(const uint8_t *blocks, const float *input, size_t n_bloc
     __m128 fin = _mm_add_ss(sum, shuf);
     float total = _mm_cvtss_f32(fin);
     return fabsf(total) < 1e-6f ? 0.0f : total;
+}
+
+/* Q8_0Block::dequantize_weight — src/io/header/blocks.rs:43-49: f32(q) * scale. */
+float orc_q8_0_dequant_weight(const uint8_t *block, int idx) {
+    uint16_t hs;
+    memcpy(&hs, block, 2);
+    float q = (float)(int8_t)block[2 + idx];
+    return q * h2f(hs);
+}
+
+void orc_q8_0_dequant(const uint8_t *blocks, size_t nblocks, float *out) {
+    for (size_t b = 0; b < nblocks; b++)
+        for (int k = 0; k < 32; k++)
+            out[b * 32 + k] = orc_q8_0_dequant_weight(blocks + b * Q8_0_BLOCK_BYTES, k);
+}
+
+/* genomic_dot_product_q8_0_avx2 — src/compute/kernels/genomic.rs:377-448:
+ * per block, the 32 signed codes widened to four 8-float vectors (elements
+ * 8c..8c+7), dq = q * scale, acc = fma(dq, x, acc) in c order; the horizontal
+ * sum and the 1e-6 flush of the Q4_0 kernel. */
+float orc_dot_q8_0_avx2(const uint8_t *blocks, const float *input, size_t n_blocks) {
+    __m256 acc = _mm256_setzero_ps();
+    for (size_t j = 0; j < n_blocks; j++) {
+        const uint8_t *blk = blocks + j * Q8_0_BLOCK_BYTES;
+        uint16_t hs;
+        memcpy(&hs, blk, 2);
+        const __m256 v_scale = _mm256_set1_ps(h2f(hs));
+        const __m256i v_qs = _mm256_loadu_si256((const __m256i *)(blk + 2));
+        const __m128i lo_128 = _mm256_castsi256_si128(v_qs);
+        const __m128i hi_128 = _mm256_extracti128_si256(v_qs, 1);
+        const __m128i lo_lo_16 = _mm_cvtepi8_epi16(lo_128);
+        const __m128i lo_hi_16 = _mm_cvtepi8_epi16(_mm_srli_si128(lo_128, 8));
+        const __m256 q_0 = _mm256_cvtepi32_ps(_mm256_cvtepi16_epi32(lo_lo_16));
+        const __m256 q_1 = _mm256_cvtepi32_ps(_mm256_cvtepi16_epi32(lo_hi_16));
+        const __m128i hi_lo_16 = _mm_cvtepi8_epi16(hi_128);
+        const __m128i hi_hi_16 = _mm_cvtepi8_epi16(_mm_srli_si128(hi_128, 8));
+        const __m256 q_2 = _mm256_cvtepi32_ps(_mm256_cvtepi16_epi32(hi_lo_16));
+        const __m256 q_3 = _mm256_cvtepi32_ps(_mm256_cvtepi16_epi32(hi_hi_16));
+        const float *in = input + j * 32;
+        const __m256 x_0 = _mm256_loadu_ps(in), x_1 = _mm256_loadu_ps(in + 8);
+        const __m256 x_2 = _mm256_loadu_ps(in + 16), x_3 = _mm256_loadu_ps(in + 24);
+        acc = _mm256_fmadd_ps(_mm256_mul_ps(q_0, v_scale), x_0, acc);
+        acc = _mm256_fmadd_ps(_mm256_mul_ps(q_1, v_scale), x_1, acc);
+        acc = _mm256_fmadd_ps(_mm256_mul_ps(q_2, v_scale), x_2, acc);
+        acc = _mm256_fmadd_ps(_mm256_mul_ps(q_3, v_scale), x_3, acc);
+    }
+    __m128 vlow = _mm256_castps256_ps128(acc);
+    __m128 vhigh = _mm256_extractf128_ps(acc, 1);
+    __m128 v128 = _mm_add_ps(vlow, vhigh);
+    __m128 hi = _mm_movehl_ps(v128, v128);
+    __m128 sum = _mm_add_ps(v128, hi);
+    __m128 shuf = _mm_shuffle_ps(sum, sum, 1);
+    __m128 fin = _mm_add_ss(sum, shuf);
+    float total = _mm_cvtss_f32(fin);
+    return fabsf(total) < 1e-6f ? 0.0f : total;
+}
+
+/* Scalar fallback of genomic_dot_product_q8_0 — genomic.rs:338-372: per block
+ * sum(q * x) in element order, times the scale.  Not the path an AVX2 host takes;
+ * kept for the factored-form check. */
+float orc_dot_q8_0_scalar(const uint8_t *blocks, const float *input, size_t n_blocks) {
+    float total = 0.0f;
+    for (size_t j = 0; j < n_blocks; j++) {
+        const uint8_t *blk = blocks + j * Q8_0_BLOCK_BYTES;
+        uint16_t hs;
+        memcpy(&hs, blk, 2);
+        float s = 0.0f;
+        for (int k = 0; k < 32; k++) {
+            float p = (float)(int8_t)blk[2 + k] * input[j * 32 + k];
+            s += p;
+        }
+        float t = s * h2f(hs);
+        total += t;
+    }
+    return fabsf(total) < 1e-6f ? 0.0f : total;
+}
+
+/* quantize_q8_0_native's block loop — src/compute/quantize/python.rs:235-300:
+ * scale = max|w| / 127, inv = 1/scale when scale > 1e-7 (else every q = 0),
+ * q = round(w * inv) (half away from zero) clamped to [-128, 127], the scale
+ * stored as f16 (round to nearest even). */
+void orc_q8_0_quantize(const float *w, size_t nblocks, uint8_t *out) {
+    for (size_t b = 0; b < nblocks; b++) {
+        const float *blk = w + b * 32;
+        uint8_t *o = out + b * Q8_0_BLOCK_BYTES;
+        float max_abs = 0.0f;
+        for (int k = 0; k < 32; k++) {
+            float a = fabsf(blk[k]);
+            if (a > max_abs) max_abs = a;
+        }
+        float scale = max_abs / 127.0f;
+        float inv = scale > 1e-7f ? 1.0f / scale : 0.0f;
+        for (int k = 0; k < 32; k++) {
+            int8_t q = 0;
+            if (scale > 1e-7f) {
+                float r = roundf(blk[k] * inv);
+                if (r < -128.0f) r = -128.0f;
+                if (r > 127.0f) r = 127.0f;
+                q = (int8_t)r;
+            }
+            o[2 + k] = (uint8_t)q;
+        }
+        uint16_t hs = orc_f32_to_f16(scale);
+        memcpy(o, &hs, 2);
+    }
 }
 
 /* Scalar fallback of genomic_dot_product_q4_0 — genomic.rs:227-260.  Not the
@@ -367,7 +473,7 @@ void orc_attention(const float *q_rope, const float *k_cache, const float *v_cac
 
 /* A GenomicLinear as the oracle sees it (src/nn/linear/mod.rs:36-57). */
 typedef struct {
-    int kind;              /* 0 = GenomicF32, 1 = GenomicQ4_0, 2 = Genomic4Bit (LUT) */
+    int kind;              /* 0 = GenomicF32, 1 = GenomicQ4_0, 2 = Genomic4Bit (LUT), 3 = GenomicQ8_0 */
     int64_t out_features;
     int64_t in_features;
     const uint8_t *db;     /* weight bytes as stored in the .flat blob */
@@ -405,6 +511,11 @@ static float compute_single_row(const orc_linear *L, int64_t i, const float *inp
         int64_t total_blocks = L->db_len / Q4_0_BLOCK_BYTES;
         if (n_blocks > 0 && row_off + n_blocks <= total_blocks)
             sum = orc_dot_q4_0_avx2(L->db + row_off * Q4_0_BLOCK_BYTES, input, (size_t)n_blocks);
+    } else if (L->kind == 3) {
+        int64_t row_off = i * n_blocks;
+        int64_t total_blocks = L->db_len / Q8_0_BLOCK_BYTES;
+        if (n_blocks > 0 && row_off + n_blocks <= total_blocks)
+            sum = orc_dot_q8_0_avx2(L->db + row_off * Q8_0_BLOCK_BYTES, input, (size_t)n_blocks);
     } else if (L->kind == 2) {
         const int64_t stride = block_size / 2;
         int64_t row_off = i * n_blocks * stride;
@@ -445,7 +556,7 @@ float orc_linear_row(const orc_linear *L, int64_t i, const float *input, int64_t
 }
 
 /* GenomicLinear::get_row_core — src/nn/linear/forward.rs:195-285 for the
- * F32, Q4_0 and LUT-4bit variants (embedding lookup). */
+ * F32, Q4_0, Q8_0 and LUT-4bit variants (embedding lookup). */
 void orc_linear_get_row(const orc_linear *L, int64_t idx, float *res) {
     int64_t K = L->in_features;
     for (int64_t t = 0; t < K; t++) res[t] = 0.0f;
@@ -459,6 +570,10 @@ void orc_linear_get_row(const orc_linear *L, int64_t idx, float *res) {
         int64_t off = safe * n_blocks;
         if (off + n_blocks <= L->db_len / Q4_0_BLOCK_BYTES)
             orc_q4_0_dequant(L->db + off * Q4_0_BLOCK_BYTES, (size_t)n_blocks, res);
+    } else if (L->kind == 3) {
+        int64_t off = safe * n_blocks;
+        if (off + n_blocks <= L->db_len / Q8_0_BLOCK_BYTES)
+            orc_q8_0_dequant(L->db + off * Q8_0_BLOCK_BYTES, (size_t)n_blocks, res);
     } else if (L->kind == 2) {
         int64_t off = safe * n_blocks * 16;
         if (off + n_blocks * 16 <= L->db_len) {

@@ -20,6 +20,9 @@ What pins each part (tests/test_oracle_*.py):
                             closed form over all 16 codes x f16 pairs
   Q4_0 / LUT / f32 dots     fp64 dot with a Higham bound; the scalar factored form;
                             the dequantised-row dot; linear/tests.rs:7-100 KAT
+  Q8_0 dequant / dot        closed form (q * scale exact) over all 256 codes x f16 edge
+                            scales; header/tests.rs:121-165 round-trip KAT through the
+                            restated writer; fp64 dot with a Higham bound; scalar form
   rms_norm                  closed form in fp64; torch CPU RMSNorm
   RoPE                      HF-style rotate_half on the CPU (split) and the
                             interleaved definition of tests/unit/test_rope_logic.py
@@ -49,7 +52,8 @@ _LIB = None
 Q4_0_BLOCK_BYTES = 20
 BLOCK_SIZE = 32  # hard-coded by load_genomic (flat_reader.rs:141)
 
-KIND_F32, KIND_Q4_0, KIND_LUT4 = 0, 1, 2
+KIND_F32, KIND_Q4_0, KIND_LUT4, KIND_Q8_0 = 0, 1, 2, 3
+Q8_0_BLOCK_BYTES = 34
 
 _fp = ctypes.POINTER(ctypes.c_float)
 _u8p = ctypes.POINTER(ctypes.c_uint8)
@@ -86,9 +90,13 @@ def lib():
         L.orc_q4_0_dequant_weight.argtypes = [ctypes.c_void_p, ctypes.c_int]
         L.orc_q4_0_dequant_weight.restype = ctypes.c_float
         L.orc_q4_0_dequant.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
-        for fn in ("orc_dot_q4_0_avx2", "orc_dot_q4_0_scalar"):
+        for fn in ("orc_dot_q4_0_avx2", "orc_dot_q4_0_scalar", "orc_dot_q8_0_avx2", "orc_dot_q8_0_scalar"):
             getattr(L, fn).argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]
             getattr(L, fn).restype = ctypes.c_float
+        L.orc_q8_0_dequant_weight.argtypes = [ctypes.c_void_p, ctypes.c_int]
+        L.orc_q8_0_dequant_weight.restype = ctypes.c_float
+        L.orc_q8_0_dequant.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+        L.orc_q8_0_quantize.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
         L.orc_dot_4bit.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                    ctypes.c_size_t, ctypes.c_size_t]
         L.orc_dot_4bit.restype = ctypes.c_float
@@ -174,6 +182,32 @@ def dot_q4_0(blocks: np.ndarray, x: np.ndarray, scalar: bool = False) -> float:
     return fn(_ptr(b), _ptr(x), b.size // Q4_0_BLOCK_BYTES)
 
 
+def q8_0_dequant(blocks: np.ndarray) -> np.ndarray:
+    """Q8_0Block::dequantize_weight over whole blocks (blocks.rs:43-49)."""
+    b = np.ascontiguousarray(blocks, dtype=np.uint8).reshape(-1)
+    nb = b.size // Q8_0_BLOCK_BYTES
+    out = np.empty(nb * 32, dtype=np.float32)
+    lib().orc_q8_0_dequant(_ptr(b), nb, _ptr(out))
+    return out
+
+
+def dot_q8_0(blocks: np.ndarray, x: np.ndarray, scalar: bool = False) -> float:
+    b = np.ascontiguousarray(blocks, dtype=np.uint8).reshape(-1)
+    x = _f32(x)
+    fn = lib().orc_dot_q8_0_scalar if scalar else lib().orc_dot_q8_0_avx2
+    return fn(_ptr(b), _ptr(x), b.size // Q8_0_BLOCK_BYTES)
+
+
+def q8_0_quantize(w: np.ndarray) -> np.ndarray:
+    """quantize_q8_0_native's blocks (compute/quantize/python.rs:235-300) as bytes."""
+    w = _f32(w).reshape(-1)
+    if w.size % 32:
+        raise ValueError("Weights length must be divisible by 32")
+    out = np.zeros(w.size // 32 * Q8_0_BLOCK_BYTES, dtype=np.uint8)
+    lib().orc_q8_0_quantize(_ptr(w), w.size // 32, _ptr(out))
+    return out
+
+
 def dot_4bit(codes: np.ndarray, x: np.ndarray, centroids: np.ndarray) -> float:
     """genomic_dot_product_4bit over one row: centroids are per block ([n_blocks][16]);
     a single 16-entry table is shared by every block, as init.rs:109-124 expands it."""
@@ -222,7 +256,7 @@ def rope(vec: np.ndarray, heads: int, head_dim: int, rope_base: float, pos: int,
 # ----------------------------------------------------------------- modules ---
 
 class GenomicLinear:
-    """GenomicLinear restricted to the flat-file formats (F32, Q4_0, LUT-4bit)."""
+    """GenomicLinear restricted to the flat-file formats (F32, Q4_0, Q8_0, LUT-4bit)."""
 
     def __init__(self, database, anchors_u8, centroids, out_features, in_features, bias,
                  bit_depth):
@@ -236,6 +270,8 @@ class GenomicLinear:
             self.kind = KIND_Q4_0 if centroids.size == 0 else KIND_LUT4
         elif bit_depth == 32:
             self.kind = KIND_F32
+        elif bit_depth == 8:
+            self.kind = KIND_Q8_0
         else:
             raise NotImplementedError(f"bit_depth {bit_depth} is outside the restated path")
         # LUT expansion (init.rs:109-124)
