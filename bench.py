@@ -49,12 +49,12 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def model_path(preset: str, seed: int, d: str) -> str:
+def model_path(preset: str, seed: int, d: str, quant_embed: int = 0) -> str:
     from gaje_hip import synth
-    path = os.path.join(d, f"gaje_{preset}_s{seed}.flat")
+    path = os.path.join(d, f"gaje_{preset}_s{seed}{'_q8embed' if quant_embed else ''}.flat")
     if not os.path.exists(path):
         t = time.perf_counter()
-        synth.write_flat(path + ".tmp", preset=preset, seed=seed)
+        synth.write_flat(path + ".tmp", preset=preset, seed=seed, quant_embed=quant_embed)
         os.replace(path + ".tmp", path)
         log(f"[bench] wrote {path} ({os.path.getsize(path) / 1e9:.2f} GB) in {time.perf_counter() - t:.1f}s")
     return path
@@ -172,6 +172,42 @@ def c3_workloads(d: str, seed: int, prefill_tokens: int = 512, batch: int = 16, 
     return prefill, decode, [int(v) for v in out[0, :4]]
 
 
+def q8_decode_workload(d: str, seed: int, preset: str, prompt_len: int, gen: int, steps: int):
+    """Batch-1 greedy decode of the same shape with Q8_0 token_embd / lm_head (the --quant-embed
+    export): the lm_head matvec reads 34 B per 32 weights instead of 128."""
+    import gaje_hip
+    from gaje_hip import ops
+    path = model_path(preset, seed, d, quant_embed=1)
+    g = gaje_hip.load_genomic_auto(path)
+    g.set_k_wta_ratio(0.0)
+    prompt = np.random.default_rng(seed).integers(0, g.vocab_size, prompt_len).astype(np.uint32)
+    g.reserve(prompt_len + gen + 1)
+    g.clear_cache_py()
+    g.prefill(prompt)
+
+    def step():
+        g.truncate_cache(prompt_len)
+        return g.decode_greedy(int(prompt[-1]), gen)
+
+    step()
+    ops.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    ops.synchronize()
+    el = time.perf_counter() - t0
+    g.truncate_cache(prompt_len + gen - 1)
+    ms, nbytes = g.time_stage("lm_head", iters=200)
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    g.close()
+    out = dict(tok_s=round(gen * steps / el, 2), ms_per_token=round(el / (gen * steps) * 1e3, 4),
+               prompt=prompt_len, gen=gen, steps=steps,
+               lm_head=dict(kernel="gemv_kernel<Q8_0, ARGMAX>", us=round(ms * 1e3, 3), bytes=int(nbytes),
+                            GBps=round(gbps, 1), frac=round(gbps / HBM_PEAK_GBPS, 4)))
+    log(f"[bench] Q8_0 embed/lm_head decode: {out['tok_s']:.1f} tok/s; lm_head {ms * 1e3:.2f} us = {gbps:.0f} GB/s")
+    return out
+
+
 def moe_workload(seed: int, T: int = 256, h: int = 1536, ffn: int = 4096, E: int = 8, iters: int = 50):
     from gaje_hip import ops, synth
     x = synth.normal(seed + 51, "moe.x", T * h).reshape(T, h)
@@ -218,6 +254,7 @@ def main():
     ap.add_argument("--no-decode", action="store_true",
                     help="skip the Qwen2-0.5B decode, its stages and the C0 matvec (profiling runs of the other workloads)")
     ap.add_argument("--no-moe", action="store_true", help="skip the MoE layer")
+    ap.add_argument("--no-q8", action="store_true", help="skip the Q8_0 token_embd/lm_head decode")
     ap.add_argument("--gemv-only", action="store_true",
                     help="only the C0 Q4_0 matvec (cold) and a 256 MiB device copy, for counter runs")
     args = ap.parse_args()
@@ -304,6 +341,9 @@ def main():
 
         g.close()
     workloads = {}
+    if not args.no_q8 and not args.no_decode:
+        workloads[f"{args.preset}_q8_0_embed_decode"] = q8_decode_workload(d, args.seed, args.preset, args.prompt,
+                                                                          args.gen, args.steps)
     if not args.no_c3:
         prefill, decode, c3_tokens = c3_workloads(d, args.seed, ctx=args.c3_ctx, gen=args.c3_gen)
         workloads["qwen2.5-1.5b_prefill_512"] = prefill

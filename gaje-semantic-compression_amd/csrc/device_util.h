@@ -131,12 +131,15 @@ __device__ __forceinline__ float embed_value(const EmbedParams &p, int64_t row, 
             const int64_t b = k / 32;
             const int i = (int)(k % 32);
             if (p.fmt == FMT_Q8_0) {
-                // packed rows (launch_pack_q8_0): dequantize_weight, q * scale (blocks.rs:43-49)
+                // packed rows (launch_pack_q8_0: tiles of 8 rows, per group of
+                // four blocks the rows' 128 code bytes, then their 8 scale bytes):
+                // dequantize_weight, q * scale (blocks.rs:43-49)
                 const int64_t G = (nb + 3) / 4;
-                const uint8_t *grp = p.w + (row * G + b / 4) * 144;
-                const int bb = (int)(b & 3), l = i & 7, c = i >> 3;
-                const float q = (float)(int32_t)(int8_t)grp[16 * l + 4 * bb + c];
-                const uint16_t sh = (uint16_t)grp[128 + 2 * bb] | ((uint16_t)grp[129 + 2 * bb] << 8);
+                const uint8_t *tile = p.w + (row >> 3) * G * 1088;
+                const int k = (int)(row & 7), bb = (int)(b & 3), l = i & 7, c = i >> 3;
+                const float q = (float)(int32_t)(int8_t)tile[(b / 4) * 1024 + 128 * k + 16 * l + 4 * bb + c];
+                const uint8_t *sp = tile + G * 1024 + (b / 4) * 64 + 8 * k + 2 * bb;
+                const uint16_t sh = (uint16_t)sp[0] | ((uint16_t)sp[1] << 8);
                 v = __fmul_rn(q, half_bits(sh));
             } else if (p.fmt == FMT_Q4_0) {
                 // packed rows (launch_pack_q4_0): element i of block b is

@@ -248,18 +248,43 @@ __device__ __forceinline__ void q4_zero_x_pad(const XView &xv, int nb) {
 
 // ---------------------------------------------------------------- Q8_0 ----
 // Packed Q8_0 rows (genomic_dot_product_q8_0_avx2, genomic.rs:377-448, has
-// the Q4_0 kernel's chain structure: lane l owns element 8c+l of every block).
-// Per group of four Q8_0Blocks (128 weights): chain l's 16 bytes at
-// [16l, 16l+16), dword b = block 4g+b, byte c = element 8c+l (signed); the four
-// f16 scales at [128, 136); 8 zero bytes.  144 bytes per group (the file's
-// 136 plus alignment for the 16-byte chain loads).
-constexpr int Q8_GROUP = 144;
+// the Q4_0 kernel's chain structure: lane l owns element 8c+l of every block),
+// in tiles of 8 rows, so that the 8 rows a wave walks together are read with
+// contiguous, aligned loads.  A tile of G groups (four Q8_0Blocks, 128
+// weights, each) holds, for group g:
+//   codes   [1024 g, 1024 g + 1024): row k's 128 bytes at 128 k, chain l's 16
+//           at 16 l within them: dword b = block 4g+b, byte c = element 8c+l
+//           (signed)
+//   scales  [1024 G + 64 g, + 64): row k's four f16 scales at 8 k
+// 1088 bytes per group and tile: the file's 136 per group and row.  Rows past
+// N in the last tile and blocks past nb are zero.
+constexpr int Q8_CODES = 1024;                     // bytes of one group's codes in a tile
+constexpr int Q8_SCALES = 64;                      // bytes of one group's scales in a tile
+constexpr int Q8_TILE_GROUP = Q8_CODES + Q8_SCALES;
 
 template <int D>
 struct Q8Ring {
     vu4 n[D];
     vu2 s[D];
 };
+
+// A row's group-0 codes (chain 0) and scales; group indices past the row's
+// last group read the last group (loaded, never used), so every read stays in
+// the row's tile.  G is the tensor's groups per row.
+struct Q8Row {
+    const uint8_t *c, *s;
+    int last;
+};
+__device__ __forceinline__ Q8Row q8_row(const uint8_t *w, int64_t row, int G) {
+    const uint8_t *t = w + (size_t)(row >> 3) * G * Q8_TILE_GROUP;
+    return Q8Row{t + (row & 7) * 128, t + (size_t)G * Q8_CODES + (row & 7) * 8, G - 1};
+}
+template <bool NT>
+__device__ __forceinline__ void q8_load(const Q8Row &q, int g, int l, vu4 &n, vu2 &sc) {
+    const int gi = g < q.last ? g : q.last;
+    n = ld_u4<NT>(q.c + (size_t)gi * Q8_CODES + 16 * l);
+    sc = ld_u2<NT>(q.s + (size_t)gi * Q8_SCALES);
+}
 
 // dq = f32(q) * scale (genomic.rs:425-428): an exact product
 __device__ __forceinline__ void q8_dequant(float (&d)[4], uint32_t codes, float scale) {
@@ -280,32 +305,34 @@ __device__ __forceinline__ float q8_group(float acc, const vu4 n, const vu2 s, c
     return acc;
 }
 
-// The row's last groups, as q4_tail: the scales of blocks that do not exist
-// become +0 (their values dequantise to +-0 against zero activations).
+// Group i's scales with those of blocks past the row's end (b = blocks left
+// from the group's first block) set to +0: their values dequantise to +-0
+// against zero activations.
+__device__ __forceinline__ vu2 q8_mask_scales(vu2 s, int b) {
+    s.x = (b > 0 ? s.x & 0xFFFFu : 0u) | (b > 1 ? s.x & 0xFFFF0000u : 0u);
+    s.y = (b > 2 ? s.y & 0xFFFFu : 0u) | (b > 3 ? s.y & 0xFFFF0000u : 0u);
+    return s;
+}
+
+// The row's last groups, as q4_tail.
 template <int T, int D>
 __device__ __forceinline__ float q8_tail(float acc, const Q8Ring<D> &r, const float *xg, X4 xc, int left) {
 #pragma unroll
     for (int i = 0; i < T; ++i) {
         const X4 xn = read_x4(xg + 16 * (i + 1));
-        const int b = left - 4 * i;
-        vu2 s = r.s[i];
-        s.x = (b > 0 ? s.x & 0xFFFFu : 0u) | (b > 1 ? s.x & 0xFFFF0000u : 0u);
-        s.y = (b > 2 ? s.y & 0xFFFFu : 0u) | (b > 3 ? s.y & 0xFFFF0000u : 0u);
-        acc = q8_group(acc, r.n[i], s, xc);
+        acc = q8_group(acc, r.n[i], q8_mask_scales(r.s[i], left - 4 * i), xc);
         xc = xn;
     }
     return acc;
 }
 
+// The ring's D slots <- groups 0..D-1 of the row.  Gw: the groups per row of
+// the tensor at w (1 for the zero stand-in of a tensor with no stored row).
 template <bool NT, int D>
-__device__ __forceinline__ void q8_prefetch(const uint8_t *w, const GemvParams &p, int64_t row, int l, Q8Ring<D> &r) {
-    const int G = (p.nb + 3) >> 2;
-    const uint8_t *rp = w + (size_t)row * G * Q8_GROUP;
+__device__ __forceinline__ void q8_prefetch(const uint8_t *w, int Gw, int64_t row, int l, Q8Ring<D> &r) {
+    const Q8Row q = q8_row(w, row, Gw);
 #pragma unroll
-    for (int i = 0; i < D; ++i) {
-        r.n[i] = ld_u4<NT>(rp + i * Q8_GROUP + 16 * l);
-        r.s[i] = ld_u2<NT>(rp + i * Q8_GROUP + 128);
-    }
+    for (int i = 0; i < D; ++i) q8_load<NT>(q, i, l, r.n[i], r.s[i]);
 }
 
 // q4_consume for packed Q8_0 rows: the same walk, ring and reduction.
@@ -315,7 +342,7 @@ __device__ __forceinline__ float q8_consume(const GemvParams &p, const XView &xv
     const int nb = p.nb;
     const int G = (nb + 3) >> 2;
     const int Gf = nb >> 2;
-    const uint8_t *gp = p.w + (size_t)row * G * Q8_GROUP + D * Q8_GROUP;  // next group to load
+    const Q8Row q = q8_row(p.w, row, G);
     const float *xg = xv.x + l * xv.stride;
     float acc = 0.0f;
     X4 xc = read_x4(xg);
@@ -325,11 +352,9 @@ __device__ __forceinline__ float q8_consume(const GemvParams &p, const XView &xv
         for (int i = 0; i < D; ++i) {
             const X4 xn = read_x4(xg + 16 * (i + 1));
             acc = q8_group(acc, r.n[i], r.s[i], xc);
-            r.n[i] = ld_u4<NT>(gp + i * Q8_GROUP + 16 * l);
-            r.s[i] = ld_u2<NT>(gp + i * Q8_GROUP + 128);
+            q8_load<NT>(q, g + D + i, l, r.n[i], r.s[i]);
             xc = xn;
         }
-        gp += D * Q8_GROUP;
         xg += 16 * D;
     }
     const int rem = G - g;
@@ -342,36 +367,39 @@ __device__ __forceinline__ float q8_consume(const GemvParams &p, const XView &xv
     return flush_small(total);
 }
 
-// Q8_0Block rows (file layout, 34 bytes per block) -> the packed layout; one
-// thread per (row, group); blocks past nb are zero.
+// Q8_0Block rows (file layout, 34 bytes per block) -> the tiled layout; one
+// thread per (tile, group, row of the tile).
 __global__ void pack_q8_0_kernel(const uint8_t *src, uint8_t *dst, int64_t N, int nb) {
     const int G = (nb + 3) >> 2;
-    const int64_t total = N * G;
+    const int64_t tiles = (N + 7) >> 3, total = tiles * G * 8;
     for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t row = t / G;
-        const int g = (int)(t - row * G);
-        const uint8_t *rs = src + (size_t)row * nb * 34;
-        uint32_t *out = (uint32_t *)(dst + ((size_t)row * G + g) * Q8_GROUP);
+        const int k = (int)(t & 7);
+        const int64_t tg = t >> 3, tile = tg / G;
+        const int g = (int)(tg - tile * G);
+        const int64_t row = tile * 8 + k;
+        uint8_t *tb = dst + (size_t)tile * G * Q8_TILE_GROUP;
+        uint32_t *codes = (uint32_t *)(tb + (size_t)g * Q8_CODES + 128 * k);
+        uint32_t *scales = (uint32_t *)(tb + (size_t)G * Q8_CODES + (size_t)g * Q8_SCALES + 8 * k);
+        const uint8_t *rs = src + (size_t)(row < N ? row : 0) * nb * 34;
         for (int l = 0; l < 8; ++l)
             for (int b = 0; b < 4; ++b) {
                 const int j = 4 * g + b;
                 uint32_t word = 0;
-                if (j < nb)
+                if (row < N && j < nb)
                     for (int c = 0; c < 4; ++c) word |= (uint32_t)rs[(size_t)j * 34 + 2 + 8 * c + l] << (8 * c);
-                out[4 * l + b] = word;
+                codes[4 * l + b] = word;
             }
         for (int h = 0; h < 2; ++h) {
             uint32_t w2 = 0;
             for (int half = 0; half < 2; ++half) {
                 const int j = 4 * g + 2 * h + half;
-                if (j < nb) w2 |= ((uint32_t)rs[(size_t)j * 34] | ((uint32_t)rs[(size_t)j * 34 + 1] << 8)) << (16 * half);
+                if (row < N && j < nb)
+                    w2 |= ((uint32_t)rs[(size_t)j * 34] | ((uint32_t)rs[(size_t)j * 34 + 1] << 8)) << (16 * half);
             }
-            out[32 + h] = w2;
+            scales[h] = w2;
         }
-        out[34] = 0;
-        out[35] = 0;
     }
-    uint32_t *pad = (uint32_t *)(dst + (size_t)total * Q8_GROUP);
+    uint32_t *pad = (uint32_t *)(dst + (size_t)tiles * G * Q8_TILE_GROUP);
     for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < Q8_TAIL_PAD / 4; t += (int64_t)gridDim.x * blockDim.x)
         pad[t] = 0;
 }
@@ -714,7 +742,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
             const uint8_t *wbase = p.rows_valid > 0 ? p.w : kZeroRows;
             const int64_t prow = q.row_ok ? q.row : 0;
             if constexpr (FMT == FMT_Q4_0) q4_prefetch<NT, D>(wbase, p, prow, s, q4r);
-            else if constexpr (FMT == FMT_Q8_0) q8_prefetch<NT, D>(wbase, p, prow, s, q8r);
+            else if constexpr (FMT == FMT_Q8_0) q8_prefetch<NT, D>(wbase, p.rows_valid > 0 ? (p.nb + 3) >> 2 : 1, prow, s, q8r);
             else f32_prefetch<NT>(wbase, p, prow, s, f32r);
         }
         if (halted) return;  // uniform; checked once the first loads are in flight
@@ -822,7 +850,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
             q = locate<FMT>(p, mode, pr, npairs, half);
             if (q.row_ok) {
                 if constexpr (FMT == FMT_Q4_0) q4_prefetch<NT, D>(p.w, p, q.row, s, q4r);
-                else if constexpr (FMT == FMT_Q8_0) q8_prefetch<NT, D>(p.w, p, q.row, s, q8r);
+                else if constexpr (FMT == FMT_Q8_0) q8_prefetch<NT, D>(p.w, (p.nb + 3) >> 2, q.row, s, q8r);
                 else if constexpr (FMT == FMT_F32) f32_prefetch<NT>(p.w, p, q.row, s, f32r);
             }
         }
@@ -899,6 +927,156 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
         }
     }
     if (mode == MODE_ARGMAX && st) {
+        unsigned long long key =
+            best_v > -INFINITY
+                ? ((unsigned long long)order_key(best_v) << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)best_i)
+                : 0ull;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const unsigned long long other = __shfl_xor(key, o, WAVE);
+            key = other > key ? other : key;
+        }
+        if (lane == 0 && key) atomicMax(&st->argmax_key, key);
+    }
+}
+
+// ------------------------------------------ Q8_0, streamed long matrices ----
+// The Q8_0 lm_head (N = vocabulary, K = n_embd <= 1024): a resident grid, 8
+// lanes per row (lane l runs chain l of q8_consume), row group rg walking rows
+// rg, rg + R, rg + 2R, ... (R row groups in the grid, so a wave covers 8
+// adjacent rows, one contiguous run of packed groups).  Two register rings
+// alternate: the next row's groups are loaded before the current row is
+// computed, so every wave keeps a row's weights in flight under its
+// arithmetic.  Values, chain order and reduction are those of q8_consume, so
+// the result is the same bit for bit.
+constexpr int Q8S_D = 8;  // ring slots: rows of at most 8 packed groups (K <= 1024)
+__device__ float kSinkOut[WAVE];  // stores of rows past N (never read)
+
+// All Q8S_D slots are loaded and walked with no branch (the wait counts then
+// stay exact, so the other ring's loads remain in flight): slots past the
+// row's G groups reload its last group and enter with +0 scales against zero
+// activations.
+template <bool NT>
+__device__ __forceinline__ void q8s_load(const Q8Row &q, int l, Q8Ring<Q8S_D> &r) {
+#pragma unroll
+    for (int i = 0; i < Q8S_D; ++i) q8_load<NT>(q, i, l, r.n[i], r.s[i]);
+}
+
+// Chain l's sum over one row: the groups in order, the scales of blocks past
+// nb set to +0 (as q8_tail).  A slot past the row adds fma(+-0, +0, acc),
+// which leaves acc unchanged except that -0 may become +0; the row total is
+// flushed to +0 when it is that small, so the result is unchanged.
+__device__ __forceinline__ float q8s_row(const float *xg, int nb, const Q8Ring<Q8S_D> &r) {
+    float acc = 0.0f;
+    X4 xc = read_x4(xg);
+#pragma unroll
+    for (int i = 0; i < Q8S_D; ++i) {
+        const X4 xn = read_x4(xg + 16 * (i + 1));
+        acc = q8_group(acc, r.n[i], q8_mask_scales(r.s[i], nb - 4 * i), xc);
+        xc = xn;
+    }
+    return acc;
+}
+
+template <bool NT, int MODE>
+__global__ __launch_bounds__(THREADS) void gemv_q8_stream_kernel(GemvParams p, int xstride) {
+    extern __shared__ __align__(16) float smem[];
+    __shared__ float inv_slot;
+    __shared__ int or_in[THREADS / WAVE], or_norm[THREADS / WAVE];
+    DevState *st = p.st;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int l = lane & 7, base = lane - l;
+    const int64_t K4 = p.K >> 2, N = p.N;
+    const int nb = p.nb, G = (nb + 3) >> 2;
+    const XView xv{smem, xstride};
+    const int64_t R = (int64_t)gridDim.x * (THREADS / 8);
+    int64_t row = (int64_t)blockIdx.x * (THREADS / 8) + (tid >> 3);
+    const uint8_t *wb = p.rows_valid > 0 ? p.w : kZeroRows;
+    const int Gw = p.rows_valid > 0 ? G : 1;
+    // rows past the stored ones (and past N) read row 0: loaded, never used
+    auto rowp = [&](int64_t r) { return q8_row(wb, r < p.rows_valid ? r : 0, Gw); };
+
+    // ---- prologue: the activation quad of this thread, the first row's
+    // weights, then the chain-major copy (normalised if requested) ----
+    const bool mine = tid < K4;
+    const float4 *x4 = (const float4 *)p.x;
+    const float4 *w4 = (const float4 *)p.norm_w;
+    const float4 xr = x4[mine ? tid : K4 - 1];
+    const float4 wr = w4 ? w4[mine ? tid : K4 - 1] : make_float4(0.f, 0.f, 0.f, 0.f);
+    __builtin_amdgcn_sched_barrier(0);
+    Q8Ring<Q8S_D> ra, rb;
+    q8s_load<NT>(rowp(row), l, ra);
+    if (st && st->halted) return;  // uniform
+    int bad_in = 0;
+    if (mine) {
+        const float q[4] = {xr.x, xr.y, xr.z, xr.w};
+        store_quad<true>(xv, tid, q);
+        bad_in = isnan(xr.x) || isnan(xr.y) || isnan(xr.z) || isnan(xr.w);
+    }
+    q4_zero_x_pad(xv, nb);
+    if (barrier_or<THREADS / WAVE>(bad_in, or_in) && p.st_in >= 0 && tid == 0) nan_flag(st, p.layer, p.st_in);
+    if (p.norm_w) {
+        rms_inv_chain_major(xv, p.K, p.eps, &inv_slot);
+        lds_barrier();
+        const float inv = inv_slot;
+        int bad = 0;
+        if (mine) {
+            float t[4] = {xr.x * inv, xr.y * inv, xr.z * inv, xr.w * inv};
+            const float w[4] = {wr.x, wr.y, wr.z, wr.w};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                t[c] = t[c] * w[c];  // (x * inv) * w, each product rounded
+                bad |= isnan(t[c]);
+            }
+            store_quad<true>(xv, tid, t);
+        }
+        if (barrier_or<THREADS / WAVE>(bad, or_norm) && p.st_norm >= 0 && tid == 0) nan_flag(st, p.layer, p.st_norm);
+    }
+    if (p.x_out && blockIdx.x == 0)
+        for (int64_t k = tid; k < p.K; k += THREADS) p.x_out[k] = xv.at(k);
+
+    // ---- rows, two per iteration: ring A holds `row`, ring B row + R; each
+    // ring is reloaded as soon as it has been walked.  The loop body has no
+    // branch: a second row at or past N walks a clamped row and stores into a
+    // sink, and the bias is read from a zero row where there is none, so the
+    // compiler's wait counts stay exact and a ring's loads stay in flight
+    // while the other ring is walked. ----
+    const float *xg = xv.x + l * xv.stride;
+    float best_v = -INFINITY;
+    int64_t best_i = 0;
+    auto bias_at = [&](int64_t r) {
+        return *(r < p.bias_len ? p.bias + r : (const float *)kZeroRows);
+    };
+    auto finish = [&](int64_t r, float acc, float bias) {
+        const float u = acc + shfl(acc, base + ((l + 4) & 7));
+        const float v = u + shfl(u, base + ((l + 2) & 7));
+        float y = shfl(flush_small(v + shfl(v, base + ((l + 1) & 7))), base);  // lane 0's order
+        y = r < p.rows_valid ? y : 0.0f;
+        y = r < p.bias_len ? y + bias : y;  // finish_row without anchors
+        *(r < N ? p.y + r : kSinkOut + lane) = y;  // the row group's lanes store the same value
+        if constexpr (MODE == MODE_ARGMAX) {
+            const bool better = r < N && y > best_v;
+            best_v = better ? y : best_v;
+            best_i = better ? r : best_i;
+        }
+    };
+    auto clamp = [&](int64_t r) { return r < N ? r : row; };
+    q8s_load<NT>(rowp(clamp(row + R)), l, rb);
+    __builtin_amdgcn_sched_barrier(0);
+    while (row < N) {
+        const int64_t r1 = row + R;
+        const float b0 = bias_at(row), b1 = bias_at(r1);
+        const float a0 = q8s_row(xg, nb, ra);
+        q8s_load<NT>(rowp(clamp(row + 2 * R)), l, ra);
+        __builtin_amdgcn_sched_barrier(0);
+        const float a1 = q8s_row(xg, nb, rb);
+        q8s_load<NT>(rowp(clamp(row + 3 * R)), l, rb);
+        __builtin_amdgcn_sched_barrier(0);
+        finish(row, a0, b0);
+        finish(r1, a1, b1);
+        row += 2 * R;
+    }
+    if constexpr (MODE == MODE_ARGMAX) {
         unsigned long long key =
             best_v > -INFINITY
                 ? ((unsigned long long)order_key(best_v) << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)best_i)
@@ -1166,13 +1344,13 @@ int q4_xstride(int64_t K) { return q4_xrow((int)(K / 32)) + 4; }
 }  // namespace
 
 int64_t q4_0_packed_bytes(int64_t N, int64_t K) { return N * ((K / 32 + 3) / 4) * 80 + Q4_TAIL_PAD; }
-int64_t q8_0_packed_bytes(int64_t N, int64_t K) { return N * ((K / 32 + 3) / 4) * Q8_GROUP + Q8_TAIL_PAD; }
+int64_t q8_0_packed_bytes(int64_t N, int64_t K) { return (N + 7) / 8 * ((K / 32 + 3) / 4) * Q8_TILE_GROUP + Q8_TAIL_PAD; }
 
 int launch_pack_q8_0(const uint8_t *src, uint8_t *dst, int64_t N, int64_t K, hipStream_t s) {
     if (N < 0 || K <= 0 || K % 32 != 0 || (N > 0 && (!src || !dst)))
         return set_error(GAJE_ERR_INVALID_ARG, "pack_q8_0: bad arguments");
     const int64_t G = (K / 32 + 3) / 4;
-    int64_t grid = (N * G + 255) / 256;
+    int64_t grid = ((N + 7) / 8 * G * 8 + 255) / 256;
     if (grid < 1) grid = 1;
     if (grid > 65535) grid = 65535;
     hipLaunchKernelGGL(pack_q8_0_kernel, dim3((unsigned)grid), dim3(256), 0, s, src, dst, N, (int)(K / 32));
@@ -1291,6 +1469,21 @@ int launch_gemv(const GemvParams &p, hipStream_t s) {
             return GAJE_OK;
         }
     }
+    // Q8_0 rows of at most 8 packed groups (the lm_head): the streamed kernel
+    if (p.fmt == FMT_Q8_0 && (p.mode == MODE_ARGMAX || p.mode == MODE_STORE) && !p.gnorm && !p.a_ptr && p.nb > 0 &&
+        (p.nb + 3) / 4 <= Q8S_D) {
+        void (*sf)(GemvParams, int);
+        if (p.mode == MODE_ARGMAX) sf = p.nontemporal ? gemv_q8_stream_kernel<true, MODE_ARGMAX> : gemv_q8_stream_kernel<false, MODE_ARGMAX>;
+        else sf = p.nontemporal ? gemv_q8_stream_kernel<true, MODE_STORE> : gemv_q8_stream_kernel<false, MODE_STORE>;
+        int per_cu = 0;
+        GAJE_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, sf, THREADS, lds));
+        int64_t grid = (p.N + THREADS / 8 - 1) / (THREADS / 8);
+        const int64_t resident = (int64_t)(per_cu > 0 ? per_cu : 1) * device_cu_count();
+        if (grid > resident) grid = resident;
+        hipLaunchKernelGGL(sf, dim3((unsigned)grid), dim3(THREADS), lds, s, p, q4_xstride(p.K));
+        GAJE_HIP_CHECK(hipGetLastError());
+        return GAJE_OK;
+    }
     KernelFn fn;
     int lpr;
     if (p.fmt == FMT_Q4_0) {
@@ -1309,6 +1502,8 @@ int launch_gemv(const GemvParams &p, hipStream_t s) {
         if (long_rows)
             fn = p.nontemporal ? gemv_kernel<FMT_Q8_0, 8, true, 2 * Q4_PREFETCH>
                                : gemv_kernel<FMT_Q8_0, 8, false, 2 * Q4_PREFETCH>;
+        else if (p.mode == MODE_ARGMAX && p.nontemporal)
+            fn = gemv_kernel<FMT_Q8_0, 8, true, Q4_PREFETCH, MODE_ARGMAX>;
         else
             fn = p.nontemporal ? gemv_kernel<FMT_Q8_0, 8, true, Q4_PREFETCH> : gemv_kernel<FMT_Q8_0, 8, false, Q4_PREFETCH>;
     } else if (p.fmt == FMT_LUT4) {
@@ -1325,6 +1520,15 @@ int launch_gemv(const GemvParams &p, hipStream_t s) {
     // tiled f32 rows stream at the best rate with one workgroup per compute
     // unit walking its share of the tiles (measured on a 151936 x 896 matrix)
     if (p.fmt == FMT_F32 && p.f32_tiled && grid > device_cu_count()) grid = device_cu_count();
+    // long Q8_0 matrices (the lm_head): one wave of resident workgroups walks
+    // the row pairs, so the activation prologue runs once per workgroup and
+    // each lane's next row streams in while it finishes the current one
+    if (p.fmt == FMT_Q8_0) {
+        int per_cu = 0;
+        GAJE_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, THREADS, lds));
+        const int64_t resident = (int64_t)(per_cu > 0 ? per_cu : 1) * device_cu_count();
+        if (grid > resident) grid = resident;
+    }
     const int xstride = (p.fmt == FMT_Q4_0 || p.fmt == FMT_Q8_0) ? q4_xstride(p.K) : 0;
     const int nw_off = (int)gemv_x_floats(p.K, p.fmt);
     hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(THREADS), lds, s, p, npairs, xstride, nw_off);

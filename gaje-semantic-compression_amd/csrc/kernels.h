@@ -102,9 +102,9 @@ int launch_gemv(const GemvParams &p, hipStream_t s);
 constexpr int64_t Q4_TAIL_PAD = 2048;
 int launch_pack_q4_0(const uint8_t *src, uint8_t *dst, int64_t N, int64_t K, hipStream_t s);
 int64_t q4_0_packed_bytes(int64_t N, int64_t K);
-// Q8_0Block rows (K % 32 == 0) -> 144-byte groups of four blocks (chain l's
-// codes at [16l, 16l+16), the four f16 scales at [128, 136)), followed by
-// Q8_TAIL_PAD bytes the matvec's prefetch may read.
+// Q8_0Block rows (K % 32 == 0) -> tiles of 8 rows: per group of four blocks,
+// the 8 rows' codes (128 bytes each, chain l's at [16l, 16l+16)) and then
+// their four f16 scales (8 bytes each); Q8_TAIL_PAD zero bytes follow.
 constexpr int64_t Q8_TAIL_PAD = 4096;
 int launch_pack_q8_0(const uint8_t *src, uint8_t *dst, int64_t N, int64_t K, hipStream_t s);
 int64_t q8_0_packed_bytes(int64_t N, int64_t K);

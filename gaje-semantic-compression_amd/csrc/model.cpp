@@ -1681,7 +1681,10 @@ extern "C" int gaje_hip_time_stage(gaje_hip_model *m, int stage, int64_t layer, 
     const size_t layer_kv = (size_t)m->n_kv * m->cap * m->hd;
     auto wbytes = [](const DevLinear &D) -> int64_t {
         const int64_t nb = D.K / 32;
-        int64_t b = D.fmt == FMT_Q4_0 ? D.N * nb * 20 : D.fmt == FMT_LUT4 ? D.N * nb * 16 : D.N * D.K * 4;
+        int64_t b = D.fmt == FMT_Q4_0   ? D.N * nb * 20
+                    : D.fmt == FMT_Q8_0 ? D.N * nb * 34
+                    : D.fmt == FMT_LUT4 ? D.N * nb * 16
+                                        : D.N * D.K * 4;
         if (D.fmt == FMT_LUT4 && D.lut) b += (D.lut_block_stride ? (D.lut_rows_own ? D.N : 1) * nb * 16 * 4 : 64);
         return b;
     };

@@ -40,7 +40,7 @@ enum {
     GAJE_ERR_NOT_FOUND = -6,     /* io::ErrorKind::NotFound: missing tensor (flat_reader.rs:93-98) */
     GAJE_ERR_NAN = -7,           /* Err("NaN ...") guards of RustGenomicBlock::forward_core */
     GAJE_ERR_MODEL = -8,         /* other Err(String): "LM Head out_features is 0!", "Prompt tokens cannot be empty" */
-    GAJE_ERR_UNSUPPORTED = -9,   /* a tensor format this build does not run (Q8_0, 2-bit) */
+    GAJE_ERR_UNSUPPORTED = -9,   /* a tensor format or shape this build does not run */
     GAJE_ERR_HIP = -10,          /* HIP runtime failure */
     GAJE_ERR_NO_DEVICE = -11     /* no usable gfx950 device */
 };
@@ -133,8 +133,9 @@ int gaje_hip_moe_ffn(const float *x, int64_t T, int64_t h, const float *router, 
                      int32_t *top_idx, float *top_w, void *workspace, int64_t workspace_bytes, void *stream);
 
 /* Q8_0 rows (Q8_0Block {f16 scale; i8 qs[32]}, blocks.rs:36-49; the
- * --quant-embed format of token_embd / lm_head): packing into 144-byte groups
- * of four blocks (n * ceil(k/128) * 144 + 4 KiB of tail padding), the matvec
+ * --quant-embed format of token_embd / lm_head): packing into tiles of 8 rows
+ * (per group of four blocks: the 8 rows' codes, 1 KiB, then their scales, 64
+ * bytes; ceil(n/8) * ceil(k/128) * 1088 + 4 KiB of zero padding), the matvec
  * of GenomicLinear::forward_core on GenomicQ8_0 (linear/forward.rs:93-101) with
  * genomic_dot_product_q8_0_avx2's order (genomic.rs:377-448) and flush, and
  * dequantize_weight over file-layout blocks, all bit-exact. */

@@ -42,22 +42,21 @@ def _q8_rows(O, n, k, seed):
 
 
 def pack_q8_0_numpy(blocks, n, k):
-    """Per group of four blocks: chain l's 16 bytes (dword b = block 4g+b, byte c =
-    element 8c+l), the four f16 scales, 8 zero bytes; missing blocks are zero."""
+    """Tiles of 8 rows; per group of four blocks the 8 rows' codes (chain l's 16
+    bytes at 16l: dword b = block 4g+b, byte c = element 8c+l), then the 8 rows'
+    four f16 scales; missing rows and blocks are zero."""
     nb = k // 32
     G = (nb + 3) // 4
-    b = np.asarray(blocks, np.uint8).reshape(n, nb, 34)
-    q = np.zeros((n, 4 * G, 32), np.uint8)
-    q[:, :nb] = b[:, :, 2:]
-    sc = np.zeros((n, 4 * G, 2), np.uint8)
-    sc[:, :nb] = b[:, :, :2]
-    q = q.reshape(n, G, 4, 4, 8)                      # [row][g][block][c][l]
-    chains = q.transpose(0, 1, 4, 2, 3).reshape(n, G, 128)
-    out = np.concatenate([chains, sc.reshape(n, G, 8), np.zeros((n, G, 8), np.uint8)], axis=2)
-    return out.reshape(-1)
+    T = (n + 7) // 8
+    b = np.zeros((8 * T, 4 * G, 34), np.uint8)
+    b[:n, :nb] = np.asarray(blocks, np.uint8).reshape(n, nb, 34)
+    q = b[:, :, 2:].reshape(T, 8, G, 4, 4, 8)            # [tile][row][g][block][c][l]
+    codes = q.transpose(0, 2, 1, 5, 3, 4).reshape(T, G * 1024)
+    sc = b[:, :, :2].reshape(T, 8, G, 8).transpose(0, 2, 1, 3).reshape(T, G * 64)
+    return np.concatenate([codes, sc], axis=1).reshape(-1)
 
 
-@pytest.mark.parametrize("n,k", [(3, 896), (5, 32), (4, 96), (7, 576)])
+@pytest.mark.parametrize("n,k", [(3, 896), (5, 32), (4, 96), (7, 576), (17, 1536), (16, 224)])
 def test_q8_0_pack_layout(hip, O, n, k):
     blocks = _q8_rows(O, n, k, 1)
     packed = hip.ops.q8_0_upload(blocks, n, k)
