@@ -1475,11 +1475,10 @@ int launch_gemv(const GemvParams &p, hipStream_t s) {
         void (*sf)(GemvParams, int);
         if (p.mode == MODE_ARGMAX) sf = p.nontemporal ? gemv_q8_stream_kernel<true, MODE_ARGMAX> : gemv_q8_stream_kernel<false, MODE_ARGMAX>;
         else sf = p.nontemporal ? gemv_q8_stream_kernel<true, MODE_STORE> : gemv_q8_stream_kernel<false, MODE_STORE>;
-        int per_cu = 0;
-        GAJE_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, sf, THREADS, lds));
+        // one workgroup per compute unit streams best (measured on a 151936 x
+        // 896 matrix: 43.9 us against 46.0 with two and 53.0 with three)
         int64_t grid = (p.N + THREADS / 8 - 1) / (THREADS / 8);
-        const int64_t resident = (int64_t)(per_cu > 0 ? per_cu : 1) * device_cu_count();
-        if (grid > resident) grid = resident;
+        if (grid > device_cu_count()) grid = device_cu_count();
         hipLaunchKernelGGL(sf, dim3((unsigned)grid), dim3(THREADS), lds, s, p, q4_xstride(p.K));
         GAJE_HIP_CHECK(hipGetLastError());
         return GAJE_OK;
