@@ -483,6 +483,33 @@ extern "C" int gaje_hip_lut4_gemv(const uint8_t *codes, const float *lut, int64_
     return launch_gemv(p, as_stream(stream));
 }
 
+extern "C" int gaje_hip_2bit_gemv(const uint8_t *codes, const float *centroids, int64_t c_len, const float *modulation,
+                                  const float *x, const float *bias, int64_t bias_len, float *y, int64_t n, int64_t k,
+                                  void *stream) {
+    GAJE_TRY(check_dims(n, k));
+    if (k % 32) return set_error(GAJE_ERR_UNSUPPORTED, "2-bit rows need k %% 32 == 0 (got %lld)", (long long)k);
+    GemvParams p = plain_gemv(FMT_G2, codes, x, bias, bias_len, y, n, k);
+    const int64_t per_row = (k / 32) * 4;
+    p.lut = centroids;
+    if (c_len == 0) {
+        p.rows_valid = 0;  // compute_single_row: no centroids, the dot is 0 (linear/forward.rs:47)
+    } else if (c_len == 4) {
+        p.lut_block_stride = 0;
+        p.lut_rows_own = 0;
+    } else if (c_len >= per_row) {
+        p.lut_block_stride = 4;
+        p.lut_rows_own = c_len == per_row ? 0 : c_len / per_row;
+    } else {
+        return set_error(GAJE_ERR_INVALID_ARG, "c_len %lld is neither 0, 4 nor >= k/32*4", (long long)c_len);
+    }
+    if (c_len && !centroids) return set_error(GAJE_ERR_INVALID_ARG, "2-bit gemv: null centroids");
+    if (modulation) {
+        p.g2_modulated = 1;
+        for (int i = 0; i < 4; ++i) p.g2_mod[i] = modulation[i];
+    }
+    return launch_gemv(p, as_stream(stream));
+}
+
 extern "C" int gaje_hip_f32_gemv(const float *w, const float *x, const float *bias, int64_t bias_len, float *y,
                                  int64_t n, int64_t k, void *stream) {
     GAJE_TRY(check_dims(n, k));

@@ -118,9 +118,9 @@ __device__ __forceinline__ float order_key_inv(uint32_t k) {
 __device__ __forceinline__ float flush_small(float t) { return fabsf(t) < 1e-6f ? 0.0f : t; }
 
 // GenomicLinear::get_row_core (linear/forward.rs:195-285) element k of `row`
-// for the embedding formats: F32 copy, Q4_0 dequantize_weight (a product then
-// a sum, blocks.rs:18-30) from the packed rows, LUT-4bit table lookup (high
-// nibble first); rows past rows_valid read as zeros.
+// for the embedding formats: F32 copy, Q4_0 / Q8_0 dequantize_weight from the
+// packed rows, LUT-4bit table lookup (high nibble first), 2-bit centroid
+// lookup; rows past rows_valid read as zeros.
 __device__ __forceinline__ float embed_value(const EmbedParams &p, int64_t row, int64_t k) {
     const int64_t nb = p.K / 32;
     float v = 0.0f;
@@ -151,6 +151,20 @@ __device__ __forceinline__ float embed_value(const EmbedParams &p, int64_t row, 
                 const float q = (float)((word >> (8 * c + 4 * (bb & 1))) & 0x0Fu);
                 const uint32_t sm = *(const uint32_t *)(grp + 64 + 4 * bb);
                 v = __fadd_rn(__fmul_rn(q, half_lo(sm)), half_hi(sm));
+            } else if (p.fmt == FMT_G2) {
+                // get_row_core on Genomic2Bit (linear/forward.rs:210-237): the
+                // block's own four centroids where the table holds them, else
+                // its first four; codes 00/01/11/10 -> c0/c1/c2/c3, MSB first
+                // (dequantize_embedding_core, compute/quantize/dequantize.rs:6-42)
+                int64_t off = 0;
+                if (p.lut_block_stride) {
+                    const int64_t own = (row * nb + b) * 4;
+                    off = p.lut_rows_own == 0 ? b * 4 : own + 4 <= p.lut_len ? own : 0;
+                }
+                const float *c = p.lut + off;
+                const uint8_t byte = p.w[(row * nb + b) * 8 + i / 4];
+                const int bits = (byte >> ((3 - (i & 3)) * 2)) & 3;
+                v = bits == 0 ? c[0] : bits == 1 ? c[1] : bits == 3 ? c[2] : c[3];
             } else {
                 const float *t = p.lut + (row < p.lut_rows_own ? row * nb * 16 : 0) + b * p.lut_block_stride;
                 const uint8_t byte = p.w[(row * nb + b) * 16 + i / 2];

@@ -569,6 +569,77 @@ __device__ __forceinline__ float row_lut4(const GemvParams &p, const float *xs, 
     return flush_small(total);
 }
 
+// ------------------------------------------------------------- 2-bit ----
+// Genomic2Bit rows (genomic_dot_product, genomic.rs:17-144, in the x86 AVX2
+// branch the reference runs): 8 bytes of MSB-first 2-bit codes per block of
+// 32, four centroids per block; code 00/01/10/11 selects c0/c1/c3/c2 (times
+// the modulation factors).  Per block the reference accumulates the 32
+// products in two 8-lane FMA accumulators over two 4-byte steps (weights
+// 16t..16t+7 to the first, 16t+8..16t+15 to the second), sums them lane by
+// lane and reduces ((a0+a4)+(a1+a5))+((a2+a6)+(a3+a7)); the row sum adds the
+// block values in block order and flushes |sum| < 1e-5.  Here lane s of the
+// row's 8 computes whole blocks s, s+8, ...; the row sum then takes the
+// eight block values of each round from the lanes in order.
+
+// Code bits at `pos` (low bit) of `word` -> the selected centroid: two
+// sign-extended bit fields used as select masks (v_bfi).
+__device__ __forceinline__ float g2_pick(uint32_t word, int pos, uint32_t c00, uint32_t c01, uint32_t c10,
+                                         uint32_t c11) {
+    const uint32_t b0 = (uint32_t)__builtin_amdgcn_sbfe((int)word, pos, 1);
+    const uint32_t b1 = (uint32_t)__builtin_amdgcn_sbfe((int)word, pos + 1, 1);
+    const uint32_t lo = (b0 & c01) | (~b0 & c00), hi = (b0 & c11) | (~b0 & c10);
+    return __uint_as_float((b1 & hi) | (~b1 & lo));
+}
+
+template <bool NT>
+__device__ __forceinline__ float row_g2(const GemvParams &p, const float *xs, int64_t row, int s, int base) {
+    const int nb = p.nb;
+    const uint8_t *rowp = p.w + (size_t)row * nb * 8;
+    const float *crow = p.lut + (row < p.lut_rows_own ? (size_t)row * nb * 4 : 0);
+    float sum = 0.0f;
+    for (int j0 = 0; j0 < nb; j0 += 8) {
+        const int j = j0 + s;
+        float bv = 0.0f;
+        if (j < nb) {
+            const vu2 cw = ld_u2<NT>(rowp + (size_t)j * 8);
+            float4 c = ld_f4<NT>(crow + (size_t)j * p.lut_block_stride);
+            if (p.g2_modulated) {  // uniform
+                c.x = c.x * p.g2_mod[0];
+                c.y = c.y * p.g2_mod[1];
+                c.z = c.z * p.g2_mod[2];
+                c.w = c.w * p.g2_mod[3];
+            }
+            // codes 00, 01, 10, 11 -> c0, c1, c3, c2
+            const uint32_t k00 = __float_as_uint(c.x), k01 = __float_as_uint(c.y), k10 = __float_as_uint(c.w),
+                           k11 = __float_as_uint(c.z);
+            const float *xb = xs + (size_t)j * 32;
+            float acc0[8], acc1[8];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const uint32_t word = t ? cw.y : cw.x;  // bytes 4t..4t+3, byte q at bits 8q
+                const float4 x0 = *(const float4 *)(xb + 16 * t), x1 = *(const float4 *)(xb + 16 * t + 4);
+                const float4 x2 = *(const float4 *)(xb + 16 * t + 8), x3 = *(const float4 *)(xb + 16 * t + 12);
+                const float xv[16] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w,
+                                      x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int pos = 8 * (e >> 2) + 6 - 2 * (e & 3);  // weight e of the step, MSB first
+                    const float w = g2_pick(word, pos, k00, k01, k10, k11);
+                    if (e < 8) acc0[e] = fmaf(w, xv[e], t ? acc0[e] : 0.0f);
+                    else acc1[e - 8] = fmaf(w, xv[e], t ? acc1[e - 8] : 0.0f);
+                }
+            }
+            float a[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) a[e] = acc0[e] + acc1[e];
+            bv = ((a[0] + a[4]) + (a[1] + a[5])) + ((a[2] + a[6]) + (a[3] + a[7]));
+        }
+        const int nv = nb - j0 < 8 ? nb - j0 : 8;  // uniform
+        for (int t = 0; t < nv; ++t) sum = sum + shfl(bv, base + t);
+    }
+    return fabsf(sum) < 1e-5f ? 0.0f : sum;
+}
+
 // compute_single_row's tail: anchors, then the bias (already loaded) if the
 // row has one.
 __device__ __forceinline__ float finish_row(const GemvParams &p, const XView &xv, int64_t r, float v, float bias) {
@@ -743,7 +814,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
             const int64_t prow = q.row_ok ? q.row : 0;
             if constexpr (FMT == FMT_Q4_0) q4_prefetch<NT, D>(wbase, p, prow, s, q4r);
             else if constexpr (FMT == FMT_Q8_0) q8_prefetch<NT, D>(wbase, p.rows_valid > 0 ? (p.nb + 3) >> 2 : 1, prow, s, q8r);
-            else f32_prefetch<NT>(wbase, p, prow, s, f32r);
+            else if constexpr (FMT == FMT_F32) f32_prefetch<NT>(wbase, p, prow, s, f32r);
         }
         if (halted) return;  // uniform; checked once the first loads are in flight
         auto store_batch = [&](int64_t m0) {
@@ -879,6 +950,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
             if constexpr (FMT == FMT_Q4_0) v = q4_consume<NT, D>(p, xv, q.row, s, row_base, q4r);
             else if constexpr (FMT == FMT_Q8_0) v = q8_consume<NT, D>(p, xv, q.row, s, row_base, q8r);
             else if constexpr (FMT == FMT_F32) v = f32_consume<NT>(p, smem, q.row, s, row_base, f32r);
+            else if constexpr (FMT == FMT_G2) v = row_g2<NT>(p, smem, q.row, s, row_base);
             else v = row_lut4<NT>(p, smem, q.row, s, row_base, tbl);
         }
         const float v1 = shfl(v, pair_base + LPR);  // r1's result (lane 0 of its group)
@@ -1419,7 +1491,9 @@ int launch_gemv(const GemvParams &p, hipStream_t s) {
     if ((p.fmt == FMT_Q4_0 || p.fmt == FMT_Q8_0) && p.K % 32 != 0)
         return set_error(GAJE_ERR_UNSUPPORTED, "gemv: Q4_0/Q8_0 rows need in_features %% 32 == 0 (got %lld)",
                          (long long)p.K);
-    if (p.fmt < FMT_F32 || p.fmt > FMT_Q8_0) return set_error(GAJE_ERR_INVALID_ARG, "gemv: unknown format %d", p.fmt);
+    if (p.fmt < FMT_F32 || p.fmt > FMT_G2) return set_error(GAJE_ERR_INVALID_ARG, "gemv: unknown format %d", p.fmt);
+    if (p.fmt == FMT_G2 && (p.K % 32 != 0 || (p.rows_valid > 0 && !p.lut)))
+        return set_error(GAJE_ERR_UNSUPPORTED, "gemv: 2-bit rows need in_features %% 32 == 0 and centroids");
     if (p.fmt != FMT_LUT4 && (((uintptr_t)p.x | (uintptr_t)p.norm_w) & 15))
         return set_error(GAJE_ERR_INVALID_ARG, "gemv: x and norm_w must be 16-byte aligned");
     if (p.rows_valid > 0 && !p.w) return set_error(GAJE_ERR_INVALID_ARG, "gemv: null weights");
@@ -1508,6 +1582,9 @@ int launch_gemv(const GemvParams &p, hipStream_t s) {
     } else if (p.fmt == FMT_LUT4) {
         lpr = 4;
         fn = gemv_kernel<FMT_LUT4, 4, false, 1>;
+    } else if (p.fmt == FMT_G2) {
+        lpr = 8;
+        fn = p.nontemporal ? gemv_kernel<FMT_G2, 8, true, 1> : gemv_kernel<FMT_G2, 8, false, 1>;
     } else {
         lpr = 2;
         if (p.mode == MODE_ARGMAX && p.nontemporal) fn = gemv_kernel<FMT_F32, 2, true, 1, MODE_ARGMAX>;

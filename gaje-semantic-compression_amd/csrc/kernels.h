@@ -13,6 +13,7 @@ enum WeightFormat : int32_t {
     FMT_Q4_0 = 1,  // 20-byte Q4_0Block rows
     FMT_LUT4 = 2,  // Genomic4Bit: 16-byte code blocks + 16-entry f32 tables
     FMT_Q8_0 = 3,  // 34-byte Q8_0Block rows
+    FMT_G2 = 4,    // Genomic2Bit: 8-byte blocks of MSB-first 2-bit codes + 4 f32 centroids per block
 };
 
 constexpr uint32_t NAN_NONE = 0xFFFFFFFFu;
@@ -55,9 +56,11 @@ struct GemvParams {
     int32_t fmt;
     int32_t f32_tiled;       // FMT_F32 weights in the tiled layout (K % 8 == 0)
     int32_t nontemporal;     // stream the weights past the caches (read-once tensors)
-    const float *lut;        // FMT_LUT4 tables
-    int64_t lut_rows_own;    // rows r < lut_rows_own use table block r*nb*16
-    int32_t lut_block_stride;// 16 = one table per block column, 0 = one shared table
+    const float *lut;        // FMT_LUT4 tables / FMT_G2 centroids (T = 16 or 4 floats per block)
+    int64_t lut_rows_own;    // rows r < lut_rows_own use the tables from r*nb*T, others from 0
+    int32_t lut_block_stride;// T = one table per block, 0 = one shared table
+    int32_t g2_modulated;    // FMT_G2: centroid k times g2_mod[k] (genomic.rs:60-63)
+    float g2_mod[4];
     int32_t nb;              // K / 32
     int64_t rows_valid;      // rows with a complete weight row (others read as 0)
     int64_t N, K;
@@ -151,6 +154,7 @@ struct EmbedParams {
     const float *lut;
     int64_t lut_rows_own;
     int32_t lut_block_stride;
+    int64_t lut_len;         // floats in lut (FMT_G2: blocks past it read the first table)
     int64_t vocab, rows_valid, K;
     float *h;
     DevState *st;

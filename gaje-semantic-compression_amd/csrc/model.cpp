@@ -49,7 +49,7 @@ struct HostLinear {
 struct DevLinear {
     int fmt = -1;
     int f32_tiled = 0;  // FMT_F32 rows in the GEMV's tiled layout
-    int64_t N = 0, K = 0, rows_valid = 0, lut_rows_own = 0;
+    int64_t N = 0, K = 0, rows_valid = 0, lut_rows_own = 0, lut_len = 0;
     int lut_block_stride = 0;
     uint8_t *w = nullptr;
     float *lut = nullptr;
@@ -139,10 +139,18 @@ int read_linear(const FlatFile &f, const std::string &name, HostLinear &L) {
     if (bit_depth == 4) L.fmt = n_cent == 0 ? FMT_Q4_0 : FMT_LUT4;
     else if (bit_depth == 32) L.fmt = FMT_F32;
     else if (bit_depth == 8) L.fmt = FMT_Q8_0;  // init.rs:40-45
-    else
-        return set_error(GAJE_ERR_UNSUPPORTED, "tensor '%s': 2-bit genomic format is not in this build", name.c_str());
+    else L.fmt = FMT_G2;                        // every other bit_depth: Genomic2Bit (init.rs:53)
+    if (L.fmt == FMT_G2) {
+        // the row dot reads 4 centroids per block from a row's table or, for
+        // rows without one, from the table's start (linear/forward.rs:40-45),
+        // and get_row indexes 4 of them: shorter tables are read past upstream
+        const uint64_t nbk = (uint64_t)(L.K / 32);
+        if ((n_cent > 0 && n_cent < 4) || (n_cent > 4 && n_cent < nbk * 4))
+            return set_error(GAJE_ERR_UNSUPPORTED, "tensor '%s': 2-bit centroid table of %llu floats (need 4 or >= %llu)",
+                             name.c_str(), (unsigned long long)n_cent, (unsigned long long)(nbk * 4));
+    }
     if (e->dna_len) L.w.assign(dna, dna + e->dna_len);
-    if (L.fmt == FMT_LUT4) {
+    if (L.fmt == FMT_LUT4 || L.fmt == FMT_G2) {
         L.lut.resize(n_cent);
         memcpy(L.lut.data(), c, n_cent * 4);
     }
@@ -169,6 +177,7 @@ int64_t rows_valid_of(const HostLinear &L) {
     if (nb == 0) return 0;
     if (L.fmt == FMT_Q4_0) return std::min<int64_t>(L.N, (int64_t)(L.w.size() / 20) / nb);
     if (L.fmt == FMT_Q8_0) return std::min<int64_t>(L.N, (int64_t)(L.w.size() / 34) / nb);
+    if (L.fmt == FMT_G2) return L.lut.size() < 4 ? 0 : std::min<int64_t>(L.N, (int64_t)L.w.size() / (nb * 8));
     if (L.lut.size() < 16) return 0;  // no table: compute_single_row yields 0
     return std::min<int64_t>(L.N, (int64_t)L.w.size() / (nb * 16));
 }
@@ -192,8 +201,25 @@ int fuse_linears(std::vector<HostLinear> parts, const std::string &name, HostLin
         any_anchor |= !p.a_ptr.empty();
     }
     for (auto &p : parts) {
-        size_t row_bytes = out.fmt == FMT_Q4_0 ? nb * 20 : out.fmt == FMT_Q8_0 ? nb * 34 : out.fmt == FMT_LUT4 ? nb * 16 : out.K * 4;
+        size_t row_bytes = out.fmt == FMT_Q4_0   ? nb * 20
+                           : out.fmt == FMT_Q8_0 ? nb * 34
+                           : out.fmt == FMT_LUT4 ? nb * 16
+                           : out.fmt == FMT_G2   ? nb * 8
+                                                 : out.K * 4;
         out.w.insert(out.w.end(), p.w.begin(), p.w.begin() + row_bytes * p.N);
+        if (out.fmt == FMT_G2) {  // per-row centroid tables, as the row dot reads them
+            const size_t per_row = nb * 4;
+            for (int64_t r = 0; r < p.N; ++r) {
+                if (p.lut.size() == 4) {  // init.rs:125-131
+                    for (int64_t b = 0; b < nb; ++b) out.lut.insert(out.lut.end(), p.lut.begin(), p.lut.end());
+                    continue;
+                }
+                const float *src = p.lut.size() >= (size_t)(r + 1) * per_row && p.lut.size() != per_row
+                                       ? p.lut.data() + r * per_row
+                                       : p.lut.data();  // the column table, or the table's start
+                out.lut.insert(out.lut.end(), src, src + per_row);
+            }
+        }
         if (out.fmt == FMT_LUT4) {  // expand to per-row tables (init.rs:109-124)
             const size_t per_row = nb * 16;
             for (int64_t r = 0; r < p.N; ++r) {
@@ -380,6 +406,18 @@ int upload_linear(gaje_hip_model *m, const HostLinear &L, DevLinear &D, bool til
     } else {
         GAJE_TRY(m->upload(&D.w, L.w.data(), L.w.size()));
     }
+    if (L.fmt == FMT_G2 && L.lut.size() >= 4) {
+        const size_t n = L.lut.size(), per_row = (size_t)nb * 4;
+        if (n == 4) {
+            D.lut_block_stride = 0;  // one table for every block (init.rs:125-131)
+            D.lut_rows_own = 0;
+        } else {
+            D.lut_block_stride = 4;  // n >= per_row (read_linear)
+            D.lut_rows_own = n == per_row ? 0 : (int64_t)(n / per_row);
+        }
+        D.lut_len = (int64_t)n;
+        GAJE_TRY(m->upload(&D.lut, L.lut.data(), n));
+    }
     if (L.fmt == FMT_LUT4 && !L.lut.empty()) {
         const size_t n = L.lut.size(), per_row = (size_t)nb * 16;
         if (n == 16) {
@@ -519,6 +557,7 @@ int enqueue_token(gaje_hip_model *m, hipEvent_t ev_blocks_done) {
     ep.lut = m->embd.lut;
     ep.lut_rows_own = m->embd.lut_rows_own;
     ep.lut_block_stride = m->embd.lut_block_stride;
+    ep.lut_len = m->embd.lut_len;
     ep.vocab = m->vocab_embd;
     ep.rows_valid = m->embd.rows_valid;
     ep.K = m->n_embd;
@@ -1129,6 +1168,7 @@ extern "C" int gaje_hip_prefill_mfma(gaje_hip_model *m, const uint32_t *ids, int
         ep.lut = m->embd.lut;
         ep.lut_rows_own = m->embd.lut_rows_own;
         ep.lut_block_stride = m->embd.lut_block_stride;
+    ep.lut_len = m->embd.lut_len;
         ep.vocab = m->vocab_embd;
         ep.rows_valid = m->embd.rows_valid;
         ep.K = m->n_embd;
@@ -1262,6 +1302,7 @@ int batch_enqueue_step(gaje_hip_batch *b, const uint32_t *ids, int64_t n, int64_
     ep.lut = m->embd.lut;
     ep.lut_rows_own = m->embd.lut_rows_own;
     ep.lut_block_stride = m->embd.lut_block_stride;
+    ep.lut_len = m->embd.lut_len;
     ep.vocab = m->vocab_embd;
     ep.rows_valid = m->embd.rows_valid;
     ep.K = E;
@@ -1684,8 +1725,10 @@ extern "C" int gaje_hip_time_stage(gaje_hip_model *m, int stage, int64_t layer, 
         int64_t b = D.fmt == FMT_Q4_0   ? D.N * nb * 20
                     : D.fmt == FMT_Q8_0 ? D.N * nb * 34
                     : D.fmt == FMT_LUT4 ? D.N * nb * 16
+                    : D.fmt == FMT_G2   ? D.N * nb * 8
                                         : D.N * D.K * 4;
         if (D.fmt == FMT_LUT4 && D.lut) b += (D.lut_block_stride ? (D.lut_rows_own ? D.N : 1) * nb * 16 * 4 : 64);
+        if (D.fmt == FMT_G2 && D.lut) b += (D.lut_block_stride ? (D.lut_rows_own ? D.N : 1) * nb * 4 * 4 : 16);
         return b;
     };
     int64_t algo = 0;

@@ -20,6 +20,11 @@
 //                     qs[m] = code[2m] | code[2m+1] << 4      (low nibble = even)
 //   LUT-4bit block  : byte m = code[2m] << 4 | code[2m+1]      (high nibble = even),
 //                     lut[row][b][j] = f32(z_j * s)
+// 2-bit body recipe (Genomic2Bit, bit_depth 2; 2-bit codes uniform, four
+// centroids per (row, block) at the quartile midpoints y_j = Phi^-1((j + 0.5) / 4)):
+//   code(row, col)  = r(key(name#codes), row*k + col) >> 62
+//   block byte m    = code[4m] << 6 | code[4m+1] << 4 | code[4m+2] << 2 | code[4m+3]
+//   centroids[row][b][j] = f32(y_j * s(row, b))   (ascending: codes 00, 01, 11, 10)
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -139,6 +144,28 @@ void gen_q4_0(uint64_t seed, const std::string &name, int64_t n, int64_t k, uint
     });
 }
 
+void gen_2bit(uint64_t seed, const std::string &name, int64_t n, int64_t k, uint8_t *codes, float *cent) {
+    const int64_t nb = k / 32;
+    double y[4];
+    for (int j = 0; j < 4; ++j) y[j] = probit((j + 0.5) / 4.0);
+    const uint64_t kc = stream_key(seed, name + "#codes"), ks = stream_key(seed, name + "#scale");
+    parallel_rows(n, [&](int64_t r0, int64_t r1) {
+        for (int64_t r = r0; r < r1; ++r)
+            for (int64_t b = 0; b < nb; ++b) {
+                double s = 0.01 + 0.04 * u01(draw(ks, (uint64_t)(r * nb + b)));
+                float *t = cent + (r * nb + b) * 4;
+                for (int j = 0; j < 4; ++j) t[j] = (float)(y[j] * s);
+                uint8_t *blk = codes + (r * nb + b) * 8;
+                for (int m = 0; m < 8; ++m) {
+                    uint64_t i = (uint64_t)(r * k + b * 32 + 4 * m);
+                    uint8_t byte = 0;
+                    for (int q = 0; q < 4; ++q) byte = (uint8_t)((byte << 2) | (draw(kc, i + q) >> 62));
+                    blk[m] = byte;
+                }
+            }
+    });
+}
+
 void gen_lut4(uint64_t seed, const std::string &name, int64_t n, int64_t k, uint8_t *codes, float *lut) {
     const int64_t nb = k / 32;
     const double *z = quantile_table();
@@ -200,7 +227,8 @@ struct Blob {
     uint64_t bit_depth, out_f, in_f;
     uint64_t dna_len, c_len, bias_len;  // bytes
     uint64_t dna_off = 0, c_off = 0, anc_off = 0, bias_off = 0;
-    // generators: 0 normal f32, 1 q4_0, 2 lut4, 3 norm weights, 4 normal f32 quantised to Q8_0
+    // generators: 0 normal f32, 1 q4_0, 2 lut4, 3 norm weights, 4 normal f32 quantised to Q8_0,
+    // 5 2-bit codes and centroids
     int kind;
     std::string stream;  // PRNG stream name of the dna values
     bool has_bias = false;
@@ -235,6 +263,13 @@ extern "C" int gaje_synth_lut4(uint64_t seed, const char *name, int64_t n, int64
     return GAJE_OK;
 }
 
+extern "C" int gaje_synth_2bit(uint64_t seed, const char *name, int64_t n, int64_t k, uint8_t *codes, float *centroids) {
+    if (!name || !codes || !centroids || n < 0 || k < 0)
+        return set_error(GAJE_ERR_INVALID_ARG, "gaje_synth_2bit: bad arguments");
+    gen_2bit(seed, name, n, k, codes, centroids);
+    return GAJE_OK;
+}
+
 extern "C" int gaje_synth_normal(uint64_t seed, const char *name, int64_t count, float mean, float sd, float *out) {
     if (!name || !out || count < 0) return set_error(GAJE_ERR_INVALID_ARG, "gaje_synth_normal: bad arguments");
     gen_normal(seed, name, count, mean, sd, out);
@@ -245,7 +280,8 @@ extern "C" int gaje_synth_write_flat(const char *path, const gaje_synth_config *
     if (!path || !cfg) return set_error(GAJE_ERR_INVALID_ARG, "gaje_synth_write_flat: null argument");
     const gaje_synth_config &c = *cfg;
     if (c.n_embd <= 0 || c.n_head <= 0 || c.n_head_kv <= 0 || c.n_blocks < 0 || c.ffn <= 0 ||
-        c.vocab_size <= 0 || c.n_embd % c.n_head != 0 || (c.body_format != 1 && c.body_format != 2))
+        c.vocab_size <= 0 || c.n_embd % c.n_head != 0 ||
+        (c.body_format != 1 && c.body_format != 2 && c.body_format != 4))
         return set_error(GAJE_ERR_INVALID_ARG, "gaje_synth_write_flat: invalid shape");
     const int64_t h = c.n_embd, hd = h / c.n_head, qd = c.n_head * hd, kvd = c.n_head_kv * hd;
     const int fmt = c.body_format;
@@ -263,6 +299,16 @@ extern "C" int gaje_synth_write_flat(const char *path, const gaje_synth_config *
         b.stream = name;
         return b;
     };
+    // bytes of a 2-bit tensor's centroid table: the leading part of the per
+    // (row, block) tables that the chosen form keeps
+    auto g2_table_bytes = [&](int64_t out_f, int64_t nb) -> uint64_t {
+        switch (c.g2_tables) {
+            case 1: return (uint64_t)(nb * 4 * 4);
+            case 2: return 16;
+            case 3: return (uint64_t)(((out_f / 2) * nb * 4 + 6) * 4);
+            default: return (uint64_t)(out_f * nb * 4 * 4);
+        }
+    };
     auto body = [&](const std::string &name, int64_t out_f, int64_t in_f) {
         int64_t nb = in_f / 32;
         Blob b{name, 4, (uint64_t)out_f, (uint64_t)in_f, 0, 0, 0};
@@ -270,6 +316,11 @@ extern "C" int gaje_synth_write_flat(const char *path, const gaje_synth_config *
         b.stream = name;
         if (fmt == 1) {
             b.dna_len = (uint64_t)(out_f * nb * 20);
+        } else if (fmt == 4) {  // Genomic2Bit: bit_depth 2, 8 code bytes and 4 centroids per block
+            b.bit_depth = 2;
+            b.kind = 5;
+            b.dna_len = (uint64_t)(out_f * nb * 8);
+            b.c_len = g2_table_bytes(out_f, nb);
         } else {
             b.dna_len = (uint64_t)(out_f * nb * 16);
             b.c_len = (uint64_t)(out_f * nb * 16 * 4);
@@ -280,15 +331,22 @@ extern "C" int gaje_synth_write_flat(const char *path, const gaje_synth_config *
     // --quant-embed (export_gaje_flat.py:25-32): token_embd and lm_head as Q8_0 (bit_depth 8)
     auto embed = [&](const std::string &name, const std::string &stream) {
         Blob b = dense(name, c.vocab_size, h, stream);
-        if (c.quant_embed) {
+        if (c.quant_embed == 1) {
             b.bit_depth = 8;
             b.kind = 4;
             b.dna_len = (uint64_t)(c.vocab_size * (h / 32) * 34);
+        } else if (c.quant_embed == 2) {
+            b.bit_depth = 2;
+            b.kind = 5;
+            b.dna_len = (uint64_t)(c.vocab_size * (h / 32) * 8);
+            b.c_len = g2_table_bytes(c.vocab_size, h / 32);
         }
         return b;
     };
+    if (c.quant_embed < 0 || c.quant_embed > 2 || c.g2_tables < 0 || c.g2_tables > 3)
+        return set_error(GAJE_ERR_INVALID_ARG, "gaje_synth_write_flat: quant_embed 0-2, g2_tables 0-3");
     if (c.quant_embed && h % 32)
-        return set_error(GAJE_ERR_INVALID_ARG, "gaje_synth_write_flat: Q8_0 embeddings need n_embd %% 32 == 0");
+        return set_error(GAJE_ERR_INVALID_ARG, "gaje_synth_write_flat: quantised embeddings need n_embd %% 32 == 0");
     blobs.push_back(embed("token_embd", "token_embd"));
     blobs.push_back(norm("output_norm"));
     blobs.push_back(embed("lm_head", c.tied_embeddings ? "token_embd" : "lm_head"));
@@ -427,6 +485,10 @@ extern "C" int gaje_synth_write_flat(const char *path, const gaje_synth_config *
             case 2:
                 lut.resize(b.c_len / 4);
                 gen_lut4(c.seed, b.stream, (int64_t)b.out_f, (int64_t)b.in_f, dna.data(), lut.data());
+                break;
+            case 5:  // the full per (row, block) tables; the blob keeps the first c_len bytes
+                lut.resize((size_t)(b.out_f * (b.in_f / 32) * 4));
+                gen_2bit(c.seed, b.stream, (int64_t)b.out_f, (int64_t)b.in_f, dna.data(), lut.data());
                 break;
             case 4: {
                 std::vector<float> w((size_t)(b.out_f * b.in_f));

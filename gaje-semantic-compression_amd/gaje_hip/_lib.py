@@ -85,7 +85,7 @@ class SynthConfig(ctypes.Structure):
                 ("qkv_bias", ctypes.c_int32), ("tied_embeddings", ctypes.c_int32),
                 ("body_format", ctypes.c_int32), ("fused", ctypes.c_int32),
                 ("rope_interleaved", ctypes.c_int32), ("use_genomic_norm", ctypes.c_int32),
-                ("quant_embed", ctypes.c_int32),
+                ("quant_embed", ctypes.c_int32), ("g2_tables", ctypes.c_int32),
                 ("seed", ctypes.c_uint64)]
 
 
@@ -125,6 +125,7 @@ SIGNATURES = [
     ("gaje_hip_q8_0_gemv", ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_vp]),
     ("gaje_hip_q8_0_dequant", ctypes.c_int, [c_vp, c_vp, c_i64, c_vp]),
     ("gaje_hip_lut4_gemv", ctypes.c_int, [c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_vp]),
+    ("gaje_hip_2bit_gemv", ctypes.c_int, [c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_vp]),
     ("gaje_hip_f32_gemv", ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_vp]),
     ("gaje_hip_q4_0_dequant", ctypes.c_int, [c_vp, c_vp, c_i64, c_vp]),
     ("gaje_hip_rmsnorm", ctypes.c_int, [c_vp, c_vp, ctypes.c_float, c_vp, c_i64, c_vp]),
@@ -170,6 +171,7 @@ SIGNATURES = [
     ("gaje_synth_write_flat", ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(SynthConfig)]),
     ("gaje_synth_q4_0", ctypes.c_int, [ctypes.c_uint64, ctypes.c_char_p, c_i64, c_i64, c_vp]),
     ("gaje_synth_lut4", ctypes.c_int, [ctypes.c_uint64, ctypes.c_char_p, c_i64, c_i64, c_vp, c_vp]),
+    ("gaje_synth_2bit", ctypes.c_int, [ctypes.c_uint64, ctypes.c_char_p, c_i64, c_i64, c_vp, c_vp]),
     ("gaje_synth_normal", ctypes.c_int, [ctypes.c_uint64, ctypes.c_char_p, c_i64, ctypes.c_float,
                                          ctypes.c_float, c_vp]),
 ]

@@ -167,6 +167,17 @@ def lut4_gemv(codes: DeviceBuffer, lut: DeviceBuffer, lut_len: int, x: DeviceBuf
                                    n, k, stream))
 
 
+def bit2_gemv(codes: DeviceBuffer, centroids: DeviceBuffer | None, c_len: int, x: DeviceBuffer,
+              y: DeviceBuffer, n: int, k: int, modulation=None, bias: DeviceBuffer | None = None,
+              bias_len: int = 0, stream=None) -> None:
+    """GenomicLinear::forward_core on Genomic2Bit rows (gaje_hip_2bit_gemv)."""
+    mod = None
+    if modulation is not None:
+        mod = np.ascontiguousarray(modulation, dtype=np.float32).reshape(4)
+    check(lib().gaje_hip_2bit_gemv(codes.ptr, _p(centroids), c_len, mod.ctypes.data if mod is not None else None,
+                                   x.ptr, _p(bias), bias_len, y.ptr, n, k, stream))
+
+
 def f32_gemv(w: DeviceBuffer, x: DeviceBuffer, y: DeviceBuffer, n: int, k: int,
              bias: DeviceBuffer | None = None, bias_len: int = 0, stream=None) -> None:
     check(lib().gaje_hip_f32_gemv(w.ptr, x.ptr, _p(bias), bias_len, y.ptr, n, k, stream))

@@ -24,6 +24,7 @@ from ._lib import SynthConfig, check, lib
 
 Q4_0 = 1
 LUT4 = 2
+BIT2 = 4  # Genomic2Bit (bit_depth 2)
 
 PRESETS = {
     "smollm2-135m": dict(n_embd=576, n_head=9, n_head_kv=3, n_blocks=30, ffn=1536, vocab_size=49152,
@@ -69,6 +70,14 @@ def lut4_tensor(seed: int, name: str, n: int, k: int):
     lut = np.empty(n * (k // 32) * 16, dtype=np.float32)
     check(lib().gaje_synth_lut4(seed, name.encode(), n, k, codes.ctypes.data, lut.ctypes.data))
     return codes, lut
+
+
+def bit2_tensor(seed: int, name: str, n: int, k: int):
+    """([n][k/32][8] code bytes, [n][k/32][4] f32 centroids) of the 2-bit recipe."""
+    codes = np.empty(n * (k // 32) * 8, dtype=np.uint8)
+    cent = np.empty(n * (k // 32) * 4, dtype=np.float32)
+    check(lib().gaje_synth_2bit(seed, name.encode(), n, k, codes.ctypes.data, cent.ctypes.data))
+    return codes, cent
 
 
 def normal(seed: int, name: str, count: int, mean: float = 0.0, std: float = 1.0) -> np.ndarray:

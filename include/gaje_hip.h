@@ -154,6 +154,17 @@ int gaje_hip_lut4_gemv(const uint8_t *codes, const float *lut, int64_t lut_len, 
                        const float *bias, int64_t bias_len, float *y, int64_t n, int64_t k,
                        void *stream);
 
+/* 2-bit matvec (Genomic2Bit rows: per block of 32, 8 bytes of MSB-first 2-bit
+ * codes): genomic_dot_product (genomic.rs:17-144, the AVX2 branch's order) over
+ * the row slicing of linear/forward.rs:33-57, |sum| < 1e-5 flushed.  c_len
+ * floats of centroids: 4 (one table), k/32*4 (one per block column) or more
+ * (rows r < c_len/(k/32*4) own their tables, later rows read the table's
+ * start), 0 (every row dot is 0).  modulation: 4 host floats multiplying
+ * centroids 0..3 (forward_core's modulation_factors), or NULL for 1. */
+int gaje_hip_2bit_gemv(const uint8_t *codes, const float *centroids, int64_t c_len, const float *modulation,
+                       const float *x, const float *bias, int64_t bias_len, float *y, int64_t n, int64_t k,
+                       void *stream);
+
 /* FP32 matvec (lm_head, GenomicF32 rows): dot_product per row
  * (compute/kernels/dot.rs:23-94 via linear/forward.rs:20-32). */
 int gaje_hip_f32_gemv(const float *w, const float *x, const float *bias, int64_t bias_len,
@@ -196,7 +207,7 @@ typedef struct {
     float eps, rope_base;
     int32_t rope_split;          /* 1 = "split" rope_style, 0 = interleaved */
     int32_t arch_family;         /* header arch_family (0 = none)           */
-    int32_t body_format;         /* 1 = Q4_0 blocks, 2 = LUT-4bit           */
+    int32_t body_format;         /* 1 = Q4_0 blocks, 2 = LUT-4bit, 4 = 2-bit */
     int32_t use_genomic_norm;
     int64_t max_ctx;             /* KV capacity currently allocated          */
     int64_t weight_bytes;        /* bytes of weights resident in HBM         */
@@ -389,11 +400,13 @@ typedef struct {
     int32_t arch_family;           /* header descriptor; 0 = JSON-only config    */
     int32_t qkv_bias;              /* 1 = write an N(0,0.02) bias for attn_qkv   */
     int32_t tied_embeddings;       /* 1 = lm_head rows equal token_embd rows     */
-    int32_t body_format;           /* 1 = Q4_0 blocks, 2 = LUT-4bit per row/block */
+    int32_t body_format;           /* 1 = Q4_0 blocks, 2 = LUT-4bit per row/block, 4 = 2-bit per row/block */
     int32_t fused;                 /* 1 = attn_qkv / ffn_gate_up, 0 = split      */
     int32_t rope_interleaved;      /* metadata rope_style "interleaved" (else "split") */
     int32_t use_genomic_norm;      /* metadata config.use_genomic_norm           */
-    int32_t quant_embed;           /* 1 = token_embd / lm_head as Q8_0 (bit_depth 8, --quant-embed) */
+    int32_t quant_embed;           /* 1 = token_embd / lm_head as Q8_0 (bit_depth 8, --quant-embed), 2 = as 2-bit */
+    int32_t g2_tables;             /* 2-bit centroid tables: 0 per (row, block), 1 per block column,
+                                      2 one shared table, 3 the first half of the rows' tables + 6 floats */
     uint64_t seed;
 } gaje_synth_config;
 
@@ -402,6 +415,8 @@ int gaje_synth_write_flat(const char *path, const gaje_synth_config *cfg);
 int gaje_synth_q4_0(uint64_t seed, const char *name, int64_t n, int64_t k, uint8_t *blocks_out);
 int gaje_synth_lut4(uint64_t seed, const char *name, int64_t n, int64_t k, uint8_t *codes_out,
                     float *lut_out);
+int gaje_synth_2bit(uint64_t seed, const char *name, int64_t n, int64_t k, uint8_t *codes_out,
+                    float *centroids_out);
 int gaje_synth_normal(uint64_t seed, const char *name, int64_t count, float mean, float stddev,
                       float *out);
 

@@ -307,6 +307,89 @@ float orc_dot_4bit(const uint8_t *weights, const float *input, const float *cent
     return fabsf(total) < 1e-6f ? 0.0f : total;
 }
 
+/* genomic_dot_product (2-bit, Gray-coded centroids) — genomic.rs:17-144.  The
+ * reference forces genomic_dot_product_scalar (:26), whose x86 AVX2+FMA branch
+ * (:67-122) runs per block: codes are read MSB first, code 00/01/10/11 selects
+ * c0/c1/c3/c2 of the block's four centroids times the modulation factors
+ * (:60-70); 4-byte steps feed 16 weights to two 8-lane FMA accumulators
+ * (weights 0-7 of the step to the first, 8-15 to the second), the lanes are
+ * summed pairwise and reduced as ((a0+a4)+(a1+a5))+((a2+a6)+(a3+a7)), and
+ * that block value is added to the row sum.  Bytes past the last 4-byte step
+ * go through the scalar loop (:124-133), each product rounded and added to the
+ * row sum.  |sum| < 1e-5 flushes to 0 (:137-139).  centroids advance by 4 per
+ * block from the row's base; modulation may be NULL (all 1). */
+float orc_dot_2bit(const uint8_t *weights, const float *input, const float *centroids, size_t stride,
+                   size_t n_blocks, const float *modulation) {
+    static const float one[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+    const float *m = modulation ? modulation : one;
+    float sum = 0.0f;
+    for (size_t j = 0; j < n_blocks; j++) {
+        const float *in = input + j * stride * 4;
+        const uint8_t *w = weights + j * stride;
+        const float *cp = centroids + j * 4;
+        const float c0 = cp[0] * m[0], c1 = cp[1] * m[1], c2 = cp[2] * m[2], c3 = cp[3] * m[3];
+        const float ca[4] = {c0, c1, c3, c2};
+        float acc0[8] = {0}, acc1[8] = {0};
+        size_t k = 0;
+        while (k + 4 <= stride) {
+            float wv[16];
+            for (int q = 0; q < 4; q++)
+                for (int b = 0; b < 4; b++) wv[4 * q + b] = ca[(w[k + q] >> (6 - 2 * b)) & 3];
+            for (int e = 0; e < 8; e++) {
+                acc0[e] = fmaf(wv[e], in[k * 4 + e], acc0[e]);
+                acc1[e] = fmaf(wv[8 + e], in[k * 4 + 8 + e], acc1[e]);
+            }
+            k += 4;
+        }
+        float a[8];
+        for (int e = 0; e < 8; e++) a[e] = acc0[e] + acc1[e];
+        const float s0 = a[0] + a[4], s1 = a[1] + a[5], s2 = a[2] + a[6], s3 = a[3] + a[7];
+        const float r = (s0 + s1) + (s2 + s3);
+        sum += r;
+        while (k < stride) {
+            const uint8_t byte = w[k];
+            for (int b = 0; b < 4; b++) {
+                const float p = ca[(byte >> ((3 - b) * 2)) & 3] * in[k * 4 + b];
+                sum += p;
+            }
+            k += 1;
+        }
+    }
+    return fabsf(sum) < 1e-5f ? 0.0f : sum;
+}
+
+/* The same function without the AVX2 branch (a host lacking AVX2/FMA runs
+ * only the scalar loop, :124-133): one rounded product and one add per weight. */
+float orc_dot_2bit_scalar(const uint8_t *weights, const float *input, const float *centroids, size_t stride,
+                          size_t n_blocks, const float *modulation) {
+    static const float one[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+    const float *m = modulation ? modulation : one;
+    float sum = 0.0f;
+    for (size_t j = 0; j < n_blocks; j++) {
+        const float *cp = centroids + j * 4;
+        const float ca[4] = {cp[0] * m[0], cp[1] * m[1], cp[3] * m[3], cp[2] * m[2]};
+        for (size_t k = 0; k < stride; k++) {
+            const uint8_t byte = weights[j * stride + k];
+            for (int b = 0; b < 4; b++) {
+                const float p = ca[(byte >> ((3 - b) * 2)) & 3] * input[j * stride * 4 + k * 4 + b];
+                sum += p;
+            }
+        }
+    }
+    return fabsf(sum) < 1e-5f ? 0.0f : sum;
+}
+
+/* dequantize_embedding_core with a block's four centroids (the get_row_core
+ * call, compute/quantize/dequantize.rs:6-42): MSB-first codes, 00/01/11/10 ->
+ * c0/c1/c2/c3. */
+void orc_dequant_2bit(const uint8_t *packed, size_t n_bytes, const float *c, float *out) {
+    for (size_t i = 0; i < n_bytes; i++)
+        for (int j = 0; j < 4; j++) {
+            const int bits = (packed[i] >> ((3 - j) * 2)) & 3;
+            out[4 * i + j] = bits == 0 ? c[0] : bits == 1 ? c[1] : bits == 3 ? c[2] : c[3];
+        }
+}
+
 /* dot_product, x86 AVX2+FMA branch — src/compute/kernels/dot.rs:43-67. */
 float orc_dot_f32(const float *a, const float *b, size_t n) {
     __m256 acc = _mm256_setzero_ps();
@@ -473,12 +556,13 @@ void orc_attention(const float *q_rope, const float *k_cache, const float *v_cac
 
 /* A GenomicLinear as the oracle sees it (src/nn/linear/mod.rs:36-57). */
 typedef struct {
-    int kind;              /* 0 = GenomicF32, 1 = GenomicQ4_0, 2 = Genomic4Bit (LUT), 3 = GenomicQ8_0 */
+    int kind;              /* 0 = GenomicF32, 1 = GenomicQ4_0, 2 = Genomic4Bit (LUT), 3 = GenomicQ8_0,
+                              4 = Genomic2Bit */
     int64_t out_features;
     int64_t in_features;
     const uint8_t *db;     /* weight bytes as stored in the .flat blob */
     int64_t db_len;
-    const float *centroids; /* expanded LUT (init.rs:109-124), kind 2 only */
+    const float *centroids; /* expanded LUT / centroids (init.rs:109-139), kinds 2 and 4 */
     int64_t centroids_len;
     const float *bias;
     int64_t bias_len;
@@ -490,7 +574,8 @@ typedef struct {
 } orc_linear;
 
 /* GenomicLinear::compute_single_row — src/nn/linear/forward.rs:11-117
- * (block_size 32, modulation factors unused by the formats restated here). */
+ * (block_size 32; the modulation factors are 1: load_genomic sets no topology,
+ * flat_reader.rs:235). */
 static float compute_single_row(const orc_linear *L, int64_t i, const float *input, int64_t in_len) {
     const int64_t block_size = 32;
     int64_t n_blocks = L->in_features / block_size;
@@ -525,6 +610,17 @@ static float compute_single_row(const orc_linear *L, int64_t i, const float *inp
         else if (L->centroids_len >= 16) c = L->centroids;
         if (n_blocks > 0 && row_off + n_blocks * stride <= L->db_len && c)
             sum = orc_dot_4bit(L->db + row_off, input, c, (size_t)stride, (size_t)n_blocks);
+    } else if (L->kind == 4) {
+        /* forward.rs:33-57: the row's centroids, else the table's start (the
+         * dot then reads 4 floats per block from there) */
+        const int64_t stride = block_size / 4;
+        int64_t row_off = i * n_blocks * stride;
+        int64_t c_start = i * n_blocks * 4;
+        const float *c = NULL;
+        if (L->centroids_len >= c_start + n_blocks * 4) c = L->centroids + c_start;
+        else if (L->centroids_len >= 4) c = L->centroids;
+        if (n_blocks > 0 && row_off + n_blocks * stride <= L->db_len && c)
+            sum = orc_dot_2bit(L->db + row_off, input, c, (size_t)stride, (size_t)n_blocks, NULL);
     }
     if (L->n_anchors > 0) {
         int64_t a_s = L->anchor_row_ptrs[i], a_e = L->anchor_row_ptrs[i + 1];
@@ -556,7 +652,7 @@ float orc_linear_row(const orc_linear *L, int64_t i, const float *input, int64_t
 }
 
 /* GenomicLinear::get_row_core — src/nn/linear/forward.rs:195-285 for the
- * F32, Q4_0, Q8_0 and LUT-4bit variants (embedding lookup). */
+ * F32, Q4_0, Q8_0, LUT-4bit and 2-bit variants (embedding lookup). */
 void orc_linear_get_row(const orc_linear *L, int64_t idx, float *res) {
     int64_t K = L->in_features;
     for (int64_t t = 0; t < K; t++) res[t] = 0.0f;
@@ -590,6 +686,23 @@ void orc_linear_get_row(const orc_linear *L, int64_t idx, float *res) {
                     res[b * 32 + k * 2] = c[byte >> 4];
                     res[b * 32 + k * 2 + 1] = c[byte & 0x0F];
                 }
+            }
+        }
+    } else if (L->kind == 4) {
+        /* forward.rs:210-237: per block the row's own centroids if present,
+         * else the first four (a table of fewer than 4 floats is refused by
+         * the loader: the reference would index past it) */
+        int64_t off = safe * n_blocks * 8;
+        if (off + n_blocks * 8 <= L->db_len) {
+            static const float zeros[4] = {0};
+            for (int64_t b = 0; b < n_blocks; b++) {
+                int64_t c_off = (safe * n_blocks + b) * 4;
+                const float *c;
+                if (L->centroids_len == 4) c = L->centroids;
+                else if (c_off + 4 <= L->centroids_len) c = L->centroids + c_off;
+                else if (L->centroids_len > 0) c = L->centroids;
+                else c = zeros;
+                orc_dequant_2bit(L->db + off + b * 8, 8, c, res + b * 32);
             }
         }
     }

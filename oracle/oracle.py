@@ -52,7 +52,7 @@ _LIB = None
 Q4_0_BLOCK_BYTES = 20
 BLOCK_SIZE = 32  # hard-coded by load_genomic (flat_reader.rs:141)
 
-KIND_F32, KIND_Q4_0, KIND_LUT4, KIND_Q8_0 = 0, 1, 2, 3
+KIND_F32, KIND_Q4_0, KIND_LUT4, KIND_Q8_0, KIND_2BIT = 0, 1, 2, 3, 4
 Q8_0_BLOCK_BYTES = 34
 
 _fp = ctypes.POINTER(ctypes.c_float)
@@ -100,6 +100,11 @@ def lib():
         L.orc_dot_4bit.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                    ctypes.c_size_t, ctypes.c_size_t]
         L.orc_dot_4bit.restype = ctypes.c_float
+        for fn in ("orc_dot_2bit", "orc_dot_2bit_scalar"):
+            getattr(L, fn).argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                       ctypes.c_size_t, ctypes.c_size_t, ctypes.c_void_p]
+            getattr(L, fn).restype = ctypes.c_float
+        L.orc_dequant_2bit.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p]
         L.orc_dot_f32.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]
         L.orc_dot_f32.restype = ctypes.c_float
         L.orc_rms_norm.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_float,
@@ -221,6 +226,56 @@ def dot_4bit(codes: np.ndarray, x: np.ndarray, centroids: np.ndarray) -> float:
     return lib().orc_dot_4bit(_ptr(c), _ptr(_f32(x)), _ptr(t), 16, nb)
 
 
+def dot_2bit(codes: np.ndarray, x: np.ndarray, centroids: np.ndarray, modulation=None,
+             scalar: bool = False, stride: int = 8) -> float:
+    """genomic_dot_product over one row (genomic.rs:17-144): `stride` code bytes per
+    block, centroids read 4 per block from the row's base ([n_blocks][4]; a single
+    4-entry table is tiled first, as init.rs:125-139 expands it)."""
+    c = np.ascontiguousarray(codes, dtype=np.uint8).reshape(-1)
+    nb = c.size // stride
+    t = _f32(centroids)
+    if t.size == 4:
+        t = np.ascontiguousarray(np.tile(t, nb))
+    if t.size < nb * 4:
+        raise ValueError("dot_2bit needs 4 centroids per block")
+    m = _f32(modulation) if modulation is not None else None
+    fn = lib().orc_dot_2bit_scalar if scalar else lib().orc_dot_2bit
+    return fn(_ptr(c), _ptr(_f32(x)), _ptr(t), stride, nb, _ptr(m) if m is not None else None)
+
+
+def quantize_embedding(vector, thresholds=None) -> bytes:
+    """quantize_embedding (compute/quantize/python.rs:38-71): 2-bit codes, MSB first,
+    00 below t0, 01 below t1, 11 below t2, 10 otherwise."""
+    t = [-0.43, 0.0, 0.43] if thresholds is None else list(thresholds)
+    v = np.asarray(vector, dtype=np.float32)
+    out = bytearray()
+    for i in range(0, v.size, 4):
+        byte = 0
+        for j in range(4):
+            if i + j < v.size:
+                val = v[i + j]
+                bits = 0b00 if val < t[0] else 0b01 if val < t[1] else 0b11 if val < t[2] else 0b10
+                byte = ((byte << 2) | bits) & 0xFF
+        out.append(byte)
+    return bytes(out)
+
+
+def dequantize_embedding(packed, dims: int, centroids=None) -> np.ndarray:
+    """dequantize_embedding_core (compute/quantize/dequantize.rs:6-42), including its
+    per-dimension table form (4 centroids per dimension when len == dims * 4)."""
+    c = np.asarray([-0.68, -0.17, 0.17, 0.68] if centroids is None else centroids, dtype=np.float32)
+    multi = c.size == dims * 4
+    rec = []
+    for byte in bytes(packed):
+        for j in range(4):
+            if len(rec) >= dims:
+                break
+            bits = (byte >> ((3 - j) * 2)) & 3
+            slot = {0: 0, 1: 1, 3: 2, 2: 3}[bits]
+            rec.append(c[len(rec) * 4 + slot] if multi else c[slot])
+    return np.asarray(rec, dtype=np.float32)
+
+
 def dot_f32(a: np.ndarray, b: np.ndarray) -> float:
     a, b = _f32(a), _f32(b)
     return lib().orc_dot_f32(_ptr(a), _ptr(b), a.size)
@@ -256,7 +311,7 @@ def rope(vec: np.ndarray, heads: int, head_dim: int, rope_base: float, pos: int,
 # ----------------------------------------------------------------- modules ---
 
 class GenomicLinear:
-    """GenomicLinear restricted to the flat-file formats (F32, Q4_0, Q8_0, LUT-4bit)."""
+    """GenomicLinear restricted to the flat-file formats (F32, Q4_0, Q8_0, LUT-4bit, 2-bit)."""
 
     def __init__(self, database, anchors_u8, centroids, out_features, in_features, bias,
                  bit_depth):
@@ -273,13 +328,21 @@ class GenomicLinear:
         elif bit_depth == 8:
             self.kind = KIND_Q8_0
         else:
-            raise NotImplementedError(f"bit_depth {bit_depth} is outside the restated path")
-        # LUT expansion (init.rs:109-124)
+            self.kind = KIND_2BIT  # every other bit_depth is Genomic2Bit (init.rs:53)
+        # centroid expansion (init.rs:109-139)
         n_blocks = self.in_features // BLOCK_SIZE
         if bit_depth == 4 and centroids.size == 16:
             centroids = np.tile(centroids, self.out_features * n_blocks)
         elif bit_depth == 4 and n_blocks and centroids.size == n_blocks * 16:
             centroids = np.tile(centroids, self.out_features)
+        elif self.kind == KIND_2BIT and centroids.size == 4:
+            centroids = np.tile(centroids, self.out_features * n_blocks)
+        elif self.kind == KIND_2BIT and n_blocks and centroids.size == n_blocks * 4:
+            centroids = np.tile(centroids, self.out_features)
+        if self.kind == KIND_2BIT and 0 < centroids.size < max(4, n_blocks * 4):
+            # the reference's row dot would read past such a table (forward.rs:40-45
+            # hands the dot the table's start for rows without their own centroids)
+            raise ValueError(f"2-bit centroid table of {centroids.size} floats")
         self.centroids = np.ascontiguousarray(centroids)
         self._parse_anchors(bytes(anchors_u8) if anchors_u8 is not None else b"")
         self._c = _OrcLinear(self.kind, self.out_features, self.in_features, _ptr(self.db),
