@@ -49,12 +49,13 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def model_path(preset: str, seed: int, d: str, quant_embed: int = 0) -> str:
+def model_path(preset: str, seed: int, d: str, quant_embed: int = 0, body_format: int = 1) -> str:
     from gaje_hip import synth
-    path = os.path.join(d, f"gaje_{preset}_s{seed}{'_q8embed' if quant_embed else ''}.flat")
+    tag = ("_q8embed" if quant_embed else "") + ("_2bit" if body_format == synth.BIT2 else "")
+    path = os.path.join(d, f"gaje_{preset}_s{seed}{tag}.flat")
     if not os.path.exists(path):
         t = time.perf_counter()
-        synth.write_flat(path + ".tmp", preset=preset, seed=seed, quant_embed=quant_embed)
+        synth.write_flat(path + ".tmp", preset=preset, seed=seed, quant_embed=quant_embed, body_format=body_format)
         os.replace(path + ".tmp", path)
         log(f"[bench] wrote {path} ({os.path.getsize(path) / 1e9:.2f} GB) in {time.perf_counter() - t:.1f}s")
     return path
@@ -172,12 +173,14 @@ def c3_workloads(d: str, seed: int, prefill_tokens: int = 512, batch: int = 16, 
     return prefill, decode, [int(v) for v in out[0, :4]]
 
 
-def q8_decode_workload(d: str, seed: int, preset: str, prompt_len: int, gen: int, steps: int):
-    """Batch-1 greedy decode of the same shape with Q8_0 token_embd / lm_head (the --quant-embed
-    export): the lm_head matvec reads 34 B per 32 weights instead of 128."""
+def variant_decode_workload(d: str, seed: int, preset: str, prompt_len: int, gen: int, steps: int,
+                            quant_embed: int = 0, body_format: int = 1):
+    """Batch-1 greedy decode of the same shape in another format: Q8_0 token_embd / lm_head
+    (quant_embed=1, the --quant-embed export: the lm_head reads 34 B per 32 weights instead
+    of 128) or a 2-bit body (body_format=4, Genomic2Bit with per-block centroids)."""
     import gaje_hip
     from gaje_hip import ops
-    path = model_path(preset, seed, d, quant_embed=1)
+    path = model_path(preset, seed, d, quant_embed=quant_embed, body_format=body_format)
     g = gaje_hip.load_genomic_auto(path)
     g.set_k_wta_ratio(0.0)
     prompt = np.random.default_rng(seed).integers(0, g.vocab_size, prompt_len).astype(np.uint32)
@@ -197,14 +200,18 @@ def q8_decode_workload(d: str, seed: int, preset: str, prompt_len: int, gen: int
     ops.synchronize()
     el = time.perf_counter() - t0
     g.truncate_cache(prompt_len + gen - 1)
-    ms, nbytes = g.time_stage("lm_head", iters=200)
-    gbps = nbytes / (ms * 1e-3) / 1e9
+    stages = {}
+    for st in (("lm_head",) if quant_embed else ("qkv", "o", "gate_up", "down")):
+        ms, nbytes = g.time_stage(st, iters=200)
+        gbps = nbytes / (ms * 1e-3) / 1e9
+        stages[st] = dict(us=round(ms * 1e3, 3), bytes=int(nbytes), GBps=round(gbps, 1),
+                          frac=round(gbps / HBM_PEAK_GBPS, 4))
     g.close()
     out = dict(tok_s=round(gen * steps / el, 2), ms_per_token=round(el / (gen * steps) * 1e3, 4),
-               prompt=prompt_len, gen=gen, steps=steps,
-               lm_head=dict(kernel="gemv_kernel<Q8_0, ARGMAX>", us=round(ms * 1e3, 3), bytes=int(nbytes),
-                            GBps=round(gbps, 1), frac=round(gbps / HBM_PEAK_GBPS, 4)))
-    log(f"[bench] Q8_0 embed/lm_head decode: {out['tok_s']:.1f} tok/s; lm_head {ms * 1e3:.2f} us = {gbps:.0f} GB/s")
+               prompt=prompt_len, gen=gen, steps=steps, stages=stages)
+    what = "Q8_0 embed/lm_head" if quant_embed else "2-bit body"
+    log(f"[bench] {what} decode: {out['tok_s']:.1f} tok/s; " +
+        ", ".join(f"{k} {v['us']:.2f} us" for k, v in stages.items()))
     return out
 
 
@@ -255,6 +262,7 @@ def main():
                     help="skip the Qwen2-0.5B decode, its stages and the C0 matvec (profiling runs of the other workloads)")
     ap.add_argument("--no-moe", action="store_true", help="skip the MoE layer")
     ap.add_argument("--no-q8", action="store_true", help="skip the Q8_0 token_embd/lm_head decode")
+    ap.add_argument("--no-2bit", action="store_true", help="skip the 2-bit body decode")
     ap.add_argument("--gemv-only", action="store_true",
                     help="only the C0 Q4_0 matvec (cold) and a 256 MiB device copy, for counter runs")
     args = ap.parse_args()
@@ -342,8 +350,11 @@ def main():
         g.close()
     workloads = {}
     if not args.no_q8 and not args.no_decode:
-        workloads[f"{args.preset}_q8_0_embed_decode"] = q8_decode_workload(d, args.seed, args.preset, args.prompt,
-                                                                          args.gen, args.steps)
+        workloads[f"{args.preset}_q8_0_embed_decode"] = variant_decode_workload(
+            d, args.seed, args.preset, args.prompt, args.gen, args.steps, quant_embed=1)
+    if not args.no_2bit and not args.no_decode:
+        workloads[f"{args.preset}_2bit_body_decode"] = variant_decode_workload(
+            d, args.seed, args.preset, args.prompt, args.gen, args.steps, body_format=4)
     if not args.no_c3:
         prefill, decode, c3_tokens = c3_workloads(d, args.seed, ctx=args.c3_ctx, gen=args.c3_gen)
         workloads["qwen2.5-1.5b_prefill_512"] = prefill

@@ -578,8 +578,13 @@ __device__ __forceinline__ float row_lut4(const GemvParams &p, const float *xs, 
 // 16t..16t+7 to the first, 16t+8..16t+15 to the second), sums them lane by
 // lane and reduces ((a0+a4)+(a1+a5))+((a2+a6)+(a3+a7)); the row sum adds the
 // block values in block order and flushes |sum| < 1e-5.  Here lane s of the
-// row's 8 computes whole blocks s, s+8, ...; the row sum then takes the
-// eight block values of each round from the lanes in order.
+// row's LPR computes whole blocks s, s+LPR, ...; the row sum then takes the
+// LPR block values of each round from the lanes in order.
+
+// Lanes per row: rows of more than 8 blocks spread over 32 lanes (one round of
+// whole blocks per lane for K <= 1024), so few-row matvecs keep short lane
+// streams.
+inline int g2_lanes(int nb) { return nb > 8 ? 32 : 8; }
 
 // Code bits at `pos` (low bit) of `word` -> the selected centroid: two
 // sign-extended bit fields used as select masks (v_bfi).
@@ -591,13 +596,13 @@ __device__ __forceinline__ float g2_pick(uint32_t word, int pos, uint32_t c00, u
     return __uint_as_float((b1 & hi) | (~b1 & lo));
 }
 
-template <bool NT>
+template <bool NT, int LPR>
 __device__ __forceinline__ float row_g2(const GemvParams &p, const float *xs, int64_t row, int s, int base) {
     const int nb = p.nb;
     const uint8_t *rowp = p.w + (size_t)row * nb * 8;
     const float *crow = p.lut + (row < p.lut_rows_own ? (size_t)row * nb * 4 : 0);
     float sum = 0.0f;
-    for (int j0 = 0; j0 < nb; j0 += 8) {
+    for (int j0 = 0; j0 < nb; j0 += LPR) {
         const int j = j0 + s;
         float bv = 0.0f;
         if (j < nb) {
@@ -634,7 +639,7 @@ __device__ __forceinline__ float row_g2(const GemvParams &p, const float *xs, in
             for (int e = 0; e < 8; ++e) a[e] = acc0[e] + acc1[e];
             bv = ((a[0] + a[4]) + (a[1] + a[5])) + ((a[2] + a[6]) + (a[3] + a[7]));
         }
-        const int nv = nb - j0 < 8 ? nb - j0 : 8;  // uniform
+        const int nv = nb - j0 < LPR ? nb - j0 : LPR;  // uniform
         for (int t = 0; t < nv; ++t) sum = sum + shfl(bv, base + t);
     }
     return fabsf(sum) < 1e-5f ? 0.0f : sum;
@@ -950,7 +955,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
             if constexpr (FMT == FMT_Q4_0) v = q4_consume<NT, D>(p, xv, q.row, s, row_base, q4r);
             else if constexpr (FMT == FMT_Q8_0) v = q8_consume<NT, D>(p, xv, q.row, s, row_base, q8r);
             else if constexpr (FMT == FMT_F32) v = f32_consume<NT>(p, smem, q.row, s, row_base, f32r);
-            else if constexpr (FMT == FMT_G2) v = row_g2<NT>(p, smem, q.row, s, row_base);
+            else if constexpr (FMT == FMT_G2) v = row_g2<NT, LPR>(p, smem, q.row, s, row_base);
             else v = row_lut4<NT>(p, smem, q.row, s, row_base, tbl);
         }
         const float v1 = shfl(v, pair_base + LPR);  // r1's result (lane 0 of its group)
@@ -1583,8 +1588,9 @@ int launch_gemv(const GemvParams &p, hipStream_t s) {
         lpr = 4;
         fn = gemv_kernel<FMT_LUT4, 4, false, 1>;
     } else if (p.fmt == FMT_G2) {
-        lpr = 8;
-        fn = p.nontemporal ? gemv_kernel<FMT_G2, 8, true, 1> : gemv_kernel<FMT_G2, 8, false, 1>;
+        lpr = g2_lanes(p.nb);
+        if (lpr == 8) fn = p.nontemporal ? gemv_kernel<FMT_G2, 8, true, 1> : gemv_kernel<FMT_G2, 8, false, 1>;
+        else fn = p.nontemporal ? gemv_kernel<FMT_G2, 32, true, 1> : gemv_kernel<FMT_G2, 32, false, 1>;
     } else {
         lpr = 2;
         if (p.mode == MODE_ARGMAX && p.nontemporal) fn = gemv_kernel<FMT_F32, 2, true, 1, MODE_ARGMAX>;
