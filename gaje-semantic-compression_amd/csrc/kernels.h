@@ -243,7 +243,12 @@ struct PrefillAttnParams {
     int64_t cap, pos0, P;
     int32_t n_head, n_kv, head_dim;
     float *out;              // [P][n_head * head_dim]
+    float *ws;               // key-chunk partials: prefill_attn_ws_floats(P, n_head, head_dim) floats
 };
+// Keys are split into at most PREFILL_ATTN_CHUNKS chunks per query block,
+// each computed by its own workgroup and merged afterwards.
+constexpr int PREFILL_ATTN_CHUNKS = 8;
+int64_t prefill_attn_ws_floats(int64_t P, int64_t n_head, int64_t head_dim);
 int launch_prefill_attention(const PrefillAttnParams &p, hipStream_t s);
 
 // Batched decode: NV (<= 16) activation vectors per matvec, each product in

@@ -302,7 +302,7 @@ struct gaje_hip_model {
     struct Prefill {
         int64_t rows = 0;        // chunk rows the buffers hold
         int64_t part_floats = 0; // split-K partials they hold
-        float *H = nullptr, *QKV = nullptr, *Q = nullptr, *ATT = nullptr, *GU = nullptr, *part = nullptr;
+        float *H = nullptr, *QKV = nullptr, *Q = nullptr, *ATT = nullptr, *GU = nullptr, *part = nullptr, *aws = nullptr;
         uint16_t *xh = nullptr, *xl = nullptr;
         int *ex = nullptr;
         uint32_t *ids = nullptr;
@@ -998,7 +998,7 @@ int prefill_reserve(gaje_hip_model *m, int64_t rows) {
     part = std::max(part, f.part_floats);
     GAJE_HIP_CHECK(hipStreamSynchronize(m->stream));
     for (void *p : {(void *)f.H, (void *)f.QKV, (void *)f.Q, (void *)f.ATT, (void *)f.GU, (void *)f.part, (void *)f.xh,
-                    (void *)f.xl, (void *)f.ex, (void *)f.ids})
+                    (void *)f.xl, (void *)f.ex, (void *)f.ids, (void *)f.aws})
         if (p) m->release(p);
     f = gaje_hip_model::Prefill();
     const int64_t kmax = prefill_kmax(m);
@@ -1012,6 +1012,7 @@ int prefill_reserve(gaje_hip_model *m, int64_t rows) {
     GAJE_TRY(m->alloc(&f.ex, (size_t)rows));
     GAJE_TRY(m->alloc(&f.ids, (size_t)rows));
     GAJE_TRY(m->alloc(&f.part, (size_t)part));
+    GAJE_TRY(m->alloc(&f.aws, (size_t)prefill_attn_ws_floats(rows, m->n_head, m->hd)));
     f.rows = rows;
     f.part_floats = part;
     return GAJE_OK;
@@ -1109,6 +1110,7 @@ int prefill_layer(gaje_hip_model *m, int64_t l, int64_t pos, int64_t P) {
     ap.n_kv = (int32_t)m->n_kv;
     ap.head_dim = (int32_t)m->hd;
     ap.out = f.ATT;
+    ap.ws = f.aws;
     GAJE_TRY(launch_prefill_attention(ap, s));
 
     sp = prefill_split(m, f.ATT, m->q_rows, P, m->q_rows);
@@ -1168,7 +1170,7 @@ extern "C" int gaje_hip_prefill_mfma(gaje_hip_model *m, const uint32_t *ids, int
         ep.lut = m->embd.lut;
         ep.lut_rows_own = m->embd.lut_rows_own;
         ep.lut_block_stride = m->embd.lut_block_stride;
-    ep.lut_len = m->embd.lut_len;
+        ep.lut_len = m->embd.lut_len;
         ep.vocab = m->vocab_embd;
         ep.rows_valid = m->embd.rows_valid;
         ep.K = m->n_embd;
