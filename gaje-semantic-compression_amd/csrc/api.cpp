@@ -333,8 +333,7 @@ MoeWorkspace moe_workspace(char *base, int64_t T, int64_t h, int64_t ffn, int64_
     MoeWorkspace w{};
     const int64_t R = 2 * T, kmax = std::max(h, ffn);
     int64_t part = 0;
-    for (int64_t m = 1; m <= R; ++m)
-        part = std::max({part, plan_gemm_q4(m, 2 * ffn, h).part_floats, plan_gemm_q4(m, h, ffn).part_floats});
+    part = std::max(plan_gemm_q4_grouped(R, E, 2 * ffn, h).part_floats, plan_gemm_q4_grouped(R, E, h, ffn).part_floats);
     w.part_floats = part;
     size_t off = 0;
     auto take = [&](size_t bytes) {
@@ -388,10 +387,8 @@ extern "C" int gaje_hip_moe_ffn(const float *x, int64_t T, int64_t h, const floa
                          (long long)workspace_bytes, w.bytes);
     hipStream_t s = as_stream(stream);
     const int64_t R = 2 * T;
-    for (int64_t e = 0; e < n_expert; ++e) {
-        GAJE_TRY(launch_q4_row_exponents((const uint8_t *)gate_up[e], 2 * ffn, h, w.ew_gu + e * 2 * ffn, s));
-        GAJE_TRY(launch_q4_row_exponents((const uint8_t *)down[e], h, ffn, w.ew_dn + e * h, s));
-    }
+    GAJE_TRY(launch_q4_row_exponents_batch((const uint8_t *const *)gate_up, (int)n_expert, 2 * ffn, h, w.ew_gu, s));
+    GAJE_TRY(launch_q4_row_exponents_batch((const uint8_t *const *)down, (int)n_expert, h, ffn, w.ew_dn, s));
     MoeParams mp{};
     mp.x = x;
     mp.ldx = h;
@@ -408,10 +405,6 @@ extern "C" int gaje_hip_moe_ffn(const float *x, int64_t T, int64_t h, const floa
     mp.y = y;
     mp.ldy = h;
     GAJE_TRY(launch_moe_route(mp, s));
-    int32_t counts[MOE_MAX_EXPERTS], offsets[MOE_MAX_EXPERTS];
-    GAJE_HIP_CHECK(hipMemcpyAsync(counts, w.counts, (size_t)n_expert * 4, hipMemcpyDeviceToHost, s));
-    GAJE_HIP_CHECK(hipMemcpyAsync(offsets, w.offsets, (size_t)n_expert * 4, hipMemcpyDeviceToHost, s));
-    GAJE_HIP_CHECK(hipStreamSynchronize(s));
 
     // gate_up of every expert over its gathered tokens
     SplitParams sp{};
@@ -425,24 +418,31 @@ extern "C" int gaje_hip_moe_ffn(const float *x, int64_t T, int64_t h, const floa
     sp.K = h;
     sp.rows = w.rows;
     GAJE_TRY(launch_split_rows(sp, s));
-    auto gemm = [&](const void *wt, const int *ew, int64_t m0, int64_t M, int64_t N, int64_t K, float *Y) {
+    // one grouped launch per product: every expert's rows (counts and offsets
+    // stay on the device; an expert holds at most T rows)
+    auto gemm = [&](const void *const *wt, const int *ew, int64_t N, int64_t K, float *Y) {
         GemmQ4Params p{};
-        p.w = (const uint8_t *)wt;
-        p.ew = ew;
-        p.xh = w.xh + m0 * K;
-        p.xl = w.xl + m0 * K;
-        p.ex = w.ex + m0;
+        p.xh = w.xh;
+        p.xl = w.xl;
+        p.ex = w.ex;
         p.ldh = K;
-        p.y = Y + m0 * N;
+        p.y = Y;
         p.ldy = N;
         p.part = w.part;
-        p.M = M;
+        p.M = R;
         p.N = N;
         p.nb = (int32_t)(K / 32);
-        return launch_gemm_q4(p, plan_gemm_q4(M, N, K), s);
+        p.g_counts = w.counts;
+        p.g_offsets = w.offsets;
+        p.g_groups = (int32_t)n_expert;
+        p.g_mtiles = (int32_t)((T + 127) / 128);
+        for (int64_t e = 0; e < n_expert; ++e) {
+            p.gw[e] = (const uint8_t *)wt[e];
+            p.gew[e] = ew + e * N;
+        }
+        return launch_gemm_q4(p, plan_gemm_q4_grouped(R, n_expert, N, K), s);
     };
-    for (int64_t e = 0; e < n_expert; ++e)
-        if (counts[e] > 0) GAJE_TRY(gemm(gate_up[e], w.ew_gu + e * 2 * ffn, offsets[e], counts[e], 2 * ffn, h, w.GU));
+    GAJE_TRY(gemm(gate_up, w.ew_gu, 2 * ffn, h, w.GU));
     // swiglu of every dispatched row, then down
     sp = SplitParams{};
     sp.x = w.GU;
@@ -457,8 +457,7 @@ extern "C" int gaje_hip_moe_ffn(const float *x, int64_t T, int64_t h, const floa
     sp.K = ffn;
     sp.st_a = sp.st_b = -1;
     GAJE_TRY(launch_split_rows(sp, s));
-    for (int64_t e = 0; e < n_expert; ++e)
-        if (counts[e] > 0) GAJE_TRY(gemm(down[e], w.ew_dn + e * h, offsets[e], counts[e], h, ffn, w.Y));
+    GAJE_TRY(gemm(down, w.ew_dn, h, ffn, w.Y));
     GAJE_TRY(launch_moe_combine(mp, w.Y, s));
     if (top_idx) GAJE_HIP_CHECK(hipMemcpyAsync(top_idx, w.top_idx, (size_t)R * 4, hipMemcpyDeviceToDevice, s));
     if (top_w) GAJE_HIP_CHECK(hipMemcpyAsync(top_w, w.top_w, (size_t)R * 4, hipMemcpyDeviceToDevice, s));

@@ -55,7 +55,17 @@ __device__ __forceinline__ int split_exponent(float maxabs) {
 // Per weight row: the exponent of its largest |d| = max(|min|, |fma(15, scale, min)|)
 // over its blocks (d is affine in the code, so the extremes are codes 0 and 15).
 // One wave per row.
-__global__ __launch_bounds__(256) void q4_row_exp_kernel(const uint8_t *w, int64_t N, int nb, int *ew) {
+struct RowExpBatch {
+    const uint8_t *w[MOE_MAX_EXPERTS];
+};
+
+// blockIdx.y selects the matrix of a batch (w = b.w[y], ew advanced by y*N).
+__global__ __launch_bounds__(256) void q4_row_exp_kernel(const uint8_t *w, int64_t N, int nb, int *ew,
+                                                         RowExpBatch b) {
+    if (gridDim.y > 1) {
+        w = b.w[blockIdx.y];
+        ew += (int64_t)blockIdx.y * N;
+    }
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= N) return;
     const int lane = threadIdx.x & 63;
@@ -189,7 +199,20 @@ __global__ __launch_bounds__(MT * 2) void gemm_q4_mfma_kernel(GemmQ4Params p) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
-    const int64_t m0 = (int64_t)blockIdx.y * MT, n0 = (int64_t)blockIdx.x * GM_NT;
+    const int64_t n0 = (int64_t)blockIdx.x * GM_NT;
+    // rows [m0, m_end) of the planes and of y, and the weights they multiply
+    int64_t m0 = (int64_t)blockIdx.y * MT, m_end = p.M;
+    const uint8_t *W = p.w;
+    const int *EW = p.ew;
+    if (p.g_counts) {  // grouped: tile `mt` of expert e (uniform)
+        const int e = (int)blockIdx.y / p.g_mtiles, mt = (int)blockIdx.y - e * p.g_mtiles;
+        const int64_t cnt = p.g_counts[e];
+        if ((int64_t)mt * MT >= cnt) return;
+        m0 = p.g_offsets[e] + (int64_t)mt * MT;
+        m_end = p.g_offsets[e] + cnt;
+        W = p.gw[e];
+        EW = p.gew[e];
+    }
     const int z = blockIdx.z;
     const int b0 = z * p.kb_per;
     const int b1 = min(p.nb, b0 + p.kb_per);
@@ -198,15 +221,15 @@ __global__ __launch_bounds__(MT * 2) void gemm_q4_mfma_kernel(GemmQ4Params p) {
     // activation staging: row ar, 16 halves at column 16*ah of each plane
     const int ar = tid >> 1, ah = tid & 1;
     int64_t am = m0 + ar;
-    if (am >= p.M) am = p.M - 1;
+    if (am >= m_end) am = m_end - 1;
     const _Float16 *xhp = (const _Float16 *)p.xh + am * p.ldh + 16 * ah;
     const _Float16 *xlp = (const _Float16 *)p.xl + am * p.ldh + 16 * ah;
     // weight staging: row br, chunks c = bq*CPT .. of each block
     const int br = tid / TPR, bq = tid % TPR;
     int64_t bn = n0 + br;
     if (bn >= p.N) bn = p.N - 1;
-    const uint8_t *wrow = p.w + (size_t)bn * G * 80;
-    const float wsc = ldexpf(1.0f, p.ew[bn]);
+    const uint8_t *wrow = W + (size_t)bn * G * 80;
+    const float wsc = ldexpf(1.0f, EW[bn]);
 
     f4 acc[4][4];
 #pragma unroll
@@ -316,14 +339,14 @@ __global__ __launch_bounds__(MT * 2) void gemm_q4_mfma_kernel(GemmQ4Params p) {
     for (int j = 0; j < 4; ++j) {
         const int64_t n = n0 + wn * 64 + 16 * j + fr;
         if (n >= p.N) continue;
-        const int en = p.ew[n];
+        const int en = EW[n];
         const float bias = (!p.part && n < p.bias_len) ? p.bias[n] : 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int64_t m = m0 + wm * 64 + 16 * i + 4 * (lane >> 4) + r;
-                if (m >= p.M) continue;
+                if (m >= m_end) continue;
                 float v = ldexpf(acc[i][j][r], -(p.ex[m] + en));
                 if (p.part) {
                     p.part[((int64_t)z * p.M + m) * p.N + n] = v;
@@ -368,7 +391,23 @@ size_t gemm_lds() { return (size_t)(4 * MT * GM_ROW + 4 * GM_NT * GM_ROW) * size
 
 int launch_q4_row_exponents(const uint8_t *packed, int64_t N, int64_t K, int *ew, hipStream_t s) {
     if (!packed || !ew || N <= 0 || K <= 0 || K % 32) return set_error(GAJE_ERR_INVALID_ARG, "row exponents: bad arguments");
-    hipLaunchKernelGGL(q4_row_exp_kernel, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, s, packed, N, (int)(K / 32), ew);
+    hipLaunchKernelGGL(q4_row_exp_kernel, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, s, packed, N, (int)(K / 32), ew,
+                       RowExpBatch{});
+    GAJE_HIP_CHECK(hipGetLastError());
+    return GAJE_OK;
+}
+
+int launch_q4_row_exponents_batch(const uint8_t *const *packed, int n, int64_t N, int64_t K, int *ew, hipStream_t s) {
+    if (!packed || !ew || n <= 0 || n > MOE_MAX_EXPERTS || N <= 0 || K <= 0 || K % 32)
+        return set_error(GAJE_ERR_INVALID_ARG, "row exponents: bad arguments");
+    if (n == 1) return launch_q4_row_exponents(packed[0], N, K, ew, s);
+    RowExpBatch b{};
+    for (int i = 0; i < n; ++i) {
+        if (!packed[i]) return set_error(GAJE_ERR_INVALID_ARG, "row exponents: matrix %d is null", i);
+        b.w[i] = packed[i];
+    }
+    hipLaunchKernelGGL(q4_row_exp_kernel, dim3((unsigned)((N + 3) / 4), (unsigned)n), dim3(256), 0, s, packed[0], N,
+                       (int)(K / 32), ew, b);
     GAJE_HIP_CHECK(hipGetLastError());
     return GAJE_OK;
 }
@@ -405,16 +444,41 @@ GemmPlan plan_gemm_q4(int64_t M, int64_t N, int64_t K) {
     return pl;
 }
 
+GemmPlan plan_gemm_q4_grouped(int64_t R, int64_t E, int64_t N, int64_t K) {
+    GemmPlan pl{};
+    pl.mt = 128;
+    // tiles that hold rows: at most R/128 full ones plus one partial per group
+    const int64_t tiles = ((R + 127) / 128 + E) * ((N + GM_NT - 1) / GM_NT);
+    const int64_t nb = K / 32;
+    const int64_t cu = device_cu_count();
+    int64_t S = 1;
+    if (tiles < cu) S = (cu + tiles - 1) / tiles;
+    int64_t kb = (nb + S - 1) / S;
+    if (kb < 8) kb = 8;
+    kb = (kb + 3) / 4 * 4;
+    pl.kb_per = (int)kb;
+    pl.splits = (int)((nb + kb - 1) / kb);
+    pl.part_floats = pl.splits > 1 ? pl.splits * R * N : 0;
+    return pl;
+}
+
 int launch_gemm_q4(const GemmQ4Params &p0, const GemmPlan &pl, hipStream_t s) {
     GemmQ4Params p = p0;
-    if (p.M < 0 || p.N <= 0 || p.nb <= 0 || !p.w || !p.ew || (p.M > 0 && (!p.xh || !p.xl || !p.ex || !p.y)))
+    const bool grouped = p.g_counts != nullptr;
+    if (p.M < 0 || p.N <= 0 || p.nb <= 0 || (!grouped && (!p.w || !p.ew)) ||
+        (grouped && (!p.g_offsets || p.g_groups <= 0 || p.g_groups > MOE_MAX_EXPERTS || p.g_mtiles <= 0 || pl.mt != 128)) ||
+        (p.M > 0 && (!p.xh || !p.xl || !p.ex || !p.y)))
         return set_error(GAJE_ERR_INVALID_ARG, "q4 gemm: bad arguments");
+    if (grouped)
+        for (int e = 0; e < p.g_groups; ++e)
+            if (!p.gw[e] || !p.gew[e]) return set_error(GAJE_ERR_INVALID_ARG, "q4 gemm: group %d has no weights", e);
     if (p.M == 0) return GAJE_OK;
     if (pl.kb_per % 4 || pl.kb_per <= 0 || (int64_t)pl.splits * pl.kb_per < p.nb || (pl.splits > 1 && !p.part))
         return set_error(GAJE_ERR_INVALID_ARG, "q4 gemm: bad plan");
     p.kb_per = pl.kb_per;
     if (pl.splits == 1) p.part = nullptr;
-    const dim3 grid((unsigned)((p.N + GM_NT - 1) / GM_NT), (unsigned)((p.M + pl.mt - 1) / pl.mt), (unsigned)pl.splits);
+    const unsigned gy = grouped ? (unsigned)(p.g_groups * p.g_mtiles) : (unsigned)((p.M + pl.mt - 1) / pl.mt);
+    const dim3 grid((unsigned)((p.N + GM_NT - 1) / GM_NT), gy, (unsigned)pl.splits);
     if (pl.mt == 256) {
         if (gemm_lds<256>() + 1024 > max_lds_per_block()) return set_error(GAJE_ERR_UNSUPPORTED, "q4 gemm: LDS");
         hipLaunchKernelGGL(gemm_q4_mfma_kernel<256>, grid, dim3(512), gemm_lds<256>(), s, p);

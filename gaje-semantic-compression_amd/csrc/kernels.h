@@ -188,10 +188,15 @@ struct SplitParams {
 int launch_split_rows(const SplitParams &p, hipStream_t s);
 // Per packed Q4_0 row: the exponent that scales its largest |d| into [2^14, 2^15).
 int launch_q4_row_exponents(const uint8_t *packed, int64_t N, int64_t K, int *ew, hipStream_t s);
+// The same for n matrices of one shape in one launch: ew[i*N .. ] for packed[i].
+int launch_q4_row_exponents_batch(const uint8_t *const *packed, int n, int64_t N, int64_t K, int *ew, hipStream_t s);
 
 // Y = X W^T over packed Q4_0 rows on the MFMA units (f16 hi/lo operand pairs,
 // fp32 accumulation): per row, the dot flushed like the reference's, + bias,
 // + residual.
+// Experts of one MoE layer (and of a grouped matrix product).
+constexpr int MOE_MAX_EXPERTS = 16;
+
 struct GemmQ4Params {
     const uint8_t *w;        // packed rows (launch_pack_q4_0)
     const int *ew;           // [N] weight row exponents
@@ -211,6 +216,14 @@ struct GemmQ4Params {
     DevState *st;            // NaN guards (or null): st_a on the row result,
     int32_t layer;           // st_b after the residual add
     int32_t st_a, st_b;
+    // grouped products (one launch for every expert): with g_counts set,
+    // blockIdx.y = e * g_mtiles + tile, expert e owns rows [g_offsets[e],
+    // g_offsets[e] + g_counts[e]) of the planes and of y (M = all rows) and
+    // multiplies them by gw[e] (row exponents gew[e])
+    const int32_t *g_counts, *g_offsets;
+    int32_t g_groups, g_mtiles;
+    const uint8_t *gw[MOE_MAX_EXPERTS];
+    const int *gew[MOE_MAX_EXPERTS];
 };
 struct GemmPlan {
     int mt;                  // activation rows per workgroup (128 or 256)
@@ -219,6 +232,8 @@ struct GemmPlan {
     int64_t part_floats;     // partial buffer the splits need (0 if one split)
 };
 GemmPlan plan_gemm_q4(int64_t M, int64_t N, int64_t K);
+// Grouped plan: 128-row tiles, splits sized for R rows spread over E groups.
+GemmPlan plan_gemm_q4_grouped(int64_t R, int64_t E, int64_t N, int64_t K);
 int launch_gemm_q4(const GemmQ4Params &p, const GemmPlan &plan, hipStream_t s);
 
 // Prompt prefill: RoPE + KV append for P tokens at positions pos0.. of one layer.
@@ -311,7 +326,6 @@ int launch_batch_begin(const BatchState &b, const uint32_t *ids, int64_t n, int6
 int launch_batch_end(const BatchState &b, uint32_t *out, int64_t n, int64_t i, int greedy, hipStream_t s);
 
 // Mixture-of-experts FFN (top-2 routing over Q4_0 SwiGLU experts).
-constexpr int MOE_MAX_EXPERTS = 16;
 struct MoeParams {
     const float *x;          // [T][ldx] token activations
     int64_t ldx, T, h;
