@@ -186,15 +186,18 @@ __global__ __launch_bounds__(256) void split_rows_kernel(SplitParams p) {
 
 __device__ __forceinline__ uint32_t word_of(const vu4 (&wq)[4], int j) { return wq[j >> 2][j & 3]; }
 
-template <int MT>
-__global__ __launch_bounds__(MT * 2) void gemm_q4_mfma_kernel(GemmQ4Params p) {
+// GA (global activations): each wave reads its activation fragments straight
+// from the planes (one block ahead, in registers) and LDS holds the weight
+// tiles only, so two workgroups share a compute unit.
+template <int MT, bool GA>
+__global__ __launch_bounds__(MT * 2, GA ? 2 : 1) void gemm_q4_mfma_kernel(GemmQ4Params p) {
     constexpr int NTH = MT * 2;
     constexpr int TPR = NTH / GM_NT;  // staging threads per weight row: 2 or 4
     constexpr int CPT = 4 / TPR;      // 8-element chunks of a block per staging thread
-    constexpr int APL = MT * GM_ROW;  // halves per activation plane
+    constexpr int APL = GA ? 0 : MT * GM_ROW;  // halves per activation plane in LDS
     constexpr int BPL = GM_NT * GM_ROW;
     extern __shared__ __align__(16) _Float16 lds[];
-    _Float16 *As = lds;                // [buf][plane][MT][GM_ROW]
+    _Float16 *As = lds;                // [buf][plane][MT][GM_ROW] (not GA)
     _Float16 *Bs = lds + 4 * APL;      // [buf][plane][GM_NT][GM_ROW]
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -257,15 +260,40 @@ __global__ __launch_bounds__(MT * 2) void gemm_q4_mfma_kernel(GemmQ4Params p) {
 
     const int g0 = b0 >> 2;  // b0 is a multiple of 4
     const int g1 = (b1 + 3) >> 2;
-    load_w(g0, wq[0], ws[0]);
-    load_x(b0, xa[0]);
-    load_x(b0 + 1, xa[1]);
-    load_w(g0 + 1, wq[1], ws[1]);
-
     const int fr = lane & 15, fk = 8 * (lane >> 4);
+    // GA: fragment rows of this wave (clamped into the tile's rows, as 32-bit
+    // half offsets from the planes)
+    uint32_t fo[4];
+    h8 fa[1][2][4];  // [plane][i] of the next block
+    if constexpr (GA) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            int64_t r = m0 + wm * 64 + 16 * i + fr;
+            if (r >= m_end) r = m_end - 1;
+            fo[i] = (uint32_t)(r * p.ldh + fk);
+        }
+    }
+    const _Float16 *xhb = (const _Float16 *)p.xh, *xlb = (const _Float16 *)p.xl;
+    auto load_frag = [&](int b, h8 (&hi)[4], h8 (&lo)[4]) {
+        const uint32_t bo = 32u * (uint32_t)(b < b1 ? b : b1 - 1);  // clamped, so every load is in bounds
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            hi[i] = *(const h8 *)(xhb + fo[i] + bo);
+            lo[i] = *(const h8 *)(xlb + fo[i] + bo);
+        }
+    };
+    load_w(g0, wq[0], ws[0]);
+    if constexpr (GA) {
+        load_frag(b0, fa[0][0], fa[0][1]);
+    } else {
+        load_x(b0, xa[0]);
+        load_x(b0 + 1, xa[1]);
+    }
+    if constexpr (!GA) load_w(g0 + 1, wq[1], ws[1]);
+
     int buf = 0;
     for (int g = g0; g < g1; ++g) {
-        const int wi = (g - g0) & 1;
+        const int wi = GA ? 0 : (g - g0) & 1;  // GA: one weight group in flight (registers)
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             // Every group runs all four blocks, branch-free (a branch here makes
@@ -277,11 +305,13 @@ __global__ __launch_bounds__(MT * 2) void gemm_q4_mfma_kernel(GemmQ4Params p) {
             const uint32_t live = b < b1 ? 0xFFFFFFFFu : 0u;
             // stage block b into LDS buffer buf
             {
-                _Float16 *ad = As + buf * 2 * APL + ar * GM_ROW + 16 * ah;
-                *(vu4 *)ad = xa[xi][0] & live;
-                *(vu4 *)(ad + 8) = xa[xi][1] & live;
-                *(vu4 *)(ad + APL) = xa[xi][2] & live;
-                *(vu4 *)(ad + APL + 8) = xa[xi][3] & live;
+                if constexpr (!GA) {
+                    _Float16 *ad = As + buf * 2 * APL + ar * GM_ROW + 16 * ah;
+                    *(vu4 *)ad = xa[xi][0] & live;
+                    *(vu4 *)(ad + 8) = xa[xi][1] & live;
+                    *(vu4 *)(ad + APL) = xa[xi][2] & live;
+                    *(vu4 *)(ad + APL + 8) = xa[xi][3] & live;
+                }
                 const uint32_t smw = ws[wi][u];
                 const float s = half_lo(smw), mn = half_hi(smw);
                 const int hb = u >> 1;
@@ -303,32 +333,56 @@ __global__ __launch_bounds__(MT * 2) void gemm_q4_mfma_kernel(GemmQ4Params p) {
                 }
             }
             // refill: activations two blocks ahead; the next-but-one weight group
-            load_x(b + 2, xa[xi]);
-            if (u == 3) load_w(g + 2, wq[wi], ws[wi]);
+            if constexpr (!GA) load_x(b + 2, xa[xi]);
+            if (u == 3) load_w(GA ? g + 1 : g + 2, wq[wi], ws[wi]);
             lds_barrier();
-            // 4 x 4 tiles x 3 products from buffer buf
-            const _Float16 *Ab = As + buf * 2 * APL + (wm * 64 + fr) * GM_ROW + fk;
+            // 4 x 4 tiles x 3 products from buffer buf; every accumulator takes
+            // hi*hi, hi*lo, lo*hi in that order
             const _Float16 *Bb = Bs + buf * 2 * BPL + (wn * 64 + fr) * GM_ROW + fk;
-            h8 ahi[4], alo[4], bhi[4], blo[4];
+            if constexpr (GA) {
+                // weights column tile by column tile, so two fragments are live.
+                // No activation mask: a split ends on a group boundary, and the
+                // blocks past nb in the row's last group have zero codes, scales
+                // and mins, so their products with the (clamped, finite)
+                // activations are zero.
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                ahi[i] = *(const h8 *)(Ab + 16 * i * GM_ROW);
-                alo[i] = *(const h8 *)(Ab + 16 * i * GM_ROW + APL);
-                bhi[i] = *(const h8 *)(Bb + 16 * i * GM_ROW);
-                blo[i] = *(const h8 *)(Bb + 16 * i * GM_ROW + BPL);
+                for (int j = 0; j < 4; ++j) {
+                    const h8 bh = *(const h8 *)(Bb + 16 * j * GM_ROW);
+                    const h8 bl = *(const h8 *)(Bb + 16 * j * GM_ROW + BPL);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[0][0][i], bh, acc[i][j], 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[0][0][i], bl, acc[i][j], 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[0][1][i], bh, acc[i][j], 0, 0, 0);
+                }
+                load_frag(b + 1, fa[0][0], fa[0][1]);  // lands while block b+1's weights are staged
+            } else {
+                const _Float16 *Ab = As + buf * 2 * APL + (wm * 64 + fr) * GM_ROW + fk;
+                h8 ahi[4], alo[4], bhi[4], blo[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    ahi[i] = *(const h8 *)(Ab + 16 * i * GM_ROW);
+                    alo[i] = *(const h8 *)(Ab + 16 * i * GM_ROW + APL);
+                    bhi[i] = *(const h8 *)(Bb + 16 * i * GM_ROW);
+                    blo[i] = *(const h8 *)(Bb + 16 * i * GM_ROW + BPL);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[i], bhi[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[i], blo[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[i], bhi[j], acc[i][j], 0, 0, 0);
             }
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[i], bhi[j], acc[i][j], 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[i], blo[j], acc[i][j], 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[i], bhi[j], acc[i][j], 0, 0, 0);
             buf ^= 1;
         }
     }
@@ -384,8 +438,8 @@ __global__ void gemm_reduce_kernel(GemmQ4Params p, int S) {
     }
 }
 
-template <int MT>
-size_t gemm_lds() { return (size_t)(4 * MT * GM_ROW + 4 * GM_NT * GM_ROW) * sizeof(_Float16); }
+template <int MT, bool GA>
+size_t gemm_lds() { return (size_t)((GA ? 0 : 4 * MT * GM_ROW) + 4 * GM_NT * GM_ROW) * sizeof(_Float16); }
 
 }  // namespace
 
@@ -426,6 +480,9 @@ int launch_split_rows(const SplitParams &p, hipStream_t s) {
     GAJE_HIP_CHECK(hipGetLastError());
     return GAJE_OK;
 }
+
+// The 128-row product reads its activation fragments from global memory.
+constexpr bool GEMM_GA = true;
 
 GemmPlan plan_gemm_q4(int64_t M, int64_t N, int64_t K) {
     GemmPlan pl{};
@@ -480,10 +537,12 @@ int launch_gemm_q4(const GemmQ4Params &p0, const GemmPlan &pl, hipStream_t s) {
     const unsigned gy = grouped ? (unsigned)(p.g_groups * p.g_mtiles) : (unsigned)((p.M + pl.mt - 1) / pl.mt);
     const dim3 grid((unsigned)((p.N + GM_NT - 1) / GM_NT), gy, (unsigned)pl.splits);
     if (pl.mt == 256) {
-        if (gemm_lds<256>() + 1024 > max_lds_per_block()) return set_error(GAJE_ERR_UNSUPPORTED, "q4 gemm: LDS");
-        hipLaunchKernelGGL(gemm_q4_mfma_kernel<256>, grid, dim3(512), gemm_lds<256>(), s, p);
+        const size_t lds = gemm_lds<256, false>();
+        if (lds + 1024 > max_lds_per_block()) return set_error(GAJE_ERR_UNSUPPORTED, "q4 gemm: LDS");
+        hipLaunchKernelGGL((gemm_q4_mfma_kernel<256, false>), grid, dim3(512), lds, s, p);
     } else {
-        hipLaunchKernelGGL(gemm_q4_mfma_kernel<128>, grid, dim3(256), gemm_lds<128>(), s, p);
+        const size_t lds = gemm_lds<128, GEMM_GA>();
+        hipLaunchKernelGGL((gemm_q4_mfma_kernel<128, GEMM_GA>), grid, dim3(256), lds, s, p);
     }
     GAJE_HIP_CHECK(hipGetLastError());
     if (pl.splits > 1) {
