@@ -21,20 +21,34 @@
 namespace gaje {
 namespace {
 
-// One workgroup per token, one wave per expert: lanes 0..7 run the eight FMA
-// chains of dot_product over the 8-float chunks, then
+// One workgroup per token, one wave per expert: the token's activations are
+// staged in LDS by the whole workgroup, then lanes 0..7 of each expert's wave
+// run the eight FMA chains of dot_product over the 8-float chunks (router
+// weights read in batches of 8 chunks ahead of the FMAs), then
 // ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7)) and the scalar tail.  Thread 0 then
 // forms the softmax, the top-2 and the renormalised weights.
 __global__ __launch_bounds__(64 * MOE_MAX_EXPERTS) void moe_route_kernel(MoeParams p) {
+    extern __shared__ __align__(16) float xs[];
     __shared__ float logit[MOE_MAX_EXPERTS];
     const int64_t t = blockIdx.x;
     const int tid = threadIdx.x, lane = tid & 63, e = tid >> 6;
-    const float *x = p.x + t * p.ldx;
+    const float *xg = p.x + t * p.ldx;
+    for (int64_t k = tid; k < p.h; k += 64 * MOE_MAX_EXPERTS) xs[k] = xg[k];
+    __syncthreads();
+    const float *x = xs;
     if (e < p.n_expert && lane < 8) {
         const float *w = p.router + (size_t)e * p.h;
         float a = 0.0f;
         const int64_t chunks = p.h / 8;
-        for (int64_t c = 0; c < chunks; ++c) a = fmaf(x[8 * c + lane], w[8 * c + lane], a);
+        int64_t c = 0;
+        for (; c + 8 <= chunks; c += 8) {
+            float wv[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) wv[u] = w[8 * (c + u) + lane];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) a = fmaf(x[8 * (c + u) + lane], wv[u], a);
+        }
+        for (; c < chunks; ++c) a = fmaf(x[8 * c + lane], w[8 * c + lane], a);
         const float a4 = __shfl(a, (lane + 4) & 7, 8);
         const float u = a + a4;                          // lane l<4: a_l + a_{l+4}
         const float u1 = __shfl(u, (lane + 1) & 7, 8);   // lane 0: u1, lane 2: u3
@@ -74,46 +88,67 @@ __global__ __launch_bounds__(64 * MOE_MAX_EXPERTS) void moe_route_kernel(MoePara
     p.top_w[2 * t + 1] = pb / den;
 }
 
-// Dispatch plan (one workgroup): for each expert, its tokens in token order
-// (an exclusive scan of the routing flags); rows[] holds the token of every
-// dispatched row (experts concatenated in id order), slot[t][k] the row of
-// token t's k-th expert, counts/offsets per expert.
+// Dispatch plan (one workgroup): for each expert, its tokens in token order;
+// rows[] holds the token of every dispatched row (experts concatenated in id
+// order), slot[t][k] the row of token t's k-th expert, counts/offsets per
+// expert.  Chunks of 1024 tokens; within a chunk an expert's rank of a token
+// is the ballot of its wave's flags below the lane plus the counts of the
+// earlier waves.  A first pass counts, a second assigns the rows.
 __global__ __launch_bounds__(1024) void moe_plan_kernel(MoeParams p) {
-    __shared__ int scan[1024];
-    __shared__ int base_s;
-    const int tid = threadIdx.x;
-    if (tid == 0) base_s = 0;
+    constexpr int NW = 1024 / 64;
+    __shared__ int wcnt[NW][MOE_MAX_EXPERTS];
+    __shared__ int run[MOE_MAX_EXPERTS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int E = p.n_expert;
+    const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
+    if (tid < MOE_MAX_EXPERTS) run[tid] = 0;
     __syncthreads();
-    for (int e = 0; e < p.n_expert; ++e) {
-        const int start = base_s;
+    for (int pass = 0; pass < 2; ++pass) {
+        if (pass == 1) {  // offsets from the counts: experts in id order
+            if (tid == 0) {
+                int o = 0;
+                for (int e = 0; e < E; ++e) {
+                    const int c = run[e];
+                    p.counts[e] = c;
+                    p.offsets[e] = o;
+                    run[e] = o;
+                    o += c;
+                }
+            }
+            __syncthreads();
+        }
         for (int64_t t0 = 0; t0 < p.T; t0 += 1024) {
             const int64_t t = t0 + tid;
-            int k = -1;
-            if (t < p.T) k = p.top_idx[2 * t] == e ? 0 : p.top_idx[2 * t + 1] == e ? 1 : -1;
-            const int f = k >= 0;
-            scan[tid] = f;
-            __syncthreads();
-            for (int o = 1; o < 1024; o <<= 1) {  // inclusive Hillis-Steele scan
-                const int v = tid >= o ? scan[tid - o] : 0;
-                __syncthreads();
-                scan[tid] += v;
-                __syncthreads();
-            }
-            const int run = base_s;
-            if (f) {
-                const int r = run + scan[tid] - 1;
-                p.rows[r] = (int32_t)t;
-                p.slot[2 * t + k] = r;
+            const int ea = t < p.T ? p.top_idx[2 * t] : -1, eb = t < p.T ? p.top_idx[2 * t + 1] : -1;
+            int pre_a = 0, pre_b = 0;
+            for (int e = 0; e < E; ++e) {
+                const uint64_t m = __ballot(ea == e || eb == e);
+                if (lane == 0) wcnt[wave][e] = __popcll(m);
+                const int pre = __popcll(m & below);
+                if (ea == e) pre_a = pre;
+                if (eb == e) pre_b = pre;
             }
             __syncthreads();
-            if (tid == 1023) base_s = run + scan[1023];
+            if (pass == 1 && t < p.T) {
+                int wa = 0, wb = 0;
+                for (int w = 0; w < wave; ++w) {
+                    wa += wcnt[w][ea];
+                    wb += wcnt[w][eb];
+                }
+                const int ra = run[ea] + wa + pre_a, rb = run[eb] + wb + pre_b;
+                p.rows[ra] = (int32_t)t;
+                p.rows[rb] = (int32_t)t;
+                p.slot[2 * t] = ra;
+                p.slot[2 * t + 1] = rb;
+            }
+            __syncthreads();
+            if (tid < E) {
+                int c = 0;
+                for (int w = 0; w < NW; ++w) c += wcnt[w][tid];
+                run[tid] += c;
+            }
             __syncthreads();
         }
-        if (tid == 0) {
-            p.counts[e] = base_s - start;
-            p.offsets[e] = start;
-        }
-        __syncthreads();
     }
 }
 
@@ -134,7 +169,8 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeParams p, const flo
 int launch_moe_route(const MoeParams &p, hipStream_t s) {
     if (p.T <= 0 || p.T > 65535 || p.n_expert < 2 || p.n_expert > MOE_MAX_EXPERTS || !p.x || !p.router || p.h <= 0)
         return set_error(GAJE_ERR_INVALID_ARG, "moe route: bad arguments");
-    hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)p.T), dim3(64 * MOE_MAX_EXPERTS), 0, s, p);
+    if ((size_t)p.h * 4 + 1024 > max_lds_per_block()) return set_error(GAJE_ERR_UNSUPPORTED, "moe route: hidden too large");
+    hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)p.T), dim3(64 * MOE_MAX_EXPERTS), (size_t)p.h * 4, s, p);
     GAJE_HIP_CHECK(hipGetLastError());
     hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(1024), 0, s, p);
     GAJE_HIP_CHECK(hipGetLastError());

@@ -56,7 +56,8 @@ def _run(hip, x, router, gu, dn, ffn):
 
 
 @pytest.mark.parametrize("T,h,ffn,E,skew", [(256, 1536, 4096, 8, 0.0), (37, 256, 512, 4, 0.0), (1, 64, 96, 2, 0.0),
-                                            (100, 256, 256, 5, 3.0)])
+                                            (100, 256, 256, 5, 3.0), (1500, 128, 128, 16, 0.0),
+                                            (2100, 64, 96, 3, 4.0)])
 def test_moe_ffn(hip, O, T, h, ffn, E, skew):
     x = hip.synth.normal(51, f"moe.x.{T}.{h}", T * h).reshape(T, h)
     router = hip.synth.normal(52, f"moe.r.{E}.{h}", E * h, 0.0, 0.02).reshape(E, h)
