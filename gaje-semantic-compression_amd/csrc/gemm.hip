@@ -489,7 +489,8 @@ GemmPlan plan_gemm_q4(int64_t M, int64_t N, int64_t K) {
     pl.mt = M > 128 ? 256 : 128;
     const int64_t tiles = ((M + pl.mt - 1) / pl.mt) * ((N + GM_NT - 1) / GM_NT);
     const int64_t nb = K / 32;
-    const int64_t cu = device_cu_count();
+    // resident workgroups: the 256-row tile's LDS allows one per compute unit
+    const int64_t cu = (pl.mt == 128 && GEMM_GA ? 2 : 1) * device_cu_count();
     int64_t S = 1;
     if (tiles < cu) S = (cu + tiles - 1) / tiles;
     int64_t kb = (nb + S - 1) / S;
@@ -507,7 +508,7 @@ GemmPlan plan_gemm_q4_grouped(int64_t R, int64_t E, int64_t N, int64_t K) {
     // tiles that hold rows: at most R/128 full ones plus one partial per group
     const int64_t tiles = ((R + 127) / 128 + E) * ((N + GM_NT - 1) / GM_NT);
     const int64_t nb = K / 32;
-    const int64_t cu = device_cu_count();
+    const int64_t cu = (GEMM_GA ? 2 : 1) * device_cu_count();  // resident 128-row workgroups
     int64_t S = 1;
     if (tiles < cu) S = (cu + tiles - 1) / tiles;
     int64_t kb = (nb + S - 1) / S;
