@@ -87,10 +87,14 @@ __global__ __launch_bounds__(256) void q4_row_exp_kernel(const uint8_t *w, int64
 // block/forward.rs:115-123), the NaN guards of RustGenomicBlock::forward_core
 // that the prologue's values decide, then the row's exponent and its f16
 // hi/lo planes.
+// Threads per row of the split pass: the row's loops are latency-bound, so a
+// row is spread over a full workgroup.
+constexpr int SPLIT_THREADS = 1024;
+
 template <int PRO>
-__global__ __launch_bounds__(256) void split_rows_kernel(SplitParams p) {
+__global__ __launch_bounds__(SPLIT_THREADS) void split_rows_kernel(SplitParams p) {
     extern __shared__ __align__(16) float xs[];
-    __shared__ float red[4];
+    __shared__ float red[SPLIT_THREADS / 64];
     __shared__ float inv_slot;
     const int64_t m = blockIdx.x;
     const int tid = threadIdx.x;
@@ -99,7 +103,7 @@ __global__ __launch_bounds__(256) void split_rows_kernel(SplitParams p) {
     int bad_a = 0, bad_b = 0;
     if constexpr (PRO == SPLIT_SWIGLU) {
         const float *ur = p.up + (p.rows ? (int64_t)p.rows[m] : m) * p.ldx;
-        for (int64_t i = tid; i < K4; i += 256) {
+        for (int64_t i = tid; i < K4; i += SPLIT_THREADS) {
             const float4 g = *(const float4 *)(xr + 4 * i), u = *(const float4 *)(ur + 4 * i);
             bad_a |= isnan(u.x) | isnan(u.y) | isnan(u.z) | isnan(u.w);
             float4 o;
@@ -111,7 +115,7 @@ __global__ __launch_bounds__(256) void split_rows_kernel(SplitParams p) {
             *(float4 *)(xs + 4 * i) = o;
         }
     } else {
-        for (int64_t i = tid; i < K4; i += 256) {
+        for (int64_t i = tid; i < K4; i += SPLIT_THREADS) {
             const float4 v = *(const float4 *)(xr + 4 * i);
             bad_a |= isnan(v.x) | isnan(v.y) | isnan(v.z) | isnan(v.w);
             *(float4 *)(xs + 4 * i) = v;
@@ -123,7 +127,7 @@ __global__ __launch_bounds__(256) void split_rows_kernel(SplitParams p) {
         rms_inv_plain(xs, K, p.eps, &inv_slot);
         __syncthreads();
         const float inv = inv_slot;
-        for (int64_t i = tid; i < K4; i += 256) {
+        for (int64_t i = tid; i < K4; i += SPLIT_THREADS) {
             float4 v = *(float4 *)(xs + 4 * i);
             const float4 g = *(const float4 *)(p.norm_w + 4 * i);
             v.x = (v.x * inv) * g.x;
@@ -152,25 +156,28 @@ __global__ __launch_bounds__(256) void split_rows_kernel(SplitParams p) {
             const float rms = inv_slot;
             if (rms > p.h_scale) {
                 const float sc = p.h_scale / rms;
-                for (int64_t k = tid; k < K; k += 256) xs[k] = xs[k] * sc;
+                for (int64_t k = tid; k < K; k += SPLIT_THREADS) xs[k] = xs[k] * sc;
             }
             __syncthreads();
         }
     }
     if (p.x_out) {  // the prologue's output row itself, for callers that keep it
-        for (int64_t i = tid; i < K4; i += 256) *(float4 *)(p.x_out + m * p.ldo + 4 * i) = *(float4 *)(xs + 4 * i);
+        for (int64_t i = tid; i < K4; i += SPLIT_THREADS) *(float4 *)(p.x_out + m * p.ldo + 4 * i) = *(float4 *)(xs + 4 * i);
     }
     float mx = 0.0f;
-    for (int64_t i = tid; i < K4; i += 256) {
+    for (int64_t i = tid; i < K4; i += SPLIT_THREADS) {
         const float4 v = *(const float4 *)(xs + 4 * i);
         mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     }
     mx = wave_max(mx);
     if ((tid & 63) == 0) red[tid >> 6] = mx;
     __syncthreads();
-    const int e = split_exponent(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+    float rmax = red[0];
+#pragma unroll
+    for (int w = 1; w < SPLIT_THREADS / 64; ++w) rmax = fmaxf(rmax, red[w]);
+    const int e = split_exponent(rmax);
     if (tid == 0) p.ex[m] = e;
-    for (int64_t i = tid; i < K4; i += 256) {
+    for (int64_t i = tid; i < K4; i += SPLIT_THREADS) {
         const float4 v = *(const float4 *)(xs + 4 * i);
         const float a[4] = {ldexpf(v.x, e), ldexpf(v.y, e), ldexpf(v.z, e), ldexpf(v.w, e)};
         h4 hi, lo;
@@ -474,9 +481,9 @@ int launch_split_rows(const SplitParams &p, hipStream_t s) {
     if (lds + 1024 > max_lds_per_block())
         return set_error(GAJE_ERR_UNSUPPORTED, "split rows: K = %lld does not fit LDS", (long long)p.K);
     if (p.up && p.norm_w) return set_error(GAJE_ERR_INVALID_ARG, "split rows: norm and swiglu prologues are exclusive");
-    if (p.up) hipLaunchKernelGGL(split_rows_kernel<SPLIT_SWIGLU>, dim3((unsigned)p.M), dim3(256), lds, s, p);
-    else if (p.norm_w) hipLaunchKernelGGL(split_rows_kernel<SPLIT_NORM>, dim3((unsigned)p.M), dim3(256), lds, s, p);
-    else hipLaunchKernelGGL(split_rows_kernel<SPLIT_PLAIN>, dim3((unsigned)p.M), dim3(256), lds, s, p);
+    if (p.up) hipLaunchKernelGGL(split_rows_kernel<SPLIT_SWIGLU>, dim3((unsigned)p.M), dim3(SPLIT_THREADS), lds, s, p);
+    else if (p.norm_w) hipLaunchKernelGGL(split_rows_kernel<SPLIT_NORM>, dim3((unsigned)p.M), dim3(SPLIT_THREADS), lds, s, p);
+    else hipLaunchKernelGGL(split_rows_kernel<SPLIT_PLAIN>, dim3((unsigned)p.M), dim3(SPLIT_THREADS), lds, s, p);
     GAJE_HIP_CHECK(hipGetLastError());
     return GAJE_OK;
 }
