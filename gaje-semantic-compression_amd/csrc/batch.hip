@@ -109,16 +109,19 @@ __global__ __launch_bounds__(NV / VPW * 64) void gemv_batch_q4_kernel(BatchGemvP
 #pragma unroll
         for (int v = 0; v < VPW; ++v) acc[j][v] = 0.0f;
 
-    load_w(0, 0);
     load_chunk(0);
+    load_w(0, 0);
     store_chunk(0);
-    __syncthreads();
+    lds_barrier();
     // one chunk from buffer `cur` (a constant at each call: the rings are
-    // indexed statically); the next chunk's loads are in flight meanwhile
+    // indexed statically); the next chunk's loads are in flight meanwhile.
+    // The activations are issued before the weights: loads complete in order,
+    // so staging them waits for them alone, and the barriers order LDS only,
+    // leaving the next chunk's weights in flight across them.
     auto chunk = [&](int c, int cur) {
         const int cn = c + 1 < nch ? c + 1 : c;
-        load_w(cn, cur ^ 1);
         load_chunk(cn);
+        load_w(cn, cur ^ 1);
         const float *xb = xs + cur * BUF + (v0 * 8 + l) * BQ_CROW;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -142,7 +145,7 @@ __global__ __launch_bounds__(NV / VPW * 64) void gemv_batch_q4_kernel(BatchGemvP
             }
         }
         store_chunk(cur ^ 1);
-        __syncthreads();
+        lds_barrier();
     };
     for (int c = 0; c < nch; c += 2) {
         chunk(c, 0);
