@@ -27,6 +27,7 @@
 #include "device_util.h"
 
 #include <cstddef>
+#include <type_traits>
 
 namespace gaje {
 
@@ -56,6 +57,61 @@ __device__ __forceinline__ float dot_ref(const float *a, const float *b, int64_t
         sum = sum + prod;
     }
     return sum;
+}
+
+// dot_product(q, k_t) chains for the four positions t4..t4+3 of one thread
+// (dot.rs:43-67): acc[u][l] is chain l of position t4+u over dimensions
+// 8c+l.  Key dimension d of the four positions is one quad of row d (byte
+// offset off + d * rowb).  A ring of RING 8-dimension chunks of quads is in
+// flight ahead of the FMAs.  q comes from uniform (scalar) loads for HD = 64;
+// a 128-float q does not fit the scalar registers and is read from LDS (qs),
+// and the chunks walk a loop of RING-chunk rounds so that the compiler cannot
+// hoist all 128 key loads of the round (they would spill).
+template <int HD>
+__device__ __forceinline__ void key_round(float (&acc)[4][8], const char *kb, uint32_t rowb, uint32_t off,
+                                          const float *qg, const float *qs) {
+    constexpr int NCH = HD / 8, RING = 4;
+    float4 kr[RING][8];
+#pragma unroll
+    for (int c = 0; c < RING; ++c)
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+            kr[c][l] = *(const float4 *)(kb + off);
+            off += rowb;
+        }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int l = 0; l < 8; ++l) acc[u][l] = 0.0f;
+    auto chunk = [&](int c, float4 (&k8)[8]) {
+        const float *q8 = HD > 64 ? qs + 8 * c : qg + 8 * c;
+        const float4 qa = *(const float4 *)q8, qb = *(const float4 *)(q8 + 4);
+        const float qc[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+            const float4 k = k8[l];
+            acc[0][l] = fmaf(qc[l], k.x, acc[0][l]);
+            acc[1][l] = fmaf(qc[l], k.y, acc[1][l]);
+            acc[2][l] = fmaf(qc[l], k.z, acc[2][l]);
+            acc[3][l] = fmaf(qc[l], k.w, acc[3][l]);
+        }
+        if (c + RING < NCH) {
+#pragma unroll
+            for (int l = 0; l < 8; ++l) {
+                k8[l] = *(const float4 *)(kb + off);
+                off += rowb;
+            }
+        }
+    };
+    if constexpr (HD > 64) {
+#pragma unroll 1
+        for (int c0 = 0; c0 < NCH; c0 += RING)
+#pragma unroll
+            for (int i = 0; i < RING; ++i) chunk(c0 + i, kr[i]);
+    } else {
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) chunk(c, kr[c % RING]);
+    }
 }
 
 // Largest score over the block (every thread passes its own running max).
@@ -140,6 +196,13 @@ __global__ __launch_bounds__(THREADS) void attn_decode_fast(AttnParams p) {
     float *sc = smem;                   // chain_row(cap) scores, then exponentials
     float *vs = sc + chain_row(cap);    // DS rows of vstride: V, then the products
     const float *qg = p.q + (size_t)h * HD;
+    // q: uniform (scalar) loads for HD = 64; a 128-float q does not fit the
+    // scalar registers (the compiler spills them), so it is read from LDS
+    __shared__ float qs[HD > 64 ? HD : 1];
+    if constexpr (HD > 64) {
+        if (tid < HD / 4) *(float4 *)(qs + 4 * tid) = *(const float4 *)(qg + 4 * tid);
+        __syncthreads();
+    }
     const float *Kh = p.k_cache + (size_t)g * p.kv_head_stride;
     const float *Vh = p.v_cache + (size_t)g * p.kv_head_stride + (size_t)d0 * cap;
 
@@ -149,45 +212,11 @@ __global__ __launch_bounds__(THREADS) void attn_decode_fast(AttnParams p) {
     // flight ahead of the FMAs.  A quad that runs past ctx stays inside the row
     // (kv_cap % 4 == 0); its extra lanes are dropped.  q is read with uniform
     // loads ----
-    constexpr int NCH = HD / 8, RING = 4;
-    const char *kb = (const char *)Kh;
     const uint32_t rowb = (uint32_t)cap * 4;
     float mx = -INFINITY;
     for (int t4 = 4 * tid; t4 < ctx; t4 += 4 * THREADS) {
-        uint32_t off = (uint32_t)t4 * 4;
-        float4 kr[RING][8];
-#pragma unroll
-        for (int c = 0; c < RING; ++c)
-#pragma unroll
-            for (int l = 0; l < 8; ++l) {
-                kr[c][l] = *(const float4 *)(kb + off);
-                off += rowb;
-            }
         float acc[4][8];
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-#pragma unroll
-            for (int l = 0; l < 8; ++l) acc[u][l] = 0.0f;
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-            const float4 qa = *(const float4 *)(qg + 8 * c), qb = *(const float4 *)(qg + 8 * c + 4);
-            const float qc[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-#pragma unroll
-            for (int l = 0; l < 8; ++l) {
-                const float4 k = kr[c % RING][l];
-                acc[0][l] = fmaf(qc[l], k.x, acc[0][l]);
-                acc[1][l] = fmaf(qc[l], k.y, acc[1][l]);
-                acc[2][l] = fmaf(qc[l], k.z, acc[2][l]);
-                acc[3][l] = fmaf(qc[l], k.w, acc[3][l]);
-            }
-            if (c + RING < NCH) {
-#pragma unroll
-                for (int l = 0; l < 8; ++l) {
-                    kr[c % RING][l] = *(const float4 *)(kb + off);
-                    off += rowb;
-                }
-            }
-        }
+        key_round<HD>(acc, (const char *)Kh, rowb, (uint32_t)t4 * 4, qg, qs);
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const float u0 = acc[u][0] + acc[u][4], u1 = acc[u][1] + acc[u][5];
@@ -269,47 +298,20 @@ __global__ __launch_bounds__(THREADS) void attn_decode_batch(AttnParams p) {
     const float *qg = p.q + z * p.seq_q_stride + (size_t)h * HD;
     const float *Kh = p.k_cache + z * p.seq_kv_stride + (size_t)g * p.kv_head_stride;
     const float *Vh = p.v_cache + z * p.seq_kv_stride + (size_t)g * p.kv_head_stride;
+    // q: uniform (scalar) loads for HD = 64; a 128-float q does not fit the
+    // scalar registers (the compiler spills them), so it is read from LDS
+    __shared__ float qs[HD > 64 ? HD : 1];
+    if constexpr (HD > 64) {
+        if (tid < HD / 4) *(float4 *)(qs + 4 * tid) = *(const float4 *)(qg + 4 * tid);
+        __syncthreads();
+    }
 
     // scores: thread j takes positions 4j..4j+3 of each round (as attn_decode_fast)
-    constexpr int NCH = HD / 8, RING = 4;
-    const char *kb = (const char *)Kh;
     const uint32_t rowb = (uint32_t)cap * 4;
     float mx = -INFINITY;
     for (int t4 = 4 * tid; t4 < ctx; t4 += 4 * THREADS) {
-        uint32_t off = (uint32_t)t4 * 4;
-        float4 kr[RING][8];
-#pragma unroll
-        for (int c = 0; c < RING; ++c)
-#pragma unroll
-            for (int l = 0; l < 8; ++l) {
-                kr[c][l] = *(const float4 *)(kb + off);
-                off += rowb;
-            }
         float acc[4][8];
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-#pragma unroll
-            for (int l = 0; l < 8; ++l) acc[u][l] = 0.0f;
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-            const float4 qa = *(const float4 *)(qg + 8 * c), qb = *(const float4 *)(qg + 8 * c + 4);
-            const float qc[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-#pragma unroll
-            for (int l = 0; l < 8; ++l) {
-                const float4 k = kr[c % RING][l];
-                acc[0][l] = fmaf(qc[l], k.x, acc[0][l]);
-                acc[1][l] = fmaf(qc[l], k.y, acc[1][l]);
-                acc[2][l] = fmaf(qc[l], k.z, acc[2][l]);
-                acc[3][l] = fmaf(qc[l], k.w, acc[3][l]);
-            }
-            if (c + RING < NCH) {
-#pragma unroll
-                for (int l = 0; l < 8; ++l) {
-                    kr[c % RING][l] = *(const float4 *)(kb + off);
-                    off += rowb;
-                }
-            }
-        }
+        key_round<HD>(acc, (const char *)Kh, rowb, (uint32_t)t4 * 4, qg, qs);
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const float u0 = acc[u][0] + acc[u][4], u1 = acc[u][1] + acc[u][5];
@@ -330,33 +332,37 @@ __global__ __launch_bounds__(THREADS) void attn_decode_batch(AttnParams p) {
     for (int t = tid; t < ctx; t += THREADS) sc[t] = sc[t] * inv;
     __syncthreads();
 
-    // out_i = ((w_0 v_0[i]) + (w_1 v_1[i])) + ..., products and sums rounded in t order
+    // out_i = ((w_0 v_0[i]) + (w_1 v_1[i])) + ..., products and sums rounded in t order.
+    // AH quads (4 AH positions) of the V row are in flight ahead of the chain, so
+    // a load issued one block ahead has the block's arithmetic to land.  Full
+    // blocks run without selects; the block holding ctx adds +0 past it (the
+    // chain starts at +0, so it is never -0 and +0 leaves it unchanged), and its
+    // w reads stay inside the scores' row: t < chain_len(ctx) (a multiple of 4 AH), where
+    // w_t = +0.
     if (tid < HD) {
         const float *v = Vh + (size_t)tid * cap;
         float acc = 0.0f;
-        constexpr int AH = 8;  // quads loaded ahead of the chain
+        constexpr int AH = 16;
+        static_assert(128 % (4 * AH) == 0, "blocks must tile chain_len");
         float4 vq[AH];
 #pragma unroll
         for (int a = 0; a < AH; ++a) vq[a] = *(const float4 *)(v + (4 * a < ctx ? 4 * a : 0));
-        for (int t0 = 0; t0 < ctx; t0 += 4 * AH) {
+        auto block = [&](int t0, auto full) {
 #pragma unroll
             for (int a = 0; a < AH; ++a) {
                 const int t = t0 + 4 * a;
-                if (t >= ctx) break;
                 const float4 vv = vq[a];
                 const int tn = t + 4 * AH;
                 vq[a] = *(const float4 *)(v + (tn < ctx ? tn : 0));
                 const float4 w = *(const float4 *)(sc + t);
-                const float vals[4] = {vv.x, vv.y, vv.z, vv.w}, ws[4] = {w.x, w.y, w.z, w.w};
+                const float pr[4] = {w.x * vv.x, w.y * vv.y, w.z * vv.z, w.w * vv.w};
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    if (t + j < ctx) {
-                        const float prod = ws[j] * vals[j];
-                        acc = acc + prod;
-                    }
-                }
+                for (int j = 0; j < 4; ++j) acc = acc + ((decltype(full)::value || t + j < ctx) ? pr[j] : 0.0f);
             }
-        }
+        };
+        int t0 = 0;
+        for (; t0 + 4 * AH <= ctx; t0 += 4 * AH) block(t0, std::true_type{});
+        if (t0 < ctx) block(t0, std::false_type{});
         const int64_t i = (int64_t)h * HD + tid, rows = (int64_t)p.n_head * HD;
         p.out[z * p.seq_q_stride + (p.out_chain_major ? (i & 7) * (rows / 8) + (i >> 3) : i)] = acc;
     }

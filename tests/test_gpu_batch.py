@@ -18,6 +18,8 @@ TINY = dict(n_embd=128, n_head=4, n_head_kv=2, n_blocks=2, ffn=256, vocab_size=1
             rope_base=1e4, arch_family=1, qkv_bias=1, tied_embeddings=0)
 HD64 = dict(n_embd=256, n_head=4, n_head_kv=2, n_blocks=2, ffn=512, vocab_size=1000, eps=1e-6,
             rope_base=1e4, arch_family=1, qkv_bias=1, tied_embeddings=0)
+HD128 = dict(n_embd=256, n_head=2, n_head_kv=1, n_blocks=1, ffn=256, vocab_size=512, eps=1e-6,
+             rope_base=1e4, arch_family=1, qkv_bias=1, tied_embeddings=0)
 
 
 @pytest.fixture(scope="module")
@@ -102,6 +104,28 @@ def test_batch_matches_independent_runs(hip, O, tmp_models, cfg, name, n_seq, le
         # out[s][i] is the argmax after feeding refs[s][i]: the oracle's token i+1
         assert list(out[s][:n_gen - 1]) == refs[s][1:], f"sequence {s}"
         assert b.cache_len(s) == len(prompts[s]) + n_gen
+    b.close()
+    g.close()
+
+
+@pytest.mark.parametrize("lengths", [[300, 140, 7], [1, 129, 257, 64]])
+def test_batch_long_context_hd128(hip, O, tmp_models, lengths):
+    """128-wide heads at contexts of several key rounds and V blocks, ragged across the batch."""
+    p = _write(hip, tmp_models / "batch_hd128.flat", seed=23, **HD128)
+    prompts = _prompts(len(lengths), lengths, HD128["vocab_size"], 24)
+    g = hip.load_genomic_auto(p)
+    g.set_k_wta_ratio(0.0)
+    b = hip.GenomicBatch(g, len(lengths), 320)
+    b.feed(_padded(prompts, hip.BATCH_INACTIVE))
+    n_gen = 6
+    firsts, refs = [], []
+    for pr in prompts:
+        _, toks = _oracle_run(O, p, pr, n_gen)
+        firsts.append(toks[0])
+        refs.append(toks)
+    out = b.decode_greedy(firsts, n_gen)
+    for s in range(len(prompts)):
+        assert list(out[s][:n_gen - 1]) == refs[s][1:], f"sequence {s}"
     b.close()
     g.close()
 
