@@ -279,6 +279,83 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(BatchRowParams p) {
     if (__syncthreads_or(bad) && tid == 0) seq_flag(p.nan_codes, s, p.layer, p.st_b);
 }
 
+// The same norm for K % 32 == 0 and K <= 16 * 256: each thread loads its
+// float4s of x and of the weights in one batch, the eight sum-of-squares
+// chains (thread l: elements 8i + l, fma(v, v, acc) in i order) read a
+// chain-major LDS copy whose rows are zero past K/8 (fma(0, 0, acc) = acc, acc
+// >= +0), and the outputs are formed from the registers.  The reduction
+// ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7)) and the rounding of every step are
+// those of rmsnorm_rows_kernel.
+constexpr int RN_XB4 = 4;
+__host__ __device__ constexpr int rn_chain_row(int64_t K) { return (int)((K / 8 + 63) / 64 * 64 + 36); }
+
+__global__ __launch_bounds__(256) void rmsnorm_rows_cm_kernel(BatchRowParams p) {
+    extern __shared__ __align__(16) float xs[];  // [8][rn_chain_row(K)]
+    __shared__ float inv_slot;
+    const int s = blockIdx.x, tid = threadIdx.x;
+    const int64_t K = p.K, K4 = K / 4, K8 = K / 8;
+    const int row = rn_chain_row(K), n = (int)((K8 + 63) / 64 * 64), tail = row - (int)K8;
+    const float *x = p.x + (size_t)s * p.ldx;
+    float4 xr[RN_XB4], wr[RN_XB4];
+#pragma unroll
+    for (int u = 0; u < RN_XB4; ++u) {
+        const int64_t m = u * 256 + tid;
+        xr[u] = m < K4 ? *(const float4 *)(x + 4 * m) : make_float4(0.f, 0.f, 0.f, 0.f);
+        wr[u] = (p.w && m < K4) ? *(const float4 *)(p.w + 4 * m) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    // the rows' zero tails [K8, row) (the chains read up to n + 32)
+    for (int t = tid; t < 8 * tail; t += 256) xs[(t / tail) * row + K8 + t % tail] = 0.0f;
+    int bad = 0;
+#pragma unroll
+    for (int u = 0; u < RN_XB4; ++u) {
+        const int64_t m = u * 256 + tid;
+        if (m >= K4) continue;
+        const float v[4] = {xr[u].x, xr[u].y, xr[u].z, xr[u].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t k = 4 * m + j;
+            xs[(k & 7) * row + (k >> 3)] = v[j];
+            bad |= isnan(v[j]);
+        }
+    }
+    if (__syncthreads_or(bad) && tid == 0) seq_flag(p.nan_codes, s, p.layer, p.st_a);
+    float inv = 1.0f;
+    if (p.w) {
+        if (tid < 8) {
+            const float acc = chain_lds_sq(0.0f, xs + tid * row, n);
+            const float a = acc + __shfl(acc, (tid + 4) & 7, 8);  // lane l<4: a_l + a_{l+4}
+            const float b = a + __shfl(a, (tid + 1) & 7, 8);      // lane 0: u0+u1, lane 2: u2+u3
+            const float tot = b + __shfl(b, (tid + 2) & 7, 8);    // lane 0: (u0+u1) + (u2+u3)
+            if (tid == 0) {
+                const float mean = tot / (float)K;
+                inv_slot = 1.0f / sqrtf(mean + p.eps);
+            }
+        }
+        __syncthreads();
+        inv = inv_slot;
+    }
+    bad = 0;
+    float *y = p.y + (size_t)s * p.ldy;
+#pragma unroll
+    for (int u = 0; u < RN_XB4; ++u) {
+        const int64_t m = u * 256 + tid;
+        if (m >= K4) continue;
+        const float v[4] = {xr[u].x, xr[u].y, xr[u].z, xr[u].w}, w[4] = {wr[u].x, wr[u].y, wr[u].z, wr[u].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t k = 4 * m + j;
+            float o = v[j];  // no weight: the plain rows
+            if (p.w) {
+                const float t = o * inv;
+                o = t * w[j];
+            }
+            bad |= isnan(o);
+            y[p.chain_major ? (k & 7) * K8 + (k >> 3) : k] = o;
+        }
+    }
+    if (__syncthreads_or(bad) && tid == 0) seq_flag(p.nan_codes, s, p.layer, p.st_b);
+}
+
 // swiglu_balanced per element (block/forward.rs:87-113) without the genomic
 // norm: a grid over (sequence, 256-element slices).
 __global__ __launch_bounds__(256) void swiglu_elems_kernel(BatchRowParams p) {
@@ -443,6 +520,11 @@ int launch_gemv_batch(const BatchGemvParams &p, hipStream_t s) {
 int launch_rmsnorm_rows(const BatchRowParams &p, hipStream_t s) {
     if (!p.x || !p.y || p.K <= 0 || p.nv <= 0 || (p.chain_major && p.K % 8))
         return set_error(GAJE_ERR_INVALID_ARG, "rmsnorm rows: bad arguments");
+    if (p.K % 32 == 0 && p.K <= RN_XB4 * 4 * 256 && p.ldx % 4 == 0 && !(((uintptr_t)p.x | (uintptr_t)p.w) & 15)) {
+        hipLaunchKernelGGL(rmsnorm_rows_cm_kernel, dim3((unsigned)p.nv), dim3(256), (size_t)8 * rn_chain_row(p.K) * 4, s, p);
+        GAJE_HIP_CHECK(hipGetLastError());
+        return GAJE_OK;
+    }
     if ((size_t)p.K * 4 + 1024 > max_lds_per_block()) return set_error(GAJE_ERR_UNSUPPORTED, "rmsnorm rows: K too large");
     hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3((unsigned)p.nv), dim3(256), (size_t)p.K * 4, s, p);
     GAJE_HIP_CHECK(hipGetLastError());
