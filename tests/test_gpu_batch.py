@@ -18,6 +18,9 @@ TINY = dict(n_embd=128, n_head=4, n_head_kv=2, n_blocks=2, ffn=256, vocab_size=1
             rope_base=1e4, arch_family=1, qkv_bias=1, tied_embeddings=0)
 HD64 = dict(n_embd=256, n_head=4, n_head_kv=2, n_blocks=2, ffn=512, vocab_size=1000, eps=1e-6,
             rope_base=1e4, arch_family=1, qkv_bias=1, tied_embeddings=0)
+# gate/up rows >= 16384: the two-rows-per-lane batched matvec
+WIDE = dict(n_embd=128, n_head=4, n_head_kv=2, n_blocks=1, ffn=8192, vocab_size=1000, eps=1e-6,
+            rope_base=1e4, arch_family=1, qkv_bias=1, tied_embeddings=0)
 HD128 = dict(n_embd=256, n_head=2, n_head_kv=1, n_blocks=1, ffn=256, vocab_size=512, eps=1e-6,
              rope_base=1e4, arch_family=1, qkv_bias=1, tied_embeddings=0)
 
@@ -78,7 +81,8 @@ def _oracle_run(O, path, prompt, n_gen):
 
 
 @pytest.mark.parametrize("cfg,name,n_seq,lengths", [(TINY, "tiny", 3, [5, 9, 7]), (HD64, "hd64", 5, [12, 4, 8]),
-                                                    (HD64, "hd64", 16, [6]), (TINY, "tiny", 1, [10])])
+                                                    (HD64, "hd64", 16, [6]), (TINY, "tiny", 1, [10]),
+                                                    (WIDE, "wide", 16, [5, 3]), (WIDE, "wide", 8, [4])])
 def test_batch_matches_independent_runs(hip, O, tmp_models, cfg, name, n_seq, lengths):
     p = _write(hip, tmp_models / f"batch_{name}.flat", seed=21, **cfg)
     prompts = _prompts(n_seq, lengths, cfg["vocab_size"], 22 + n_seq)
