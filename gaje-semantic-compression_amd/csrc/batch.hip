@@ -246,6 +246,94 @@ __global__ __launch_bounds__(256) void gemv_batch_f32_kernel(BatchGemvParams p) 
     }
 }
 
+// The same products for a batch of 16, register-blocked over rows: lanes 2r,
+// 2r+1 of a wave own rows r + 32j (j < RB; one 32-row tile each) of the
+// wave's 32*RB rows, chains 0..3 and 4..7 as above, and a workgroup takes VG
+// of the vectors (the batch splits over the grid), so each activation quad
+// read from LDS feeds RB rows.  Workgroups b, b+8, b+16, b+24 take one row
+// block's four vector groups; consecutive workgroups go to the eight XCDs in
+// turn, so the four land on one XCD and its L2 serves the block's rows
+// three times of four.
+constexpr int F32B_RB = 4, F32B_VG = 4, F32B_AHEAD = 4;
+constexpr int64_t F32B_ROWS = 128 * F32B_RB;  // rows per workgroup
+
+__global__ __launch_bounds__(256) void gemv_batch_f32_rb_kernel(BatchGemvParams p, int64_t nblk) {
+    constexpr int RB = F32B_RB, VG = F32B_VG, AHEAD = F32B_AHEAD;
+    extern __shared__ __align__(16) float xs[];  // [VG][K]
+    const int b = blockIdx.x;
+    const int64_t blk = ((int64_t)(b >> 5) << 3) | (b & 7);
+    if (blk >= nblk) return;  // whole workgroup: the grid is rounded up to 32
+    const int vz = ((b >> 3) & 3) * VG;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t K = p.K, K4 = K / 4;
+    for (int64_t i = tid; i < VG * K4; i += 256) {
+        const int64_t v = i / K4, q = i - v * K4;
+        *(float4 *)(xs + v * K + 4 * q) = *(const float4 *)(p.x + (size_t)(vz + v) * p.ldx + 4 * q);
+    }
+    __syncthreads();
+    const int s = lane & 1;
+    const int64_t r0 = blk * F32B_ROWS + wave * (32 * RB) + (lane >> 1);
+    const float *wl[RB];
+#pragma unroll
+    for (int j = 0; j < RB; ++j) {
+        const int64_t row = r0 + 32 * j;
+        const int64_t lrow = row < p.N ? row : p.N - 1;
+        wl[j] = (const float *)p.w + (size_t)(lrow >> 5) * (size_t)K * 32 + (lrow & 31) * 8 + 4 * s;
+    }
+    const int64_t chunks = K / 8;
+    float acc[RB][VG][4];
+#pragma unroll
+    for (int j = 0; j < RB; ++j)
+#pragma unroll
+        for (int v = 0; v < VG; ++v) acc[j][v][0] = acc[j][v][1] = acc[j][v][2] = acc[j][v][3] = 0.0f;
+    float4 ring[AHEAD][RB];
+#pragma unroll
+    for (int u = 0; u < AHEAD; ++u)
+#pragma unroll
+        for (int j = 0; j < RB; ++j) ring[u][j] = ld_f4<true>(wl[j] + 256 * (u < chunks ? u : chunks - 1));
+    for (int64_t c0 = 0; c0 < chunks; c0 += AHEAD) {
+#pragma unroll
+        for (int u = 0; u < AHEAD; ++u) {
+            const int64_t c = c0 + u;
+            if (c >= chunks) break;
+            float4 w[RB];
+#pragma unroll
+            for (int j = 0; j < RB; ++j) w[j] = ring[u][j];
+            const int64_t cn = c + AHEAD < chunks ? c + AHEAD : chunks - 1;
+#pragma unroll
+            for (int j = 0; j < RB; ++j) ring[u][j] = ld_f4<true>(wl[j] + 256 * cn);
+#pragma unroll
+            for (int v = 0; v < VG; ++v) {
+                const float4 x = *(const float4 *)(xs + v * K + 8 * c + 4 * s);
+#pragma unroll
+                for (int j = 0; j < RB; ++j) {
+                    acc[j][v][0] = fmaf(x.x, w[j].x, acc[j][v][0]);
+                    acc[j][v][1] = fmaf(x.y, w[j].y, acc[j][v][1]);
+                    acc[j][v][2] = fmaf(x.z, w[j].z, acc[j][v][2]);
+                    acc[j][v][3] = fmaf(x.w, w[j].w, acc[j][v][3]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < RB; ++j) {
+        const int64_t row = r0 + 32 * j;
+#pragma unroll
+        for (int v = 0; v < VG; ++v) {
+            // lane 2r: chains 0..3, lane 2r+1: 4..7 -> ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7))
+            const float u0 = acc[j][v][0] + __shfl_xor(acc[j][v][0], 1, WAVE);
+            const float u1 = acc[j][v][1] + __shfl_xor(acc[j][v][1], 1, WAVE);
+            const float u2 = acc[j][v][2] + __shfl_xor(acc[j][v][2], 1, WAVE);
+            const float u3 = acc[j][v][3] + __shfl_xor(acc[j][v][3], 1, WAVE);
+            const int sv = vz + v;
+            if (s != 0 || row >= p.N || sv >= p.nv) continue;
+            float y = (u0 + u1) + (u2 + u3);
+            if (row < p.bias_len) y = y + p.bias[row];
+            p.y[(size_t)sv * p.ldy + row] = y;
+        }
+    }
+}
+
 // rms_norm per sequence row (norm.rs:52-88): threads 0..7 run the chains,
 // out = (x * inv) * w.  Guards: st_a on the input, st_b on the output.
 __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(BatchRowParams p) {
@@ -524,6 +612,14 @@ int launch_gemv_batch(const BatchGemvParams &p, hipStream_t s) {
         if (p.mode != MODE_STORE) return set_error(GAJE_ERR_UNSUPPORTED, "batched matvec: f32 rows store only");
         if (nv == 4) return launch_f32<4>(p, s);
         if (nv == 8) return launch_f32<8>(p, s);
+        const size_t lds = (size_t)F32B_VG * p.K * 4;
+        if (lds + 1024 <= max_lds_per_block()) {
+            const int64_t nblk = (p.N + F32B_ROWS - 1) / F32B_ROWS;
+            const int64_t grid = (nblk + 7) / 8 * 32;  // 16 / F32B_VG = 4 vector groups per block
+            hipLaunchKernelGGL(gemv_batch_f32_rb_kernel, dim3((unsigned)grid), dim3(256), lds, s, p, nblk);
+            GAJE_HIP_CHECK(hipGetLastError());
+            return GAJE_OK;
+        }
         return launch_f32<16>(p, s);
     }
     return set_error(GAJE_ERR_UNSUPPORTED, "batched matvec: weight format %d", p.fmt);
