@@ -148,7 +148,7 @@ __device__ __forceinline__ float serial_sum(const float *e, int n) {
 
 // Padded chain length for ctx positions, and the LDS row length that holds it
 // plus the chain's read-ahead (chain_lds reads 32 floats past the end).
-__host__ __device__ constexpr int chain_len(int64_t ctx) { return (int)((ctx + 127) / 128 * 128); }
+__host__ __device__ constexpr int chain_len(int64_t ctx) { return (int)((ctx + 63) / 64 * 64); }
 __host__ __device__ constexpr int chain_row(int64_t cap) { return chain_len(cap) + 64; }
 
 // Streaming kernel: head dimension HD known at compile time (64 or 128),
@@ -343,7 +343,7 @@ __global__ __launch_bounds__(THREADS) void attn_decode_batch(AttnParams p) {
         const float *v = Vh + (size_t)tid * cap;
         float acc = 0.0f;
         constexpr int AH = 16;
-        static_assert(128 % (4 * AH) == 0, "blocks must tile chain_len");
+        static_assert(64 % (4 * AH) == 0, "blocks must tile chain_len");
         float4 vq[AH];
 #pragma unroll
         for (int a = 0; a < AH; ++a) vq[a] = *(const float4 *)(v + (4 * a < ctx ? 4 * a : 0));
