@@ -61,32 +61,52 @@ def model_path(preset: str, seed: int, d: str, quant_embed: int = 0, body_format
     return path
 
 
-def q4_gemv_c0(iters: int = 1024, hot: bool = True):
-    """The C0 matvec: Q4_0 K=896 N=4864, cold (128 copies) and hot (1 copy)."""
+def q4_gemv_c0(iters: int = 1024, hot: bool = True, stream: bool = True):
+    """The C0 matvec: Q4_0 K=896 N=4864, cold (128 copies) and hot (1 copy); the
+    launch floors of its grid; and one launch over all 128 copies as a single
+    622,592-row matrix (348 MB), the kernel's streaming rate."""
     from gaje_hip import ops, synth
     n, k = 4864, 896
     blocks = synth.q4_0_tensor(0, "c0.gemv", n, k)
-    packed = ops.q4_0_upload(blocks, n, k).read(np.uint8)  # same 2,723,840 bytes, GEMV order
-    stride = (packed.nbytes + 255) // 256 * 256
+    wbytes = n * ((k + 127) // 128) * 80  # the same 2,723,840 bytes, GEMV order
+    packed = ops.q4_0_upload(blocks, n, k).read(np.uint8)[:wbytes]
+    stride = (wbytes + 255) // 256 * 256
     copies = 128
-    w = ops.DeviceBuffer(stride * copies)
-    host = np.zeros(stride * copies, dtype=np.uint8)
+    w = ops.DeviceBuffer(stride * copies + 4096)  # + the tail the prefetch ring may read past the last row
+    host = np.zeros(stride * copies + 4096, dtype=np.uint8)
     for c in range(copies):
-        host[c * stride:c * stride + packed.nbytes] = packed
+        host[c * stride:c * stride + wbytes] = packed
     w.write(host)
+    del host
     x = ops.DeviceBuffer.from_array(synth.normal(0, "c0.x", k))
-    y = ops.DeviceBuffer(n * 4)
+    y = ops.DeviceBuffer(n * copies * 4)
     algo = blocks.nbytes + k * 4 + n * 4  # weights + x + y
     cold_ms = ops.bench_gemv(1, w, stride, copies, x, y, n, k, iters)
     hot_ms = ops.bench_gemv(1, w, stride, 1, x, y, n, k, iters) if hot else None
-    w.close()
+    # floors of a launch with the C0 grid (n rows x 8 chain lanes, 256 threads)
+    grid = (n * 8 + 255) // 256
+    empty_ms = ops.bench_floor(None, 0, grid, 256, iters)
+    read_ms = ops.bench_floor(w, packed.nbytes, 256, 256, iters)
     out = dict(shape="N=4864 K=896 (Q4_0Block 20 B / 32 weights, packed on device)", algorithmic_bytes=algo,
                launches=iters, cold_us=cold_ms * 1e3, cold_GBps=algo / (cold_ms * 1e-3) / 1e9,
                cold_frac=algo / (cold_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
-               copies=copies, note="cold = 128 distinct copies cycled (348 MB > 256 MB LLC), "
-                                   "graph-replayed back-to-back launches; hot = one copy")
+               copies=copies, empty_kernel_us=empty_ms * 1e3, plain_read_us=read_ms * 1e3,
+               note="cold = 128 distinct copies cycled (348 MB > 256 MB LLC), graph-replayed back-to-back "
+                    "launches, per-launch time including the launch boundary; hot = one copy; "
+                    f"empty_kernel_us = an empty kernel of the same grid ({grid} x 256); plain_read_us = a "
+                    "read-only kernel over the same 2,723,840 weight bytes (256 x 256 threads)")
     if hot_ms is not None:
         out.update(hot_us=hot_ms * 1e3, hot_GBps=algo / (hot_ms * 1e-3) / 1e9)
+    if stream and stride == packed.nbytes:
+        ns = n * copies  # the copies are contiguous: one matrix of 622,592 rows
+        s_ms = ops.bench_gemv(1, w, 0, 1, x, y, ns, k, 64)
+        s_algo = ns * (k // 32) * 20 + k * 4 + ns * 4
+        sr_ms = ops.bench_floor(w, ns * (k // 32) * 20, 4096, 256, 64)
+        out.update(stream_rows=ns, stream_bytes=s_algo, stream_us=s_ms * 1e3,
+                   stream_GBps=s_algo / (s_ms * 1e-3) / 1e9,
+                   stream_frac=s_algo / (s_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
+                   stream_plain_read_GBps=ns * (k // 32) * 20 / (sr_ms * 1e-3) / 1e9)
+    w.close()
     return out
 
 

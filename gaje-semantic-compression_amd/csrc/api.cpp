@@ -580,6 +580,59 @@ extern "C" int gaje_hip_argmax(const float *x, int64_t n, uint32_t *idx, void *s
     return launch_argmax(x, n, idx, as_stream(stream));
 }
 
+namespace {
+
+// Average device time per launch of `per_pass` launches issued by launch_all on
+// stream s, repeated until `iters` launches ran: captured once in a HIP graph
+// and replayed, timed with HIP events on s.  With GAJE_HIP_PROFILE set the
+// launches are issued one by one instead, so that a kernel tracer sees each.
+template <class F>
+int time_launches(F &&launch_all, int per_pass, int iters, hipStream_t s, float *avg_ms) {
+    int rc = launch_all();  // warm-up, eager (validates the arguments)
+    const int reps = (iters + per_pass - 1) / per_pass;
+    float ms = 0.0f;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    hipGraph_t g = nullptr;
+    hipGraphExec_t ge = nullptr;
+    if (rc == GAJE_OK && (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess))
+        rc = set_error(GAJE_ERR_HIP, "event create failed");
+    if (rc == GAJE_OK && getenv("GAJE_HIP_PROFILE")) {
+        (void)hipEventRecord(e0, s);
+        for (int r = 0; r < reps && rc == GAJE_OK; ++r) rc = launch_all();
+        (void)hipEventRecord(e1, s);
+    } else if (rc == GAJE_OK) {
+        if (hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+            rc = set_error(GAJE_ERR_HIP, "graph capture failed");
+        } else {
+            rc = launch_all();
+            if (hipStreamEndCapture(s, &g) != hipSuccess && rc == GAJE_OK)
+                rc = set_error(GAJE_ERR_HIP, "graph capture failed");
+        }
+        if (rc == GAJE_OK && hipGraphInstantiate(&ge, g, nullptr, nullptr, 0) != hipSuccess)
+            rc = set_error(GAJE_ERR_HIP, "graph instantiate failed");
+        if (rc == GAJE_OK) {
+            (void)hipGraphLaunch(ge, s);  // first replay uploads the graph
+            (void)hipEventRecord(e0, s);
+            for (int r = 0; r < reps; ++r) (void)hipGraphLaunch(ge, s);
+            (void)hipEventRecord(e1, s);
+        }
+    }
+    if (rc == GAJE_OK) {
+        if (hipEventSynchronize(e1) != hipSuccess) rc = set_error(GAJE_ERR_HIP, "benchmark replay failed");
+        else (void)hipEventElapsedTime(&ms, e0, e1);
+    }
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (ge) (void)hipGraphExecDestroy(ge);
+    if (g) (void)hipGraphDestroy(g);
+    (void)hipStreamSynchronize(s);
+    GAJE_TRY(rc);
+    *avg_ms = ms / (float)(reps * per_pass);
+    return GAJE_OK;
+}
+
+}  // namespace
+
 extern "C" int gaje_hip_bench_gemv(int format, const void *w_base, size_t copy_stride, const float *lut_base,
                                    size_t lut_stride, int copies, const float *x, float *y, int64_t n, int64_t k,
                                    int iters, float *avg_ms) {
@@ -608,55 +661,22 @@ extern "C" int gaje_hip_bench_gemv(int format, const void *w_base, size_t copy_s
         }
         return GAJE_OK;
     };
-    int rc = launch_all();  // warm-up, eager (validates the arguments)
-    if (rc == GAJE_OK && getenv("GAJE_HIP_PROFILE")) {
-        // eager launches only, so that a kernel tracer sees every dispatch
-        int reps = (iters + per_pass - 1) / per_pass;
-        hipEvent_t a = nullptr, b = nullptr;
-        float ms = 0.0f;
-        (void)hipEventCreate(&a);
-        (void)hipEventCreate(&b);
-        (void)hipEventRecord(a, s);
-        for (int r = 0; r < reps && rc == GAJE_OK; ++r) rc = launch_all();
-        (void)hipEventRecord(b, s);
-        if (rc == GAJE_OK && hipEventSynchronize(b) == hipSuccess) (void)hipEventElapsedTime(&ms, a, b);
-        (void)hipEventDestroy(a);
-        (void)hipEventDestroy(b);
-        (void)hipStreamSynchronize(s);
-        (void)hipStreamDestroy(s);
-        GAJE_TRY(rc);
-        *avg_ms = ms / (float)(reps * per_pass);
-        return GAJE_OK;
-    }
-    hipGraph_t g = nullptr;
-    hipGraphExec_t ge = nullptr;
-    hipEvent_t e0 = nullptr, e1 = nullptr;
-    float ms = 0.0f;
-    int reps = (iters + per_pass - 1) / per_pass;
-    if (rc == GAJE_OK && hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) == hipSuccess) {
-        rc = launch_all();
-        if (hipStreamEndCapture(s, &g) != hipSuccess && rc == GAJE_OK)
-            rc = set_error(GAJE_ERR_HIP, "graph capture failed");
-    }
-    if (rc == GAJE_OK && hipGraphInstantiate(&ge, g, nullptr, nullptr, 0) != hipSuccess)
-        rc = set_error(GAJE_ERR_HIP, "graph instantiate failed");
-    if (rc == GAJE_OK) {
-        (void)hipGraphLaunch(ge, s);  // first replay uploads the graph
-        (void)hipEventCreate(&e0);
-        (void)hipEventCreate(&e1);
-        (void)hipEventRecord(e0, s);
-        for (int r = 0; r < reps; ++r) (void)hipGraphLaunch(ge, s);
-        (void)hipEventRecord(e1, s);
-        if (hipEventSynchronize(e1) != hipSuccess) rc = set_error(GAJE_ERR_HIP, "benchmark replay failed");
-        else (void)hipEventElapsedTime(&ms, e0, e1);
-    }
-    if (e0) (void)hipEventDestroy(e0);
-    if (e1) (void)hipEventDestroy(e1);
-    if (ge) (void)hipGraphExecDestroy(ge);
-    if (g) (void)hipGraphDestroy(g);
-    (void)hipStreamSynchronize(s);
+    const int rc = time_launches(launch_all, per_pass, iters, s, avg_ms);
     (void)hipStreamDestroy(s);
-    GAJE_TRY(rc);
-    *avg_ms = ms / (float)(reps * per_pass);
-    return GAJE_OK;
+    return rc;
+}
+
+extern "C" int gaje_hip_bench_floor(const void *buf, int64_t bytes, int grid, int block, int iters, float *avg_ms) {
+    clear_error();
+    if (!avg_ms || iters <= 0 || grid <= 0 || block <= 0 || bytes < 0)
+        return set_error(GAJE_ERR_INVALID_ARG, "bad benchmark arguments");
+    hipStream_t s;
+    GAJE_HIP_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    auto launch_all = [&]() -> int {
+        for (int i = 0; i < 128; ++i) GAJE_TRY(launch_floor_probe(buf, bytes, (unsigned)grid, (unsigned)block, s));
+        return GAJE_OK;
+    };
+    const int rc = time_launches(launch_all, 128, iters, s, avg_ms);
+    (void)hipStreamDestroy(s);
+    return rc;
 }

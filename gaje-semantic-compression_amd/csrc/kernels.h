@@ -351,6 +351,9 @@ int launch_rmsnorm(const float *x, const float *w, float eps, float *y, int64_t 
 int launch_swiglu(const float *g, const float *u, float *out, int64_t n, hipStream_t s);
 int launch_expf(const float *x, float *y, int64_t n, hipStream_t s);
 int launch_fill_u32(uint32_t *p, uint32_t v, int64_t n, hipStream_t s);
+// bytes == 0: an empty kernel of grid x block; else a plain read of `bytes`
+// (>= 256) of buf, whose first 256 bytes it may overwrite.
+int launch_floor_probe(const void *buf, int64_t bytes, unsigned grid, unsigned block, hipStream_t s);
 // Host-driven state update ordered on the stream.  Negative pos / out_cap /
 // step keep the current value; reset_guards clears halted, nan_code and the
 // argmax.

@@ -167,6 +167,28 @@ __global__ void fill_u32_kernel(uint32_t *p, uint32_t v, int64_t n) {
         p[i] = v;
 }
 
+// Floor probes for the benchmarks: a kernel that does nothing, and one that
+// reads n16 16-byte words (four loads in flight per thread, grid-strided) and
+// folds them, writing only when the fold hits one fixed value so the loads
+// stay.  Launch boundary and plain-read time of a launch of the same grid.
+__global__ void empty_kernel() {}
+
+__global__ __launch_bounds__(256) void read_kernel(const uint8_t *buf, int64_t n16, uint32_t *sink) {
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    uint32_t acc = 0;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += 4 * step) {
+        vu4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t j = i + u * step;
+            v[u] = j < n16 ? ld_u4<true>(buf + 16 * j) : vu4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    if (acc == 0x9E3779B9u) sink[blockIdx.x & 63] = acc;
+}
+
 unsigned grid_for(int64_t n, int threads, unsigned cap = 4096) {
     int64_t g = (n + threads - 1) / threads;
     if (g < 1) g = 1;
@@ -254,6 +276,17 @@ int launch_swiglu(const float *g, const float *u, float *out, int64_t n, hipStre
     if (n < 0 || (n > 0 && (!g || !u || !out))) return set_error(GAJE_ERR_INVALID_ARG, "swiglu: bad arguments");
     if (n == 0) return GAJE_OK;
     hipLaunchKernelGGL(swiglu_kernel, dim3(grid_for(n, 256)), dim3(256), 0, s, g, u, out, n);
+    GAJE_HIP_CHECK(hipGetLastError());
+    return GAJE_OK;
+}
+
+int launch_floor_probe(const void *buf, int64_t bytes, unsigned grid, unsigned block, hipStream_t s) {
+    if (grid == 0 || block == 0 || block > 1024 || (bytes > 0 && (!buf || bytes < 256 || block > 256)))
+        return set_error(GAJE_ERR_INVALID_ARG, "floor probe: bad arguments");
+    if (bytes == 0) hipLaunchKernelGGL(empty_kernel, dim3(grid), dim3(block), 0, s);
+    else
+        hipLaunchKernelGGL(read_kernel, dim3(grid), dim3(block), 0, s, (const uint8_t *)buf, bytes / 16,
+                           (uint32_t *)const_cast<void *>(buf));
     GAJE_HIP_CHECK(hipGetLastError());
     return GAJE_OK;
 }

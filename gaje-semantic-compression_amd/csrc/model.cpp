@@ -289,7 +289,7 @@ struct gaje_hip_model {
 
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
-    bool graph_kwta_blocks = false;
+    int64_t graph_block_k = 0;      // block K-WTA k baked into the captured graph (0 = none)
 
     float kwta_ratio = 0.5f;        // GenomicLLM k_wta_ratio after load_genomic (flat_reader.rs:234)
     float block_kwta_ratio = 0.0f;  // RustGenomicBlock k_wta_ratio (block/init.rs:42)
@@ -533,6 +533,14 @@ int reserve_ctx(gaje_hip_model *m, int64_t positions) {
     return GAJE_OK;
 }
 
+// k of the blocks' lateral_inhibition_kwta (block/forward.rs:144-148,
+// k = max(1, n_embd * ratio)), or 0 when the ratio leaves it off.
+int64_t block_kwta_k(const gaje_hip_model *m) {
+    if (!(m->block_kwta_ratio > 0.0f && m->block_kwta_ratio < 1.0f)) return 0;
+    const int64_t k = (int64_t)((float)m->n_embd * m->block_kwta_ratio);
+    return k < 1 ? 1 : k;
+}
+
 // Output norm -> lm_head logits with the running argmax -> next token, advance
 // (llm/forward.rs:38-46) for the hidden state in m->h.
 int enqueue_head(gaje_hip_model *m) {
@@ -626,19 +634,18 @@ int enqueue_token(gaje_hip_model *m, hipEvent_t ev_blocks_done) {
         p.st_b = ST_FINAL;
         GAJE_TRY(launch_gemv(p, m->stream));
 
-        if (m->block_kwta_ratio > 0.0f && m->block_kwta_ratio < 1.0f) {
-            int64_t k = (int64_t)((float)m->n_embd * m->block_kwta_ratio);
-            if (k < 1) k = 1;
-            GAJE_TRY(launch_kwta(m->h, m->n_embd, k, m->st, m->stream));
-        }
+        const int64_t bk = block_kwta_k(m);
+        if (bk > 0) GAJE_TRY(launch_kwta(m->h, m->n_embd, bk, m->st, m->stream));
     }
     if (ev_blocks_done) GAJE_HIP_CHECK(hipEventRecord(ev_blocks_done, m->stream));
     return enqueue_head(m);
 }
 
+// The graph bakes the block K-WTA k into a kernel argument, so it is keyed by
+// that k: a ratio change that changes k recaptures it.
 int ensure_graph(gaje_hip_model *m) {
-    const bool kb = m->block_kwta_ratio > 0.0f && m->block_kwta_ratio < 1.0f;
-    if (m->graph_exec && m->graph_kwta_blocks == kb) return GAJE_OK;
+    const int64_t bk = block_kwta_k(m);
+    if (m->graph_exec && m->graph_block_k == bk) return GAJE_OK;
     drop_graph(m);
     GAJE_HIP_CHECK(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
     int rc = enqueue_token(m, nullptr);
@@ -651,7 +658,7 @@ int ensure_graph(gaje_hip_model *m) {
     if (e != hipSuccess) return set_error(GAJE_ERR_HIP, "graph capture failed: %s", hipGetErrorString(e));
     m->graph = g;
     GAJE_HIP_CHECK(hipGraphInstantiate(&m->graph_exec, g, nullptr, nullptr, 0));
-    m->graph_kwta_blocks = kb;
+    m->graph_block_k = bk;
     return GAJE_OK;
 }
 

@@ -25,6 +25,21 @@
 //   code(row, col)  = r(key(name#codes), row*k + col) >> 62
 //   block byte m    = code[4m] << 6 | code[4m+1] << 4 | code[4m+2] << 2 | code[4m+3]
 //   centroids[row][b][j] = f32(y_j * s(row, b))   (ascending: codes 00, 01, 11, 10)
+// Sparse f16 anchors (the "GAJE" buffer of GenomicLinear::new, init.rs:61-107),
+// optional for body tensors: row r > 0 holds r(key(name#anchors), r) >> 62
+// anchors (0..3), row 0 1 + (r(key, 0) >> 63), anchor j at column r(key(name#anchors), n + 4r + j) % k, value
+// f16(0.05 * normal(key(name#anchors), 4r + j)), in row then column order.
+// The buffer is "GAJE", count, the u32 flat indices, the f16 values, then:
+//   form 1  n+1 u64 row pointers (the CSR path of init.rs:82-90); indices
+//           r*k + col + k*n*(j & 1), so odd anchors sit past the tensor and
+//           only index % in_features (forward.rs:106) places them; row 1's
+//           range is inverted (pointer[2] = pointer[1] - 1, skipped, :104),
+//           and row 2 then starts one anchor early
+//   form 2  the two pointers {0, count} of genomize_4bit_core
+//           (genomize.rs:373-376): too short for n > 1, so the rows come from
+//           the flat indices (:91-103)
+//   form 3  no pointers (the same fallback)
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -221,12 +236,45 @@ void quantize_q8_0(const float *w, int64_t nblocks, uint8_t *out) {
     });
 }
 
+// The anchor buffer of an n x k body tensor in the given form (1..3).
+std::vector<uint8_t> gen_anchors(uint64_t seed, const std::string &name, int64_t n, int64_t k, int form) {
+    const uint64_t key = stream_key(seed, name + "#anchors");
+    std::vector<uint32_t> idx;
+    std::vector<uint16_t> val;
+    std::vector<uint64_t> ptr(1, 0);
+    for (int64_t r = 0; r < n; ++r) {
+        const int cnt = r == 0 ? 1 + (int)(draw(key, 0) >> 63) : (int)(draw(key, (uint64_t)r) >> 62);
+        std::vector<int64_t> cols;
+        for (int j = 0; j < cnt; ++j) cols.push_back((int64_t)(draw(key, (uint64_t)(n + 4 * r + j)) % (uint64_t)k));
+        std::sort(cols.begin(), cols.end());
+        for (int j = 0; j < cnt; ++j) {
+            int64_t flat = r * k + cols[j];
+            if (form == 1 && (j & 1)) flat += k * n;
+            idx.push_back((uint32_t)flat);
+            val.push_back(f32_to_f16((float)(0.05 * normal_at(key, (uint64_t)(4 * r + j)))));
+        }
+        ptr.push_back(idx.size());
+    }
+    if (form == 1 && n > 2 && ptr[1] >= 1) ptr[2] = ptr[1] - 1;
+    if (form == 2) ptr = {0, (uint64_t)idx.size()};
+    if (form == 3) ptr.clear();
+    const uint32_t count = (uint32_t)idx.size();
+    std::vector<uint8_t> buf(8 + (size_t)count * 6 + ptr.size() * 8);
+    memcpy(buf.data(), "GAJE", 4);
+    memcpy(buf.data() + 4, &count, 4);
+    memcpy(buf.data() + 8, idx.data(), (size_t)count * 4);
+    memcpy(buf.data() + 8 + (size_t)count * 4, val.data(), (size_t)count * 2);
+    memcpy(buf.data() + 8 + (size_t)count * 6, ptr.data(), ptr.size() * 8);
+    return buf;
+}
+
 // One directory entry plus the generator of its bytes.
 struct Blob {
     std::string name;
     uint64_t bit_depth, out_f, in_f;
     uint64_t dna_len, c_len, bias_len;  // bytes
     uint64_t dna_off = 0, c_off = 0, anc_off = 0, bias_off = 0;
+    std::vector<uint8_t> anchors;       // the GAJE anchor buffer, empty for none
     // generators: 0 normal f32, 1 q4_0, 2 lut4, 3 norm weights, 4 normal f32 quantised to Q8_0,
     // 5 2-bit codes and centroids
     int kind;
@@ -325,6 +373,7 @@ extern "C" int gaje_synth_write_flat(const char *path, const gaje_synth_config *
             b.dna_len = (uint64_t)(out_f * nb * 16);
             b.c_len = (uint64_t)(out_f * nb * 16 * 4);
         }
+        if (c.anchors) b.anchors = gen_anchors(c.seed, name, out_f, in_f, c.anchors);
         return b;
     };
 
@@ -343,8 +392,9 @@ extern "C" int gaje_synth_write_flat(const char *path, const gaje_synth_config *
         }
         return b;
     };
-    if (c.quant_embed < 0 || c.quant_embed > 2 || c.g2_tables < 0 || c.g2_tables > 3)
-        return set_error(GAJE_ERR_INVALID_ARG, "gaje_synth_write_flat: quant_embed 0-2, g2_tables 0-3");
+    if (c.quant_embed < 0 || c.quant_embed > 2 || c.g2_tables < 0 || c.g2_tables > 3 || c.anchors < 0 ||
+        c.anchors > 3)
+        return set_error(GAJE_ERR_INVALID_ARG, "gaje_synth_write_flat: quant_embed 0-2, g2_tables 0-3, anchors 0-3");
     if (c.quant_embed && h % 32)
         return set_error(GAJE_ERR_INVALID_ARG, "gaje_synth_write_flat: quantised embeddings need n_embd %% 32 == 0");
     blobs.push_back(embed("token_embd", "token_embd"));
@@ -398,6 +448,7 @@ extern "C" int gaje_synth_write_flat(const char *path, const gaje_synth_config *
         b.c_off = cur;
         cur = align64(cur + b.c_len);
         b.anc_off = cur;
+        cur = align64(cur + b.anchors.size());
         if (b.has_bias) {
             b.bias_off = cur;
             cur = align64(cur + b.bias_len);
@@ -420,10 +471,11 @@ extern "C" int gaje_synth_write_flat(const char *path, const gaje_synth_config *
         snprintf(buf, sizeof buf,
                  "%s{\"name\": \"%s\", \"bit_depth\": %llu, \"out_features\": %llu, \"in_features\": %llu, "
                  "\"dna_off\": %llu, \"dna_len\": %llu, \"c_off\": %llu, \"c_len\": %llu, \"anc_off\": %llu, "
-                 "\"anc_len\": 0, \"bias_off\": %llu, \"bias_len\": %llu}",
+                 "\"anc_len\": %llu, \"bias_off\": %llu, \"bias_len\": %llu}",
                  i ? ", " : "", b.name.c_str(), (unsigned long long)b.bit_depth, (unsigned long long)b.out_f,
                  (unsigned long long)b.in_f, (unsigned long long)b.dna_off, (unsigned long long)b.dna_len,
                  (unsigned long long)b.c_off, (unsigned long long)b.c_len, (unsigned long long)b.anc_off,
+                 (unsigned long long)b.anchors.size(),
                  (unsigned long long)(b.has_bias ? b.bias_off : 0), (unsigned long long)(b.has_bias ? b.bias_len : 0));
         dir += buf;
     }
@@ -499,6 +551,7 @@ extern "C" int gaje_synth_write_flat(const char *path, const gaje_synth_config *
         }
         put(dna.data(), b.dna_off, b.dna_len);
         if (b.c_len) put(lut.data(), b.c_off, b.c_len);
+        if (!b.anchors.empty()) put(b.anchors.data(), b.anc_off, b.anchors.size());
         if (b.has_bias) {
             std::vector<float> bias(b.bias_len / 4);
             gen_normal(c.seed, b.bias_stream, (int64_t)bias.size(), 0.0, 0.02, bias.data());

@@ -86,7 +86,7 @@ class SynthConfig(ctypes.Structure):
                 ("body_format", ctypes.c_int32), ("fused", ctypes.c_int32),
                 ("rope_interleaved", ctypes.c_int32), ("use_genomic_norm", ctypes.c_int32),
                 ("quant_embed", ctypes.c_int32), ("g2_tables", ctypes.c_int32),
-                ("seed", ctypes.c_uint64)]
+                ("anchors", ctypes.c_int32), ("seed", ctypes.c_uint64)]
 
 
 # (name, restype, argtypes): every symbol include/gaje_hip.h declares.
@@ -165,6 +165,8 @@ SIGNATURES = [
     ("gaje_hip_bench_gemv", ctypes.c_int, [ctypes.c_int, c_vp, ctypes.c_size_t, c_vp, ctypes.c_size_t,
                                            ctypes.c_int, c_vp, c_vp, c_i64, c_i64, ctypes.c_int,
                                            ctypes.POINTER(ctypes.c_float)]),
+    ("gaje_hip_bench_floor", ctypes.c_int, [c_vp, c_i64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                            ctypes.POINTER(ctypes.c_float)]),
     ("gaje_flat_header_from_bytes", ctypes.c_int, [c_vp, ctypes.c_size_t, ctypes.POINTER(FlatHeader)]),
     ("gaje_flat_inspect", ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(FlatInfo)]),
     ("gaje_flat_tensor_entry", ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(FlatTensor)]),

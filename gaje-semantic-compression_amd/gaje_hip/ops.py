@@ -226,6 +226,15 @@ def bench_gemv(fmt: int, w: DeviceBuffer, copy_stride: int, copies: int, x: Devi
     return ms.value
 
 
+def bench_floor(buf: DeviceBuffer | None, nbytes: int, grid: int, block: int, iters: int) -> float:
+    """Average ms per launch of an empty kernel (nbytes == 0) or of a plain read of
+    nbytes of buf, with the given grid (graph replays, as bench_gemv)."""
+    ms = ctypes.c_float()
+    check(lib().gaje_hip_bench_floor(_p(buf), int(nbytes), int(grid), int(block), int(iters),
+                                     ctypes.byref(ms)))
+    return ms.value
+
+
 class Stream:
     def __init__(self):
         s = ctypes.c_void_p()

@@ -347,6 +347,14 @@ int gaje_hip_bench_gemv(int format, const void *w_base, size_t copy_stride, cons
                         size_t lut_stride, int copies, const float *x, float *y, int64_t n, int64_t k,
                         int iters, float *avg_ms);
 
+/* Average device time per launch of a floor probe, timed as
+ * gaje_hip_bench_gemv times its launches: bytes == 0 launches an empty kernel
+ * of grid x block threads (the launch boundary alone); bytes >= 256 a plain
+ * read of the first `bytes` of the device buffer buf (16-byte loads, block <=
+ * 256), whose first 256 bytes it may overwrite.  No reference counterpart:
+ * the floors that a matvec launch of the same grid cannot go below. */
+int gaje_hip_bench_floor(const void *buf, int64_t bytes, int grid, int block, int iters, float *avg_ms);
+
 /* ------------------------------------------------- .gaje.flat reader --- */
 /* Host-only entry points over the reader that gaje_hip_open uses, so a
  * file can be inspected (and the reader tested) without a GPU. */
@@ -407,6 +415,10 @@ typedef struct {
     int32_t quant_embed;           /* 1 = token_embd / lm_head as Q8_0 (bit_depth 8, --quant-embed), 2 = as 2-bit */
     int32_t g2_tables;             /* 2-bit centroid tables: 0 per (row, block), 1 per block column,
                                       2 one shared table, 3 the first half of the rows' tables + 6 floats */
+    int32_t anchors;               /* sparse f16 anchors on every body tensor (GenomicLinear::new's
+                                      "GAJE" buffer, init.rs:61-107): 0 none, 1 with n+1 row pointers
+                                      (some column indices past in_features, one inverted row range),
+                                      2 with genomize_4bit_core's two pointers, 3 with none */
     uint64_t seed;
 } gaje_synth_config;
 

@@ -21,6 +21,9 @@ HD64 = dict(n_embd=256, n_head=4, n_head_kv=2, n_blocks=2, ffn=512, vocab_size=1
 # gate/up rows >= 16384: the two-rows-per-lane batched matvec
 WIDE = dict(n_embd=128, n_head=4, n_head_kv=2, n_blocks=1, ffn=8192, vocab_size=1000, eps=1e-6,
             rope_base=1e4, arch_family=1, qkv_bias=1, tied_embeddings=0)
+# the same rows with K = 1024: the two-rows-per-lane matvec over two activation chunks
+WIDE_K = dict(n_embd=1024, n_head=8, n_head_kv=2, n_blocks=1, ffn=8192, vocab_size=1000, eps=1e-6,
+              rope_base=1e4, arch_family=1, qkv_bias=1, tied_embeddings=0)
 HD128 = dict(n_embd=256, n_head=2, n_head_kv=1, n_blocks=1, ffn=256, vocab_size=512, eps=1e-6,
              rope_base=1e4, arch_family=1, qkv_bias=1, tied_embeddings=0)
 
@@ -82,7 +85,8 @@ def _oracle_run(O, path, prompt, n_gen):
 
 @pytest.mark.parametrize("cfg,name,n_seq,lengths", [(TINY, "tiny", 3, [5, 9, 7]), (HD64, "hd64", 5, [12, 4, 8]),
                                                     (HD64, "hd64", 16, [6]), (TINY, "tiny", 1, [10]),
-                                                    (WIDE, "wide", 16, [5, 3]), (WIDE, "wide", 8, [4])])
+                                                    (WIDE, "wide", 16, [5, 3]), (WIDE, "wide", 8, [4]),
+                                                    (WIDE_K, "widek", 16, [4, 2]), (WIDE_K, "widek", 11, [3])])
 def test_batch_matches_independent_runs(hip, O, tmp_models, cfg, name, n_seq, lengths):
     p = _write(hip, tmp_models / f"batch_{name}.flat", seed=21, **cfg)
     prompts = _prompts(n_seq, lengths, cfg["vocab_size"], 22 + n_seq)
@@ -134,14 +138,16 @@ def test_batch_long_context_hd128(hip, O, tmp_models, lengths):
     g.close()
 
 
-def test_batch_benchmark_shape(hip, O, tmp_models):
-    """The Qwen2.5-1.5B block shapes (hd 128, GQA 6:1, ffn 8960, QKV bias), two blocks."""
+@pytest.mark.parametrize("n_seq", [4, 11, 16])
+def test_batch_benchmark_shape(hip, O, tmp_models, n_seq):
+    """The Qwen2.5-1.5B block shapes (hd 128, GQA 6:1, ffn 8960, QKV bias), two blocks; at 16 and
+    11 sequences the 17920-row gate_up runs the two-rows-per-lane matvec over three chunks."""
     p = _write(hip, tmp_models / "batch_c3_2blk.flat", preset="qwen2.5-1.5b", seed=0, n_blocks=2,
                vocab_size=4096)
-    prompts = _prompts(4, [12], 4096, 31)
+    prompts = _prompts(n_seq, [12], 4096, 31)
     g = hip.load_genomic_auto(p)
     g.set_k_wta_ratio(0.0)
-    b = hip.GenomicBatch(g, 4, 128)
+    b = hip.GenomicBatch(g, n_seq, 128)
     logits = b.feed(_padded(prompts, hip.BATCH_INACTIVE), want_logits=True)
     firsts = []
     refs = []
@@ -151,8 +157,8 @@ def test_batch_benchmark_shape(hip, O, tmp_models):
         firsts.append(toks[0])
         refs.append(toks)
     out = b.decode_greedy(firsts, 4)
-    for s in range(4):
-        assert list(out[s][:3]) == refs[s][1:]
+    for s in range(n_seq):
+        assert list(out[s][:3]) == refs[s][1:], f"sequence {s}"
     b.close()
     g.close()
 

@@ -122,6 +122,28 @@ def test_tiny_block_kwta(hip, O, tiny):
     g.close()
 
 
+def test_tiny_block_kwta_ratio_change(hip, O, tiny):
+    """Changing the ratio on one handle changes the blocks' k (block/forward.rs:144-148)
+    in the captured token step: 0.75, decode, 0.25, decode, then off."""
+    g = hip.load_genomic_auto(tiny)
+    r = O.load_genomic(tiny)
+    toks = _tokens(9, TINY["vocab_size"], 12)
+    for j, ratio in enumerate((0.75, 0.25, 0.0, 0.75)):
+        g.set_k_wta_ratio(ratio)
+        r.set_k_wta_ratio(ratio)
+        for i, t in enumerate(toks[j * 2:j * 2 + 3]):
+            gl = g.forward(t, j == 0 and i == 0)
+            rl = r.forward_core(t, j == 0 and i == 0)
+            assert same_bits(gl, rl), f"ratio {ratio}: logits differ at token {i}"
+        # the greedy loop replays the same graph
+        out = g.decode_greedy(toks[j], 2)
+        feed = int(toks[j])
+        for tok in out:
+            assert int(tok) == O.argmax_first(r.forward_core(feed, False))
+            feed = int(tok)
+    g.close()
+
+
 def _check_greedy(gen, O, path, first, n, prompt=None):
     r = O.load_genomic(path)
     r.set_k_wta_ratio(0.0)

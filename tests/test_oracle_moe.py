@@ -43,3 +43,75 @@ def test_moe_route_ties_and_logits():
     assert list(idx[0]) == [2, 0]
     # the logits are the reference dot_product (a single exact case)
     assert O.dot_f32(x[0], router[2]) == 1.0
+
+
+def _random_q4_0(rng, n, k):
+    """n rows of k/32 Q4_0Blocks: codes uniform in 0..15, f16 scale in
+    [0.01, 0.05), min = -7.5 * scale (a centred affine grid)."""
+    nb = n * k // 32
+    scale = rng.uniform(0.01, 0.05, nb).astype(np.float16)
+    mn = (np.float32(-7.5) * scale.astype(np.float32)).astype(np.float16)
+    codes = rng.integers(0, 16, (nb, 32)).astype(np.uint8)
+    blk = np.zeros((nb, 20), np.uint8)
+    blk[:, 0:2] = scale.view(np.uint8).reshape(nb, 2)
+    blk[:, 2:4] = mn.view(np.uint8).reshape(nb, 2)
+    blk[:, 4:] = codes[:, 0::2] | (codes[:, 1::2] << 4)
+    return blk.reshape(-1)
+
+
+def _moe_f64(x, idx, w, gate_up, down, ffn):
+    """The MoE layer composed in float64 from the exactly dequantised experts:
+    y_t = w_a FFN_a(x_t) + w_b FFN_b(x_t), FFN_e(x) = D_e (silu(g) * u) with
+    [g; u] = GU_e x and silu taken on the gate clamped to [-64, 64]
+    (activation.rs:35-51: sigma of the clamped gate times the raw gate)."""
+    from oracle import oracle as O
+    h = x.shape[1]
+    GU = [O.q4_0_dequant(b).astype(np.float64).reshape(2 * ffn, h) for b in gate_up]
+    D = [O.q4_0_dequant(b).astype(np.float64).reshape(h, ffn) for b in down]
+    y = np.zeros(x.shape, np.float64)
+    for t in range(x.shape[0]):
+        for k in range(2):
+            e = int(idx[t, k])
+            gu = GU[e] @ x[t].astype(np.float64)
+            g, u = gu[:ffn], gu[ffn:]
+            sig = 1.0 / (1.0 + np.exp(-np.clip(g, -64.0, 64.0)))
+            y[t] += float(w[t, k]) * (D[e] @ (g * sig * u))
+    return y
+
+
+def _rel(got, ref):
+    from conftest import floored_rel_err
+    return floored_rel_err(got, ref)
+
+
+def test_moe_ffn_against_float64_composition(monkeypatch):
+    """The oracle's expert dispatch and combine against a float64 composition of
+    the same routing; a swapped pair of routing weights, a wrong expert for the
+    second slot, or gate and up exchanged in the oracle each leave the bound."""
+    from oracle import oracle as O
+    rng = np.random.default_rng(11)
+    T, h, ffn, E = 10, 64, 96, 4
+    x = rng.standard_normal((T, h)).astype(np.float32)
+    router = (0.3 * rng.standard_normal((E, h))).astype(np.float32)
+    gate_up = [_random_q4_0(rng, 2 * ffn, h) for _ in range(E)]
+    down = [_random_q4_0(rng, h, ffn) for _ in range(E)]
+    y, idx, w = O.moe_ffn(x, router, gate_up, down, ffn)
+    assert not np.array_equal(w[:, 0], w[:, 1])  # the swap below changes something
+    ref = _moe_f64(x, idx, w, gate_up, down, ffn)
+    err = _rel(y, ref)
+    assert err < 1e-4, err  # float32 rounding of two chained products and the combine
+
+    route = O.moe_route
+    # slip 1: the routing weights swapped between the two experts
+    monkeypatch.setattr(O, "moe_route", lambda x_, r_: (route(x_, r_)[0], route(x_, r_)[1][:, ::-1].copy()))
+    assert _rel(O.moe_ffn(x, router, gate_up, down, ffn)[0], ref) > 1e-2
+    # slip 2: the second slot takes the next expert
+    monkeypatch.setattr(O, "moe_route", lambda x_, r_: (np.stack([route(x_, r_)[0][:, 0],
+                                                                  (route(x_, r_)[0][:, 1] + 1) % E], 1),
+                                                        route(x_, r_)[1]))
+    assert _rel(O.moe_ffn(x, router, gate_up, down, ffn)[0], ref) > 1e-2
+    monkeypatch.setattr(O, "moe_route", route)
+    # slip 3: gate and up exchanged
+    sw = O.swiglu_balanced
+    monkeypatch.setattr(O, "swiglu_balanced", lambda g, u: sw(u, g))
+    assert _rel(O.moe_ffn(x, router, gate_up, down, ffn)[0], ref) > 1e-2
