@@ -127,12 +127,50 @@ __device__ __forceinline__ X4 read_x4(const float *xg) {
 // One full packed group (blocks 4g .. 4g+3): the sixteen dequantised values
 // are formed before the chain consumes them, so the conversions overlap the
 // LDS reads instead of alternating with the dependent FMAs.
+//
+// The codes are never converted to float on their own.  A 4-bit code q masked
+// into bits 0..3 of a 16-bit half is the f16 subnormal q * 2^-24, and masked
+// into bits 4..7 it is q * 2^-20; v_fma_mix_f32 reads such a half exactly, so
+// fma(q * 2^-k, scale * 2^k, min) with the f32 scale * 2^k (exact: a power-of-
+// two shift of an f16) has the exact product q * scale and rounds once, the
+// same value as fma(q, scale, min) for every scale and min.  A chain dword h
+// holds block 2h's codes in the low nibbles (element c in byte c) and block
+// 2h+1's in the high ones, so one AND gives two of block 2h's codes at 2^-24
+// (elements 0 and 2 in the halves) and one two of block 2h+1's at 2^-20; the
+// dword shifted right by 8 gives elements 1 and 3 the same way.  Per group
+// that is 2 shifts, 8 ANDs and 4 scale products instead of 16 byte-to-float
+// conversions (half-rate instructions) and 6 masks.
+__device__ __forceinline__ float f16_lo(uint32_t v) {
+    union { uint16_t u; _Float16 h; } c;
+    c.u = (uint16_t)v;
+    return (float)c.h;
+}
+__device__ __forceinline__ float f16_hi(uint32_t v) {
+    union { uint16_t u; _Float16 h; } c;
+    c.u = (uint16_t)(v >> 16);
+    return (float)c.h;
+}
+
+// The four values of block 2h (dq = 0) or 2h+1 (dq = 1) of chain dword n,
+// with sm its scale | min << 16 word.
+template <int DQ>
+__device__ __forceinline__ void q4_dequant_dw(float (&d)[4], uint32_t n, uint32_t sm) {
+    constexpr uint32_t M = DQ ? 0x00F000F0u : 0x000F000Fu;
+    const float S = half_lo(sm) * (DQ ? 1048576.0f : 16777216.0f);  // scale * 2^20 or 2^24, exact
+    const float mn = half_hi(sm);
+    const uint32_t e02 = opaque_and(n, M), e13 = opaque_and(n >> 8, M);
+    d[0] = fmaf(f16_lo(e02), S, mn);
+    d[1] = fmaf(f16_lo(e13), S, mn);
+    d[2] = fmaf(f16_hi(e02), S, mn);
+    d[3] = fmaf(f16_hi(e13), S, mn);
+}
+
 __device__ __forceinline__ float q4_group(float acc, const vu2 n, const vu4 s, const X4 &x) {
     float d0[4], d1[4], d2[4], d3[4];
-    q4_dequant(d0, opaque_and(n.x, 0x0F0F0F0Fu), s.x);
-    q4_dequant(d1, opaque_and(n.x >> 4, 0x0F0F0F0Fu), s.y);
-    q4_dequant(d2, opaque_and(n.y, 0x0F0F0F0Fu), s.z);
-    q4_dequant(d3, opaque_and(n.y >> 4, 0x0F0F0F0Fu), s.w);
+    q4_dequant_dw<0>(d0, n.x, s.x);
+    q4_dequant_dw<1>(d1, n.x, s.y);
+    q4_dequant_dw<0>(d2, n.y, s.z);
+    q4_dequant_dw<1>(d3, n.y, s.w);
     acc = q4_chain(acc, d0, x.b0);
     acc = q4_chain(acc, d1, x.b1);
     acc = q4_chain(acc, d2, x.b2);
@@ -1167,6 +1205,308 @@ __global__ __launch_bounds__(THREADS) void gemv_q8_stream_kernel(GemvParams p, i
     }
 }
 
+// ------------------------------------------ Q4_0 rows through LDS-direct ----
+// Rows of at most 8 packed groups (K <= 1024) streamed through LDS.  A wave
+// walks 8-row tiles (tile t = rows 8t..8t+7, whose packed bytes are one
+// contiguous run; a SwiGLU tile adds the up rows ffn+8t..): it copies each
+// tile into its own LDS stages with global_load_lds_dwordx4 (each lane 16
+// bytes, one KiB per instruction, no VGPRs), up to Q4L stages ahead, and lane
+// (row r, chain l) then reads its chain's codes (8 bytes) and the group's
+// scale/min words (16 bytes, the same for the row's 8 lanes) from LDS.  Against
+// loading them into VGPRs this issues a fifth of the load instructions and
+// fetches the scale/min words once instead of eight times.  The values, the
+// chain order and the reduction are q4_consume's: a row's last group is zero
+// past its nb blocks in the packed layout (scale = min = 0, codes 0), and the
+// activation rows are zero there too, so fma(+0, +0, acc) leaves the chain as
+// it is.
+//
+// Every load of the kernel is such a copy (the activations, the norm weights
+// and the exponential's table too), issued as inline assembly so that the
+// compiler's wait-count model, which would otherwise wait for all of them
+// before each LDS read, leaves them alone; the kernel waits for its own copies
+// with explicit s_waitcnt vmcnt counts.  Loads return in order, so "at most n
+// outstanding" means every copy but the last n has landed.  A wave only reads
+// the stages it filled itself, so no barrier orders them; the shared prologue
+// data is copied by wave 0 before its tiles and published with a barrier.
+
+// LDS byte address of a pointer into the workgroup's shared memory.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)p;
+}
+
+// One wave instruction: each active lane copies the 16 bytes at g into LDS at
+// lds + 16 * lane (lds is wave-uniform).  M0 is set inside the statement; the
+// kernels that use it hold nothing else in M0 (checked in their assembly).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_dma16(const void *g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt"
+                 :
+                 : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds))
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// A 32-bit load through the scalar data cache (uniform address), waited for.
+__device__ __forceinline__ int32_t s_load_i32(const void *p) {
+    int32_t v;
+    asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p) : "memory");
+    return v;
+}
+
+// s_waitcnt for at most n outstanding vector memory operations (gfx9 encoding:
+// vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt left at their maxima).
+template <int n>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(n >= 0 && n < 64, "vmcnt is six bits");
+    __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// wait_vmcnt<k * per> for a wave-uniform k in [0, KMAX].
+template <int per, int KMAX>
+__device__ __forceinline__ void wait_vmcnt_stages(int k) {
+    if constexpr (KMAX > 0) {
+        if (k >= KMAX) {
+            wait_vmcnt<KMAX * per>();
+            return;
+        }
+        wait_vmcnt_stages<per, KMAX - 1>(k);
+    } else {
+        wait_vmcnt<0>();
+    }
+}
+
+// wait_vmcnt<a * NA + b * NB> for wave-uniform a, b in [0, KMAX].
+template <int NA, int NB, int KMAX, int A = KMAX, int B = KMAX>
+__device__ __forceinline__ void wait_vmcnt_ab(int a, int b) {
+    static_assert(KMAX * (NA + NB) < 64, "vmcnt is six bits");
+    if (a == A && b == B) {
+        wait_vmcnt<A * NA + B * NB>();
+        return;
+    }
+    if constexpr (B > 0) wait_vmcnt_ab<NA, NB, KMAX, A, B - 1>(a, b);
+    else if constexpr (A > 0) wait_vmcnt_ab<NA, NB, KMAX, A - 1, KMAX>(a, b);
+    else wait_vmcnt<0>();
+}
+
+// Copies the N KiB from byte `off` of the weights into LDS at `dst` (wave
+// uniform).  Lanes whose bytes lie past `limit` (the bytes the tensor's
+// allocation holds, padding included) read the tensor's first bytes instead:
+// those LDS bytes belong to rows past the last one, which are never stored.
+template <int N>
+__device__ __forceinline__ void q4l_copy(const uint8_t *w, int64_t off, int64_t limit, uint32_t dst, int lane) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        int64_t a = off + i * 1024 + lane * 16;
+        a = a + 16 <= limit ? a : 0;
+        lds_dma16(w + a, dst + i * 1024);
+    }
+}
+
+// Copies n bytes (n % 16 == 0) from g to LDS at dst with one wave.
+__device__ __forceinline__ void lds_copy_bytes(const void *g, int64_t n, uint32_t dst, int lane) {
+    for (int64_t o = 0; o < n; o += 1024)
+        if (o + lane * 16 < n) lds_dma16((const uint8_t *)g + o + lane * 16, dst + (uint32_t)o);
+}
+
+// Chain l of the rows at rp0 and rp1 (LDS), interleaved: groups 0..G-1 in
+// order, then the reduction and the flush (q4_consume's sequence).  xr holds
+// chain l's activations (16 per group), in registers for the whole kernel.
+// Lane `base` holds the rows.
+template <int G>
+__device__ __forceinline__ void q4l_rows2(const uint8_t *rp0, const uint8_t *rp1, const float4 (&xr)[4 * G], int l,
+                                          int base, float &y0, float &y1) {
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const vu2 n0 = *(const vu2 *)(rp0 + g * 80 + 8 * l), n1 = *(const vu2 *)(rp1 + g * 80 + 8 * l);
+        const vu4 s0 = *(const vu4 *)(rp0 + g * 80 + 64), s1 = *(const vu4 *)(rp1 + g * 80 + 64);
+        const X4 x{xr[4 * g], xr[4 * g + 1], xr[4 * g + 2], xr[4 * g + 3]};
+        a0 = q4_group(a0, n0, s0, x);
+        a1 = q4_group(a1, n1, s1, x);
+    }
+    float u = a0 + shfl(a0, base + ((l + 4) & 7)), v = u + shfl(u, base + ((l + 2) & 7));
+    y0 = flush_small(v + shfl(v, base + ((l + 1) & 7)));
+    u = a1 + shfl(a1, base + ((l + 4) & 7));
+    v = u + shfl(u, base + ((l + 2) & 7));
+    y1 = flush_small(v + shfl(v, base + ((l + 1) & 7)));
+}
+
+// One chain: q4l_rows2 for the row at rp alone.
+template <int G>
+__device__ __forceinline__ float q4l_row1(const uint8_t *rp, const float4 (&xr)[4 * G], int l, int base) {
+    float a = 0.0f;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const vu2 n = *(const vu2 *)(rp + g * 80 + 8 * l);
+        const vu4 sm = *(const vu4 *)(rp + g * 80 + 64);
+        a = q4_group(a, n, sm, X4{xr[4 * g], xr[4 * g + 1], xr[4 * g + 2], xr[4 * g + 3]});
+    }
+    const float u = a + shfl(a, base + ((l + 4) & 7)), v = u + shfl(u, base + ((l + 2) & 7));
+    return flush_small(v + shfl(v, base + ((l + 1) & 7)));
+}
+
+// Modes: MODE_STORE (y[r] = row r; a tile is 8 ROWS rows, lane (r, l) walks
+// rows r (and r + 8)) and MODE_SWIGLU (y[p] = swiglu(row p, row p + ffn) with
+// the NaN guards of block/forward.rs:97-113; a tile is 8 gate rows and their
+// up rows, lane (r, l) walks gate row r and its up row).  No bias, anchors or
+// genomic norm (the launcher routes those elsewhere).  G = packed groups per
+// row.
+template <int MODE, int WAVES, int STAGES, int G, int ROWS>
+__global__ __launch_bounds__(WAVES * WAVE) void gemv_q4_lds_kernel(GemvParams p, int xstride, int64_t limit, int raw_bytes) {
+    static_assert(ROWS == 2 || (ROWS == 1 && MODE == MODE_STORE), "one or two rows per lane");
+    constexpr int ROW_BYTES = G * 80;
+    constexpr int TROWS = MODE == MODE_SWIGLU ? 4 * ROWS : 8 * ROWS;  // output rows per tile
+    constexpr int HALF = (TROWS * ROW_BYTES + 1023) / 1024;           // copies per TROWS rows
+    constexpr int PER = MODE == MODE_SWIGLU ? 2 * HALF : HALF;        // copies per stage
+    extern __shared__ __align__(16) float smem[];
+    __shared__ float inv_slot;
+    __shared__ int or_in[WAVES], or_norm[WAVES];
+    DevState *st = p.st;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l = lane & 7, r = lane >> 3, base = lane - l;
+    const int64_t K4 = p.K >> 2;
+    const XView xv{smem, xstride};
+    uint8_t *raw = (uint8_t *)(smem + 8 * xstride);  // x, then norm_w, then the exponential table
+    uint8_t *stages = raw + raw_bytes + (size_t)wave * STAGES * PER * 1024;
+    const int64_t rows = MODE == MODE_SWIGLU ? p.ffn : p.N;
+    const int64_t ntiles = (rows + TROWS - 1) / TROWS;
+    const int64_t gw = (int64_t)blockIdx.x * WAVES + wave, nw = (int64_t)gridDim.x * WAVES;
+    // tile t: rows 8 ROWS t.. (store), or gate rows 8t.. then up rows ffn + 8t..
+    auto issue = [&](int64_t t, int stage) {
+        const uint32_t dst = lds_addr(stages + stage * PER * 1024);
+        if constexpr (MODE == MODE_SWIGLU) {
+            q4l_copy<HALF>(p.w, t * TROWS * ROW_BYTES, limit, dst, lane);
+            q4l_copy<HALF>(p.w, (t * TROWS + p.ffn) * ROW_BYTES, limit, dst + HALF * 1024, lane);
+        } else {
+            q4l_copy<PER>(p.w, t * TROWS * ROW_BYTES, limit, dst, lane);
+        }
+    };
+
+    // ---- prologue: wave 0 copies the activations (and the norm weights and
+    // the exponential's table), then every wave its first tiles ----
+    const int64_t xb = p.K * 4;  // raw layout: x [0, xb), norm_w [xb, 2 xb), exp table after
+    const int64_t tb = p.norm_w ? 2 * xb : xb;
+    if (wave == 0) {
+        lds_copy_bytes(p.x, xb, lds_addr(raw), lane);
+        if (p.norm_w) lds_copy_bytes(p.norm_w, xb, lds_addr(raw + xb), lane);
+        if (MODE == MODE_SWIGLU) lds_copy_bytes(kExp2Tab, 256, lds_addr(raw + tb), lane);
+    }
+    int first = 0;  // tiles this wave has in flight
+    for (int i = 0; i < STAGES; ++i)
+        if (gw + i * nw < ntiles) {
+            issue(gw + i * nw, i);
+            ++first;
+        }
+    if (st && s_load_i32(&st->halted)) {
+        wait_vmcnt<0>();  // no copy may land after the workgroup's LDS is released
+        return;  // uniform
+    }
+    if (wave == 0) wait_vmcnt_stages<PER, STAGES>(first);  // the shared data has landed
+    lds_barrier();
+    const float *xraw = (const float *)raw, *wraw = (const float *)(raw + xb);
+    const uint64_t *etab = (const uint64_t *)(raw + tb);
+    constexpr int NT = WAVES * WAVE;
+    int bad_in = 0;
+    for (int64_t m = tid; m < K4; m += NT) {
+        const float4 v = *(const float4 *)(xraw + 4 * m);
+        const float q[4] = {v.x, v.y, v.z, v.w};
+        store_quad<true>(xv, (int)m, q);
+        bad_in |= isnan(v.x) || isnan(v.y) || isnan(v.z) || isnan(v.w);
+    }
+    q4_zero_x_pad(xv, p.nb);
+    if (barrier_or<WAVES>(bad_in, or_in) && p.st_in >= 0 && tid == 0) nan_flag(st, p.layer, p.st_in);
+    if (p.norm_w) {
+        rms_inv_chain_major(xv, p.K, p.eps, &inv_slot);
+        lds_barrier();
+        const float inv = inv_slot;
+        int bad = 0;
+        for (int64_t m = tid; m < K4; m += NT) {
+            const float4 xq = *(const float4 *)(xraw + 4 * m), wq = *(const float4 *)(wraw + 4 * m);
+            float t[4] = {xq.x * inv, xq.y * inv, xq.z * inv, xq.w * inv};
+            const float w[4] = {wq.x, wq.y, wq.z, wq.w};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                t[c] = t[c] * w[c];  // (x * inv) * w, each product rounded
+                bad |= isnan(t[c]);
+            }
+            store_quad<true>(xv, (int)m, t);
+        }
+        if (barrier_or<WAVES>(bad, or_norm) && p.st_norm >= 0 && tid == 0) nan_flag(st, p.layer, p.st_norm);
+    }
+
+    // ---- tiles: wait for the oldest stage, walk its rows, store them, refill
+    // the stage with the tile STAGES ahead.  Issued after this stage's copies
+    // are the stores of the last min(it, STAGES - 1) tiles (NST each: rows past
+    // the end store into a sink, so the count is fixed) and the copies of the
+    // next min(left, STAGES - 1) tiles; the wait lets exactly those remain
+    // (a NaN flag's atomic only makes it wait longer). ----
+    constexpr int NST = MODE == MODE_SWIGLU ? 1 : ROWS;
+    float4 xr4[4 * G];  // chain l's activations, read once
+    {
+        const float *xg = xv.x + l * xv.stride;
+#pragma unroll
+        for (int i = 0; i < 4 * G; ++i) xr4[i] = *(const float4 *)(xg + 4 * i);
+    }
+    int stage = 0, it = 0;
+    int64_t left = gw < ntiles ? (ntiles - 1 - gw) / nw : 0;  // this wave's tiles after t
+    for (int64_t t = gw; t < ntiles; t += nw, --left, ++it) {
+        wait_vmcnt_ab<NST, PER, STAGES - 1>(it < STAGES - 1 ? it : STAGES - 1,
+                                            (int)(left < STAGES - 1 ? left : STAGES - 1));
+        const uint8_t *st0 = stages + stage * PER * 1024;
+        float y0, y1 = 0.0f;
+        if constexpr (MODE == MODE_SWIGLU) {
+            q4l_rows2<G>(st0 + r * ROW_BYTES, st0 + HALF * 1024 + r * ROW_BYTES, xr4, l, base, y0, y1);
+        } else if constexpr (ROWS == 2) {
+            q4l_rows2<G>(st0 + r * ROW_BYTES, st0 + (r + 8) * ROW_BYTES, xr4, l, base, y0, y1);
+        } else {
+            y0 = q4l_row1<G>(st0 + r * ROW_BYTES, xr4, l, base);
+        }
+        if (lane == base) {
+            if constexpr (MODE == MODE_STORE) {
+                const int64_t row = t * TROWS + r;
+                *(row < rows ? p.y + row : kSinkOut + lane) = y0;
+                if constexpr (ROWS == 2) *(row + 8 < rows ? p.y + row + 8 : kSinkOut + lane) = y1;
+            } else {
+                const int64_t row = t * TROWS + r;
+                const bool ok = row < rows;
+                if (ok && isnan(y1)) nan_flag(st, p.layer, p.st_a);
+                const float o = swiglu1(y0, y1, etab);
+                if (ok && isnan(o)) nan_flag(st, p.layer, p.st_b);
+                *(ok ? p.y + row : kSinkOut + lane) = o;
+            }
+        }
+        if (t + STAGES * nw < ntiles) {
+            // the stage's LDS reads have returned: it can be refilled
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+            issue(t + STAGES * nw, stage);
+        }
+        stage = stage + 1 == STAGES ? 0 : stage + 1;
+    }
+    wait_vmcnt<0>();
+}
+
+template <int MODE, int WAVES, int STAGES, int ROWS>
+void *q4l_kernel(int G) {
+    switch (G) {
+        case 1: return (void *)gemv_q4_lds_kernel<MODE, WAVES, STAGES, 1, ROWS>;
+        case 2: return (void *)gemv_q4_lds_kernel<MODE, WAVES, STAGES, 2, ROWS>;
+        case 3: return (void *)gemv_q4_lds_kernel<MODE, WAVES, STAGES, 3, ROWS>;
+        case 4: return (void *)gemv_q4_lds_kernel<MODE, WAVES, STAGES, 4, ROWS>;
+        case 5: return (void *)gemv_q4_lds_kernel<MODE, WAVES, STAGES, 5, ROWS>;
+        case 6: return (void *)gemv_q4_lds_kernel<MODE, WAVES, STAGES, 6, ROWS>;
+        case 7: return (void *)gemv_q4_lds_kernel<MODE, WAVES, STAGES, 7, ROWS>;
+        default: return (void *)gemv_q4_lds_kernel<MODE, WAVES, STAGES, 8, ROWS>;
+    }
+}
+
+// LDS stage bytes of the LDS-staged Q4_0 kernel for rows of G groups.
+int q4l_stage_bytes(int mode, int G, int rows) {
+    const int trows = mode == MODE_SWIGLU ? 4 * rows : 8 * rows;
+    const int half = (trows * G * 80 + 1023) / 1024;
+    return 1024 * (mode == MODE_SWIGLU ? 2 * half : half);
+}
+
 // ------------------------------------------------- Q4_0, split waves ----
 // A matvec with too few rows to fill the chip is bound by the length of one
 // lane's instruction stream, and per element that stream is a byte-to-float
@@ -1544,6 +1884,55 @@ int launch_gemv(const GemvParams &p, hipStream_t s) {
             else if (p.mode == MODE_RESIDUAL) fn = p.norm_w ? gemv_q4_split_kernel<MODE_RESIDUAL, true> : gemv_q4_split_kernel<MODE_RESIDUAL, false>;
             else fn = p.norm_w ? gemv_q4_split_kernel<MODE_STORE, true> : gemv_q4_split_kernel<MODE_STORE, false>;
             hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(THREADS), slds, s, p, npairs, xs);
+            GAJE_HIP_CHECK(hipGetLastError());
+            return GAJE_OK;
+        }
+    }
+    // Q4_0 rows of at most 8 packed groups, every row stored: the LDS-staged
+    // kernel (SwiGLU pairs only as streams: for a few thousand pairs the
+    // row-per-lane kernel, whose four waves share the RMSNorm prologue and
+    // whose lanes each walk one chain, measured faster: 6.7 against 7.5 us at
+    // 4864 pairs of K = 896)
+    if (p.fmt == FMT_Q4_0 && (p.mode == MODE_STORE || p.mode == MODE_SWIGLU) && !p.gnorm && !p.a_ptr && !p.x_out &&
+        p.bias_len == 0 && p.nb > 0 && (p.nb + 3) / 4 <= 8 && p.rows_valid == p.N &&
+        (p.mode == MODE_STORE || (p.ffn + 3) / 4 > 8 * (int64_t)device_cu_count())) {
+        const int64_t rows = p.mode == MODE_SWIGLU ? p.ffn : p.N;
+        const int xs = q4_xstride(p.K);
+        const int G = (p.nb + 3) / 4;
+        const int raw = (int)(p.K * 4 * (p.norm_w ? 2 : 1) + (p.mode == MODE_SWIGLU ? 256 : 0));
+        const size_t fixed = (size_t)8 * xs * 4 + raw + 1024;
+        const bool swiglu = p.mode == MODE_SWIGLU;
+        void *fn = nullptr;
+        int waves = 0, nst = 0;
+        size_t stage = 0;
+        int64_t grid = 0;
+        const int64_t trows1 = swiglu ? 4 : 8;  // output rows per tile with one row per lane
+        if ((rows + trows1 - 1) / trows1 <= 8 * (int64_t)device_cu_count()) {
+            // few tiles (rows, not SwiGLU pairs): one 8-row tile (one row per lane) per
+            // wave, all at once; single-wave workgroups, or four waves sharing one
+            // RMSNorm prologue
+            stage = (size_t)q4l_stage_bytes(p.mode, G, 1);
+            waves = p.norm_w ? 4 : 1;
+            nst = 1;
+            grid = ((rows + trows1 - 1) / trows1 + waves - 1) / waves;
+            fn = p.norm_w ? q4l_kernel<MODE_STORE, 4, 1, 1>(G) : q4l_kernel<MODE_STORE, 1, 1, 1>(G);
+        } else {
+            // streams: persistent workgroups, 16-row tiles (two rows per lane); two waves
+            // per SIMD with two stages each where the LDS holds them, else one with three
+            stage = (size_t)q4l_stage_bytes(p.mode, G, 2);
+            const bool two = fixed + 8 * 2 * stage <= max_lds_per_block();
+            waves = two ? 8 : 4;
+            nst = two ? 2 : 3;
+            const int64_t ntiles = (rows + 2 * trows1 - 1) / (2 * trows1);
+            grid = std::min<int64_t>((ntiles + waves - 1) / waves, device_cu_count());
+            if (swiglu) fn = two ? q4l_kernel<MODE_SWIGLU, 8, 2, 2>(G) : q4l_kernel<MODE_SWIGLU, 4, 3, 2>(G);
+            else fn = two ? q4l_kernel<MODE_STORE, 8, 2, 2>(G) : q4l_kernel<MODE_STORE, 4, 3, 2>(G);
+        }
+        const size_t lds = fixed - 1024 + (size_t)waves * nst * stage;
+        if (lds + 1024 <= max_lds_per_block()) {
+            const int64_t limit = q4_0_packed_bytes(p.N, p.K);
+            hipLaunchKernelGGL((void (*)(GemvParams, int, int64_t, int))fn, dim3((unsigned)grid), dim3(waves * WAVE),
+                               lds, s, p, xs, limit, raw);
             GAJE_HIP_CHECK(hipGetLastError());
             return GAJE_OK;
         }

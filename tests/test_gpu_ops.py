@@ -130,6 +130,20 @@ def test_q4_0_gemv(hip, O, n, k):
     assert same_bits(got, ref)
 
 
+@pytest.mark.parametrize("n,k", [(4864, 896), (963, 576), (5, 32), (9, 96), (11, 160), (64, 1024), (1, 128),
+                                 (4099, 896), (20000, 896), (12345, 576), (16411, 1024), (40, 1056)])
+def test_q4_0_gemv_no_bias(hip, O, n, k):
+    """Rows without a bias and K <= 1024 stream through the LDS-staged matvec: partial
+    last tiles, several tiles per wave (n >= 8192), one-block rows."""
+    blocks = hip.synth.q4_0_tensor(16, f"gemvnb.{n}.{k}", n, k)
+    x = hip.synth.normal(17, f"xnb.{k}", k)
+    y = _out(hip, n * 4)
+    hip.ops.q4_0_gemv(hip.ops.q4_0_upload(blocks, n, k), _dev(hip, x), y, n, k)
+    got = y.read(np.float32)
+    ref = _oracle_q4_rows(O, blocks, x, n, k)
+    assert same_bits(got, ref)
+
+
 def test_q4_0_gemv_flush_rule(hip, O):
     # rows built to cancel exactly: the reference flushes |t| < 1e-6 to 0 before the bias
     k = 64
