@@ -30,6 +30,20 @@ struct DevState {
     unsigned long long argmax_key;  // packed (orderable logit, ~index) maximum
 };
 
+// State of the greedy generate loop kept on the device (generate_native_core,
+// llm/forward.rs:236-327): the generated tokens, their seen-set as a bitmap,
+// the penalty and the EOS ids.  Its kernels run after each token step.
+constexpr int GEN_MAX_EOS = 64;
+struct GenState {
+    int32_t n_gen;             // tokens generated so far (written to the token buffer)
+    int32_t stop;              // 0 running, 1 EOS, 2 repetition-loop detector
+    int32_t n_eos;
+    float penalty;             // repetition_penalty, applied when > 1
+    unsigned long long key;    // penalised argmax (orderable logit, ~index)
+    uint32_t eos[GEN_MAX_EOS];
+};
+enum GenStop : int32_t { GEN_RUNNING = 0, GEN_EOS = 1, GEN_LOOP = 2 };
+
 // NaN guard stages of RustGenomicBlock::forward_core (block/forward.rs).
 enum NanStage : int32_t {
     ST_INPUT = 0,       // "Input x is NaN"                    :11-13
@@ -344,6 +358,14 @@ int launch_moe_combine(const MoeParams &p, const float *Y, hipStream_t s);
 
 int launch_finalize(DevState *st, uint32_t *out_tokens, hipStream_t s);
 int launch_kwta(float *x, int64_t n, int64_t k, DevState *st, hipStream_t s);
+// Greedy generate step on the device: gen_select replaces st->token with the
+// argmax of the penalised logits (penalty > 1) into gs->key; gen_control takes
+// that choice (select) or st->token, appends it to the generated tokens and
+// stops the loop (halting the state) on EOS or a repetition loop.  seen:
+// ceil(n / 32) words.
+int launch_gen_select(const float *logits, int64_t n, const uint32_t *seen, DevState *st, GenState *gs, hipStream_t s);
+int launch_gen_control(DevState *st, GenState *gs, uint32_t *seen, int64_t n_seen, uint32_t *tokens, int select,
+                       hipStream_t s);
 int launch_argmax(const float *x, int64_t n, uint32_t *idx, hipStream_t s);
 int launch_dequant_q4_0(const uint8_t *blocks, float *out, int64_t nblocks, hipStream_t s);
 int launch_dequant_q8_0(const uint8_t *blocks, float *out, int64_t nblocks, hipStream_t s);

@@ -117,6 +117,75 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float *x, int64_t n,
     if (threadIdx.x == 0) *idx = best ? 0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFull) : 0u;
 }
 
+// generate_native_core's penalty and greedy choice (llm/forward.rs:243-271):
+// v = logits[t], and for a generated (seen) t with penalty > 1, v * penalty if
+// v < 0 else v / penalty; the first maximum with a strict '>' (NaN never wins,
+// all -inf/NaN -> 0), folded into gs->key as (orderable v, ~t).  The K-WTA
+// filter (forward_core's) has already been applied to the logits in place.
+__global__ __launch_bounds__(256) void gen_select_kernel(const float *x, int64_t n, const uint32_t *seen,
+                                                        const DevState *st, GenState *gs) {
+    if (st->halted) return;
+    const float pen = gs->penalty;
+    float bv = -INFINITY;
+    int64_t bi = 0;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        float v = x[i];
+        if ((seen[i >> 5] >> (i & 31)) & 1u) v = v < 0.0f ? v * pen : v / pen;
+        if (v > bv) { bv = v; bi = i; }
+    }
+    unsigned long long key = bv > -INFINITY ? ((unsigned long long)order_key(bv) << 32) | (0xFFFFFFFFull - (uint64_t)bi) : 0ull;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const unsigned long long other = __shfl_xor(key, o, WAVE);
+        key = other > key ? other : key;
+    }
+    if ((threadIdx.x & 63) == 0 && key) atomicMax(&gs->key, key);
+}
+
+// The loop's bookkeeping after a token's choice (llm/forward.rs:296-318): the
+// penalised choice (if any) becomes st->token; the token is appended and
+// marked seen (EOS ids are not: an EOS ends the loop, :300-302); then the
+// repetition-loop detector: for w = 2..=48 with n >= 3w, the last three
+// w-long chunks equal -> stop.  A stop halts the state, so later token steps
+// and these kernels do nothing.  One wave; lane w - 2 checks window w.
+__global__ __launch_bounds__(64) void gen_control_kernel(DevState *st, GenState *gs, uint32_t *seen, int64_t n_seen,
+                                                        uint32_t *tokens, int select) {
+    if (st->halted) return;
+    const int lane = threadIdx.x;
+    uint32_t tok = st->token;
+    if (select) {
+        const unsigned long long key = gs->key;
+        tok = key ? 0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFull) : 0u;
+    }
+    const int n = gs->n_gen + 1;  // tokens generated including this one
+    bool eos = false;
+    for (int i = 0; i < gs->n_eos; ++i) eos |= gs->eos[i] == tok;
+    int rep = 0;
+    const int w = lane + 2;
+    if (!eos && w <= 48 && n >= 3 * w) {
+        // chunk [n-w, n) against [n-2w, n-w) and [n-3w, n-2w); token n-1 is tok
+        bool same = true;
+        for (int i = 0; i < w && same; ++i) {
+            const uint32_t a = (n - w + i == n - 1) ? tok : tokens[n - w + i];
+            same = a == tokens[n - 2 * w + i] && a == tokens[n - 3 * w + i];
+        }
+        rep = same;
+    }
+    rep = __any(rep);
+    __syncthreads();
+    if (lane == 0) {
+        tokens[n - 1] = tok;
+        gs->n_gen = n;
+        gs->key = 0ull;
+        st->token = tok;
+        if (!eos && (int64_t)tok < n_seen) atomicOr(&seen[tok >> 5], 1u << (tok & 31));
+        if (eos || rep) {
+            gs->stop = eos ? GEN_EOS : GEN_LOOP;
+            st->halted = 1;
+        }
+    }
+}
+
 // Q4_0Block::dequantize_weight (io/header/blocks.rs:18-30): q*scale then +min,
 // rounded separately (no FMA contraction).
 __global__ void dequant_q4_0_kernel(const uint8_t *blocks, float *out, int64_t nblocks) {
@@ -276,6 +345,21 @@ int launch_swiglu(const float *g, const float *u, float *out, int64_t n, hipStre
     if (n < 0 || (n > 0 && (!g || !u || !out))) return set_error(GAJE_ERR_INVALID_ARG, "swiglu: bad arguments");
     if (n == 0) return GAJE_OK;
     hipLaunchKernelGGL(swiglu_kernel, dim3(grid_for(n, 256)), dim3(256), 0, s, g, u, out, n);
+    GAJE_HIP_CHECK(hipGetLastError());
+    return GAJE_OK;
+}
+
+int launch_gen_select(const float *logits, int64_t n, const uint32_t *seen, DevState *st, GenState *gs, hipStream_t s) {
+    if (!logits || !seen || !st || !gs || n <= 0) return set_error(GAJE_ERR_INVALID_ARG, "gen_select: bad arguments");
+    hipLaunchKernelGGL(gen_select_kernel, dim3(grid_for(n, 256, 256)), dim3(256), 0, s, logits, n, seen, st, gs);
+    GAJE_HIP_CHECK(hipGetLastError());
+    return GAJE_OK;
+}
+
+int launch_gen_control(DevState *st, GenState *gs, uint32_t *seen, int64_t n_seen, uint32_t *tokens, int select,
+                       hipStream_t s) {
+    if (!st || !gs || !seen || !tokens) return set_error(GAJE_ERR_INVALID_ARG, "gen_control: bad arguments");
+    hipLaunchKernelGGL(gen_control_kernel, dim3(1), dim3(64), 0, s, st, gs, seen, n_seen, tokens, select);
     GAJE_HIP_CHECK(hipGetLastError());
     return GAJE_OK;
 }

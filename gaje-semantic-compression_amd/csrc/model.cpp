@@ -283,6 +283,11 @@ struct gaje_hip_model {
     DevState *st = nullptr;
     uint32_t *out_tokens = nullptr;
     int64_t out_cap = 0;
+    // greedy generate loop on the device: its state, the seen-set bitmap and
+    // the generated tokens (grown on demand)
+    GenState *gen = nullptr;
+    uint32_t *gen_seen = nullptr, *gen_tokens = nullptr;
+    int64_t gen_cap = 0;
     // KV cache and RoPE table
     float *k_cache = nullptr, *v_cache = nullptr, *rope_cos = nullptr, *rope_sin = nullptr;
     int64_t cap = 0;
@@ -1623,6 +1628,70 @@ extern "C" int gaje_hip_decode_greedy(gaje_hip_model *m, uint32_t first_token, i
     return GAJE_OK;
 }
 
+namespace {
+
+// generate_native_core's greedy loop (temperature <= 1e-5) with the choice,
+// the penalty, EOS and the loop detector on the device: after each token step
+// gen_select (penalty > 1, over the K-WTA-filtered logits) and gen_control run
+// on the stream, and the host only reads the loop's state every GEN_CHUNK
+// tokens to stop enqueuing.  The prompt has been fed; the state's token is
+// the argmax of its last logits.
+constexpr int64_t GEN_CHUNK = 32;
+
+int generate_device(gaje_hip_model *m, int64_t max_new, float repetition_penalty, const uint32_t *eos_ids,
+                    int64_t n_eos, uint32_t *out_tokens, int64_t *n_out) {
+    if (!m->gen) {
+        GAJE_TRY(m->alloc(&m->gen, 1));
+        GAJE_TRY(m->alloc(&m->gen_seen, (size_t)((m->vocab_out + 31) / 32)));
+    }
+    if (max_new > m->gen_cap) {
+        if (m->gen_tokens) m->release(m->gen_tokens);
+        m->gen_tokens = nullptr;
+        m->gen_cap = 0;
+        GAJE_TRY(m->alloc(&m->gen_tokens, (size_t)max_new));
+        m->gen_cap = max_new;
+    }
+    GAJE_TRY(reserve_ctx(m, m->pos + max_new));
+    if (!m->profile) GAJE_TRY(ensure_graph(m));
+    GenState g;
+    memset(&g, 0, sizeof g);
+    g.n_eos = (int32_t)n_eos;
+    g.penalty = repetition_penalty;
+    for (int64_t i = 0; i < n_eos; ++i) g.eos[i] = eos_ids[i];
+    GAJE_HIP_CHECK(hipMemcpyAsync(m->gen, &g, sizeof g, hipMemcpyHostToDevice, m->stream));
+    GAJE_TRY(launch_fill_u32(m->gen_seen, 0u, (m->vocab_out + 31) / 32, m->stream));
+    const bool select = repetition_penalty > 1.0f;
+    const bool kwta = m->kwta_ratio > 0.0f && m->kwta_ratio < 1.0f;
+    DevState s;
+    GenState gs;
+    for (int64_t i = 0; i < max_new;) {
+        const int64_t end = std::min(max_new, i + GEN_CHUNK);
+        for (; i < end; ++i) {
+            if (i > 0) GAJE_TRY(run_token(m));  // forward_core of the previous token
+            if (select) {
+                // forward_core's K-WTA, then the penalised choice (K-WTA keeps the
+                // maximum, so without a penalty the token step's argmax stands)
+                if (kwta) GAJE_TRY(launch_kwta(m->logits, m->vocab_out, kwta_k(m->vocab_out, m->kwta_ratio), m->st, m->stream));
+                GAJE_TRY(launch_gen_select(m->logits, m->vocab_out, m->gen_seen, m->st, m->gen, m->stream));
+            }
+            GAJE_TRY(launch_gen_control(m->st, m->gen, m->gen_seen, m->vocab_out, m->gen_tokens, select, m->stream));
+        }
+        // a loop that ends by count forwards its last token too (llm/forward.rs:320)
+        if (i == max_new) GAJE_TRY(run_token(m));
+        GAJE_HIP_CHECK(hipMemcpyAsync(&gs, m->gen, sizeof gs, hipMemcpyDeviceToHost, m->stream));
+        GAJE_TRY(read_state(m, s));
+        if (s.halted) break;
+    }
+    m->pos = s.pos;
+    if (gs.n_gen > 0)
+        GAJE_HIP_CHECK(hipMemcpy(out_tokens, m->gen_tokens, (size_t)gs.n_gen * 4, hipMemcpyDeviceToHost));
+    if (n_out) *n_out = gs.n_gen;
+    if (s.halted && gs.stop == GEN_RUNNING) return nan_error(s);
+    return GAJE_OK;
+}
+
+}  // namespace
+
 extern "C" int gaje_hip_generate(gaje_hip_model *m, const uint32_t *prompt, int64_t n_prompt, int64_t max_new,
                                  float temperature, float repetition_penalty, const uint32_t *eos_ids, int64_t n_eos,
                                  uint64_t seed, uint32_t *out_tokens, int64_t *n_out) {
@@ -1634,6 +1703,11 @@ extern "C" int gaje_hip_generate(gaje_hip_model *m, const uint32_t *prompt, int6
         return set_error(GAJE_ERR_INVALID_ARG, "bad generate arguments");
     m->pos = 0;  // clear_cache_core
     GAJE_TRY(gaje_hip_prefill(m, prompt, n_prompt, nullptr));
+    if (max_new == 0) return GAJE_OK;
+    if (temperature <= 1e-5f && n_eos <= GEN_MAX_EOS)
+        return generate_device(m, max_new, repetition_penalty, eos_ids, n_eos, out_tokens, n_out);
+    // multinomial sampling (or more EOS ids than the device list holds): the
+    // loop on the host, over the logits of each step
     const bool kwta = m->kwta_ratio > 0.0f && m->kwta_ratio < 1.0f;
     if (kwta) GAJE_TRY(launch_kwta(m->logits, m->vocab_out, kwta_k(m->vocab_out, m->kwta_ratio), m->st, m->stream));
     std::vector<float> logits((size_t)m->vocab_out);

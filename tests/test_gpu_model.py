@@ -202,6 +202,52 @@ def test_tiny_generate_greedy_matches_oracle(hip, O, tiny):
     g.close()
 
 
+def _oracle_generate(O, path, prompt, max_new, penalty, eos, kwta):
+    r = O.load_genomic(path)
+    r.set_k_wta_ratio(kwta)
+    out = r.generate_native_core(prompt, max_new, 0.0, penalty, eos)
+    return out, r.blocks[0].attn.k_cache_len()
+
+
+@pytest.mark.parametrize("penalty,kwta,max_new", [(1.3, 0.0, 40), (1.15, 0.5, 70), (1.0, 0.0, 70),
+                                                  (1.0, 0.5, 33), (2.5, 0.25, 100)])
+def test_tiny_generate_device_loop(hip, O, tiny, penalty, kwta, max_new):
+    """The greedy loop on the device (penalty over the K-WTA-filtered logits, EOS, the
+    loop detector, chunks of 32 steps): the oracle's tokens and cache length."""
+    prompt = _tokens(9, TINY["vocab_size"], 13)
+    g = hip.load_genomic_auto(tiny)
+    g.set_k_wta_ratio(kwta)
+    ref, ref_len = _oracle_generate(O, tiny, prompt, max_new, penalty, [2], kwta)
+    got = g.generate_native_py(prompt, max_new_tokens=max_new, temperature=0.0, repetition_penalty=penalty,
+                               eos_token_ids=[2])
+    print(f"generate penalty {penalty} kwta {kwta}: {len(got)} tokens, ref {len(ref)}")
+    assert got == ref
+    assert g.cache_len() == ref_len
+    g.close()
+
+
+def test_tiny_generate_eos_and_host_path(hip, O, tiny):
+    """An EOS id the stream reaches ends the loop there (the EOS is returned, not fed);
+    more EOS ids than the device list holds take the host loop, with the same tokens."""
+    prompt = _tokens(7, TINY["vocab_size"], 14)
+    g = hip.load_genomic_auto(tiny)
+    g.set_k_wta_ratio(0.0)
+    free = g.generate_native_py(prompt, max_new_tokens=20, temperature=0.0, repetition_penalty=1.4,
+                                eos_token_ids=[])
+    eos = free[4]
+    cut = free[:free.index(eos) + 1]
+    ref, ref_len = _oracle_generate(O, tiny, prompt, 20, 1.4, [eos], 0.0)
+    assert ref == cut
+    got = g.generate_native_py(prompt, max_new_tokens=20, temperature=0.0, repetition_penalty=1.4,
+                               eos_token_ids=[eos])
+    assert got == ref and g.cache_len() == ref_len == len(prompt) + len(ref) - 1
+    many = [eos] + list(range(TINY["vocab_size"] - 80, TINY["vocab_size"]))
+    ref2, _ = _oracle_generate(O, tiny, prompt, 20, 1.4, many, 0.0)
+    assert g.generate_native_py(prompt, max_new_tokens=20, temperature=0.0, repetition_penalty=1.4,
+                                eos_token_ids=many) == ref2
+    g.close()
+
+
 def test_tiny_generate_empty_prompt_error(hip, tiny):
     g = hip.load_genomic_auto(tiny)
     with pytest.raises(ValueError, match="Prompt tokens cannot be empty"):
