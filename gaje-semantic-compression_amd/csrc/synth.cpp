@@ -49,6 +49,7 @@
 
 #include "common.h"
 #include "flat.h"
+#include "quantize.h"
 
 namespace gaje {
 namespace {
@@ -98,27 +99,6 @@ const double *quantile_table() {
         init = true;
     }
     return z;
-}
-
-// IEEE binary32 -> binary16, round to nearest even (half::f16::from_f32).
-uint16_t f32_to_f16(float f) {
-    uint32_t x;
-    memcpy(&x, &f, 4);
-    uint32_t sign = (x >> 16) & 0x8000u, exp = (x >> 23) & 0xFFu, mant = x & 0x7FFFFFu;
-    if (exp == 0xFF) return (uint16_t)(sign | 0x7C00u | (mant ? 0x200u | (mant >> 13) : 0));
-    int e = (int)exp - 127 + 15;
-    if (e >= 31) return (uint16_t)(sign | 0x7C00u);
-    if (e <= 0) {
-        if (e < -10) return (uint16_t)sign;
-        uint32_t full = mant | 0x800000u;
-        int shift = 14 - e;
-        uint32_t h = full >> shift, rem = full & ((1u << shift) - 1), half = 1u << (shift - 1);
-        if (rem > half || (rem == half && (h & 1u))) ++h;
-        return (uint16_t)(sign | h);
-    }
-    uint32_t h = ((uint32_t)e << 10) | (mant >> 13), rem = mant & 0x1FFFu;
-    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ++h;
-    return (uint16_t)(sign | h);
 }
 
 template <class F>
@@ -205,34 +185,6 @@ void gen_normal(uint64_t seed, const std::string &name, int64_t count, double me
     const uint64_t key = stream_key(seed, name);
     parallel_rows(count, [&](int64_t a, int64_t b) {
         for (int64_t i = a; i < b; ++i) out[i] = (float)(mean + sd * normal_at(key, (uint64_t)i));
-    });
-}
-
-// quantize_q8_0_native's block loop (compute/quantize/python.rs:235-300):
-// scale = max|w| / 127, inv = 1/scale when scale > 1e-7 (else every code 0),
-// q = round(w * inv) half away from zero, clamped to [-128, 127]; the scale
-// stored as f16 rounded to nearest even (half::f16::from_f32).
-void quantize_q8_0(const float *w, int64_t nblocks, uint8_t *out) {
-    parallel_rows(nblocks, [&](int64_t a, int64_t b) {
-        for (int64_t j = a; j < b; ++j) {
-            const float *blk = w + j * 32;
-            uint8_t *o = out + j * 34;
-            float max_abs = 0.0f;
-            for (int k = 0; k < 32; ++k) max_abs = std::fabs(blk[k]) > max_abs ? std::fabs(blk[k]) : max_abs;
-            const float scale = max_abs / 127.0f;
-            const float inv = scale > 1e-7f ? 1.0f / scale : 0.0f;
-            for (int k = 0; k < 32; ++k) {
-                int8_t q = 0;
-                if (scale > 1e-7f) {
-                    float r = std::round(blk[k] * inv);
-                    r = r < -128.0f ? -128.0f : r > 127.0f ? 127.0f : r;
-                    q = (int8_t)r;
-                }
-                o[2 + k] = (uint8_t)q;
-            }
-            const _Float16 hs = (_Float16)scale;
-            memcpy(o, &hs, 2);
-        }
     });
 }
 
@@ -545,7 +497,7 @@ extern "C" int gaje_synth_write_flat(const char *path, const gaje_synth_config *
             case 4: {
                 std::vector<float> w((size_t)(b.out_f * b.in_f));
                 gen_normal(c.seed, b.stream, (int64_t)w.size(), 0.0, 0.02, w.data());
-                quantize_q8_0(w.data(), (int64_t)(w.size() / 32), dna.data());
+                quantize_q8_0(w.data(), (int64_t)w.size(), dna.data());
                 break;
             }
         }

@@ -44,6 +44,12 @@ class GajeIOError(GajeError, OSError):
     """std::io::Error / HeaderError of the reference reader."""
 
 
+class FlatWriterHeader(ctypes.Structure):
+    _fields_ = [("flags", ctypes.c_uint32), ("group_size", ctypes.c_uint32), ("quant_format", ctypes.c_uint32),
+                ("arch_family", ctypes.c_uint32), ("n_embd", ctypes.c_uint32), ("n_head", ctypes.c_uint32),
+                ("n_head_kv", ctypes.c_uint32), ("n_blocks", ctypes.c_uint32), ("qk_permute", ctypes.c_uint32)]
+
+
 class ModelInfo(ctypes.Structure):
     _fields_ = [("n_embd", c_i64), ("n_head", c_i64), ("n_head_kv", c_i64), ("n_blocks", c_i64),
                 ("head_dim", c_i64), ("ffn", c_i64), ("vocab_size", c_i64), ("eps", ctypes.c_float),
@@ -170,6 +176,20 @@ SIGNATURES = [
     ("gaje_flat_header_from_bytes", ctypes.c_int, [c_vp, ctypes.c_size_t, ctypes.POINTER(FlatHeader)]),
     ("gaje_flat_inspect", ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(FlatInfo)]),
     ("gaje_flat_tensor_entry", ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(FlatTensor)]),
+    ("gaje_flat_writer_create", ctypes.c_int, [ctypes.POINTER(c_vp)]),
+    ("gaje_flat_writer_free", None, [c_vp]),
+    ("gaje_flat_writer_add_norm", ctypes.c_int, [c_vp, ctypes.c_char_p, c_vp, c_i64]),
+    ("gaje_flat_writer_add_f32", ctypes.c_int, [c_vp, ctypes.c_char_p, c_vp, c_i64, c_i64, c_vp, c_i64]),
+    ("gaje_flat_writer_add_q4_0", ctypes.c_int, [c_vp, ctypes.c_char_p, c_vp, c_i64, c_i64, c_vp, c_i64]),
+    ("gaje_flat_writer_add_q8_0", ctypes.c_int, [c_vp, ctypes.c_char_p, c_vp, c_i64, c_i64, c_vp, c_i64]),
+    ("gaje_flat_writer_add_lut4", ctypes.c_int, [c_vp, ctypes.c_char_p, c_vp, c_i64, c_i64, ctypes.c_float, c_vp,
+                                                 c_i64]),
+    ("gaje_flat_writer_write", ctypes.c_int, [c_vp, ctypes.c_char_p, ctypes.c_char_p,
+                                              ctypes.POINTER(FlatWriterHeader)]),
+    ("gaje_quantize_q4_0", ctypes.c_int, [c_vp, c_i64, c_vp]),
+    ("gaje_quantize_q8_0", ctypes.c_int, [c_vp, c_i64, c_vp]),
+    ("gaje_genomize_4bit", ctypes.c_int, [c_vp, c_i64, c_i64, ctypes.c_float, c_vp, c_vp, c_vp,
+                                          ctypes.POINTER(c_i64)]),
     ("gaje_synth_write_flat", ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(SynthConfig)]),
     ("gaje_synth_q4_0", ctypes.c_int, [ctypes.c_uint64, ctypes.c_char_p, c_i64, c_i64, c_vp]),
     ("gaje_synth_lut4", ctypes.c_int, [ctypes.c_uint64, ctypes.c_char_p, c_i64, c_i64, c_vp, c_vp]),

@@ -398,6 +398,49 @@ typedef struct {
  * GAJE_ERR_NOT_FOUND if the directory has none. */
 int gaje_flat_tensor_entry(const char *path, const char *name, gaje_flat_tensor *out);
 
+/* ------------------------------------------- .gaje.flat writer (f32 in) --- */
+/* The exporter's container and tensor routines (scripts/export_gaje_flat.py:
+ * 184-483) over f32 weights, with the quantisers its GenomicLayer calls
+ * (python/gaje/nn/stabilized.py:242-323).  Tensors are added in file order;
+ * each becomes a directory entry and 64-byte-aligned dna / centroid / anchor
+ * (/ bias) sub-blobs.  A writer handle is not re-entrant. */
+typedef struct gaje_flat_writer gaje_flat_writer;
+typedef struct {
+    uint32_t flags;          /* 0x3 = fused qkv + gate_up (informational)        */
+    uint32_t group_size;     /* 32                                               */
+    uint32_t quant_format;   /* 0 legacy/LUT, 1 Q4_0, 2 Q8_0 (not read by loaders) */
+    uint32_t arch_family, n_embd, n_head, n_head_kv, n_blocks, qk_permute;
+} gaje_flat_writer_header;
+int gaje_flat_writer_create(gaje_flat_writer **out);
+void gaje_flat_writer_free(gaje_flat_writer *w);
+/* A norm weight: bit_depth 32, in_features 1, centroid/anchor offsets 0. */
+int gaje_flat_writer_add_norm(gaje_flat_writer *w, const char *name, const float *weights, int64_t n);
+/* [out][in] row-major f32 weights as bit_depth 32 (token_embd / lm_head). */
+int gaje_flat_writer_add_f32(gaje_flat_writer *w, const char *name, const float *weights, int64_t out_features,
+                             int64_t in_features, const float *bias, int64_t bias_len);
+/* quantize_q4_0_native (compute/quantize/python.rs:151-232) -> bit_depth 4, no centroids. */
+int gaje_flat_writer_add_q4_0(gaje_flat_writer *w, const char *name, const float *weights, int64_t out_features,
+                              int64_t in_features, const float *bias, int64_t bias_len);
+/* quantize_q8_0_native (compute/quantize/python.rs:235-300) -> bit_depth 8 (--quant-embed). */
+int gaje_flat_writer_add_q8_0(gaje_flat_writer *w, const char *name, const float *weights, int64_t out_features,
+                              int64_t in_features, const float *bias, int64_t bias_len);
+/* genomize_4bit_core (compute/quantize/genomize.rs:286-382) with block 32 ->
+ * bit_depth 4 with per-(row, block) centroids and its anchor buffer. */
+int gaje_flat_writer_add_lut4(gaje_flat_writer *w, const char *name, const float *weights, int64_t out_features,
+                              int64_t in_features, float anchor_threshold, const float *bias, int64_t bias_len);
+/* Header, metadata JSON (json.dumps of the exporter's metadata dict), directory and blobs. */
+int gaje_flat_writer_write(gaje_flat_writer *w, const char *path, const char *metadata_json,
+                           const gaje_flat_writer_header *header);
+
+/* The quantisers alone.  n % 32 == 0; blocks_out holds n/32 * 20 (Q4_0) or
+ * n/32 * 34 (Q8_0) bytes.  gaje_genomize_4bit: codes_out n/block_size *
+ * block_size/2 bytes, centroids_out n/block_size * 16 floats, anchors_out (may
+ * be NULL to query) *anchors_len bytes in, the buffer's size out. */
+int gaje_quantize_q4_0(const float *weights, int64_t n, uint8_t *blocks_out);
+int gaje_quantize_q8_0(const float *weights, int64_t n, uint8_t *blocks_out);
+int gaje_genomize_4bit(const float *weights, int64_t n, int64_t block_size, float anchor_threshold,
+                       uint8_t *codes_out, float *centroids_out, uint8_t *anchors_out, int64_t *anchors_len);
+
 /* ----------------------------------------------- synthetic .flat writer --- */
 /* Random-init model writer for the benchmark shapes (no checkpoints exist in
  * this environment).  Writes the .gaje.flat v2 layout of
