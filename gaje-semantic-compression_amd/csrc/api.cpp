@@ -317,6 +317,49 @@ extern "C" int gaje_hip_q4_0_gemm_mfma(const void *packed, const float *X, const
 
 namespace {
 
+// Scratch of gaje_hip_q4_0_gemm_mfma_noalloc: a file-scope device array (each
+// GPU holds its own copy for the life of the process), whose address is taken
+// once per device with that device current and kept; host code uses only
+// that address, never the array's name.
+static __device__ __align__(256) uint8_t scratch[GAJE_NOALLOC_SCRATCH_BYTES];
+
+constexpr int NOALLOC_MAX_DEVICES = 64;
+std::atomic<void *> g_scratch_ptr[NOALLOC_MAX_DEVICES];
+
+int scratch_ptr(void **out) {
+    int dev = 0;
+    GAJE_HIP_CHECK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= NOALLOC_MAX_DEVICES)
+        return set_error(GAJE_ERR_UNSUPPORTED, "device %d beyond the %d this build's scratch table holds", dev,
+                         NOALLOC_MAX_DEVICES);
+    void *p = g_scratch_ptr[dev].load();
+    if (!p) {
+        GAJE_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        g_scratch_ptr[dev].store(p);
+    }
+    *out = p;
+    return GAJE_OK;
+}
+
+}  // namespace
+
+extern "C" int gaje_hip_q4_0_gemm_mfma_noalloc(const void *packed, const float *X, const float *bias, int64_t bias_len,
+                                               float *Y, int64_t m, int64_t n, int64_t k, void *stream) {
+    clear_error();
+    const int64_t need = gaje_hip_q4_0_gemm_mfma_workspace(m, n, k);
+    if (need < 0) return set_error(GAJE_ERR_INVALID_ARG, "bad gemm arguments");
+    if (need > GAJE_NOALLOC_SCRATCH_BYTES)
+        return set_error(GAJE_ERR_UNSUPPORTED,
+                         "gemm of %lld x %lld x %lld needs %lld bytes of scratch, beyond the %lld this entry point holds",
+                         (long long)m, (long long)n, (long long)k, (long long)need,
+                         (long long)GAJE_NOALLOC_SCRATCH_BYTES);
+    void *ws = nullptr;
+    GAJE_TRY(scratch_ptr(&ws));
+    return gaje_hip_q4_0_gemm_mfma(packed, X, bias, bias_len, Y, m, n, k, ws, GAJE_NOALLOC_SCRATCH_BYTES, stream);
+}
+
+namespace {
+
 // Workspace of gaje_hip_moe_ffn.
 struct MoeWorkspace {
     int *ew_gu, *ew_dn;              // [E][2 ffn], [E][h] weight row exponents

@@ -123,6 +123,7 @@ SIGNATURES = [
     ("gaje_hip_q4_0_gemm_mfma_workspace", c_i64, [c_i64, c_i64, c_i64]),
     ("gaje_hip_q4_0_gemm_mfma", ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_vp,
                                                c_i64, c_vp]),
+    ("gaje_hip_q4_0_gemm_mfma_noalloc", ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_vp]),
     ("gaje_hip_moe_ffn_workspace", c_i64, [c_i64, c_i64, c_i64, c_i64]),
     ("gaje_hip_moe_ffn", ctypes.c_int, [c_vp, c_i64, c_i64, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp,
                                         c_vp, c_i64, c_vp]),

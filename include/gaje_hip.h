@@ -113,6 +113,19 @@ int gaje_hip_q4_0_gemm_mfma(const void *packed, const float *X, const float *bia
                             float *Y, int64_t m, int64_t n, int64_t k, void *workspace,
                             int64_t workspace_bytes, void *stream);
 
+/* gaje_hip_q4_0_gemm_mfma without a workspace argument and without allocating:
+ * no counterpart in the reference; for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc).  The workspace is a file-scope device array of
+ * GAJE_NOALLOC_SCRATCH_BYTES that each GPU holds for the life of the process;
+ * a product whose gaje_hip_q4_0_gemm_mfma_workspace(m, n, k) exceeds it fails
+ * with GAJE_ERR_UNSUPPORTED.  Every call on one GPU shares that array: calls
+ * that overlap on one GPU (several streams or host threads) race.  Results are
+ * those of gaje_hip_q4_0_gemm_mfma bit for bit. */
+#define GAJE_NOALLOC_SCRATCH_BYTES (64ll << 20)
+int gaje_hip_q4_0_gemm_mfma_noalloc(const void *packed, const float *X, const float *bias, int64_t bias_len,
+                                    float *Y, int64_t m, int64_t n, int64_t k, void *stream);
+
 /* Mixture-of-experts SwiGLU FFN layer with top-2 routing over Q4_0 experts.
  * No reference counterpart (the reference has no MoE); a composition of its
  * primitives: router logits l_e = dot_product(x_t, router_e) (dot.rs:23-94,
