@@ -11,10 +11,18 @@ prefilled once before timing; every step rewinds the cache to the prompt.
 
 Also reported on the same run:
   - per-stage device time of the exact kernels of the decode step (HIP events
-    on the model stream) and the roofline of the dominant one;
-  - the single Q4_0 matvec at K=896, N=4864 (the C0 shape), cycling 128 weight
-    copies (348 MB, beyond the 256 MB last-level cache) and hot in cache;
-  - the CPU oracle (AVX2 restatement of the reference kernels) on the host cores.
+    on the model stream);
+  - the Q4_0 matvec: one launch over a 622,592 x 896 matrix (351 MB, the
+    kernel's streaming rate, which the roofline reports), the single matvec at
+    K=896, N=4864 (the C0 shape) cycling 128 weight copies (348 MB, beyond the
+    256 MB last-level cache) and hot in cache, beside the launch floors (an
+    empty kernel of its grid, a plain read of its bytes); and the C0-LUT matvec
+    (layout B: 16-byte codes and per-block f32 tables) cycling 40 copies;
+  - the same decode with K-WTA on (ratio 0.5, the flat-load default) and the
+    SmolLM2-135M-shaped decode (128-token prompt, then 256 tokens);
+  - the CPU oracle (AVX2 restatement of the reference kernels) on the host
+    cores: decode at the context the GPU runs at, and the C0 matvec, at the
+    host's thread count and at 1 thread.
 
 Secondary workloads (same JSON line, under "workloads"):
   - Qwen2.5-1.5B-shaped (hidden 1536, 28 layers, 12/2 heads, ffn 8960,
@@ -22,7 +30,8 @@ Secondary workloads (same JSON line, under "workloads"):
     greedy decode (each sequence fed a 1024-token random context, then 128
     steps, bit-exact per sequence);
   - a Q4_0 MoE SwiGLU FFN layer: hidden 1536, 8 experts of ffn 4096, top-2,
-    256 tokens.
+    256 tokens;
+  - the Qwen2-0.5B shape with Q8_0 token_embd/lm_head and with a 2-bit body.
 
 Prints ONE JSON line on stdout; progress goes to stderr.
 """
@@ -41,7 +50,8 @@ for _p in (REPO, PKG):
 
 import numpy as np  # noqa: E402
 
-HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, published
+HBM_PEAK_GBPS = 8000.0   # MI355X HBM3E, published
+MFMA_F16_TFLOPS = 2500.0  # MI355X dense f16 MFMA, published
 METRIC = "Q4_0 GEMV HBM GB/s (% of peak); decode tok/s, Qwen2-0.5B shape, batch 1"
 
 
@@ -64,7 +74,7 @@ def model_path(preset: str, seed: int, d: str, quant_embed: int = 0, body_format
 def q4_gemv_c0(iters: int = 1024, hot: bool = True, stream: bool = True):
     """The C0 matvec: Q4_0 K=896 N=4864, cold (128 copies) and hot (1 copy); the
     launch floors of its grid; and one launch over all 128 copies as a single
-    622,592-row matrix (348 MB), the kernel's streaming rate."""
+    622,592-row matrix (351 MB), the kernel's streaming rate."""
     from gaje_hip import ops, synth
     n, k = 4864, 896
     blocks = synth.q4_0_tensor(0, "c0.gemv", n, k)
@@ -72,7 +82,7 @@ def q4_gemv_c0(iters: int = 1024, hot: bool = True, stream: bool = True):
     packed = ops.q4_0_upload(blocks, n, k).read(np.uint8)[:wbytes]
     stride = (wbytes + 255) // 256 * 256
     copies = 128
-    w = ops.DeviceBuffer(stride * copies + 4096)  # + the tail the prefetch ring may read past the last row
+    w = ops.DeviceBuffer(stride * copies + 4096)  # + the tail a tile copy may read past the last row
     host = np.zeros(stride * copies + 4096, dtype=np.uint8)
     for c in range(copies):
         host[c * stride:c * stride + wbytes] = packed
@@ -83,21 +93,22 @@ def q4_gemv_c0(iters: int = 1024, hot: bool = True, stream: bool = True):
     algo = blocks.nbytes + k * 4 + n * 4  # weights + x + y
     cold_ms = ops.bench_gemv(1, w, stride, copies, x, y, n, k, iters)
     hot_ms = ops.bench_gemv(1, w, stride, 1, x, y, n, k, iters) if hot else None
-    # floors of a launch with the C0 grid (n rows x 8 chain lanes, 256 threads)
-    grid = (n * 8 + 255) // 256
-    empty_ms = ops.bench_floor(None, 0, grid, 256, iters)
-    read_ms = ops.bench_floor(w, packed.nbytes, 256, 256, iters)
+    # floors of a launch: an empty kernel of the C0 matvec's grid (one 64-thread
+    # workgroup per 8 rows) and a plain read of its weight bytes
+    grid = (n + 7) // 8
+    empty_ms = ops.bench_floor(None, 0, grid, 64, iters)
+    read_ms = ops.bench_floor(w, wbytes, 256, 256, iters)
     out = dict(shape="N=4864 K=896 (Q4_0Block 20 B / 32 weights, packed on device)", algorithmic_bytes=algo,
                launches=iters, cold_us=cold_ms * 1e3, cold_GBps=algo / (cold_ms * 1e-3) / 1e9,
                cold_frac=algo / (cold_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
                copies=copies, empty_kernel_us=empty_ms * 1e3, plain_read_us=read_ms * 1e3,
                note="cold = 128 distinct copies cycled (348 MB > 256 MB LLC), graph-replayed back-to-back "
                     "launches, per-launch time including the launch boundary; hot = one copy; "
-                    f"empty_kernel_us = an empty kernel of the same grid ({grid} x 256); plain_read_us = a "
+                    f"empty_kernel_us = an empty kernel of the same grid ({grid} x 64); plain_read_us = a "
                     "read-only kernel over the same 2,723,840 weight bytes (256 x 256 threads)")
     if hot_ms is not None:
         out.update(hot_us=hot_ms * 1e3, hot_GBps=algo / (hot_ms * 1e-3) / 1e9)
-    if stream and stride == packed.nbytes:
+    if stream and stride == wbytes:
         ns = n * copies  # the copies are contiguous: one matrix of 622,592 rows
         s_ms = ops.bench_gemv(1, w, 0, 1, x, y, ns, k, 64)
         s_algo = ns * (k // 32) * 20 + k * 4 + ns * 4
@@ -110,12 +121,35 @@ def q4_gemv_c0(iters: int = 1024, hot: bool = True, stream: bool = True):
     return out
 
 
-TRAFFIC_FILE = os.path.join(REPO, "profiles", "q4_0_gemv_c0_traffic.json")
+def lut_gemv_c0(copies: int = 40, iters: int = 512):
+    """C0-LUT: the same shape in layout B (16-byte high-nibble-first codes and a
+    per-(row, block) 16-entry f32 table), 10,918,400 algorithmic bytes, cycling
+    `copies` distinct copies (437 MB, beyond the 256 MB last-level cache)."""
+    from gaje_hip import ops, synth
+    n, k = 4864, 896
+    codes, lut = synth.lut4_tensor(0, "c0.lut", n, k)
+    cw, lw = codes.nbytes, lut.nbytes
+    W = ops.DeviceBuffer(cw * copies + 4096)
+    L = ops.DeviceBuffer(lw * copies)
+    W.write(np.tile(codes, copies))
+    L.write(np.tile(lut, copies))
+    x = ops.DeviceBuffer.from_array(synth.normal(0, "c0.x", k))
+    y = ops.DeviceBuffer(n * 4)
+    ms = ops.bench_gemv(2, W, cw, copies, x, y, n, k, iters, lut=L, lut_stride=lw)
+    algo = cw + lw + k * 4 + n * 4
+    W.close()
+    L.close()
+    return dict(shape="N=4864 K=896 (layout B: 16 B codes + 64 B f32 table per 32 weights)", algorithmic_bytes=algo,
+                copies=copies, cold_us=ms * 1e3, cold_GBps=algo / (ms * 1e-3) / 1e9,
+                cold_frac=algo / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS)
+
+
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "q4_0_gemv_stream_622592x896_traffic.json")
 
 
 def read_traffic():
-    """HBM bytes per C0 launch from the committed rocprofv3 counter runs (FETCH_SIZE +
-    WRITE_SIZE, scaled by a plain copy's reading), or None if they were not collected."""
+    """HBM bytes per launch of the streaming Q4_0 matvec from the committed rocprofv3
+    counter runs (FETCH_SIZE + WRITE_SIZE, scaled by a plain copy's reading), or None."""
     try:
         with open(TRAFFIC_FILE) as f:
             return json.load(f)["traffic_bytes_per_launch"]
@@ -123,25 +157,118 @@ def read_traffic():
         return None
 
 
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(path: str, prompt, seconds: float, threads: int):
-    """The oracle's decode on the host cores: greedy chain from the prompt's first token."""
+    """The oracle's decode on the host cores at the context the GPU decodes at: the
+    prompt fed token by token (untimed), then greedy tokens timed at `threads` and
+    at 1 thread; and the C0 Q4_0 matvec at both thread counts."""
+    from gaje_hip import synth
     from oracle import oracle as O
     O.set_threads(threads)
     r = O.load_genomic(path)
     r.set_k_wta_ratio(0.0)
-    tok = int(prompt[0])
-    r.forward_core(tok, True)  # first token also pages the weights in (untimed)
-    n, t0 = 0, time.perf_counter()
-    while True:
-        logits = r.forward_core(tok, False)
-        tok = O.argmax_first(logits)
-        n += 1
-        el = time.perf_counter() - t0
-        if (el >= seconds and n >= 4) or n >= 512:
-            break
-    return dict(value=n / el, unit="tok/s", cores=O.get_threads(), kind="port",
-                sample=f"{n} greedy decode tokens (ctx 2..{n + 1}) of the same model on the host, "
-                       f"{O.get_threads()} threads; AVX2 restatement of the reference kernels")
+    t = time.perf_counter()
+    last = None
+    for i, tok in enumerate(prompt):
+        last = r.forward_core(int(tok), i == 0)
+    log(f"[bench] cpu oracle: prefilled {len(prompt)} tokens in {time.perf_counter() - t:.1f}s")
+    tok = O.argmax_first(last)
+
+    def decode(nthreads, budget):
+        nonlocal tok
+        O.set_threads(nthreads)
+        n, t0 = 0, time.perf_counter()
+        ctx0 = r.blocks[0].attn.k_cache_len()
+        while True:
+            tok = O.argmax_first(r.forward_core(tok))
+            n += 1
+            el = time.perf_counter() - t0
+            if (el >= budget and n >= 2) or n >= 256:
+                return n / el, n, ctx0
+    tps_n, n_n, ctx_n = decode(threads, seconds)
+    tps_1, n_1, ctx_1 = decode(1, seconds)
+    # the C0 matvec
+    n, k = 4864, 896
+    L = O.GenomicLinear(synth.q4_0_tensor(0, "c0.gemv", n, k), b"", None, n, k, None, 4)
+    x = synth.normal(0, "c0.x", k)
+    algo = n * k // 32 * 20 + k * 4 + n * 4
+    gemv = {}
+    for nt in (threads, 1):
+        O.set_threads(nt)
+        L.forward_core(x)
+        reps, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < 1.0:
+            L.forward_core(x)
+            reps += 1
+        us = (time.perf_counter() - t0) / reps * 1e6
+        gemv[f"threads_{nt}"] = dict(us=round(us, 2), GBps=round(algo / (us * 1e-6) / 1e9, 2))
+    O.set_threads(threads)
+    return dict(value=round(tps_n, 2), unit="tok/s", cores=threads, kind="port",
+                sample=f"{n_n} greedy decode tokens of the same model at contexts {ctx_n + 1}..{ctx_n + n_n} "
+                       f"after the {len(prompt)}-token prompt, {threads} threads; the AVX2 restatement of the "
+                       "reference kernels (oracle/gaje_oracle.c, -O3 -mavx2 -mfma)",
+                one_thread=dict(value=round(tps_1, 2), unit="tok/s", tokens=n_1,
+                                contexts=f"{ctx_1 + 1}..{ctx_1 + n_1}"),
+                cpu_model=cpu_model(), nproc=os.cpu_count(),
+                threads_note=f"{threads} threads: the host's OMP_NUM_THREADS (the CPU share of the GPU box), "
+                             "not nproc",
+                c0_gemv=gemv)
+
+
+def decode_workload(d: str, seed: int, preset: str, prompt_len: int, gen: int, steps: int, warmup: int = 1,
+                    kwta: float = 0.0, quant_embed: int = 0, body_format: int = 1, stages=None):
+    """Batch-1 greedy decode: prompt fed token by token once, then `steps` timed runs
+    of the fixed-length greedy loop from the prompt state (cache rewound each time)."""
+    import gaje_hip
+    from gaje_hip import ops
+    path = model_path(preset, seed, d, quant_embed=quant_embed, body_format=body_format)
+    g = gaje_hip.load_genomic_auto(path)
+    g.set_k_wta_ratio(kwta)
+    prompt = np.random.default_rng(seed).integers(0, g.vocab_size, prompt_len).astype(np.uint32)
+    g.reserve(prompt_len + gen + 1)
+    g.clear_cache_py()
+    g.prefill(prompt)
+
+    def step():
+        g.truncate_cache(prompt_len)
+        return g.decode_greedy(int(prompt[-1]), gen)
+
+    for _ in range(warmup):
+        step()
+    ops.synchronize()
+    toks = []
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        toks = step()
+    ops.synchronize()
+    el = time.perf_counter() - t0
+    out = dict(tok_s=round(gen * steps / el, 2), ms_per_token=round(el / (gen * steps) * 1e3, 4),
+               prompt=prompt_len, gen=gen, steps=steps, el=el, last_tokens=[int(t) for t in toks[-4:]])
+    if stages:
+        counts = {s: g.info["n_blocks"] for s in ("qkv", "attention", "o", "gate_up", "down")}
+        counts["lm_head"] = 1
+        g.truncate_cache(prompt_len + gen - 1)  # time at the last step's context
+        st = {}
+        for s in stages:
+            ms, nbytes = g.time_stage(s, layer=0, iters=200 if s != "token" else 50)
+            gbps = nbytes / (ms * 1e-3) / 1e9
+            st[s] = dict(us=round(ms * 1e3, 3), bytes=int(nbytes), GBps=round(gbps, 1),
+                         frac=round(gbps / HBM_PEAK_GBPS, 4))
+            if s in counts:
+                st[s]["per_token_us"] = round(ms * 1e3 * counts[s], 2)
+        out["stages"] = st
+    g.close()
+    return out, path, prompt
 
 
 def c3_workloads(d: str, seed: int, prefill_tokens: int = 512, batch: int = 16, ctx: int = 1024, gen: int = 128):
@@ -165,11 +292,17 @@ def c3_workloads(d: str, seed: int, prefill_tokens: int = 512, batch: int = 16, 
     pf = min(times[1:])
     body_flop = 2.0 * prefill_tokens * sum(
         n * k for n, k in ((2048, 1536), (1536, 1536), (17920, 1536), (1536, 8960))) * g.info["n_blocks"]
+    useful = body_flop / pf / 1e12
     prefill = dict(tokens=prefill_tokens, ms=round(pf * 1e3, 3), tok_s=round(prefill_tokens / pf, 1),
-                   body_TFLOPs=round(body_flop / pf / 1e12, 2), body_flop=body_flop,
-                   precision="f16 hi/lo operand pairs, fp32 accumulation (fp32-level accuracy)")
+                   body_TFLOPs=round(useful, 2), body_flop=body_flop,
+                   mfma_frac_useful=round(useful / MFMA_F16_TFLOPS, 4),
+                   mfma_frac_issued=round(3 * useful / MFMA_F16_TFLOPS, 4),
+                   precision="f16 hi/lo operand pairs, fp32 accumulation (fp32-level accuracy): three f16 MFMA "
+                             "products per useful one, so issued = 3 x useful",
+                   peak=f"{MFMA_F16_TFLOPS:.0f} TFLOP/s dense f16 MFMA")
     log(f"[bench] C3 prefill {prefill_tokens}: {pf * 1e3:.2f} ms = {prefill_tokens / pf:.0f} tok/s, "
-        f"body {body_flop / pf / 1e12:.1f} TFLOP/s")
+        f"body {useful:.1f} TFLOP/s useful ({100 * useful / MFMA_F16_TFLOPS:.1f}% of f16 MFMA peak, "
+        f"{300 * useful / MFMA_F16_TFLOPS:.1f}% issued)")
     b = gaje_hip.GenomicBatch(g, batch, ctx + 2 * gen + 1)
     ctx_ids = rng.integers(0, g.vocab_size, (batch, ctx)).astype(np.uint32)
     t = time.perf_counter()
@@ -193,48 +326,6 @@ def c3_workloads(d: str, seed: int, prefill_tokens: int = 512, batch: int = 16, 
     return prefill, decode, [int(v) for v in out[0, :4]]
 
 
-def variant_decode_workload(d: str, seed: int, preset: str, prompt_len: int, gen: int, steps: int,
-                            quant_embed: int = 0, body_format: int = 1):
-    """Batch-1 greedy decode of the same shape in another format: Q8_0 token_embd / lm_head
-    (quant_embed=1, the --quant-embed export: the lm_head reads 34 B per 32 weights instead
-    of 128) or a 2-bit body (body_format=4, Genomic2Bit with per-block centroids)."""
-    import gaje_hip
-    from gaje_hip import ops
-    path = model_path(preset, seed, d, quant_embed=quant_embed, body_format=body_format)
-    g = gaje_hip.load_genomic_auto(path)
-    g.set_k_wta_ratio(0.0)
-    prompt = np.random.default_rng(seed).integers(0, g.vocab_size, prompt_len).astype(np.uint32)
-    g.reserve(prompt_len + gen + 1)
-    g.clear_cache_py()
-    g.prefill(prompt)
-
-    def step():
-        g.truncate_cache(prompt_len)
-        return g.decode_greedy(int(prompt[-1]), gen)
-
-    step()
-    ops.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        step()
-    ops.synchronize()
-    el = time.perf_counter() - t0
-    g.truncate_cache(prompt_len + gen - 1)
-    stages = {}
-    for st in (("lm_head",) if quant_embed else ("qkv", "o", "gate_up", "down")):
-        ms, nbytes = g.time_stage(st, iters=200)
-        gbps = nbytes / (ms * 1e-3) / 1e9
-        stages[st] = dict(us=round(ms * 1e3, 3), bytes=int(nbytes), GBps=round(gbps, 1),
-                          frac=round(gbps / HBM_PEAK_GBPS, 4))
-    g.close()
-    out = dict(tok_s=round(gen * steps / el, 2), ms_per_token=round(el / (gen * steps) * 1e3, 4),
-               prompt=prompt_len, gen=gen, steps=steps, stages=stages)
-    what = "Q8_0 embed/lm_head" if quant_embed else "2-bit body"
-    log(f"[bench] {what} decode: {out['tok_s']:.1f} tok/s; " +
-        ", ".join(f"{k} {v['us']:.2f} us" for k, v in stages.items()))
-    return out
-
-
 def moe_workload(seed: int, T: int = 256, h: int = 1536, ffn: int = 4096, E: int = 8, iters: int = 50):
     from gaje_hip import ops, synth
     x = synth.normal(seed + 51, "moe.x", T * h).reshape(T, h)
@@ -256,9 +347,12 @@ def moe_workload(seed: int, T: int = 256, h: int = 1536, ffn: int = 4096, E: int
     ms = e0.elapsed_ms(e1) / iters
     flop = 2.0 * T * 2 * (2 * ffn * h + h * ffn)
     wbytes = E * (2 * ffn * h + h * ffn) * 20 // 32
-    log(f"[bench] C4 MoE layer: {ms * 1e3:.1f} us, {flop / ms / 1e9:.1f} TFLOP/s (expert products)")
+    useful = flop / ms / 1e9
+    log(f"[bench] C4 MoE layer: {ms * 1e3:.1f} us, {useful:.1f} TFLOP/s useful (expert products)")
     return dict(tokens=T, hidden=h, ffn=ffn, experts=E, top_k=2, us_per_layer=round(ms * 1e3, 2),
-                expert_TFLOPs=round(flop / ms / 1e9, 2), expert_flop=flop, expert_weight_bytes=wbytes,
+                expert_TFLOPs=round(useful, 2), expert_flop=flop, expert_weight_bytes=wbytes,
+                mfma_frac_useful=round(useful / MFMA_F16_TFLOPS, 4),
+                mfma_frac_issued=round(3 * useful / MFMA_F16_TFLOPS, 4),
                 tokens_per_s=round(T / ms * 1e3, 1))
 
 
@@ -272,19 +366,21 @@ def main():
     ap.add_argument("--gen", type=int, default=256)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--model-dir", default=None)
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-stages", action="store_true")
     ap.add_argument("--no-c3", action="store_true", help="skip the Qwen2.5-1.5B prefill and batched decode")
     ap.add_argument("--c3-ctx", type=int, default=1024, help="context fed to each batched sequence")
     ap.add_argument("--c3-gen", type=int, default=128, help="batched greedy steps timed")
     ap.add_argument("--no-decode", action="store_true",
-                    help="skip the Qwen2-0.5B decode, its stages and the C0 matvec (profiling runs of the other workloads)")
+                    help="skip the Qwen2-0.5B decode, its stages and the matvecs (profiling runs of the other workloads)")
     ap.add_argument("--no-moe", action="store_true", help="skip the MoE layer")
     ap.add_argument("--no-q8", action="store_true", help="skip the Q8_0 token_embd/lm_head decode")
     ap.add_argument("--no-2bit", action="store_true", help="skip the 2-bit body decode")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the K-WTA-on decode, the SmolLM2-135M decode and the C0-LUT matvec")
     ap.add_argument("--gemv-only", action="store_true",
-                    help="only the C0 Q4_0 matvec (cold) and a 256 MiB device copy, for counter runs")
+                    help="only the Q4_0 matvecs (C0 cold, the 351 MB stream) and a 256 MiB device copy, for counter runs")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -300,83 +396,75 @@ def main():
         sys.exit(1)
     log(f"[bench] device: {ops.device_name(0)}")
     if args.gemv_only:
-        # a copy kernel of known size (the counters' scale) and the C0 matvec
+        # a copy kernel of known size (the counters' scale) and the matvecs
         nbytes = 256 << 20
         a, b = ops.DeviceBuffer(nbytes), ops.DeviceBuffer(nbytes)
         ops.memcpy_d2d(b, a, nbytes)
         ops.synchronize()
-        gemv = q4_gemv_c0(hot=False)
-        log(f"[bench] Q4_0 GEMV C0: cold {gemv['cold_us']:.2f} us = {gemv['cold_GBps']:.0f} GB/s")
+        gemv = q4_gemv_c0(iters=256, hot=False)
+        log(f"[bench] Q4_0 GEMV C0: cold {gemv['cold_us']:.2f} us; stream {gemv['stream_us']:.2f} us")
         print(json.dumps({"q4_0_gemv": gemv, "copy_bytes": nbytes}), flush=True)
         return
 
     d = args.model_dir or tempfile.gettempdir()
-    tok_s = el = None
-    toks = []
-    stages, gemv, roofline, path, prompt = {}, None, None, None, None
+    dec, stages, gemv, lut, roofline, path, prompt = None, {}, None, None, None, None, None
+    workloads = {}
     if not args.no_decode:
-        path = model_path(args.preset, args.seed, d)
-        t = time.perf_counter()
-        g = gaje_hip.load_genomic_auto(path)
-        log(f"[bench] loaded {g.info['weight_bytes'] / 1e9:.2f} GB of weights into HBM in {time.perf_counter() - t:.1f}s")
-        g.set_k_wta_ratio(0.0)
-        vocab = g.vocab_size
-        prompt = np.random.default_rng(args.seed).integers(0, vocab, args.prompt).astype(np.uint32)
-        g.reserve(args.prompt + args.gen + 1)
-        g.clear_cache_py()
-        t = time.perf_counter()
-        g.prefill(prompt)
-        log(f"[bench] prefilled {args.prompt} tokens token-by-token in {time.perf_counter() - t:.2f}s")
-
-        def step():
-            g.truncate_cache(args.prompt)
-            return g.decode_greedy(int(prompt[-1]), args.gen)
-
-        for _ in range(args.warmup):
-            step()
-        ops.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            toks = step()
-        ops.synchronize()
-        el = time.perf_counter() - t0
-        tok_s = args.gen * args.steps / el
-        log(f"[bench] decode: {tok_s:.1f} tok/s ({el / args.steps * 1e3:.1f} ms per {args.gen}-token step)")
-
-        stages = {}
-        roofline = None
-        if not args.no_stages:
-            counts = {"qkv": g.info["n_blocks"], "attention": g.info["n_blocks"], "o": g.info["n_blocks"],
-                      "gate_up": g.info["n_blocks"], "down": g.info["n_blocks"], "lm_head": 1}
-            g.truncate_cache(args.prompt + args.gen - 1)  # time at the last step's context
-            for s in ("qkv", "attention", "o", "gate_up", "down", "lm_head", "token"):
-                ms, nbytes = g.time_stage(s, layer=0, iters=200 if s != "token" else 50)
-                gbps = nbytes / (ms * 1e-3) / 1e9
-                stages[s] = dict(us=round(ms * 1e3, 3), bytes=int(nbytes), GBps=round(gbps, 1),
-                                 frac=round(gbps / HBM_PEAK_GBPS, 4))
-                if s in counts:
-                    stages[s]["per_token_us"] = round(ms * 1e3 * counts[s], 2)
-                log(f"[bench] stage {s:9s}: {ms * 1e3:8.2f} us  {gbps:8.1f} GB/s")
+        stage_list = None if args.no_stages else ("qkv", "attention", "o", "gate_up", "down", "lm_head", "token")
+        dec, path, prompt = decode_workload(d, args.seed, args.preset, args.prompt, args.gen, args.steps,
+                                            args.warmup, stages=stage_list)
+        stages = dec.pop("stages", {})
+        log(f"[bench] decode: {dec['tok_s']:.1f} tok/s ({dec['el'] / args.steps * 1e3:.1f} ms per "
+            f"{args.gen}-token step)")
+        for s, v in stages.items():
+            log(f"[bench] stage {s:9s}: {v['us']:8.2f} us  {v['GBps']:8.1f} GB/s")
 
         gemv = q4_gemv_c0()
         log(f"[bench] Q4_0 GEMV C0: cold {gemv['cold_us']:.2f} us = {gemv['cold_GBps']:.0f} GB/s "
-            f"({100 * gemv['cold_frac']:.1f}% of HBM peak); hot {gemv['hot_us']:.2f} us")
-        # the metric's kernel: the C0 Q4_0 matvec, cold, timed with HIP events on its own stream
-        roofline = dict(kernel="gemv_kernel<Q4_0> (C0: K=896, N=4864, 128 cold weight copies)", bound="hbm",
-                        achieved=round(gemv["cold_GBps"], 1), peak=HBM_PEAK_GBPS, unit="GB/s",
-                        frac=round(gemv["cold_frac"], 4), traffic=read_traffic(),
-                        bytes_per_launch=gemv["algorithmic_bytes"], us_per_launch=round(gemv["cold_us"], 3))
-
-        g.close()
-    workloads = {}
+            f"({100 * gemv['cold_frac']:.1f}% of HBM peak); hot {gemv['hot_us']:.2f} us; launch floors: empty "
+            f"{gemv['empty_kernel_us']:.2f} us, plain read {gemv['plain_read_us']:.2f} us")
+        log(f"[bench] Q4_0 GEMV stream 622592x896: {gemv['stream_us']:.1f} us = {gemv['stream_GBps']:.0f} GB/s "
+            f"({100 * gemv['stream_frac']:.1f}% of HBM peak; plain read {gemv['stream_plain_read_GBps']:.0f} GB/s)")
+        # the metric's kernel: the Q4_0 matvec streaming one 351 MB matrix, timed
+        # with HIP events on the stream that launches it
+        roofline = dict(kernel="gemv_q4_lds_kernel (Q4_0 STORE, 8 waves x 2 stages, 16-row tiles; one launch over "
+                               "a 622,592 x 896 matrix)", bound="hbm",
+                        achieved=round(gemv["stream_GBps"], 1), peak=HBM_PEAK_GBPS, unit="GB/s",
+                        frac=round(gemv["stream_frac"], 4), traffic=read_traffic(),
+                        bytes_per_launch=gemv["stream_bytes"], us_per_launch=round(gemv["stream_us"], 3),
+                        c0_launch=dict(bytes=gemv["algorithmic_bytes"], us=round(gemv["cold_us"], 3),
+                                       GBps=round(gemv["cold_GBps"], 1), frac=round(gemv["cold_frac"], 4),
+                                       floor_empty_kernel_us=round(gemv["empty_kernel_us"], 3)))
+        if not args.no_extra:
+            lut = lut_gemv_c0()
+            log(f"[bench] C0-LUT GEMV: cold {lut['cold_us']:.2f} us = {lut['cold_GBps']:.0f} GB/s "
+                f"({100 * lut['cold_frac']:.1f}% of HBM peak)")
+            kw, _, _ = decode_workload(d, args.seed, args.preset, args.prompt, args.gen, args.steps, args.warmup,
+                                       kwta=0.5)
+            kw.pop("el")
+            kw["kwta"] = 0.5
+            workloads[f"{args.preset}_decode_kwta_0.5"] = kw
+            log(f"[bench] decode with K-WTA 0.5: {kw['tok_s']:.1f} tok/s")
+            c1, _, _ = decode_workload(d, args.seed, "smollm2-135m", 128, 256, args.steps, args.warmup,
+                                       stages=None if args.no_stages else ("qkv", "attention", "o", "gate_up",
+                                                                           "down", "lm_head"))
+            c1.pop("el")
+            workloads["smollm2-135m_decode_128+256"] = c1
+            log(f"[bench] SmolLM2-135M decode (128 + 256): {c1['tok_s']:.1f} tok/s")
     if not args.no_q8 and not args.no_decode:
-        workloads[f"{args.preset}_q8_0_embed_decode"] = variant_decode_workload(
-            d, args.seed, args.preset, args.prompt, args.gen, args.steps, quant_embed=1)
+        q8, _, _ = decode_workload(d, args.seed, args.preset, args.prompt, args.gen, args.steps, args.warmup,
+                                   quant_embed=1, stages=None if args.no_stages else ("lm_head",))
+        q8.pop("el")
+        workloads[f"{args.preset}_q8_0_embed_decode"] = q8
+        log(f"[bench] Q8_0 embed/lm_head decode: {q8['tok_s']:.1f} tok/s")
     if not args.no_2bit and not args.no_decode:
-        workloads[f"{args.preset}_2bit_body_decode"] = variant_decode_workload(
-            d, args.seed, args.preset, args.prompt, args.gen, args.steps, body_format=4)
+        b2, _, _ = decode_workload(d, args.seed, args.preset, args.prompt, args.gen, args.steps, args.warmup,
+                                   body_format=4, stages=None if args.no_stages else ("qkv", "o", "gate_up", "down"))
+        b2.pop("el")
+        workloads[f"{args.preset}_2bit_body_decode"] = b2
+        log(f"[bench] 2-bit body decode: {b2['tok_s']:.1f} tok/s")
     if not args.no_c3:
-        prefill, decode, c3_tokens = c3_workloads(d, args.seed, ctx=args.c3_ctx, gen=args.c3_gen)
+        prefill, decode, _ = c3_workloads(d, args.seed, ctx=args.c3_ctx, gen=args.c3_gen)
         workloads["qwen2.5-1.5b_prefill_512"] = prefill
         workloads["qwen2.5-1.5b_batch16_decode"] = decode
     if not args.no_moe:
@@ -384,18 +472,19 @@ def main():
 
     cpu = None
     if not args.no_cpu and path is not None:
-        threads = min(16, os.cpu_count() or 1)
+        threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
         cpu = cpu_baseline(path, prompt, args.cpu_seconds, threads)
-        log(f"[bench] cpu oracle: {cpu['value']:.2f} tok/s on {cpu['cores']} threads")
+        log(f"[bench] cpu oracle ({cpu['cpu_model']}): {cpu['value']:.2f} tok/s on {cpu['cores']} threads, "
+            f"{cpu['one_thread']['value']:.2f} tok/s on 1; C0 matvec {cpu['c0_gemv']}")
 
     out = {
         "metric": METRIC,
-        "value": round(tok_s, 2) if tok_s else None,
+        "value": dec["tok_s"] if dec else None,
         "unit": "tok/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(el / args.steps * 1e3, 3) if el else None,
+        "ms_per_step": round(dec["el"] / args.steps * 1e3, 3) if dec else None,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -408,9 +497,10 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "q4_0_gemv": gemv,
+        "lut4_gemv_c0": lut,
         "stages": stages,
         "workloads": workloads,
-        "last_tokens": [int(t) for t in toks[-4:]],
+        "last_tokens": dec["last_tokens"] if dec else [],
     }
     print(json.dumps(out), flush=True)
 

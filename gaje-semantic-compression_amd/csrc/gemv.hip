@@ -1290,15 +1290,17 @@ __device__ __forceinline__ void wait_vmcnt_ab(int a, int b) {
 }
 
 // Copies the N KiB from byte `off` of the weights into LDS at `dst` (wave
-// uniform).  Lanes whose bytes lie past `limit` (the bytes the tensor's
-// allocation holds, padding included) read the tensor's first bytes instead:
-// those LDS bytes belong to rows past the last one, which are never stored.
+// uniform).  Lanes whose bytes lie at or past `end` (the tile's last byte, or
+// the tensor's allocation end if that comes first) read the tile's first 16
+// bytes again: those LDS bytes are never read as rows of this tile, and
+// re-reading bytes the tile fetches anyway keeps the next tile's rows (another
+// workgroup's, often on another L2) out of this one's memory traffic.
 template <int N>
-__device__ __forceinline__ void q4l_copy(const uint8_t *w, int64_t off, int64_t limit, uint32_t dst, int lane) {
+__device__ __forceinline__ void q4l_copy(const uint8_t *w, int64_t off, int64_t end, uint32_t dst, int lane) {
 #pragma unroll
     for (int i = 0; i < N; ++i) {
         int64_t a = off + i * 1024 + lane * 16;
-        a = a + 16 <= limit ? a : 0;
+        a = a + 16 <= end ? a : off;
         lds_dma16(w + a, dst + i * 1024);
     }
 }
@@ -1375,11 +1377,14 @@ __global__ __launch_bounds__(WAVES * WAVE) void gemv_q4_lds_kernel(GemvParams p,
     // tile t: rows 8 ROWS t.. (store), or gate rows 8t.. then up rows ffn + 8t..
     auto issue = [&](int64_t t, int stage) {
         const uint32_t dst = lds_addr(stages + stage * PER * 1024);
+        constexpr int64_t TB = (int64_t)TROWS * ROW_BYTES;
         if constexpr (MODE == MODE_SWIGLU) {
-            q4l_copy<HALF>(p.w, t * TROWS * ROW_BYTES, limit, dst, lane);
-            q4l_copy<HALF>(p.w, (t * TROWS + p.ffn) * ROW_BYTES, limit, dst + HALF * 1024, lane);
+            const int64_t g0 = t * TB, u0 = (t * TROWS + p.ffn) * ROW_BYTES;
+            q4l_copy<HALF>(p.w, g0, g0 + TB < limit ? g0 + TB : limit, dst, lane);
+            q4l_copy<HALF>(p.w, u0, u0 + TB < limit ? u0 + TB : limit, dst + HALF * 1024, lane);
         } else {
-            q4l_copy<PER>(p.w, t * TROWS * ROW_BYTES, limit, dst, lane);
+            const int64_t o0 = t * TB;
+            q4l_copy<PER>(p.w, o0, o0 + TB < limit ? o0 + TB : limit, dst, lane);
         }
     };
 
@@ -1544,7 +1549,20 @@ __device__ __forceinline__ float q4_chain4(float acc, const float4 d, const floa
     return acc;
 }
 
-template <int MODE, bool NORM>
+// The tiled form (TILE) copies the workgroup's whole share of the matrix into
+// LDS when it starts: producer wave pw copies, for every stage, the bytes of
+// its SPLIT_PQ groups of the 8 rows (1280 bytes, unit (row, j) at 160 row +
+// 80 j) with global_load_lds_dwordx4, two instructions per stage, all issued
+// before the first stage is produced; wave 0 copies the activations (and the
+// norm weights) the same way in one batch.  Every load then waits out one
+// memory latency instead of one per stage.  The producers dequantise from LDS
+// with q4_dequant_dw (the values of q4_dequant, fewer instructions), one
+// barrier per stage.  The copies are inline assembly waited with explicit
+// vmcnt counts (stage s of nstage may leave 2 (nstage - 1 - s) outstanding).
+constexpr int SPLIT_TILE_UNIT = 8 * SPLIT_PQ * 80;  // bytes one producer copies per stage
+constexpr int SPLIT_TILE_MAX_STAGES = 31;           // 2 copies per stage within the six-bit vmcnt
+
+template <int MODE, bool NORM, bool TILE>
 __global__ __launch_bounds__(THREADS) void gemv_q4_split_kernel(GemvParams p, int64_t npairs, int xstride) {
     extern __shared__ __align__(16) float smem[];
     DevState *st = p.st;
@@ -1553,6 +1571,9 @@ __global__ __launch_bounds__(THREADS) void gemv_q4_split_kernel(GemvParams p, in
     const int nb = p.nb, G = (nb + 3) >> 2, nstage = (G + SPLIT_SQ - 1) / SPLIT_SQ;
     const XView xv{smem, xstride};
     float *ring = smem + 8 * xstride;  // [2][64 chain lanes][SPLIT_DSTRIDE]
+    // TILE: the activations (and norm weights) as copied, then the tile
+    uint8_t *raw = (uint8_t *)(ring + 2 * 64 * SPLIT_DSTRIDE);
+    uint8_t *tile = raw + K * 4 * (NORM ? 2 : 1);
     const int l = lane & 7;
     const int64_t pr = (int64_t)blockIdx.x * SPLIT_PAIRS + (lane >> 4);
     PairRows q;  // (locate, with the pairing of this kernel's mode only)
@@ -1569,9 +1590,68 @@ __global__ __launch_bounds__(THREADS) void gemv_q4_split_kernel(GemvParams p, in
     }
     q.row = ((lane >> 3) & 1) ? q.r1 : q.r0;
     q.row_ok = q.pair_ok && q.row >= 0 && q.row < p.rows_valid;
-    const int halted = st ? st->halted : 0;
+    if constexpr (TILE) {
+        if (wave > 0) {
+            // ---- producers, tiled: copy every stage's bytes, then dequantise
+            // stage by stage as the copies land ----
+            const int pw = wave - 1;
+            const uint8_t *src[2];
+            int jj[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {  // this lane's 16 bytes of each copy
+                const int b = i * 1024 + lane * 16, rho = (b < SPLIT_TILE_UNIT ? b : 0) / 160;
+                jj[i] = (b % 160) / 80;
+                const int64_t cpr = (int64_t)blockIdx.x * SPLIT_PAIRS + (rho >> 1);
+                int64_t c0 = 0, c1 = -1;
+                if (cpr < npairs) {
+                    if constexpr (MODE == MODE_QKV) {
+                        pair_rows(p, MODE_QKV, cpr, c0, c1);
+                    } else {
+                        c0 = 2 * cpr;
+                        c1 = 2 * cpr + 1 < p.N ? 2 * cpr + 1 : -1;
+                    }
+                }
+                const int64_t row = (rho & 1) ? c1 : c0;
+                const bool ok = cpr < npairs && row >= 0 && row < p.rows_valid;
+                src[i] = (p.rows_valid > 0 ? p.w : kZeroRows) + (size_t)(ok ? row : 0) * G * 80 + b % 80;
+            }
+            for (int sg = 0; sg < nstage; ++sg) {
+                const uint32_t dst = lds_addr(tile + (size_t)(sg * 3 + pw) * SPLIT_TILE_UNIT);
+                const int g0 = sg * SPLIT_SQ + pw * SPLIT_PQ;
+                const int ga = g0 + jj[0] < G ? g0 + jj[0] : G - 1, gb = g0 + jj[1] < G ? g0 + jj[1] : G - 1;
+                lds_dma16(src[0] + (size_t)ga * 80, dst);
+                if (lane < (SPLIT_TILE_UNIT - 1024) / 16) lds_dma16(src[1] + (size_t)gb * 80, dst + 1024);
+            }
+            if (st && s_load_i32(&st->halted)) {
+                wait_vmcnt<0>();  // no copy may land after the workgroup's LDS is released
+                return;           // uniform
+            }
+            const int rho = lane >> 3;
+            for (int sg = 0; sg < nstage; ++sg) {
+                wait_vmcnt_stages<2, SPLIT_TILE_MAX_STAGES>(nstage - 1 - sg);
+                const uint8_t *u = tile + (size_t)(sg * 3 + pw) * SPLIT_TILE_UNIT + rho * 160;
+                float *dst = ring + ((sg & 1) * 64 + lane) * SPLIT_DSTRIDE + 16 * pw * SPLIT_PQ;
+#pragma unroll
+                for (int j = 0; j < SPLIT_PQ; ++j) {
+                    const vu2 n = *(const vu2 *)(u + j * 80 + 8 * l);
+                    const vu4 sw = *(const vu4 *)(u + j * 80 + 64);
+                    float d[4][4];
+                    q4_dequant_dw<0>(d[0], n.x, sw.x);
+                    q4_dequant_dw<1>(d[1], n.x, sw.y);
+                    q4_dequant_dw<0>(d[2], n.y, sw.z);
+                    q4_dequant_dw<1>(d[3], n.y, sw.w);
+#pragma unroll
+                    for (int b = 0; b < 4; ++b)
+                        *(float4 *)(dst + 16 * j + 4 * b) = make_float4(d[b][0], d[b][1], d[b][2], d[b][3]);
+                }
+                lds_barrier();
+            }
+            return;  // wave 0 passes no further barrier
+        }
+    }
+    const int halted = TILE ? 0 : (st ? st->halted : 0);
 
-    if (wave > 0) {
+    if (!TILE && wave > 0) {
         // ---- producers: wave 1 + pw dequantises groups pw*PQ .. pw*PQ + PQ-1
         // of every stage for the 64 chain lanes; loads run two stages ahead.
         // Stages are produced in pairs with no branch around the loads (past
@@ -1619,23 +1699,41 @@ __global__ __launch_bounds__(THREADS) void gemv_q4_split_kernel(GemvParams p, in
     }
 
     // ---- wave 0 ----
+    if constexpr (TILE) {
+        lds_copy_bytes(p.x, K * 4, lds_addr(raw), lane);
+        if constexpr (NORM) lds_copy_bytes(p.norm_w, K * 4, lds_addr(raw + K * 4), lane);
+        if (st && s_load_i32(&st->halted)) {
+            wait_vmcnt<0>();
+            return;
+        }
+        wait_vmcnt<0>();  // this wave's copies have landed (it alone reads them)
+    }
     if (halted) return;
     // activations -> chain-major LDS (batches of 8 float4 per lane); with a
     // norm the vector is one batch and stays in registers for the normalising
+    // (tiled: read from the copies, any length)
     const bool leader = q.pair_ok && (lane & 15) == 0;
     float b0 = 0.0f, b1 = 0.0f, old0 = 0.0f, old1 = 0.0f, cs = 0.0f, sn = 0.0f;
     int pos = 0;
-    const float4 *x4 = (const float4 *)p.x;
-    const float4 *w4 = (const float4 *)p.norm_w;  // non-null exactly when NORM
+    const float4 *x4 = TILE ? (const float4 *)raw : (const float4 *)p.x;
+    const float4 *w4 = TILE ? (const float4 *)(raw + K * 4) : (const float4 *)p.norm_w;  // used exactly when NORM
     int bad_in = 0;
-    float4 v[8], w[NORM ? 8 : 1];
-    for (int64_t m0 = 0; m0 < K4; m0 += 8 * 64) {
+    float4 v[8], w[NORM && !TILE ? 8 : 1];
+    if constexpr (TILE) {
+        for (int64_t m = lane; m < K4; m += 64) {
+            const float4 a = x4[m];
+            const float qd[4] = {a.x, a.y, a.z, a.w};
+            store_quad<true>(xv, (int)m, qd);
+            bad_in |= isnan(a.x) | isnan(a.y) | isnan(a.z) | isnan(a.w);
+        }
+    }
+    for (int64_t m0 = 0; !TILE && m0 < K4; m0 += 8 * 64) {
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
             const int64_t m = m0 + u * 64 + lane;
             v[u] = x4[m < K4 ? m : K4 - 1];
         }
-        if constexpr (NORM) {
+        if constexpr (NORM && !TILE) {
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
                 const int64_t m = m0 + u * 64 + lane;
@@ -1685,12 +1783,11 @@ __global__ __launch_bounds__(THREADS) void gemv_q4_split_kernel(GemvParams p, in
         const float tot = u2 + __shfl(u2, (lane + 2) & 7, 8);
         const float inv = __shfl(1.0f / sqrtf(tot / (float)K + p.eps), 0, WAVE);
         int bad = 0;
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int64_t m = u * 64 + lane;
-            if (m < K4) {
-                float t[4] = {v[u].x * inv, v[u].y * inv, v[u].z * inv, v[u].w * inv};
-                const float wn[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+        if constexpr (TILE) {
+            for (int64_t m = lane; m < K4; m += 64) {
+                const float4 a = x4[m], b = w4[m];
+                float t[4] = {a.x * inv, a.y * inv, a.z * inv, a.w * inv};
+                const float wn[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
                     t[c] = t[c] * wn[c];
@@ -1698,13 +1795,28 @@ __global__ __launch_bounds__(THREADS) void gemv_q4_split_kernel(GemvParams p, in
                 }
                 store_quad<true>(xv, (int)m, t);
             }
+        } else {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int64_t m = u * 64 + lane;
+                if (m < K4) {
+                    float t[4] = {v[u].x * inv, v[u].y * inv, v[u].z * inv, v[u].w * inv};
+                    const float wn[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        t[c] = t[c] * wn[c];
+                        bad |= isnan(t[c]);
+                    }
+                    store_quad<true>(xv, (int)m, t);
+                }
+            }
         }
         if (__any(bad) && p.st_norm >= 0 && lane == 0) nan_flag(st, p.layer, p.st_norm);
     }
     // the 64 chains, one stage per barrier
     float acc = 0.0f;
     const float *xg = xv.x + l * xstride;
-    const int nbar = (nstage + 1) & ~1;  // the producers' barriers (stages in pairs)
+    const int nbar = TILE ? nstage : (nstage + 1) & ~1;  // the producers' barriers (untiled: stages in pairs)
     for (int s = 0; s < nbar; ++s) {
         lds_barrier();
         if (s >= nstage) break;  // (the producers' unused last stage)
@@ -1816,6 +1928,13 @@ static int64_t gemv_x_floats(int64_t K, int fmt) {
 // the row) and the two ring buffers.
 static int64_t split_lds_floats(int64_t K) { return 8 * ((int64_t)split_xrow((int)(K / 32)) + 4) + 2 * 64 * SPLIT_DSTRIDE; }
 
+// Bytes the tiled split kernel adds: the copied activations (and norm
+// weights) and every stage's tile.
+static int64_t split_tile_bytes(int64_t K, bool norm) {
+    const int64_t G = (K / 32 + 3) / 4, nstage = (G + SPLIT_SQ - 1) / SPLIT_SQ;
+    return K * 4 * (norm ? 2 : 1) + nstage * 3 * SPLIT_TILE_UNIT;
+}
+
 size_t gemv_lds_bytes(int64_t K, int fmt, bool norm) {
     // Q4_0: + what the reads ahead may touch past the last chain row: the row
     // walk's next group (16 floats) and the sum-of-squares chain's read-ahead
@@ -1874,16 +1993,28 @@ int launch_gemv(const GemvParams &p, hipStream_t s) {
     if (npairs == 0) return GAJE_OK;
     // latency-bound Q4_0 matvecs (few rows): split waves
     if (p.fmt == FMT_Q4_0 && (p.mode == MODE_STORE || p.mode == MODE_RESIDUAL || p.mode == MODE_QKV) && !p.gnorm &&
-        !p.x_out && 2 * npairs <= SPLIT_MAX_ROWS && p.nb > 0 && (!p.norm_w || p.K / 4 <= SPLIT_NORM_MAX_K4)) {
+        !p.x_out && 2 * npairs <= SPLIT_MAX_ROWS && p.nb > 0) {
         const size_t slds = (size_t)split_lds_floats(p.K) * 4;
-        if (slds + 1024 <= max_lds_per_block()) {
+        const size_t tlds = slds + (size_t)split_tile_bytes(p.K, p.norm_w != nullptr);
+        const int64_t G = (p.nb + 3) / 4;
+        const bool tile = (G + SPLIT_SQ - 1) / SPLIT_SQ <= SPLIT_TILE_MAX_STAGES && (int64_t)G * 80 <= 65536 &&
+                          tlds + 1024 <= max_lds_per_block();
+        const bool untiled = slds + 1024 <= max_lds_per_block() && (!p.norm_w || p.K / 4 <= SPLIT_NORM_MAX_K4);
+        if (tile || untiled) {
             const int64_t grid = (npairs + SPLIT_PAIRS - 1) / SPLIT_PAIRS;
             const int xs = split_xrow(p.nb) + 4;
             void (*fn)(GemvParams, int64_t, int);
-            if (p.mode == MODE_QKV) fn = p.norm_w ? gemv_q4_split_kernel<MODE_QKV, true> : gemv_q4_split_kernel<MODE_QKV, false>;
-            else if (p.mode == MODE_RESIDUAL) fn = p.norm_w ? gemv_q4_split_kernel<MODE_RESIDUAL, true> : gemv_q4_split_kernel<MODE_RESIDUAL, false>;
-            else fn = p.norm_w ? gemv_q4_split_kernel<MODE_STORE, true> : gemv_q4_split_kernel<MODE_STORE, false>;
-            hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(THREADS), slds, s, p, npairs, xs);
+            const bool n = p.norm_w != nullptr;
+            if (tile) {
+                if (p.mode == MODE_QKV) fn = n ? gemv_q4_split_kernel<MODE_QKV, true, true> : gemv_q4_split_kernel<MODE_QKV, false, true>;
+                else if (p.mode == MODE_RESIDUAL) fn = n ? gemv_q4_split_kernel<MODE_RESIDUAL, true, true> : gemv_q4_split_kernel<MODE_RESIDUAL, false, true>;
+                else fn = n ? gemv_q4_split_kernel<MODE_STORE, true, true> : gemv_q4_split_kernel<MODE_STORE, false, true>;
+            } else {
+                if (p.mode == MODE_QKV) fn = n ? gemv_q4_split_kernel<MODE_QKV, true, false> : gemv_q4_split_kernel<MODE_QKV, false, false>;
+                else if (p.mode == MODE_RESIDUAL) fn = n ? gemv_q4_split_kernel<MODE_RESIDUAL, true, false> : gemv_q4_split_kernel<MODE_RESIDUAL, false, false>;
+                else fn = n ? gemv_q4_split_kernel<MODE_STORE, true, false> : gemv_q4_split_kernel<MODE_STORE, false, false>;
+            }
+            hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(THREADS), tile ? tlds : slds, s, p, npairs, xs);
             GAJE_HIP_CHECK(hipGetLastError());
             return GAJE_OK;
         }

@@ -1799,7 +1799,7 @@ extern "C" int gaje_hip_time_stage(gaje_hip_model *m, int stage, int64_t layer, 
     if (stage >= GAJE_STAGE_QKV && stage <= GAJE_STAGE_DOWN && (layer < 0 || layer >= m->n_layers))
         return set_error(GAJE_ERR_INVALID_ARG, "layer %lld out of range", (long long)layer);
     GAJE_TRY(reserve_ctx(m, m->pos + 1));
-    if (stage == GAJE_STAGE_TOKEN) GAJE_TRY(ensure_graph(m));
+    if (stage == GAJE_STAGE_TOKEN && !m->profile) GAJE_TRY(ensure_graph(m));
     GAJE_TRY(launch_state_set(m->st, (int32_t)m->pos, 0, -1, -1, 1, m->stream));
     const int64_t nb_q = m->n_embd / 32;
     const size_t layer_kv = (size_t)m->n_kv * m->cap * m->hd;
@@ -1892,7 +1892,10 @@ extern "C" int gaje_hip_time_stage(gaje_hip_model *m, int stage, int64_t layer, 
                 for (auto &Ly : m->layers) a += wbytes(Ly.qkv) + wbytes(Ly.o) + wbytes(Ly.gate_up) + wbytes(Ly.down);
                 a += m->n_layers * (int64_t)(m->pos + 1) * 2 * m->kv_rows * 4;
                 algo = a;
-                GAJE_HIP_CHECK(hipGraphLaunch(m->graph_exec, m->stream));
+                // profiling builds launch the token's kernels one by one: the
+                // kernel tracer faults on graph replays
+                if (m->profile) GAJE_TRY(enqueue_token(m, nullptr));
+                else GAJE_HIP_CHECK(hipGraphLaunch(m->graph_exec, m->stream));
                 // keep the position fixed so every replay is the same token
                 return launch_state_set(m->st, (int32_t)m->pos, 0, -1, -1, 1, m->stream);
             }
