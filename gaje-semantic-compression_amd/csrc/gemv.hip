@@ -1549,20 +1549,7 @@ __device__ __forceinline__ float q4_chain4(float acc, const float4 d, const floa
     return acc;
 }
 
-// The tiled form (TILE) copies the workgroup's whole share of the matrix into
-// LDS when it starts: producer wave pw copies, for every stage, the bytes of
-// its SPLIT_PQ groups of the 8 rows (1280 bytes, unit (row, j) at 160 row +
-// 80 j) with global_load_lds_dwordx4, two instructions per stage, all issued
-// before the first stage is produced; wave 0 copies the activations (and the
-// norm weights) the same way in one batch.  Every load then waits out one
-// memory latency instead of one per stage.  The producers dequantise from LDS
-// with q4_dequant_dw (the values of q4_dequant, fewer instructions), one
-// barrier per stage.  The copies are inline assembly waited with explicit
-// vmcnt counts (stage s of nstage may leave 2 (nstage - 1 - s) outstanding).
-constexpr int SPLIT_TILE_UNIT = 8 * SPLIT_PQ * 80;  // bytes one producer copies per stage
-constexpr int SPLIT_TILE_MAX_STAGES = 31;           // 2 copies per stage within the six-bit vmcnt
-
-template <int MODE, bool NORM, bool TILE>
+template <int MODE, bool NORM>
 __global__ __launch_bounds__(THREADS) void gemv_q4_split_kernel(GemvParams p, int64_t npairs, int xstride) {
     extern __shared__ __align__(16) float smem[];
     DevState *st = p.st;
@@ -1571,9 +1558,6 @@ __global__ __launch_bounds__(THREADS) void gemv_q4_split_kernel(GemvParams p, in
     const int nb = p.nb, G = (nb + 3) >> 2, nstage = (G + SPLIT_SQ - 1) / SPLIT_SQ;
     const XView xv{smem, xstride};
     float *ring = smem + 8 * xstride;  // [2][64 chain lanes][SPLIT_DSTRIDE]
-    // TILE: the activations (and norm weights) as copied, then the tile
-    uint8_t *raw = (uint8_t *)(ring + 2 * 64 * SPLIT_DSTRIDE);
-    uint8_t *tile = raw + K * 4 * (NORM ? 2 : 1);
     const int l = lane & 7;
     const int64_t pr = (int64_t)blockIdx.x * SPLIT_PAIRS + (lane >> 4);
     PairRows q;  // (locate, with the pairing of this kernel's mode only)
@@ -1590,68 +1574,9 @@ __global__ __launch_bounds__(THREADS) void gemv_q4_split_kernel(GemvParams p, in
     }
     q.row = ((lane >> 3) & 1) ? q.r1 : q.r0;
     q.row_ok = q.pair_ok && q.row >= 0 && q.row < p.rows_valid;
-    if constexpr (TILE) {
-        if (wave > 0) {
-            // ---- producers, tiled: copy every stage's bytes, then dequantise
-            // stage by stage as the copies land ----
-            const int pw = wave - 1;
-            const uint8_t *src[2];
-            int jj[2];
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {  // this lane's 16 bytes of each copy
-                const int b = i * 1024 + lane * 16, rho = (b < SPLIT_TILE_UNIT ? b : 0) / 160;
-                jj[i] = (b % 160) / 80;
-                const int64_t cpr = (int64_t)blockIdx.x * SPLIT_PAIRS + (rho >> 1);
-                int64_t c0 = 0, c1 = -1;
-                if (cpr < npairs) {
-                    if constexpr (MODE == MODE_QKV) {
-                        pair_rows(p, MODE_QKV, cpr, c0, c1);
-                    } else {
-                        c0 = 2 * cpr;
-                        c1 = 2 * cpr + 1 < p.N ? 2 * cpr + 1 : -1;
-                    }
-                }
-                const int64_t row = (rho & 1) ? c1 : c0;
-                const bool ok = cpr < npairs && row >= 0 && row < p.rows_valid;
-                src[i] = (p.rows_valid > 0 ? p.w : kZeroRows) + (size_t)(ok ? row : 0) * G * 80 + b % 80;
-            }
-            for (int sg = 0; sg < nstage; ++sg) {
-                const uint32_t dst = lds_addr(tile + (size_t)(sg * 3 + pw) * SPLIT_TILE_UNIT);
-                const int g0 = sg * SPLIT_SQ + pw * SPLIT_PQ;
-                const int ga = g0 + jj[0] < G ? g0 + jj[0] : G - 1, gb = g0 + jj[1] < G ? g0 + jj[1] : G - 1;
-                lds_dma16(src[0] + (size_t)ga * 80, dst);
-                if (lane < (SPLIT_TILE_UNIT - 1024) / 16) lds_dma16(src[1] + (size_t)gb * 80, dst + 1024);
-            }
-            if (st && s_load_i32(&st->halted)) {
-                wait_vmcnt<0>();  // no copy may land after the workgroup's LDS is released
-                return;           // uniform
-            }
-            const int rho = lane >> 3;
-            for (int sg = 0; sg < nstage; ++sg) {
-                wait_vmcnt_stages<2, SPLIT_TILE_MAX_STAGES>(nstage - 1 - sg);
-                const uint8_t *u = tile + (size_t)(sg * 3 + pw) * SPLIT_TILE_UNIT + rho * 160;
-                float *dst = ring + ((sg & 1) * 64 + lane) * SPLIT_DSTRIDE + 16 * pw * SPLIT_PQ;
-#pragma unroll
-                for (int j = 0; j < SPLIT_PQ; ++j) {
-                    const vu2 n = *(const vu2 *)(u + j * 80 + 8 * l);
-                    const vu4 sw = *(const vu4 *)(u + j * 80 + 64);
-                    float d[4][4];
-                    q4_dequant_dw<0>(d[0], n.x, sw.x);
-                    q4_dequant_dw<1>(d[1], n.x, sw.y);
-                    q4_dequant_dw<0>(d[2], n.y, sw.z);
-                    q4_dequant_dw<1>(d[3], n.y, sw.w);
-#pragma unroll
-                    for (int b = 0; b < 4; ++b)
-                        *(float4 *)(dst + 16 * j + 4 * b) = make_float4(d[b][0], d[b][1], d[b][2], d[b][3]);
-                }
-                lds_barrier();
-            }
-            return;  // wave 0 passes no further barrier
-        }
-    }
-    const int halted = TILE ? 0 : (st ? st->halted : 0);
+    const int halted = st ? st->halted : 0;
 
-    if (!TILE && wave > 0) {
+    if (wave > 0) {
         // ---- producers: wave 1 + pw dequantises groups pw*PQ .. pw*PQ + PQ-1
         // of every stage for the 64 chain lanes; loads run two stages ahead.
         // Stages are produced in pairs with no branch around the loads (past
@@ -1699,41 +1624,23 @@ __global__ __launch_bounds__(THREADS) void gemv_q4_split_kernel(GemvParams p, in
     }
 
     // ---- wave 0 ----
-    if constexpr (TILE) {
-        lds_copy_bytes(p.x, K * 4, lds_addr(raw), lane);
-        if constexpr (NORM) lds_copy_bytes(p.norm_w, K * 4, lds_addr(raw + K * 4), lane);
-        if (st && s_load_i32(&st->halted)) {
-            wait_vmcnt<0>();
-            return;
-        }
-        wait_vmcnt<0>();  // this wave's copies have landed (it alone reads them)
-    }
     if (halted) return;
     // activations -> chain-major LDS (batches of 8 float4 per lane); with a
     // norm the vector is one batch and stays in registers for the normalising
-    // (tiled: read from the copies, any length)
     const bool leader = q.pair_ok && (lane & 15) == 0;
     float b0 = 0.0f, b1 = 0.0f, old0 = 0.0f, old1 = 0.0f, cs = 0.0f, sn = 0.0f;
     int pos = 0;
-    const float4 *x4 = TILE ? (const float4 *)raw : (const float4 *)p.x;
-    const float4 *w4 = TILE ? (const float4 *)(raw + K * 4) : (const float4 *)p.norm_w;  // used exactly when NORM
+    const float4 *x4 = (const float4 *)p.x;
+    const float4 *w4 = (const float4 *)p.norm_w;  // non-null exactly when NORM
     int bad_in = 0;
-    float4 v[8], w[NORM && !TILE ? 8 : 1];
-    if constexpr (TILE) {
-        for (int64_t m = lane; m < K4; m += 64) {
-            const float4 a = x4[m];
-            const float qd[4] = {a.x, a.y, a.z, a.w};
-            store_quad<true>(xv, (int)m, qd);
-            bad_in |= isnan(a.x) | isnan(a.y) | isnan(a.z) | isnan(a.w);
-        }
-    }
-    for (int64_t m0 = 0; !TILE && m0 < K4; m0 += 8 * 64) {
+    float4 v[8], w[NORM ? 8 : 1];
+    for (int64_t m0 = 0; m0 < K4; m0 += 8 * 64) {
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
             const int64_t m = m0 + u * 64 + lane;
             v[u] = x4[m < K4 ? m : K4 - 1];
         }
-        if constexpr (NORM && !TILE) {
+        if constexpr (NORM) {
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
                 const int64_t m = m0 + u * 64 + lane;
@@ -1783,11 +1690,12 @@ __global__ __launch_bounds__(THREADS) void gemv_q4_split_kernel(GemvParams p, in
         const float tot = u2 + __shfl(u2, (lane + 2) & 7, 8);
         const float inv = __shfl(1.0f / sqrtf(tot / (float)K + p.eps), 0, WAVE);
         int bad = 0;
-        if constexpr (TILE) {
-            for (int64_t m = lane; m < K4; m += 64) {
-                const float4 a = x4[m], b = w4[m];
-                float t[4] = {a.x * inv, a.y * inv, a.z * inv, a.w * inv};
-                const float wn[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int64_t m = u * 64 + lane;
+            if (m < K4) {
+                float t[4] = {v[u].x * inv, v[u].y * inv, v[u].z * inv, v[u].w * inv};
+                const float wn[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
                     t[c] = t[c] * wn[c];
@@ -1795,28 +1703,13 @@ __global__ __launch_bounds__(THREADS) void gemv_q4_split_kernel(GemvParams p, in
                 }
                 store_quad<true>(xv, (int)m, t);
             }
-        } else {
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int64_t m = u * 64 + lane;
-                if (m < K4) {
-                    float t[4] = {v[u].x * inv, v[u].y * inv, v[u].z * inv, v[u].w * inv};
-                    const float wn[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
-#pragma unroll
-                    for (int c = 0; c < 4; ++c) {
-                        t[c] = t[c] * wn[c];
-                        bad |= isnan(t[c]);
-                    }
-                    store_quad<true>(xv, (int)m, t);
-                }
-            }
         }
         if (__any(bad) && p.st_norm >= 0 && lane == 0) nan_flag(st, p.layer, p.st_norm);
     }
     // the 64 chains, one stage per barrier
     float acc = 0.0f;
     const float *xg = xv.x + l * xstride;
-    const int nbar = TILE ? nstage : (nstage + 1) & ~1;  // the producers' barriers (untiled: stages in pairs)
+    const int nbar = (nstage + 1) & ~1;  // the producers' barriers (stages in pairs)
     for (int s = 0; s < nbar; ++s) {
         lds_barrier();
         if (s >= nstage) break;  // (the producers' unused last stage)
@@ -1861,6 +1754,403 @@ __global__ __launch_bounds__(THREADS) void gemv_q4_split_kernel(GemvParams p, in
     } else {
         qkv_store(p, r0, r1, y0, y1, cs, sn, pos);
     }
+}
+
+// ----------------------------------- Q4_0, one chain wave fed from LDS ----
+// The split kernel's division of labour on a narrower tile, for matvecs of up
+// to a few thousand rows.  Wave 0 of a workgroup walks the 32 chains of 4 rows
+// (2 row pairs; lane 8ρ + l is chain l of row ρ, lanes 32..63 idle in the
+// walk) and does nothing per weight but its fma: the dequantised values come
+// from an LDS ring that waves 1..3 fill one stage (CH_SQ packed groups) ahead,
+// one producer lane per (chain, group) of the stage.  Measured on the 896-row
+// matvecs of a 0.5B decode, an 8-row walk is bound by the LDS port (the eight
+// rows of a chain read the same activations, and each read costs its full
+// width), at about 13 cycles per step against the 4.6 of one wave's fma issue;
+// with 4 rows the bytes per step fit under the fma rate.
+//
+// Everything the workgroup reads is copied into LDS when it starts, with
+// global_load_lds_dwordx4 (inline assembly, waited with explicit vmcnt counts):
+// each producer copies its 4 rows x 2 groups (640 bytes, one instruction) of
+// every stage before dequantising the first, and wave 0 copies the activations
+// (and the norm weights).  The chains read the activations in their natural
+// layout (element 128g + 32b + 8c + l for chain l's value c of block b of
+// group g: ds_read2 pairs), so nothing is rearranged before the first step.
+// The values, the chain order, the reduction and the epilogues are the split
+// kernel's, so the result is the same bit for bit.
+constexpr int CH_PAIRS = 2;                     // row pairs per workgroup
+constexpr int CH_LANES = 16 * CH_PAIRS;         // chain lanes (4 rows x 8 chains)
+constexpr int CH_SQ = 3 * WAVE / CH_LANES;      // groups per stage: one per producer lane
+constexpr int CH_DSTRIDE = 16 * CH_SQ + 4;      // ring floats per chain lane (stride / 4 odd)
+constexpr int CH_UNIT = 2 * CH_PAIRS * 2 * 80;  // bytes one producer copies per stage
+constexpr int CH_MAX_STAGES = 60;               // one copy per stage within the six-bit vmcnt
+constexpr int CH_AHEAD = 2;                     // groups of ring reads in flight ahead of the fmas
+constexpr int CH_XREG_MAX = 8;                  // rows of up to this many groups keep x in registers
+static_assert(CH_SQ == 6 && CH_UNIT <= 1024, "one copy instruction per producer and stage");
+
+// The rows of chain lane cl (0..CH_LANES-1) of this workgroup.
+template <int MODE>
+__device__ __forceinline__ PairRows chain_rows(const GemvParams &p, int64_t npairs, int cl) {
+    PairRows q;
+    const int64_t pr = (int64_t)blockIdx.x * CH_PAIRS + (cl >> 4);
+    q.pair_ok = pr < npairs;
+    q.r0 = 0;
+    q.r1 = -1;
+    if (q.pair_ok) {
+        if constexpr (MODE == MODE_QKV) {
+            pair_rows(p, MODE_QKV, pr, q.r0, q.r1);
+        } else {
+            q.r0 = 2 * pr;
+            q.r1 = 2 * pr + 1 < p.N ? 2 * pr + 1 : -1;
+        }
+    }
+    q.row = ((cl >> 3) & 1) ? q.r1 : q.r0;
+    q.row_ok = q.pair_ok && q.row >= 0 && q.row < p.rows_valid;
+    return q;
+}
+
+// Chain-major row stride (floats) of gemv_q4_chain_kernel: 16 per packed
+// group, plus 4 so that stride / 4 is odd (the eight rows' 16-byte reads fall
+// in distinct banks).
+__host__ __device__ constexpr int chain_xstride(int64_t K) { return (int)(16 * ((K / 32 + 3) / 4) + 4); }
+
+// LDS bytes of gemv_q4_chain_kernel: the ring, the activations as copied (zero
+// to the last group's end), with a norm its weights, the chain-major copy and
+// the stages' copies.
+__host__ __device__ constexpr int64_t chain_lds_bytes(int64_t K, bool norm) {
+    const int64_t G = (K / 32 + 3) / 4, xf = 128 * G, nstage = (G + CH_SQ - 1) / CH_SQ;
+    return (2 * CH_LANES * CH_DSTRIDE + xf + (norm ? K : 0) + 8 * (int64_t)chain_xstride(K)) * 4 +
+           nstage * 3 * CH_UNIT;
+}
+
+// rms_norm's reduction of the eight sum-of-squares chains held by lanes 0..7:
+// ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7)), read out of the lanes (no LDS round
+// trip), the same value in every lane.
+__device__ __forceinline__ float rms_tot8(float a) {
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), i));
+    return ((v[0] + v[4]) + (v[1] + v[5])) + ((v[2] + v[6]) + (v[3] + v[7]));
+}
+
+template <int MODE, bool NORM, int GX>
+__global__ __launch_bounds__(THREADS) void gemv_q4_chain_kernel(GemvParams p, int64_t npairs, int xstride) {
+    extern __shared__ __align__(16) float smem[];
+    DevState *st = p.st;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t K = p.K, K4 = K >> 2;
+    const int nb = p.nb, G = GX > 0 ? GX : (nb + 3) >> 2, nstage = (G + CH_SQ - 1) / CH_SQ;  // (G == GX: launcher)
+    const int64_t XF = 128 * (int64_t)G;
+    float *ring = smem;                              // [2][CH_LANES][CH_DSTRIDE]
+    float *xs = ring + 2 * CH_LANES * CH_DSTRIDE;    // activations as copied, zero from K to XF
+    float *wn = xs + XF;                             // NORM: the norm weights (K)
+    float *xcm = wn + (NORM ? K : 0);                // the chain-major copy: 8 rows of xstride
+    uint8_t *tile = (uint8_t *)(xcm + 8 * xstride);  // [stage][producer][CH_UNIT]
+
+    if (wave > 0) {
+        // ---- producers: copy every stage's bytes, then dequantise stage by
+        // stage as the copies land.  Copy lane i (i < 40) moves bytes 16i..16i+15
+        // of the unit: (row ρ, group j) at 160 ρ + 80 j ----
+        const int pw = wave - 1;
+        const uint8_t *src;
+        int jj;
+        {
+            const int b = lane * 16 < CH_UNIT ? lane * 16 : 0, u = b / 80;
+            jj = u & 1;
+            const PairRows q = chain_rows<MODE>(p, npairs, 8 * (u >> 1));
+            src = (p.rows_valid > 0 ? p.w : kZeroRows) + (size_t)(q.row_ok ? q.row : 0) * G * 80 + b % 80;
+        }
+        for (int sg = 0; sg < nstage; ++sg) {
+            int g = sg * CH_SQ + 2 * pw + jj;
+            g = g < G ? g : G - 1;  // past the row: its last group again, never read by a chain
+            if (lane < CH_UNIT / 16)
+                lds_dma16(src + (size_t)g * 80, lds_addr(tile + (size_t)(sg * 3 + pw) * CH_UNIT));
+        }
+        if (st && s_load_i32(&st->halted)) {
+            wait_vmcnt<0>();  // no copy may land after the workgroup's LDS is released
+            return;           // uniform
+        }
+        const int cl = lane & (CH_LANES - 1), l = cl & 7, jl = lane >> 5;
+        for (int sg = 0; sg < nstage; ++sg) {
+            wait_vmcnt_stages<1, CH_MAX_STAGES>(nstage - 1 - sg);
+            const uint8_t *u = tile + (size_t)(sg * 3 + pw) * CH_UNIT + (cl >> 3) * 160 + jl * 80;
+            const vu2 n = *(const vu2 *)(u + 8 * l);
+            const vu4 sw = *(const vu4 *)(u + 64);
+            float d[4][4];
+            q4_dequant_dw<0>(d[0], n.x, sw.x);
+            q4_dequant_dw<1>(d[1], n.x, sw.y);
+            q4_dequant_dw<0>(d[2], n.y, sw.z);
+            q4_dequant_dw<1>(d[3], n.y, sw.w);
+            float *dst = ring + ((sg & 1) * CH_LANES + cl) * CH_DSTRIDE + 16 * (2 * pw + jl);
+#pragma unroll
+            for (int b = 0; b < 4; ++b) *(float4 *)(dst + 4 * b) = make_float4(d[b][0], d[b][1], d[b][2], d[b][3]);
+            lds_barrier();
+        }
+        // the activations landed before wave 0's first barrier: NaN inputs are
+        // flagged here, off the chains' path
+        int bad = 0;
+        for (int64_t m = (int64_t)(wave - 1) * WAVE + lane; m < K4; m += 3 * WAVE) {
+            const float4 v = *(const float4 *)(xs + 4 * m);
+            bad |= isnan(v.x) | isnan(v.y) | isnan(v.z) | isnan(v.w);
+        }
+        if (__any(bad) && p.st_in >= 0 && lane == 0) nan_flag(st, p.layer, p.st_in);
+        return;  // wave 0 passes no further barrier
+    }
+
+    // ---- wave 0: the activations (and the norm weights), then the
+    // epilogue operands (they land with them) ----
+    const PairRows q = chain_rows<MODE>(p, npairs, lane & (CH_LANES - 1));
+    const bool leader = lane < CH_LANES && q.pair_ok && (lane & 15) == 0;
+    float b0 = 0.0f, b1 = 0.0f, old0 = 0.0f, old1 = 0.0f, cs = 0.0f, sn = 0.0f;
+    int pos = 0;
+    for (int64_t m = K4 + lane; m < XF / 4; m += WAVE) *(float4 *)(xs + 4 * m) = make_float4(0.f, 0.f, 0.f, 0.f);
+    lds_copy_bytes(p.x, K * 4, lds_addr(xs), lane);
+    if constexpr (NORM) lds_copy_bytes(p.norm_w, K * 4, lds_addr(wn), lane);
+    if (leader) {  // (after the copies: their addresses need no kernel argument)
+        if (q.r0 < p.bias_len) b0 = p.bias[q.r0];
+        if (q.r1 >= 0 && q.r1 < p.bias_len) b1 = p.bias[q.r1];
+        if constexpr (MODE == MODE_RESIDUAL) {
+            old0 = p.y[q.r0];
+            if (q.r1 >= 0) old1 = p.y[q.r1];
+        } else if constexpr (MODE == MODE_QKV) {
+            pos = st->pos;
+            const int hh = p.head_dim >> 1;
+            const int i = (int)(((int64_t)blockIdx.x * CH_PAIRS + (lane >> 4)) % hh);
+            cs = p.rope_cos[(size_t)pos * hh + i];
+            sn = p.rope_sin[(size_t)pos * hh + i];
+        }
+    }
+    if (st && s_load_i32(&st->halted)) {
+        wait_vmcnt<0>();
+        return;
+    }
+    wait_vmcnt<0>();  // this wave's copies have landed (it alone reads them before the barriers)
+    const int l = lane & 7;
+    float4 xq[GX > 0 ? 4 * GX : 1];  // GX > 0: chain l's values c = 4i..4i+3 at xq[i]
+    const float *xr = xcm + l * xstride;  // GX == 0: chain l's row of the chain-major copy
+    if constexpr (GX > 0) {
+        // rows of at most 8 groups: each chain lane reads its 16 GX values
+        // straight from the copy (element 8c + l, zero from K), no chain-major
+        // copy.  With a norm: rms_norm (norm.rs:52-88), eight fma chains over
+        // elements 8c + l (lanes 0..7, from registers; fma(0, 0, acc) leaves a
+        // chain as it is past K / 8), ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7)),
+        // then (x * inv) * w for every element, each product rounded, into
+        // the normalised copy (xcm's space, natural layout), which the lanes
+        // then read as above
+        const float *src = xs;
+        if constexpr (NORM) {
+            float ss = 0.0f;
+            if (lane < 8) {
+                // reads two 16-value chunks ahead of the fmas (pinned)
+                constexpr int NC = GX;  // chunks of 16 values
+                float v[3][16];
+                auto load = [&](int k, float (&d)[16]) {
+#pragma unroll
+                    for (int c = 0; c < 16; ++c) d[c] = xs[8 * (16 * k + c) + lane];
+                };
+                load(0, v[0]);
+                if (NC > 1) load(1, v[1]);
+#pragma unroll
+                for (int k = 0; k < NC; ++k) {
+                    if (k + 2 < NC) load(k + 2, v[(k + 2) % 3]);
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int c = 0; c < 16; ++c) ss = fmaf(v[k % 3][c], v[k % 3][c], ss);
+                }
+            }
+            const float tot = rms_tot8(ss);
+            const float inv = 1.0f / sqrtf(tot / (float)K + p.eps);
+            constexpr int NQ = (32 * GX + WAVE - 1) / WAVE;  // quads of XF per lane
+            float4 a[NQ], w[NQ];
+#pragma unroll
+            for (int u = 0; u < NQ; ++u) {
+                const int m = u * WAVE + lane < 32 * GX ? u * WAVE + lane : 0;
+                a[u] = *(const float4 *)(xs + 4 * m);
+                w[u] = *(const float4 *)(wn + 4 * (m < K4 ? m : 0));
+            }
+            int bad = 0;
+#pragma unroll
+            for (int u = 0; u < NQ; ++u) {
+                const int m = u * WAVE + lane;
+                if (m < 32 * GX) {
+                    const float4 o = make_float4((a[u].x * inv) * w[u].x, (a[u].y * inv) * w[u].y,
+                                                 (a[u].z * inv) * w[u].z, (a[u].w * inv) * w[u].w);
+                    if (m < K4) bad |= isnan(o.x) | isnan(o.y) | isnan(o.z) | isnan(o.w);
+                    *(float4 *)(xcm + 4 * m) = m < K4 ? o : make_float4(0.f, 0.f, 0.f, 0.f);
+                }
+            }
+            if (__any(bad) && p.st_norm >= 0 && lane == 0) nan_flag(st, p.layer, p.st_norm);
+            src = xcm;
+        }
+        if (lane < CH_LANES) {
+#pragma unroll
+            for (int i = 0; i < 4 * GX; ++i)
+                xq[i] = make_float4(src[32 * i + l], src[32 * i + 8 + l], src[32 * i + 16 + l], src[32 * i + 24 + l]);
+        }
+    } else {
+        // longer rows: the chain-major copy, row l holding elements 8c + l at c
+        // (zero from K / 8): 32 elements (8 quads) per lane and round, chain l
+        // of elements 32q.. being (x[32q + l], x[32q + 8 + l], x[32q + 16 + l],
+        // x[32q + 24 + l]) at c = 4q of row l
+        for (int64_t qd = lane; qd < XF / 32; qd += WAVE) {
+            float4 f[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) f[k] = *(const float4 *)(xs + 32 * qd + 4 * k);
+#pragma unroll
+            for (int ll = 0; ll < 8; ++ll) {
+                const int h = ll >> 2;
+                auto pick = [&](const float4 &v) { return (ll & 3) == 0 ? v.x : (ll & 3) == 1 ? v.y : (ll & 3) == 2 ? v.z : v.w; };
+                *(float4 *)(xcm + ll * xstride + 4 * qd) = make_float4(pick(f[h]), pick(f[2 + h]), pick(f[4 + h]), pick(f[6 + h]));
+            }
+        }
+        if constexpr (NORM) {
+            // rms_norm as above, over the chain-major rows, in place
+            float ss = 0.0f;
+            if (lane < 8) {
+                const float4 *r4 = (const float4 *)(xcm + lane * xstride);
+#pragma unroll 8
+                for (int64_t c = 0; c < XF / 32; ++c) {
+                    const float4 v = r4[c];
+                    ss = fmaf(v.x, v.x, ss);
+                    ss = fmaf(v.y, v.y, ss);
+                    ss = fmaf(v.z, v.z, ss);
+                    ss = fmaf(v.w, v.w, ss);
+                }
+            }
+            const float u1 = ss + __shfl(ss, (lane + 4) & 7, 8);
+            const float u2 = u1 + __shfl(u1, (lane + 1) & 7, 8);
+            const float tot = u2 + __shfl(u2, (lane + 2) & 7, 8);
+            const float inv = __shfl(1.0f / sqrtf(tot / (float)K + p.eps), 0, WAVE);
+            int bad = 0;
+            for (int64_t m = lane; m < K4; m += WAVE) {  // quad m: row m % 8, c = 4 (m / 8) < K / 8
+                const int ll = (int)(m & 7);
+                const int64_t c = 4 * (m >> 3);
+                float4 &v = *(float4 *)(xcm + ll * xstride + c);
+                const float4 a = v;
+                const float *w = wn + 8 * c + ll;
+                v = make_float4((a.x * inv) * w[0], (a.y * inv) * w[8], (a.z * inv) * w[16], (a.w * inv) * w[24]);
+                bad |= isnan(v.x) | isnan(v.y) | isnan(v.z) | isnan(v.w);
+            }
+            if (__any(bad) && p.st_norm >= 0 && lane == 0) nan_flag(st, p.layer, p.st_norm);
+        }
+    }
+
+    // ---- the 32 chains, one stage per barrier.  Each group's ring values
+    // (and, from LDS, activations) are read CH_AHEAD groups ahead of its fmas,
+    // the order pinned with scheduling barriers (the compiler otherwise moves
+    // each read to just before its use and waits out its latency).  With
+    // GX > 0 (rows of GX <= 8 packed groups) chain l's activations sit in
+    // registers for the whole walk: a wave pays about 9 cycles of issue per
+    // 512-byte LDS read against 4.6 per fma, so halving the reads per group
+    // is most of the walk's speed ----
+    float acc = 0.0f;
+    auto walk_stage = [&](int sg) {
+        const float *dl = ring + ((sg & 1) * CH_LANES + lane) * CH_DSTRIDE;
+        const int g0 = sg * CH_SQ;
+        auto getx = [&](int j) -> X4 {
+            if constexpr (GX > 0) {
+                const int g = g0 + j < GX ? g0 + j : GX - 1;
+                return X4{xq[4 * g], xq[4 * g + 1], xq[4 * g + 2], xq[4 * g + 3]};
+            } else {
+                return read_x4(xr + 16 * (g0 + j < G ? g0 + j : G - 1));
+            }
+        };
+        X4 d[CH_AHEAD], x[CH_AHEAD];
+#pragma unroll
+        for (int k = 0; k < CH_AHEAD; ++k) {
+            d[k] = read_x4(dl + 16 * k);
+            x[k] = getx(k);
+        }
+#pragma unroll
+        for (int j = 0; j < CH_SQ; ++j) {
+            X4 dn = d[CH_AHEAD - 1], xn = x[CH_AHEAD - 1];
+            if (j + CH_AHEAD < CH_SQ) {
+                dn = read_x4(dl + 16 * (j + CH_AHEAD));
+                xn = getx(j + CH_AHEAD);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (j == 0 || g0 + j < G) {  // (group g0 exists: sg < nstage)
+                acc = q4_chain4(acc, d[0].b0, x[0].b0);
+                acc = q4_chain4(acc, d[0].b1, x[0].b1);
+                acc = q4_chain4(acc, d[0].b2, x[0].b2);
+                acc = q4_chain4(acc, d[0].b3, x[0].b3);
+            }
+#pragma unroll
+            for (int k = 0; k + 1 < CH_AHEAD; ++k) {
+                d[k] = d[k + 1];
+                x[k] = x[k + 1];
+            }
+            d[CH_AHEAD - 1] = dn;
+            x[CH_AHEAD - 1] = xn;
+        }
+    };
+    if constexpr (GX > 0) {
+        constexpr int NST = (GX + CH_SQ - 1) / CH_SQ;
+#pragma unroll
+        for (int sg = 0; sg < NST; ++sg) {
+            lds_barrier();
+            if (lane < CH_LANES) walk_stage(sg);
+        }
+    } else {
+        for (int sg = 0; sg < nstage; ++sg) {
+            lds_barrier();
+            if (lane < CH_LANES) walk_stage(sg);
+        }
+    }
+    // lanes 8ρ..8ρ+7 hold a row's chains 0..7: the reduction of q4_consume
+    const int base = lane & ~7;
+    const float u = acc + shfl(acc, base + ((l + 4) & 7));
+    const float vv = u + shfl(u, base + ((l + 2) & 7));
+    const float total = q.row_ok ? flush_small(vv + shfl(vv, base + ((l + 1) & 7))) : 0.0f;
+    const float v1 = shfl(total, (lane & ~15) + 8);  // the pair's second row
+    if (!leader) return;
+    auto finish = [&](int64_t r, float v, float bias) {  // finish_row over this kernel's copy of x
+        if (p.a_ptr) {
+            for (int64_t k = p.a_ptr[r]; k < p.a_ptr[r + 1]; ++k) {
+                const int64_t e = p.a_col[k];
+                const float xe = GX > 0 ? (NORM ? xcm[e] : xs[e]) : xcm[(e & 7) * xstride + (e >> 3)];
+                const float prod = xe * half_bits(p.a_val[k]);
+                v = v + prod;
+            }
+        }
+        if (r < p.bias_len) v = v + bias;
+        return v;
+    };
+    const int64_t r0 = q.r0, r1 = q.r1;
+    const float y0 = finish(r0, total, b0);
+    const float y1 = r1 >= 0 ? finish(r1, v1, b1) : 0.0f;
+    if constexpr (MODE == MODE_STORE) {
+        p.y[r0] = y0;
+        if (r1 >= 0) p.y[r1] = y1;
+    } else if constexpr (MODE == MODE_RESIDUAL) {
+        if (isnan(y0) || (r1 >= 0 && isnan(y1))) nan_flag(st, p.layer, p.st_a);
+        const float h0 = old0 + y0;
+        p.y[r0] = h0;
+        bool bad = isnan(h0);
+        if (r1 >= 0) {
+            const float h1 = old1 + y1;
+            p.y[r1] = h1;
+            bad |= isnan(h1);
+        }
+        if (bad) nan_flag(st, p.layer, p.st_b);
+    } else {
+        qkv_store(p, r0, r1, y0, y1, cs, sn, pos);
+    }
+}
+
+// gemv_q4_chain_kernel for a mode, norm and row length (G packed groups).
+template <int MODE, bool NORM, int GX = CH_XREG_MAX>
+void (*chain_kernel_g(int G))(GemvParams, int64_t, int) {
+    if constexpr (GX == 0) {
+        return gemv_q4_chain_kernel<MODE, NORM, 0>;
+    } else {
+        if (G == GX) return gemv_q4_chain_kernel<MODE, NORM, GX>;
+        return chain_kernel_g<MODE, NORM, GX - 1>(G);
+    }
+}
+void (*chain_kernel(int mode, bool norm, int G))(GemvParams, int64_t, int) {
+    if (mode == MODE_QKV) return norm ? chain_kernel_g<MODE_QKV, true>(G) : chain_kernel_g<MODE_QKV, false>(G);
+    if (mode == MODE_RESIDUAL) return norm ? chain_kernel_g<MODE_RESIDUAL, true>(G) : chain_kernel_g<MODE_RESIDUAL, false>(G);
+    return norm ? chain_kernel_g<MODE_STORE, true>(G) : chain_kernel_g<MODE_STORE, false>(G);
 }
 
 using KernelFn = void (*)(GemvParams, int64_t, int, int);
@@ -1928,13 +2218,6 @@ static int64_t gemv_x_floats(int64_t K, int fmt) {
 // the row) and the two ring buffers.
 static int64_t split_lds_floats(int64_t K) { return 8 * ((int64_t)split_xrow((int)(K / 32)) + 4) + 2 * 64 * SPLIT_DSTRIDE; }
 
-// Bytes the tiled split kernel adds: the copied activations (and norm
-// weights) and every stage's tile.
-static int64_t split_tile_bytes(int64_t K, bool norm) {
-    const int64_t G = (K / 32 + 3) / 4, nstage = (G + SPLIT_SQ - 1) / SPLIT_SQ;
-    return K * 4 * (norm ? 2 : 1) + nstage * 3 * SPLIT_TILE_UNIT;
-}
-
 size_t gemv_lds_bytes(int64_t K, int fmt, bool norm) {
     // Q4_0: + what the reads ahead may touch past the last chain row: the row
     // walk's next group (16 floats) and the sum-of-squares chain's read-ahead
@@ -1993,28 +2276,29 @@ int launch_gemv(const GemvParams &p, hipStream_t s) {
     if (npairs == 0) return GAJE_OK;
     // latency-bound Q4_0 matvecs (few rows): split waves
     if (p.fmt == FMT_Q4_0 && (p.mode == MODE_STORE || p.mode == MODE_RESIDUAL || p.mode == MODE_QKV) && !p.gnorm &&
-        !p.x_out && 2 * npairs <= SPLIT_MAX_ROWS && p.nb > 0) {
-        const size_t slds = (size_t)split_lds_floats(p.K) * 4;
-        const size_t tlds = slds + (size_t)split_tile_bytes(p.K, p.norm_w != nullptr);
+        !p.x_out && p.nb > 0 && (npairs + CH_PAIRS - 1) / CH_PAIRS <= 2 * (int64_t)device_cu_count()) {
         const int64_t G = (p.nb + 3) / 4;
-        const bool tile = (G + SPLIT_SQ - 1) / SPLIT_SQ <= SPLIT_TILE_MAX_STAGES && (int64_t)G * 80 <= 65536 &&
-                          tlds + 1024 <= max_lds_per_block();
-        const bool untiled = slds + 1024 <= max_lds_per_block() && (!p.norm_w || p.K / 4 <= SPLIT_NORM_MAX_K4);
-        if (tile || untiled) {
+        const size_t clds = (size_t)chain_lds_bytes(p.K, p.norm_w != nullptr);
+        if ((G + CH_SQ - 1) / CH_SQ <= CH_MAX_STAGES && G * 80 <= (int64_t)sizeof(kZeroRows) &&
+            clds + 1024 <= max_lds_per_block()) {
+            const int64_t grid = (npairs + CH_PAIRS - 1) / CH_PAIRS;
+            void (*fn)(GemvParams, int64_t, int) = chain_kernel(p.mode, p.norm_w != nullptr, (int)G);
+            hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(THREADS), clds, s, p, npairs, chain_xstride(p.K));
+            GAJE_HIP_CHECK(hipGetLastError());
+            return GAJE_OK;
+        }
+    }
+    if (p.fmt == FMT_Q4_0 && (p.mode == MODE_STORE || p.mode == MODE_RESIDUAL || p.mode == MODE_QKV) && !p.gnorm &&
+        !p.x_out && 2 * npairs <= SPLIT_MAX_ROWS && p.nb > 0 && (!p.norm_w || p.K / 4 <= SPLIT_NORM_MAX_K4)) {
+        const size_t slds = (size_t)split_lds_floats(p.K) * 4;
+        if (slds + 1024 <= max_lds_per_block()) {
             const int64_t grid = (npairs + SPLIT_PAIRS - 1) / SPLIT_PAIRS;
             const int xs = split_xrow(p.nb) + 4;
             void (*fn)(GemvParams, int64_t, int);
-            const bool n = p.norm_w != nullptr;
-            if (tile) {
-                if (p.mode == MODE_QKV) fn = n ? gemv_q4_split_kernel<MODE_QKV, true, true> : gemv_q4_split_kernel<MODE_QKV, false, true>;
-                else if (p.mode == MODE_RESIDUAL) fn = n ? gemv_q4_split_kernel<MODE_RESIDUAL, true, true> : gemv_q4_split_kernel<MODE_RESIDUAL, false, true>;
-                else fn = n ? gemv_q4_split_kernel<MODE_STORE, true, true> : gemv_q4_split_kernel<MODE_STORE, false, true>;
-            } else {
-                if (p.mode == MODE_QKV) fn = n ? gemv_q4_split_kernel<MODE_QKV, true, false> : gemv_q4_split_kernel<MODE_QKV, false, false>;
-                else if (p.mode == MODE_RESIDUAL) fn = n ? gemv_q4_split_kernel<MODE_RESIDUAL, true, false> : gemv_q4_split_kernel<MODE_RESIDUAL, false, false>;
-                else fn = n ? gemv_q4_split_kernel<MODE_STORE, true, false> : gemv_q4_split_kernel<MODE_STORE, false, false>;
-            }
-            hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(THREADS), tile ? tlds : slds, s, p, npairs, xs);
+            if (p.mode == MODE_QKV) fn = p.norm_w ? gemv_q4_split_kernel<MODE_QKV, true> : gemv_q4_split_kernel<MODE_QKV, false>;
+            else if (p.mode == MODE_RESIDUAL) fn = p.norm_w ? gemv_q4_split_kernel<MODE_RESIDUAL, true> : gemv_q4_split_kernel<MODE_RESIDUAL, false>;
+            else fn = p.norm_w ? gemv_q4_split_kernel<MODE_STORE, true> : gemv_q4_split_kernel<MODE_STORE, false>;
+            hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(THREADS), slds, s, p, npairs, xs);
             GAJE_HIP_CHECK(hipGetLastError());
             return GAJE_OK;
         }
