@@ -12,6 +12,11 @@
 // expf on all 2^32 single-precision inputs (tests/test_expf_ref.py sweeps
 // them on the CPU, tests/test_gpu_ops.py checks the device build).
 //
+// Attribution: the algorithm, its 2^(i/32) table and its polynomial
+// coefficients are those of Arm's optimized-routines expf (Copyright (c) Arm
+// Limited; MIT OR Apache-2.0 WITH LLVM-exception), the implementation glibc
+// adopted for expf.
+//
 // Usable from host C++ (the CPU sweep) and from HIP device code.
 #pragma once
 
