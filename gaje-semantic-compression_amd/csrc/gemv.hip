@@ -696,6 +696,16 @@ __device__ __forceinline__ float finish_row(const GemvParams &p, const XView &xv
     return v;
 }
 
+// rms_norm's reduction of the eight sum-of-squares chains held by lanes 0..7:
+// ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7)), read out of the lanes (no LDS round
+// trip), the same value in every lane.
+__device__ __forceinline__ float rms_tot8(float a) {
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), i));
+    return ((v[0] + v[4]) + (v[1] + v[5])) + ((v[2] + v[6]) + (v[3] + v[7]));
+}
+
 // rms_norm's 1/rms over the chain-major LDS copy (norm.rs:52-88): lane l < 8
 // walks chain l (elements 8i + l), which is its own LDS row, reduces the eight
 // chains, and lane 0 stores 1/sqrt(ss/n + eps) in *inv_slot.  K % 32 == 0 here,
@@ -708,9 +718,7 @@ __device__ inline void rms_inv_chain_major(const XView &xv, int64_t K, float eps
     if (tid >= 8) return;
     const int n8 = (int)(K / 8);
     const float acc = chain_lds_sq(0.0f, xv.x + tid * xv.stride, (n8 + 63) & ~63);
-    const float u = acc + __shfl(acc, (tid + 4) & 7, 8);  // lane l<4: a_l + a_{l+4}
-    const float v = u + __shfl(u, (tid + 1) & 7, 8);      // lane 0: u0+u1, lane 2: u2+u3
-    const float tot = v + __shfl(v, (tid + 2) & 7, 8);    // lane 0: (u0+u1) + (u2+u3)
+    const float tot = rms_tot8(acc);  // ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7))
     if (tid == 0) {
         const float mean = tot / (float)K;
         *inv_slot = 1.0f / sqrtf(mean + eps);
@@ -1820,16 +1828,6 @@ __host__ __device__ constexpr int64_t chain_lds_bytes(int64_t K, bool norm) {
     const int64_t G = (K / 32 + 3) / 4, xf = 128 * G, nstage = (G + CH_SQ - 1) / CH_SQ;
     return (2 * CH_LANES * CH_DSTRIDE + xf + (norm ? K : 0) + 8 * (int64_t)chain_xstride(K)) * 4 +
            nstage * 3 * CH_UNIT;
-}
-
-// rms_norm's reduction of the eight sum-of-squares chains held by lanes 0..7:
-// ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7)), read out of the lanes (no LDS round
-// trip), the same value in every lane.
-__device__ __forceinline__ float rms_tot8(float a) {
-    float v[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), i));
-    return ((v[0] + v[4]) + (v[1] + v[5])) + ((v[2] + v[6]) + (v[3] + v[7]));
 }
 
 template <int MODE, bool NORM, int GX>
