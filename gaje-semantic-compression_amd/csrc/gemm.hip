@@ -247,7 +247,8 @@ __global__ __launch_bounds__(MT * 2, GA ? 2 : 1) void gemm_q4_mfma_kernel(GemmQ4
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = (f4){0.f, 0.f, 0.f, 0.f};
 
-    // two activation blocks and two weight groups in flight
+    // two activation blocks (GA: their fragments) and two weight groups (GA:
+    // one) in flight
     vu4 xa[2][4];
     vu4 wq[2][4], ws[2];
     auto load_x = [&](int b, vu4 (&r)[4]) {
@@ -271,7 +272,7 @@ __global__ __launch_bounds__(MT * 2, GA ? 2 : 1) void gemm_q4_mfma_kernel(GemmQ4
     // GA: fragment rows of this wave (clamped into the tile's rows, as 32-bit
     // half offsets from the planes)
     uint32_t fo[4];
-    h8 fa[1][2][4];  // [plane][i] of the next block
+    h8 fa[2][2][4];  // [block & 1][plane][i]: the next two blocks
     if constexpr (GA) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -292,6 +293,7 @@ __global__ __launch_bounds__(MT * 2, GA ? 2 : 1) void gemm_q4_mfma_kernel(GemmQ4
     load_w(g0, wq[0], ws[0]);
     if constexpr (GA) {
         load_frag(b0, fa[0][0], fa[0][1]);
+        load_frag(b0 + 1, fa[1][0], fa[1][1]);
     } else {
         load_x(b0, xa[0]);
         load_x(b0 + 1, xa[1]);
@@ -358,15 +360,15 @@ __global__ __launch_bounds__(MT * 2, GA ? 2 : 1) void gemm_q4_mfma_kernel(GemmQ4
                     const h8 bl = *(const h8 *)(Bb + 16 * j * GM_ROW + BPL);
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[0][0][i], bh, acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[xi][0][i], bh, acc[i][j], 0, 0, 0);
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[0][0][i], bl, acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[xi][0][i], bl, acc[i][j], 0, 0, 0);
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[0][1][i], bh, acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[xi][1][i], bh, acc[i][j], 0, 0, 0);
                 }
-                load_frag(b + 1, fa[0][0], fa[0][1]);  // lands while block b+1's weights are staged
+                load_frag(b + 2, fa[xi][0], fa[xi][1]);  // two blocks ahead
             } else {
                 const _Float16 *Ab = As + buf * 2 * APL + (wm * 64 + fr) * GM_ROW + fk;
                 h8 ahi[4], alo[4], bhi[4], blo[4];
@@ -511,6 +513,10 @@ GemmPlan plan_gemm_q4(int64_t M, int64_t N, int64_t K) {
 
 GemmPlan plan_gemm_q4_grouped(int64_t R, int64_t E, int64_t N, int64_t K) {
     GemmPlan pl{};
+    // 128-row tiles although the experts hold R/E rows on average (64 at the
+    // benchmark's 256 tokens x top-2 over 8 experts): each workgroup
+    // dequantises its 128 weight rows once, and 64-row tiles, which dequantise
+    // them once per 64 rows, measured slower (343 against 259 us per layer)
     pl.mt = 128;
     // tiles that hold rows: at most R/128 full ones plus one partial per group
     const int64_t tiles = ((R + 127) / 128 + E) * ((N + GM_NT - 1) / GM_NT);
