@@ -1036,6 +1036,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
                 const float o = swiglu1(y0, y1, etab);
                 if (isnan(o)) nan_flag(st, p.layer, p.st_b);
                 p.y[pr] = o;
+                if (p.y_cm) p.y_cm[(pr & 7) * p.cm_stride + (pr >> 3)] = o;
                 break;
             }
             case MODE_ARGMAX: {
@@ -1454,7 +1455,7 @@ __global__ __launch_bounds__(WAVES * WAVE) void gemv_q4_lds_kernel(GemvParams p,
     // the end store into a sink, so the count is fixed) and the copies of the
     // next min(left, STAGES - 1) tiles; the wait lets exactly those remain
     // (a NaN flag's atomic only makes it wait longer). ----
-    constexpr int NST = MODE == MODE_SWIGLU ? 1 : ROWS;
+    constexpr int NST = MODE == MODE_SWIGLU ? 2 : ROWS;  // SwiGLU: y and the chain-major copy (or the sink)
     float4 xr4[4 * G];  // chain l's activations, read once
     {
         const float *xg = xv.x + l * xv.stride;
@@ -1487,6 +1488,7 @@ __global__ __launch_bounds__(WAVES * WAVE) void gemv_q4_lds_kernel(GemvParams p,
                 const float o = swiglu1(y0, y1, etab);
                 if (ok && isnan(o)) nan_flag(st, p.layer, p.st_b);
                 *(ok ? p.y + row : kSinkOut + lane) = o;
+                *(ok && p.y_cm ? p.y_cm + (row & 7) * p.cm_stride + (row >> 3) : kSinkOut + lane) = o;
             }
         }
         if (t + STAGES * nw < ntiles) {
@@ -1884,10 +1886,12 @@ __global__ __launch_bounds__(THREADS) void gemv_q4_chain_kernel(GemvParams p, in
             lds_barrier();
         }
         // the activations landed before wave 0's first barrier: NaN inputs are
-        // flagged here, off the chains' path
+        // flagged here, off the chains' path (longer rows: from the chain-major
+        // copy, quad m = row m % 8, c = 4 (m / 8))
         int bad = 0;
         for (int64_t m = (int64_t)(wave - 1) * WAVE + lane; m < K4; m += 3 * WAVE) {
-            const float4 v = *(const float4 *)(xs + 4 * m);
+            const float4 v = GX > 0 ? *(const float4 *)(xs + 4 * m)
+                                    : *(const float4 *)(xcm + (m & 7) * xstride + 4 * (m >> 3));
             bad |= isnan(v.x) | isnan(v.y) | isnan(v.z) | isnan(v.w);
         }
         if (__any(bad) && p.st_in >= 0 && lane == 0) nan_flag(st, p.layer, p.st_in);
@@ -1900,9 +1904,16 @@ __global__ __launch_bounds__(THREADS) void gemv_q4_chain_kernel(GemvParams p, in
     const bool leader = lane < CH_LANES && q.pair_ok && (lane & 15) == 0;
     float b0 = 0.0f, b1 = 0.0f, old0 = 0.0f, old1 = 0.0f, cs = 0.0f, sn = 0.0f;
     int pos = 0;
-    for (int64_t m = K4 + lane; m < XF / 4; m += WAVE) *(float4 *)(xs + 4 * m) = make_float4(0.f, 0.f, 0.f, 0.f);
-    lds_copy_bytes(p.x, K * 4, lds_addr(xs), lane);
-    if constexpr (NORM) lds_copy_bytes(p.norm_w, K * 4, lds_addr(wn), lane);
+    // longer rows whose producer also wrote the chain-major copy (x_cm, the
+    // launcher checks its stride): that copy is this kernel's xcm as it stands
+    const bool have_cm = GX == 0 && !NORM && p.x_cm != nullptr;
+    if (have_cm) {
+        lds_copy_bytes(p.x_cm, (int64_t)8 * xstride * 4, lds_addr(xcm), lane);
+    } else {
+        for (int64_t m = K4 + lane; m < XF / 4; m += WAVE) *(float4 *)(xs + 4 * m) = make_float4(0.f, 0.f, 0.f, 0.f);
+        lds_copy_bytes(p.x, K * 4, lds_addr(xs), lane);
+        if constexpr (NORM) lds_copy_bytes(p.norm_w, K * 4, lds_addr(wn), lane);
+    }
     if (leader) {  // (after the copies: their addresses need no kernel argument)
         if (q.r0 < p.bias_len) b0 = p.bias[q.r0];
         if (q.r1 >= 0 && q.r1 < p.bias_len) b1 = p.bias[q.r1];
@@ -1989,7 +2000,7 @@ __global__ __launch_bounds__(THREADS) void gemv_q4_chain_kernel(GemvParams p, in
         // (zero from K / 8): 32 elements (8 quads) per lane and round, chain l
         // of elements 32q.. being (x[32q + l], x[32q + 8 + l], x[32q + 16 + l],
         // x[32q + 24 + l]) at c = 4q of row l
-        for (int64_t qd = lane; qd < XF / 32; qd += WAVE) {
+        for (int64_t qd = have_cm ? XF / 32 : lane; qd < XF / 32; qd += WAVE) {
             float4 f[8];
 #pragma unroll
             for (int k = 0; k < 8; ++k) f[k] = *(const float4 *)(xs + 32 * qd + 4 * k);
@@ -2160,6 +2171,7 @@ int q4_xstride(int64_t K) { return q4_xrow((int)(K / 32)) + 4; }
 
 }  // namespace
 
+int gemv_chain_stride(int64_t K) { return chain_xstride(K); }
 int64_t q4_0_packed_bytes(int64_t N, int64_t K) { return N * ((K / 32 + 3) / 4) * 80 + Q4_TAIL_PAD; }
 int64_t q8_0_packed_bytes(int64_t N, int64_t K) { return (N + 7) / 8 * ((K / 32 + 3) / 4) * Q8_TILE_GROUP + Q8_TAIL_PAD; }
 
@@ -2258,6 +2270,8 @@ int launch_gemv(const GemvParams &p, hipStream_t s) {
             break;
         case MODE_SWIGLU:
             if (p.ffn <= 0 || 2 * p.ffn > p.N) return set_error(GAJE_ERR_INVALID_ARG, "gemv: bad SwiGLU arguments");
+            if (p.y_cm && p.cm_stride < (p.ffn + 7) / 8)
+                return set_error(GAJE_ERR_INVALID_ARG, "gemv: chain-major output stride too short");
             npairs = p.ffn;
             break;
         case MODE_ARGMAX:
@@ -2281,7 +2295,9 @@ int launch_gemv(const GemvParams &p, hipStream_t s) {
             clds + 1024 <= max_lds_per_block()) {
             const int64_t grid = (npairs + CH_PAIRS - 1) / CH_PAIRS;
             void (*fn)(GemvParams, int64_t, int) = chain_kernel(p.mode, p.norm_w != nullptr, (int)G);
-            hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(THREADS), clds, s, p, npairs, chain_xstride(p.K));
+            GemvParams pc = p;  // x_cm only in the layout this kernel copies whole
+            if (pc.x_cm && (pc.cm_stride != chain_xstride(p.K) || ((uintptr_t)pc.x_cm & 15))) pc.x_cm = nullptr;
+            hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(THREADS), clds, s, pc, npairs, chain_xstride(p.K));
             GAJE_HIP_CHECK(hipGetLastError());
             return GAJE_OK;
         }

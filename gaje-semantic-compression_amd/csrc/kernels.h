@@ -104,6 +104,13 @@ struct GemvParams {
     int64_t kv_head_stride;            // kv_cap * head_dim
     int64_t kv_cap;                    // positions per cache row
     int64_t ffn;
+    // chain-major copies (element e at (e % 8) * cm_stride + e / 8, rows of
+    // cm_stride = gemv_chain_stride(K) floats, zero past K / 8): y_cm, when
+    // set, receives a SwiGLU output as well as y; x_cm, when set, holds x in
+    // that layout for the kernels that read it so (the others read x)
+    float *y_cm;
+    const float *x_cm;
+    int32_t cm_stride;
     // guards (stage < 0 disables a check)
     DevState *st;
     int32_t layer;
@@ -113,6 +120,8 @@ struct GemvParams {
 // Validates shapes against what the kernels assume and launches; returns a
 // GAJE_* status.
 int launch_gemv(const GemvParams &p, hipStream_t s);
+// Row stride (floats) of the chain-major activation layout for in_features K.
+int gemv_chain_stride(int64_t K);
 // Q4_0Block rows (file layout, K % 32 == 0) -> the GEMV's packed row layout.
 // A packed tensor is followed by Q4_TAIL_PAD bytes that the GEMV's prefetch
 // may read (and never uses); q4_0_packed_bytes includes them.

@@ -280,6 +280,10 @@ struct gaje_hip_model {
 
     // activations and scratch
     float *h = nullptr, *q = nullptr, *attn_out = nullptr, *act = nullptr, *logits = nullptr, *hnorm = nullptr;
+    // the SwiGLU output also in the chain-major layout (8 rows of act_cm_stride
+    // floats, zero past ffn / 8), which the down matvec copies as it stands
+    float *act_cm = nullptr;
+    int32_t act_cm_stride = 0;
     DevState *st = nullptr;
     uint32_t *out_tokens = nullptr;
     int64_t out_cap = 0;
@@ -626,11 +630,15 @@ int enqueue_token(gaje_hip_model *m, hipEvent_t ev_blocks_done) {
         p.mode = MODE_SWIGLU;
         p.ffn = m->ffn;
         p.y = m->act;
+        p.y_cm = m->act_cm;
+        p.cm_stride = m->act_cm_stride;
         p.st_a = ST_UP;
         p.st_b = ST_FFN_OUT;
         GAJE_TRY(launch_gemv(p, m->stream));
 
         p = gemv_base(m, Ly.down, m->act);
+        p.x_cm = m->act_cm;
+        p.cm_stride = m->act_cm_stride;
         p.layer = (int32_t)l;
         p.gnorm = m->use_genomic_norm;
         p.mode = MODE_RESIDUAL;
@@ -851,6 +859,11 @@ extern "C" int gaje_hip_open(const char *path, int device, gaje_hip_model **out)
     GAJE_TRY(m->alloc(&m->q, (size_t)qn));
     GAJE_TRY(m->alloc(&m->attn_out, (size_t)qn));
     GAJE_TRY(m->alloc(&m->act, (size_t)std::max<int64_t>(m->ffn, 1)));
+    if (m->ffn > 0) {
+        m->act_cm_stride = gemv_chain_stride(m->ffn);
+        GAJE_TRY(m->alloc(&m->act_cm, (size_t)8 * m->act_cm_stride));
+        GAJE_HIP_CHECK(hipMemset(m->act_cm, 0, (size_t)8 * m->act_cm_stride * sizeof(float)));
+    }
     GAJE_TRY(m->alloc(&m->logits, (size_t)m->vocab_out));
     GAJE_TRY(m->alloc(&m->st, 1));
     GAJE_HIP_CHECK(hipMemset(m->st, 0, sizeof(DevState)));
@@ -1851,9 +1864,13 @@ extern "C" int gaje_hip_time_stage(gaje_hip_model *m, int stage, int64_t layer, 
                     p.mode = MODE_SWIGLU;
                     p.ffn = m->ffn;
                     p.y = m->act;
+                    p.y_cm = m->act_cm;
+                    p.cm_stride = m->act_cm_stride;
                     algo = wbytes(Ly.gate_up) + (2 * m->n_embd + m->ffn) * 4;
                 } else {
                     p = gemv_base(m, Ly.down, m->act);
+                    p.x_cm = m->act_cm;
+                    p.cm_stride = m->act_cm_stride;
                     p.mode = MODE_RESIDUAL;
                     p.y = m->h;
                     algo = wbytes(Ly.down) + (m->ffn + 2 * m->n_embd) * 4;
