@@ -239,26 +239,30 @@ namespace {
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-// Workspace of gaje_hip_q4_0_gemm_mfma: weight row exponents, activation row
-// exponents, the two f16 activation planes, split-K partials.
+// Workspace of gaje_hip_q4_0_gemm_mfma: activation row exponents, the f16
+// activation plane (hi | lo per block, rows padded to gemm_bs_plane_rows),
+// the two block-sum planes, split-K partials.
 struct GemmWorkspace {
-    int *ew, *ex;
-    uint16_t *xh, *xl;
+    int *ex;
+    uint16_t *xh, *sh, *sl;
+    int64_t plane_rows, ldsum;
     float *part;
     size_t bytes;
 };
 
-GemmWorkspace gemm_workspace(char *base, int64_t m, int64_t n, int64_t k, const GemmPlan &pl) {
+GemmWorkspace gemm_workspace(char *base, int64_t m, int64_t k, const GemmBsPlan &pl) {
     GemmWorkspace w{};
     size_t off = 0;
-    w.ew = (int *)(base + off);
-    off = align256(off + (size_t)n * 4);
     w.ex = (int *)(base + off);
     off = align256(off + (size_t)m * 4);
+    w.plane_rows = gemm_bs_plane_rows(m);
     w.xh = (uint16_t *)(base + off);
-    off = align256(off + (size_t)m * k * 2);
-    w.xl = (uint16_t *)(base + off);
-    off = align256(off + (size_t)m * k * 2);
+    off = align256(off + (size_t)(w.plane_rows * 2 * k) * 2);
+    w.ldsum = gemm_bs_sum_cols(k);
+    w.sh = (uint16_t *)(base + off);
+    off = align256(off + (size_t)(m * w.ldsum) * 2);
+    w.sl = (uint16_t *)(base + off);
+    off = align256(off + (size_t)(m * w.ldsum) * 2);
     w.part = (float *)(base + off);
     off = align256(off + (size_t)pl.part_floats * 4);
     w.bytes = off;
@@ -270,7 +274,7 @@ GemmWorkspace gemm_workspace(char *base, int64_t m, int64_t n, int64_t k, const 
 extern "C" int64_t gaje_hip_q4_0_gemm_mfma_workspace(int64_t m, int64_t n, int64_t k) {
     if (m < 0 || n <= 0 || k <= 0 || k % 32 != 0) return -1;
     if (m == 0) return 0;
-    return (int64_t)gemm_workspace(nullptr, m, n, k, plan_gemm_q4(m, n, k)).bytes;
+    return (int64_t)gemm_workspace(nullptr, m, k, plan_gemm_q4_bs(m, n, k)).bytes;
 }
 
 extern "C" int gaje_hip_q4_0_gemm_mfma(const void *packed, const float *X, const float *bias, int64_t bias_len,
@@ -280,30 +284,34 @@ extern "C" int gaje_hip_q4_0_gemm_mfma(const void *packed, const float *X, const
     if (k % 32 || m < 0 || (m > 0 && (!X || !Y || !packed || !workspace)) || bias_len < 0 || (bias_len > 0 && !bias))
         return set_error(GAJE_ERR_INVALID_ARG, "bad gemm arguments");
     if (m == 0 || n == 0) return GAJE_OK;
-    const GemmPlan pl = plan_gemm_q4(m, n, k);
-    const GemmWorkspace w = gemm_workspace((char *)workspace, m, n, k, pl);
+    if (((uintptr_t)workspace & 15) != 0) return set_error(GAJE_ERR_INVALID_ARG, "gemm workspace must be 16-byte aligned");
+    const GemmBsPlan pl = plan_gemm_q4_bs(m, n, k);
+    const GemmWorkspace w = gemm_workspace((char *)workspace, m, k, pl);
     if ((int64_t)w.bytes > workspace_bytes)
         return set_error(GAJE_ERR_INVALID_ARG, "gemm workspace of %lld bytes is smaller than the %zu needed",
                          (long long)workspace_bytes, w.bytes);
     hipStream_t s = as_stream(stream);
-    GAJE_TRY(launch_q4_row_exponents((const uint8_t *)packed, n, k, w.ew, s));
     SplitParams sp{};
     sp.x = X;
     sp.ldx = k;
     sp.xh = w.xh;
-    sp.xl = w.xl;
-    sp.ldh = k;
+    sp.ldh = 2 * k;
     sp.ex = w.ex;
     sp.M = m;
     sp.K = k;
+    sp.sh = w.sh;
+    sp.sl = w.sl;
+    sp.ldsum = w.ldsum;
     GAJE_TRY(launch_split_rows(sp, s));
-    GemmQ4Params p{};
+    GemmBsParams p{};
     p.w = (const uint8_t *)packed;
-    p.ew = w.ew;
     p.xh = w.xh;
-    p.xl = w.xl;
+    p.plane_rows = w.plane_rows;
+    p.sh = w.sh;
+    p.sl = w.sl;
     p.ex = w.ex;
-    p.ldh = k;
+    p.ldh = 2 * k;
+    p.ldsum = w.ldsum;
     p.bias = bias;
     p.bias_len = bias_len;
     p.y = Y;
@@ -312,7 +320,7 @@ extern "C" int gaje_hip_q4_0_gemm_mfma(const void *packed, const float *X, const
     p.M = m;
     p.N = n;
     p.nb = (int32_t)(k / 32);
-    return launch_gemm_q4(p, pl, s);
+    return launch_gemm_q4_bs(p, pl, s);
 }
 
 namespace {

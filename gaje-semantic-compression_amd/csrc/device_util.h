@@ -34,6 +34,57 @@ __device__ __forceinline__ bool barrier_or(int pred, int *slots) {
     return r;
 }
 
+// LDS byte address of a pointer into the workgroup's shared memory.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)p;
+}
+
+// One wave instruction: each active lane copies the 16 bytes at g into LDS at
+// lds + 16 * lane (lds is wave-uniform).  M0 is set inside the statement; the
+// kernels that use it hold nothing else in M0 (checked in their assembly).
+// The default is a streaming (non-temporal) read; TEMPORAL keeps the line in
+// the caches for data that other workgroups read again.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+template <bool TEMPORAL = false>
+__device__ __forceinline__ void lds_dma16(const void *g, uint32_t lds) {
+    if constexpr (TEMPORAL)
+        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                     :
+                     : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds))
+                     : "memory", "m0");
+    else
+        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt"
+                     :
+                     : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds))
+                     : "memory", "m0");
+}
+// The same copy addressed as a wave-uniform base (SGPR pair) plus a 32-bit
+// per-lane byte offset: one VGPR per address instead of two.  base must be
+// wave-uniform; it is moved to SGPRs with readfirstlane (a uniform value the
+// compiler computed on the VALU is still in VGPRs).
+__device__ __forceinline__ void lds_dma16_so(const void *base, uint32_t voff, uint32_t lds) {
+    // (readfirstlane returns int: each half goes through uint32_t, or the low
+    // half would sign-extend into the high one)
+    const uint64_t b = (uint64_t)(uintptr_t)base;
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+    const uint64_t bs = ((uint64_t)hi << 32) | lo;
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :
+                 : "v"(voff), "s"(bs), "s"(__builtin_amdgcn_readfirstlane(lds))
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// s_waitcnt for at most n outstanding vector memory operations (gfx9 encoding:
+// vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt left at their maxima).
+template <int n>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(n >= 0 && n < 64, "vmcnt is six bits");
+    __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);

@@ -177,6 +177,36 @@ __global__ __launch_bounds__(SPLIT_THREADS) void split_rows_kernel(SplitParams p
     for (int w = 1; w < SPLIT_THREADS / 64; ++w) rmax = fmaxf(rmax, red[w]);
     const int e = split_exponent(rmax);
     if (tid == 0) p.ex[m] = e;
+    if (p.sh) {
+        // block-scaled layout: one plane, block b at halves 64 b.. holding its
+        // 32 hi halves then its 32 lo halves; position 8 kg + t of each holds
+        // element 32 b + 2 kg + 8 (t & 3) + (t >> 2)
+        for (int64_t u = tid; u < (K >> 3); u += SPLIT_THREADS) {
+            const int64_t e0 = 32 * (u >> 2) + 2 * (u & 3);
+            h8 hi, lo;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const float a = ldexpf(xs[e0 + 8 * (t & 3) + (t >> 2)], e);
+                hi[t] = (_Float16)a;
+                lo[t] = (_Float16)(a - (float)hi[t]);
+            }
+            _Float16 *row = (_Float16 *)p.xh + m * p.ldh + 64 * (u >> 2) + 8 * (u & 3);
+            *(h8 *)row = hi;
+            *(h8 *)(row + 32) = lo;
+        }
+        // block sums, 2^-5 sum x' (|x'| < 2^15, so below 2^15), zero past the last block
+        const int64_t nb = K >> 5;
+        for (int64_t b = tid; b < p.ldsum; b += SPLIT_THREADS) {
+            float sum = 0.0f;
+            if (b < nb)
+                for (int t = 0; t < 32; ++t) sum = sum + ldexpf(xs[32 * b + t], e);
+            const float v = ldexpf(sum, -5);
+            const _Float16 hi = (_Float16)v;
+            ((_Float16 *)p.sh)[m * p.ldsum + b] = hi;
+            ((_Float16 *)p.sl)[m * p.ldsum + b] = (_Float16)(v - (float)hi);
+        }
+        return;
+    }
     for (int64_t i = tid; i < K4; i += SPLIT_THREADS) {
         const float4 v = *(const float4 *)(xs + 4 * i);
         const float a[4] = {ldexpf(v.x, e), ldexpf(v.y, e), ldexpf(v.z, e), ldexpf(v.w, e)};
@@ -450,6 +480,373 @@ __global__ void gemm_reduce_kernel(GemmQ4Params p, int S) {
 template <int MT, bool GA>
 size_t gemm_lds() { return (size_t)((GA ? 0 : 4 * MT * GM_ROW) + 4 * GM_NT * GM_ROW) * sizeof(_Float16); }
 
+// ---------------------------------------------------------------------------
+// Block-scaled product (the dense products of prefill and
+// gaje_hip_q4_0_gemm_mfma).
+//
+// The Q4_0 dot product regrouped by block b (blocks.rs:18-30, d = fma(q, s, mn)):
+//   sum_k x_k (q_k s_b + mn_b) = sum_b s_b P_b + sum_b mn_b X_b,
+//   P_b = sum_{k in b} x_k q_k,   X_b = sum_{k in b} x_k.
+// The codes q (0..15) are exact f16 operands, so P_b takes two MFMA products
+// (x_hi q + x_lo q, fp32 accumulation) where an f16 pair for the dequantised
+// weight takes three; s_b scales each block's 16 x 16 partial in fp32 on the
+// VALU, beside the matrix core.  The min term is one more product over the
+// block index: the block sums X'' = 2^-5 X' (an f16 pair) times the f16 mins.
+// Row result: 2^-ex (32 sum_b mn_b X''_b + sum_b s_b P'_b), x' = 2^ex x.
+//
+// Operand layout.  Packed Q4_0 word 4 kg + hh of a group holds, in byte c,
+// element 8 c + 2 kg of blocks 2 hh (low nibble) and 2 hh + 1 (high nibble);
+// word 4 kg + 2 + hh holds element 8 c + 2 kg + 1.  The split pass writes
+// each activation block permuted to match: position 8 kg + t holds element
+// 2 kg + 8 (t & 3) + (t >> 2), so the 8 halves of MFMA lane group kg are the
+// 8 codes of that word pair.  A code byte becomes f16 1024 + q by v_perm
+// against 0x64 bytes, then q by a packed f16 subtraction; the high nibbles are
+// used in place (16 q, with the block's scale divided by 16).
+//
+// Tiling (gfx950, wave64).  A workgroup is W waves of 64 activation rows and
+// 9 tiles of 16 weight rows (144); every wave holds 4 x 9 accumulators of
+// v_mfma_f32_16x16x32_f16 (one Q4_0 block per step).
+// - Activations: each wave streams its own rows into a private LDS ring of
+//   three blocks with global_load_lds (two blocks ahead), XOR-swizzled by
+//   16-byte chunk so that fragment reads are conflict-free.
+// - Weights: the raw 80-byte groups of the tile are copied into LDS one group
+//   ahead (code quads already in fragment-lane order), and each block pair's
+//   fragments are expanded into LDS once, shared by the waves (two barriers
+//   per group).
+// - No other vector memory access is made in the main loop, so the explicit
+//   vmcnt waits are exact.
+// - The grid is ordered so that the workgroups of one activation tile and
+//   split share an XCD, and so its L2.
+// Split-K over groups fills the device when there are few output tiles; the
+// partials are summed in a fixed order by gemm_reduce_kernel.
+constexpr int BS_J = 9;                                     // 16-row weight tiles per workgroup
+constexpr int BS_NT = 16 * BS_J;                            // 144 weight rows
+constexpr int BS_ABLK = 8192;                               // one block of a wave's rows: 64 rows x 128 B (hi | lo)
+constexpr int BS_RING = 3;                                  // ring slots per wave
+constexpr int BS_RAW_DMA = (BS_NT * 5 + 63) / 64;           // 12 copy instructions per raw group (144 rows x 80 B)
+constexpr int BS_RAW = BS_RAW_DMA * 1024;                   // one raw group, rows 80 bytes apart, padded
+constexpr int BS_BF = BS_J * 2 * 1024;                      // one block pair's code fragments
+constexpr int BS_SC = BS_NT * 8;                            // one block pair's scales (float2 per weight row)
+
+template <int W>
+constexpr size_t bs_lds() { return (size_t)W * BS_RING * BS_ABLK + 2 * BS_RAW + 2 * BS_BF + 2 * BS_SC; }
+
+struct BsGrid {
+    int32_t ntiles, splits, kb_per, units, total;  // units: 16-row weight units ceil(N / 16)
+};
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+// f16 1024 + byte (bytes 2 s, 2 s + 1 of t), minus 1024: the two codes as f16.
+template <int S>
+__device__ __forceinline__ uint32_t code_pair(uint32_t t) {
+    constexpr uint32_t sel = S == 0 ? 0x04010400u : 0x04030402u;
+    const uint32_t v = __builtin_amdgcn_perm(0x64646464u, t, sel);
+    const h2 r = __builtin_bit_cast(h2, v) + (h2){(_Float16)-1024.0f, (_Float16)-1024.0f};
+    return __builtin_bit_cast(uint32_t, r);
+}
+
+template <int W>
+__global__ __launch_bounds__(64 * W, 1) void gemm_q4_bs_kernel(GemmBsParams p, BsGrid gd) {
+    constexpr int RAWW = BS_RAW_DMA / W;       // raw copy instructions per wave per group
+    constexpr int CVW = (BS_J + W - 1) / W;    // fragment tiles each wave expands per pair
+    static_assert(BS_RAW_DMA % W == 0, "raw copies split evenly over the waves");
+    static_assert(16 + RAWW < 64 && W * BS_RING * BS_ABLK + 2 * (BS_RAW + BS_BF + BS_SC) <= 163840, "limits");
+    extern __shared__ __align__(16) uint8_t bs_mem[];
+    // w through readfirstlane: the copies' bases must be provably wave-uniform (SGPRs)
+    const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int fr = lane & 15, kg = lane >> 4;
+
+    // consecutive workgroups alternate over the 8 XCDs; XCD x takes the x-th
+    // contiguous run of (row tile, split, weight tile) indices
+    const int Q = (int)(gridDim.x >> 3);
+    const int idx = (int)(blockIdx.x & 7) * Q + (int)(blockIdx.x >> 3);
+    if (idx >= gd.total) return;
+    const int t = idx % gd.ntiles, mz = idx / gd.ntiles;
+    const int z = mz % gd.splits, mt = mz / gd.splits;
+    const int ubase = gd.units / gd.ntiles, urem = gd.units % gd.ntiles;
+    const int nj = ubase + (t < urem ? 1 : 0);  // 16-row weight units of this tile (<= BS_J)
+    const int64_t n0 = 16 * (int64_t)(t * ubase + min(t, urem));
+    const int64_t m0 = (int64_t)mt * (64 * W) + 64 * w;  // this wave's first activation row
+    const int b0 = z * gd.kb_per, b1 = min(p.nb, b0 + gd.kb_per);
+    const int nblk = b1 - b0, ngr = (nblk + 3) >> 2;
+    const int G = (p.nb + 3) >> 2;
+    const int64_t wstride = (int64_t)G * 80;
+
+    uint8_t *ring = bs_mem + w * (BS_RING * BS_ABLK);
+    uint8_t *raw = bs_mem + W * BS_RING * BS_ABLK;  // [2][BS_RAW]
+    uint8_t *bfr = raw + 2 * BS_RAW;             // [2][BS_BF]
+    float *sc = (float *)(bfr + 2 * BS_BF);      // [2][BS_NT][2]
+
+    // byte offset of the weight row of tile column c (dummy columns past nj
+    // repeat the last real one; the launcher checks that it fits 32 bits)
+    auto wrow_off = [&](int c) -> uint32_t {
+        if (c >= 16 * nj) c = 16 * nj - 1;
+        int64_t n = n0 + c;
+        if (n >= p.N) n = p.N - 1;
+        return (uint32_t)(n * wstride);
+    };
+    auto wrow = [&](int c) -> const uint8_t * { return p.w + wrow_off(c); };
+
+    // activation copies: per block a wave copies its 64 rows x 128 bytes (the
+    // block's hi | lo halves, one cache line per row).  Instruction q takes rows
+    // 8q..8q+7: lane -> row R = 8q + (lane >> 3), LDS chunk lane & 7, holding
+    // global chunk (lane & 7) ^ ((R >> 1) & 7), so that the fragment reads of
+    // 16 consecutive rows fall in distinct banks.  (R >> 1) & 7 is
+    // (lane >> 4) ^ 4 (q & 1): one lane offset for even q, one for odd.  The
+    // plane holds plane_rows >= the tile's rows, so no row is clamped, and its
+    // byte offsets fit 32 bits (both checked by the launcher).
+    const uint32_t arow = (uint32_t)((lane >> 3) * 2 * p.ldh);
+    const uint32_t aoffs[2] = {arow + 16 * ((lane & 7) ^ (lane >> 4)), arow + 16 * ((lane & 7) ^ (lane >> 4) ^ 4)};
+    auto dma_a = [&](int kk, int slot) {
+        const int64_t b = b0 + min(kk, nblk - 1);
+        const uint32_t dst = lds_addr(ring + slot * BS_ABLK);
+        const uint8_t *base = (const uint8_t *)p.xh + m0 * 2 * p.ldh + 128 * b;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) lds_dma16_so(base + q * 16 * p.ldh, aoffs[q & 1], dst + q * 1024);
+    };
+
+    // raw group copies: the tile's 144 weight rows x the 80 bytes of group g,
+    // rows 80 bytes apart (chunk c = 5 row + part); instruction ii of the 12
+    // takes chunks 64 ii + lane (past the 720 real ones: the last again, into
+    // the padding).  Every lane copies, so the main loop has no branch: the
+    // compiler would otherwise sink the fmas of a block below its later MFMAs.
+    uint32_t rsrc[RAWW];
+#pragma unroll
+    for (int r = 0; r < RAWW; ++r) {
+        const int c = min(64 * (w + W * r) + lane, 5 * BS_NT - 1);
+        rsrc[r] = wrow_off(c / 5) + 16 * (c % 5);
+    }
+    auto dma_raw = [&](int h, int buf) {
+        const uint8_t *gbase = p.w + ((int64_t)(b0 >> 2) + min(h, ngr - 1)) * 80;
+        const uint32_t base = lds_addr(raw + buf * BS_RAW);
+#pragma unroll
+        for (int r = 0; r < RAWW; ++r) lds_dma16_so(gbase, rsrc[r], base + (w + W * r) * 1024);
+    };
+
+    // expand block pair hh of the raw group in buffer rb into fragment buffer
+    // pb; wave w takes tiles w, w + W, ..  (past nj: tile nj - 1 again, the
+    // same bytes another wave writes, so that no wave branches)
+    auto expand = [&](int rb, int hh, int pb) {
+        const uint8_t *rg = raw + rb * BS_RAW;
+        uint8_t *bd = bfr + pb * BS_BF;
+#pragma unroll
+        for (int r = 0; r < CVW; ++r) {
+            const int j = min(w + W * r, nj - 1);
+            const uint8_t *rrow = rg + (16 * j + fr) * 80;
+            const vu4 q = *(const vu4 *)(rrow + 16 * kg);
+            const uint32_t wa = hh ? q[1] : q[0], wb = hh ? q[3] : q[2];
+            const uint32_t la = wa & 0x0F0F0F0Fu, lb = wb & 0x0F0F0F0Fu;
+            const uint32_t ua = wa & 0xF0F0F0F0u, ub = wb & 0xF0F0F0F0u;
+            const vu4 f0 = {code_pair<0>(la), code_pair<1>(la), code_pair<0>(lb), code_pair<1>(lb)};
+            const vu4 f1 = {code_pair<0>(ua), code_pair<1>(ua), code_pair<0>(ub), code_pair<1>(ub)};
+            *(vu4 *)(bd + (2 * j) * 1024 + lane * 16) = f0;
+            *(vu4 *)(bd + (2 * j + 1) * 1024 + lane * 16) = f1;
+            // the four lanes of a weight row write its scales alike
+            const vu4 sw = *(const vu4 *)(rrow + 64);
+            const float s0 = half_lo(hh ? sw[2] : sw[0]), s1 = half_lo(hh ? sw[3] : sw[1]) * 0.0625f;
+            *(float2 *)(sc + pb * 2 * BS_NT + 2 * (16 * j + fr)) = make_float2(s0, s1);
+        }
+    };
+
+    f4 acc[4][BS_J];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < BS_J; ++j) acc[i][j] = (f4){0.f, 0.f, 0.f, 0.f};
+
+    // One block: activation fragments of ring slot `slot`, code fragments and
+    // scales of pair buffer pb, block bb of the pair.  Software-pipelined by
+    // weight tile: the fragment of tile j + 1 is read while tile j computes,
+    // and the MFMAs of tile j issue one by one between the fmas of tile j - 1
+    // (sched_group_barrier); a scheduling barrier per tile keeps the compiler
+    // from hoisting every product (and its registers) ahead of the fmas.
+    // fragment (i, plane P) of lane (fr, kg): row 16 i + fr, chunk (4 P + kg) ^ ((fr >> 1) & 7)
+    const uint32_t aoff0 = fr * 128 + 16 * (kg ^ ((fr >> 1) & 7)), aoff1 = aoff0 ^ 64;
+    auto compute = [&](int slot, int pb, int bb) {
+        const uint8_t *ab = ring + slot * BS_ABLK;
+        h8 a[4][2];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            a[i][0] = *(const h8 *)(ab + i * 2048 + aoff0);
+            a[i][1] = *(const h8 *)(ab + i * 2048 + aoff1);
+        }
+        const uint8_t *bq = bfr + pb * BS_BF + bb * 1024 + lane * 16;
+        // (volatile: the compiler would otherwise move each scale read to just
+        // before its first use, exposing its latency on every tile)
+        typedef const __attribute__((address_space(3))) volatile float lds_vf;
+        lds_vf *sp = (lds_vf *)(sc + pb * 2 * BS_NT + 2 * fr + bb);
+        f4 pr[2][4];
+        // scales of tiles j - 1 (fmas this step), j and j + 1 (read this step)
+        float s_prev = 0.0f, s_cur = sp[0];
+        h8 bcur = *(const h8 *)bq;
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j <= BS_J; ++j) {
+            h8 bnext = bcur;
+            float s_next = 0.0f;
+            if (j + 1 < BS_J) {
+                bnext = *(const h8 *)(bq + (j + 1) * 2048);
+                s_next = sp[32 * (j + 1)];
+            }
+            if (j < BS_J) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    pr[j & 1][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i][0], bcur, (f4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    pr[j & 1][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i][1], bcur, pr[j & 1][i], 0, 0, 0);
+            }
+            if (j > 0) {
+                const int jp = j - 1;
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[i][jp][r] = fmaf(s_prev, pr[jp & 1][i][r], acc[i][jp][r]);
+            }
+            if (j > 0 && j < BS_J) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // the next fragment and scale
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // two fmas
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            bcur = bnext;
+            s_prev = s_cur;
+            s_cur = s_next;
+        }
+    };
+
+    // prologue: raw groups 0 and 1, activation blocks 0 and 1 in flight
+    dma_raw(0, 0);
+    dma_raw(1, 1);
+    dma_a(0, 0);
+    dma_a(1, 1);
+
+    // the min term over this split's blocks: MFMAs over the block index, the
+    // block-sum planes against the f16 mins (blocks outside [b0, b1) masked),
+    // one tile at a time into a temporary, so that the accumulators are only
+    // ever VALU operands
+    {
+        const _Float16 *sh = (const _Float16 *)p.sh, *sl = (const _Float16 *)p.sl;
+        int64_t srow[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            int64_t r = m0 + 16 * i + fr;
+            if (r >= p.M) r = p.M - 1;
+            srow[i] = r * p.ldsum;
+        }
+        const uint8_t *jrow[BS_J];
+#pragma unroll
+        for (int j = 0; j < BS_J; ++j) jrow[j] = wrow(16 * j + fr) + 64;
+        for (int c = b0 >> 5; c <= (b1 - 1) >> 5; ++c) {
+            const int bl = 32 * c + 8 * kg;  // this lane's first block
+            h8 xs[4][2];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                xs[i][0] = *(const h8 *)(sh + srow[i] + bl);
+                xs[i][1] = *(const h8 *)(sl + srow[i] + bl);
+            }
+            const int64_t ga = (int64_t)min(bl >> 2, G - 1) * 80, gb = (int64_t)min((bl >> 2) + 1, G - 1) * 80;
+            uint32_t keep[2] = {0u, 0u};  // bit u: block bl + 4 h + u lies in [b0, b1)
+#pragma unroll
+            for (int u = 0; u < 8; ++u) keep[u >> 2] |= (bl + u >= b0 && bl + u < b1) ? 1u << (u & 3) : 0u;
+#pragma unroll
+            for (int j = 0; j < BS_J; ++j) {
+                vu4 sa = *(const vu4 *)(jrow[j] + ga);
+                vu4 sb = *(const vu4 *)(jrow[j] + gb);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    sa[u] = (keep[0] >> u) & 1u ? sa[u] : 0u;
+                    sb[u] = (keep[1] >> u) & 1u ? sb[u] : 0u;
+                }
+                const vu4 mn = {__builtin_amdgcn_perm(sa[1], sa[0], 0x07060302u), __builtin_amdgcn_perm(sa[3], sa[2], 0x07060302u),
+                                __builtin_amdgcn_perm(sb[1], sb[0], 0x07060302u), __builtin_amdgcn_perm(sb[3], sb[2], 0x07060302u)};
+                const h8 mh = __builtin_bit_cast(h8, mn);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    f4 tm = __builtin_amdgcn_mfma_f32_16x16x32_f16(xs[i][0], mh, (f4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    tm = __builtin_amdgcn_mfma_f32_16x16x32_f16(xs[i][1], mh, tm, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[i][j][r] = fmaf(32.0f, tm[r], acc[i][j][r]);
+                }
+            }
+        }
+    }
+
+    wait_vmcnt<0>();
+    lds_barrier();       // raw group 0 of every wave
+    expand(0, 0, 0);     // pair 0
+    lds_barrier();
+
+    // Per group h (blocks 4h..4h+3 of the split, pairs 2h and 2h+1).  Issue
+    // order of the copies: A(4h+2), A(4h+3), raw(h+2), A(4h+4), A(4h+5), so
+    // A(k) has 16 copy instructions issued after it, or 16 + RAWW when raw
+    // copies fall between, and raw(h+1) has 32 by the middle of group h.
+    int slot = 0;
+    auto next = [](int s) { return s == BS_RING - 1 ? 0 : s + 1; };
+    for (int h = 0; h < ngr; ++h) {
+        const int k = 4 * h;
+        dma_a(k + 2, next(next(slot)));
+        wait_vmcnt<16>();
+        compute(slot, 0, 0);
+        slot = next(slot);
+        dma_a(k + 3, next(next(slot)));
+        wait_vmcnt<16>();
+        compute(slot, 0, 1);
+        slot = next(slot);
+        expand(h & 1, 1, 1);      // pair 2h + 1
+        wait_vmcnt<32>();         // this wave's copies of raw group h + 1
+        lds_barrier();
+        dma_raw(h + 2, h & 1);    // buffer h & 1 is free: both its pairs are expanded
+        dma_a(k + 4, next(next(slot)));
+        wait_vmcnt<16 + RAWW>();
+        compute(slot, 1, 0);
+        slot = next(slot);
+        dma_a(k + 5, next(next(slot)));
+        wait_vmcnt<16 + RAWW>();
+        compute(slot, 1, 1);
+        slot = next(slot);
+        expand((h + 1) & 1, 0, 0);  // pair 2h + 2
+        lds_barrier();
+    }
+    wait_vmcnt<0>();  // no copy into LDS outlives the workgroup
+
+    // epilogue: lane holds rows 4 (lane >> 4) + r of column lane & 15 of each tile
+    int bad_a = 0, bad_b = 0;
+#pragma unroll
+    for (int j = 0; j < BS_J; ++j) {
+        const int64_t n = n0 + 16 * j + fr;
+        if (j >= nj || n >= p.N) continue;
+        const float bias = (!p.part && n < p.bias_len) ? p.bias[n] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t m = m0 + 16 * i + 4 * kg + r;
+                if (m >= p.M) continue;
+                float v = ldexpf(acc[i][j][r], -p.ex[m]);
+                if (p.part) {
+                    p.part[((int64_t)z * p.M + m) * p.N + n] = v;
+                } else {
+                    v = flush_small(v);
+                    if (n < p.bias_len) v = v + bias;
+                    bad_a |= isnan(v);
+                    if (p.resid) v = p.resid[m * p.ldr + n] + v;
+                    bad_b |= isnan(v);
+                    p.y[m * p.ldy + n] = v;
+                }
+            }
+        }
+    }
+    if (p.st) {
+        if (__any(bad_a) && lane == 0) nan_flag(p.st, p.layer, p.st_a);
+        if (__any(bad_b) && lane == 0) nan_flag(p.st, p.layer, p.st_b);
+    }
+}
+
 }  // namespace
 
 int launch_q4_row_exponents(const uint8_t *packed, int64_t N, int64_t K, int *ew, hipStream_t s) {
@@ -476,8 +873,11 @@ int launch_q4_row_exponents_batch(const uint8_t *const *packed, int n, int64_t N
 }
 
 int launch_split_rows(const SplitParams &p, hipStream_t s) {
-    if (p.M < 0 || p.K <= 0 || p.K % 32 || (p.M > 0 && (!p.x || !p.xh || !p.xl || !p.ex)) || p.ldx < p.K || p.ldh < p.K)
+    if (p.M < 0 || p.K <= 0 || p.K % 32 || (p.M > 0 && (!p.x || !p.xh || (!p.xl && !p.sh) || !p.ex)) || p.ldx < p.K ||
+        p.ldh < (p.sh ? 2 : 1) * p.K)
         return set_error(GAJE_ERR_INVALID_ARG, "split rows: bad arguments");
+    if (p.sh && (!p.sl || p.ldsum < gemm_bs_sum_cols(p.K) || p.ldh % 8))
+        return set_error(GAJE_ERR_INVALID_ARG, "split rows: bad block-sum planes");
     if (p.M == 0) return GAJE_OK;
     const size_t lds = (size_t)p.K * 4;
     if (lds + 1024 > max_lds_per_block())
@@ -531,6 +931,96 @@ GemmPlan plan_gemm_q4_grouped(int64_t R, int64_t E, int64_t N, int64_t K) {
     pl.splits = (int)((nb + kb - 1) / kb);
     pl.part_floats = pl.splits > 1 ? pl.splits * R * N : 0;
     return pl;
+}
+
+int64_t gemm_bs_sum_cols(int64_t K) { return (K / 32 + 31) / 32 * 32; }
+int64_t gemm_bs_plane_rows(int64_t M) { return (M + 255) / 256 * 256; }
+
+GemmBsPlan plan_gemm_q4_bs(int64_t M, int64_t N, int64_t K) {
+    GemmBsPlan pl{};
+    pl.waves = M <= 64 ? 1 : (M <= 128 ? 2 : 4);
+    const int64_t mt = 64 * pl.waves;
+    pl.mtiles = (int)((M + mt - 1) / mt);
+    const int64_t units = (N + 15) / 16;
+    pl.ntiles = (int)((units + BS_J - 1) / BS_J);
+    const int64_t tiles = (int64_t)pl.mtiles * pl.ntiles;
+    const int64_t nb = K / 32;
+    const int64_t cu = device_cu_count();  // one workgroup per compute unit (LDS)
+    const int64_t S = tiles < cu ? cu / tiles : 1;
+    int64_t kb = (nb + S - 1) / S;
+    kb = (kb + 3) / 4 * 4;  // splits start on group boundaries
+    if (kb < 4) kb = 4;
+    pl.kb_per = (int)kb;
+    pl.splits = (int)((nb + kb - 1) / kb);
+    pl.part_floats = pl.splits > 1 ? (int64_t)pl.splits * M * N : 0;
+    return pl;
+}
+
+int launch_gemm_q4_bs(const GemmBsParams &p, const GemmBsPlan &pl, hipStream_t s) {
+    if (p.M < 0 || p.N <= 0 || p.nb <= 0 || !p.w ||
+        (p.M > 0 && (!p.xh || !p.sh || !p.sl || !p.ex || !p.y || p.ldh < 64 * (int64_t)p.nb ||
+                     p.ldsum < gemm_bs_sum_cols(32 * (int64_t)p.nb))))
+        return set_error(GAJE_ERR_INVALID_ARG, "q4 block-scaled gemm: bad arguments");
+    if ((((uintptr_t)p.xh | (uintptr_t)p.sh | (uintptr_t)p.sl) & 15) || p.ldh % 8 || p.ldsum % 8)
+        return set_error(GAJE_ERR_INVALID_ARG, "q4 block-scaled gemm: planes must be 16-byte aligned");
+    if (p.M == 0) return GAJE_OK;
+    const int64_t mt = 64 * (int64_t)pl.waves;
+    if (p.plane_rows < (int64_t)pl.mtiles * mt)
+        return set_error(GAJE_ERR_INVALID_ARG, "q4 block-scaled gemm: the activation plane holds %lld rows, the tiles read %lld",
+                         (long long)p.plane_rows, (long long)pl.mtiles * mt);
+    if (2 * p.plane_rows * p.ldh >= ((int64_t)1 << 32) || p.N * (int64_t)((p.nb + 3) / 4) * 80 >= ((int64_t)1 << 32))
+        return set_error(GAJE_ERR_UNSUPPORTED, "q4 block-scaled gemm: operands beyond 4 GiB");
+    if ((pl.waves != 1 && pl.waves != 2 && pl.waves != 4) || pl.mtiles != (p.M + mt - 1) / mt || pl.ntiles <= 0 ||
+        pl.ntiles * (int64_t)BS_J < (p.N + 15) / 16 || pl.kb_per % 4 || pl.kb_per <= 0 ||
+        (int64_t)pl.splits * pl.kb_per < p.nb || (int64_t)(pl.splits - 1) * pl.kb_per >= p.nb ||
+        (pl.splits > 1 && !p.part))
+        return set_error(GAJE_ERR_INVALID_ARG, "q4 block-scaled gemm: bad plan");
+    GemmBsParams q = p;
+    if (pl.splits == 1) q.part = nullptr;
+    BsGrid gd{};
+    gd.ntiles = pl.ntiles;
+    gd.splits = pl.splits;
+    gd.kb_per = pl.kb_per;
+    gd.units = (int32_t)((p.N + 15) / 16);
+    const int64_t total = (int64_t)pl.mtiles * pl.splits * pl.ntiles;
+    if (total > (1 << 30)) return set_error(GAJE_ERR_UNSUPPORTED, "q4 block-scaled gemm: too many tiles");
+    gd.total = (int32_t)total;
+    const dim3 grid((unsigned)((total + 7) / 8 * 8));
+    switch (pl.waves) {
+    case 1:
+        hipLaunchKernelGGL(gemm_q4_bs_kernel<1>, grid, dim3(64), bs_lds<1>(), s, q, gd);
+        break;
+    case 2:
+        hipLaunchKernelGGL(gemm_q4_bs_kernel<2>, grid, dim3(128), bs_lds<2>(), s, q, gd);
+        break;
+    default:
+        if (bs_lds<4>() > max_lds_per_block()) return set_error(GAJE_ERR_UNSUPPORTED, "q4 block-scaled gemm: LDS");
+        hipLaunchKernelGGL(gemm_q4_bs_kernel<4>, grid, dim3(256), bs_lds<4>(), s, q, gd);
+        break;
+    }
+    GAJE_HIP_CHECK(hipGetLastError());
+    if (pl.splits > 1) {
+        GemmQ4Params r{};
+        r.bias = p.bias;
+        r.bias_len = p.bias_len;
+        r.resid = p.resid;
+        r.ldr = p.ldr;
+        r.y = p.y;
+        r.ldy = p.ldy;
+        r.part = p.part;
+        r.M = p.M;
+        r.N = p.N;
+        r.st = p.st;
+        r.layer = p.layer;
+        r.st_a = p.st_a;
+        r.st_b = p.st_b;
+        const int64_t elems = p.M * p.N;
+        int64_t g = (elems + 255) / 256;
+        if (g > 4096) g = 4096;
+        hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)g), dim3(256), 0, s, r, pl.splits);
+        GAJE_HIP_CHECK(hipGetLastError());
+    }
+    return GAJE_OK;
 }
 
 int launch_gemm_q4(const GemmQ4Params &p0, const GemmPlan &pl, hipStream_t s) {

@@ -1238,37 +1238,11 @@ __global__ __launch_bounds__(THREADS) void gemv_q8_stream_kernel(GemvParams p, i
 // the stages it filled itself, so no barrier orders them; the shared prologue
 // data is copied by wave 0 before its tiles and published with a barrier.
 
-// LDS byte address of a pointer into the workgroup's shared memory.
-__device__ __forceinline__ uint32_t lds_addr(const void *p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)p;
-}
-
-// One wave instruction: each active lane copies the 16 bytes at g into LDS at
-// lds + 16 * lane (lds is wave-uniform).  M0 is set inside the statement; the
-// kernels that use it hold nothing else in M0 (checked in their assembly).
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void lds_dma16(const void *g, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt"
-                 :
-                 : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds))
-                 : "memory", "m0");
-}
-#pragma clang diagnostic pop
-
 // A 32-bit load through the scalar data cache (uniform address), waited for.
 __device__ __forceinline__ int32_t s_load_i32(const void *p) {
     int32_t v;
     asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p) : "memory");
     return v;
-}
-
-// s_waitcnt for at most n outstanding vector memory operations (gfx9 encoding:
-// vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt left at their maxima).
-template <int n>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(n >= 0 && n < 64, "vmcnt is six bits");
-    __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
 // wait_vmcnt<k * per> for a wave-uniform k in [0, KMAX].

@@ -207,6 +207,12 @@ struct SplitParams {
     int *ex;                 // [M] row exponents
     int64_t M, K;
     const int32_t *rows;     // plane row m takes input row rows[m] (a gather), or null
+    // With sh set, xh alone takes the block-scaled product's layout (per
+    // block its hi then its lo halves, each block permuted, see gemm.hip;
+    // ldh >= 2K, xl unused) and sh/sl [M][ldsum] receive the block sums
+    // 2^-5 * sum_{k in b} x'[k] as an f16 pair (zero past K/32).
+    uint16_t *sh, *sl;
+    int64_t ldsum;
 };
 int launch_split_rows(const SplitParams &p, hipStream_t s);
 // Per packed Q4_0 row: the exponent that scales its largest |d| into [2^14, 2^15).
@@ -255,6 +261,44 @@ struct GemmPlan {
     int64_t part_floats;     // partial buffer the splits need (0 if one split)
 };
 GemmPlan plan_gemm_q4(int64_t M, int64_t N, int64_t K);
+
+// Block-scaled Q4_0 product (the dense products of prefill and
+// gaje_hip_q4_0_gemm_mfma): Y = X W^T as sum_b scale_b P_b + sum_b min_b X_b
+// per block b, P_b on the MFMA units with the 4-bit codes as exact f16
+// operands.  Its activation planes come from launch_split_rows with sh set.
+struct GemmBsParams {
+    const uint8_t *w;        // packed rows (launch_pack_q4_0)
+    const uint16_t *xh;      // activation plane [plane_rows][ldh] (hi | lo per block, ldh >= 2K)
+    int64_t plane_rows;      // rows allocated: >= gemm_bs_plane_rows(M) (rows past M are read, not used)
+    const uint16_t *sh, *sl; // block-sum planes [M][ldsum]
+    const int *ex;           // [M] activation row exponents
+    int64_t ldh, ldsum;
+    const float *bias;
+    int64_t bias_len;
+    const float *resid;      // Y = resid + row result, or null (may alias y)
+    int64_t ldr;
+    float *y;
+    int64_t ldy;
+    float *part;             // split-K partials [splits][M][N] (plan.part_floats)
+    int64_t M, N;
+    int32_t nb;              // K / 32
+    DevState *st;            // NaN guards as in GemmQ4Params
+    int32_t layer;
+    int32_t st_a, st_b;
+};
+struct GemmBsPlan {
+    int waves;               // 64-row wave tiles per workgroup (1, 2 or 4)
+    int mtiles, ntiles;      // activation-row tiles, weight-row tiles (<= 144 rows)
+    int splits, kb_per;      // K splits of kb_per blocks (a multiple of 4)
+    int64_t part_floats;     // partial buffer the splits need (0 if one split)
+};
+GemmBsPlan plan_gemm_q4_bs(int64_t M, int64_t N, int64_t K);
+int launch_gemm_q4_bs(const GemmBsParams &p, const GemmBsPlan &plan, hipStream_t s);
+// Columns of the block-sum planes for a K: K/32 rounded up to a multiple of 32.
+int64_t gemm_bs_sum_cols(int64_t K);
+// Rows the activation plane must hold for M activation rows (a multiple of 256).
+int64_t gemm_bs_plane_rows(int64_t M);
+
 // Grouped plan: 128-row tiles, splits sized for R rows spread over E groups.
 GemmPlan plan_gemm_q4_grouped(int64_t R, int64_t E, int64_t N, int64_t K);
 int launch_gemm_q4(const GemmQ4Params &p, const GemmPlan &plan, hipStream_t s);

@@ -58,7 +58,6 @@ struct DevLinear {
     int64_t *a_ptr = nullptr;
     uint32_t *a_col = nullptr;
     uint16_t *a_val = nullptr;
-    int *ew = nullptr;  // FMT_Q4_0: per-row exponents of the MFMA matrix product
     int64_t bytes = 0;
 };
 
@@ -312,7 +311,8 @@ struct gaje_hip_model {
         int64_t rows = 0;        // chunk rows the buffers hold
         int64_t part_floats = 0; // split-K partials they hold
         float *H = nullptr, *QKV = nullptr, *Q = nullptr, *ATT = nullptr, *GU = nullptr, *part = nullptr, *aws = nullptr;
-        uint16_t *xh = nullptr, *xl = nullptr;
+        uint16_t *xh = nullptr;                 // activation plane [gemm_bs_plane_rows(rows)][2 kmax]
+        uint16_t *sh = nullptr, *sl = nullptr;  // block-sum planes [rows][gemm_bs_sum_cols(kmax)]
         int *ex = nullptr;
         uint32_t *ids = nullptr;
     } pf;
@@ -379,10 +379,6 @@ int upload_linear(gaje_hip_model *m, const HostLinear &L, DevLinear &D, bool til
         m->release(tmp);
         GAJE_TRY(rc);
         m->weight_bytes += packed;
-        if (D.rows_valid > 0) {
-            GAJE_TRY(m->alloc(&D.ew, (size_t)D.rows_valid));
-            GAJE_TRY(launch_q4_row_exponents(D.w, D.rows_valid, L.K, D.ew, m->stream));
-        }
     } else if (L.fmt == FMT_Q8_0) {
         // stage the file's Q8_0Block rows and pack them into 144-byte groups
         const size_t raw = (size_t)D.rows_valid * nb * 34;
@@ -1002,7 +998,7 @@ int prefill_mfma_supported(const gaje_hip_model *m) {
         return set_error(GAJE_ERR_UNSUPPORTED, "MFMA prefill: head_dim %lld (64 or 128 only)", (long long)m->hd);
     for (const Layer &Ly : m->layers)
         for (const DevLinear *D : {&Ly.qkv, &Ly.o, &Ly.gate_up, &Ly.down})
-            if (D->fmt != FMT_Q4_0 || D->a_ptr || D->rows_valid != D->N || !D->ew)
+            if (D->fmt != FMT_Q4_0 || D->a_ptr || D->rows_valid != D->N)
                 return set_error(GAJE_ERR_UNSUPPORTED,
                                  "MFMA prefill needs complete Q4_0 body tensors without anchors (use gaje_hip_prefill)");
     return GAJE_OK;
@@ -1017,13 +1013,13 @@ int prefill_reserve(gaje_hip_model *m, int64_t rows) {
     const Layer &L0 = m->layers[0];
     int64_t part = 0;
     for (const DevLinear *D : {&L0.qkv, &L0.o, &L0.gate_up, &L0.down})
-        part = std::max(part, plan_gemm_q4(rows, D->N, D->K).part_floats);
+        part = std::max(part, plan_gemm_q4_bs(rows, D->N, D->K).part_floats);
     if (rows <= f.rows && part <= f.part_floats) return GAJE_OK;
     rows = std::max(rows, f.rows);
     part = std::max(part, f.part_floats);
     GAJE_HIP_CHECK(hipStreamSynchronize(m->stream));
     for (void *p : {(void *)f.H, (void *)f.QKV, (void *)f.Q, (void *)f.ATT, (void *)f.GU, (void *)f.part, (void *)f.xh,
-                    (void *)f.xl, (void *)f.ex, (void *)f.ids, (void *)f.aws})
+                    (void *)f.sh, (void *)f.sl, (void *)f.ex, (void *)f.ids, (void *)f.aws})
         if (p) m->release(p);
     f = gaje_hip_model::Prefill();
     const int64_t kmax = prefill_kmax(m);
@@ -1032,8 +1028,9 @@ int prefill_reserve(gaje_hip_model *m, int64_t rows) {
     GAJE_TRY(m->alloc(&f.Q, (size_t)(rows * m->q_rows)));
     GAJE_TRY(m->alloc(&f.ATT, (size_t)(rows * m->q_rows)));
     GAJE_TRY(m->alloc(&f.GU, (size_t)(rows * L0.gate_up.N)));
-    GAJE_TRY(m->alloc(&f.xh, (size_t)(rows * kmax)));
-    GAJE_TRY(m->alloc(&f.xl, (size_t)(rows * kmax)));
+    GAJE_TRY(m->alloc(&f.xh, (size_t)(gemm_bs_plane_rows(rows) * 2 * kmax)));
+    GAJE_TRY(m->alloc(&f.sh, (size_t)(rows * gemm_bs_sum_cols(kmax))));
+    GAJE_TRY(m->alloc(&f.sl, (size_t)(rows * gemm_bs_sum_cols(kmax))));
     GAJE_TRY(m->alloc(&f.ex, (size_t)rows));
     GAJE_TRY(m->alloc(&f.ids, (size_t)rows));
     GAJE_TRY(m->alloc(&f.part, (size_t)part));
@@ -1050,11 +1047,13 @@ SplitParams prefill_split(const gaje_hip_model *m, const float *x, int64_t ldx, 
     sp.eps = m->eps;
     sp.h_scale = 1.0f;
     sp.xh = m->pf.xh;
-    sp.xl = m->pf.xl;
-    sp.ldh = K;
+    sp.ldh = 2 * K;
     sp.ex = m->pf.ex;
     sp.M = P;
     sp.K = K;
+    sp.sh = m->pf.sh;
+    sp.sl = m->pf.sl;
+    sp.ldsum = gemm_bs_sum_cols(K);
     sp.st = m->st;
     sp.st_a = sp.st_b = ST_NONE;
     return sp;
@@ -1064,15 +1063,17 @@ SplitParams prefill_split(const gaje_hip_model *m, const float *x, int64_t ldx, 
 int prefill_gemm(gaje_hip_model *m, const DevLinear &D, int64_t P, float *y, const float *resid, int32_t layer,
                  int32_t st_a, int32_t st_b) {
     const auto &f = m->pf;
-    const GemmPlan pl = plan_gemm_q4(P, D.N, D.K);
+    const GemmBsPlan pl = plan_gemm_q4_bs(P, D.N, D.K);
     if (pl.part_floats > f.part_floats) return set_error(GAJE_ERR_INVALID_ARG, "prefill: split-K buffer too small");
-    GemmQ4Params p{};
+    GemmBsParams p{};
     p.w = D.w;
-    p.ew = D.ew;
     p.xh = f.xh;
-    p.xl = f.xl;
+    p.plane_rows = gemm_bs_plane_rows(f.rows);
+    p.sh = f.sh;
+    p.sl = f.sl;
     p.ex = f.ex;
-    p.ldh = D.K;
+    p.ldh = 2 * D.K;
+    p.ldsum = gemm_bs_sum_cols(D.K);
     p.bias = D.bias;
     p.bias_len = D.bias_len;
     p.resid = resid;
@@ -1087,7 +1088,7 @@ int prefill_gemm(gaje_hip_model *m, const DevLinear &D, int64_t P, float *y, con
     p.layer = layer;
     p.st_a = st_a;
     p.st_b = st_b;
-    return launch_gemm_q4(p, pl, m->stream);
+    return launch_gemm_q4_bs(p, pl, m->stream);
 }
 
 // One block (RustGenomicBlock::forward_core, block/forward.rs:10-157) for the

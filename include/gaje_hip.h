@@ -102,12 +102,15 @@ int gaje_hip_q4_0_gemm(const void *packed, const float *X, const float *bias, in
 
 /* The same product on the MFMA units, for prompt prefill and other calls
  * with many activation rows (Y[m][n] = X[m][k] W^T, + bias).  Not bit-exact:
- * both operands are carried as f16 hi/lo pairs with fp32 accumulation, so each
- * output is the reference's dot product (genomic.rs:263-336, then the
- * |t| < 1e-6 flush and the bias add of linear/forward.rs:84-92,113-115) to
- * about fp32 accuracy in a different summation order.  `workspace` is device
- * memory of at least gaje_hip_q4_0_gemm_mfma_workspace(m, n, k) bytes
- * (-1 for an invalid shape); calls that share a workspace must not overlap. */
+ * the dot product is regrouped by Q4_0 block (scale times the block's
+ * code product, plus min times the block's activation sum), the activations
+ * carried as f16 hi/lo pairs and the 4-bit codes exactly, with fp32
+ * accumulation, so each output is the reference's dot product
+ * (genomic.rs:263-336, then the |t| < 1e-6 flush and the bias add of
+ * linear/forward.rs:84-92,113-115) to about fp32 accuracy in a different
+ * summation order.  `workspace` is 16-byte aligned device memory of at least
+ * gaje_hip_q4_0_gemm_mfma_workspace(m, n, k) bytes (-1 for an invalid shape);
+ * calls that share a workspace must not overlap. */
 int64_t gaje_hip_q4_0_gemm_mfma_workspace(int64_t m, int64_t n, int64_t k);
 int gaje_hip_q4_0_gemm_mfma(const void *packed, const float *X, const float *bias, int64_t bias_len,
                             float *Y, int64_t m, int64_t n, int64_t k, void *workspace,
