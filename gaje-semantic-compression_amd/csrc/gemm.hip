@@ -503,33 +503,45 @@ size_t gemm_lds() { return (size_t)((GA ? 0 : 4 * MT * GM_ROW) + 4 * GM_NT * GM_
 // against 0x64 bytes, then q by a packed f16 subtraction; the high nibbles are
 // used in place (16 q, with the block's scale divided by 16).
 //
-// Tiling (gfx950, wave64).  A workgroup is W waves of 64 activation rows and
-// 9 tiles of 16 weight rows (144); every wave holds 4 x 9 accumulators of
-// v_mfma_f32_16x16x32_f16 (one Q4_0 block per step).
-// - Activations: each wave streams its own rows into a private LDS ring of
-//   three blocks with global_load_lds (two blocks ahead), XOR-swizzled by
-//   16-byte chunk so that fragment reads are conflict-free.
-// - Weights: the raw 80-byte groups of the tile are copied into LDS one group
-//   ahead (code quads already in fragment-lane order), and each block pair's
-//   fragments are expanded into LDS once, shared by the waves (two barriers
-//   per group).
+// Tiling (gfx950, wave64).  A workgroup is W waves of 32 activation rows and
+// 9 tiles of 16 weight rows (144); every wave holds 2 x 9 accumulators of
+// v_mfma_f32_16x16x32_f16 (one Q4_0 block per step).  Eight waves (two per
+// SIMD) for a 256-row tile: one wave cannot keep the matrix core busy, or run
+// its VALU work beside its own MFMAs, but two waves of a SIMD interleave
+// (measured: 16x16x32 f16 issued from one wave per SIMD runs at half rate,
+// from two at the full rate with two fmas per MFMA at ~85%).
+// - Activations: the split pass stores each block's hi and lo halves together
+//   (128 bytes per row); each wave streams its own rows into a private LDS
+//   ring of three blocks with global_load_lds, two blocks ahead, XOR-swizzled
+//   by 16-byte chunk so that fragment reads are conflict-free.
+// - Weights: the raw 80-byte groups of the tile's rows are copied into LDS one
+//   group ahead; each block's code fragments and scales are expanded into LDS
+//   one block ahead by all waves together (one barrier per block).
 // - No other vector memory access is made in the main loop, so the explicit
 //   vmcnt waits are exact.
 // - The grid is ordered so that the workgroups of one activation tile and
 //   split share an XCD, and so its L2.
 // Split-K over groups fills the device when there are few output tiles; the
 // partials are summed in a fixed order by gemm_reduce_kernel.
-constexpr int BS_J = 9;                                     // 16-row weight tiles per workgroup
-constexpr int BS_NT = 16 * BS_J;                            // 144 weight rows
-constexpr int BS_ABLK = 8192;                               // one block of a wave's rows: 64 rows x 128 B (hi | lo)
-constexpr int BS_RING = 3;                                  // ring slots per wave
-constexpr int BS_RAW_DMA = (BS_NT * 5 + 63) / 64;           // 12 copy instructions per raw group (144 rows x 80 B)
-constexpr int BS_RAW = BS_RAW_DMA * 1024;                   // one raw group, rows 80 bytes apart, padded
-constexpr int BS_BF = BS_J * 2 * 1024;                      // one block pair's code fragments
-constexpr int BS_SC = BS_NT * 8;                            // one block pair's scales (float2 per weight row)
+constexpr int BS_J = 9;                         // 16-row weight tiles per workgroup
+constexpr int BS_NT = 16 * BS_J;                // 144 weight rows
+constexpr int BS_WR = 32;                       // activation rows per wave
+constexpr int BS_ABLK = BS_WR * 128;            // one block of a wave's rows (hi | lo)
+constexpr int BS_ADMA = BS_ABLK / 1024;         // its copy instructions
+constexpr int BS_RING = 3;                      // ring slots per wave
+constexpr int BS_RAWC = BS_NT * 5;              // 16-byte chunks of one raw group (144 rows x 80 B)
+constexpr int BS_BF = BS_J * 1024;              // one block's code fragments
+constexpr int BS_SC = BS_NT * 4;                // one block's scales
 
 template <int W>
-constexpr size_t bs_lds() { return (size_t)W * BS_RING * BS_ABLK + 2 * BS_RAW + 2 * BS_BF + 2 * BS_SC; }
+struct BsShape {
+    static constexpr int RAWW = (BS_RAWC + 64 * W - 1) / (64 * W);  // raw copy instructions per wave per group
+    static constexpr int RAW = RAWW * W * 1024;                     // one raw group buffer (padded)
+    static constexpr int CVW = (BS_J + W - 1) / W;                  // fragment tiles each wave expands per block
+    static constexpr size_t LDS = (size_t)W * BS_RING * BS_ABLK + 2 * RAW + 2 * BS_BF + 2 * BS_SC;
+};
+template <int W>
+constexpr size_t bs_lds() { return BsShape<W>::LDS; }
 
 struct BsGrid {
     int32_t ntiles, splits, kb_per, units, total;  // units: 16-row weight units ceil(N / 16)
@@ -548,10 +560,9 @@ __device__ __forceinline__ uint32_t code_pair(uint32_t t) {
 
 template <int W>
 __global__ __launch_bounds__(64 * W, 1) void gemm_q4_bs_kernel(GemmBsParams p, BsGrid gd) {
-    constexpr int RAWW = BS_RAW_DMA / W;       // raw copy instructions per wave per group
-    constexpr int CVW = (BS_J + W - 1) / W;    // fragment tiles each wave expands per pair
-    static_assert(BS_RAW_DMA % W == 0, "raw copies split evenly over the waves");
-    static_assert(16 + RAWW < 64 && W * BS_RING * BS_ABLK + 2 * (BS_RAW + BS_BF + BS_SC) <= 163840, "limits");
+    using S = BsShape<W>;
+    constexpr int RAWW = S::RAWW, CVW = S::CVW;
+    static_assert(2 * BS_ADMA + 2 * RAWW < 64 && S::LDS <= 163840, "limits");
     extern __shared__ __align__(16) uint8_t bs_mem[];
     // w through readfirstlane: the copies' bases must be provably wave-uniform (SGPRs)
     const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -567,16 +578,16 @@ __global__ __launch_bounds__(64 * W, 1) void gemm_q4_bs_kernel(GemmBsParams p, B
     const int ubase = gd.units / gd.ntiles, urem = gd.units % gd.ntiles;
     const int nj = ubase + (t < urem ? 1 : 0);  // 16-row weight units of this tile (<= BS_J)
     const int64_t n0 = 16 * (int64_t)(t * ubase + min(t, urem));
-    const int64_t m0 = (int64_t)mt * (64 * W) + 64 * w;  // this wave's first activation row
+    const int64_t m0 = (int64_t)mt * (BS_WR * W) + BS_WR * w;  // this wave's first activation row
     const int b0 = z * gd.kb_per, b1 = min(p.nb, b0 + gd.kb_per);
     const int nblk = b1 - b0, ngr = (nblk + 3) >> 2;
     const int G = (p.nb + 3) >> 2;
     const int64_t wstride = (int64_t)G * 80;
 
     uint8_t *ring = bs_mem + w * (BS_RING * BS_ABLK);
-    uint8_t *raw = bs_mem + W * BS_RING * BS_ABLK;  // [2][BS_RAW]
-    uint8_t *bfr = raw + 2 * BS_RAW;             // [2][BS_BF]
-    float *sc = (float *)(bfr + 2 * BS_BF);      // [2][BS_NT][2]
+    uint8_t *raw = bs_mem + W * BS_RING * BS_ABLK;  // [2][S::RAW]
+    uint8_t *bfr = raw + 2 * S::RAW;                // [2][BS_BF]
+    float *sc = (float *)(bfr + 2 * BS_BF);         // [2][BS_NT]
 
     // byte offset of the weight row of tile column c (dummy columns past nj
     // repeat the last real one; the launcher checks that it fits 32 bits)
@@ -588,7 +599,7 @@ __global__ __launch_bounds__(64 * W, 1) void gemm_q4_bs_kernel(GemmBsParams p, B
     };
     auto wrow = [&](int c) -> const uint8_t * { return p.w + wrow_off(c); };
 
-    // activation copies: per block a wave copies its 64 rows x 128 bytes (the
+    // activation copies: per block a wave copies its 32 rows x 128 bytes (the
     // block's hi | lo halves, one cache line per row).  Instruction q takes rows
     // 8q..8q+7: lane -> row R = 8q + (lane >> 3), LDS chunk lane & 7, holding
     // global chunk (lane & 7) ^ ((R >> 1) & 7), so that the fragment reads of
@@ -603,80 +614,78 @@ __global__ __launch_bounds__(64 * W, 1) void gemm_q4_bs_kernel(GemmBsParams p, B
         const uint32_t dst = lds_addr(ring + slot * BS_ABLK);
         const uint8_t *base = (const uint8_t *)p.xh + m0 * 2 * p.ldh + 128 * b;
 #pragma unroll
-        for (int q = 0; q < 8; ++q) lds_dma16_so(base + q * 16 * p.ldh, aoffs[q & 1], dst + q * 1024);
+        for (int q = 0; q < BS_ADMA; ++q) lds_dma16_so(base + q * 16 * p.ldh, aoffs[q & 1], dst + q * 1024);
     };
 
     // raw group copies: the tile's 144 weight rows x the 80 bytes of group g,
-    // rows 80 bytes apart (chunk c = 5 row + part); instruction ii of the 12
-    // takes chunks 64 ii + lane (past the 720 real ones: the last again, into
-    // the padding).  Every lane copies, so the main loop has no branch: the
-    // compiler would otherwise sink the fmas of a block below its later MFMAs.
+    // rows 80 bytes apart (chunk c = 5 row + part); instruction ii takes chunks
+    // 64 ii + lane (past the 720 real ones: the last again, into the padding).
+    // Every lane copies, so the main loop has no branch: the compiler would
+    // otherwise sink the fmas of a block below its later MFMAs.
     uint32_t rsrc[RAWW];
 #pragma unroll
     for (int r = 0; r < RAWW; ++r) {
-        const int c = min(64 * (w + W * r) + lane, 5 * BS_NT - 1);
+        const int c = min(64 * (w + W * r) + lane, BS_RAWC - 1);
         rsrc[r] = wrow_off(c / 5) + 16 * (c % 5);
     }
     auto dma_raw = [&](int h, int buf) {
         const uint8_t *gbase = p.w + ((int64_t)(b0 >> 2) + min(h, ngr - 1)) * 80;
-        const uint32_t base = lds_addr(raw + buf * BS_RAW);
+        const uint32_t base = lds_addr(raw + buf * S::RAW);
 #pragma unroll
         for (int r = 0; r < RAWW; ++r) lds_dma16_so(gbase, rsrc[r], base + (w + W * r) * 1024);
     };
 
-    // expand block pair hh of the raw group in buffer rb into fragment buffer
-    // pb; wave w takes tiles w, w + W, ..  (past nj: tile nj - 1 again, the
-    // same bytes another wave writes, so that no wave branches)
-    auto expand = [&](int rb, int hh, int pb) {
-        const uint8_t *rg = raw + rb * BS_RAW;
+    // expand block kk (of the split) from its raw group into fragment buffer
+    // pb: wave w takes tiles w, w + W, ..  (past nj: tile nj - 1 again, the
+    // same bytes another wave writes, so that no wave branches).  Block u of a
+    // group is nibble u & 1 of code words u >> 1 and 2 + (u >> 1).
+    auto expand = [&](int kk, int pb) {
+        const int u = kk & 3;
+        const uint8_t *rg = raw + ((kk >> 2) & 1) * S::RAW;
         uint8_t *bd = bfr + pb * BS_BF;
+        const uint32_t mask = (u & 1) ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
 #pragma unroll
         for (int r = 0; r < CVW; ++r) {
             const int j = min(w + W * r, nj - 1);
             const uint8_t *rrow = rg + (16 * j + fr) * 80;
             const vu4 q = *(const vu4 *)(rrow + 16 * kg);
-            const uint32_t wa = hh ? q[1] : q[0], wb = hh ? q[3] : q[2];
-            const uint32_t la = wa & 0x0F0F0F0Fu, lb = wb & 0x0F0F0F0Fu;
-            const uint32_t ua = wa & 0xF0F0F0F0u, ub = wb & 0xF0F0F0F0u;
-            const vu4 f0 = {code_pair<0>(la), code_pair<1>(la), code_pair<0>(lb), code_pair<1>(lb)};
-            const vu4 f1 = {code_pair<0>(ua), code_pair<1>(ua), code_pair<0>(ub), code_pair<1>(ub)};
-            *(vu4 *)(bd + (2 * j) * 1024 + lane * 16) = f0;
-            *(vu4 *)(bd + (2 * j + 1) * 1024 + lane * 16) = f1;
-            // the four lanes of a weight row write its scales alike
-            const vu4 sw = *(const vu4 *)(rrow + 64);
-            const float s0 = half_lo(hh ? sw[2] : sw[0]), s1 = half_lo(hh ? sw[3] : sw[1]) * 0.0625f;
-            *(float2 *)(sc + pb * 2 * BS_NT + 2 * (16 * j + fr)) = make_float2(s0, s1);
+            const uint32_t wa = (u & 2 ? q[1] : q[0]) & mask, wb = (u & 2 ? q[3] : q[2]) & mask;
+            const vu4 f = {code_pair<0>(wa), code_pair<1>(wa), code_pair<0>(wb), code_pair<1>(wb)};
+            *(vu4 *)(bd + j * 1024 + lane * 16) = f;
+            // the four lanes of a weight row write its scale alike
+            const uint32_t sw = *(const uint32_t *)(rrow + 64 + 4 * u);
+            sc[pb * BS_NT + 16 * j + fr] = (u & 1) ? half_lo(sw) * 0.0625f : half_lo(sw);
         }
     };
 
-    f4 acc[4][BS_J];
+    f4 acc[2][BS_J];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < BS_J; ++j) acc[i][j] = (f4){0.f, 0.f, 0.f, 0.f};
 
     // One block: activation fragments of ring slot `slot`, code fragments and
-    // scales of pair buffer pb, block bb of the pair.  Software-pipelined by
-    // weight tile: the fragment of tile j + 1 is read while tile j computes,
-    // and the MFMAs of tile j issue one by one between the fmas of tile j - 1
-    // (sched_group_barrier); a scheduling barrier per tile keeps the compiler
-    // from hoisting every product (and its registers) ahead of the fmas.
-    // fragment (i, plane P) of lane (fr, kg): row 16 i + fr, chunk (4 P + kg) ^ ((fr >> 1) & 7)
+    // scales of buffer pb.  Software-pipelined by weight tile: the fragment of
+    // tile j + 1 is read while tile j computes, and the MFMAs of tile j issue
+    // one by one between the fmas of tile j - 1 (sched_group_barrier); a
+    // scheduling barrier per tile keeps the compiler from hoisting every
+    // product (and its registers) ahead of the fmas.
+    // Fragment (i, plane P) of lane (fr, kg): row 16 i + fr, chunk (4 P + kg) ^ ((fr >> 1) & 7).
     const uint32_t aoff0 = fr * 128 + 16 * (kg ^ ((fr >> 1) & 7)), aoff1 = aoff0 ^ 64;
-    auto compute = [&](int slot, int pb, int bb) {
+    auto compute = [&](int slot, int pb) {
         const uint8_t *ab = ring + slot * BS_ABLK;
-        h8 a[4][2];
+        h8 a[2][2];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < 2; ++i) {
             a[i][0] = *(const h8 *)(ab + i * 2048 + aoff0);
             a[i][1] = *(const h8 *)(ab + i * 2048 + aoff1);
         }
-        const uint8_t *bq = bfr + pb * BS_BF + bb * 1024 + lane * 16;
-        // (volatile: the compiler would otherwise move each scale read to just
-        // before its first use, exposing its latency on every tile)
+        const uint8_t *bq = bfr + pb * BS_BF + lane * 16;
+        // (volatile, through an LDS pointer: the compiler would otherwise move
+        // each scale read to just before its first use, exposing its latency)
         typedef const __attribute__((address_space(3))) volatile float lds_vf;
-        lds_vf *sp = (lds_vf *)(sc + pb * 2 * BS_NT + 2 * fr + bb);
-        f4 pr[2][4];
+        lds_vf *sp = (lds_vf *)(sc + pb * BS_NT + fr);
+        f4 pr[2][2];
         // scales of tiles j - 1 (fmas this step), j and j + 1 (read this step)
         float s_prev = 0.0f, s_cur = sp[0];
         h8 bcur = *(const h8 *)bq;
@@ -686,28 +695,28 @@ __global__ __launch_bounds__(64 * W, 1) void gemm_q4_bs_kernel(GemmBsParams p, B
             h8 bnext = bcur;
             float s_next = 0.0f;
             if (j + 1 < BS_J) {
-                bnext = *(const h8 *)(bq + (j + 1) * 2048);
-                s_next = sp[32 * (j + 1)];
+                bnext = *(const h8 *)(bq + (j + 1) * 1024);
+                s_next = sp[16 * (j + 1)];
             }
             if (j < BS_J) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
+                for (int i = 0; i < 2; ++i)
                     pr[j & 1][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i][0], bcur, (f4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
+                for (int i = 0; i < 2; ++i)
                     pr[j & 1][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i][1], bcur, pr[j & 1][i], 0, 0, 0);
             }
             if (j > 0) {
                 const int jp = j - 1;
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
+                for (int i = 0; i < 2; ++i)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) acc[i][jp][r] = fmaf(s_prev, pr[jp & 1][i][r], acc[i][jp][r]);
             }
             if (j > 0 && j < BS_J) {
                 __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // the next fragment and scale
 #pragma unroll
-                for (int k = 0; k < 8; ++k) {
+                for (int k = 0; k < 4; ++k) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
                     __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // two fmas
                 }
@@ -719,9 +728,9 @@ __global__ __launch_bounds__(64 * W, 1) void gemm_q4_bs_kernel(GemmBsParams p, B
         }
     };
 
-    // prologue: raw groups 0 and 1, activation blocks 0 and 1 in flight
+    // prologue: raw group 0, activation blocks 0 and 1 in flight (raw group 1
+    // is the loop's first raw copy)
     dma_raw(0, 0);
-    dma_raw(1, 1);
     dma_a(0, 0);
     dma_a(1, 1);
 
@@ -731,9 +740,9 @@ __global__ __launch_bounds__(64 * W, 1) void gemm_q4_bs_kernel(GemmBsParams p, B
     // ever VALU operands
     {
         const _Float16 *sh = (const _Float16 *)p.sh, *sl = (const _Float16 *)p.sl;
-        int64_t srow[4];
+        int64_t srow[2];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < 2; ++i) {
             int64_t r = m0 + 16 * i + fr;
             if (r >= p.M) r = p.M - 1;
             srow[i] = r * p.ldsum;
@@ -743,30 +752,39 @@ __global__ __launch_bounds__(64 * W, 1) void gemm_q4_bs_kernel(GemmBsParams p, B
         for (int j = 0; j < BS_J; ++j) jrow[j] = wrow(16 * j + fr) + 64;
         for (int c = b0 >> 5; c <= (b1 - 1) >> 5; ++c) {
             const int bl = 32 * c + 8 * kg;  // this lane's first block
-            h8 xs[4][2];
+            h8 xs[2][2];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < 2; ++i) {
                 xs[i][0] = *(const h8 *)(sh + srow[i] + bl);
                 xs[i][1] = *(const h8 *)(sl + srow[i] + bl);
             }
             const int64_t ga = (int64_t)min(bl >> 2, G - 1) * 80, gb = (int64_t)min((bl >> 2) + 1, G - 1) * 80;
+            vu4 sa[BS_J], sb[BS_J];
+#pragma unroll
+            for (int j = 0; j < BS_J; ++j) {
+                sa[j] = *(const vu4 *)(jrow[j] + ga);
+                sb[j] = *(const vu4 *)(jrow[j] + gb);
+            }
+            // all of the chunk's loads in flight together (one round trip): the
+            // scheduler would otherwise move each tile's loads to its MFMAs
+            __builtin_amdgcn_sched_barrier(0);
             uint32_t keep[2] = {0u, 0u};  // bit u: block bl + 4 h + u lies in [b0, b1)
 #pragma unroll
             for (int u = 0; u < 8; ++u) keep[u >> 2] |= (bl + u >= b0 && bl + u < b1) ? 1u << (u & 3) : 0u;
 #pragma unroll
             for (int j = 0; j < BS_J; ++j) {
-                vu4 sa = *(const vu4 *)(jrow[j] + ga);
-                vu4 sb = *(const vu4 *)(jrow[j] + gb);
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
-                    sa[u] = (keep[0] >> u) & 1u ? sa[u] : 0u;
-                    sb[u] = (keep[1] >> u) & 1u ? sb[u] : 0u;
+                    sa[j][u] = (keep[0] >> u) & 1u ? sa[j][u] : 0u;
+                    sb[j][u] = (keep[1] >> u) & 1u ? sb[j][u] : 0u;
                 }
-                const vu4 mn = {__builtin_amdgcn_perm(sa[1], sa[0], 0x07060302u), __builtin_amdgcn_perm(sa[3], sa[2], 0x07060302u),
-                                __builtin_amdgcn_perm(sb[1], sb[0], 0x07060302u), __builtin_amdgcn_perm(sb[3], sb[2], 0x07060302u)};
+                const vu4 mn = {__builtin_amdgcn_perm(sa[j][1], sa[j][0], 0x07060302u),
+                                __builtin_amdgcn_perm(sa[j][3], sa[j][2], 0x07060302u),
+                                __builtin_amdgcn_perm(sb[j][1], sb[j][0], 0x07060302u),
+                                __builtin_amdgcn_perm(sb[j][3], sb[j][2], 0x07060302u)};
                 const h8 mh = __builtin_bit_cast(h8, mn);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
+                for (int i = 0; i < 2; ++i) {
                     f4 tm = __builtin_amdgcn_mfma_f32_16x16x32_f16(xs[i][0], mh, (f4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
                     tm = __builtin_amdgcn_mfma_f32_16x16x32_f16(xs[i][1], mh, tm, 0, 0, 0);
 #pragma unroll
@@ -777,69 +795,103 @@ __global__ __launch_bounds__(64 * W, 1) void gemm_q4_bs_kernel(GemmBsParams p, B
     }
 
     wait_vmcnt<0>();
-    lds_barrier();       // raw group 0 of every wave
-    expand(0, 0, 0);     // pair 0
-    lds_barrier();
+    lds_barrier();   // raw group 0 of every wave
+    expand(0, 0);    // block 0
 
-    // Per group h (blocks 4h..4h+3 of the split, pairs 2h and 2h+1).  Issue
-    // order of the copies: A(4h+2), A(4h+3), raw(h+2), A(4h+4), A(4h+5), so
-    // A(k) has 16 copy instructions issued after it, or 16 + RAWW when raw
-    // copies fall between, and raw(h+1) has 32 by the middle of group h.
+    // Per block k (unrolled by groups of 4 blocks, h = k / 4):
+    //   issue A(k + 2); wait for A(k); barrier (publishes the fragments of
+    //   block k, expanded during block k - 1, and every wave's raw copies);
+    //   at k = 4h issue raw(h + 1); compute block k; expand block k + 1.
+    // A(k) has A(k + 1) and A(k + 2) issued after it (2 BS_ADMA copies), and
+    // raw(h + 1) too when k = 4h + 1 or 4h + 2.  raw(h + 1) precedes A(4h + 2)
+    // and A(4h + 3), so the wait for A(4h + 3) covers it before the barrier
+    // that precedes the expansion of block 4h + 4; its buffer held group
+    // h - 1, whose last expansion (block 4h - 1) precedes the barrier of
+    // block 4h.
     int slot = 0;
     auto next = [](int s) { return s == BS_RING - 1 ? 0 : s + 1; };
     for (int h = 0; h < ngr; ++h) {
         const int k = 4 * h;
         dma_a(k + 2, next(next(slot)));
-        wait_vmcnt<16>();
-        compute(slot, 0, 0);
+        wait_vmcnt<2 * BS_ADMA>();
+        lds_barrier();
+        dma_raw(h + 1, (h + 1) & 1);
+        compute(slot, 0);
         slot = next(slot);
+        expand(k + 1, 1);
+
         dma_a(k + 3, next(next(slot)));
-        wait_vmcnt<16>();
-        compute(slot, 0, 1);
-        slot = next(slot);
-        expand(h & 1, 1, 1);      // pair 2h + 1
-        wait_vmcnt<32>();         // this wave's copies of raw group h + 1
+        wait_vmcnt<2 * BS_ADMA + RAWW>();
         lds_barrier();
-        dma_raw(h + 2, h & 1);    // buffer h & 1 is free: both its pairs are expanded
+        compute(slot, 1);
+        slot = next(slot);
+        expand(k + 2, 0);
+
         dma_a(k + 4, next(next(slot)));
-        wait_vmcnt<16 + RAWW>();
-        compute(slot, 1, 0);
-        slot = next(slot);
-        dma_a(k + 5, next(next(slot)));
-        wait_vmcnt<16 + RAWW>();
-        compute(slot, 1, 1);
-        slot = next(slot);
-        expand((h + 1) & 1, 0, 0);  // pair 2h + 2
+        wait_vmcnt<2 * BS_ADMA + RAWW>();
         lds_barrier();
+        compute(slot, 0);
+        slot = next(slot);
+        expand(k + 3, 1);
+
+        dma_a(k + 5, next(next(slot)));
+        wait_vmcnt<2 * BS_ADMA>();
+        lds_barrier();
+        compute(slot, 1);
+        slot = next(slot);
+        expand(k + 4, 0);
     }
     wait_vmcnt<0>();  // no copy into LDS outlives the workgroup
 
-    // epilogue: lane holds rows 4 (lane >> 4) + r of column lane & 15 of each tile
+    // epilogue: lane holds rows 4 (lane >> 4) + r of column lane & 15 of each
+    // tile.  Every global read is issued before its stores (row exponents and
+    // biases once, residuals per weight tile, at clamped addresses), so the
+    // stores, predicated on the row and column, do not wait one round trip each.
+    int exr[2][4];
+    bool mok[2][4];
+    int64_t mrow[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t m = m0 + 16 * i + 4 * kg + r;
+            mok[i][r] = m < p.M;
+            mrow[i][r] = mok[i][r] ? m : p.M - 1;
+            exr[i][r] = p.ex[mrow[i][r]];
+        }
     int bad_a = 0, bad_b = 0;
 #pragma unroll
     for (int j = 0; j < BS_J; ++j) {
         const int64_t n = n0 + 16 * j + fr;
-        if (j >= nj || n >= p.N) continue;
-        const float bias = (!p.part && n < p.bias_len) ? p.bias[n] : 0.0f;
+        const bool nok = j < nj && n < p.N;
+        const int64_t nc = nok ? n : n0;
+        if (p.part) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (nok && mok[i][r])
+                        p.part[((int64_t)z * p.M + mrow[i][r]) * p.N + nc] = ldexpf(acc[i][j][r], -exr[i][r]);
+            continue;
+        }
+        const float bias = nc < p.bias_len ? p.bias[nc] : 0.0f;
+        float res[2][4];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) res[i][r] = p.resid ? p.resid[mrow[i][r] * p.ldr + nc] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int64_t m = m0 + 16 * i + 4 * kg + r;
-                if (m >= p.M) continue;
-                float v = ldexpf(acc[i][j][r], -p.ex[m]);
-                if (p.part) {
-                    p.part[((int64_t)z * p.M + m) * p.N + n] = v;
-                } else {
-                    v = flush_small(v);
-                    if (n < p.bias_len) v = v + bias;
-                    bad_a |= isnan(v);
-                    if (p.resid) v = p.resid[m * p.ldr + n] + v;
-                    bad_b |= isnan(v);
-                    p.y[m * p.ldy + n] = v;
-                }
+                float v = flush_small(ldexpf(acc[i][j][r], -exr[i][r]));
+                if (nc < p.bias_len) v = v + bias;
+                const bool ok = nok && mok[i][r];
+                bad_a |= ok && isnan(v);
+                if (p.resid) v = res[i][r] + v;
+                bad_b |= ok && isnan(v);
+                if (ok) p.y[mrow[i][r] * p.ldy + nc] = v;
             }
-        }
     }
     if (p.st) {
         if (__any(bad_a) && lane == 0) nan_flag(p.st, p.layer, p.st_a);
@@ -938,8 +990,8 @@ int64_t gemm_bs_plane_rows(int64_t M) { return (M + 255) / 256 * 256; }
 
 GemmBsPlan plan_gemm_q4_bs(int64_t M, int64_t N, int64_t K) {
     GemmBsPlan pl{};
-    pl.waves = M <= 64 ? 1 : (M <= 128 ? 2 : 4);
-    const int64_t mt = 64 * pl.waves;
+    pl.waves = M <= 64 ? 2 : (M <= 128 ? 4 : 8);
+    const int64_t mt = BS_WR * pl.waves;
     pl.mtiles = (int)((M + mt - 1) / mt);
     const int64_t units = (N + 15) / 16;
     pl.ntiles = (int)((units + BS_J - 1) / BS_J);
@@ -964,13 +1016,13 @@ int launch_gemm_q4_bs(const GemmBsParams &p, const GemmBsPlan &pl, hipStream_t s
     if ((((uintptr_t)p.xh | (uintptr_t)p.sh | (uintptr_t)p.sl) & 15) || p.ldh % 8 || p.ldsum % 8)
         return set_error(GAJE_ERR_INVALID_ARG, "q4 block-scaled gemm: planes must be 16-byte aligned");
     if (p.M == 0) return GAJE_OK;
-    const int64_t mt = 64 * (int64_t)pl.waves;
+    const int64_t mt = BS_WR * (int64_t)pl.waves;
     if (p.plane_rows < (int64_t)pl.mtiles * mt)
         return set_error(GAJE_ERR_INVALID_ARG, "q4 block-scaled gemm: the activation plane holds %lld rows, the tiles read %lld",
                          (long long)p.plane_rows, (long long)pl.mtiles * mt);
     if (2 * p.plane_rows * p.ldh >= ((int64_t)1 << 32) || p.N * (int64_t)((p.nb + 3) / 4) * 80 >= ((int64_t)1 << 32))
         return set_error(GAJE_ERR_UNSUPPORTED, "q4 block-scaled gemm: operands beyond 4 GiB");
-    if ((pl.waves != 1 && pl.waves != 2 && pl.waves != 4) || pl.mtiles != (p.M + mt - 1) / mt || pl.ntiles <= 0 ||
+    if ((pl.waves != 2 && pl.waves != 4 && pl.waves != 8) || pl.mtiles != (p.M + mt - 1) / mt || pl.ntiles <= 0 ||
         pl.ntiles * (int64_t)BS_J < (p.N + 15) / 16 || pl.kb_per % 4 || pl.kb_per <= 0 ||
         (int64_t)pl.splits * pl.kb_per < p.nb || (int64_t)(pl.splits - 1) * pl.kb_per >= p.nb ||
         (pl.splits > 1 && !p.part))
@@ -986,16 +1038,16 @@ int launch_gemm_q4_bs(const GemmBsParams &p, const GemmBsPlan &pl, hipStream_t s
     if (total > (1 << 30)) return set_error(GAJE_ERR_UNSUPPORTED, "q4 block-scaled gemm: too many tiles");
     gd.total = (int32_t)total;
     const dim3 grid((unsigned)((total + 7) / 8 * 8));
+    if (bs_lds<8>() > max_lds_per_block()) return set_error(GAJE_ERR_UNSUPPORTED, "q4 block-scaled gemm: LDS");
     switch (pl.waves) {
-    case 1:
-        hipLaunchKernelGGL(gemm_q4_bs_kernel<1>, grid, dim3(64), bs_lds<1>(), s, q, gd);
-        break;
     case 2:
         hipLaunchKernelGGL(gemm_q4_bs_kernel<2>, grid, dim3(128), bs_lds<2>(), s, q, gd);
         break;
-    default:
-        if (bs_lds<4>() > max_lds_per_block()) return set_error(GAJE_ERR_UNSUPPORTED, "q4 block-scaled gemm: LDS");
+    case 4:
         hipLaunchKernelGGL(gemm_q4_bs_kernel<4>, grid, dim3(256), bs_lds<4>(), s, q, gd);
+        break;
+    default:
+        hipLaunchKernelGGL(gemm_q4_bs_kernel<8>, grid, dim3(512), bs_lds<8>(), s, q, gd);
         break;
     }
     GAJE_HIP_CHECK(hipGetLastError());

@@ -287,7 +287,7 @@ struct GemmBsParams {
     int32_t st_a, st_b;
 };
 struct GemmBsPlan {
-    int waves;               // 64-row wave tiles per workgroup (1, 2 or 4)
+    int waves;               // 32-row wave tiles per workgroup (2, 4 or 8)
     int mtiles, ntiles;      // activation-row tiles, weight-row tiles (<= 144 rows)
     int splits, kb_per;      // K splits of kb_per blocks (a multiple of 4)
     int64_t part_floats;     // partial buffer the splits need (0 if one split)
