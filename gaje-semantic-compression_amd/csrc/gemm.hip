@@ -506,17 +506,19 @@ size_t gemm_lds() { return (size_t)((GA ? 0 : 4 * MT * GM_ROW) + 4 * GM_NT * GM_
 // Tiling (gfx950, wave64).  A workgroup is W waves of 32 activation rows and
 // 9 tiles of 16 weight rows (144); every wave holds 2 x 9 accumulators of
 // v_mfma_f32_16x16x32_f16 (one Q4_0 block per step).  Eight waves (two per
-// SIMD) for a 256-row tile: one wave cannot keep the matrix core busy, or run
-// its VALU work beside its own MFMAs, but two waves of a SIMD interleave
-// (measured: 16x16x32 f16 issued from one wave per SIMD runs at half rate,
-// from two at the full rate with two fmas per MFMA at ~85%).
+// SIMD) for a 256-row tile, so that one wave's LDS waits and expansions
+// overlap the other's MFMAs.  (Measured by wall clock on 256 workgroups: one
+// wave per SIMD issuing 16x16x32 f16 MFMAs reaches ~1.7-1.9 PFLOP/s with up to
+// two independent fp32 fmas per MFMA, and VALU issue binds from about three.
+// The block scales cost two fmas per MFMA here, so the VALU work beside them
+// must stay small.)
 // - Activations: the split pass stores each block's hi and lo halves together
 //   (128 bytes per row); each wave streams its own rows into a private LDS
 //   ring of three blocks with global_load_lds, two blocks ahead, XOR-swizzled
 //   by 16-byte chunk so that fragment reads are conflict-free.
 // - Weights: the raw 80-byte groups of the tile's rows are copied into LDS one
-//   group ahead; each block's code fragments and scales are expanded into LDS
-//   one block ahead by all waves together (one barrier per block).
+//   group ahead; each pair of blocks' code fragments and scales is expanded
+//   into LDS one pair ahead by all waves together (one barrier per pair).
 // - No other vector memory access is made in the main loop, so the explicit
 //   vmcnt waits are exact.
 // - The grid is ordered so that the workgroups of one activation tile and
@@ -530,15 +532,16 @@ constexpr int BS_ABLK = BS_WR * 128;            // one block of a wave's rows (h
 constexpr int BS_ADMA = BS_ABLK / 1024;         // its copy instructions
 constexpr int BS_RING = 3;                      // ring slots per wave
 constexpr int BS_RAWC = BS_NT * 5;              // 16-byte chunks of one raw group (144 rows x 80 B)
+constexpr int BS_RAW = 768 * 16;                // one raw group buffer (720 chunks, padded to 12 copies)
 constexpr int BS_BF = BS_J * 1024;              // one block's code fragments
 constexpr int BS_SC = BS_NT * 4;                // one block's scales
 
 template <int W>
 struct BsShape {
-    static constexpr int RAWW = (BS_RAWC + 64 * W - 1) / (64 * W);  // raw copy instructions per wave per group
-    static constexpr int RAW = RAWW * W * 1024;                     // one raw group buffer (padded)
-    static constexpr int CVW = (BS_J + W - 1) / W;                  // fragment tiles each wave expands per block
-    static constexpr size_t LDS = (size_t)W * BS_RING * BS_ABLK + 2 * RAW + 2 * BS_BF + 2 * BS_SC;
+    static constexpr int RAWW = (768 + 64 * W - 1) / (64 * W);  // raw copy instructions per wave per group
+    static constexpr int CVW = (2 * BS_J + W - 1) / W;          // (block, tile) fragments each wave expands per pair
+    // ring, two raw groups, fragments and scales of two block pairs
+    static constexpr size_t LDS = (size_t)W * BS_RING * BS_ABLK + 2 * BS_RAW + 4 * BS_BF + 4 * BS_SC;
 };
 template <int W>
 constexpr size_t bs_lds() { return BsShape<W>::LDS; }
@@ -548,6 +551,11 @@ struct BsGrid {
 };
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+template <bool B>
+struct BsRole {
+    static constexpr bool value = B;
+};
 
 // f16 1024 + byte (bytes 2 s, 2 s + 1 of t), minus 1024: the two codes as f16.
 template <int S>
@@ -562,7 +570,7 @@ template <int W>
 __global__ __launch_bounds__(64 * W, 1) void gemm_q4_bs_kernel(GemmBsParams p, BsGrid gd) {
     using S = BsShape<W>;
     constexpr int RAWW = S::RAWW, CVW = S::CVW;
-    static_assert(2 * BS_ADMA + 2 * RAWW < 64 && S::LDS <= 163840, "limits");
+    static_assert(4 * BS_ADMA + RAWW < 64 && S::LDS <= 163840 && W <= 12, "limits");
     extern __shared__ __align__(16) uint8_t bs_mem[];
     // w through readfirstlane: the copies' bases must be provably wave-uniform (SGPRs)
     const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -585,9 +593,9 @@ __global__ __launch_bounds__(64 * W, 1) void gemm_q4_bs_kernel(GemmBsParams p, B
     const int64_t wstride = (int64_t)G * 80;
 
     uint8_t *ring = bs_mem + w * (BS_RING * BS_ABLK);
-    uint8_t *raw = bs_mem + W * BS_RING * BS_ABLK;  // [2][S::RAW]
-    uint8_t *bfr = raw + 2 * S::RAW;                // [2][BS_BF]
-    float *sc = (float *)(bfr + 2 * BS_BF);         // [2][BS_NT]
+    uint8_t *raw = bs_mem + W * BS_RING * BS_ABLK;  // [2 groups][BS_RAW]
+    uint8_t *bfr = raw + 2 * BS_RAW;                // [2 pairs][2 blocks][BS_BF]
+    float *sc = (float *)(bfr + 4 * BS_BF);         // [2 pairs][2 blocks][BS_NT]
 
     // byte offset of the weight row of tile column c (dummy columns past nj
     // repeat the last real one; the launcher checks that it fits 32 bits)
@@ -618,43 +626,58 @@ __global__ __launch_bounds__(64 * W, 1) void gemm_q4_bs_kernel(GemmBsParams p, B
     };
 
     // raw group copies: the tile's 144 weight rows x the 80 bytes of group g,
-    // rows 80 bytes apart (chunk c = 5 row + part); instruction ii takes chunks
-    // 64 ii + lane (past the 720 real ones: the last again, into the padding).
-    // Every lane copies, so the main loop has no branch: the compiler would
-    // otherwise sink the fmas of a block below its later MFMAs.
-    uint32_t rsrc[RAWW];
+    // rows 80 bytes apart (chunk c = 5 row + part), as 12 copy instructions of
+    // 64 chunks: copy i takes chunks 64 i + lane (past the 720 real ones: the
+    // last again, into the padding).  Wave w issues copies w, w + W, ..; in
+    // place of one past copy 11 it issues copy w again (same bytes, same place),
+    // so that every wave issues RAWW copies and no lane branches: the compiler
+    // would otherwise sink the fmas of a block below its later MFMAs.
+    uint32_t rsrc[RAWW], rdst[RAWW];
 #pragma unroll
     for (int r = 0; r < RAWW; ++r) {
-        const int c = min(64 * (w + W * r) + lane, BS_RAWC - 1);
+        const int ci = w + W * r < 12 ? w + W * r : w;
+        const int c = min(64 * ci + lane, BS_RAWC - 1);
         rsrc[r] = wrow_off(c / 5) + 16 * (c % 5);
+        rdst[r] = (uint32_t)ci * 1024;
     }
     auto dma_raw = [&](int h, int buf) {
         const uint8_t *gbase = p.w + ((int64_t)(b0 >> 2) + min(h, ngr - 1)) * 80;
-        const uint32_t base = lds_addr(raw + buf * S::RAW);
+        const uint32_t base = lds_addr(raw + buf * BS_RAW);
 #pragma unroll
-        for (int r = 0; r < RAWW; ++r) lds_dma16_so(gbase, rsrc[r], base + (w + W * r) * 1024);
+        for (int r = 0; r < RAWW; ++r) lds_dma16_so(gbase, rsrc[r], base + rdst[r]);
     };
 
-    // expand block kk (of the split) from its raw group into fragment buffer
-    // pb: wave w takes tiles w, w + W, ..  (past nj: tile nj - 1 again, the
-    // same bytes another wave writes, so that no wave branches).  Block u of a
-    // group is nibble u & 1 of code words u >> 1 and 2 + (u >> 1).
-    auto expand = [&](int kk, int pb) {
-        const int u = kk & 3;
-        const uint8_t *rg = raw + ((kk >> 2) & 1) * S::RAW;
-        uint8_t *bd = bfr + pb * BS_BF;
-        const uint32_t mask = (u & 1) ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
+    // expand block pair pp (blocks 2 pp, 2 pp + 1 of the split) from its raw
+    // group into fragment buffer pb: the 18 (block, tile) fragments go to the
+    // waves in turn, x = w, w + W, .. (past 17, or past tile nj - 1, the last
+    // one again: the same bytes another wave writes, so that no wave branches).
+    // Block u of a group is nibble u & 1 of code words u >> 1 and 2 + (u >> 1).
+    auto expand = [&](int pp, int pb) {
+        const uint8_t *rg = raw + ((pp >> 1) & 1) * BS_RAW;
+        const int hu = 2 * (pp & 1);  // the pair's first block within its group
+        // every read first (one LDS round trip), then the conversions and writes
+        vu4 q[CVW];
+        uint32_t sw[CVW];
+        int ee[CVW], jj[CVW];
 #pragma unroll
         for (int r = 0; r < CVW; ++r) {
-            const int j = min(w + W * r, nj - 1);
-            const uint8_t *rrow = rg + (16 * j + fr) * 80;
-            const vu4 q = *(const vu4 *)(rrow + 16 * kg);
-            const uint32_t wa = (u & 2 ? q[1] : q[0]) & mask, wb = (u & 2 ? q[3] : q[2]) & mask;
+            const int x = min(w + W * r, 2 * BS_J - 1);
+            ee[r] = x >= BS_J ? 1 : 0;
+            jj[r] = min(x - BS_J * ee[r], nj - 1);
+            const uint8_t *rrow = rg + (16 * jj[r] + fr) * 80;
+            q[r] = *(const vu4 *)(rrow + 16 * kg);
+            sw[r] = *(const uint32_t *)(rrow + 64 + 4 * (hu + ee[r]));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int r = 0; r < CVW; ++r) {
+            const int e = ee[r], j = jj[r];
+            const uint32_t mask = e ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
+            const uint32_t wa = (hu ? q[r][1] : q[r][0]) & mask, wb = (hu ? q[r][3] : q[r][2]) & mask;
             const vu4 f = {code_pair<0>(wa), code_pair<1>(wa), code_pair<0>(wb), code_pair<1>(wb)};
-            *(vu4 *)(bd + j * 1024 + lane * 16) = f;
+            *(vu4 *)(bfr + (2 * pb + e) * BS_BF + j * 1024 + lane * 16) = f;
             // the four lanes of a weight row write its scale alike
-            const uint32_t sw = *(const uint32_t *)(rrow + 64 + 4 * u);
-            sc[pb * BS_NT + 16 * j + fr] = (u & 1) ? half_lo(sw) * 0.0625f : half_lo(sw);
+            sc[(2 * pb + e) * BS_NT + 16 * j + fr] = e ? half_lo(sw[r]) * 0.0625f : half_lo(sw[r]);
         }
     };
 
@@ -665,14 +688,14 @@ __global__ __launch_bounds__(64 * W, 1) void gemm_q4_bs_kernel(GemmBsParams p, B
         for (int j = 0; j < BS_J; ++j) acc[i][j] = (f4){0.f, 0.f, 0.f, 0.f};
 
     // One block: activation fragments of ring slot `slot`, code fragments and
-    // scales of buffer pb.  Software-pipelined by weight tile: the fragment of
+    // scales of block buffer fb (pair buffer fb >> 1, block fb & 1).  Software-pipelined by weight tile: the fragment of
     // tile j + 1 is read while tile j computes, and the MFMAs of tile j issue
     // one by one between the fmas of tile j - 1 (sched_group_barrier); a
     // scheduling barrier per tile keeps the compiler from hoisting every
     // product (and its registers) ahead of the fmas.
     // Fragment (i, plane P) of lane (fr, kg): row 16 i + fr, chunk (4 P + kg) ^ ((fr >> 1) & 7).
     const uint32_t aoff0 = fr * 128 + 16 * (kg ^ ((fr >> 1) & 7)), aoff1 = aoff0 ^ 64;
-    auto compute = [&](int slot, int pb) {
+    auto compute = [&](int slot, int fb) {
         const uint8_t *ab = ring + slot * BS_ABLK;
         h8 a[2][2];
 #pragma unroll
@@ -680,11 +703,11 @@ __global__ __launch_bounds__(64 * W, 1) void gemm_q4_bs_kernel(GemmBsParams p, B
             a[i][0] = *(const h8 *)(ab + i * 2048 + aoff0);
             a[i][1] = *(const h8 *)(ab + i * 2048 + aoff1);
         }
-        const uint8_t *bq = bfr + pb * BS_BF + lane * 16;
+        const uint8_t *bq = bfr + fb * BS_BF + lane * 16;
         // (volatile, through an LDS pointer: the compiler would otherwise move
         // each scale read to just before its first use, exposing its latency)
         typedef const __attribute__((address_space(3))) volatile float lds_vf;
-        lds_vf *sp = (lds_vf *)(sc + pb * BS_NT + fr);
+        lds_vf *sp = (lds_vf *)(sc + fb * BS_NT + fr);
         f4 pr[2][2];
         // scales of tiles j - 1 (fmas this step), j and j + 1 (read this step)
         float s_prev = 0.0f, s_cur = sp[0];
@@ -728,11 +751,12 @@ __global__ __launch_bounds__(64 * W, 1) void gemm_q4_bs_kernel(GemmBsParams p, B
         }
     };
 
-    // prologue: raw group 0, activation blocks 0 and 1 in flight (raw group 1
-    // is the loop's first raw copy)
+    // prologue: raw groups 0 and 1, activation blocks 0, 1 and 2 in flight
     dma_raw(0, 0);
     dma_a(0, 0);
+    dma_raw(1, 1);
     dma_a(1, 1);
+    dma_a(2, 2);
 
     // the min term over this split's blocks: MFMAs over the block index, the
     // block-sum planes against the f16 mins (blocks outside [b0, b1) masked),
@@ -795,52 +819,69 @@ __global__ __launch_bounds__(64 * W, 1) void gemm_q4_bs_kernel(GemmBsParams p, B
     }
 
     wait_vmcnt<0>();
-    lds_barrier();   // raw group 0 of every wave
-    expand(0, 0);    // block 0
+    lds_barrier();   // raw groups 0 and 1 of every wave
+    expand(0, 0);    // blocks 0 and 1
+    lds_barrier();
 
-    // Per block k (unrolled by groups of 4 blocks, h = k / 4):
-    //   issue A(k + 2); wait for A(k); barrier (publishes the fragments of
-    //   block k, expanded during block k - 1, and every wave's raw copies);
-    //   at k = 4h issue raw(h + 1); compute block k; expand block k + 1.
-    // A(k) has A(k + 1) and A(k + 2) issued after it (2 BS_ADMA copies), and
-    // raw(h + 1) too when k = 4h + 1 or 4h + 2.  raw(h + 1) precedes A(4h + 2)
-    // and A(4h + 3), so the wait for A(4h + 3) covers it before the barrier
-    // that precedes the expansion of block 4h + 4; its buffer held group
-    // h - 1, whose last expansion (block 4h - 1) precedes the barrier of
-    // block 4h.
+    // One interval between barriers per block pair p (blocks 2 p, 2 p + 1):
+    // compute pair p from fragment buffer p & 1 and expand pair p + 1 into the
+    // other.  The upper half of the waves expands first and computes after, the
+    // lower half the reverse, so that the two waves of a SIMD overlap one's
+    // expansion with the other's MFMAs.
+    // - The activation copy of block k + 3 takes the ring slot of block k once
+    //   block k is computed (two blocks of work ahead of its use); each wave
+    //   waits for its own copies only, so no barrier is needed for them.
+    // - Raw group h + 1 is issued at the start of interval 2 h - 1 (its buffer
+    //   held group h - 1, last expanded in interval 2 h - 2) and waited for at
+    //   the end of interval 2 h, before the barrier that precedes its first
+    //   expansion (pair 2 h + 2, in interval 2 h + 1).
+    // Copies a wave has issued after the one it waits for (in issue order):
+    //   A(4h):   raw(h+1), A(4h+1), A(4h+2)    A(4h+1): A(4h+2), A(4h+3)
+    //   A(4h+2): A(4h+3), A(4h+4), raw(h+2)    A(4h+3): A(4h+4), raw(h+2), A(4h+5)
+    //   raw(h+1) at the end of interval 2h: A(4h+1) .. A(4h+4)
+    // (each wait is followed by a compiler memory barrier, so that no ring read
+    // is scheduled above it).
     int slot = 0;
     auto next = [](int s) { return s == BS_RING - 1 ? 0 : s + 1; };
-    for (int h = 0; h < ngr; ++h) {
-        const int k = 4 * h;
-        dma_a(k + 2, next(next(slot)));
-        wait_vmcnt<2 * BS_ADMA>();
-        lds_barrier();
-        dma_raw(h + 1, (h + 1) & 1);
-        compute(slot, 0);
-        slot = next(slot);
-        expand(k + 1, 1);
+    auto run = [&](auto role) {
+        constexpr bool EXPAND_FIRST = decltype(role)::value;
+        for (int h = 0; h < ngr; ++h) {
+            const int k = 4 * h;
+            // interval 2h: pair 2h from buffer 0, pair 2h + 1 into buffer 1
+            if constexpr (EXPAND_FIRST) expand(2 * h + 1, 1);
+            wait_vmcnt<RAWW + 2 * BS_ADMA>();
+            __asm__ volatile("" ::: "memory");
+            compute(slot, 0);
+            dma_a(k + 3, slot);
+            slot = next(slot);
+            wait_vmcnt<2 * BS_ADMA>();
+            __asm__ volatile("" ::: "memory");
+            compute(slot, 1);
+            dma_a(k + 4, slot);
+            slot = next(slot);
+            if constexpr (!EXPAND_FIRST) expand(2 * h + 1, 1);
+            wait_vmcnt<4 * BS_ADMA>();
+            lds_barrier();
 
-        dma_a(k + 3, next(next(slot)));
-        wait_vmcnt<2 * BS_ADMA + RAWW>();
-        lds_barrier();
-        compute(slot, 1);
-        slot = next(slot);
-        expand(k + 2, 0);
-
-        dma_a(k + 4, next(next(slot)));
-        wait_vmcnt<2 * BS_ADMA + RAWW>();
-        lds_barrier();
-        compute(slot, 0);
-        slot = next(slot);
-        expand(k + 3, 1);
-
-        dma_a(k + 5, next(next(slot)));
-        wait_vmcnt<2 * BS_ADMA>();
-        lds_barrier();
-        compute(slot, 1);
-        slot = next(slot);
-        expand(k + 4, 0);
-    }
+            // interval 2h + 1: pair 2h + 1 from buffer 1, pair 2h + 2 into buffer 0
+            dma_raw(h + 2, h & 1);
+            if constexpr (EXPAND_FIRST) expand(2 * h + 2, 0);
+            wait_vmcnt<2 * BS_ADMA + RAWW>();
+            __asm__ volatile("" ::: "memory");
+            compute(slot, 2);
+            dma_a(k + 5, slot);
+            slot = next(slot);
+            wait_vmcnt<2 * BS_ADMA + RAWW>();
+            __asm__ volatile("" ::: "memory");
+            compute(slot, 3);
+            dma_a(k + 6, slot);
+            slot = next(slot);
+            if constexpr (!EXPAND_FIRST) expand(2 * h + 2, 0);
+            lds_barrier();
+        }
+    };
+    if (w >= W / 2) run(BsRole<true>{});
+    else run(BsRole<false>{});
     wait_vmcnt<0>();  // no copy into LDS outlives the workgroup
 
     // epilogue: lane holds rows 4 (lane >> 4) + r of column lane & 15 of each
