@@ -244,13 +244,13 @@ size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 // the two block-sum planes, split-K partials.
 struct GemmWorkspace {
     int *ex;
-    uint16_t *xh, *sh, *sl;
+    uint16_t *xh, *sh, *sl, *mins;
     int64_t plane_rows, ldsum;
     float *part;
     size_t bytes;
 };
 
-GemmWorkspace gemm_workspace(char *base, int64_t m, int64_t k, const GemmBsPlan &pl) {
+GemmWorkspace gemm_workspace(char *base, int64_t m, int64_t n, int64_t k, const GemmBsPlan &pl) {
     GemmWorkspace w{};
     size_t off = 0;
     w.ex = (int *)(base + off);
@@ -265,6 +265,8 @@ GemmWorkspace gemm_workspace(char *base, int64_t m, int64_t k, const GemmBsPlan 
     off = align256(off + (size_t)(m * w.ldsum) * 2);
     w.part = (float *)(base + off);
     off = align256(off + (size_t)pl.part_floats * 4);
+    w.mins = (uint16_t *)(base + off);  // [n][ldsum]: the weight rows' block mins
+    off = align256(off + (size_t)(n * w.ldsum) * 2);
     w.bytes = off;
     return w;
 }
@@ -274,7 +276,7 @@ GemmWorkspace gemm_workspace(char *base, int64_t m, int64_t k, const GemmBsPlan 
 extern "C" int64_t gaje_hip_q4_0_gemm_mfma_workspace(int64_t m, int64_t n, int64_t k) {
     if (m < 0 || n <= 0 || k <= 0 || k % 32 != 0) return -1;
     if (m == 0) return 0;
-    return (int64_t)gemm_workspace(nullptr, m, k, plan_gemm_q4_bs(m, n, k)).bytes;
+    return (int64_t)gemm_workspace(nullptr, m, n, k, plan_gemm_q4_bs(m, n, k)).bytes;
 }
 
 extern "C" int gaje_hip_q4_0_gemm_mfma(const void *packed, const float *X, const float *bias, int64_t bias_len,
@@ -286,7 +288,7 @@ extern "C" int gaje_hip_q4_0_gemm_mfma(const void *packed, const float *X, const
     if (m == 0 || n == 0) return GAJE_OK;
     if (((uintptr_t)workspace & 15) != 0) return set_error(GAJE_ERR_INVALID_ARG, "gemm workspace must be 16-byte aligned");
     const GemmBsPlan pl = plan_gemm_q4_bs(m, n, k);
-    const GemmWorkspace w = gemm_workspace((char *)workspace, m, k, pl);
+    const GemmWorkspace w = gemm_workspace((char *)workspace, m, n, k, pl);
     if ((int64_t)w.bytes > workspace_bytes)
         return set_error(GAJE_ERR_INVALID_ARG, "gemm workspace of %lld bytes is smaller than the %zu needed",
                          (long long)workspace_bytes, w.bytes);
@@ -303,8 +305,11 @@ extern "C" int gaje_hip_q4_0_gemm_mfma(const void *packed, const float *X, const
     sp.sl = w.sl;
     sp.ldsum = w.ldsum;
     GAJE_TRY(launch_split_rows(sp, s));
+    GAJE_TRY(launch_q4_mins((const uint8_t *)packed, n, k, w.mins, w.ldsum, s));
     GemmBsParams p{};
     p.w = (const uint8_t *)packed;
+    p.mins = w.mins;
+    p.ldm = w.ldsum;
     p.xh = w.xh;
     p.plane_rows = w.plane_rows;
     p.sh = w.sh;

@@ -605,7 +605,6 @@ __global__ __launch_bounds__(64 * W, 1) void gemm_q4_bs_kernel(GemmBsParams p, B
         if (n >= p.N) n = p.N - 1;
         return (uint32_t)(n * wstride);
     };
-    auto wrow = [&](int c) -> const uint8_t * { return p.w + wrow_off(c); };
 
     // activation copies: per block a wave copies its 32 rows x 128 bytes (the
     // block's hi | lo halves, one cache line per row).  Instruction q takes rows
@@ -759,9 +758,9 @@ __global__ __launch_bounds__(64 * W, 1) void gemm_q4_bs_kernel(GemmBsParams p, B
     dma_a(2, 2);
 
     // the min term over this split's blocks: MFMAs over the block index, the
-    // block-sum planes against the f16 mins (blocks outside [b0, b1) masked),
-    // one tile at a time into a temporary, so that the accumulators are only
-    // ever VALU operands
+    // block-sum planes against the dense f16 mins (blocks outside [b0, b1)
+    // masked), one tile at a time into a temporary, so that the accumulators
+    // are only ever VALU operands
     {
         const _Float16 *sh = (const _Float16 *)p.sh, *sl = (const _Float16 *)p.sl;
         int64_t srow[2];
@@ -771,9 +770,15 @@ __global__ __launch_bounds__(64 * W, 1) void gemm_q4_bs_kernel(GemmBsParams p, B
             if (r >= p.M) r = p.M - 1;
             srow[i] = r * p.ldsum;
         }
-        const uint8_t *jrow[BS_J];
+        const uint16_t *mrow[BS_J];
 #pragma unroll
-        for (int j = 0; j < BS_J; ++j) jrow[j] = wrow(16 * j + fr) + 64;
+        for (int j = 0; j < BS_J; ++j) {
+            int c = 16 * j + fr;
+            if (c >= 16 * nj) c = 16 * nj - 1;
+            int64_t n = n0 + c;
+            if (n >= p.N) n = p.N - 1;
+            mrow[j] = p.mins + n * p.ldm;
+        }
         for (int c = b0 >> 5; c <= (b1 - 1) >> 5; ++c) {
             const int bl = 32 * c + 8 * kg;  // this lane's first block
             h8 xs[2][2];
@@ -782,30 +787,20 @@ __global__ __launch_bounds__(64 * W, 1) void gemm_q4_bs_kernel(GemmBsParams p, B
                 xs[i][0] = *(const h8 *)(sh + srow[i] + bl);
                 xs[i][1] = *(const h8 *)(sl + srow[i] + bl);
             }
-            const int64_t ga = (int64_t)min(bl >> 2, G - 1) * 80, gb = (int64_t)min((bl >> 2) + 1, G - 1) * 80;
-            vu4 sa[BS_J], sb[BS_J];
+            vu4 mq[BS_J];
 #pragma unroll
-            for (int j = 0; j < BS_J; ++j) {
-                sa[j] = *(const vu4 *)(jrow[j] + ga);
-                sb[j] = *(const vu4 *)(jrow[j] + gb);
-            }
+            for (int j = 0; j < BS_J; ++j) mq[j] = *(const vu4 *)(mrow[j] + bl);
             // all of the chunk's loads in flight together (one round trip): the
             // scheduler would otherwise move each tile's loads to its MFMAs
             __builtin_amdgcn_sched_barrier(0);
-            uint32_t keep[2] = {0u, 0u};  // bit u: block bl + 4 h + u lies in [b0, b1)
+            uint32_t keep[4];  // the halves of blocks bl + 2 q, bl + 2 q + 1 inside [b0, b1)
 #pragma unroll
-            for (int u = 0; u < 8; ++u) keep[u >> 2] |= (bl + u >= b0 && bl + u < b1) ? 1u << (u & 3) : 0u;
+            for (int q = 0; q < 4; ++q)
+                keep[q] = (bl + 2 * q >= b0 && bl + 2 * q < b1 ? 0x0000FFFFu : 0u) |
+                          (bl + 2 * q + 1 >= b0 && bl + 2 * q + 1 < b1 ? 0xFFFF0000u : 0u);
 #pragma unroll
             for (int j = 0; j < BS_J; ++j) {
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    sa[j][u] = (keep[0] >> u) & 1u ? sa[j][u] : 0u;
-                    sb[j][u] = (keep[1] >> u) & 1u ? sb[j][u] : 0u;
-                }
-                const vu4 mn = {__builtin_amdgcn_perm(sa[j][1], sa[j][0], 0x07060302u),
-                                __builtin_amdgcn_perm(sa[j][3], sa[j][2], 0x07060302u),
-                                __builtin_amdgcn_perm(sb[j][1], sb[j][0], 0x07060302u),
-                                __builtin_amdgcn_perm(sb[j][3], sb[j][2], 0x07060302u)};
+                const vu4 mn = {mq[j][0] & keep[0], mq[j][1] & keep[1], mq[j][2] & keep[2], mq[j][3] & keep[3]};
                 const h8 mh = __builtin_bit_cast(h8, mn);
 #pragma unroll
                 for (int i = 0; i < 2; ++i) {
@@ -940,6 +935,19 @@ __global__ __launch_bounds__(64 * W, 1) void gemm_q4_bs_kernel(GemmBsParams p, B
     }
 }
 
+// mins[n][b] = the f16 min of block b of row n (the high half of word b % 4
+// of the group's scale words, at byte 64 of its 80), 0 for b >= nb.
+__global__ __launch_bounds__(256) void q4_mins_kernel(const uint8_t *w, int64_t N, int nb, uint16_t *mins, int64_t ldm) {
+    const int64_t G = (nb + 3) / 4, total = N * ldm;
+    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+        const int64_t n = e / ldm;
+        const int b = (int)(e - n * ldm);
+        uint16_t v = 0;
+        if (b < nb) v = (uint16_t)(*(const uint32_t *)(w + (n * G + (b >> 2)) * 80 + 64 + 4 * (b & 3)) >> 16);
+        mins[e] = v;
+    }
+}
+
 }  // namespace
 
 int launch_q4_row_exponents(const uint8_t *packed, int64_t N, int64_t K, int *ew, hipStream_t s) {
@@ -1027,6 +1035,17 @@ GemmPlan plan_gemm_q4_grouped(int64_t R, int64_t E, int64_t N, int64_t K) {
 }
 
 int64_t gemm_bs_sum_cols(int64_t K) { return (K / 32 + 31) / 32 * 32; }
+
+int launch_q4_mins(const uint8_t *packed, int64_t N, int64_t K, uint16_t *mins, int64_t ldm, hipStream_t s) {
+    if (!packed || !mins || N <= 0 || K <= 0 || K % 32 || ldm < gemm_bs_sum_cols(K) || N * ldm >= ((int64_t)1 << 40))
+        return set_error(GAJE_ERR_INVALID_ARG, "q4 block mins: bad arguments");
+    const int64_t total = N * ldm;
+    int64_t g = (total + 255) / 256;
+    if (g > 65536) g = 65536;
+    hipLaunchKernelGGL(q4_mins_kernel, dim3((unsigned)g), dim3(256), 0, s, packed, N, (int)(K / 32), mins, ldm);
+    GAJE_HIP_CHECK(hipGetLastError());
+    return GAJE_OK;
+}
 int64_t gemm_bs_plane_rows(int64_t M) { return (M + 255) / 256 * 256; }
 
 GemmBsPlan plan_gemm_q4_bs(int64_t M, int64_t N, int64_t K) {
@@ -1054,7 +1073,10 @@ int launch_gemm_q4_bs(const GemmBsParams &p, const GemmBsPlan &pl, hipStream_t s
         (p.M > 0 && (!p.xh || !p.sh || !p.sl || !p.ex || !p.y || p.ldh < 64 * (int64_t)p.nb ||
                      p.ldsum < gemm_bs_sum_cols(32 * (int64_t)p.nb))))
         return set_error(GAJE_ERR_INVALID_ARG, "q4 block-scaled gemm: bad arguments");
-    if ((((uintptr_t)p.xh | (uintptr_t)p.sh | (uintptr_t)p.sl) & 15) || p.ldh % 8 || p.ldsum % 8)
+    if (p.M > 0 && (!p.mins || p.ldm < gemm_bs_sum_cols(32 * (int64_t)p.nb)))
+        return set_error(GAJE_ERR_INVALID_ARG, "q4 block-scaled gemm: no block mins");
+    if ((((uintptr_t)p.xh | (uintptr_t)p.sh | (uintptr_t)p.sl | (uintptr_t)p.mins) & 15) || p.ldh % 8 || p.ldsum % 8 ||
+        p.ldm % 8)
         return set_error(GAJE_ERR_INVALID_ARG, "q4 block-scaled gemm: planes must be 16-byte aligned");
     if (p.M == 0) return GAJE_OK;
     const int64_t mt = BS_WR * (int64_t)pl.waves;

@@ -268,6 +268,8 @@ GemmPlan plan_gemm_q4(int64_t M, int64_t N, int64_t K);
 // operands.  Its activation planes come from launch_split_rows with sh set.
 struct GemmBsParams {
     const uint8_t *w;        // packed rows (launch_pack_q4_0)
+    const uint16_t *mins;    // the rows' block mins as f16, [N][ldm] (launch_q4_mins)
+    int64_t ldm;             // >= gemm_bs_sum_cols(K)
     const uint16_t *xh;      // activation plane [plane_rows][ldh] (hi | lo per block, ldh >= 2K)
     int64_t plane_rows;      // rows allocated: >= gemm_bs_plane_rows(M) (rows past M are read, not used)
     const uint16_t *sh, *sl; // block-sum planes [M][ldsum]
@@ -296,6 +298,9 @@ GemmBsPlan plan_gemm_q4_bs(int64_t M, int64_t N, int64_t K);
 int launch_gemm_q4_bs(const GemmBsParams &p, const GemmBsPlan &plan, hipStream_t s);
 // Columns of the block-sum planes for a K: K/32 rounded up to a multiple of 32.
 int64_t gemm_bs_sum_cols(int64_t K);
+// The block mins of packed Q4_0 rows as a dense f16 matrix [N][ldm] (zero past
+// K / 32 blocks), ldm >= gemm_bs_sum_cols(K): the min term's operand.
+int launch_q4_mins(const uint8_t *packed, int64_t N, int64_t K, uint16_t *mins, int64_t ldm, hipStream_t s);
 // Rows the activation plane must hold for M activation rows (a multiple of 256).
 int64_t gemm_bs_plane_rows(int64_t M);
 
@@ -326,11 +331,14 @@ struct PrefillAttnParams {
     int32_t n_head, n_kv, head_dim;
     float *out;              // [P][n_head * head_dim]
     float *ws;               // key-chunk partials: prefill_attn_ws_floats(P, n_head, head_dim) floats
+    uint16_t *kv16;          // f16 pairs of the keys and values: prefill_kv16_halves(kv16_keys, ..) halves
+    int64_t kv16_keys;       // positions kv16 holds (>= pos0 + P)
 };
 // Keys are split into at most PREFILL_ATTN_CHUNKS chunks per query block,
 // each computed by its own workgroup and merged afterwards.
 constexpr int PREFILL_ATTN_CHUNKS = 8;
 int64_t prefill_attn_ws_floats(int64_t P, int64_t n_head, int64_t head_dim);
+int64_t prefill_kv16_halves(int64_t keys, int64_t n_kv, int64_t head_dim);
 int launch_prefill_attention(const PrefillAttnParams &p, hipStream_t s);
 
 // Batched decode: NV (<= 16) activation vectors per matvec, each product in

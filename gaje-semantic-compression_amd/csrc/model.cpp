@@ -59,6 +59,8 @@ struct DevLinear {
     uint32_t *a_col = nullptr;
     uint16_t *a_val = nullptr;
     int64_t bytes = 0;
+    uint16_t *mins = nullptr;  // FMT_Q4_0: the block mins [N][ldm] the MFMA prefill's products read
+    int64_t ldm = 0;
 };
 
 struct Layer {
@@ -315,6 +317,8 @@ struct gaje_hip_model {
         uint16_t *sh = nullptr, *sl = nullptr;  // block-sum planes [rows][gemm_bs_sum_cols(kmax)]
         int *ex = nullptr;
         uint32_t *ids = nullptr;
+        uint16_t *kv16 = nullptr;  // attention's f16 keys and values, prefill_kv16_halves(kv16_keys, ..)
+        int64_t kv16_keys = 0;
     } pf;
 
     std::vector<void *> allocs;
@@ -1021,7 +1025,11 @@ int prefill_reserve(gaje_hip_model *m, int64_t rows) {
     for (void *p : {(void *)f.H, (void *)f.QKV, (void *)f.Q, (void *)f.ATT, (void *)f.GU, (void *)f.part, (void *)f.xh,
                     (void *)f.sh, (void *)f.sl, (void *)f.ex, (void *)f.ids, (void *)f.aws})
         if (p) m->release(p);
+    uint16_t *kv16 = f.kv16;
+    const int64_t kv16_keys = f.kv16_keys;
     f = gaje_hip_model::Prefill();
+    f.kv16 = kv16;
+    f.kv16_keys = kv16_keys;
     const int64_t kmax = prefill_kmax(m);
     GAJE_TRY(m->alloc(&f.H, (size_t)(rows * m->n_embd)));
     GAJE_TRY(m->alloc(&f.QKV, (size_t)(rows * L0.qkv.N)));
@@ -1067,6 +1075,8 @@ int prefill_gemm(gaje_hip_model *m, const DevLinear &D, int64_t P, float *y, con
     if (pl.part_floats > f.part_floats) return set_error(GAJE_ERR_INVALID_ARG, "prefill: split-K buffer too small");
     GemmBsParams p{};
     p.w = D.w;
+    p.mins = D.mins;
+    p.ldm = D.ldm;
     p.xh = f.xh;
     p.plane_rows = gemm_bs_plane_rows(f.rows);
     p.sh = f.sh;
@@ -1137,6 +1147,8 @@ int prefill_layer(gaje_hip_model *m, int64_t l, int64_t pos, int64_t P) {
     ap.head_dim = (int32_t)m->hd;
     ap.out = f.ATT;
     ap.ws = f.aws;
+    ap.kv16 = f.kv16;
+    ap.kv16_keys = f.kv16_keys;
     GAJE_TRY(launch_prefill_attention(ap, s));
 
     sp = prefill_split(m, f.ATT, m->q_rows, P, m->q_rows);
@@ -1175,6 +1187,25 @@ extern "C" int gaje_hip_prefill_mfma(gaje_hip_model *m, const uint32_t *ids, int
     const int64_t pos0 = m->pos;
     GAJE_TRY(reserve_ctx(m, pos0 + n));
     hipStream_t s = m->stream;
+    if (m->n_layers > 0 && !m->layers[0].qkv.mins) {
+        // the products' dense block mins, built once per body tensor
+        for (Layer &Ly : m->layers)
+            for (DevLinear *D : {&Ly.qkv, &Ly.o, &Ly.gate_up, &Ly.down}) {
+                D->ldm = gemm_bs_sum_cols(D->K);
+                GAJE_TRY(m->alloc(&D->mins, (size_t)(D->N * D->ldm)));
+                GAJE_TRY(launch_q4_mins(D->w, D->N, D->K, D->mins, D->ldm, s));
+            }
+    }
+    if (m->n_layers > 0 && m->pf.kv16_keys < pos0 + n) {
+        // the attention's converted keys and values, for every position this prompt reaches
+        GAJE_HIP_CHECK(hipStreamSynchronize(s));
+        if (m->pf.kv16) m->release(m->pf.kv16);
+        m->pf.kv16 = nullptr;
+        m->pf.kv16_keys = 0;
+        const int64_t keys = (pos0 + n + 255) / 256 * 256;
+        GAJE_TRY(m->alloc(&m->pf.kv16, (size_t)prefill_kv16_halves(keys, m->n_kv, m->hd)));
+        m->pf.kv16_keys = keys;
+    }
     GAJE_TRY(launch_state_set(m->st, (int32_t)pos0, ids[n - 1], -1, -1, 1, s));
     int64_t last_rows = 0;
     for (int64_t c0 = 0; c0 < n; c0 += PREFILL_CHUNK) {

@@ -56,201 +56,261 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(PrefillRopeParams p) {
     }
 }
 
-// Causal GQA attention of a chunk on the fp32 matrix cores (flash-style, one
-// wave per 16 query tokens of one query head).  Per key tile of 16 positions:
-//   S = Q K^T (v_mfma_f32_16x16x4_f32 over the head dimension), scaled by
-//   1/sqrt(head_dim), masked past each query's position; the running row max
-//   m and sum l are updated (e = expf(s - m), earlier terms rescaled by
-//   expf(m_old - m)); O += P V (P reshaped through LDS into the A layout, the
-//   V tile staged in LDS).  out = O / (l + 1e-12).  Products and sums are
-//   fp32 with another association than the reference's serial loops
-//   (attention.rs:87-127): fp32 accuracy, not its bits.
-// Lane layout of the instruction (lane i, checked on the device): A[i%16][i/16],
-// B[i/16][i%16], D[4*(i/16)+r][i%16] in component r.
+// Causal GQA attention of a chunk on the f16 matrix cores, each fp32 operand
+// split into an f16 pair (hi = f16(x), lo = f16(x - hi)) and each product
+// taken as hi.hi + hi.lo + lo.hi (v_mfma_f32_16x16x32_f16, fp32
+// accumulation; the dropped lo.lo term is below 2^-22 relative).  One wave
+// per 16 queries of one query head and one chunk of keys, walked 32 keys at a
+// time, all transposed so that every lane keeps one query:
+//   S^T = K Q^T   (keys x queries; lane (fr, kg) holds keys 4 kg + r and
+//                  16 + 4 kg + r of query fr),
+//   scaled by log2(e)/sqrt(head_dim) and masked past the query's position;
+//   the running max m (over the four lanes of the query) and the lane's
+//   partial sum l are updated (e = exp2(s - m) on the hardware exp2, ~1 ulp,
+//   earlier terms rescaled by exp2(m_old - m));
+//   O^T += V^T P^T (dims x queries; P^T straight from the lanes of S^T, whose
+//                  key order the converted V tiles follow).
+// out = O / (l + 1e-12) in the merge.  Products and sums are fp32 with another
+// association than the reference's serial loops (attention.rs:87-127): fp32
+// accuracy, not its bits.  Operands must stay below 65504 in magnitude (the
+// f16 range of the hi part).
+// Lane layout of v_mfma_f32_16x16x32_f16 (lane i): A[i % 16][8 (i / 16) + e],
+// B[8 (i / 16) + e][i % 16], D[4 (i / 16) + r][i % 16] in component r.
+typedef _Float16 ah8 __attribute__((ext_vector_type(8)));
 typedef float f4v __attribute__((ext_vector_type(4)));
 
-// Reductions over the 16 lanes of a DPP row (the lanes holding one 4-row group
-// of a tile): xor 1, xor 2, the half-row mirror and the row mirror.  Each step
-// combines symmetric pairs, so all 16 lanes end with the same value.
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+__device__ __forceinline__ void split_f16(float x, _Float16 &hi, _Float16 &lo) {
+    hi = (_Float16)x;
+    lo = (_Float16)(x - (float)hi);
 }
-__device__ __forceinline__ float row16_max(float v) {
-    v = fmaxf(v, dpp_f<0xB1>(v));
-    v = fmaxf(v, dpp_f<0x4E>(v));
-    v = fmaxf(v, dpp_f<0x141>(v));
-    return fmaxf(v, dpp_f<0x140>(v));
-}
-__device__ __forceinline__ float row16_sum(float v) {
-    v = v + dpp_f<0xB1>(v);
-    v = v + dpp_f<0x4E>(v);
-    v = v + dpp_f<0x141>(v);
-    return v + dpp_f<0x140>(v);
+
+// The f16 pairs of the cache's keys and values [0, keys) (zero up to a
+// multiple of 32), in the layouts of the fragments above:
+//   K16[g][pos][s][hi 32 | lo 32]: dimensions 32 s .. 32 s + 31 of key pos;
+//   V16[g][d][tile][hi 32 | lo 32]: keys of the 32-key tile, slot 8 kg + 4 u + r
+//   holding key 32 tile + 16 u + 4 kg + r (the key order of P^T's lanes).
+// One workgroup per (tile, kv head, 32 dimensions); four elements of each
+// operand per thread.
+__global__ __launch_bounds__(256) void prefill_kv16_kernel(PrefillAttnParams p, int ntiles) {
+    __shared__ float kt[32][33];  // this tile's keys, [dimension][key]
+    const int tile = blockIdx.x, g = blockIdx.y, tid = threadIdx.x, HD = p.head_dim;
+    const int d0 = 32 * (int)blockIdx.z;
+    const int64_t k0 = (int64_t)tile * 32, keys = p.pos0 + p.P;
+    const float *K = p.k_cache + ((int64_t)g * HD + d0) * p.cap, *V = p.v_cache + ((int64_t)g * HD + d0) * p.cap;
+    uint16_t *k16 = p.kv16 + (int64_t)g * ntiles * 32 * 2 * HD;
+    uint16_t *v16 = p.kv16 + (int64_t)p.n_kv * ntiles * 32 * 2 * HD + ((int64_t)g * HD + d0) * ntiles * 64;
+    float kv[4], vv[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int e = tid + 256 * q, d = e >> 5, j = e & 31;
+        const int kg = j >> 3, u = (j >> 2) & 1, r = j & 3;
+        const int64_t pos = k0 + 16 * u + 4 * kg + r;
+        kv[q] = k0 + j < keys ? K[(int64_t)d * p.cap + k0 + j] : 0.0f;
+        vv[q] = pos < keys ? V[(int64_t)d * p.cap + pos] : 0.0f;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int e = tid + 256 * q, d = e >> 5, j = e & 31;
+        kt[d][j] = kv[q];
+        _Float16 hi, lo;
+        split_f16(vv[q], hi, lo);
+        uint16_t *dst = v16 + ((int64_t)d * ntiles + tile) * 64;
+        dst[j] = __builtin_bit_cast(uint16_t, hi);
+        dst[32 + j] = __builtin_bit_cast(uint16_t, lo);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int e = tid + 256 * q, j = e >> 5, d = e & 31;
+        _Float16 hi, lo;
+        split_f16(kt[d][j], hi, lo);
+        uint16_t *dst = k16 + (k0 + j) * 2 * HD + d0 * 2 + d;
+        dst[0] = __builtin_bit_cast(uint16_t, hi);
+        dst[32] = __builtin_bit_cast(uint16_t, lo);
+    }
 }
 
 // Workgroup (query block, query head, key chunk c) walks keys [c*kch,
 // (c+1)*kch) and writes its rows' running max m, sum l and unnormalised O to
 // the workspace; prefill_attn_merge_kernel combines the chunks.
-// HD / 64 waves per workgroup: wave w owns head dimensions [64w, 64w + 64),
-// both for its partial S = Q K^T (the partials are exchanged through LDS and
-// summed as wave 0's + wave 1's in both waves, so both hold the same S and
-// run the same softmax) and for its 64 columns of O.
 template <int HD>
-__global__ __launch_bounds__(HD) void prefill_attn_mfma_kernel(PrefillAttnParams p, int64_t kch) {
-    constexpr int NW = HD / 64;   // waves
-    constexpr int NS = 16;        // k-steps of a wave's partial S (64 dimensions)
-    constexpr int NT = 4;         // 16-column tiles of a wave's O
-    constexpr int NV = 4;         // float4s of a wave's V tile per lane
-    constexpr int VS = 17;        // LDS stride (floats) of a V-tile row (one row per dimension)
-    __shared__ float ps[NW][16 * 16];
-    __shared__ float vt[NW][64 * VS];
-    __shared__ f4v sx[NW > 1 ? NW : 1][64];
-    __shared__ uint64_t tab[32];  // the exponential's table
-    const int tid = threadIdx.x, w = tid >> 6, i = tid & 63, c16 = i & 15, q4 = i >> 4;
-    if (tid < 32) tab[tid] = kExp2Tab[tid];
+__global__ __launch_bounds__(64) void prefill_attn_f16_kernel(PrefillAttnParams p, int64_t kch, int ntiles) {
+    constexpr int NS = HD / 32;  // k-steps of S^T over the head dimension
+    constexpr int NT = HD / 16;  // 16-dimension tiles of O^T
+    const int i = threadIdx.x, fr = i & 15, kg = i >> 4;
     const int nqb = (int)((p.P + 15) / 16);
     const int qb = nqb - 1 - (int)blockIdx.x;  // longest blocks first
     const int h = blockIdx.y;
     const int g = h / (p.n_head / p.n_kv);
     const int64_t t0 = (int64_t)qb * 16;
     const int64_t q_rows = (int64_t)p.n_head * HD;
-    const float scale = 1.0f / sqrtf((float)HD);
-    const float *Kh = p.k_cache + ((int64_t)g * HD + 64 * w) * p.cap;
-    const float *Vh = p.v_cache + ((int64_t)g * HD + 64 * w) * p.cap;
-    const int64_t last_key = p.pos0 + p.P - 1;  // keys past it are not written yet
-
-    // A operand of S: Q[t0 + i%16][h*HD + 64w + 4s + i/16] (zero past the chunk)
-    float qa[NS];
-    {
-        const int64_t t = t0 + c16;
-        const float *qr = p.q + (t < p.P ? t : 0) * q_rows + (int64_t)h * HD + 64 * w;
-#pragma unroll
-        for (int st = 0; st < NS; ++st) qa[st] = t < p.P ? qr[4 * st + q4] : 0.0f;
-    }
-    f4v o[NT];
-#pragma unroll
-    for (int t = 0; t < NT; ++t) o[t] = f4v{0.f, 0.f, 0.f, 0.f};
-    float m[4], l[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        m[r] = -INFINITY;
-        l[r] = 0.0f;
-    }
+    const float scale_l2 = 1.4426950408889634f / sqrtf((float)HD);  // log2(e) / sqrt(head_dim)
     const int64_t tmax = (t0 + 15 < p.P ? t0 + 15 : p.P - 1);
     const int64_t kbeg = (int64_t)blockIdx.z * kch;
     if (kbeg > p.pos0 + tmax) return;  // uniform: no key of this chunk is seen by the block
     const int64_t kend = (p.pos0 + tmax < kbeg + kch - 1 ? p.pos0 + tmax : kbeg + kch - 1);  // last key walked
-    // a tile's operands: K as the B values of the partial S (K[64w + 4s + i/16]
-    // [key k0 + i%16]), V as quads (dimension 64w + e/4, keys k0 + 4(e%4) ..);
-    // keys past last_key read as 0.  The next tile's are in flight while this
-    // one is computed.
-    float kb[NS];
-    float4 vq[NV];
-    auto load_tile = [&](int64_t k0) {
-        const int64_t kk = k0 + c16;
-        const float *kp = Kh + (kk <= last_key ? kk : 0);
+    const int64_t t = t0 + fr, qpos = p.pos0 + t;  // this lane's query and its position
+
+    // B operand of S^T: Q[t][h HD + 32 s + 8 kg + e] (zero past the chunk)
+    ah8 qh[NS], ql[NS];
+    {
+        const float *qr = p.q + (t < p.P ? t : 0) * q_rows + (int64_t)h * HD + 8 * kg;
 #pragma unroll
-        for (int st = 0; st < NS; ++st) kb[st] = kk <= last_key ? kp[(int64_t)(4 * st + q4) * p.cap] : 0.0f;
+        for (int s = 0; s < NS; ++s) {
+            const float4 a = *(const float4 *)(qr + 32 * s), b = *(const float4 *)(qr + 32 * s + 4);
+            const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
-        for (int u = 0; u < NV; ++u) {
-            const int e = i + 64 * u;
-            const int64_t key = k0 + (e & 3) * 4;
-            const float *vr = Vh + (int64_t)(e >> 2) * p.cap;
-            if (key + 3 <= last_key) {
-                vq[u] = *(const float4 *)(vr + key);
-            } else {
-                vq[u].x = key <= last_key ? vr[key] : 0.0f;
-                vq[u].y = key + 1 <= last_key ? vr[key + 1] : 0.0f;
-                vq[u].z = key + 2 <= last_key ? vr[key + 2] : 0.0f;
-                vq[u].w = 0.0f;
+            for (int e = 0; e < 8; ++e) {
+                _Float16 hi, lo;
+                split_f16(t < p.P ? v[e] : 0.0f, hi, lo);
+                qh[s][e] = hi;
+                ql[s][e] = lo;
+            }
+        }
+    }
+    const uint16_t *k16 = p.kv16 + (int64_t)g * ntiles * 32 * 2 * HD + 8 * kg;
+    const uint16_t *v16 = p.kv16 + (int64_t)p.n_kv * ntiles * 32 * 2 * HD + (int64_t)g * HD * ntiles * 64 + 8 * kg;
+    f4v o[NT];
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) o[tt] = f4v{0.f, 0.f, 0.f, 0.f};
+    float m = -INFINITY, l = 0.0f;
+    // the key fragments of a tile (loaded one tile ahead, during the previous
+    // tile's softmax and P V) and its value fragments (loaded before its softmax)
+    ah8 kf[2][NS][2], vf[NT][2];
+    auto load_k = [&](int64_t k0) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const uint16_t *kr = k16 + (k0 + 16 * u + fr) * 2 * HD;
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                kf[u][s][0] = *(const ah8 *)(kr + 64 * s);
+                kf[u][s][1] = *(const ah8 *)(kr + 64 * s + 32);
             }
         }
     };
-    load_tile(kbeg);
-    for (int64_t k0 = kbeg; k0 <= kend; k0 += 16) {
-        const int64_t kk = k0 + c16;
-        f4v sacc = {0.f, 0.f, 0.f, 0.f};
+    load_k(kbeg);
+    for (int64_t k0 = kbeg; k0 <= kend; k0 += 32) {
+        // ---- S^T over keys k0 + 16 u + fr ----
+        f4v sacc[2];
 #pragma unroll
-        for (int st = 0; st < NS; ++st) sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[st], kb[st], sacc, 0, 0, 0);
-        lds_barrier();  // the previous tile's reads of vt, ps and sx are done (LDS only: the prefetch stays in flight)
-        if constexpr (NW > 1) sx[w][i] = sacc;
+        for (int u = 0; u < 2; ++u) {
+            sacc[u] = f4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int u = 0; u < NV; ++u) {
-            const int e = i + 64 * u;
-            float *dst = vt[w] + (e >> 2) * VS + (e & 3) * 4;
-            dst[0] = vq[u].x;
-            dst[1] = vq[u].y;
-            dst[2] = vq[u].z;
-            dst[3] = vq[u].w;
+            for (int s = 0; s < NS; ++s) {
+                sacc[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[u][s][0], qh[s], sacc[u], 0, 0, 0);
+                sacc[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[u][s][0], ql[s], sacc[u], 0, 0, 0);
+                sacc[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[u][s][1], qh[s], sacc[u], 0, 0, 0);
+            }
         }
-        if (k0 + 16 <= kend) load_tile(k0 + 16);  // uniform
-        if constexpr (NW > 1) {
-            lds_barrier();
-            sacc = sx[0][i] + sx[1][i];  // the same sum in both waves
+        {
+            const uint16_t *vt = v16 + (k0 >> 5) * 64;
+#pragma unroll
+            for (int tt = 0; tt < NT; ++tt) {
+                const uint16_t *vr = vt + (int64_t)(16 * tt + fr) * ntiles * 64;
+                vf[tt][0] = *(const ah8 *)vr;
+                vf[tt][1] = *(const ah8 *)(vr + 32);
+            }
         }
-        // ---- online softmax over the tile's rows 4*(i/16) + r ----
-        float pr[4];
+        if (k0 + 32 <= kend) load_k(k0 + 32);  // uniform
+        // ---- online softmax of query fr over keys k0 + 16 u + 4 kg + r ----
+        // scores in log2 units (s / sqrt(head_dim) * log2(e)), so that the
+        // exponentials are exp2; masked keys are -inf, whose exp2 is 0
+        float sv[2][4], mx = -INFINITY;
+        const int rel = (int)(qpos - k0);  // keys k0 + j with j <= rel are seen
+        if (p.pos0 + t0 - k0 >= 31) {      // uniform: no key of the tile is masked for the block
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int64_t row_pos = p.pos0 + t0 + 4 * q4 + r;  // this row's query position
-            const bool ok = kk <= row_pos && kk <= last_key;
-            const float sv = ok ? sacc[r] * scale : -INFINITY;
-            const float mn = fmaxf(m[r], row16_max(sv));
-            const float alpha = mn == -INFINITY ? 1.0f : expf_ref_t(m[r] - mn, tab);
-            const float pv = sv == -INFINITY ? 0.0f : expf_ref_t(sv - mn, tab);
-            l[r] = l[r] * alpha + row16_sum(pv);
-            m[r] = mn;
+            for (int u = 0; u < 2; ++u)
 #pragma unroll
-            for (int t = 0; t < NT; ++t) o[t][r] *= alpha;
-            pr[r] = pv;
+                for (int r = 0; r < 4; ++r) {
+                    sv[u][r] = sacc[u][r] * scale_l2;
+                    mx = fmaxf(mx, sv[u][r]);
+                }
+        } else {
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    sv[u][r] = 16 * u + 4 * kg + r <= rel ? sacc[u][r] * scale_l2 : -INFINITY;
+                    mx = fmaxf(mx, sv[u][r]);
+                }
         }
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float mn = fmaxf(m, mx);
+        const float alpha = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - mn);
+        const float mb = mn == -INFINITY ? 0.0f : mn;
+        ah8 ph, pl;
+        float psum = 0.0f;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) ps[w][(4 * q4 + r) * 16 + c16] = pr[r];
-        lds_barrier();
-        // ---- O += P V: A = P[i%16][4s + i/16], B = V[key 4s + i/16][dim 16t + i%16] ----
+        for (int u = 0; u < 2; ++u)
 #pragma unroll
-        for (int st = 0; st < 4; ++st) {
-            const float a = ps[w][c16 * 16 + 4 * st + q4];
+            for (int r = 0; r < 4; ++r) {
+                const float pv = __builtin_amdgcn_exp2f(sv[u][r] - mb);
+                psum = psum + pv;
+                _Float16 hi, lo;
+                split_f16(pv, hi, lo);
+                ph[4 * u + r] = hi;
+                pl[4 * u + r] = lo;
+            }
+        l = l * alpha + psum;
+        m = mn;
+        // ---- O^T += V^T P^T over dimensions 16 tt + fr ----
 #pragma unroll
-            for (int t = 0; t < NT; ++t)
-                o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vt[w][(16 * t + c16) * VS + 4 * st + q4], o[t], 0, 0, 0);
+        for (int tt = 0; tt < NT; ++tt) {
+            o[tt] = o[tt] * alpha;
+            o[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[tt][0], ph, o[tt], 0, 0, 0);
+            o[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[tt][0], pl, o[tt], 0, 0, 0);
+            o[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[tt][1], ph, o[tt], 0, 0, 0);
         }
     }
-    // ---- partials of the block's rows inside the chunk: ws[c][t][h] = {m, l, O[HD]} ----
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int64_t t = t0 + 4 * q4 + r;
-        if (t >= p.P) continue;
+    // the query's sum over its four lanes; partials ws[c][t][h] = {m, l, O[HD]}
+    l = l + __shfl_xor(l, 16);
+    l = l + __shfl_xor(l, 32);
+    if (t < p.P) {
         float *rec = p.ws + (((int64_t)blockIdx.z * p.P + t) * p.n_head + h) * (HD + 2);
-        if (w == 0 && c16 == 0) {
-            rec[0] = m[r];
-            rec[1] = l[r];
+        if (kg == 0) {
+            rec[0] = m;
+            rec[1] = l;
         }
 #pragma unroll
-        for (int tt = 0; tt < NT; ++tt) rec[2 + 64 * w + 16 * tt + c16] = o[tt][r];
+        for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) rec[2 + 16 * tt + 4 * kg + r] = o[tt][r];
     }
 }
 
-// out[t][h] = (sum_c O_c e^(m_c - m)) / (sum_c l_c e^(m_c - m) + 1e-12), m = max_c m_c,
+// out[t][h] = (sum_c O_c 2^(m_c - m)) / (sum_c l_c 2^(m_c - m) + 1e-12), m = max_c m_c
+// (the chunks' maxima are in log2 units),
 // over the chunks that hold keys at or before the row's position.  One
 // workgroup per (token, head), one thread per dimension.
 __global__ __launch_bounds__(128) void prefill_attn_merge_kernel(PrefillAttnParams p, int64_t kch) {
     const int64_t t = blockIdx.x;
     const int h = blockIdx.y, d = threadIdx.x, HD = p.head_dim;
-    const int nc = (int)((p.pos0 + t) / kch) + 1;
+    const int nc = (int)((p.pos0 + t) / kch) + 1;  // <= PREFILL_ATTN_CHUNKS
     const int64_t rs = (int64_t)p.n_head * (HD + 2);
     const float *rec = p.ws + (t * p.n_head + h) * (HD + 2);
     const int64_t cstride = p.P * rs;
-    float mx = -INFINITY;
-    for (int c = 0; c < nc; ++c) mx = fmaxf(mx, rec[c * cstride]);
-    float l = 0.0f, o = 0.0f;
-    for (int c = 0; c < nc; ++c) {
-        const float *rc = rec + c * cstride;
-        const float e = expf_ref(rc[0] - mx);
-        l = l + rc[1] * e;
-        if (d < HD) o = o + rc[2 + d] * e;
+    // every chunk's record read at once (one round trip)
+    float mc[PREFILL_ATTN_CHUNKS], lc[PREFILL_ATTN_CHUNKS], oc[PREFILL_ATTN_CHUNKS];
+#pragma unroll
+    for (int c = 0; c < PREFILL_ATTN_CHUNKS; ++c) {
+        const float *rc = rec + (c < nc ? c : 0) * cstride;
+        mc[c] = rc[0];
+        lc[c] = rc[1];
+        oc[c] = d < HD ? rc[2 + d] : 0.0f;
     }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < PREFILL_ATTN_CHUNKS; ++c)
+        if (c < nc) mx = fmaxf(mx, mc[c]);
+    float l = 0.0f, o = 0.0f;
+#pragma unroll
+    for (int c = 0; c < PREFILL_ATTN_CHUNKS; ++c)
+        if (c < nc) {
+            const float e = exp2f(mc[c] - mx);
+            l = l + lc[c] * e;
+            o = o + oc[c] * e;
+        }
     if (d < HD) p.out[t * (int64_t)p.n_head * HD + (int64_t)h * HD + d] = o * (1.0f / (l + 1e-12f));
 }
 
@@ -269,27 +329,35 @@ int64_t prefill_attn_ws_floats(int64_t P, int64_t n_head, int64_t head_dim) {
     return (int64_t)PREFILL_ATTN_CHUNKS * P * n_head * (head_dim + 2);
 }
 
+int64_t prefill_kv16_halves(int64_t keys, int64_t n_kv, int64_t head_dim) {
+    return 4 * n_kv * ((keys + 31) / 32 * 32) * head_dim;
+}
+
 int launch_prefill_attention(const PrefillAttnParams &p, hipStream_t s) {
     if (p.P <= 0 || !p.q || !p.k_cache || !p.v_cache || !p.out || p.n_kv <= 0 || p.n_head % p.n_kv ||
         p.pos0 < 0 || p.pos0 + p.P > p.cap || p.P > 65535)
         return set_error(GAJE_ERR_INVALID_ARG, "prefill attention: bad arguments");
-    if (p.cap % 4) return set_error(GAJE_ERR_UNSUPPORTED, "prefill attention: KV capacity %% 4 != 0");
-    if (p.head_dim == 64 || p.head_dim == 128) {
-        if (!p.ws) return set_error(GAJE_ERR_INVALID_ARG, "prefill attention: no workspace");
-        // key chunks of at least 128 keys, at most PREFILL_ATTN_CHUNKS of them
-        const int64_t keys = p.pos0 + p.P;
-        int64_t kch = (keys + PREFILL_ATTN_CHUNKS - 1) / PREFILL_ATTN_CHUNKS;
-        kch = kch < 128 ? 128 : (kch + 15) / 16 * 16;
-        const int64_t nch = (keys + kch - 1) / kch;
-        const dim3 grid((unsigned)((p.P + 15) / 16), (unsigned)p.n_head, (unsigned)nch);
-        if (p.head_dim == 64) hipLaunchKernelGGL(prefill_attn_mfma_kernel<64>, grid, dim3(64), 0, s, p, kch);
-        else hipLaunchKernelGGL(prefill_attn_mfma_kernel<128>, grid, dim3(128), 0, s, p, kch);
-        GAJE_HIP_CHECK(hipGetLastError());
-        hipLaunchKernelGGL(prefill_attn_merge_kernel, dim3((unsigned)p.P, (unsigned)p.n_head), dim3(128), 0, s, p, kch);
-        GAJE_HIP_CHECK(hipGetLastError());
-        return GAJE_OK;
-    }
-    return set_error(GAJE_ERR_UNSUPPORTED, "prefill attention: head_dim %d (64 or 128 only)", p.head_dim);
+    if (p.head_dim != 64 && p.head_dim != 128)
+        return set_error(GAJE_ERR_UNSUPPORTED, "prefill attention: head_dim %d (64 or 128 only)", p.head_dim);
+    const int64_t keys = p.pos0 + p.P;
+    if (!p.ws || !p.kv16 || p.kv16_keys < keys)
+        return set_error(GAJE_ERR_INVALID_ARG, "prefill attention: workspace too small");
+    // the converted keys and values, [0, keys) padded to whole 32-key tiles
+    const int ntiles = (int)((keys + 31) / 32);
+    hipLaunchKernelGGL(prefill_kv16_kernel, dim3((unsigned)ntiles, (unsigned)p.n_kv, (unsigned)(p.head_dim / 32)), dim3(256), 0,
+                       s, p, ntiles);
+    GAJE_HIP_CHECK(hipGetLastError());
+    // key chunks of at least 128 keys (whole tiles), at most PREFILL_ATTN_CHUNKS of them
+    int64_t kch = (keys + PREFILL_ATTN_CHUNKS - 1) / PREFILL_ATTN_CHUNKS;
+    kch = kch < 128 ? 128 : (kch + 31) / 32 * 32;
+    const int64_t nch = (keys + kch - 1) / kch;
+    const dim3 grid((unsigned)((p.P + 15) / 16), (unsigned)p.n_head, (unsigned)nch);
+    if (p.head_dim == 64) hipLaunchKernelGGL(prefill_attn_f16_kernel<64>, grid, dim3(64), 0, s, p, kch, ntiles);
+    else hipLaunchKernelGGL(prefill_attn_f16_kernel<128>, grid, dim3(64), 0, s, p, kch, ntiles);
+    GAJE_HIP_CHECK(hipGetLastError());
+    hipLaunchKernelGGL(prefill_attn_merge_kernel, dim3((unsigned)p.P, (unsigned)p.n_head), dim3(128), 0, s, p, kch);
+    GAJE_HIP_CHECK(hipGetLastError());
+    return GAJE_OK;
 }
 
 }  // namespace gaje
