@@ -114,6 +114,65 @@ __global__ __launch_bounds__(SPLIT_THREADS) void split_rows_kernel(SplitParams p
             bad_b |= isnan(o.x) | isnan(o.y) | isnan(o.z) | isnan(o.w);
             *(float4 *)(xs + 4 * i) = o;
         }
+    } else if (p.part) {
+        // the deferred split-K reduce of the producing product, in
+        // gemm_reduce_kernel's order, its NaN guards included
+        float *yr = const_cast<float *>(p.x) + m * p.ldx;  // x is the product's output here
+        const int64_t pstride = p.M * p.K;
+        int bad_ya = 0, bad_yb = 0;
+        for (int64_t i = tid; i < K4; i += SPLIT_THREADS) {
+            // bias and residual as whole float4s, read beside the partials
+            float bj[4] = {0.0f, 0.0f, 0.0f, 0.0f}, rj[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (4 * i + 4 <= p.bias_len) {
+                const float4 b = *(const float4 *)(p.bias + 4 * i);
+                bj[0] = b.x;
+                bj[1] = b.y;
+                bj[2] = b.z;
+                bj[3] = b.w;
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (4 * i + j < p.bias_len) bj[j] = p.bias[4 * i + j];
+            }
+            if (p.resid) {
+                const float4 r = *(const float4 *)(p.resid + m * p.ldx + 4 * i);
+                rj[0] = r.x;
+                rj[1] = r.y;
+                rj[2] = r.z;
+                rj[3] = r.w;
+            }
+            const float *pp = p.part + m * p.K + 4 * i;
+            float4 v = *(const float4 *)pp;
+            // eight partials in flight at a time (clamped reads, no branch),
+            // added in split order
+            for (int z0 = 1; z0 < p.nsplit; z0 += 8) {
+                float4 q[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) q[j] = *(const float4 *)(pp + min(z0 + j, p.nsplit - 1) * pstride);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const bool ok = z0 + j < p.nsplit;
+                    v.x = ok ? v.x + q[j].x : v.x;
+                    v.y = ok ? v.y + q[j].y : v.y;
+                    v.z = ok ? v.z + q[j].z : v.z;
+                    v.w = ok ? v.w + q[j].w : v.w;
+                }
+            }
+            float a[4] = {flush_small(v.x), flush_small(v.y), flush_small(v.z), flush_small(v.w)};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (4 * i + j < p.bias_len) a[j] = a[j] + bj[j];
+                bad_ya |= isnan(a[j]);
+                if (p.resid) a[j] = rj[j] + a[j];
+                bad_yb |= isnan(a[j]);
+            }
+            const float4 o = {a[0], a[1], a[2], a[3]};
+            *(float4 *)(yr + 4 * i) = o;
+            bad_a |= isnan(o.x) | isnan(o.y) | isnan(o.z) | isnan(o.w);
+            *(float4 *)(xs + 4 * i) = o;
+        }
+        if (__syncthreads_or(bad_ya) && tid == 0) nan_flag(p.st, p.y_layer, p.st_ya);
+        if (__syncthreads_or(bad_yb) && tid == 0) nan_flag(p.st, p.y_layer, p.st_yb);
     } else {
         for (int64_t i = tid; i < K4; i += SPLIT_THREADS) {
             const float4 v = *(const float4 *)(xr + 4 * i);
@@ -467,7 +526,13 @@ __global__ void gemm_reduce_kernel(GemmQ4Params p, int S) {
     for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
         const int64_t m = t / p.N, n = t - m * p.N;
         float v = p.part[t];
-        for (int z = 1; z < S; ++z) v += p.part[(int64_t)z * total + t];
+        for (int z0 = 1; z0 < S; z0 += 8) {  // eight partials in flight (clamped reads), added in split order
+            float q[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) q[j] = p.part[(int64_t)min(z0 + j, S - 1) * total + t];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v = z0 + j < S ? v + q[j] : v;
+        }
         v = flush_small(v);
         if (n < p.bias_len) v = v + p.bias[n];
         if (isnan(v)) nan_flag(p.st, p.layer, p.st_a);
@@ -984,6 +1049,9 @@ int launch_split_rows(const SplitParams &p, hipStream_t s) {
     if (lds + 1024 > max_lds_per_block())
         return set_error(GAJE_ERR_UNSUPPORTED, "split rows: K = %lld does not fit LDS", (long long)p.K);
     if (p.up && p.norm_w) return set_error(GAJE_ERR_INVALID_ARG, "split rows: norm and swiglu prologues are exclusive");
+    if (p.part && (p.up || p.rows || p.nsplit < 1 || p.ldx != p.K || (p.resid && p.resid != p.x) || p.bias_len < 0 ||
+                   (p.bias_len > 0 && !p.bias) || ((uintptr_t)p.part & 15)))
+        return set_error(GAJE_ERR_INVALID_ARG, "split rows: bad split-K prologue");
     if (p.up) hipLaunchKernelGGL(split_rows_kernel<SPLIT_SWIGLU>, dim3((unsigned)p.M), dim3(SPLIT_THREADS), lds, s, p);
     else if (p.norm_w) hipLaunchKernelGGL(split_rows_kernel<SPLIT_NORM>, dim3((unsigned)p.M), dim3(SPLIT_THREADS), lds, s, p);
     else hipLaunchKernelGGL(split_rows_kernel<SPLIT_PLAIN>, dim3((unsigned)p.M), dim3(SPLIT_THREADS), lds, s, p);
@@ -1114,7 +1182,7 @@ int launch_gemm_q4_bs(const GemmBsParams &p, const GemmBsPlan &pl, hipStream_t s
         break;
     }
     GAJE_HIP_CHECK(hipGetLastError());
-    if (pl.splits > 1) {
+    if (pl.splits > 1 && !p.defer_reduce) {
         GemmQ4Params r{};
         r.bias = p.bias;
         r.bias_len = p.bias_len;

@@ -213,6 +213,17 @@ struct SplitParams {
     // 2^-5 * sum_{k in b} x'[k] as an f16 pair (zero past K/32).
     uint16_t *sh, *sl;
     int64_t ldsum;
+    // Split-K prologue (without up or rows): the input rows are first formed
+    // from the partials of a block-scaled product whose reduce was deferred,
+    // as gemm_reduce_kernel would: x = resid + (flush_small(sum_z part[z]) +
+    // bias), written to x (in place over resid when they alias) before the split.
+    const float *part;       // [nsplit][M][K], or null
+    int32_t nsplit;
+    const float *bias;
+    int64_t bias_len;
+    const float *resid;      // [M][ldx] or null
+    int32_t st_ya, st_yb;    // the product's NaN guards (after the bias, after resid)
+    int32_t y_layer;         // the product's layer, for those guards
 };
 int launch_split_rows(const SplitParams &p, hipStream_t s);
 // Per packed Q4_0 row: the exponent that scales its largest |d| into [2^14, 2^15).
@@ -287,6 +298,7 @@ struct GemmBsParams {
     DevState *st;            // NaN guards as in GemmQ4Params
     int32_t layer;
     int32_t st_a, st_b;
+    int32_t defer_reduce;    // splits > 1: leave the partials for a split pass's prologue
 };
 struct GemmBsPlan {
     int waves;               // 32-row wave tiles per workgroup (2, 4 or 8)

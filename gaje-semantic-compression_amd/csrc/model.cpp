@@ -1068,8 +1068,32 @@ SplitParams prefill_split(const gaje_hip_model *m, const float *x, int64_t ldx, 
 }
 
 // Y[P][D.N] = rows of the current activation planes x D (+ bias) (+ resid).
+// A deferred split-K reduce: the product's partials wait in pf.part for the
+// next split pass, which forms the rows itself (SplitParams' prologue).
+struct PendingReduce {
+    int32_t nsplit = 0;  // 0: none
+    const float *bias = nullptr;
+    int64_t bias_len = 0;
+    bool resid = false;
+    int32_t st_a = ST_NONE, st_b = ST_NONE, layer = 0;
+};
+
+void take_pending(const gaje_hip_model *m, PendingReduce &pr, SplitParams &sp) {
+    if (!pr.nsplit) return;
+    sp.part = m->pf.part;
+    sp.nsplit = pr.nsplit;
+    sp.bias = pr.bias;
+    sp.bias_len = pr.bias_len;
+    sp.resid = pr.resid ? sp.x : nullptr;
+    sp.st_ya = pr.st_a;
+    sp.st_yb = pr.st_b;
+    sp.y_layer = pr.layer;
+    pr = PendingReduce();
+}
+
+// With `pending`, a split-K product leaves its reduce to the next split pass.
 int prefill_gemm(gaje_hip_model *m, const DevLinear &D, int64_t P, float *y, const float *resid, int32_t layer,
-                 int32_t st_a, int32_t st_b) {
+                 int32_t st_a, int32_t st_b, PendingReduce *pending = nullptr) {
     const auto &f = m->pf;
     const GemmBsPlan pl = plan_gemm_q4_bs(P, D.N, D.K);
     if (pl.part_floats > f.part_floats) return set_error(GAJE_ERR_INVALID_ARG, "prefill: split-K buffer too small");
@@ -1098,12 +1122,25 @@ int prefill_gemm(gaje_hip_model *m, const DevLinear &D, int64_t P, float *y, con
     p.layer = layer;
     p.st_a = st_a;
     p.st_b = st_b;
+    if (pending && pl.splits > 1 && (!resid || resid == y)) {
+        p.defer_reduce = 1;
+        pending->nsplit = pl.splits;
+        pending->bias = D.bias;
+        pending->bias_len = D.bias_len;
+        pending->resid = resid != nullptr;
+        pending->st_a = st_a;
+        pending->st_b = st_b;
+        pending->layer = layer;
+    }
     return launch_gemm_q4_bs(p, pl, m->stream);
 }
 
 // One block (RustGenomicBlock::forward_core, block/forward.rs:10-157) for the
 // P tokens of the current chunk at positions pos..pos+P-1, in place on pf.H.
-int prefill_layer(gaje_hip_model *m, int64_t l, int64_t pos, int64_t P) {
+// `pending`: the previous block's down product may leave its split-K reduce
+// to this block's first split pass, and this block's may leave its own to the
+// next block's (never the last block's: its rows go to the head).
+int prefill_layer(gaje_hip_model *m, int64_t l, int64_t pos, int64_t P, PendingReduce &pending) {
     Layer &Ly = m->layers[l];
     auto &f = m->pf;
     hipStream_t s = m->stream;
@@ -1111,6 +1148,7 @@ int prefill_layer(gaje_hip_model *m, int64_t l, int64_t pos, int64_t P) {
     const size_t layer_kv = (size_t)m->n_kv * m->cap * m->hd;
 
     SplitParams sp = prefill_split(m, f.H, m->n_embd, P, m->n_embd);
+    take_pending(m, pending, sp);
     sp.norm_w = Ly.attn_norm;
     sp.layer = li;
     sp.st_a = ST_INPUT;
@@ -1153,9 +1191,10 @@ int prefill_layer(gaje_hip_model *m, int64_t l, int64_t pos, int64_t P) {
 
     sp = prefill_split(m, f.ATT, m->q_rows, P, m->q_rows);
     GAJE_TRY(launch_split_rows(sp, s));
-    GAJE_TRY(prefill_gemm(m, Ly.o, P, f.H, f.H, li, ST_NONE, ST_NONE));
+    GAJE_TRY(prefill_gemm(m, Ly.o, P, f.H, f.H, li, ST_NONE, ST_NONE, &pending));
 
     sp = prefill_split(m, f.H, m->n_embd, P, m->n_embd);
+    take_pending(m, pending, sp);
     sp.norm_w = Ly.ffn_norm;
     GAJE_TRY(launch_split_rows(sp, s));
     GAJE_TRY(prefill_gemm(m, Ly.gate_up, P, f.GU, nullptr, li, ST_NONE, ST_NONE));
@@ -1167,9 +1206,11 @@ int prefill_layer(gaje_hip_model *m, int64_t l, int64_t pos, int64_t P) {
     sp.st_a = ST_UP;
     sp.st_b = ST_FFN_OUT;
     GAJE_TRY(launch_split_rows(sp, s));
-    GAJE_TRY(prefill_gemm(m, Ly.down, P, f.H, f.H, li, ST_PROJ_FFN, ST_FINAL));
+    const bool kwta = m->block_kwta_ratio > 0.0f && m->block_kwta_ratio < 1.0f;
+    GAJE_TRY(prefill_gemm(m, Ly.down, P, f.H, f.H, li, ST_PROJ_FFN, ST_FINAL,
+                          l + 1 < m->n_layers && !kwta ? &pending : nullptr));
 
-    if (m->block_kwta_ratio > 0.0f && m->block_kwta_ratio < 1.0f) {
+    if (kwta) {
         const int64_t k = kwta_k(m->n_embd, m->block_kwta_ratio);
         for (int64_t t = 0; t < P; ++t) GAJE_TRY(launch_kwta(f.H + t * m->n_embd, m->n_embd, k, m->st, s));
     }
@@ -1233,7 +1274,8 @@ extern "C" int gaje_hip_prefill_mfma(gaje_hip_model *m, const uint32_t *ids, int
         ep.K = m->n_embd;
         ep.h = f.H;
         GAJE_TRY(launch_embed_rows(ep, f.ids, P, s));
-        for (int64_t l = 0; l < m->n_layers; ++l) GAJE_TRY(prefill_layer(m, l, pos0 + c0, P));
+        PendingReduce pending;
+        for (int64_t l = 0; l < m->n_layers; ++l) GAJE_TRY(prefill_layer(m, l, pos0 + c0, P, pending));
         last_rows = P;
         // the ids copy reads host memory the caller owns only for this call
         GAJE_HIP_CHECK(hipStreamSynchronize(s));
