@@ -244,7 +244,8 @@ size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 // the two block-sum planes, split-K partials.
 struct GemmWorkspace {
     int *ex;
-    uint16_t *xh, *sh, *sl, *mins;
+    uint16_t *xh, *sh, *sl, *mins, *wf;
+    float *wsc;
     int64_t plane_rows, ldsum;
     float *part;
     size_t bytes;
@@ -267,6 +268,10 @@ GemmWorkspace gemm_workspace(char *base, int64_t m, int64_t n, int64_t k, const 
     off = align256(off + (size_t)pl.part_floats * 4);
     w.mins = (uint16_t *)(base + off);  // [n][ldsum]: the weight rows' block mins
     off = align256(off + (size_t)(n * w.ldsum) * 2);
+    w.wf = (uint16_t *)(base + off);    // the weight rows' code fragments and scales
+    off = align256(off + (size_t)q4_frag_halves(n, k) * 2);
+    w.wsc = (float *)(base + off);
+    off = align256(off + (size_t)q4_frag_scale_floats(n, k) * 4);
     w.bytes = off;
     return w;
 }
@@ -306,8 +311,11 @@ extern "C" int gaje_hip_q4_0_gemm_mfma(const void *packed, const float *X, const
     sp.ldsum = w.ldsum;
     GAJE_TRY(launch_split_rows(sp, s));
     GAJE_TRY(launch_q4_mins((const uint8_t *)packed, n, k, w.mins, w.ldsum, s));
+    GAJE_TRY(launch_q4_frags((const uint8_t *)packed, n, k, w.wf, w.wsc, s));
     GemmBsParams p{};
-    p.w = (const uint8_t *)packed;
+    p.wf = w.wf;
+    p.wsc = w.wsc;
+    p.nbp4 = q4_frag_nbp4(k);
     p.mins = w.mins;
     p.ldm = w.ldsum;
     p.xh = w.xh;

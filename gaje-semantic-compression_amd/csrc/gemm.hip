@@ -41,6 +41,19 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 
 enum SplitPrologue { SPLIT_PLAIN = 0, SPLIT_NORM = 1, SPLIT_SWIGLU = 2 };
 
+// swiglu_balanced (activation.rs:40-49: the gate clamped to [-64, 64], the
+// sigmoid from exp(-|g|), silu(g) * u) for the MFMA paths, which are held to
+// fp32 accuracy rather than the reference's bits: the exponential on the
+// hardware exp2 and the quotient on the hardware reciprocal (each ~1 ulp),
+// without branches.
+__device__ __forceinline__ float swiglu_fast(float g, float u) {
+    const float gs = fminf(fmaxf(g, -64.0f), 64.0f);
+    const float ex = __builtin_amdgcn_exp2f(-fabsf(gs) * 1.4426950408889634f);
+    const float r = __builtin_amdgcn_rcpf(1.0f + ex);
+    const float sig = gs >= 0.0f ? r : ex * r;
+    return (g * sig) * u;
+}
+
 constexpr int GM_NT = 128;   // weight rows per workgroup
 constexpr int GM_ROW = 40;   // halves per LDS tile row (32 + 8 pad)
 
@@ -107,10 +120,10 @@ __global__ __launch_bounds__(SPLIT_THREADS) void split_rows_kernel(SplitParams p
             const float4 g = *(const float4 *)(xr + 4 * i), u = *(const float4 *)(ur + 4 * i);
             bad_a |= isnan(u.x) | isnan(u.y) | isnan(u.z) | isnan(u.w);
             float4 o;
-            o.x = swiglu1(g.x, u.x);
-            o.y = swiglu1(g.y, u.y);
-            o.z = swiglu1(g.z, u.z);
-            o.w = swiglu1(g.w, u.w);
+            o.x = swiglu_fast(g.x, u.x);
+            o.y = swiglu_fast(g.y, u.y);
+            o.z = swiglu_fast(g.z, u.z);
+            o.w = swiglu_fast(g.w, u.w);
             bad_b |= isnan(o.x) | isnan(o.y) | isnan(o.z) | isnan(o.w);
             *(float4 *)(xs + 4 * i) = o;
         }
@@ -565,8 +578,12 @@ size_t gemm_lds() { return (size_t)((GA ? 0 : 4 * MT * GM_ROW) + 4 * GM_NT * GM_
 // each activation block permuted to match: position 8 kg + t holds element
 // 2 kg + 8 (t & 3) + (t >> 2), so the 8 halves of MFMA lane group kg are the
 // 8 codes of that word pair.  A code byte becomes f16 1024 + q by v_perm
-// against 0x64 bytes, then q by a packed f16 subtraction; the high nibbles are
-// used in place (16 q, with the block's scale divided by 16).
+// against 0x64 bytes, then q by a packed f16 subtraction.  This expansion runs
+// once per weight matrix (q4_frag_kernel): the products read the codes as f16
+// fragments, [16-row tile][block][64 lanes][8 halves] (1 KiB per tile and
+// block, in the MFMA's lane order), and the scales as fp32 [tile][block][16],
+// both zero past the last row and block: four times the packed bytes, traded
+// for no expansion work in the product's loop.
 //
 // Tiling (gfx950, wave64).  A workgroup is W waves of 32 activation rows and
 // 9 tiles of 16 weight rows (144); every wave holds 2 x 9 accumulators of
@@ -581,9 +598,9 @@ size_t gemm_lds() { return (size_t)((GA ? 0 : 4 * MT * GM_ROW) + 4 * GM_NT * GM_
 //   (128 bytes per row); each wave streams its own rows into a private LDS
 //   ring of three blocks with global_load_lds, two blocks ahead, XOR-swizzled
 //   by 16-byte chunk so that fragment reads are conflict-free.
-// - Weights: the raw 80-byte groups of the tile's rows are copied into LDS one
-//   group ahead; each pair of blocks' code fragments and scales is expanded
-//   into LDS one pair ahead by all waves together (one barrier per pair).
+// - Weights: each pair of blocks' code fragments and scales is copied into LDS
+//   by all waves together, two pairs ahead (three buffers, one barrier per
+//   pair).
 // - No other vector memory access is made in the main loop, so the explicit
 //   vmcnt waits are exact.
 // - The grid is ordered so that the workgroups of one activation tile and
@@ -596,31 +613,28 @@ constexpr int BS_WR = 32;                       // activation rows per wave
 constexpr int BS_ABLK = BS_WR * 128;            // one block of a wave's rows (hi | lo)
 constexpr int BS_ADMA = BS_ABLK / 1024;         // its copy instructions
 constexpr int BS_RING = 3;                      // ring slots per wave
-constexpr int BS_RAWC = BS_NT * 5;              // 16-byte chunks of one raw group (144 rows x 80 B)
-constexpr int BS_RAW = 768 * 16;                // one raw group buffer (720 chunks, padded to 12 copies)
 constexpr int BS_BF = BS_J * 1024;              // one block's code fragments
-constexpr int BS_SC = BS_NT * 4;                // one block's scales
+constexpr int BS_NB = 3;                        // weight buffers (intervals)
 
-template <int W>
+// W waves of 32 rows, BPI blocks per interval between barriers; a weight
+// buffer holds an interval's BPI x 9 fragments, then its BPI x 144 scales
+// (one 1 KiB copy per block).
+template <int W, int BPI>
 struct BsShape {
-    static constexpr int RAWW = (768 + 64 * W - 1) / (64 * W);  // raw copy instructions per wave per group
-    static constexpr int CVW = (2 * BS_J + W - 1) / W;          // (block, tile) fragments each wave expands per pair
-    // ring, two raw groups, fragments and scales of two block pairs
-    static constexpr size_t LDS = (size_t)W * BS_RING * BS_ABLK + 2 * BS_RAW + 4 * BS_BF + 4 * BS_SC;
+    static constexpr int BCOPY = (BS_J + 1) * BPI;             // weight copy instructions per interval
+    static constexpr int BDMA = (BCOPY + W - 1) / W;           // of them per wave
+    static constexpr int PB = BPI * (BS_BF + 1024);            // bytes per weight buffer
+    static constexpr size_t LDS = (size_t)W * BS_RING * BS_ABLK + BS_NB * PB;
+    static constexpr int WG_PER_CU = BPI == 1 ? 2 : 1;
 };
-template <int W>
-constexpr size_t bs_lds() { return BsShape<W>::LDS; }
+template <int W, int BPI>
+constexpr size_t bs_lds() { return BsShape<W, BPI>::LDS; }
 
 struct BsGrid {
     int32_t ntiles, splits, kb_per, units, total;  // units: 16-row weight units ceil(N / 16)
 };
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-
-template <bool B>
-struct BsRole {
-    static constexpr bool value = B;
-};
 
 // f16 1024 + byte (bytes 2 s, 2 s + 1 of t), minus 1024: the two codes as f16.
 template <int S>
@@ -631,11 +645,11 @@ __device__ __forceinline__ uint32_t code_pair(uint32_t t) {
     return __builtin_bit_cast(uint32_t, r);
 }
 
-template <int W>
-__global__ __launch_bounds__(64 * W, 1) void gemm_q4_bs_kernel(GemmBsParams p, BsGrid gd) {
-    using S = BsShape<W>;
-    constexpr int RAWW = S::RAWW, CVW = S::CVW;
-    static_assert(4 * BS_ADMA + RAWW < 64 && S::LDS <= 163840 && W <= 12, "limits");
+template <int W, int BPI>
+__global__ __launch_bounds__(64 * W, (BsShape<W, BPI>::WG_PER_CU)) void gemm_q4_bs_kernel(GemmBsParams p, BsGrid gd) {
+    using S = BsShape<W, BPI>;
+    constexpr int BDMA = S::BDMA, BCOPY = S::BCOPY, PB = S::PB;
+    static_assert(4 * BS_ADMA + 3 * BDMA < 64 && S::LDS * S::WG_PER_CU <= 163840, "limits");
     extern __shared__ __align__(16) uint8_t bs_mem[];
     // w through readfirstlane: the copies' bases must be provably wave-uniform (SGPRs)
     const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -653,23 +667,11 @@ __global__ __launch_bounds__(64 * W, 1) void gemm_q4_bs_kernel(GemmBsParams p, B
     const int64_t n0 = 16 * (int64_t)(t * ubase + min(t, urem));
     const int64_t m0 = (int64_t)mt * (BS_WR * W) + BS_WR * w;  // this wave's first activation row
     const int b0 = z * gd.kb_per, b1 = min(p.nb, b0 + gd.kb_per);
-    const int nblk = b1 - b0, ngr = (nblk + 3) >> 2;
-    const int G = (p.nb + 3) >> 2;
-    const int64_t wstride = (int64_t)G * 80;
+    const int nblk = b1 - b0, npr = (nblk + BPI - 1) / BPI;  // blocks, intervals of this split
+    const int64_t t16 = n0 >> 4;                        // the tile's first 16-row fragment tile
 
     uint8_t *ring = bs_mem + w * (BS_RING * BS_ABLK);
-    uint8_t *raw = bs_mem + W * BS_RING * BS_ABLK;  // [2 groups][BS_RAW]
-    uint8_t *bfr = raw + 2 * BS_RAW;                // [2 pairs][2 blocks][BS_BF]
-    float *sc = (float *)(bfr + 4 * BS_BF);         // [2 pairs][2 blocks][BS_NT]
-
-    // byte offset of the weight row of tile column c (dummy columns past nj
-    // repeat the last real one; the launcher checks that it fits 32 bits)
-    auto wrow_off = [&](int c) -> uint32_t {
-        if (c >= 16 * nj) c = 16 * nj - 1;
-        int64_t n = n0 + c;
-        if (n >= p.N) n = p.N - 1;
-        return (uint32_t)(n * wstride);
-    };
+    uint8_t *bfr = bs_mem + W * BS_RING * BS_ABLK;  // [3][PB]: fragments, then scales (block e at 144 e floats)
 
     // activation copies: per block a wave copies its 32 rows x 128 bytes (the
     // block's hi | lo halves, one cache line per row).  Instruction q takes rows
@@ -689,59 +691,43 @@ __global__ __launch_bounds__(64 * W, 1) void gemm_q4_bs_kernel(GemmBsParams p, B
         for (int q = 0; q < BS_ADMA; ++q) lds_dma16_so(base + q * 16 * p.ldh, aoffs[q & 1], dst + q * 1024);
     };
 
-    // raw group copies: the tile's 144 weight rows x the 80 bytes of group g,
-    // rows 80 bytes apart (chunk c = 5 row + part), as 12 copy instructions of
-    // 64 chunks: copy i takes chunks 64 i + lane (past the 720 real ones: the
-    // last again, into the padding).  Wave w issues copies w, w + W, ..; in
-    // place of one past copy 11 it issues copy w again (same bytes, same place),
-    // so that every wave issues RAWW copies and no lane branches: the compiler
-    // would otherwise sink the fmas of a block below its later MFMAs.
-    uint32_t rsrc[RAWW], rdst[RAWW];
+    // weight copies of interval pp into buffer pb: copy ci < 9 BPI takes the
+    // 1 KiB fragment of (block e = ci / 9, tile j = ci % 9), as it lies in
+    // global memory; the BPI copies after them take the interval's BPI x 9 x
+    // 16 scales, lane l of copy s reading chunk c = min(64 s + l, 36 BPI - 1)
+    // of four (block c / 36, tile (c % 36) / 4, quarter c % 4).  Tiles past
+    // nj - 1 repeat the last one.  Wave w issues copies w, w + W, ..; in place
+    // of one past the last it issues copy w again (same bytes, same place), so
+    // that every wave issues BDMA copies and no lane branches: the compiler
+    // would otherwise sink the fmas of a block below its later MFMAs.  Offsets
+    // fit 32 bits (checked by the launcher).
+    int cidx[BDMA];
+    uint32_t coff[BDMA], cdst[BDMA];
 #pragma unroll
-    for (int r = 0; r < RAWW; ++r) {
-        const int ci = w + W * r < 12 ? w + W * r : w;
-        const int c = min(64 * ci + lane, BS_RAWC - 1);
-        rsrc[r] = wrow_off(c / 5) + 16 * (c % 5);
-        rdst[r] = (uint32_t)ci * 1024;
-    }
-    auto dma_raw = [&](int h, int buf) {
-        const uint8_t *gbase = p.w + ((int64_t)(b0 >> 2) + min(h, ngr - 1)) * 80;
-        const uint32_t base = lds_addr(raw + buf * BS_RAW);
-#pragma unroll
-        for (int r = 0; r < RAWW; ++r) lds_dma16_so(gbase, rsrc[r], base + rdst[r]);
-    };
-
-    // expand block pair pp (blocks 2 pp, 2 pp + 1 of the split) from its raw
-    // group into fragment buffer pb: the 18 (block, tile) fragments go to the
-    // waves in turn, x = w, w + W, .. (past 17, or past tile nj - 1, the last
-    // one again: the same bytes another wave writes, so that no wave branches).
-    // Block u of a group is nibble u & 1 of code words u >> 1 and 2 + (u >> 1).
-    auto expand = [&](int pp, int pb) {
-        const uint8_t *rg = raw + ((pp >> 1) & 1) * BS_RAW;
-        const int hu = 2 * (pp & 1);  // the pair's first block within its group
-        // every read first (one LDS round trip), then the conversions and writes
-        vu4 q[CVW];
-        uint32_t sw[CVW];
-        int ee[CVW], jj[CVW];
-#pragma unroll
-        for (int r = 0; r < CVW; ++r) {
-            const int x = min(w + W * r, 2 * BS_J - 1);
-            ee[r] = x >= BS_J ? 1 : 0;
-            jj[r] = min(x - BS_J * ee[r], nj - 1);
-            const uint8_t *rrow = rg + (16 * jj[r] + fr) * 80;
-            q[r] = *(const vu4 *)(rrow + 16 * kg);
-            sw[r] = *(const uint32_t *)(rrow + 64 + 4 * (hu + ee[r]));
+    for (int r = 0; r < BDMA; ++r) {
+        const int ci = w + W * r < BCOPY ? w + W * r : w;
+        cidx[r] = ci;
+        if (ci < BPI * BS_J) {
+            const int e = ci / BS_J, j = min(ci % BS_J, nj - 1);
+            coff[r] = (uint32_t)(((t16 + j) * p.nbp4 + e) * 1024 + lane * 16);
+            cdst[r] = (uint32_t)((e * BS_J + ci % BS_J) * 1024);
+        } else {
+            const int c = min(64 * (ci - BPI * BS_J) + lane, 36 * BPI - 1);
+            const int e = c / 36, j = min((c % 36) / 4, nj - 1);
+            coff[r] = (uint32_t)((((t16 + j) * p.nbp4 + e) * 16 + 4 * (c % 4)) * 4);
+            cdst[r] = (uint32_t)(BPI * BS_BF + (ci - BPI * BS_J) * 1024);
         }
-        __builtin_amdgcn_sched_barrier(0);
+    }
+    auto dma_b = [&](int pp, int pb) {
+        const int64_t b = b0 + BPI * (int64_t)min(pp, npr - 1);
+        const uint8_t *fbase = (const uint8_t *)p.wf + b * 1024;
+        const uint8_t *sbase = (const uint8_t *)p.wsc + b * 64;
+        const uint32_t base = lds_addr(bfr + pb * PB);
 #pragma unroll
-        for (int r = 0; r < CVW; ++r) {
-            const int e = ee[r], j = jj[r];
-            const uint32_t mask = e ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
-            const uint32_t wa = (hu ? q[r][1] : q[r][0]) & mask, wb = (hu ? q[r][3] : q[r][2]) & mask;
-            const vu4 f = {code_pair<0>(wa), code_pair<1>(wa), code_pair<0>(wb), code_pair<1>(wb)};
-            *(vu4 *)(bfr + (2 * pb + e) * BS_BF + j * 1024 + lane * 16) = f;
-            // the four lanes of a weight row write its scale alike
-            sc[(2 * pb + e) * BS_NT + 16 * j + fr] = e ? half_lo(sw[r]) * 0.0625f : half_lo(sw[r]);
+        for (int r = 0; r < BDMA; ++r) {
+            // cidx is wave-uniform: the source is chosen without a lane branch
+            const uint8_t *src = cidx[r] < BPI * BS_J ? fbase : sbase;
+            lds_dma16_so(src, coff[r], base + cdst[r]);
         }
     };
 
@@ -752,14 +738,14 @@ __global__ __launch_bounds__(64 * W, 1) void gemm_q4_bs_kernel(GemmBsParams p, B
         for (int j = 0; j < BS_J; ++j) acc[i][j] = (f4){0.f, 0.f, 0.f, 0.f};
 
     // One block: activation fragments of ring slot `slot`, code fragments and
-    // scales of block buffer fb (pair buffer fb >> 1, block fb & 1).  Software-pipelined by weight tile: the fragment of
+    // scales of block e of pair buffer pb.  Software-pipelined by weight tile: the fragment of
     // tile j + 1 is read while tile j computes, and the MFMAs of tile j issue
     // one by one between the fmas of tile j - 1 (sched_group_barrier); a
     // scheduling barrier per tile keeps the compiler from hoisting every
     // product (and its registers) ahead of the fmas.
     // Fragment (i, plane P) of lane (fr, kg): row 16 i + fr, chunk (4 P + kg) ^ ((fr >> 1) & 7).
     const uint32_t aoff0 = fr * 128 + 16 * (kg ^ ((fr >> 1) & 7)), aoff1 = aoff0 ^ 64;
-    auto compute = [&](int slot, int fb) {
+    auto compute = [&](int slot, int pb, int e) {
         const uint8_t *ab = ring + slot * BS_ABLK;
         h8 a[2][2];
 #pragma unroll
@@ -767,11 +753,11 @@ __global__ __launch_bounds__(64 * W, 1) void gemm_q4_bs_kernel(GemmBsParams p, B
             a[i][0] = *(const h8 *)(ab + i * 2048 + aoff0);
             a[i][1] = *(const h8 *)(ab + i * 2048 + aoff1);
         }
-        const uint8_t *bq = bfr + fb * BS_BF + lane * 16;
+        const uint8_t *bq = bfr + pb * PB + e * BS_BF + lane * 16;
         // (volatile, through an LDS pointer: the compiler would otherwise move
         // each scale read to just before its first use, exposing its latency)
         typedef const __attribute__((address_space(3))) volatile float lds_vf;
-        lds_vf *sp = (lds_vf *)(sc + fb * BS_NT + fr);
+        lds_vf *sp = (lds_vf *)((const float *)(bfr + pb * PB + BPI * BS_BF) + e * BS_NT + fr);
         f4 pr[2][2];
         // scales of tiles j - 1 (fmas this step), j and j + 1 (read this step)
         float s_prev = 0.0f, s_cur = sp[0];
@@ -815,10 +801,10 @@ __global__ __launch_bounds__(64 * W, 1) void gemm_q4_bs_kernel(GemmBsParams p, B
         }
     };
 
-    // prologue: raw groups 0 and 1, activation blocks 0, 1 and 2 in flight
-    dma_raw(0, 0);
+    // prologue: the weights of pairs 0 and 1, activation blocks 0, 1 and 2 in flight
+    dma_b(0, 0);
+    dma_b(1, 1);
     dma_a(0, 0);
-    dma_raw(1, 1);
     dma_a(1, 1);
     dma_a(2, 2);
 
@@ -879,69 +865,52 @@ __global__ __launch_bounds__(64 * W, 1) void gemm_q4_bs_kernel(GemmBsParams p, B
     }
 
     wait_vmcnt<0>();
-    lds_barrier();   // raw groups 0 and 1 of every wave
-    expand(0, 0);    // blocks 0 and 1
-    lds_barrier();
+    lds_barrier();   // pairs 0 and 1 of every wave's weight copies
 
-    // One interval between barriers per block pair p (blocks 2 p, 2 p + 1):
-    // compute pair p from fragment buffer p & 1 and expand pair p + 1 into the
-    // other.  The upper half of the waves expands first and computes after, the
-    // lower half the reverse, so that the two waves of a SIMD overlap one's
-    // expansion with the other's MFMAs.
+    // One interval between barriers per BPI blocks (interval p: blocks BPI p ..):
+    // issue the weights of interval p + 2 into buffer (p + 2) % 3 (it held
+    // interval p - 1, computed before this interval's barrier), then compute
+    // interval p from buffer p % 3.
     // - The activation copy of block k + 3 takes the ring slot of block k once
     //   block k is computed (two blocks of work ahead of its use); each wave
     //   waits for its own copies only, so no barrier is needed for them.
-    // - Raw group h + 1 is issued at the start of interval 2 h - 1 (its buffer
-    //   held group h - 1, last expanded in interval 2 h - 2) and waited for at
-    //   the end of interval 2 h, before the barrier that precedes its first
-    //   expansion (pair 2 h + 2, in interval 2 h + 1).
+    // - The weights of interval p + 1 (issued one interval earlier) are waited
+    //   for at the end of interval p, before the barrier that publishes them.
     // Copies a wave has issued after the one it waits for (in issue order):
-    //   A(4h):   raw(h+1), A(4h+1), A(4h+2)    A(4h+1): A(4h+2), A(4h+3)
-    //   A(4h+2): A(4h+3), A(4h+4), raw(h+2)    A(4h+3): A(4h+4), raw(h+2), A(4h+5)
-    //   raw(h+1) at the end of interval 2h: A(4h+1) .. A(4h+4)
-    // (each wait is followed by a compiler memory barrier, so that no ring read
-    // is scheduled above it).
-    int slot = 0;
-    auto next = [](int s) { return s == BS_RING - 1 ? 0 : s + 1; };
-    auto run = [&](auto role) {
-        constexpr bool EXPAND_FIRST = decltype(role)::value;
-        for (int h = 0; h < ngr; ++h) {
-            const int k = 4 * h;
-            // interval 2h: pair 2h from buffer 0, pair 2h + 1 into buffer 1
-            if constexpr (EXPAND_FIRST) expand(2 * h + 1, 1);
-            wait_vmcnt<RAWW + 2 * BS_ADMA>();
+    //   BPI = 2: A(2p):   B(p+1), A(2p+1), A(2p+2), B(p+2)          = 2 ADMA + 2 BDMA
+    //            A(2p+1): A(2p+2), B(p+2), A(2p+3)                  = 2 ADMA + BDMA
+    //            B(p+1):  A(2p+1), A(2p+2), B(p+2), A(2p+3), A(2p+4) = 4 ADMA + BDMA
+    //   BPI = 1: A(p):    B(p), A(p+1), B(p+1), A(p+2), B(p+2)      = 2 ADMA + 3 BDMA
+    //            B(p+1):  A(p+2), B(p+2), A(p+3)                    = 2 ADMA + BDMA
+    // (each wait on the ring is followed by a compiler memory barrier, so that
+    // no ring read is scheduled above it).
+    int slot = 0, pb = 0;
+    for (int pp = 0; pp < npr; ++pp) {
+        const int k = BPI * pp;
+        dma_b(pp + 2, pb == 0 ? 2 : pb - 1);
+        if constexpr (BPI == 2) {
+            wait_vmcnt<2 * BS_ADMA + 2 * BDMA>();
             __asm__ volatile("" ::: "memory");
-            compute(slot, 0);
+            compute(slot, pb, 0);
             dma_a(k + 3, slot);
-            slot = next(slot);
-            wait_vmcnt<2 * BS_ADMA>();
+            slot = slot == BS_RING - 1 ? 0 : slot + 1;
+            wait_vmcnt<2 * BS_ADMA + BDMA>();
             __asm__ volatile("" ::: "memory");
-            compute(slot, 1);
+            compute(slot, pb, 1);
             dma_a(k + 4, slot);
-            slot = next(slot);
-            if constexpr (!EXPAND_FIRST) expand(2 * h + 1, 1);
-            wait_vmcnt<4 * BS_ADMA>();
-            lds_barrier();
-
-            // interval 2h + 1: pair 2h + 1 from buffer 1, pair 2h + 2 into buffer 0
-            dma_raw(h + 2, h & 1);
-            if constexpr (EXPAND_FIRST) expand(2 * h + 2, 0);
-            wait_vmcnt<2 * BS_ADMA + RAWW>();
+            slot = slot == BS_RING - 1 ? 0 : slot + 1;
+            wait_vmcnt<4 * BS_ADMA + BDMA>();
+        } else {
+            wait_vmcnt<2 * BS_ADMA + 3 * BDMA>();
             __asm__ volatile("" ::: "memory");
-            compute(slot, 2);
-            dma_a(k + 5, slot);
-            slot = next(slot);
-            wait_vmcnt<2 * BS_ADMA + RAWW>();
-            __asm__ volatile("" ::: "memory");
-            compute(slot, 3);
-            dma_a(k + 6, slot);
-            slot = next(slot);
-            if constexpr (!EXPAND_FIRST) expand(2 * h + 2, 0);
-            lds_barrier();
+            compute(slot, pb, 0);
+            dma_a(k + 3, slot);
+            slot = slot == BS_RING - 1 ? 0 : slot + 1;
+            wait_vmcnt<2 * BS_ADMA + BDMA>();
         }
-    };
-    if (w >= W / 2) run(BsRole<true>{});
-    else run(BsRole<false>{});
+        lds_barrier();
+        pb = pb == BS_NB - 1 ? 0 : pb + 1;
+    }
     wait_vmcnt<0>();  // no copy into LDS outlives the workgroup
 
     // epilogue: lane holds rows 4 (lane >> 4) + r of column lane & 15 of each
@@ -1013,7 +982,56 @@ __global__ __launch_bounds__(256) void q4_mins_kernel(const uint8_t *w, int64_t 
     }
 }
 
+// The product's weight operands from packed Q4_0 rows: per 16-row tile and
+// block, the MFMA fragment of its codes as f16 (lane (fr, kg) holds the codes
+// of row 16 tile + fr, block b, elements 2 kg + 8 (t & 3) + (t >> 2), t =
+// 0..7, the activation plane's order), and the 16 rows' scales as fp32; zero
+// past row N and block nb.  One wave per (tile, block).
+__global__ __launch_bounds__(256) void q4_frag_kernel(const uint8_t *w, int64_t N, int nb, int64_t nbp4, uint16_t *wf,
+                                                      float *wsc) {
+    const int lane = threadIdx.x & 63, fr = lane & 15, kg = lane >> 4;
+    const int64_t T = (N + 15) / 16, G = (nb + 3) / 4;
+    const int64_t chunk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (chunk >= T * nbp4) return;
+    const int64_t tile = chunk / nbp4;
+    const int b = (int)(chunk - tile * nbp4);
+    const int64_t n = 16 * tile + fr;
+    vu4 f = {0u, 0u, 0u, 0u};
+    float scale = 0.0f;
+    if (n < N && b < nb) {
+        const uint8_t *grp = w + (n * G + (b >> 2)) * 80;
+        const vu4 q = *(const vu4 *)(grp + 16 * kg);
+        const int u = b & 3;
+        uint32_t wa = u & 2 ? q[1] : q[0], wb = u & 2 ? q[3] : q[2];
+        if (u & 1) {
+            wa >>= 4;
+            wb >>= 4;
+        }
+        wa &= 0x0F0F0F0Fu;
+        wb &= 0x0F0F0F0Fu;
+        f = (vu4){code_pair<0>(wa), code_pair<1>(wa), code_pair<0>(wb), code_pair<1>(wb)};
+        scale = half_lo(*(const uint32_t *)(grp + 64 + 4 * u));
+    }
+    *(vu4 *)(wf + chunk * 512 + lane * 8) = f;
+    if (kg == 0) wsc[chunk * 16 + fr] = scale;
+}
+
 }  // namespace
+
+int64_t q4_frag_nbp4(int64_t K) { return (K / 32 + 3) / 4 * 4; }
+int64_t q4_frag_halves(int64_t N, int64_t K) { return (N + 15) / 16 * q4_frag_nbp4(K) * 512; }
+int64_t q4_frag_scale_floats(int64_t N, int64_t K) { return (N + 15) / 16 * q4_frag_nbp4(K) * 16; }
+
+int launch_q4_frags(const uint8_t *packed, int64_t N, int64_t K, uint16_t *wf, float *wsc, hipStream_t s) {
+    if (!packed || !wf || !wsc || N <= 0 || K <= 0 || K % 32)
+        return set_error(GAJE_ERR_INVALID_ARG, "q4 fragments: bad arguments");
+    const int64_t chunks = (N + 15) / 16 * q4_frag_nbp4(K);
+    if ((chunks + 3) / 4 > 0x7fffffff) return set_error(GAJE_ERR_UNSUPPORTED, "q4 fragments: too many");
+    hipLaunchKernelGGL(q4_frag_kernel, dim3((unsigned)((chunks + 3) / 4)), dim3(256), 0, s, packed, N, (int)(K / 32),
+                       q4_frag_nbp4(K), wf, wsc);
+    GAJE_HIP_CHECK(hipGetLastError());
+    return GAJE_OK;
+}
 
 int launch_q4_row_exponents(const uint8_t *packed, int64_t N, int64_t K, int *ew, hipStream_t s) {
     if (!packed || !ew || N <= 0 || K <= 0 || K % 32) return set_error(GAJE_ERR_INVALID_ARG, "row exponents: bad arguments");
@@ -1118,6 +1136,8 @@ int64_t gemm_bs_plane_rows(int64_t M) { return (M + 255) / 256 * 256; }
 
 GemmBsPlan plan_gemm_q4_bs(int64_t M, int64_t N, int64_t K) {
     GemmBsPlan pl{};
+    // 256-row tiles of eight waves, one workgroup per compute unit; below 129
+    // rows 128- or 64-row tiles, two workgroups per compute unit
     pl.waves = M <= 64 ? 2 : (M <= 128 ? 4 : 8);
     const int64_t mt = BS_WR * pl.waves;
     pl.mtiles = (int)((M + mt - 1) / mt);
@@ -1125,7 +1145,7 @@ GemmBsPlan plan_gemm_q4_bs(int64_t M, int64_t N, int64_t K) {
     pl.ntiles = (int)((units + BS_J - 1) / BS_J);
     const int64_t tiles = (int64_t)pl.mtiles * pl.ntiles;
     const int64_t nb = K / 32;
-    const int64_t cu = device_cu_count();  // one workgroup per compute unit (LDS)
+    const int64_t cu = (pl.waves == 8 ? 1 : 2) * device_cu_count();  // resident workgroups
     const int64_t S = tiles < cu ? cu / tiles : 1;
     int64_t kb = (nb + S - 1) / S;
     kb = (kb + 3) / 4 * 4;  // splits start on group boundaries
@@ -1137,7 +1157,7 @@ GemmBsPlan plan_gemm_q4_bs(int64_t M, int64_t N, int64_t K) {
 }
 
 int launch_gemm_q4_bs(const GemmBsParams &p, const GemmBsPlan &pl, hipStream_t s) {
-    if (p.M < 0 || p.N <= 0 || p.nb <= 0 || !p.w ||
+    if (p.M < 0 || p.N <= 0 || p.nb <= 0 || !p.wf || !p.wsc || p.nbp4 != q4_frag_nbp4(32 * (int64_t)p.nb) ||
         (p.M > 0 && (!p.xh || !p.sh || !p.sl || !p.ex || !p.y || p.ldh < 64 * (int64_t)p.nb ||
                      p.ldsum < gemm_bs_sum_cols(32 * (int64_t)p.nb))))
         return set_error(GAJE_ERR_INVALID_ARG, "q4 block-scaled gemm: bad arguments");
@@ -1151,8 +1171,10 @@ int launch_gemm_q4_bs(const GemmBsParams &p, const GemmBsPlan &pl, hipStream_t s
     if (p.plane_rows < (int64_t)pl.mtiles * mt)
         return set_error(GAJE_ERR_INVALID_ARG, "q4 block-scaled gemm: the activation plane holds %lld rows, the tiles read %lld",
                          (long long)p.plane_rows, (long long)pl.mtiles * mt);
-    if (2 * p.plane_rows * p.ldh >= ((int64_t)1 << 32) || p.N * (int64_t)((p.nb + 3) / 4) * 80 >= ((int64_t)1 << 32))
+    if (2 * p.plane_rows * p.ldh >= ((int64_t)1 << 32) || 2 * q4_frag_halves(p.N, 32 * (int64_t)p.nb) >= ((int64_t)1 << 32))
         return set_error(GAJE_ERR_UNSUPPORTED, "q4 block-scaled gemm: operands beyond 4 GiB");
+    if (((uintptr_t)p.wf | (uintptr_t)p.wsc) & 15)
+        return set_error(GAJE_ERR_INVALID_ARG, "q4 block-scaled gemm: weight fragments must be 16-byte aligned");
     if ((pl.waves != 2 && pl.waves != 4 && pl.waves != 8) || pl.mtiles != (p.M + mt - 1) / mt || pl.ntiles <= 0 ||
         pl.ntiles * (int64_t)BS_J < (p.N + 15) / 16 || pl.kb_per % 4 || pl.kb_per <= 0 ||
         (int64_t)pl.splits * pl.kb_per < p.nb || (int64_t)(pl.splits - 1) * pl.kb_per >= p.nb ||
@@ -1169,16 +1191,16 @@ int launch_gemm_q4_bs(const GemmBsParams &p, const GemmBsPlan &pl, hipStream_t s
     if (total > (1 << 30)) return set_error(GAJE_ERR_UNSUPPORTED, "q4 block-scaled gemm: too many tiles");
     gd.total = (int32_t)total;
     const dim3 grid((unsigned)((total + 7) / 8 * 8));
-    if (bs_lds<8>() > max_lds_per_block()) return set_error(GAJE_ERR_UNSUPPORTED, "q4 block-scaled gemm: LDS");
+    if (bs_lds<8, 2>() > max_lds_per_block()) return set_error(GAJE_ERR_UNSUPPORTED, "q4 block-scaled gemm: LDS");
     switch (pl.waves) {
     case 2:
-        hipLaunchKernelGGL(gemm_q4_bs_kernel<2>, grid, dim3(128), bs_lds<2>(), s, q, gd);
+        gemm_q4_bs_kernel<2, 1><<<grid, dim3(128), bs_lds<2, 1>(), s>>>(q, gd);
         break;
     case 4:
-        hipLaunchKernelGGL(gemm_q4_bs_kernel<4>, grid, dim3(256), bs_lds<4>(), s, q, gd);
+        gemm_q4_bs_kernel<4, 1><<<grid, dim3(256), bs_lds<4, 1>(), s>>>(q, gd);
         break;
     default:
-        hipLaunchKernelGGL(gemm_q4_bs_kernel<8>, grid, dim3(512), bs_lds<8>(), s, q, gd);
+        gemm_q4_bs_kernel<8, 2><<<grid, dim3(512), bs_lds<8, 2>(), s>>>(q, gd);
         break;
     }
     GAJE_HIP_CHECK(hipGetLastError());

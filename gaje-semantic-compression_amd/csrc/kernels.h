@@ -278,7 +278,9 @@ GemmPlan plan_gemm_q4(int64_t M, int64_t N, int64_t K);
 // per block b, P_b on the MFMA units with the 4-bit codes as exact f16
 // operands.  Its activation planes come from launch_split_rows with sh set.
 struct GemmBsParams {
-    const uint8_t *w;        // packed rows (launch_pack_q4_0)
+    const uint16_t *wf;      // the rows' code fragments (launch_q4_frags)
+    const float *wsc;        // and their scales
+    int64_t nbp4;            // q4_frag_nbp4(K)
     const uint16_t *mins;    // the rows' block mins as f16, [N][ldm] (launch_q4_mins)
     int64_t ldm;             // >= gemm_bs_sum_cols(K)
     const uint16_t *xh;      // activation plane [plane_rows][ldh] (hi | lo per block, ldh >= 2K)
@@ -313,6 +315,14 @@ int64_t gemm_bs_sum_cols(int64_t K);
 // The block mins of packed Q4_0 rows as a dense f16 matrix [N][ldm] (zero past
 // K / 32 blocks), ldm >= gemm_bs_sum_cols(K): the min term's operand.
 int launch_q4_mins(const uint8_t *packed, int64_t N, int64_t K, uint16_t *mins, int64_t ldm, hipStream_t s);
+// The block-scaled product's weight operands from packed Q4_0 rows: per
+// 16-row tile and block, the MFMA fragment of the codes as f16 (1 KiB) and the
+// 16 scales as fp32, zero past row N and block K / 32 (blocks padded to a
+// multiple of 4): q4_frag_halves(N, K) halves and q4_frag_scale_floats(N, K) floats.
+int64_t q4_frag_nbp4(int64_t K);
+int64_t q4_frag_halves(int64_t N, int64_t K);
+int64_t q4_frag_scale_floats(int64_t N, int64_t K);
+int launch_q4_frags(const uint8_t *packed, int64_t N, int64_t K, uint16_t *wf, float *wsc, hipStream_t s);
 // Rows the activation plane must hold for M activation rows (a multiple of 256).
 int64_t gemm_bs_plane_rows(int64_t M);
 

@@ -61,6 +61,8 @@ struct DevLinear {
     int64_t bytes = 0;
     uint16_t *mins = nullptr;  // FMT_Q4_0: the block mins [N][ldm] the MFMA prefill's products read
     int64_t ldm = 0;
+    uint16_t *wf = nullptr;    // and their code fragments and scales (launch_q4_frags)
+    float *wsc = nullptr;
 };
 
 struct Layer {
@@ -1098,7 +1100,9 @@ int prefill_gemm(gaje_hip_model *m, const DevLinear &D, int64_t P, float *y, con
     const GemmBsPlan pl = plan_gemm_q4_bs(P, D.N, D.K);
     if (pl.part_floats > f.part_floats) return set_error(GAJE_ERR_INVALID_ARG, "prefill: split-K buffer too small");
     GemmBsParams p{};
-    p.w = D.w;
+    p.wf = D.wf;
+    p.wsc = D.wsc;
+    p.nbp4 = q4_frag_nbp4(D.K);
     p.mins = D.mins;
     p.ldm = D.ldm;
     p.xh = f.xh;
@@ -1229,12 +1233,15 @@ extern "C" int gaje_hip_prefill_mfma(gaje_hip_model *m, const uint32_t *ids, int
     GAJE_TRY(reserve_ctx(m, pos0 + n));
     hipStream_t s = m->stream;
     if (m->n_layers > 0 && !m->layers[0].qkv.mins) {
-        // the products' dense block mins, built once per body tensor
+        // the products' dense block mins and code fragments, built once per body tensor
         for (Layer &Ly : m->layers)
             for (DevLinear *D : {&Ly.qkv, &Ly.o, &Ly.gate_up, &Ly.down}) {
                 D->ldm = gemm_bs_sum_cols(D->K);
                 GAJE_TRY(m->alloc(&D->mins, (size_t)(D->N * D->ldm)));
                 GAJE_TRY(launch_q4_mins(D->w, D->N, D->K, D->mins, D->ldm, s));
+                GAJE_TRY(m->alloc(&D->wf, (size_t)q4_frag_halves(D->N, D->K)));
+                GAJE_TRY(m->alloc(&D->wsc, (size_t)q4_frag_scale_floats(D->N, D->K)));
+                GAJE_TRY(launch_q4_frags(D->w, D->N, D->K, D->wf, D->wsc, s));
             }
     }
     if (m->n_layers > 0 && m->pf.kv16_keys < pos0 + n) {
