@@ -27,6 +27,7 @@
 // Split-K over blocks fills the device when there are few output tiles; the
 // partial products are summed in a fixed order by gemm_reduce_kernel.
 #include <hip/hip_runtime.h>
+#include <type_traits>
 
 #include "common.h"
 #include "device_util.h"
@@ -94,70 +95,79 @@ __global__ __launch_bounds__(256) void q4_row_exp_kernel(const uint8_t *w, int64
     if (lane == 0) ew[row] = split_exponent(mx);
 }
 
-// One activation row per workgroup: a prologue (none, rms_norm in the
-// reference's chain order (norm.rs:52-88), or swiglu_balanced of a gate/up pair
-// (activation.rs:35-51) with the optional use_genomic_norm scaling of
-// block/forward.rs:115-123), the NaN guards of RustGenomicBlock::forward_core
-// that the prologue's values decide, then the row's exponent and its f16
-// hi/lo planes.
-// Threads per row of the split pass: the row's loops are latency-bound, so a
-// row is spread over a full workgroup.
-constexpr int SPLIT_THREADS = 1024;
-
-template <int PRO>
-__global__ __launch_bounds__(SPLIT_THREADS) void split_rows_kernel(SplitParams p) {
+// One activation row per workgroup: a prologue (none, rms_norm (norm.rs:52-88),
+// or swiglu_balanced of a gate/up pair (activation.rs:35-51) with the optional
+// use_genomic_norm scaling of block/forward.rs:115-123; or the deferred
+// split-K reduce of the producing product), the NaN guards of
+// RustGenomicBlock::forward_core that the prologue's values decide, then the
+// row's exponent and its f16 hi/lo planes.  The MFMA paths this feeds are held
+// to fp32 accuracy, not the reference's bits, so the row's sums are taken as
+// trees (the lanes' partials, then the waves') rather than in the chain order.
+// Latency-bound: every input load of a thread is issued at once, the row's
+// values stay in registers (NTH threads x IT float4s), and the pass has three
+// barriers.
+template <int PRO, int NTH, int IT>
+__global__ __launch_bounds__(NTH) void split_rows_kernel(SplitParams p) {
+    constexpr int NWV = NTH / 64;
     extern __shared__ __align__(16) float xs[];
-    __shared__ float red[SPLIT_THREADS / 64];
-    __shared__ float inv_slot;
+    __shared__ float red[2][NWV];
+    __shared__ int badw[NWV];
     const int64_t m = blockIdx.x;
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, wv = tid >> 6;
     const int64_t K = p.K, K4 = K >> 2;
-    const float *xr = p.x + (p.rows ? (int64_t)p.rows[m] : m) * p.ldx;
-    int bad_a = 0, bad_b = 0;
-    if constexpr (PRO == SPLIT_SWIGLU) {
-        const float *ur = p.up + (p.rows ? (int64_t)p.rows[m] : m) * p.ldx;
-        for (int64_t i = tid; i < K4; i += SPLIT_THREADS) {
-            const float4 g = *(const float4 *)(xr + 4 * i), u = *(const float4 *)(ur + 4 * i);
-            bad_a |= isnan(u.x) | isnan(u.y) | isnan(u.z) | isnan(u.w);
+    const int64_t src_row = p.rows ? (int64_t)p.rows[m] : m;
+    const float *xr = p.x + src_row * p.ldx;
+    int bad = 0;  // bit 0: st_a, 1: st_b, 2: st_ya, 3: st_yb
+    float4 v[IT];
+    // ---- every load first ----
+    float4 g4[IT], u4[IT], b4[IT], r4[IT], pv[IT];
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+        const int64_t i = tid + (int64_t)NTH * it;
+        if (i < K4) {
+            if constexpr (PRO == SPLIT_SWIGLU) {
+                g4[it] = *(const float4 *)(xr + 4 * i);
+                u4[it] = *(const float4 *)(p.up + src_row * p.ldx + 4 * i);
+            } else if (p.part) {
+                pv[it] = *(const float4 *)(p.part + m * p.K + 4 * i);
+                if (4 * i + 4 <= p.bias_len) {
+                    b4[it] = *(const float4 *)(p.bias + 4 * i);
+                } else {
+                    float bb[4] = {0.f, 0.f, 0.f, 0.f};
+                    for (int j = 0; j < 4; ++j)
+                        if (4 * i + j < p.bias_len) bb[j] = p.bias[4 * i + j];
+                    b4[it] = make_float4(bb[0], bb[1], bb[2], bb[3]);
+                }
+                r4[it] = p.resid ? *(const float4 *)(p.resid + m * p.ldx + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+            } else {
+                g4[it] = *(const float4 *)(xr + 4 * i);
+            }
+            if constexpr (PRO == SPLIT_NORM) u4[it] = *(const float4 *)(p.norm_w + 4 * i);
+        }
+    }
+    // ---- the prologue's row ----
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+        const int64_t i = tid + (int64_t)NTH * it;
+        v[it] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (i >= K4) continue;
+        if constexpr (PRO == SPLIT_SWIGLU) {
+            const float4 g = g4[it], u = u4[it];
+            bad |= isnan(u.x) | isnan(u.y) | isnan(u.z) | isnan(u.w);
             float4 o;
             o.x = swiglu_fast(g.x, u.x);
             o.y = swiglu_fast(g.y, u.y);
             o.z = swiglu_fast(g.z, u.z);
             o.w = swiglu_fast(g.w, u.w);
-            bad_b |= isnan(o.x) | isnan(o.y) | isnan(o.z) | isnan(o.w);
-            *(float4 *)(xs + 4 * i) = o;
-        }
-    } else if (p.part) {
-        // the deferred split-K reduce of the producing product, in
-        // gemm_reduce_kernel's order, its NaN guards included
-        float *yr = const_cast<float *>(p.x) + m * p.ldx;  // x is the product's output here
-        const int64_t pstride = p.M * p.K;
-        int bad_ya = 0, bad_yb = 0;
-        for (int64_t i = tid; i < K4; i += SPLIT_THREADS) {
-            // bias and residual as whole float4s, read beside the partials
-            float bj[4] = {0.0f, 0.0f, 0.0f, 0.0f}, rj[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (4 * i + 4 <= p.bias_len) {
-                const float4 b = *(const float4 *)(p.bias + 4 * i);
-                bj[0] = b.x;
-                bj[1] = b.y;
-                bj[2] = b.z;
-                bj[3] = b.w;
-            } else {
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    if (4 * i + j < p.bias_len) bj[j] = p.bias[4 * i + j];
-            }
-            if (p.resid) {
-                const float4 r = *(const float4 *)(p.resid + m * p.ldx + 4 * i);
-                rj[0] = r.x;
-                rj[1] = r.y;
-                rj[2] = r.z;
-                rj[3] = r.w;
-            }
+            bad |= (isnan(o.x) | isnan(o.y) | isnan(o.z) | isnan(o.w)) << 1;
+            v[it] = o;
+        } else if (p.part) {
+            // the deferred split-K reduce, in gemm_reduce_kernel's order: the
+            // partials in split order (eight in flight, clamped reads), flush,
+            // bias, residual
             const float *pp = p.part + m * p.K + 4 * i;
-            float4 v = *(const float4 *)pp;
-            // eight partials in flight at a time (clamped reads, no branch),
-            // added in split order
+            const int64_t pstride = p.M * p.K;
+            float4 s = pv[it];
             for (int z0 = 1; z0 < p.nsplit; z0 += 8) {
                 float4 q[8];
 #pragma unroll
@@ -165,123 +175,143 @@ __global__ __launch_bounds__(SPLIT_THREADS) void split_rows_kernel(SplitParams p
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     const bool ok = z0 + j < p.nsplit;
-                    v.x = ok ? v.x + q[j].x : v.x;
-                    v.y = ok ? v.y + q[j].y : v.y;
-                    v.z = ok ? v.z + q[j].z : v.z;
-                    v.w = ok ? v.w + q[j].w : v.w;
+                    s.x = ok ? s.x + q[j].x : s.x;
+                    s.y = ok ? s.y + q[j].y : s.y;
+                    s.z = ok ? s.z + q[j].z : s.z;
+                    s.w = ok ? s.w + q[j].w : s.w;
                 }
             }
-            float a[4] = {flush_small(v.x), flush_small(v.y), flush_small(v.z), flush_small(v.w)};
+            float a[4] = {flush_small(s.x), flush_small(s.y), flush_small(s.z), flush_small(s.w)};
+            const float bb[4] = {b4[it].x, b4[it].y, b4[it].z, b4[it].w}, rr[4] = {r4[it].x, r4[it].y, r4[it].z, r4[it].w};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                if (4 * i + j < p.bias_len) a[j] = a[j] + bj[j];
-                bad_ya |= isnan(a[j]);
-                if (p.resid) a[j] = rj[j] + a[j];
-                bad_yb |= isnan(a[j]);
+                if (4 * i + j < p.bias_len) a[j] = a[j] + bb[j];
+                bad |= isnan(a[j]) << 2;
+                if (p.resid) a[j] = rr[j] + a[j];
+                bad |= isnan(a[j]) << 3;
             }
-            const float4 o = {a[0], a[1], a[2], a[3]};
-            *(float4 *)(yr + 4 * i) = o;
-            bad_a |= isnan(o.x) | isnan(o.y) | isnan(o.z) | isnan(o.w);
-            *(float4 *)(xs + 4 * i) = o;
-        }
-        if (__syncthreads_or(bad_ya) && tid == 0) nan_flag(p.st, p.y_layer, p.st_ya);
-        if (__syncthreads_or(bad_yb) && tid == 0) nan_flag(p.st, p.y_layer, p.st_yb);
-    } else {
-        for (int64_t i = tid; i < K4; i += SPLIT_THREADS) {
-            const float4 v = *(const float4 *)(xr + 4 * i);
-            bad_a |= isnan(v.x) | isnan(v.y) | isnan(v.z) | isnan(v.w);
-            *(float4 *)(xs + 4 * i) = v;
+            v[it] = make_float4(a[0], a[1], a[2], a[3]);
+            *(float4 *)(const_cast<float *>(p.x) + m * p.ldx + 4 * i) = v[it];  // x is the product's output here
+            bad |= isnan(a[0]) | isnan(a[1]) | isnan(a[2]) | isnan(a[3]);
+        } else {
+            v[it] = g4[it];
+            bad |= isnan(v[it].x) | isnan(v[it].y) | isnan(v[it].z) | isnan(v[it].w);
         }
     }
-    const bool any_a = __syncthreads_or(bad_a);
-    if (any_a && tid == 0) nan_flag(p.st, p.layer, p.st_a);
-    if constexpr (PRO == SPLIT_NORM) {
-        rms_inv_plain(xs, K, p.eps, &inv_slot);
+    // a block reduction of one float (op 0: sum, 1: max) over all threads; slot k alternates
+    auto block_reduce = [&](float x, int op, int k) -> float {
+        x = op ? wave_max(x) : wave_sum(x);
+        if ((tid & 63) == 0) red[k][wv] = x;
         __syncthreads();
-        const float inv = inv_slot;
-        for (int64_t i = tid; i < K4; i += SPLIT_THREADS) {
-            float4 v = *(float4 *)(xs + 4 * i);
-            const float4 g = *(const float4 *)(p.norm_w + 4 * i);
-            v.x = (v.x * inv) * g.x;
-            v.y = (v.y * inv) * g.y;
-            v.z = (v.z * inv) * g.z;
-            v.w = (v.w * inv) * g.w;
-            bad_b |= isnan(v.x) | isnan(v.y) | isnan(v.z) | isnan(v.w);
-            *(float4 *)(xs + 4 * i) = v;
+        float r = red[k][0];
+#pragma unroll
+        for (int w = 1; w < NWV; ++w) r = op ? fmaxf(r, red[k][w]) : r + red[k][w];
+        return r;
+    };
+    if constexpr (PRO == SPLIT_NORM) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int it = 0; it < IT; ++it) ss += v[it].x * v[it].x + v[it].y * v[it].y + v[it].z * v[it].z + v[it].w * v[it].w;
+        const float inv = 1.0f / sqrtf(block_reduce(ss, 0, 0) / (float)K + p.eps);
+#pragma unroll
+        for (int it = 0; it < IT; ++it) {
+            const int64_t i = tid + (int64_t)NTH * it;
+            if (i >= K4) continue;
+            const float4 g = u4[it];
+            v[it].x = (v[it].x * inv) * g.x;
+            v[it].y = (v[it].y * inv) * g.y;
+            v[it].z = (v[it].z * inv) * g.z;
+            v[it].w = (v[it].w * inv) * g.w;
+            bad |= (isnan(v[it].x) | isnan(v[it].y) | isnan(v[it].z) | isnan(v[it].w)) << 1;
         }
-    }
-    if constexpr (PRO != SPLIT_PLAIN) {
-        if (__syncthreads_or(bad_b) && tid == 0) nan_flag(p.st, p.layer, p.st_b);
     }
     if constexpr (PRO == SPLIT_SWIGLU) {
-        if (p.gnorm) {
-            // the reference's rayon sum has no fixed order; a sequential one here
-            if (tid == 0) {
-                float ss = 0.0f;
-                for (int64_t k = 0; k < K; ++k) {
-                    const float sq = xs[k] * xs[k];
-                    ss = ss + sq;
-                }
-                inv_slot = sqrtf(ss / (float)K + p.eps);
-            }
-            __syncthreads();
-            const float rms = inv_slot;
+        if (p.gnorm) {  // the reference's rayon sum has no fixed order: a tree here
+            float ss = 0.0f;
+#pragma unroll
+            for (int it = 0; it < IT; ++it) ss += v[it].x * v[it].x + v[it].y * v[it].y + v[it].z * v[it].z + v[it].w * v[it].w;
+            const float rms = sqrtf(block_reduce(ss, 0, 0) / (float)K + p.eps);
             if (rms > p.h_scale) {
                 const float sc = p.h_scale / rms;
-                for (int64_t k = tid; k < K; k += SPLIT_THREADS) xs[k] = xs[k] * sc;
+#pragma unroll
+                for (int it = 0; it < IT; ++it) {
+                    v[it].x = v[it].x * sc;
+                    v[it].y = v[it].y * sc;
+                    v[it].z = v[it].z * sc;
+                    v[it].w = v[it].w * sc;
+                }
             }
-            __syncthreads();
         }
     }
-    if (p.x_out) {  // the prologue's output row itself, for callers that keep it
-        for (int64_t i = tid; i < K4; i += SPLIT_THREADS) *(float4 *)(p.x_out + m * p.ldo + 4 * i) = *(float4 *)(xs + 4 * i);
-    }
     float mx = 0.0f;
-    for (int64_t i = tid; i < K4; i += SPLIT_THREADS) {
-        const float4 v = *(const float4 *)(xs + 4 * i);
-        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-    }
-    mx = wave_max(mx);
-    if ((tid & 63) == 0) red[tid >> 6] = mx;
-    __syncthreads();
-    float rmax = red[0];
 #pragma unroll
-    for (int w = 1; w < SPLIT_THREADS / 64; ++w) rmax = fmaxf(rmax, red[w]);
-    const int e = split_exponent(rmax);
-    if (tid == 0) p.ex[m] = e;
+    for (int it = 0; it < IT; ++it) {
+        const int64_t i = tid + (int64_t)NTH * it;
+        if (i >= K4) continue;
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[it].x), fabsf(v[it].y)), fmaxf(fabsf(v[it].z), fabsf(v[it].w))));
+        *(float4 *)(xs + 4 * i) = v[it];
+        if (p.x_out) *(float4 *)(p.x_out + m * p.ldo + 4 * i) = v[it];
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) bad |= __shfl_xor(bad, off);
+    if ((tid & 63) == 0) badw[wv] = bad;
+    const int e = split_exponent(block_reduce(mx, 1, 1));  // (its barrier also publishes xs and badw)
+    if (tid == 0) {
+        p.ex[m] = e;
+        int b = 0;
+#pragma unroll
+        for (int w = 0; w < NWV; ++w) b |= badw[w];
+        if (p.part) {
+            if (b & 4) nan_flag(p.st, p.y_layer, p.st_ya);
+            if (b & 8) nan_flag(p.st, p.y_layer, p.st_yb);
+        }
+        if (b & 1) nan_flag(p.st, p.layer, p.st_a);
+        if ((b & 2) && PRO != SPLIT_PLAIN) nan_flag(p.st, p.layer, p.st_b);
+    }
     if (p.sh) {
         // block-scaled layout: one plane, block b at halves 64 b.. holding its
         // 32 hi halves then its 32 lo halves; position 8 kg + t of each holds
-        // element 32 b + 2 kg + 8 (t & 3) + (t >> 2)
-        for (int64_t u = tid; u < (K >> 3); u += SPLIT_THREADS) {
-            const int64_t e0 = 32 * (u >> 2) + 2 * (u & 3);
-            h8 hi, lo;
-#pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                const float a = ldexpf(xs[e0 + 8 * (t & 3) + (t >> 2)], e);
-                hi[t] = (_Float16)a;
-                lo[t] = (_Float16)(a - (float)hi[t]);
-            }
-            _Float16 *row = (_Float16 *)p.xh + m * p.ldh + 64 * (u >> 2) + 8 * (u & 3);
-            *(h8 *)row = hi;
-            *(h8 *)(row + 32) = lo;
-        }
-        // block sums, 2^-5 sum x' (|x'| < 2^15, so below 2^15), zero past the last block
+        // element 32 b + 2 kg + 8 (t & 3) + (t >> 2).  Chunk u (8 halves) is
+        // (block u >> 2, kg = u & 3); the block sum 2^-5 sum x' (|x'| < 2^15)
+        // is the four chunks' partials over consecutive lanes.
         const int64_t nb = K >> 5;
-        for (int64_t b = tid; b < p.ldsum; b += SPLIT_THREADS) {
-            float sum = 0.0f;
-            if (b < nb)
-                for (int t = 0; t < 32; ++t) sum = sum + ldexpf(xs[32 * b + t], e);
-            const float v = ldexpf(sum, -5);
-            const _Float16 hi = (_Float16)v;
-            ((_Float16 *)p.sh)[m * p.ldsum + b] = hi;
-            ((_Float16 *)p.sl)[m * p.ldsum + b] = (_Float16)(v - (float)hi);
+        for (int64_t u0 = 0; u0 < (K >> 3); u0 += NTH) {
+            const int64_t u = u0 + tid;
+            float s8 = 0.0f;
+            if (u < (K >> 3)) {
+                const int64_t e0 = 32 * (u >> 2) + 2 * (u & 3);
+                h8 hi, lo;
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    const float a = ldexpf(xs[e0 + 8 * (t & 3) + (t >> 2)], e);
+                    hi[t] = (_Float16)a;
+                    lo[t] = (_Float16)(a - (float)hi[t]);
+                    s8 += a;
+                }
+                _Float16 *row = (_Float16 *)p.xh + m * p.ldh + 64 * (u >> 2) + 8 * (u & 3);
+                *(h8 *)row = hi;
+                *(h8 *)(row + 32) = lo;
+            }
+            s8 += __shfl_xor(s8, 1);
+            s8 += __shfl_xor(s8, 2);
+            if (u < (K >> 3) && (u & 3) == 0) {
+                const float sv = ldexpf(s8, -5);
+                const _Float16 hv = (_Float16)sv;
+                ((_Float16 *)p.sh)[m * p.ldsum + (u >> 2)] = hv;
+                ((_Float16 *)p.sl)[m * p.ldsum + (u >> 2)] = (_Float16)(sv - (float)hv);
+            }
+        }
+        for (int64_t b = nb + tid; b < p.ldsum; b += NTH) {  // zero past the last block
+            ((_Float16 *)p.sh)[m * p.ldsum + b] = (_Float16)0.0f;
+            ((_Float16 *)p.sl)[m * p.ldsum + b] = (_Float16)0.0f;
         }
         return;
     }
-    for (int64_t i = tid; i < K4; i += SPLIT_THREADS) {
-        const float4 v = *(const float4 *)(xs + 4 * i);
-        const float a[4] = {ldexpf(v.x, e), ldexpf(v.y, e), ldexpf(v.z, e), ldexpf(v.w, e)};
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+        const int64_t i = tid + (int64_t)NTH * it;
+        if (i >= K4) continue;
+        const float a[4] = {ldexpf(v[it].x, e), ldexpf(v[it].y, e), ldexpf(v[it].z, e), ldexpf(v[it].w, e)};
         h4 hi, lo;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -1064,15 +1094,25 @@ int launch_split_rows(const SplitParams &p, hipStream_t s) {
         return set_error(GAJE_ERR_INVALID_ARG, "split rows: bad block-sum planes");
     if (p.M == 0) return GAJE_OK;
     const size_t lds = (size_t)p.K * 4;
-    if (lds + 1024 > max_lds_per_block())
+    if (lds + 1024 > max_lds_per_block() || p.K > 40960)
         return set_error(GAJE_ERR_UNSUPPORTED, "split rows: K = %lld does not fit LDS", (long long)p.K);
     if (p.up && p.norm_w) return set_error(GAJE_ERR_INVALID_ARG, "split rows: norm and swiglu prologues are exclusive");
     if (p.part && (p.up || p.rows || p.nsplit < 1 || p.ldx != p.K || (p.resid && p.resid != p.x) || p.bias_len < 0 ||
                    (p.bias_len > 0 && !p.bias) || ((uintptr_t)p.part & 15)))
         return set_error(GAJE_ERR_INVALID_ARG, "split rows: bad split-K prologue");
-    if (p.up) hipLaunchKernelGGL(split_rows_kernel<SPLIT_SWIGLU>, dim3((unsigned)p.M), dim3(SPLIT_THREADS), lds, s, p);
-    else if (p.norm_w) hipLaunchKernelGGL(split_rows_kernel<SPLIT_NORM>, dim3((unsigned)p.M), dim3(SPLIT_THREADS), lds, s, p);
-    else hipLaunchKernelGGL(split_rows_kernel<SPLIT_PLAIN>, dim3((unsigned)p.M), dim3(SPLIT_THREADS), lds, s, p);
+    // threads x float4s per thread covering the row: 256 x 2, 256 x 4, 1024 x 4, 1024 x 10
+    const int64_t K4 = p.K / 4;
+    const dim3 grid((unsigned)p.M);
+    auto go = [&](auto pro) {
+        constexpr int PRO = decltype(pro)::value;
+        if (K4 <= 512) split_rows_kernel<PRO, 256, 2><<<grid, dim3(256), lds, s>>>(p);
+        else if (K4 <= 1024) split_rows_kernel<PRO, 256, 4><<<grid, dim3(256), lds, s>>>(p);
+        else if (K4 <= 4096) split_rows_kernel<PRO, 1024, 4><<<grid, dim3(1024), lds, s>>>(p);
+        else split_rows_kernel<PRO, 1024, 10><<<grid, dim3(1024), lds, s>>>(p);
+    };
+    if (p.up) go(std::integral_constant<int, SPLIT_SWIGLU>{});
+    else if (p.norm_w) go(std::integral_constant<int, SPLIT_NORM>{});
+    else go(std::integral_constant<int, SPLIT_PLAIN>{});
     GAJE_HIP_CHECK(hipGetLastError());
     return GAJE_OK;
 }
