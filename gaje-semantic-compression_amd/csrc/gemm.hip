@@ -121,10 +121,30 @@ __global__ __launch_bounds__(NTH) void split_rows_kernel(SplitParams p) {
     float4 v[IT];
     // ---- every load first ----
     float4 g4[IT], u4[IT], b4[IT], r4[IT], pv[IT];
+    // attention-merge prologue: the row's float4 i lies in head 4 i / hd; the
+    // records of its key chunks c < nc (clamped reads)
+    constexpr int NCH = PREFILL_ATTN_CHUNKS;
+    float am[PRO == SPLIT_PLAIN ? IT : 1][NCH], al[PRO == SPLIT_PLAIN ? IT : 1][NCH];
+    float4 ao[PRO == SPLIT_PLAIN ? IT : 1][NCH];
+    const int anc = p.attn_ws ? (int)((p.attn_pos0 + m) / p.attn_kch) + 1 : 0;
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
         const int64_t i = tid + (int64_t)NTH * it;
         if (i < K4) {
+            if constexpr (PRO == SPLIT_PLAIN) {
+                if (p.attn_ws) {
+                    const int64_t h = 4 * i / p.attn_hd, d = 4 * i - h * p.attn_hd;
+                    const int64_t rs = (int64_t)p.attn_hd + PREFILL_ATTN_REC_PAD;
+#pragma unroll
+                    for (int c = 0; c < NCH; ++c) {
+                        const float *rc = p.attn_ws + (((int64_t)min(c, anc - 1) * p.M + m) * p.attn_heads + h) * rs;
+                        am[it][c] = rc[0];
+                        al[it][c] = rc[1];
+                        ao[it][c] = *(const float4 *)(rc + PREFILL_ATTN_REC_PAD + d);
+                    }
+                    continue;
+                }
+            }
             if constexpr (PRO == SPLIT_SWIGLU) {
                 g4[it] = *(const float4 *)(xr + 4 * i);
                 u4[it] = *(const float4 *)(p.up + src_row * p.ldx + 4 * i);
@@ -193,6 +213,30 @@ __global__ __launch_bounds__(NTH) void split_rows_kernel(SplitParams p) {
             v[it] = make_float4(a[0], a[1], a[2], a[3]);
             *(float4 *)(const_cast<float *>(p.x) + m * p.ldx + 4 * i) = v[it];  // x is the product's output here
             bad |= isnan(a[0]) | isnan(a[1]) | isnan(a[2]) | isnan(a[3]);
+        } else if (PRO == SPLIT_PLAIN && p.attn_ws) {
+            // out = (sum_c O_c 2^(m_c - m)) / (sum_c l_c 2^(m_c - m) + 1e-12), m =
+            // max_c m_c, as prefill_attn_merge_kernel (the maxima in log2 units)
+            if constexpr (PRO == SPLIT_PLAIN) {
+                float mx = -INFINITY;
+#pragma unroll
+                for (int c = 0; c < NCH; ++c)
+                    if (c < anc) mx = fmaxf(mx, am[it][c]);
+                float l = 0.0f;
+                float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                for (int c = 0; c < NCH; ++c)
+                    if (c < anc) {
+                        const float e = exp2f(am[it][c] - mx);
+                        l = l + al[it][c] * e;
+                        o.x = o.x + ao[it][c].x * e;
+                        o.y = o.y + ao[it][c].y * e;
+                        o.z = o.z + ao[it][c].z * e;
+                        o.w = o.w + ao[it][c].w * e;
+                    }
+                const float r = 1.0f / (l + 1e-12f);
+                v[it] = make_float4(o.x * r, o.y * r, o.z * r, o.w * r);
+                bad |= isnan(v[it].x) | isnan(v[it].y) | isnan(v[it].z) | isnan(v[it].w);
+            }
         } else {
             v[it] = g4[it];
             bad |= isnan(v[it].x) | isnan(v[it].y) | isnan(v[it].z) | isnan(v[it].w);
@@ -1100,6 +1144,10 @@ int launch_split_rows(const SplitParams &p, hipStream_t s) {
     if (p.part && (p.up || p.rows || p.nsplit < 1 || p.ldx != p.K || (p.resid && p.resid != p.x) || p.bias_len < 0 ||
                    (p.bias_len > 0 && !p.bias) || ((uintptr_t)p.part & 15)))
         return set_error(GAJE_ERR_INVALID_ARG, "split rows: bad split-K prologue");
+    if (p.attn_ws && (p.up || p.norm_w || p.part || p.rows || p.attn_hd <= 0 || p.attn_hd % 4 || p.attn_heads <= 0 ||
+                      (int64_t)p.attn_heads * p.attn_hd != p.K || p.attn_kch <= 0 || p.attn_pos0 < 0 ||
+                      (p.attn_pos0 + p.M + p.attn_kch - 1) / p.attn_kch > PREFILL_ATTN_CHUNKS))
+        return set_error(GAJE_ERR_INVALID_ARG, "split rows: bad attention-merge prologue");
     // threads x float4s per thread covering the row: 256 x 2, 256 x 4, 1024 x 4, 1024 x 10
     const int64_t K4 = p.K / 4;
     const dim3 grid((unsigned)p.M);

@@ -224,6 +224,12 @@ struct SplitParams {
     const float *resid;      // [M][ldx] or null
     int32_t st_ya, st_yb;    // the product's NaN guards (after the bias, after resid)
     int32_t y_layer;         // the product's layer, for those guards
+    // Attention-merge prologue (without up, rows, part or norm): row t is the
+    // causal attention output of query t, merged from the key chunks' partials
+    // (PrefillAttnParams::ws, chunks of attn_kch keys; K = n_head * head_dim).
+    const float *attn_ws;
+    int64_t attn_kch, attn_pos0;
+    int32_t attn_hd, attn_heads;
 };
 int launch_split_rows(const SplitParams &p, hipStream_t s);
 // Per packed Q4_0 row: the exponent that scales its largest |d| into [2^14, 2^15).
@@ -343,6 +349,16 @@ struct PrefillRopeParams {
     // of its own cache (k/v_cache + t * seq_kv_stride); pos0 unused
     const int32_t *seq_pos;
     int64_t seq_kv_stride;
+    // prefill: the qkv rows from a split-K product's partials, [nsplit][P][ldq]
+    // (its deferred reduce: flush_small(sum) + bias), or null
+    const float *part;
+    int32_t nsplit;
+    const float *bias;
+    int64_t bias_len;
+    // prefill: also the keys' and values' f16 pairs for the attention
+    // (PrefillAttnParams::kv16, kv16_ntiles 32-key tiles), or null
+    uint16_t *kv16;
+    int32_t kv16_ntiles;
 };
 int launch_rope_kv(const PrefillRopeParams &p, hipStream_t s);
 // Causal GQA attention of P queries (positions pos0..) over the cache.
@@ -355,11 +371,17 @@ struct PrefillAttnParams {
     float *ws;               // key-chunk partials: prefill_attn_ws_floats(P, n_head, head_dim) floats
     uint16_t *kv16;          // f16 pairs of the keys and values: prefill_kv16_halves(kv16_keys, ..) halves
     int64_t kv16_keys;       // positions kv16 holds (>= pos0 + P)
+    int32_t merged_later;    // the chunks' partials are left for a split pass (SplitParams::attn_ws)
+    int32_t kv16_rope;       // launch_rope_kv wrote the chunk's positions of kv16
 };
 // Keys are split into at most PREFILL_ATTN_CHUNKS chunks per query block,
 // each computed by its own workgroup and merged afterwards.
 constexpr int PREFILL_ATTN_CHUNKS = 8;
 int64_t prefill_attn_ws_floats(int64_t P, int64_t n_head, int64_t head_dim);
+// Key chunk length of the attention's partials for `keys` keys (the merge's kch).
+int64_t prefill_attn_kch(int64_t keys);
+// A record of the partials: {m, l, -, -, O[head_dim]} (O 16-byte aligned).
+constexpr int PREFILL_ATTN_REC_PAD = 4;
 int64_t prefill_kv16_halves(int64_t keys, int64_t n_kv, int64_t head_dim);
 int launch_prefill_attention(const PrefillAttnParams &p, hipStream_t s);
 

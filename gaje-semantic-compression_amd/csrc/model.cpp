@@ -1158,7 +1158,8 @@ int prefill_layer(gaje_hip_model *m, int64_t l, int64_t pos, int64_t P, PendingR
     sp.st_a = ST_INPUT;
     sp.st_b = Ly.attn_norm ? ST_ATTN_NORM : ST_NONE;
     GAJE_TRY(launch_split_rows(sp, s));
-    GAJE_TRY(prefill_gemm(m, Ly.qkv, P, f.QKV, nullptr, li, ST_NONE, ST_NONE));
+    PendingReduce qkv_pending;
+    GAJE_TRY(prefill_gemm(m, Ly.qkv, P, f.QKV, nullptr, li, ST_NONE, ST_NONE, &qkv_pending));
 
     PrefillRopeParams rp{};
     rp.qkv = f.QKV;
@@ -1175,6 +1176,14 @@ int prefill_layer(gaje_hip_model *m, int64_t l, int64_t pos, int64_t P, PendingR
     rp.rope_split = m->rope_split;
     rp.rope_cos = m->rope_cos;
     rp.rope_sin = m->rope_sin;
+    if (qkv_pending.nsplit) {  // the qkv product's reduce, in the RoPE pass
+        rp.part = f.part;
+        rp.nsplit = qkv_pending.nsplit;
+        rp.bias = qkv_pending.bias;
+        rp.bias_len = qkv_pending.bias_len;
+    }
+    rp.kv16 = f.kv16;
+    rp.kv16_ntiles = (int32_t)((pos + P + 31) / 32);
     GAJE_TRY(launch_rope_kv(rp, s));
 
     PrefillAttnParams ap{};
@@ -1191,9 +1200,16 @@ int prefill_layer(gaje_hip_model *m, int64_t l, int64_t pos, int64_t P, PendingR
     ap.ws = f.aws;
     ap.kv16 = f.kv16;
     ap.kv16_keys = f.kv16_keys;
+    ap.kv16_rope = 1;
+    ap.merged_later = 1;  // the merge is the next split pass's prologue
     GAJE_TRY(launch_prefill_attention(ap, s));
 
     sp = prefill_split(m, f.ATT, m->q_rows, P, m->q_rows);
+    sp.attn_ws = f.aws;
+    sp.attn_kch = prefill_attn_kch(pos + P);
+    sp.attn_pos0 = pos;
+    sp.attn_hd = (int32_t)m->hd;
+    sp.attn_heads = (int32_t)m->n_head;
     GAJE_TRY(launch_split_rows(sp, s));
     GAJE_TRY(prefill_gemm(m, Ly.o, P, f.H, f.H, li, ST_NONE, ST_NONE, &pending));
 
@@ -1252,6 +1268,9 @@ extern "C" int gaje_hip_prefill_mfma(gaje_hip_model *m, const uint32_t *ids, int
         m->pf.kv16_keys = 0;
         const int64_t keys = (pos0 + n + 255) / 256 * 256;
         GAJE_TRY(m->alloc(&m->pf.kv16, (size_t)prefill_kv16_halves(keys, m->n_kv, m->hd)));
+        // zero once: the attention reads whole 32-key tiles, and its value
+        // tiles past the last key must hold finite numbers
+        GAJE_HIP_CHECK(hipMemsetAsync(m->pf.kv16, 0, (size_t)prefill_kv16_halves(keys, m->n_kv, m->hd) * 2, s));
         m->pf.kv16_keys = keys;
     }
     GAJE_TRY(launch_state_set(m->st, (int32_t)pos0, ids[n - 1], -1, -1, 1, s));

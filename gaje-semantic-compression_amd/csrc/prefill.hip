@@ -18,8 +18,12 @@ namespace {
 // RoPE of GenomicAttention::forward_attention_core (attention.rs:56-84) on the
 // q and k rows of each token, from the host-built table of the decode path,
 // each product rounded as in the decode epilogue; k and v appended to the
-// cache at the token's position.  One workgroup per token.
+// cache at the token's position.  One workgroup per token.  In prefill the row
+// may first be reduced from the qkv product's split-K partials (its deferred
+// reduce, in gemm_reduce_kernel's order), and the keys and values are also
+// written as the attention's f16 pairs (prefill_kv16_kernel's layouts).
 __global__ __launch_bounds__(256) void rope_kv_kernel(PrefillRopeParams p) {
+    extern __shared__ __align__(16) float rowbuf[];  // the reduced row (with part)
     const int64_t t = blockIdx.x;
     int64_t pos = p.pos0 + t;
     if (p.seq_pos) {
@@ -31,6 +35,34 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(PrefillRopeParams p) {
     const float *row = p.qkv + t * p.ldq;
     const int hd = p.head_dim, half = hd >> 1;
     const int64_t q_rows = (int64_t)p.n_head * hd, kv_rows = (int64_t)p.n_kv * hd;
+    if (p.part) {
+        const int64_t n_all = q_rows + 2 * kv_rows, pstride = p.P * p.ldq;
+        for (int64_t n = threadIdx.x; n < n_all; n += blockDim.x) {
+            const float *pp = p.part + t * p.ldq + n;
+            float v = pp[0];
+            for (int z0 = 1; z0 < p.nsplit; z0 += 8) {  // eight partials in flight, added in split order
+                float q[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) q[j] = pp[(int64_t)min(z0 + j, p.nsplit - 1) * pstride];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v = z0 + j < p.nsplit ? v + q[j] : v;
+            }
+            v = flush_small(v);
+            if (n < p.bias_len) v = v + p.bias[n];
+            rowbuf[n] = v;
+        }
+        __syncthreads();
+        row = rowbuf;
+    }
+    // the attention's f16 pairs: K16[g][pos][d / 32][hi 32 | lo 32],
+    // V16[g][d][pos / 32][hi 32 | lo 32] at slot 8 kg + 4 u + r of key 16 u + 4 kg + r
+    const int64_t nt = p.kv16_ntiles;
+    uint16_t *k16 = p.kv16, *v16 = p.kv16 ? p.kv16 + (int64_t)p.n_kv * nt * 32 * 2 * hd : nullptr;
+    auto put_pair = [](uint16_t *dst, float x) {
+        const _Float16 hi = (_Float16)x;
+        dst[0] = __builtin_bit_cast(uint16_t, hi);
+        dst[32] = __builtin_bit_cast(uint16_t, (_Float16)(x - (float)hi));
+    };
     const int64_t pairs = (int64_t)(p.n_head + p.n_kv) * half;
     for (int64_t pr = threadIdx.x; pr < pairs; pr += blockDim.x) {
         const int64_t head = pr / half;
@@ -45,14 +77,24 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(PrefillRopeParams p) {
             p.q_out[t * q_rows + head * hd + d0] = o0;
             p.q_out[t * q_rows + head * hd + d1] = o1;
         } else {
-            float *kc = p.k_cache + (head - p.n_head) * hd * p.cap + pos;
+            const int64_t g = head - p.n_head;
+            float *kc = p.k_cache + g * hd * p.cap + pos;
             kc[(int64_t)d0 * p.cap] = o0;
             kc[(int64_t)d1 * p.cap] = o1;
+            if (k16) {
+                uint16_t *kr = k16 + (g * nt * 32 + pos) * 2 * hd;
+                put_pair(kr + (d0 >> 5) * 64 + (d0 & 31), o0);
+                put_pair(kr + (d1 >> 5) * 64 + (d1 & 31), o1);
+            }
         }
     }
+    const int w = (int)(pos & 31);
+    const int slot = 8 * ((w & 15) >> 2) + 4 * (w >> 4) + (w & 3);
     for (int64_t j = threadIdx.x; j < kv_rows; j += blockDim.x) {
         const int64_t vh = j / hd, d = j - vh * hd;
-        p.v_cache[(vh * hd + d) * p.cap + pos] = row[q_rows + kv_rows + j];
+        const float v = row[q_rows + kv_rows + j];
+        p.v_cache[(vh * hd + d) * p.cap + pos] = v;
+        if (v16) put_pair(v16 + ((vh * hd + d) * nt + (pos >> 5)) * 64 + slot, v);
     }
 }
 
@@ -263,19 +305,18 @@ __global__ __launch_bounds__(64) void prefill_attn_f16_kernel(PrefillAttnParams 
             o[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[tt][1], ph, o[tt], 0, 0, 0);
         }
     }
-    // the query's sum over its four lanes; partials ws[c][t][h] = {m, l, O[HD]}
+    // the query's sum over its four lanes; partials ws[c][t][h] = {m, l, -, -, O[HD]}
     l = l + __shfl_xor(l, 16);
     l = l + __shfl_xor(l, 32);
     if (t < p.P) {
-        float *rec = p.ws + (((int64_t)blockIdx.z * p.P + t) * p.n_head + h) * (HD + 2);
+        float *rec = p.ws + (((int64_t)blockIdx.z * p.P + t) * p.n_head + h) * (HD + PREFILL_ATTN_REC_PAD);
         if (kg == 0) {
             rec[0] = m;
             rec[1] = l;
         }
 #pragma unroll
         for (int tt = 0; tt < NT; ++tt)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) rec[2 + 16 * tt + 4 * kg + r] = o[tt][r];
+            *(f4v *)(rec + PREFILL_ATTN_REC_PAD + 16 * tt + 4 * kg) = o[tt];
     }
 }
 
@@ -287,8 +328,8 @@ __global__ __launch_bounds__(128) void prefill_attn_merge_kernel(PrefillAttnPara
     const int64_t t = blockIdx.x;
     const int h = blockIdx.y, d = threadIdx.x, HD = p.head_dim;
     const int nc = (int)((p.pos0 + t) / kch) + 1;  // <= PREFILL_ATTN_CHUNKS
-    const int64_t rs = (int64_t)p.n_head * (HD + 2);
-    const float *rec = p.ws + (t * p.n_head + h) * (HD + 2);
+    const int64_t rs = (int64_t)p.n_head * (HD + PREFILL_ATTN_REC_PAD);
+    const float *rec = p.ws + (t * p.n_head + h) * (HD + PREFILL_ATTN_REC_PAD);
     const int64_t cstride = p.P * rs;
     // every chunk's record read at once (one round trip)
     float mc[PREFILL_ATTN_CHUNKS], lc[PREFILL_ATTN_CHUNKS], oc[PREFILL_ATTN_CHUNKS];
@@ -297,7 +338,7 @@ __global__ __launch_bounds__(128) void prefill_attn_merge_kernel(PrefillAttnPara
         const float *rc = rec + (c < nc ? c : 0) * cstride;
         mc[c] = rc[0];
         lc[c] = rc[1];
-        oc[c] = d < HD ? rc[2 + d] : 0.0f;
+        oc[c] = d < HD ? rc[PREFILL_ATTN_REC_PAD + d] : 0.0f;
     }
     float mx = -INFINITY;
 #pragma unroll
@@ -320,43 +361,61 @@ int launch_rope_kv(const PrefillRopeParams &p, hipStream_t s) {
     if (p.P <= 0 || !p.qkv || !p.q_out || !p.k_cache || !p.v_cache || p.head_dim <= 0 || p.head_dim % 2 ||
         (!p.seq_pos && (p.pos0 < 0 || p.pos0 + p.P > p.cap)))
         return set_error(GAJE_ERR_INVALID_ARG, "rope/kv: bad arguments");
-    hipLaunchKernelGGL(rope_kv_kernel, dim3((unsigned)p.P), dim3(256), 0, s, p);
+    const int64_t row = (int64_t)(p.n_head + 2 * p.n_kv) * p.head_dim;
+    if ((p.part || p.kv16) && (p.seq_pos || p.head_dim % 32))
+        return set_error(GAJE_ERR_INVALID_ARG, "rope/kv: bad prefill arguments");
+    if (p.part && (p.nsplit < 1 || p.ldq < row || row * 4 > 65536 || p.bias_len < 0 || (p.bias_len > 0 && !p.bias)))
+        return set_error(GAJE_ERR_INVALID_ARG, "rope/kv: bad split-K prologue");
+    if (p.kv16 && (int64_t)p.kv16_ntiles * 32 < p.pos0 + p.P)
+        return set_error(GAJE_ERR_INVALID_ARG, "rope/kv: f16 key tiles too few");
+    hipLaunchKernelGGL(rope_kv_kernel, dim3((unsigned)p.P), dim3(256), p.part ? (size_t)row * 4 : 0, s, p);
     GAJE_HIP_CHECK(hipGetLastError());
     return GAJE_OK;
 }
 
 int64_t prefill_attn_ws_floats(int64_t P, int64_t n_head, int64_t head_dim) {
-    return (int64_t)PREFILL_ATTN_CHUNKS * P * n_head * (head_dim + 2);
+    return (int64_t)PREFILL_ATTN_CHUNKS * P * n_head * (head_dim + PREFILL_ATTN_REC_PAD);
 }
 
 int64_t prefill_kv16_halves(int64_t keys, int64_t n_kv, int64_t head_dim) {
     return 4 * n_kv * ((keys + 31) / 32 * 32) * head_dim;
 }
 
+// key chunks of at least 128 keys (whole 32-key tiles), at most PREFILL_ATTN_CHUNKS of them
+int64_t prefill_attn_kch(int64_t keys) {
+    int64_t kch = (keys + PREFILL_ATTN_CHUNKS - 1) / PREFILL_ATTN_CHUNKS;
+    return kch < 128 ? 128 : (kch + 31) / 32 * 32;
+}
+
 int launch_prefill_attention(const PrefillAttnParams &p, hipStream_t s) {
-    if (p.P <= 0 || !p.q || !p.k_cache || !p.v_cache || !p.out || p.n_kv <= 0 || p.n_head % p.n_kv ||
-        p.pos0 < 0 || p.pos0 + p.P > p.cap || p.P > 65535)
+    if (p.P <= 0 || !p.q || !p.k_cache || !p.v_cache || (!p.out && !p.merged_later) || p.n_kv <= 0 ||
+        p.n_head % p.n_kv || p.pos0 < 0 || p.pos0 + p.P > p.cap || p.P > 65535)
         return set_error(GAJE_ERR_INVALID_ARG, "prefill attention: bad arguments");
     if (p.head_dim != 64 && p.head_dim != 128)
         return set_error(GAJE_ERR_UNSUPPORTED, "prefill attention: head_dim %d (64 or 128 only)", p.head_dim);
     const int64_t keys = p.pos0 + p.P;
     if (!p.ws || !p.kv16 || p.kv16_keys < keys)
         return set_error(GAJE_ERR_INVALID_ARG, "prefill attention: workspace too small");
-    // the converted keys and values, [0, keys) padded to whole 32-key tiles
+    // the converted keys and values, [0, keys) padded to whole 32-key tiles:
+    // the tiles before the chunk here (when launch_rope_kv wrote the chunk's
+    // positions), or all of them
     const int ntiles = (int)((keys + 31) / 32);
-    hipLaunchKernelGGL(prefill_kv16_kernel, dim3((unsigned)ntiles, (unsigned)p.n_kv, (unsigned)(p.head_dim / 32)), dim3(256), 0,
-                       s, p, ntiles);
-    GAJE_HIP_CHECK(hipGetLastError());
-    // key chunks of at least 128 keys (whole tiles), at most PREFILL_ATTN_CHUNKS of them
-    int64_t kch = (keys + PREFILL_ATTN_CHUNKS - 1) / PREFILL_ATTN_CHUNKS;
-    kch = kch < 128 ? 128 : (kch + 31) / 32 * 32;
+    const int conv = p.kv16_rope ? (int)((p.pos0 + 31) / 32) : ntiles;
+    if (conv > 0) {
+        hipLaunchKernelGGL(prefill_kv16_kernel, dim3((unsigned)conv, (unsigned)p.n_kv, (unsigned)(p.head_dim / 32)),
+                           dim3(256), 0, s, p, ntiles);
+        GAJE_HIP_CHECK(hipGetLastError());
+    }
+    const int64_t kch = prefill_attn_kch(keys);
     const int64_t nch = (keys + kch - 1) / kch;
     const dim3 grid((unsigned)((p.P + 15) / 16), (unsigned)p.n_head, (unsigned)nch);
     if (p.head_dim == 64) hipLaunchKernelGGL(prefill_attn_f16_kernel<64>, grid, dim3(64), 0, s, p, kch, ntiles);
     else hipLaunchKernelGGL(prefill_attn_f16_kernel<128>, grid, dim3(64), 0, s, p, kch, ntiles);
     GAJE_HIP_CHECK(hipGetLastError());
-    hipLaunchKernelGGL(prefill_attn_merge_kernel, dim3((unsigned)p.P, (unsigned)p.n_head), dim3(128), 0, s, p, kch);
-    GAJE_HIP_CHECK(hipGetLastError());
+    if (!p.merged_later) {
+        hipLaunchKernelGGL(prefill_attn_merge_kernel, dim3((unsigned)p.P, (unsigned)p.n_head), dim3(128), 0, s, p, kch);
+        GAJE_HIP_CHECK(hipGetLastError());
+    }
     return GAJE_OK;
 }
 
