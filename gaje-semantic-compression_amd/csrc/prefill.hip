@@ -382,6 +382,7 @@ int64_t prefill_kv16_halves(int64_t keys, int64_t n_kv, int64_t head_dim) {
 }
 
 // key chunks of at least 128 keys (whole 32-key tiles), at most PREFILL_ATTN_CHUNKS of them
+// (64-key chunks measured slower: 29.0 against 25.9 us per layer at 512 tokens)
 int64_t prefill_attn_kch(int64_t keys) {
     int64_t kch = (keys + PREFILL_ATTN_CHUNKS - 1) / PREFILL_ATTN_CHUNKS;
     return kch < 128 ? 128 : (kch + 31) / 32 * 32;
