@@ -110,7 +110,9 @@ int gaje_hip_q4_0_gemm(const void *packed, const float *X, const float *bias, in
  * linear/forward.rs:84-92,113-115) to about fp32 accuracy in a different
  * summation order.  `workspace` is 16-byte aligned device memory of at least
  * gaje_hip_q4_0_gemm_mfma_workspace(m, n, k) bytes (-1 for an invalid shape);
- * calls that share a workspace must not overlap. */
+ * it also holds the weight rows' codes as f16 MFMA fragments (about two bytes
+ * per weight), rebuilt from `packed` on each call; calls that share a
+ * workspace must not overlap. */
 int64_t gaje_hip_q4_0_gemm_mfma_workspace(int64_t m, int64_t n, int64_t k);
 int gaje_hip_q4_0_gemm_mfma(const void *packed, const float *X, const float *bias, int64_t bias_len,
                             float *Y, int64_t m, int64_t n, int64_t k, void *workspace,
