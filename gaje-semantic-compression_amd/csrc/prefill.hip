@@ -36,20 +36,45 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(PrefillRopeParams p) {
     const int hd = p.head_dim, half = hd >> 1;
     const int64_t q_rows = (int64_t)p.n_head * hd, kv_rows = (int64_t)p.n_kv * hd;
     if (p.part) {
-        const int64_t n_all = q_rows + 2 * kv_rows, pstride = p.P * p.ldq;
-        for (int64_t n = threadIdx.x; n < n_all; n += blockDim.x) {
-            const float *pp = p.part + t * p.ldq + n;
-            float v = pp[0];
-            for (int z0 = 1; z0 < p.nsplit; z0 += 8) {  // eight partials in flight, added in split order
-                float q[8];
+        // float4s, two per thread per round, every partial of a round in flight
+        // before any sum (the first nine; more are added after, in order)
+        const int64_t n4 = (q_rows + 2 * kv_rows) >> 2, pstride = p.P * p.ldq;
+        for (int64_t i0 = threadIdx.x; i0 < n4; i0 += 2 * blockDim.x) {
+            float4 sv[2], q[2][8];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) q[j] = pp[(int64_t)min(z0 + j, p.nsplit - 1) * pstride];
+            for (int u = 0; u < 2; ++u) {
+                const int64_t i = min(i0 + (int64_t)u * blockDim.x, n4 - 1);
+                const float *pp = p.part + t * p.ldq + 4 * i;
+                sv[u] = *(const float4 *)pp;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) v = z0 + j < p.nsplit ? v + q[j] : v;
+                for (int j = 0; j < 8; ++j) q[u][j] = *(const float4 *)(pp + (int64_t)min(1 + j, p.nsplit - 1) * pstride);
             }
-            v = flush_small(v);
-            if (n < p.bias_len) v = v + p.bias[n];
-            rowbuf[n] = v;
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int64_t i = i0 + (int64_t)u * blockDim.x;
+                if (i >= n4) continue;
+                float4 v = sv[u];
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (1 + j < p.nsplit) {
+                        v.x += q[u][j].x;
+                        v.y += q[u][j].y;
+                        v.z += q[u][j].z;
+                        v.w += q[u][j].w;
+                    }
+                for (int z = 9; z < p.nsplit; ++z) {
+                    const float4 r = *(const float4 *)(p.part + t * p.ldq + 4 * i + (int64_t)z * pstride);
+                    v.x += r.x;
+                    v.y += r.y;
+                    v.z += r.z;
+                    v.w += r.w;
+                }
+                float a[4] = {flush_small(v.x), flush_small(v.y), flush_small(v.z), flush_small(v.w)};
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (4 * i + j < p.bias_len) a[j] = a[j] + p.bias[4 * i + j];
+                *(float4 *)(rowbuf + 4 * i) = make_float4(a[0], a[1], a[2], a[3]);
+            }
         }
         __syncthreads();
         row = rowbuf;
@@ -95,6 +120,125 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(PrefillRopeParams p) {
         const float v = row[q_rows + kv_rows + j];
         p.v_cache[(vh * hd + d) * p.cap + pos] = v;
         if (v16) put_pair(v16 + ((vh * hd + d) * nt + (pos >> 5)) * 64 + slot, v);
+    }
+}
+
+// The prefill's RoPE and KV append by tiles of 32 tokens x one head (grid:
+// token tiles x (n_head + 2 n_kv) heads, q heads then k heads then v heads),
+// so that the cache's position-major rows and the attention's f16 pairs are
+// written along positions: the tile's values (from the qkv rows, or reduced
+// from the qkv product's split-K partials as gemm_reduce_kernel would: the
+// partials in split order, flush_small, bias) are staged in LDS; q and k
+// heads are rotated as rope_kv_kernel does (attention.rs:56-84, the decode
+// epilogue's rounding); q rows go to q_out, k and v to the cache at positions
+// pos0 + t and to kv16 (the layouts of prefill_kv16_kernel).
+__global__ __launch_bounds__(1024) void prefill_rope_kernel(PrefillRopeParams p) {
+    __shared__ float tile[32][129];  // [token][dimension], head_dim <= 128
+    const int tid = threadIdx.x, hd = p.head_dim, half = hd >> 1, hd4 = hd >> 2;
+    const int head = blockIdx.y;
+    const int64_t t0 = (int64_t)blockIdx.x * 32;
+    const int nt = (int)min((int64_t)32, p.P - t0);
+    const int64_t col0 = (int64_t)head * hd;
+    const int64_t q_rows = (int64_t)p.n_head * hd;
+    // ---- the tile: 32 x hd values, one float4 per thread (hd <= 128), all nine
+    // partial loads of a thread issued before any sum ----
+    const int k = tid;
+    if (k < 32 * hd4) {
+        const int r = k / hd4, c4 = k - r * hd4;
+        const int64_t t = t0 + min(r, nt - 1);
+        float4 v;
+        if (p.part) {
+            const int64_t pstride = p.P * p.ldq;
+            const float *pp = p.part + t * p.ldq + col0 + 4 * c4;
+            float4 q[8];
+            v = *(const float4 *)pp;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) q[j] = *(const float4 *)(pp + (int64_t)min(1 + j, p.nsplit - 1) * pstride);
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (1 + j < p.nsplit) {
+                    v.x += q[j].x;
+                    v.y += q[j].y;
+                    v.z += q[j].z;
+                    v.w += q[j].w;
+                }
+            for (int z = 9; z < p.nsplit; ++z) {
+                const float4 w = *(const float4 *)(pp + (int64_t)z * pstride);
+                v.x += w.x;
+                v.y += w.y;
+                v.z += w.z;
+                v.w += w.w;
+            }
+            float a[4] = {flush_small(v.x), flush_small(v.y), flush_small(v.z), flush_small(v.w)};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int64_t n = col0 + 4 * c4 + j;
+                if (n < p.bias_len) a[j] = a[j] + p.bias[n];
+            }
+            v = make_float4(a[0], a[1], a[2], a[3]);
+        } else {
+            v = *(const float4 *)(p.qkv + t * p.ldq + col0 + 4 * c4);
+        }
+        tile[r][4 * c4] = v.x;
+        tile[r][4 * c4 + 1] = v.y;
+        tile[r][4 * c4 + 2] = v.z;
+        tile[r][4 * c4 + 3] = v.w;
+    }
+    __syncthreads();
+    const bool is_q = head < p.n_head, is_v = head >= p.n_head + p.n_kv;
+    // ---- rotation of q and k heads, in place: pair (r, i), tokens fastest ----
+    if (!is_v) {
+        for (int k = tid; k < 32 * half; k += 1024) {
+            const int r = k & 31, i = k >> 5;
+            if (r >= nt) continue;
+            const int64_t pos = p.pos0 + t0 + r;
+            const int d0 = p.rope_split ? i : 2 * i;
+            const int d1 = p.rope_split ? i + half : 2 * i + 1;
+            const float y0 = tile[r][d0], y1 = tile[r][d1];
+            const float cs = p.rope_cos[pos * half + i], sn = p.rope_sin[pos * half + i];
+            const float a0 = y0 * cs, a1 = y1 * sn, a2 = y0 * sn, a3 = y1 * cs;
+            tile[r][d0] = a0 - a1;
+            tile[r][d1] = a2 + a3;
+        }
+        __syncthreads();
+    }
+    if (is_q) {  // q rows, dimensions fastest
+        for (int k = tid; k < 32 * hd; k += 1024) {
+            const int r = k / hd, d = k - r * hd;
+            if (r < nt) p.q_out[(t0 + r) * q_rows + col0 + d] = tile[r][d];
+        }
+        return;
+    }
+    const int64_t g = is_v ? head - p.n_head - p.n_kv : head - p.n_head;
+    float *cache = (is_v ? p.v_cache : p.k_cache) + g * hd * p.cap + p.pos0 + t0;
+    // the cache's rows [d][pos]: tokens fastest
+    for (int k = tid; k < 32 * hd; k += 1024) {
+        const int r = k & 31, d = k >> 5;
+        if (r < nt) cache[(int64_t)d * p.cap + r] = tile[r][d];
+    }
+    if (!p.kv16) return;
+    const int64_t ntl = p.kv16_ntiles;
+    auto put_pair = [](uint16_t *dst, float x) {
+        const _Float16 hi = (_Float16)x;
+        dst[0] = __builtin_bit_cast(uint16_t, hi);
+        dst[32] = __builtin_bit_cast(uint16_t, (_Float16)(x - (float)hi));
+    };
+    if (!is_v) {  // K16[g][pos][d / 32][hi 32 | lo 32]: dimensions fastest
+        uint16_t *k16 = p.kv16 + (g * ntl * 32 + p.pos0 + t0) * 2 * hd;
+        for (int k = tid; k < 32 * hd; k += 1024) {
+            const int r = k / hd, d = k - r * hd;
+            if (r < nt) put_pair(k16 + (int64_t)r * 2 * hd + (d >> 5) * 64 + (d & 31), tile[r][d]);
+        }
+    } else {  // V16[g][d][pos / 32][slot]: tokens fastest
+        uint16_t *v16 = p.kv16 + (int64_t)p.n_kv * ntl * 32 * 2 * hd + g * hd * ntl * 64;
+        for (int k = tid; k < 32 * hd; k += 1024) {
+            const int r = k & 31, d = k >> 5;
+            if (r >= nt) continue;
+            const int64_t pos = p.pos0 + t0 + r;
+            const int w = (int)(pos & 31);
+            const int slot = 8 * ((w & 15) >> 2) + 4 * (w >> 4) + (w & 3);
+            put_pair(v16 + ((int64_t)d * ntl + (pos >> 5)) * 64 + slot, tile[r][d]);
+        }
     }
 }
 
@@ -364,10 +508,17 @@ int launch_rope_kv(const PrefillRopeParams &p, hipStream_t s) {
     const int64_t row = (int64_t)(p.n_head + 2 * p.n_kv) * p.head_dim;
     if ((p.part || p.kv16) && (p.seq_pos || p.head_dim % 32))
         return set_error(GAJE_ERR_INVALID_ARG, "rope/kv: bad prefill arguments");
-    if (p.part && (p.nsplit < 1 || p.ldq < row || row * 4 > 65536 || p.bias_len < 0 || (p.bias_len > 0 && !p.bias)))
+    if (p.part && (p.nsplit < 1 || p.ldq < row || p.ldq % 4 || row * 4 > 65536 || p.bias_len < 0 || (p.bias_len > 0 && !p.bias) ||
+                   ((uintptr_t)p.part & 15)))
         return set_error(GAJE_ERR_INVALID_ARG, "rope/kv: bad split-K prologue");
     if (p.kv16 && (int64_t)p.kv16_ntiles * 32 < p.pos0 + p.P)
         return set_error(GAJE_ERR_INVALID_ARG, "rope/kv: f16 key tiles too few");
+    if (!p.seq_pos && p.head_dim <= 128 && p.head_dim % 4 == 0 && p.ldq % 4 == 0 && !((uintptr_t)p.qkv & 15)) {
+        hipLaunchKernelGGL(prefill_rope_kernel, dim3((unsigned)((p.P + 31) / 32), (unsigned)(p.n_head + 2 * p.n_kv)),
+                           dim3(1024), 0, s, p);
+        GAJE_HIP_CHECK(hipGetLastError());
+        return GAJE_OK;
+    }
     hipLaunchKernelGGL(rope_kv_kernel, dim3((unsigned)p.P), dim3(256), p.part ? (size_t)row * 4 : 0, s, p);
     GAJE_HIP_CHECK(hipGetLastError());
     return GAJE_OK;
