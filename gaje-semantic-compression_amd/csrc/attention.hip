@@ -12,17 +12,17 @@
 // The current token's k/v were appended by the fused QKV kernel, so the range
 // 0..pos is the causal window.
 //
-// Cache layout: K and V are both [kv head][dim][position].  A thread scoring
-// four consecutive positions reads one 16-byte quad of each key dimension's
-// row, so a wave's key loads are contiguous 1 KiB runs; an output dimension's
-// chain reads one contiguous V row.
+// Cache layout: K and V are both [kv head][dim][position].  A lane scoring
+// four consecutive positions reads one 16-byte quad of each of its key
+// dimensions' rows, so a wave's key loads are contiguous runs; an output
+// dimension's chain reads one contiguous V row.
 //
 // Scores, exponentials and products are computed in parallel over positions;
 // the two serial chains (the softmax sum, and each output dimension's
-// accumulation) run one lane per chain as the reference's loops do, reading
-// LDS.  A chain is bound by its own length, so the parallel work is spread over
-// several workgroups per head (one per slice of output dimensions) to keep the
-// loads that feed the chains short.
+// accumulation) keep the reference's order, one add at a time.  A chain is
+// bound by its own length, so the parallel work is spread over several
+// workgroups per head (one per slice of output dimensions) to keep the loads
+// that feed the chains short.
 #include "common.h"
 #include "device_util.h"
 
@@ -151,133 +151,342 @@ __device__ __forceinline__ float serial_sum(const float *e, int n) {
 __host__ __device__ constexpr int chain_len(int64_t ctx) { return (int)((ctx + 63) / 64 * 64); }
 __host__ __device__ constexpr int chain_row(int64_t cap) { return chain_len(cap) + 64; }
 
-// Streaming kernel: head dimension HD known at compile time (64 or 128),
-// capacity % 4 == 0.  Workgroup (h, slice) owns output dimensions
-// [slice*DS, slice*DS + DS) of query head h: it computes all of the head's
-// scores (one quad of positions per thread and round), and copies only its DS
-// rows of V into LDS with LDS-direct loads, so they land while the scores are
-// computed and both serial chains read LDS only.
 typedef __attribute__((address_space(3))) void lds_void;
 
+// v_mov_b32_dpp of a float (CTRL: quad_perm 0x00-0xFF, row_shl:n 0x100+n,
+// wave_ror:1 0x13C).  Lanes whose source lane lies outside the row get an
+// unspecified value; every use below reads only lanes with a valid source.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+
+// "Baton" chains: G = 64 / L serial sums run in one wave, the sum of chain g
+// being v_g[0] + v_g[1] + ... + v_g[32 P - 1] in order, rounded after every add.
+// At phase p (0 <= p < P) lane (g L + p) mod 64 holds chain g's running sum and
+// adds the 32 values v_g[32 p .. 32 p + 31] from its own registers; the first
+// of those adds takes the sum from the lane before (DPP wave_ror:1: lane i
+// reads lane i - 1), which hands each chain on to the next lane.  Every lane
+// executes every add (the sums held by the other lanes are discarded), so a
+// phase is 32 dependent adds with no LDS read in the chain.  Values are read
+// from LDS (chain g's row at base + g * stride, 16-byte aligned) one tile of L
+// phases ahead, lane j of region r = lane / L holding phase t L + j of chain
+// (r - t) mod G in tile t.  P is even and L a multiple of 4.  Returns each
+// lane's sum; chain g's result is in lane (g L + P - 1) mod 64.
+constexpr int BATON_KT = 32;  // values per lane and phase
+
+// acc = wave_ror1(acc) + x; the two wait states cover the VALU write of acc
+// that the DPP read follows.
+__device__ __forceinline__ float ror_add(float acc, float x) {
+    asm volatile("s_nop 1\n\tv_add_f32_dpp %0, %0, %1 wave_ror:1 row_mask:0xf bank_mask:0xf" : "+v"(acc) : "v"(x));
+    return acc;
+}
+
+struct NoWait {
+    __device__ void operator()(int) const {}
+};
+
+// ready(t) is called before tile t's values are read.
+template <int L, class Ready = NoWait>
+__device__ __forceinline__ float baton_chains(const float *base, int stride, int P, int lane, Ready ready = {}) {
+    constexpr int G = 64 / L, KT = BATON_KT;
+    const int r = lane / L, j = lane % L;
+    float va[KT], vb[KT];
+    auto load = [&](float (&v)[KT], int t) {
+        ready(t);
+        const int ph = min(t * L + j, P - 1);  // lanes past the last phase re-read it (unused)
+        const int g = ((r - t) % G + G) % G;
+        const float4 *src = (const float4 *)(base + g * stride + ph * KT);
+#pragma unroll
+        for (int i = 0; i < KT / 4; ++i) {
+            const float4 x = src[i];
+            v[4 * i] = x.x;
+            v[4 * i + 1] = x.y;
+            v[4 * i + 2] = x.z;
+            v[4 * i + 3] = x.w;
+        }
+    };
+    auto run = [&](const float (&v)[KT], int t, float acc) {
+        const int nph = min(L, P - t * L);
+        for (int q = 0; q < nph; q += 2) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                acc = ror_add(acc, v[0]);
+#pragma unroll
+                for (int i = 1; i < KT; ++i) acc = acc + v[i];
+            }
+        }
+        return acc;
+    };
+    float acc = 0.0f;  // +0 in every lane: the first hand-off passes +0 to each chain's first lane
+    const int T = (P + L - 1) / L;
+    load(va, 0);
+    for (int t = 0; t < T; t += 2) {
+        if (t + 1 < T) load(vb, t + 1);
+        acc = run(va, t, acc);
+        if (t + 1 >= T) break;
+        if (t + 2 < T) load(va, t + 2);
+        acc = run(vb, t + 1, acc);
+    }
+    return acc;
+}
+
+// Wide decode attention: head dimension HD (64 or 128) known at compile time,
+// kv_cap % 4 == 0, one workgroup of WIDE threads per (query head, slice of DS
+// output dimensions).
+//
+// Scores.  A quad of four consecutive positions is scored by LQ = HD / 16
+// lanes: lane m of the quad runs dot.rs's chains l = m and m + 4 (HD = 64) or
+// l = m (HD = 128) over the key dimensions 8c + l, so each lane keeps 16 key
+// loads (quads of rows of the [dim][position] cache) in flight, and the QW
+// quads of a wave sit in consecutive lanes so that each row's reads coalesce.
+// The horizontal sum ((a0 + a4) + (a1 + a5)) + ((a2 + a6) + (a3 + a7)) is
+// formed with lane shuffles: a_l + a_{l+4} in one lane (HD = 64) or across
+// lanes m ^ 4 (HD = 128), then the pair sums across lanes m ^ 1 and m ^ 2;
+// addition is commutative, so every lane of the quad holds the same four
+// totals, and lane m (m < 4) keeps position t4 + m.  The waves whose quads lie
+// below 512 positions issue their first-round key loads before the decode
+// state is read (up to the capacity), so that the state's latency hides behind
+// them; the others read the position first and load only quads below the
+// context.  Scores at or past the context are dropped.  Each wave takes q with
+// one load and lane shuffles, so no barrier precedes the dot products.
+//
+// Softmax and output.  The exponentials are formed in parallel; the softmax
+// sum (one chain) and the DS output dimensions' sums (DS chains) each run in
+// one wave as baton chains.  Four waves copy the slice's V rows into LDS with
+// LDS-direct loads while the softmax sum runs; the other waves then replace
+// them, tile by tile, by the products w_t * v_t[i] (w_t = e_t * inv rounded
+// first, +0 past the context) while wave 0 runs the output chains.
+constexpr int WIDE = 1024;
+
+template <int HD>
+struct WideShape {
+    static constexpr int LQ = HD / 16;        // lanes per quad of positions
+    static constexpr int QW = WAVE / LQ;      // quads per wave
+    static constexpr int CPL = 8 / LQ;        // dot chains per lane
+    static constexpr int NCH = HD / 8;        // 8-dimension chunks
+    static constexpr int NK = NCH * CPL;      // key quads (loads) per lane
+    static constexpr int PR = WIDE / LQ * 4;  // positions per round
+    static_assert(NK == 16, "16 key loads per lane");
+};
+
+// Key quads of one lane: k[c * CPL + h] is row 8c + m + 4h at byte offset off.
+template <int HD>
+__device__ __forceinline__ void wide_keys(float4 (&k)[16], const char *kb, uint32_t rowb, uint32_t off, int m) {
+    using S = WideShape<HD>;
+#pragma unroll
+    for (int c = 0; c < S::NCH; ++c)
+#pragma unroll
+        for (int h = 0; h < S::CPL; ++h) k[c * S::CPL + h] = *(const float4 *)(kb + (uint32_t)(8 * c + m + 4 * h) * rowb + off);
+}
+
+// dot_product(q, k_t) * scale for position t4 + (m & 3) (valid in lanes m < 4).
+// Lane m of a quad is lane m * QW + (quad % QW) of its wave.
+template <int HD>
+__device__ __forceinline__ float wide_score(const float4 (&k)[16], const float (&qv)[16], int m, float scale) {
+    using S = WideShape<HD>;
+    float acc[S::CPL][4];
+#pragma unroll
+    for (int h = 0; h < S::CPL; ++h)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[h][u] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < S::NCH; ++c)
+#pragma unroll
+        for (int h = 0; h < S::CPL; ++h) {
+            const int e = c * S::CPL + h;
+            acc[h][0] = fmaf(qv[e], k[e].x, acc[h][0]);
+            acc[h][1] = fmaf(qv[e], k[e].y, acc[h][1]);
+            acc[h][2] = fmaf(qv[e], k[e].z, acc[h][2]);
+            acc[h][3] = fmaf(qv[e], k[e].w, acc[h][3]);
+        }
+    float tot[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        float pair;  // a_l + a_{l+4}
+        if constexpr (S::CPL == 2) pair = acc[0][u] + acc[1][u];
+        else pair = acc[0][u] + __shfl_xor(acc[0][u], 4 * S::QW, WAVE);
+        const float s2 = pair + __shfl_xor(pair, S::QW, WAVE);  // (u0 + u1), (u2 + u3)
+        tot[u] = (s2 + __shfl_xor(s2, 2 * S::QW, WAVE)) * scale;
+    }
+    const int u = m & 3;
+    return u == 0 ? tot[0] : u == 1 ? tot[1] : u == 2 ? tot[2] : tot[3];
+}
+
 template <int HD, int DS>
-__global__ __launch_bounds__(THREADS) void attn_decode_fast(AttnParams p) {
+__global__ __launch_bounds__(WIDE) void attn_decode_wide(AttnParams p) {
+    using S = WideShape<HD>;
     extern __shared__ __align__(16) float smem[];
-    __shared__ float red[THREADS / WAVE];
+    __shared__ float red[WIDE / WAVE];
     __shared__ float inv_slot;
-    __shared__ uint64_t tab[32];  // the exponential's table, read from LDS
+    __shared__ uint64_t tab[32];              // the exponential's table, read from LDS
+    __shared__ int pdone[32];                 // producer waves done with each product tile
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int h = blockIdx.x;
-    const uint64_t tabv = tid < 32 ? kExp2Tab[tid] : 0;
-    int ctx = (int)p.ctx;
-    if (p.seq_pos) {  // batched decode: this block's sequence
-        const int z = blockIdx.z;
-        const int pos = p.seq_pos[z];
-        if (pos < 0) return;
-        ctx = pos + 1;
-        p.q += z * p.seq_q_stride;
-        p.out += z * p.seq_q_stride;
-        p.k_cache += z * p.seq_kv_stride;
-        p.v_cache += z * p.seq_kv_stride;
-    } else if (p.st) {
-        typedef int vi4 __attribute__((ext_vector_type(4)));
-        const vi4 s4 = *(const volatile vi4 *)p.st;  // pos, token, step, halted: one load
-        if (s4.w) return;                            // before any LDS-direct copy is in flight
-        ctx = s4.x + 1;
-    }
-
     const int d0 = blockIdx.y * DS;
     const int g = h / (p.n_head / p.n_head_kv);
     const float scale = 1.0f / sqrtf((float)HD);
     const int64_t cap = p.kv_cap;
-    const int n = chain_len(ctx);
-    const int vstride = chain_row(cap) + 4;  // LDS row stride of the V slice (bank spread)
-
-    float *sc = smem;                   // chain_row(cap) scores, then exponentials
-    float *vs = sc + chain_row(cap);    // DS rows of vstride: V, then the products
-    const float *qg = p.q + (size_t)h * HD;
-    // q: uniform (scalar) loads for HD = 64; a 128-float q does not fit the
-    // scalar registers (the compiler spills them), so it is read from LDS
-    __shared__ float qs[HD > 64 ? HD : 1];
-    if constexpr (HD > 64) {
-        if (tid < HD / 4) *(float4 *)(qs + 4 * tid) = *(const float4 *)(qg + 4 * tid);
-        __syncthreads();
-    }
     const float *Kh = p.k_cache + (size_t)g * p.kv_head_stride;
     const float *Vh = p.v_cache + (size_t)g * p.kv_head_stride + (size_t)d0 * cap;
-
-    // ---- scores: thread j takes positions 4j..4j+3 of each round; key
-    // dimension d of those positions is one quad of row d (a 32-bit byte
-    // offset walks the rows).  RING 8-dimension chunks of the quads are in
-    // flight ahead of the FMAs.  A quad that runs past ctx stays inside the row
-    // (kv_cap % 4 == 0); its extra lanes are dropped.  q is read with uniform
-    // loads ----
     const uint32_t rowb = (uint32_t)cap * 4;
-    float mx = -INFINITY;
-    for (int t4 = 4 * tid; t4 < ctx; t4 += 4 * THREADS) {
-        float acc[4][8];
-        key_round<HD>(acc, (const char *)Kh, rowb, (uint32_t)t4 * 4, qg, qs);
+    // lane m of quad `quad`: the QW quads of a wave are its lanes 0..QW-1, so that
+    // QW lanes read consecutive quads of one key row (coalesced 16-byte reads)
+    const int m = lane / S::QW, quad = wave * S::QW + lane % S::QW;
+
+    // ---- issue: the decode state, q, the first round of key quads ----
+    typedef int vi4 __attribute__((ext_vector_type(4)));
+    vi4 s4 = {0, 0, 0, 0};
+    // pos, token, step, halted: one vector load, waited for only where it is
+    // used (nothing writes the state during this kernel).  A volatile load would
+    // be waited for at once, and a scalar load shares its wait count with the
+    // kernel arguments, so the address is moved into VGPRs.
+    if (p.st) {
+        uint64_t sp = (uint64_t)(uintptr_t)p.st;
+        asm volatile("" : "+v"(sp));
+        s4 = *(const __attribute__((address_space(1))) vi4 *)sp;
+    }
+    // q: every wave loads the head's q (lane i element i, and 64 + i for HD =
+    // 128) and hands each lane its 16 values with lane shuffles, so no barrier
+    // stands between the key loads and the dot products
+    const float qa = p.q[(size_t)h * HD + lane];
+    const float qb = HD > 64 ? p.q[(size_t)h * HD + 64 + lane] : 0.0f;
+    const uint64_t tabv = tid < 32 ? kExp2Tab[tid] : 0;
+    // Round 0.  The waves whose quads start below SPEC positions load them before
+    // the context is known (up to the capacity; a quad past it re-reads the last
+    // quad below it), so that the state's latency hides behind their loads; the
+    // other waves wait for the state and load only quads below the context.
+    constexpr int SPEC = 512;
+    const int wpos = wave * S::QW * 4;
+    float4 k[16];
+    if (p.st && wpos < SPEC) {
+        const int lim0 = (int)min(cap, (int64_t)S::PR);
+        wide_keys<HD>(k, (const char *)Kh, rowb, (uint32_t)min(4 * quad, lim0 - 4) * 4, m);
+    } else {
+        // the position through the scalar cache: a vector load would queue behind
+        // the other waves' key loads
+        int pos = 0;
+        if (p.st) asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(pos) : "s"(p.st) : "memory");
+        const int c1 = p.st ? (int)min((int64_t)max(pos + 1, 1), cap) : (int)p.ctx;
+        if (wpos < c1) {
+            const int lim0 = min((c1 + 3) & ~3, S::PR);
+            wide_keys<HD>(k, (const char *)Kh, rowb, (uint32_t)min(4 * quad, lim0 - 4) * 4, m);
+        } else {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const float u0 = acc[u][0] + acc[u][4], u1 = acc[u][1] + acc[u][5];
-            const float u2 = acc[u][2] + acc[u][6], u3 = acc[u][3] + acc[u][7];
-            const float s = ((u0 + u1) + (u2 + u3)) * scale;
-            if (t4 + u < ctx) {
-                sc[t4 + u] = s;
-                mx = fmaxf(mx, s);  // NaN never wins, as with the reference's '>'
-            }
+            for (int i = 0; i < 16; ++i) k[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         }
     }
-    // ---- V slice -> LDS, issued by the last wave once its scores are done
-    // (the first 768 positions leave it none), so the other waves' key loads
-    // never wait behind the copies (loads complete in order).  One wave
-    // instruction copies 256 positions of a row (lane i its quad i); quads at or
-    // past ctx are not copied, and a copied quad ends before the row's capacity
-    // (kv_cap % 4 == 0) ----
-    if (wave == THREADS / WAVE - 1) {
-        const int nchunk = (ctx + 255) >> 8;
-        for (int j = 0; j < DS; ++j)
-            for (int ch = 0; ch < nchunk; ++ch) {
-                const int t = ch * 256 + lane * 4;
-                if (t < ctx)
-                    __builtin_amdgcn_global_load_lds((const void *)(Vh + (size_t)j * cap + t),
-                                                     (lds_void *)(vs + j * vstride + ch * 256), 16, 0, 0);
-            }
+    float qv[16];  // qv[c * CPL + h] = q[8c + m + 4h]
+#pragma unroll
+    for (int c = 0; c < S::NCH; ++c)
+#pragma unroll
+        for (int hh = 0; hh < S::CPL; ++hh) {
+            const int j0 = 8 * c + 4 * hh;  // + m
+            qv[c * S::CPL + hh] = __shfl(j0 < 64 ? qa : qb, (j0 & 63) + m, WAVE);
+        }
+    if (tid < 32) tab[tid] = tabv;  // (published by the barrier after the scores)
+    int ctx = (int)p.ctx;
+    if (p.st) {  // (the state is uniform: readfirstlane keeps the loop bounds scalar)
+        if (__builtin_amdgcn_readfirstlane(s4.w)) return;  // halted: nothing of this step runs
+        ctx = __builtin_amdgcn_readfirstlane(s4.x) + 1;
     }
-    if (tid < 32) tab[tid] = tabv;
-    __builtin_amdgcn_s_waitcnt(0);  // this thread's LDS-direct copies have landed
-    const float max_s = block_max(mx, red);  // (its barrier publishes them to the block)
+    const int n = chain_len(ctx);
+    const int vstride = chain_row(cap) + 4;  // LDS row stride of the V slice (bank spread)
+    float *sc = smem;                        // chain_row(cap) scores, then exponentials
+    float *vs = sc + chain_row(cap);         // DS rows of vstride: V, then the products
+
+    // ---- scores ----
+    float mx = -INFINITY;
+    for (int t0 = 0;;) {
+        const float s = wide_score<HD>(k, qv, m, scale);
+        const int t = t0 + 4 * quad + (m & 3);
+        if (m < 4 && t < ctx) {
+            sc[t] = s;
+            mx = fmaxf(mx, s);  // NaN never wins, as with the reference's '>'
+        }
+        t0 += S::PR;
+        if (t0 >= ctx) break;
+        wide_keys<HD>(k, (const char *)Kh, rowb, (uint32_t)min(t0 + 4 * quad, ((ctx + 3) & ~3) - 4) * 4, m);
+    }
+    mx = wave_max(mx);
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    float max_s = red[0];
+#pragma unroll
+    for (int w = 1; w < WIDE / WAVE; ++w) max_s = fmaxf(max_s, red[w]);
 
     // exponentials, +0 up to the padded chain length
-    for (int t = tid; t < n; t += THREADS) sc[t] = t < ctx ? expf_ref_t(sc[t] - max_s, tab) : 0.0f;
+    for (int t = tid; t < n; t += WIDE) sc[t] = t < ctx ? expf_ref_t(sc[t] - max_s, tab) : 0.0f;
+    if (tid < 32) pdone[tid] = 0;
     __syncthreads();
-    if (tid == 0) inv_slot = 1.0f / (chain_lds(0.0f, sc, n) + 1e-12f);
+    const int P = n / BATON_KT;
+    if (wave == 0) {
+        const float acc = baton_chains<64>(sc, 0, P, lane);
+        const float sum = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), (P - 1) & 63));
+        if (lane == 0) inv_slot = 1.0f / (sum + 1e-12f);
+    }
+    // ---- V slice -> LDS (waves 12..15, lane i copies quad i of a 256-position
+    // chunk; quads at or past ctx are not copied, a copied quad ends before the
+    // row's capacity).  Issued while wave 0 runs the softmax sum, once the key
+    // loads are done (so that they do not queue behind them) ----
+    constexpr int VW = 4;
+    if (wave >= WIDE / WAVE - VW) {
+        const int nchunk = (ctx + 255) >> 8;
+        for (int task = wave - (WIDE / WAVE - VW); task < DS * nchunk; task += VW) {
+            const int j = task / nchunk, ch = task - j * nchunk;
+            const int t = ch * 256 + lane * 4;
+            if (t < ctx)
+                __builtin_amdgcn_global_load_lds((const void *)(Vh + (size_t)j * cap + t),
+                                                 (lds_void *)(vs + j * vstride + ch * 256), 16, 0, 0);
+        }
+    }
+
+    __builtin_amdgcn_s_waitcnt(0);  // the V copies of this thread have landed
     __syncthreads();
     const float inv = inv_slot;
 
-    // products w_t * v_t[i] in place, w_t = e_t * inv rounded first; +0 past ctx
-    for (int t = 4 * tid; t < n; t += 4 * THREADS) {
-        const float4 e = *(const float4 *)(sc + t);
-        const float w[4] = {e.x * inv, e.y * inv, e.z * inv, e.w * inv};
-#pragma unroll
-        for (int j = 0; j < DS; ++j) {
-            float4 &v4 = *(float4 *)(vs + j * vstride + t);
-            const float4 v = v4;
-            v4 = make_float4(t < ctx ? w[0] * v.x : 0.0f, t + 1 < ctx ? w[1] * v.y : 0.0f,
-                             t + 2 < ctx ? w[2] * v.z : 0.0f, t + 3 < ctx ? w[3] * v.w : 0.0f);
+    // ---- products w_t * v_t[i] in place (w_t = e_t * inv rounded first; +0
+    // past ctx), formed by waves 1..15 tile by tile in the order the output
+    // chains read them (a tile: positions [t TP, t TP + TP) of every row), each
+    // wave counting the tiles it has written in pdone; wave 0 runs the DS output
+    // chains and waits for a tile's count before reading it.  The producers wait
+    // for nothing, so every wait ends. ----
+    constexpr int L = 64 / DS, TP = L * BATON_KT, NPROD = WIDE / WAVE - 1;
+    static_assert((TP & 3) == 0, "tiles of whole quads");
+    const int nq = n >> 2, T = (n + TP - 1) / TP;  // T <= 32: n <= 64 TP (the capacity check bounds n)
+    if (wave != 0) {
+        for (int t = 0; t < T; ++t) {
+            const int qa = t * (TP / 4), nt = min(nq - qa, TP / 4);
+            for (int task = tid - WAVE; task < DS * nt; task += WIDE - WAVE) {
+                const int j = task % DS, t4 = 4 * (qa + task / DS);
+                const float4 e = *(const float4 *)(sc + t4);
+                float4 &v4 = *(float4 *)(vs + j * vstride + t4);
+                const float4 v = v4;
+                v4 = make_float4(t4 < ctx ? (e.x * inv) * v.x : 0.0f, t4 + 1 < ctx ? (e.y * inv) * v.y : 0.0f,
+                                 t4 + 2 < ctx ? (e.z * inv) * v.z : 0.0f, t4 + 3 < ctx ? (e.w * inv) * v.w : 0.0f);
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // this wave's writes of the tile come first
+            if (lane == 0) __hip_atomic_fetch_add(&pdone[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
+    } else {
+        // ---- out_i = sum_t products, DS chains in wave 0 ----
+        auto ready = [&](int t) {
+            while (__hip_atomic_load(&pdone[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < NPROD)
+                __builtin_amdgcn_s_sleep(1);
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        };
+        const float acc = baton_chains<L>(vs, vstride, P, lane, ready);
+        const int rel = (lane - (P - 1)) & 63;
+        if (rel % L == 0) p.out[(size_t)h * HD + d0 + rel / L] = acc;
     }
-    __syncthreads();
-
-    // ---- out_i = sum_t products, one chain per output dimension ----
-    if (tid < DS) p.out[(size_t)h * HD + d0 + tid] = chain_lds(0.0f, vs + tid * vstride, n);
 }
 
 // Batched decode (several sequences per launch): one workgroup per (query
 // head, sequence) computes the head's scores once; after the softmax each
 // output dimension's chain runs in its own thread (threads 0..HD-1), reading
 // its V row straight from memory (the row is contiguous and the loads run
-// ahead of the adds).  Same rounding sequence as attn_decode_fast.
+// ahead of the adds).  Same rounding sequence as attn_decode_wide.
 template <int HD>
 __global__ __launch_bounds__(THREADS) void attn_decode_batch(AttnParams p) {
     extern __shared__ __align__(16) float smem[];  // chain_row(cap): scores, exponentials, weights
@@ -306,7 +515,7 @@ __global__ __launch_bounds__(THREADS) void attn_decode_batch(AttnParams p) {
         __syncthreads();
     }
 
-    // scores: thread j takes positions 4j..4j+3 of each round (as attn_decode_fast)
+    // scores: thread j takes positions 4j..4j+3 of each round
     const uint32_t rowb = (uint32_t)cap * 4;
     float mx = -INFINITY;
     for (int t4 = 4 * tid; t4 < ctx; t4 += 4 * THREADS) {
@@ -371,10 +580,13 @@ __global__ __launch_bounds__(THREADS) void attn_decode_batch(AttnParams p) {
 // Output dimensions per workgroup of the streaming kernel for this capacity,
 // or 0 if even one V row does not fit.
 size_t fast_lds_bytes(int64_t cap, int ds) { return (size_t)(chain_row(cap) + (size_t)ds * (chain_row(cap) + 4)) * 4; }
+// The wide kernel's slice: the largest DS whose rows fit LDS, with at most 32
+// product tiles of 64 / DS * BATON_KT positions (its per-tile counters).
 int fast_slice(int head_dim, int64_t cap) {
     for (int ds = 8; ds >= 1; ds >>= 1) {
         if (head_dim % ds) continue;
-        if (fast_lds_bytes(cap, ds) + 1024 <= max_lds_per_block()) return ds;
+        if (fast_lds_bytes(cap, ds) + 1024 <= max_lds_per_block() && chain_len(cap) <= 32 * (64 / ds) * BATON_KT)
+            return ds;
     }
     return 0;
 }
@@ -483,10 +695,10 @@ int launch_attention(const AttnParams &p, hipStream_t s) {
         const size_t flds = fast_lds_bytes(p.kv_cap, ds);
         void (*fn)(AttnParams);
         if (p.head_dim == 64)
-            fn = ds == 8 ? attn_decode_fast<64, 8> : ds == 4 ? attn_decode_fast<64, 4> : ds == 2 ? attn_decode_fast<64, 2> : attn_decode_fast<64, 1>;
+            fn = ds == 8 ? attn_decode_wide<64, 8> : ds == 4 ? attn_decode_wide<64, 4> : ds == 2 ? attn_decode_wide<64, 2> : attn_decode_wide<64, 1>;
         else
-            fn = ds == 8 ? attn_decode_fast<128, 8> : ds == 4 ? attn_decode_fast<128, 4> : ds == 2 ? attn_decode_fast<128, 2> : attn_decode_fast<128, 1>;
-        hipLaunchKernelGGL(fn, dim3(p.n_head, p.head_dim / ds, nz), dim3(THREADS), flds, s, p);
+            fn = ds == 8 ? attn_decode_wide<128, 8> : ds == 4 ? attn_decode_wide<128, 4> : ds == 2 ? attn_decode_wide<128, 2> : attn_decode_wide<128, 1>;
+        hipLaunchKernelGGL(fn, dim3(p.n_head, p.head_dim / ds, nz), dim3(WIDE), flds, s, p);
     } else {
         hipLaunchKernelGGL(attn_decode_generic, dim3(p.n_head, 1, nz), dim3(THREADS), lds, s, p);
     }
