@@ -482,6 +482,239 @@ __global__ __launch_bounds__(WIDE) void attn_decode_wide(AttnParams p) {
     }
 }
 
+// Bounded spin on an LDS counter: returns once *c >= target.  The producers
+// and consumers below wait on each other only along a chain that always ends
+// (see attn_batch_wide), so the bound is never reached; it keeps a mistake
+// from turning into a hang (the results would then be wrong, not late).
+__device__ __forceinline__ void lds_wait_ge(int *c, int target) {
+    for (int spin = 0; spin < (1 << 22); ++spin) {
+        if (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+// Batched decode, wide form: one workgroup of WIDE threads per (query head,
+// sequence).  Scores, exponentials and the softmax sum as attn_decode_wide
+// (the context is known from seq_pos, so no load is speculative).  The output
+// then streams V through a ring of BW_NB LDS tiles of BW_TP(HD) positions x HD
+// rows: waves 4..15 (producers) load the V rows with coalesced reads BW_D
+// tiles ahead (the first BW_D during the softmax sum), form the products w_t * v_t[i] (w_t = e_t * inv rounded first,
+// +0 past the context) into buffer t % BW_NB and count the tile in ready[];
+// waves 0..3 run HD / 4 output chains each as baton chains over the tiles and
+// count each tile in freed[] once its values are in registers.  A producer
+// waits for buffer t % BW_NB to be freed by tile t - BW_NB, and a chain wave
+// for tile t to be ready; since the chains never wait for a tile past the one
+// after the tile they run, and BW_NB >= 2, every wait ends.
+constexpr int BW_NB = 3;      // tile buffers
+constexpr int BW_NCW = 4;     // chain waves
+constexpr int BW_D = 6;       // V tiles in flight per producer thread (registers)
+template <int HD> struct BwShape {
+    static constexpr int G = HD / BW_NCW;          // chains per chain wave
+    static constexpr int L = WAVE / G;             // lanes per chain
+    static constexpr int TP = L * BATON_KT;        // positions per tile
+    static constexpr int TPS = TP + 4;             // LDS row stride (bank spread)
+    static constexpr int TILE = HD * TPS;          // floats per buffer
+    static constexpr int NPW = WIDE / WAVE - BW_NCW;  // producer waves
+    static constexpr int TASKS = HD * TP / 4;      // float4 products per tile
+    static constexpr int PT = (TASKS + NPW * WAVE - 1) / (NPW * WAVE);  // per producer thread
+};
+size_t batch_wide_lds_bytes(int head_dim, int64_t cap) {
+    const int64_t tile = head_dim == 64 ? BwShape<64>::TILE : BwShape<128>::TILE;
+    return (size_t)(chain_row(cap) + BW_NB * tile) * 4;
+}
+
+template <int HD>
+__global__ __launch_bounds__(WIDE) void attn_batch_wide(AttnParams p) {
+    using S = WideShape<HD>;
+    using B = BwShape<HD>;
+    extern __shared__ __align__(16) float smem[];
+    __shared__ float red[WIDE / WAVE];
+    __shared__ float inv_slot;
+    __shared__ uint64_t tab[32];
+    __shared__ int ready[BW_NB], freed[BW_NB], inv_flag;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // XCD-aware order: workgroup i runs on XCD i % 8, and the R = n_head / n_kv
+    // query heads of one (kv head, sequence) group take ids of one residue, so
+    // they share an L2 and its K/V rows are fetched from memory once
+    const int R = p.n_head / p.n_head_kv, id = blockIdx.x, slot = id >> 3;
+    const int group = (slot / R) * 8 + (id & 7);
+    if (group >= p.n_head_kv * p.n_seq) return;  // padding of the grid (uniform)
+    const int g = group % p.n_head_kv, z = group / p.n_head_kv, h = g * R + slot % R;
+    const int pos = p.seq_pos[z];
+    if (pos < 0) return;  // (uniform)
+    const int ctx = pos + 1;
+    const float *q = p.q + z * p.seq_q_stride + (size_t)h * HD;
+    const float scale = 1.0f / sqrtf((float)HD);
+    const int64_t cap = p.kv_cap;
+    const float *Kh = p.k_cache + z * p.seq_kv_stride + (size_t)g * p.kv_head_stride;
+    const float *Vh = p.v_cache + z * p.seq_kv_stride + (size_t)g * p.kv_head_stride;
+    const uint32_t rowb = (uint32_t)cap * 4;
+    const int m = lane / S::QW, quad = wave * S::QW + lane % S::QW;
+    const int n = chain_len(ctx);
+    float *sc = smem;                  // chain_row(cap) scores, then exponentials
+    float *tiles = sc + chain_row(cap);  // [BW_NB][HD][TPS] products
+
+    const float qa = q[lane];
+    const float qb = HD > 64 ? q[64 + lane] : 0.0f;
+    if (tid < 32) tab[tid] = kExp2Tab[tid];
+    if (tid < BW_NB) ready[tid] = freed[tid] = 0;
+    if (tid == 0) inv_flag = 0;
+    float4 k[16];
+    const int ctx4 = (ctx + 3) & ~3;
+    if (wave * S::QW * 4 < ctx)
+        wide_keys<HD>(k, (const char *)Kh, rowb, (uint32_t)min(4 * quad, min(ctx4, S::PR) - 4) * 4, m);
+    else
+#pragma unroll
+        for (int i = 0; i < 16; ++i) k[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float qv[16];
+#pragma unroll
+    for (int c = 0; c < S::NCH; ++c)
+#pragma unroll
+        for (int hh = 0; hh < S::CPL; ++hh) {
+            const int j0 = 8 * c + 4 * hh;
+            qv[c * S::CPL + hh] = __shfl(j0 < 64 ? qa : qb, (j0 & 63) + m, WAVE);
+        }
+
+    // ---- scores ----
+    float mx = -INFINITY;
+    for (int t0 = 0;;) {
+        const float sv = wide_score<HD>(k, qv, m, scale);
+        const int t = t0 + 4 * quad + (m & 3);
+        if (m < 4 && t < ctx) {
+            sc[t] = sv;
+            mx = fmaxf(mx, sv);
+        }
+        t0 += S::PR;
+        if (t0 >= ctx) break;
+        wide_keys<HD>(k, (const char *)Kh, rowb, (uint32_t)min(t0 + 4 * quad, ctx4 - 4) * 4, m);
+    }
+    mx = wave_max(mx);
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    float max_s = red[0];
+#pragma unroll
+    for (int w = 1; w < WIDE / WAVE; ++w) max_s = fmaxf(max_s, red[w]);
+    for (int t = tid; t < n; t += WIDE) sc[t] = t < ctx ? expf_ref_t(sc[t] - max_s, tab) : 0.0f;
+
+    const int T = (n + B::TP - 1) / B::TP;
+    const int P = n / BATON_KT;
+    __syncthreads();  // the exponentials (and the counters' zeros) are in LDS
+
+    if (wave >= BW_NCW) {
+        // ---- producers: the first BW_D tiles' V loads go out while wave 0 runs
+        // the softmax sum; the products wait for inv (inv_flag) ----
+        const int pt = tid - BW_NCW * WAVE;  // producer thread index (waves 4..15)
+        float4 vr[BW_D][B::PT];
+        auto loadV = [&](float4 (&v)[B::PT], int t) {
+#pragma unroll
+            for (int i = 0; i < B::PT; ++i) {
+                const int task = pt + i * B::NPW * WAVE;
+                const int row = task / (B::TP / 4), q4 = task % (B::TP / 4);
+                const int t4 = t * B::TP + 4 * q4;
+                v[i] = task < B::TASKS && t4 < ctx ? *(const float4 *)(Vh + (size_t)row * cap + t4)
+                                                   : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
+        };
+#pragma unroll
+        for (int d = 0; d < BW_D; ++d)
+            if (d < T) loadV(vr[d], d);
+        lds_wait_ge(&inv_flag, 1);
+        const float inv = inv_slot;
+        auto produce = [&](const float4 (&v)[B::PT], int t) {
+            const int b = t % BW_NB;
+            if (t >= BW_NB) lds_wait_ge(&freed[b], BW_NCW * (t / BW_NB));
+            float *dst = tiles + b * B::TILE;
+#pragma unroll
+            for (int i = 0; i < B::PT; ++i) {
+                const int task = pt + i * B::NPW * WAVE;
+                if (task >= B::TASKS) continue;
+                const int row = task / (B::TP / 4), q4 = task % (B::TP / 4);
+                const int t4 = t * B::TP + 4 * q4;
+                const float4 e = *(const float4 *)(sc + min(t4, n - 4));
+                const float4 x = v[i];
+                *(float4 *)(dst + row * B::TPS + 4 * q4) =
+                    make_float4(t4 < ctx ? (e.x * inv) * x.x : 0.0f, t4 + 1 < ctx ? (e.y * inv) * x.y : 0.0f,
+                                t4 + 2 < ctx ? (e.z * inv) * x.z : 0.0f, t4 + 3 < ctx ? (e.w * inv) * x.w : 0.0f);
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            if (lane == 0) __hip_atomic_fetch_add(&ready[b], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        };
+        for (int t0 = 0; t0 < T; t0 += BW_D) {
+#pragma unroll
+            for (int d = 0; d < BW_D; ++d) {
+                const int t = t0 + d;
+                if (t < T) {
+                    produce(vr[d], t);
+                    if (t + BW_D < T) loadV(vr[d], t + BW_D);
+                }
+            }
+        }
+        return;
+    }
+
+    if (wave == 0) {  // the softmax sum; inv is published through inv_flag
+        const float acc = baton_chains<64>(sc, 0, P, lane);
+        const float sum = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), (P - 1) & 63));
+        if (lane == 0) {
+            inv_slot = 1.0f / (sum + 1e-12f);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            __hip_atomic_store(&inv_flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+    }
+
+    // ---- chain waves: chains wave * G .. wave * G + G - 1 (output dimensions) ----
+    {
+        constexpr int L = B::L, G = B::G, KT = BATON_KT;
+        const int r = lane / L, j = lane % L;
+        float xa[KT], xb[KT];
+        auto load = [&](float (&x)[KT], int t) {
+            lds_wait_ge(&ready[t % BW_NB], B::NPW * (t / BW_NB + 1));
+            const int jj = min(j, P - 1 - t * L);  // lanes past the last phase re-read it (unused)
+            const int gg = ((r - t) % G + G) % G;
+            const float4 *src = (const float4 *)(tiles + (t % BW_NB) * B::TILE + (wave * G + gg) * B::TPS + jj * KT);
+#pragma unroll
+            for (int i = 0; i < KT / 4; ++i) {
+                const float4 v = src[i];
+                x[4 * i] = v.x;
+                x[4 * i + 1] = v.y;
+                x[4 * i + 2] = v.z;
+                x[4 * i + 3] = v.w;
+            }
+        };
+        auto run = [&](const float (&x)[KT], int t, float acc) {
+            const int nph = min(L, P - t * L);
+            for (int qq = 0; qq < nph; qq += 2) {
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    acc = ror_add(acc, x[0]);
+#pragma unroll
+                    for (int i = 1; i < KT; ++i) acc = acc + x[i];
+                }
+            }
+            // this tile's values are in registers (the adds used them): its buffer is free
+            if (lane == 0) __hip_atomic_fetch_add(&freed[t % BW_NB], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            return acc;
+        };
+        const int Tc = (P + L - 1) / L;  // == T
+        float acc = 0.0f;
+        load(xa, 0);
+        for (int t = 0; t < Tc; t += 2) {
+            if (t + 1 < Tc) load(xb, t + 1);
+            acc = run(xa, t, acc);
+            if (t + 1 >= Tc) break;
+            if (t + 2 < Tc) load(xa, t + 2);
+            acc = run(xb, t + 1, acc);
+        }
+        const int rel = (lane - (P - 1)) & 63;
+        if (rel % L == 0) {
+            const int64_t i = (int64_t)h * HD + wave * G + rel / L, rows = (int64_t)p.n_head * HD;
+            p.out[z * p.seq_q_stride + (p.out_chain_major ? (i & 7) * (rows / 8) + (i >> 3) : i)] = acc;
+        }
+    }
+}
+
 // Batched decode (several sequences per launch): one workgroup per (query
 // head, sequence) computes the head's scores once; after the softmax each
 // output dimension's chain runs in its own thread (threads 0..HD-1), reading
@@ -682,6 +915,15 @@ int launch_attention(const AttnParams &p, hipStream_t s) {
         return set_error(GAJE_ERR_INVALID_ARG, "attention: chain-major output needs a batch and n_head*head_dim %% 8 == 0");
     const bool batch_kernel = p.seq_pos && p.kv_cap % 4 == 0 && (p.head_dim == 64 || p.head_dim == 128) &&
                               (size_t)chain_row(p.kv_cap) * 4 + 1024 <= max_lds_per_block();
+    if (batch_kernel && batch_wide_lds_bytes(p.head_dim, p.kv_cap) + 1024 <= max_lds_per_block()) {
+        const size_t blds = batch_wide_lds_bytes(p.head_dim, p.kv_cap);
+        const int64_t groups = (int64_t)p.n_head_kv * nz, R = p.n_head / p.n_head_kv;
+        const dim3 grid((unsigned)((groups + 7) / 8 * 8 * R));  // ids: (8 groups) x R per block of rows
+        if (p.head_dim == 64) hipLaunchKernelGGL(attn_batch_wide<64>, grid, dim3(WIDE), blds, s, p);
+        else hipLaunchKernelGGL(attn_batch_wide<128>, grid, dim3(WIDE), blds, s, p);
+        GAJE_HIP_CHECK(hipGetLastError());
+        return GAJE_OK;
+    }
     if (batch_kernel) {
         const size_t blds = (size_t)chain_row(p.kv_cap) * 4;
         if (p.head_dim == 64) hipLaunchKernelGGL(attn_decode_batch<64>, dim3(p.n_head, 1, nz), dim3(THREADS), blds, s, p);
