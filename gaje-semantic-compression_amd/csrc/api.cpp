@@ -528,6 +528,225 @@ extern "C" int gaje_hip_moe_ffn(const float *x, int64_t T, int64_t h, const floa
     return GAJE_OK;
 }
 
+namespace {
+
+// The prepared experts of gaje_hip_moe_prepare: for each of the two products
+// (gate_up: N = 2 ffn, K = h; down: N = h, K = ffn) every expert's code
+// fragments, fragment scales and dense block mins (the block-scaled product's
+// weight operands), one expert after the other at fixed strides.
+struct MoePrepared {
+    int64_t wf_stride[2], wsc_stride[2], mins_stride[2], ldm[2];
+    uint16_t *wf[2];
+    float *wsc[2];
+    uint16_t *mins[2];
+    size_t bytes;
+};
+
+MoePrepared moe_prepared(char *base, int64_t h, int64_t ffn, int64_t E) {
+    MoePrepared w{};
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        char *p = base + off;
+        off = align256(off + bytes);
+        return p;
+    };
+    const int64_t NN[2] = {2 * ffn, h}, KK[2] = {h, ffn};
+    for (int i = 0; i < 2; ++i) {
+        w.ldm[i] = gemm_bs_sum_cols(KK[i]);
+        w.wf_stride[i] = (q4_frag_halves(NN[i], KK[i]) + 511) / 512 * 512;
+        w.wsc_stride[i] = (q4_frag_scale_floats(NN[i], KK[i]) + 63) / 64 * 64;
+        w.mins_stride[i] = (NN[i] * w.ldm[i] + 127) / 128 * 128;
+        w.wf[i] = (uint16_t *)take((size_t)(E * w.wf_stride[i]) * 2);
+        w.wsc[i] = (float *)take((size_t)(E * w.wsc_stride[i]) * 4);
+        w.mins[i] = (uint16_t *)take((size_t)(E * w.mins_stride[i]) * 2);
+    }
+    w.bytes = off;
+    return w;
+}
+
+// Workspace of gaje_hip_moe_ffn_prepared: the routing, the block-scaled
+// activation planes of the dispatched rows, the two products' results and
+// their split-K partials.
+struct MoeBsWorkspace {
+    int32_t *top_idx, *rows, *slot, *counts, *offsets;
+    float *top_w;
+    uint16_t *xh, *sh, *sl;          // [plane_rows][2 kmax], [2T][ldsum] x 2
+    int64_t plane_rows, ldsum;
+    int *ex;                         // [2T]
+    float *GU, *Y, *part;            // [2T][2 ffn], [2T][h], split-K partials
+    GemmBsPlan pgu, pdn;
+    size_t bytes;
+};
+
+MoeBsWorkspace moe_bs_workspace(char *base, int64_t T, int64_t h, int64_t ffn, int64_t E) {
+    MoeBsWorkspace w{};
+    const int64_t R = 2 * T, kmax = std::max(h, ffn);
+    w.pgu = plan_gemm_q4_bs_grouped(R, E, T, 2 * ffn, h);
+    w.pdn = plan_gemm_q4_bs_grouped(R, E, T, h, ffn);
+    const int64_t mt = BS_WR_ROWS * std::max(w.pgu.waves, w.pdn.waves);
+    const int64_t gm = std::max(w.pgu.mtiles, w.pdn.mtiles) / E;  // row tiles per group
+    w.plane_rows = gemm_bs_plane_rows(R + gm * mt);
+    w.ldsum = gemm_bs_sum_cols(kmax);
+    const int64_t part = std::max(w.pgu.part_floats, w.pdn.part_floats);
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        char *p = base + off;
+        off = align256(off + bytes);
+        return p;
+    };
+    w.top_idx = (int32_t *)take((size_t)R * 4);
+    w.top_w = (float *)take((size_t)R * 4);
+    w.rows = (int32_t *)take((size_t)R * 4);
+    w.slot = (int32_t *)take((size_t)R * 4);
+    w.counts = (int32_t *)take((size_t)E * 4);
+    w.offsets = (int32_t *)take((size_t)E * 4);
+    w.xh = (uint16_t *)take((size_t)(w.plane_rows * 2 * kmax) * 2);
+    w.sh = (uint16_t *)take((size_t)(R * w.ldsum) * 2);
+    w.sl = (uint16_t *)take((size_t)(R * w.ldsum) * 2);
+    w.ex = (int *)take((size_t)R * 4);
+    w.GU = (float *)take((size_t)(R * 2 * ffn) * 4);
+    w.Y = (float *)take((size_t)(R * h) * 4);
+    w.part = (float *)take((size_t)part * 4);
+    w.bytes = off;
+    return w;
+}
+
+}  // namespace
+
+extern "C" int64_t gaje_hip_moe_prepared_bytes(int64_t h, int64_t ffn, int64_t n_expert) {
+    clear_error();
+    if (check_moe(1, h, ffn, n_expert) != GAJE_OK) return -1;
+    return (int64_t)moe_prepared(nullptr, h, ffn, n_expert).bytes;
+}
+
+extern "C" int gaje_hip_moe_prepare(const void *const *gate_up, const void *const *down, int64_t h, int64_t ffn,
+                                    int64_t n_expert, void *prepared, int64_t prepared_bytes, void *stream) {
+    clear_error();
+    GAJE_TRY(check_moe(1, h, ffn, n_expert));
+    if (!gate_up || !down || !prepared) return set_error(GAJE_ERR_INVALID_ARG, "moe prepare: null argument");
+    for (int64_t e = 0; e < n_expert; ++e)
+        if (!gate_up[e] || !down[e]) return set_error(GAJE_ERR_INVALID_ARG, "moe prepare: expert %lld has no weights", (long long)e);
+    const MoePrepared w = moe_prepared((char *)prepared, h, ffn, n_expert);
+    if ((int64_t)w.bytes > prepared_bytes)
+        return set_error(GAJE_ERR_INVALID_ARG, "moe prepare: %lld bytes given, %zu needed", (long long)prepared_bytes, w.bytes);
+    if ((uintptr_t)prepared & 255) return set_error(GAJE_ERR_INVALID_ARG, "moe prepare: the buffer must be 256-byte aligned");
+    hipStream_t s = as_stream(stream);
+    const int64_t NN[2] = {2 * ffn, h}, KK[2] = {h, ffn};
+    for (int i = 0; i < 2; ++i)
+        for (int64_t e = 0; e < n_expert; ++e) {
+            const uint8_t *pk = (const uint8_t *)(i == 0 ? gate_up[e] : down[e]);
+            GAJE_TRY(launch_q4_frags(pk, NN[i], KK[i], w.wf[i] + e * w.wf_stride[i], w.wsc[i] + e * w.wsc_stride[i], s));
+            GAJE_TRY(launch_q4_mins(pk, NN[i], KK[i], w.mins[i] + e * w.mins_stride[i], w.ldm[i], s));
+        }
+    return GAJE_OK;
+}
+
+extern "C" int64_t gaje_hip_moe_ffn_prepared_workspace(int64_t T, int64_t h, int64_t ffn, int64_t n_expert) {
+    clear_error();
+    if (check_moe(T, h, ffn, n_expert) != GAJE_OK) return -1;
+    return (int64_t)moe_bs_workspace(nullptr, T, h, ffn, n_expert).bytes;
+}
+
+extern "C" int gaje_hip_moe_ffn_prepared(const float *x, int64_t T, int64_t h, const float *router, int64_t n_expert,
+                                         const void *prepared, int64_t ffn, float *y, int32_t *top_idx, float *top_w,
+                                         void *workspace, int64_t workspace_bytes, void *stream) {
+    clear_error();
+    GAJE_TRY(check_moe(T, h, ffn, n_expert));
+    if (!x || !router || !prepared || !y || !workspace) return set_error(GAJE_ERR_INVALID_ARG, "moe: null argument");
+    if ((uintptr_t)prepared & 255) return set_error(GAJE_ERR_INVALID_ARG, "moe: the prepared experts must be 256-byte aligned");
+    const MoePrepared pw = moe_prepared((char *)prepared, h, ffn, n_expert);
+    const MoeBsWorkspace w = moe_bs_workspace((char *)workspace, T, h, ffn, n_expert);
+    if ((int64_t)w.bytes > workspace_bytes)
+        return set_error(GAJE_ERR_INVALID_ARG, "moe workspace of %lld bytes is smaller than the %zu needed",
+                         (long long)workspace_bytes, w.bytes);
+    hipStream_t s = as_stream(stream);
+    const int64_t R = 2 * T;
+    MoeParams mp{};
+    mp.x = x;
+    mp.ldx = h;
+    mp.T = T;
+    mp.h = h;
+    mp.router = router;
+    mp.n_expert = (int32_t)n_expert;
+    mp.top_idx = w.top_idx;
+    mp.top_w = w.top_w;
+    mp.rows = w.rows;
+    mp.slot = w.slot;
+    mp.counts = w.counts;
+    mp.offsets = w.offsets;
+    mp.y = y;
+    mp.ldy = h;
+    GAJE_TRY(launch_moe_route(mp, s));
+
+    // the dispatched rows (gathered in expert order) in the block-scaled layout
+    SplitParams sp{};
+    sp.x = x;
+    sp.ldx = h;
+    sp.xh = w.xh;
+    sp.ldh = 2 * h;
+    sp.sh = w.sh;
+    sp.sl = w.sl;
+    sp.ldsum = w.ldsum;
+    sp.ex = w.ex;
+    sp.M = R;
+    sp.K = h;
+    sp.rows = w.rows;
+    GAJE_TRY(launch_split_rows(sp, s));
+    // one grouped launch per product over every expert's rows (counts and
+    // offsets stay on the device; an expert holds at most T rows)
+    auto gemm = [&](int i, const GemmBsPlan &pl, int64_t N, int64_t K, float *Y) {
+        GemmBsParams p{};
+        p.wf = pw.wf[i];
+        p.wsc = pw.wsc[i];
+        p.nbp4 = q4_frag_nbp4(K);
+        p.mins = pw.mins[i];
+        p.ldm = pw.ldm[i];
+        p.xh = w.xh;
+        p.plane_rows = w.plane_rows;
+        p.sh = w.sh;
+        p.sl = w.sl;
+        p.ex = w.ex;
+        p.ldh = 2 * K;
+        p.ldsum = w.ldsum;
+        p.y = Y;
+        p.ldy = N;
+        p.part = w.part;
+        p.M = R;
+        p.N = N;
+        p.nb = (int32_t)(K / 32);
+        p.g_counts = w.counts;
+        p.g_offsets = w.offsets;
+        p.g_groups = (int32_t)n_expert;
+        p.g_mtiles = (int32_t)(pl.mtiles / n_expert);
+        p.g_wf_stride = pw.wf_stride[i];
+        p.g_wsc_stride = pw.wsc_stride[i];
+        p.g_mins_stride = pw.mins_stride[i];
+        return launch_gemm_q4_bs(p, pl, s);
+    };
+    GAJE_TRY(gemm(0, w.pgu, 2 * ffn, h, w.GU));
+    // swiglu of every dispatched row into the planes, then down
+    sp = SplitParams{};
+    sp.x = w.GU;
+    sp.up = w.GU + ffn;
+    sp.ldx = 2 * ffn;
+    sp.h_scale = 1.0f;
+    sp.xh = w.xh;
+    sp.ldh = 2 * ffn;
+    sp.sh = w.sh;
+    sp.sl = w.sl;
+    sp.ldsum = w.ldsum;
+    sp.ex = w.ex;
+    sp.M = R;
+    sp.K = ffn;
+    sp.st_a = sp.st_b = -1;
+    GAJE_TRY(launch_split_rows(sp, s));
+    GAJE_TRY(gemm(1, w.pdn, h, ffn, w.Y));
+    GAJE_TRY(launch_moe_combine(mp, w.Y, s));
+    if (top_idx) GAJE_HIP_CHECK(hipMemcpyAsync(top_idx, w.top_idx, (size_t)R * 4, hipMemcpyDeviceToDevice, s));
+    if (top_w) GAJE_HIP_CHECK(hipMemcpyAsync(top_w, w.top_w, (size_t)R * 4, hipMemcpyDeviceToDevice, s));
+    return GAJE_OK;
+}
+
 extern "C" int gaje_hip_lut4_gemv(const uint8_t *codes, const float *lut, int64_t lut_len, const float *x,
                                   const float *bias, int64_t bias_len, float *y, int64_t n, int64_t k, void *stream) {
     GAJE_TRY(check_dims(n, k));

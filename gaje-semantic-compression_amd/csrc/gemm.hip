@@ -683,7 +683,7 @@ size_t gemm_lds() { return (size_t)((GA ? 0 : 4 * MT * GM_ROW) + 4 * GM_NT * GM_
 // partials are summed in a fixed order by gemm_reduce_kernel.
 constexpr int BS_J = 9;                         // 16-row weight tiles per workgroup
 constexpr int BS_NT = 16 * BS_J;                // 144 weight rows
-constexpr int BS_WR = 32;                       // activation rows per wave
+constexpr int BS_WR = BS_WR_ROWS;               // activation rows per wave
 constexpr int BS_ABLK = BS_WR * 128;            // one block of a wave's rows (hi | lo)
 constexpr int BS_ADMA = BS_ABLK / 1024;         // its copy instructions
 constexpr int BS_RING = 3;                      // ring slots per wave
@@ -739,7 +739,18 @@ __global__ __launch_bounds__(64 * W, (BsShape<W, BPI>::WG_PER_CU)) void gemm_q4_
     const int ubase = gd.units / gd.ntiles, urem = gd.units % gd.ntiles;
     const int nj = ubase + (t < urem ? 1 : 0);  // 16-row weight units of this tile (<= BS_J)
     const int64_t n0 = 16 * (int64_t)(t * ubase + min(t, urem));
-    const int64_t m0 = (int64_t)mt * (BS_WR * W) + BS_WR * w;  // this wave's first activation row
+    int64_t m0 = (int64_t)mt * (BS_WR * W) + BS_WR * w;  // this wave's first activation row
+    int64_t mend = p.M;                                   // rows at or past it are not stored
+    if (p.g_counts) {  // grouped: row tile mtl of group e, with that group's operands (uniform)
+        const int e = mt / p.g_mtiles, mtl = mt - e * p.g_mtiles;
+        const int64_t cnt = p.g_counts[e];
+        if ((int64_t)mtl * (BS_WR * W) >= cnt) return;  // before any copy or barrier
+        m0 = p.g_offsets[e] + (int64_t)mtl * (BS_WR * W) + BS_WR * w;
+        mend = p.g_offsets[e] + cnt;
+        p.wf += e * p.g_wf_stride;
+        p.wsc += e * p.g_wsc_stride;
+        p.mins += e * p.g_mins_stride;
+    }
     const int b0 = z * gd.kb_per, b1 = min(p.nb, b0 + gd.kb_per);
     const int nblk = b1 - b0, npr = (nblk + BPI - 1) / BPI;  // blocks, intervals of this split
     const int64_t t16 = n0 >> 4;                        // the tile's first 16-row fragment tile
@@ -999,7 +1010,7 @@ __global__ __launch_bounds__(64 * W, (BsShape<W, BPI>::WG_PER_CU)) void gemm_q4_
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int64_t m = m0 + 16 * i + 4 * kg + r;
-            mok[i][r] = m < p.M;
+            mok[i][r] = m < mend;
             mrow[i][r] = mok[i][r] ? m : p.M - 1;
             exr[i][r] = p.ex[mrow[i][r]];
         }
@@ -1244,6 +1255,31 @@ GemmBsPlan plan_gemm_q4_bs(int64_t M, int64_t N, int64_t K) {
     return pl;
 }
 
+GemmBsPlan plan_gemm_q4_bs_grouped(int64_t R, int64_t E, int64_t T, int64_t N, int64_t K) {
+    GemmBsPlan pl{};
+    // the tile height follows the mean group (the MoE's 256 tokens x top-2
+    // over 8 experts: 64 rows each, one 64-row tile); a group holds at most T
+    // rows, so every group has T / tile row tiles in the grid, and the empty
+    // ones return at once
+    const int64_t mean = (R + E - 1) / E;
+    pl.waves = mean <= 64 ? 2 : (mean <= 128 ? 4 : 8);
+    const int64_t mt = BS_WR * pl.waves;
+    pl.mtiles = (int)(E * ((T + mt - 1) / mt));
+    const int64_t units = (N + 15) / 16;
+    pl.ntiles = (int)((units + BS_J - 1) / BS_J);
+    const int64_t active = ((R + mt - 1) / mt + E - 1) * pl.ntiles;  // tiles holding rows, at most
+    const int64_t nb = K / 32;
+    const int64_t cu = (pl.waves == 8 ? 1 : 2) * device_cu_count();
+    const int64_t S = active < cu ? cu / active : 1;
+    int64_t kb = (nb + S - 1) / S;
+    kb = (kb + 3) / 4 * 4;
+    if (kb < 4) kb = 4;
+    pl.kb_per = (int)kb;
+    pl.splits = (int)((nb + kb - 1) / kb);
+    pl.part_floats = pl.splits > 1 ? (int64_t)pl.splits * R * N : 0;
+    return pl;
+}
+
 int launch_gemm_q4_bs(const GemmBsParams &p, const GemmBsPlan &pl, hipStream_t s) {
     if (p.M < 0 || p.N <= 0 || p.nb <= 0 || !p.wf || !p.wsc || p.nbp4 != q4_frag_nbp4(32 * (int64_t)p.nb) ||
         (p.M > 0 && (!p.xh || !p.sh || !p.sl || !p.ex || !p.y || p.ldh < 64 * (int64_t)p.nb ||
@@ -1256,14 +1292,23 @@ int launch_gemm_q4_bs(const GemmBsParams &p, const GemmBsPlan &pl, hipStream_t s
         return set_error(GAJE_ERR_INVALID_ARG, "q4 block-scaled gemm: planes must be 16-byte aligned");
     if (p.M == 0) return GAJE_OK;
     const int64_t mt = BS_WR * (int64_t)pl.waves;
-    if (p.plane_rows < (int64_t)pl.mtiles * mt)
+    const bool grouped = p.g_counts != nullptr;
+    if (grouped && (!p.g_offsets || p.g_groups <= 0 || p.g_groups > MOE_MAX_EXPERTS || p.g_mtiles <= 0 ||
+                    pl.mtiles != (int64_t)p.g_groups * p.g_mtiles || p.g_wf_stride % 512 || p.g_wsc_stride % 16 ||
+                    p.g_mins_stride % 8 || p.g_wf_stride < q4_frag_halves(p.N, 32 * (int64_t)p.nb) ||
+                    p.g_wsc_stride < q4_frag_scale_floats(p.N, 32 * (int64_t)p.nb) || p.g_mins_stride < p.N * p.ldm))
+        return set_error(GAJE_ERR_INVALID_ARG, "q4 block-scaled gemm: bad groups");
+    // rows read: a grouped tile starts inside the M rows and reads one tile on
+    const int64_t rows_read = grouped ? p.M + (int64_t)p.g_mtiles * mt : (int64_t)pl.mtiles * mt;
+    if (p.plane_rows < rows_read)
         return set_error(GAJE_ERR_INVALID_ARG, "q4 block-scaled gemm: the activation plane holds %lld rows, the tiles read %lld",
-                         (long long)p.plane_rows, (long long)pl.mtiles * mt);
-    if (2 * p.plane_rows * p.ldh >= ((int64_t)1 << 32) || 2 * q4_frag_halves(p.N, 32 * (int64_t)p.nb) >= ((int64_t)1 << 32))
+                         (long long)p.plane_rows, (long long)rows_read);
+    if (2 * p.plane_rows * p.ldh >= ((int64_t)1 << 32) ||
+        2 * q4_frag_halves(p.N, 32 * (int64_t)p.nb) >= ((int64_t)1 << 32))
         return set_error(GAJE_ERR_UNSUPPORTED, "q4 block-scaled gemm: operands beyond 4 GiB");
     if (((uintptr_t)p.wf | (uintptr_t)p.wsc) & 15)
         return set_error(GAJE_ERR_INVALID_ARG, "q4 block-scaled gemm: weight fragments must be 16-byte aligned");
-    if ((pl.waves != 2 && pl.waves != 4 && pl.waves != 8) || pl.mtiles != (p.M + mt - 1) / mt || pl.ntiles <= 0 ||
+    if ((pl.waves != 2 && pl.waves != 4 && pl.waves != 8) || (!grouped && pl.mtiles != (p.M + mt - 1) / mt) || pl.ntiles <= 0 ||
         pl.ntiles * (int64_t)BS_J < (p.N + 15) / 16 || pl.kb_per % 4 || pl.kb_per <= 0 ||
         (int64_t)pl.splits * pl.kb_per < p.nb || (int64_t)(pl.splits - 1) * pl.kb_per >= p.nb ||
         (pl.splits > 1 && !p.part))

@@ -307,6 +307,15 @@ struct GemmBsParams {
     int32_t layer;
     int32_t st_a, st_b;
     int32_t defer_reduce;    // splits > 1: leave the partials for a split pass's prologue
+    // grouped products (the MoE experts, one launch for every expert): with
+    // g_counts set, the row tiles are g_groups x g_mtiles; tile mt of group e
+    // covers rows g_offsets[e] + mt * tile.. of the planes and of y, up to
+    // g_offsets[e] + g_counts[e] (M = all rows), and multiplies them by group
+    // e's operands at wf + e * g_wf_stride halves, wsc + e * g_wsc_stride
+    // floats and mins + e * g_mins_stride halves
+    const int32_t *g_counts, *g_offsets;
+    int32_t g_groups, g_mtiles;
+    int64_t g_wf_stride, g_wsc_stride, g_mins_stride;
 };
 struct GemmBsPlan {
     int waves;               // 32-row wave tiles per workgroup (2, 4 or 8)
@@ -314,7 +323,11 @@ struct GemmBsPlan {
     int splits, kb_per;      // K splits of kb_per blocks (a multiple of 4)
     int64_t part_floats;     // partial buffer the splits need (0 if one split)
 };
+constexpr int BS_WR_ROWS = 32;  // activation rows per wave tile of the block-scaled product
 GemmBsPlan plan_gemm_q4_bs(int64_t M, int64_t N, int64_t K);
+// Grouped plan: R rows over E groups of at most T rows each (mtiles = E x the
+// tiles of T rows; the tile height follows the mean group size).
+GemmBsPlan plan_gemm_q4_bs_grouped(int64_t R, int64_t E, int64_t T, int64_t N, int64_t K);
 int launch_gemm_q4_bs(const GemmBsParams &p, const GemmBsPlan &plan, hipStream_t s);
 // Columns of the block-sum planes for a K: K/32 rounded up to a multiple of 32.
 int64_t gemm_bs_sum_cols(int64_t K);

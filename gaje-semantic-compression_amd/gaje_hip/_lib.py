@@ -127,6 +127,11 @@ SIGNATURES = [
     ("gaje_hip_moe_ffn_workspace", c_i64, [c_i64, c_i64, c_i64, c_i64]),
     ("gaje_hip_moe_ffn", ctypes.c_int, [c_vp, c_i64, c_i64, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp,
                                         c_vp, c_i64, c_vp]),
+    ("gaje_hip_moe_prepared_bytes", c_i64, [c_i64, c_i64, c_i64]),
+    ("gaje_hip_moe_prepare", ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp]),
+    ("gaje_hip_moe_ffn_prepared_workspace", c_i64, [c_i64, c_i64, c_i64, c_i64]),
+    ("gaje_hip_moe_ffn_prepared", ctypes.c_int, [c_vp, c_i64, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_vp, c_vp,
+                                                 c_vp, c_i64, c_vp]),
     ("gaje_hip_q8_0_packed_bytes", c_i64, [c_i64, c_i64]),
     ("gaje_hip_q8_0_pack", ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, c_vp]),
     ("gaje_hip_q8_0_gemv", ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_vp]),

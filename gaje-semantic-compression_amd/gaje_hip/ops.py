@@ -137,6 +137,30 @@ def moe_ffn(x: DeviceBuffer, T: int, h: int, router: DeviceBuffer, gate_up, down
                                  workspace.ptr, workspace.nbytes, stream))
 
 
+def moe_prepared_bytes(h: int, ffn: int, n_expert: int) -> int:
+    return int(lib().gaje_hip_moe_prepared_bytes(h, ffn, n_expert))
+
+
+def moe_prepare(gate_up, down, h: int, ffn: int, prepared: DeviceBuffer, stream=None) -> None:
+    """The block-scaled weight operands of every expert (gaje_hip_moe_prepare)."""
+    E = len(gate_up)
+    gu = (ctypes.c_void_p * E)(*[b.ptr for b in gate_up])
+    dn = (ctypes.c_void_p * E)(*[b.ptr for b in down])
+    check(lib().gaje_hip_moe_prepare(gu, dn, h, ffn, E, prepared.ptr, prepared.nbytes, stream))
+
+
+def moe_ffn_prepared_workspace(T: int, h: int, ffn: int, n_expert: int) -> int:
+    return int(lib().gaje_hip_moe_ffn_prepared_workspace(T, h, ffn, n_expert))
+
+
+def moe_ffn_prepared(x: DeviceBuffer, T: int, h: int, router: DeviceBuffer, n_expert: int, prepared: DeviceBuffer,
+                     ffn: int, y: DeviceBuffer, workspace: DeviceBuffer, top_idx: DeviceBuffer | None = None,
+                     top_w: DeviceBuffer | None = None, stream=None) -> None:
+    """Top-2 MoE SwiGLU FFN over prepared experts (gaje_hip_moe_ffn_prepared)."""
+    check(lib().gaje_hip_moe_ffn_prepared(x.ptr, T, h, router.ptr, n_expert, prepared.ptr, ffn, y.ptr,
+                                          _p(top_idx), _p(top_w), workspace.ptr, workspace.nbytes, stream))
+
+
 def q8_0_packed_bytes(n: int, k: int) -> int:
     return int(lib().gaje_hip_q8_0_packed_bytes(n, k))
 

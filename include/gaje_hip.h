@@ -150,6 +150,24 @@ int gaje_hip_moe_ffn(const float *x, int64_t T, int64_t h, const float *router, 
                      const void *const *gate_up, const void *const *down, int64_t ffn, float *y,
                      int32_t *top_idx, float *top_w, void *workspace, int64_t workspace_bytes, void *stream);
 
+/* The same layer over prepared experts: gaje_hip_moe_prepare builds, once per
+ * set of experts, the block-scaled product's weight operands (per expert and
+ * product: the codes as f16 MFMA fragments, the fragment scales and the dense
+ * block mins; about 3.3x the packed bytes) into a caller-owned, 256-byte
+ * aligned device buffer of gaje_hip_moe_prepared_bytes; gaje_hip_moe_ffn_
+ * prepared then runs the layer with one grouped block-scaled product per
+ * projection (a row tile per ~64 dispatched rows, no dequantisation per
+ * tile).  Routing, composition, accuracy and arguments as gaje_hip_moe_ffn;
+ * no reference counterpart.  The prepared buffer depends only on the experts'
+ * packed rows: prepare again after changing them. */
+int64_t gaje_hip_moe_prepared_bytes(int64_t h, int64_t ffn, int64_t n_expert);
+int gaje_hip_moe_prepare(const void *const *gate_up, const void *const *down, int64_t h, int64_t ffn,
+                         int64_t n_expert, void *prepared, int64_t prepared_bytes, void *stream);
+int64_t gaje_hip_moe_ffn_prepared_workspace(int64_t T, int64_t h, int64_t ffn, int64_t n_expert);
+int gaje_hip_moe_ffn_prepared(const float *x, int64_t T, int64_t h, const float *router, int64_t n_expert,
+                              const void *prepared, int64_t ffn, float *y, int32_t *top_idx, float *top_w,
+                              void *workspace, int64_t workspace_bytes, void *stream);
+
 /* Q8_0 rows (Q8_0Block {f16 scale; i8 qs[32]}, blocks.rs:36-49; the
  * --quant-embed format of token_embd / lm_head): packing into tiles of 8 rows
  * (per group of four blocks: the 8 rows' codes, 1 KiB, then their scales, 64
