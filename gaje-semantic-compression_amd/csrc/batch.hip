@@ -249,24 +249,29 @@ __global__ __launch_bounds__(256) void gemv_batch_f32_kernel(BatchGemvParams p) 
 // The same products for a batch of 16, register-blocked over rows: lanes 2r,
 // 2r+1 of a wave own rows r + 32j (j < RB; one 32-row tile each) of the
 // wave's 32*RB rows, chains 0..3 and 4..7 as above, and a workgroup takes VG
-// of the vectors (the batch splits over the grid), so each activation quad
-// read from LDS feeds RB rows.  Workgroups b, b+8, b+16, b+24 take one row
-// block's four vector groups; consecutive workgroups go to the eight XCDs in
-// turn, so the four land on one XCD and its L2 serves the block's rows
-// three times of four.
-constexpr int F32B_RB = 4, F32B_VG = 4, F32B_AHEAD = 4;
-constexpr int64_t F32B_ROWS = 128 * F32B_RB;  // rows per workgroup
+// of the vectors, so each activation quad read from LDS feeds RB rows.
+// VG = 16 (all vectors, when their activations fit LDS): every weight row is
+// read once.  VG = 4: the batch splits over the grid, workgroups b, b+8,
+// b+16, b+24 taking one row block's four vector groups; consecutive
+// workgroups go to the eight XCDs in turn, so the four land on one XCD and its
+// L2 serves the block's rows three times of four (measured: 372 us for the
+// 151936 x 1536 lm_head of batch 16, its L2-to-CU traffic four times the
+// weights; VG = 16 reads them once).
+constexpr int F32B_AHEAD = 4;
+template <int RB, int NT> constexpr int64_t f32b_rows() { return NT / 2 * RB; }  // rows per workgroup
 
-__global__ __launch_bounds__(256) void gemv_batch_f32_rb_kernel(BatchGemvParams p, int64_t nblk) {
-    constexpr int RB = F32B_RB, VG = F32B_VG, AHEAD = F32B_AHEAD;
+template <int RB, int VG, int NT>
+__global__ __launch_bounds__(NT) void gemv_batch_f32_rb_kernel(BatchGemvParams p, int64_t nblk) {
+    constexpr int AHEAD = F32B_AHEAD, NVG = 16 / VG;
+    constexpr int64_t F32B_ROWS = f32b_rows<RB, NT>();
     extern __shared__ __align__(16) float xs[];  // [VG][K]
     const int b = blockIdx.x;
-    const int64_t blk = ((int64_t)(b >> 5) << 3) | (b & 7);
-    if (blk >= nblk) return;  // whole workgroup: the grid is rounded up to 32
-    const int vz = ((b >> 3) & 3) * VG;
+    const int64_t blk = NVG == 1 ? (int64_t)b : (((int64_t)(b >> 5) << 3) | (b & 7));
+    if (blk >= nblk) return;  // whole workgroup: the grid is rounded up to 32 (NVG = 4)
+    const int vz = NVG == 1 ? 0 : ((b >> 3) & 3) * VG;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t K = p.K, K4 = K / 4;
-    for (int64_t i = tid; i < VG * K4; i += 256) {
+    for (int64_t i = tid; i < VG * K4; i += NT) {
         const int64_t v = i / K4, q = i - v * K4;
         *(float4 *)(xs + v * K + 4 * q) = *(const float4 *)(p.x + (size_t)(vz + v) * p.ldx + 4 * q);
     }
@@ -612,11 +617,22 @@ int launch_gemv_batch(const BatchGemvParams &p, hipStream_t s) {
         if (p.mode != MODE_STORE) return set_error(GAJE_ERR_UNSUPPORTED, "batched matvec: f32 rows store only");
         if (nv == 4) return launch_f32<4>(p, s);
         if (nv == 8) return launch_f32<8>(p, s);
-        const size_t lds = (size_t)F32B_VG * p.K * 4;
-        if (lds + 1024 <= max_lds_per_block()) {
-            const int64_t nblk = (p.N + F32B_ROWS - 1) / F32B_ROWS;
-            const int64_t grid = (nblk + 7) / 8 * 32;  // 16 / F32B_VG = 4 vector groups per block
-            hipLaunchKernelGGL(gemv_batch_f32_rb_kernel, dim3((unsigned)grid), dim3(256), lds, s, p, nblk);
+        if ((size_t)16 * p.K * 4 + 1024 <= max_lds_per_block()) {
+            // all 16 vectors in one workgroup of 8 waves (two per SIMD: the
+            // workgroup's LDS allows one per compute unit), one row per lane
+            constexpr int RB = 1, NT = 512;
+            const int64_t nblk = (p.N + f32b_rows<RB, NT>() - 1) / f32b_rows<RB, NT>();
+            hipLaunchKernelGGL((gemv_batch_f32_rb_kernel<RB, 16, NT>), dim3((unsigned)nblk), dim3(NT),
+                               (size_t)16 * p.K * 4, s, p, nblk);
+            GAJE_HIP_CHECK(hipGetLastError());
+            return GAJE_OK;
+        }
+        if ((size_t)4 * p.K * 4 + 1024 <= max_lds_per_block()) {
+            constexpr int RB = 4, NT = 256;
+            const int64_t nblk = (p.N + f32b_rows<RB, NT>() - 1) / f32b_rows<RB, NT>();
+            const int64_t grid = (nblk + 7) / 8 * 32;  // 4 vector groups per block
+            hipLaunchKernelGGL((gemv_batch_f32_rb_kernel<RB, 4, NT>), dim3((unsigned)grid), dim3(NT), (size_t)4 * p.K * 4,
+                               s, p, nblk);
             GAJE_HIP_CHECK(hipGetLastError());
             return GAJE_OK;
         }
