@@ -156,7 +156,13 @@ __device__ __forceinline__ float f16_hi(uint32_t v) {
 template <int DQ>
 __device__ __forceinline__ void q4_dequant_dw(float (&d)[4], uint32_t n, uint32_t sm) {
     constexpr uint32_t M = DQ ? 0x00F000F0u : 0x000F000Fu;
-    const float S = half_lo(sm) * (DQ ? 1048576.0f : 16777216.0f);  // scale * 2^20 or 2^24, exact
+    // S = scale * 2^20 or 2^24 in one v_fma_mix_f32 reading the f16 scale from
+    // the low half (exact: a power-of-two shift of an f16; + -0 keeps the
+    // product's sign, zeros included), in place of a conversion and a multiply
+    float S;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]"
+        : "=v"(S)
+        : "v"(sm), "v"(DQ ? 1048576.0f : 16777216.0f), "v"(-0.0f));
     const float mn = half_hi(sm);
     const uint32_t e02 = opaque_and(n, M), e13 = opaque_and(n >> 8, M);
     d[0] = fmaf(f16_lo(e02), S, mn);
