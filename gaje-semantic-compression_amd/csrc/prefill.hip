@@ -464,6 +464,208 @@ __global__ __launch_bounds__(64) void prefill_attn_f16_kernel(PrefillAttnParams 
     }
 }
 
+// The same attention with the key and value fragments shared by a GQA group:
+// workgroup (query block, kv head g, key chunk c) runs one wave per query head
+// of the group (R = n_head / n_kv waves), and each 32-key tile's K and V
+// fragments are staged once into LDS by all the waves (read one tile ahead
+// into registers, double-buffered, one barrier per tile) instead of being read
+// from memory by every wave.  Each wave's products, softmax and record are
+// prefill_attn_f16_kernel's, operand for operand.  LDS rows are padded (a key
+// row by 16 bytes, a value row by 16 bytes) so that the fragment reads of
+// consecutive rows fall in distinct banks.
+constexpr int GQA_PER = 8;  // staged float4s per thread and tile, at most
+template <int HD> struct GqaShape {
+    static constexpr int KROW = 2 * HD + 8;                // halves per key row
+    static constexpr int VROW = 64 + 8;                    // halves per value row
+    static constexpr int TILE = 32 * KROW + HD * VROW;     // halves per tile
+    static constexpr int F4 = 16 * HD;                     // float4s per tile (keys, then values)
+};
+size_t prefill_gqa_lds_bytes(int head_dim) {
+    return (size_t)2 * (head_dim == 64 ? GqaShape<64>::TILE : GqaShape<128>::TILE) * 2;
+}
+bool prefill_gqa_fits(int head_dim, int R) {
+    return R >= 1 && R <= 8 && 16 * head_dim <= GQA_PER * 64 * R;
+}
+
+template <int HD>
+__global__ __launch_bounds__(512) void prefill_attn_gqa_kernel(PrefillAttnParams p, int64_t kch, int ntiles) {
+    using Q = GqaShape<HD>;
+    constexpr int NS = HD / 32, NT = HD / 16;
+    extern __shared__ __align__(16) uint16_t gq_lds[];  // [2][TILE]
+    const int R = p.n_head / p.n_kv, NTH = 64 * R;
+    const int tid = threadIdx.x, wave = tid >> 6, i = tid & 63, fr = i & 15, kg = i >> 4;
+    const int nqb = (int)((p.P + 15) / 16);
+    const int qb = nqb - 1 - (int)blockIdx.x;  // longest blocks first
+    const int g = blockIdx.y, h = g * R + wave;
+    const int64_t t0 = (int64_t)qb * 16;
+    const int64_t q_rows = (int64_t)p.n_head * HD;
+    const float scale_l2 = 1.4426950408889634f / sqrtf((float)HD);
+    const int64_t tmax = (t0 + 15 < p.P ? t0 + 15 : p.P - 1);
+    const int64_t kbeg = (int64_t)blockIdx.z * kch;
+    if (kbeg > p.pos0 + tmax) return;  // uniform over the workgroup
+    const int64_t kend = (p.pos0 + tmax < kbeg + kch - 1 ? p.pos0 + tmax : kbeg + kch - 1);
+    const int64_t t = t0 + fr, qpos = p.pos0 + t;
+
+    ah8 qh[NS], ql[NS];
+    {
+        const float *qr = p.q + (t < p.P ? t : 0) * q_rows + (int64_t)h * HD + 8 * kg;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            const float4 a = *(const float4 *)(qr + 32 * s), b = *(const float4 *)(qr + 32 * s + 4);
+            const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                _Float16 hi, lo;
+                split_f16(t < p.P ? v[e] : 0.0f, hi, lo);
+                qh[s][e] = hi;
+                ql[s][e] = lo;
+            }
+        }
+    }
+    // the group's converted keys [pos][2 HD] and values [d][tile][64]
+    const uint16_t *k16 = p.kv16 + (int64_t)g * ntiles * 32 * 2 * HD;
+    const uint16_t *v16 = p.kv16 + (int64_t)p.n_kv * ntiles * 32 * 2 * HD + (int64_t)g * HD * ntiles * 64;
+    // staging: float4 e of a tile is key row e / (HD / 4), chunk e % (HD / 4)
+    // (e < 8 HD), else value row (e - 8 HD) / 8, chunk (e - 8 HD) % 8; every
+    // row of the tile lies inside the converted range (whole 32-key tiles)
+    float4 rg[GQA_PER];
+    auto stage_load = [&](int64_t k0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < GQA_PER; ++j) {
+            const int e = tid + j * NTH;
+            const uint16_t *src;
+            if (e < 8 * HD) {
+                const int row = e / (HD / 4), c = e % (HD / 4);
+                src = k16 + (k0 + row) * 2 * HD + 8 * c;
+            } else {
+                const int e2 = (e < Q::F4 ? e : Q::F4 - 1) - 8 * HD, d = e2 >> 3, c = e2 & 7;
+                src = v16 + ((int64_t)d * ntiles + (k0 >> 5)) * 64 + 8 * c;
+            }
+            float4 x = float4{0.f, 0.f, 0.f, 0.f};
+            if (e < Q::F4) x = *(const float4 *)src;
+            rg[j] = x;
+        }
+    };
+    auto stage_store = [&](int buf) __attribute__((always_inline)) {
+        uint16_t *dst0 = gq_lds + buf * Q::TILE;
+#pragma unroll
+        for (int j = 0; j < GQA_PER; ++j) {
+            const int e = tid + j * NTH;
+            if (e >= Q::F4) break;  // the later j lie beyond it too
+            uint16_t *dst;
+            if (e < 8 * HD) {
+                const int row = e / (HD / 4), c = e % (HD / 4);
+                dst = dst0 + row * Q::KROW + 8 * c;
+            } else {
+                const int e2 = e - 8 * HD, d = e2 >> 3, c = e2 & 7;
+                dst = dst0 + 32 * Q::KROW + d * Q::VROW + 8 * c;
+            }
+            *(float4 *)dst = rg[j];
+        }
+    };
+    stage_load(kbeg);
+    stage_store(0);
+    __syncthreads();
+
+    f4v o[NT];
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) o[tt] = f4v{0.f, 0.f, 0.f, 0.f};
+    float m = -INFINITY, l = 0.0f;
+    int buf = 0;
+    for (int64_t k0 = kbeg; k0 <= kend; k0 += 32) {
+        const bool more = k0 + 32 <= kend;  // uniform
+        if (more) stage_load(k0 + 32);      // in flight during this tile
+        const uint16_t *kt = gq_lds + buf * Q::TILE + 8 * kg;
+        const uint16_t *vt = gq_lds + buf * Q::TILE + 32 * Q::KROW + 8 * kg;
+        // ---- S^T over keys k0 + 16 u + fr (one key half's fragments live at a time) ----
+        f4v sacc[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            ah8 kf[NS][2];
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                const uint16_t *kr = kt + (16 * u + fr) * Q::KROW + 64 * s;
+                kf[s][0] = *(const ah8 *)kr;
+                kf[s][1] = *(const ah8 *)(kr + 32);
+            }
+            sacc[u] = f4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                sacc[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[s][0], qh[s], sacc[u], 0, 0, 0);
+                sacc[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[s][0], ql[s], sacc[u], 0, 0, 0);
+                sacc[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[s][1], qh[s], sacc[u], 0, 0, 0);
+            }
+        }
+        // ---- online softmax of query fr over keys k0 + 16 u + 4 kg + r (log2 units) ----
+        float sv[2][4], mx = -INFINITY;
+        const int rel = (int)(qpos - k0);
+        if (p.pos0 + t0 - k0 >= 31) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    sv[u][r] = sacc[u][r] * scale_l2;
+                    mx = fmaxf(mx, sv[u][r]);
+                }
+        } else {
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    sv[u][r] = 16 * u + 4 * kg + r <= rel ? sacc[u][r] * scale_l2 : -INFINITY;
+                    mx = fmaxf(mx, sv[u][r]);
+                }
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float mn = fmaxf(m, mx);
+        const float alpha = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - mn);
+        const float mb = mn == -INFINITY ? 0.0f : mn;
+        ah8 ph, pl;
+        float psum = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float pv = __builtin_amdgcn_exp2f(sv[u][r] - mb);
+                psum = psum + pv;
+                _Float16 hi, lo;
+                split_f16(pv, hi, lo);
+                ph[4 * u + r] = hi;
+                pl[4 * u + r] = lo;
+            }
+        l = l * alpha + psum;
+        m = mn;
+        // ---- O^T += V^T P^T over dimensions 16 tt + fr ----
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt) {
+            const uint16_t *vr = vt + (16 * tt + fr) * Q::VROW;
+            const ah8 vf0 = *(const ah8 *)vr, vf1 = *(const ah8 *)(vr + 32);
+            o[tt] = o[tt] * alpha;
+            o[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf0, ph, o[tt], 0, 0, 0);
+            o[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf0, pl, o[tt], 0, 0, 0);
+            o[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf1, ph, o[tt], 0, 0, 0);
+        }
+        // the next tile into the other buffer (every wave finished reading it
+        // before the previous barrier), then one barrier
+        if (more) stage_store(buf ^ 1);
+        __syncthreads();
+        buf ^= 1;
+    }
+    l = l + __shfl_xor(l, 16);
+    l = l + __shfl_xor(l, 32);
+    if (t < p.P) {
+        float *rec = p.ws + (((int64_t)blockIdx.z * p.P + t) * p.n_head + h) * (HD + PREFILL_ATTN_REC_PAD);
+        if (kg == 0) {
+            rec[0] = m;
+            rec[1] = l;
+        }
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt)
+            *(f4v *)(rec + PREFILL_ATTN_REC_PAD + 16 * tt + 4 * kg) = o[tt];
+    }
+}
+
 // out[t][h] = (sum_c O_c 2^(m_c - m)) / (sum_c l_c 2^(m_c - m) + 1e-12), m = max_c m_c
 // (the chunks' maxima are in log2 units),
 // over the chunks that hold keys at or before the row's position.  One
@@ -533,7 +735,8 @@ int64_t prefill_kv16_halves(int64_t keys, int64_t n_kv, int64_t head_dim) {
 }
 
 // key chunks of at least 128 keys (whole 32-key tiles), at most PREFILL_ATTN_CHUNKS of them
-// (64-key chunks measured slower: 29.0 against 25.9 us per layer at 512 tokens)
+// (64-key chunks measured slower at 512 tokens: 29.0 against 25.9 us per layer
+// for the per-head kernel, 19.6 against 14.7 us for the GQA-shared one)
 int64_t prefill_attn_kch(int64_t keys) {
     int64_t kch = (keys + PREFILL_ATTN_CHUNKS - 1) / PREFILL_ATTN_CHUNKS;
     return kch < 128 ? 128 : (kch + 31) / 32 * 32;
@@ -560,9 +763,17 @@ int launch_prefill_attention(const PrefillAttnParams &p, hipStream_t s) {
     }
     const int64_t kch = prefill_attn_kch(keys);
     const int64_t nch = (keys + kch - 1) / kch;
-    const dim3 grid((unsigned)((p.P + 15) / 16), (unsigned)p.n_head, (unsigned)nch);
-    if (p.head_dim == 64) hipLaunchKernelGGL(prefill_attn_f16_kernel<64>, grid, dim3(64), 0, s, p, kch, ntiles);
-    else hipLaunchKernelGGL(prefill_attn_f16_kernel<128>, grid, dim3(64), 0, s, p, kch, ntiles);
+    const int R = p.n_head / p.n_kv;
+    if (prefill_gqa_fits(p.head_dim, R) && prefill_gqa_lds_bytes(p.head_dim) + 1024 <= max_lds_per_block()) {
+        const dim3 grid((unsigned)((p.P + 15) / 16), (unsigned)p.n_kv, (unsigned)nch);
+        const size_t lds = prefill_gqa_lds_bytes(p.head_dim);
+        if (p.head_dim == 64) hipLaunchKernelGGL(prefill_attn_gqa_kernel<64>, grid, dim3(64 * R), lds, s, p, kch, ntiles);
+        else hipLaunchKernelGGL(prefill_attn_gqa_kernel<128>, grid, dim3(64 * R), lds, s, p, kch, ntiles);
+    } else {
+        const dim3 grid((unsigned)((p.P + 15) / 16), (unsigned)p.n_head, (unsigned)nch);
+        if (p.head_dim == 64) hipLaunchKernelGGL(prefill_attn_f16_kernel<64>, grid, dim3(64), 0, s, p, kch, ntiles);
+        else hipLaunchKernelGGL(prefill_attn_f16_kernel<128>, grid, dim3(64), 0, s, p, kch, ntiles);
+    }
     GAJE_HIP_CHECK(hipGetLastError());
     if (!p.merged_later) {
         hipLaunchKernelGGL(prefill_attn_merge_kernel, dim3((unsigned)p.P, (unsigned)p.n_head), dim3(128), 0, s, p, kch);

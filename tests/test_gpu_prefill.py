@@ -28,6 +28,10 @@ HD64 = dict(n_embd=256, n_head=4, n_head_kv=2, n_blocks=2, ffn=512, vocab_size=1
             rope_base=1e4, arch_family=1, qkv_bias=1, tied_embeddings=0)
 HD128 = dict(n_embd=512, n_head=4, n_head_kv=1, n_blocks=3, ffn=1024, vocab_size=2048, eps=1e-6,
              rope_base=1e6, arch_family=3, qkv_bias=1, tied_embeddings=0)
+# shapes the GQA-shared attention kernel does not take (one query head per kv
+# head; two query heads of 128 dimensions per kv head), run by the per-head kernel
+HD64_MHA = dict(HD64, n_head_kv=4)
+HD128_R2 = dict(HD128, n_head_kv=2)
 
 
 @pytest.fixture(scope="module")
@@ -75,7 +79,8 @@ def _check(got, ref, label):
         assert int(np.argmax(got)) == int(np.argmax(ref))
 
 
-@pytest.mark.parametrize("cfg,name,n", [(HD64, "hd64", 40), (HD128, "hd128", 70)])
+@pytest.mark.parametrize("cfg,name,n", [(HD64, "hd64", 40), (HD128, "hd128", 70), (HD128, "hd128_long", 300),
+                                        (HD64_MHA, "hd64_mha", 40), (HD128_R2, "hd128_r2", 70)])
 def test_prefill_mfma_last_logits(hip, O, tmp_models, cfg, name, n):
     p = _write(hip, tmp_models / f"pf_{name}.flat", seed=11, **cfg)
     prompt = _tokens(n, cfg["vocab_size"], 12)
