@@ -367,6 +367,9 @@ int scratch_ptr(void **out) {
 extern "C" int gaje_hip_q4_0_gemm_mfma_noalloc(const void *packed, const float *X, const float *bias, int64_t bias_len,
                                                float *Y, int64_t m, int64_t n, int64_t k, void *stream) {
     clear_error();
+    GAJE_TRY(check_dims(n, k));
+    if (k % 32 || m < 0) return set_error(GAJE_ERR_INVALID_ARG, "bad gemm arguments");
+    if (m == 0 || n == 0) return GAJE_OK;  // an empty product, as gaje_hip_q4_0_gemm_mfma returns it
     const int64_t need = gaje_hip_q4_0_gemm_mfma_workspace(m, n, k);
     if (need < 0) return set_error(GAJE_ERR_INVALID_ARG, "bad gemm arguments");
     if (need > GAJE_NOALLOC_SCRATCH_BYTES)

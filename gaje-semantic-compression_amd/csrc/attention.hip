@@ -313,6 +313,31 @@ __device__ __forceinline__ float wide_score(const float4 (&k)[16], const float (
     return u == 0 ? tot[0] : u == 1 ? tot[1] : u == 2 ? tot[2] : tot[3];
 }
 
+// Bounded spin on an LDS counter: returns true once *c >= target, false if
+// the bound (2^22 polls, tens of milliseconds) runs out.  The producers and
+// consumers of the kernels below wait on each other only along chains that
+// always end, so the bound is never reached; it keeps a mistake from turning
+// into a hang, and the caller reports a wait that ran out (ST_WAIT in the
+// sequence's guard code) so the host returns an error instead of the outputs.
+__device__ __forceinline__ void wait_ran_out(const AttnParams &p, int z) {
+    const uint32_t code = (uint32_t)(p.layer * 8 + ST_WAIT);
+    if (p.seq_nan) atomicMin(&p.seq_nan[z], code);
+    else if (p.st) atomicMin(&p.st->nan_code, code);
+}
+
+__device__ __forceinline__ bool lds_wait_ge(int *c, int target) {
+    bool ok = false;
+    for (int spin = 0; spin < (1 << 22); ++spin) {
+        if (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) {
+            ok = true;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    return ok;
+}
+
 template <int HD, int DS>
 __global__ __launch_bounds__(WIDE) void attn_decode_wide(AttnParams p) {
     using S = WideShape<HD>;
@@ -473,28 +498,17 @@ __global__ __launch_bounds__(WIDE) void attn_decode_wide(AttnParams p) {
         }
     } else {
         // ---- out_i = sum_t products, DS chains in wave 0 ----
+        bool waited_out = false;
         auto ready = [&](int t) {
-            while (__hip_atomic_load(&pdone[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < NPROD)
-                __builtin_amdgcn_s_sleep(1);
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+            if (!lds_wait_ge(&pdone[t], NPROD)) waited_out = true;
         };
         const float acc = baton_chains<L>(vs, vstride, P, lane, ready);
         const int rel = (lane - (P - 1)) & 63;
         if (rel % L == 0) p.out[(size_t)h * HD + d0 + rel / L] = acc;
+        if (waited_out && lane == 0) wait_ran_out(p, 0);
     }
 }
 
-// Bounded spin on an LDS counter: returns once *c >= target.  The producers
-// and consumers below wait on each other only along a chain that always ends
-// (see attn_batch_wide), so the bound is never reached; it keeps a mistake
-// from turning into a hang (the results would then be wrong, not late).
-__device__ __forceinline__ void lds_wait_ge(int *c, int target) {
-    for (int spin = 0; spin < (1 << 22); ++spin) {
-        if (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
-        __builtin_amdgcn_s_sleep(1);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-}
 
 // Batched decode, wide form: one workgroup of WIDE threads per (query head,
 // sequence).  Scores, exponentials and the softmax sum as attn_decode_wide
@@ -622,11 +636,11 @@ __global__ __launch_bounds__(WIDE) void attn_batch_wide(AttnParams p) {
 #pragma unroll
         for (int d = 0; d < BW_D; ++d)
             if (d < T) loadV(vr[d], d);
-        lds_wait_ge(&inv_flag, 1);
+        bool waited_out = !lds_wait_ge(&inv_flag, 1);
         const float inv = inv_slot;
         auto produce = [&](const float4 (&v)[B::PT], int t) {
             const int b = t % BW_NB;
-            if (t >= BW_NB) lds_wait_ge(&freed[b], BW_NCW * (t / BW_NB));
+            if (t >= BW_NB && !lds_wait_ge(&freed[b], BW_NCW * (t / BW_NB))) waited_out = true;
             float *dst = tiles + b * B::TILE;
 #pragma unroll
             for (int i = 0; i < B::PT; ++i) {
@@ -653,6 +667,7 @@ __global__ __launch_bounds__(WIDE) void attn_batch_wide(AttnParams p) {
                 }
             }
         }
+        if (waited_out && lane == 0) wait_ran_out(p, z);
         return;
     }
 
@@ -671,8 +686,9 @@ __global__ __launch_bounds__(WIDE) void attn_batch_wide(AttnParams p) {
         constexpr int L = B::L, G = B::G, KT = BATON_KT;
         const int r = lane / L, j = lane % L;
         float xa[KT], xb[KT];
+        bool waited_out = false;
         auto load = [&](float (&x)[KT], int t) {
-            lds_wait_ge(&ready[t % BW_NB], B::NPW * (t / BW_NB + 1));
+            if (!lds_wait_ge(&ready[t % BW_NB], B::NPW * (t / BW_NB + 1))) waited_out = true;
             const int jj = min(j, P - 1 - t * L);  // lanes past the last phase re-read it (unused)
             const int gg = ((r - t) % G + G) % G;
             const float4 *src = (const float4 *)(tiles + (t % BW_NB) * B::TILE + (wave * G + gg) * B::TPS + jj * KT);
@@ -714,6 +730,7 @@ __global__ __launch_bounds__(WIDE) void attn_batch_wide(AttnParams p) {
             const int64_t i = (int64_t)h * HD + wave * G + rel / L, rows = (int64_t)p.n_head * HD;
             p.out[z * p.seq_q_stride + (p.out_chain_major ? (i & 7) * (rows / 8) + (i >> 3) : i)] = acc;
         }
+        if (waited_out && lane == 0) wait_ran_out(p, z);
     }
 }
 

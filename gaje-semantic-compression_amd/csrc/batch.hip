@@ -519,7 +519,7 @@ __global__ __launch_bounds__(1024) void argmax_rows_kernel(const float *x, int64
     for (int64_t i = tid; i < n; i += 1024) {
         const float v = x[(size_t)s * ld + i];
         if (isnan(v)) continue;
-        const unsigned long long k = ((unsigned long long)order_key(v) << 32) | (0xFFFFFFFFu - (uint32_t)i);
+        const unsigned long long k = ((unsigned long long)max_key(v) << 32) | (0xFFFFFFFFu - (uint32_t)i);
         key = k > key ? k : key;
     }
     for (int o = 32; o > 0; o >>= 1) {

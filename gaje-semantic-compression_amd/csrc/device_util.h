@@ -160,6 +160,10 @@ __device__ __forceinline__ uint32_t order_key(float f) {
     uint32_t u = __float_as_uint(f);
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
+// Key of a logit for the first-maximum searches: -0 is taken as +0 first, so
+// that the two zeros tie as they do under the reference's strict '>'
+// (llm/forward.rs:262-271) and the lower index wins.
+__device__ __forceinline__ uint32_t max_key(float f) { return order_key(f == 0.0f ? 0.0f : f); }
 __device__ __forceinline__ float order_key_inv(uint32_t k) {
     uint32_t u = (k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k;
     return __uint_as_float(u);

@@ -1059,7 +1059,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(GemvParams p, int64_t npa
     if (mode == MODE_ARGMAX && st) {
         unsigned long long key =
             best_v > -INFINITY
-                ? ((unsigned long long)order_key(best_v) << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)best_i)
+                ? ((unsigned long long)max_key(best_v) << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)best_i)
                 : 0ull;
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) {
@@ -1209,7 +1209,7 @@ __global__ __launch_bounds__(THREADS) void gemv_q8_stream_kernel(GemvParams p, i
     if constexpr (MODE == MODE_ARGMAX) {
         unsigned long long key =
             best_v > -INFINITY
-                ? ((unsigned long long)order_key(best_v) << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)best_i)
+                ? ((unsigned long long)max_key(best_v) << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)best_i)
                 : 0ull;
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) {

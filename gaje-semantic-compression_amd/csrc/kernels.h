@@ -52,6 +52,8 @@ enum NanStage : int32_t {
     ST_FFN_OUT = 3,     // "NaN in ffn_out"                    :111-113
     ST_PROJ_FFN = 4,    // "NaN in projected_ffn"              :128-130
     ST_FINAL = 5,       // "NaN after projected_ffn addition"  :138-140
+    ST_WAIT = 6,        // a bounded in-kernel wait ran out (an internal error:
+                        // that step's attention outputs are invalid)
     ST_NONE = -1,
 };
 
@@ -165,6 +167,11 @@ struct AttnParams {
     int64_t seq_kv_stride, seq_q_stride;
     int32_t n_seq;
     int32_t out_chain_major;
+    // where a kernel whose LDS producers and consumers wait on each other
+    // reports a wait that ran out of its spin bound (layer * 8 + ST_WAIT):
+    // st->nan_code for one sequence, seq_nan[z] for batched sequence z
+    uint32_t *seq_nan;
+    int32_t layer;
 };
 int launch_attention(const AttnParams &p, hipStream_t s);
 size_t attention_lds_bytes(int head_dim, int64_t max_ctx);

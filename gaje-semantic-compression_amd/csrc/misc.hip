@@ -112,7 +112,7 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float *x, int64_t n,
         if (v > bv) { bv = v; bi = i; }
     }
     if (bv > -INFINITY)
-        atomicMax(&best, ((unsigned long long)order_key(bv) << 32) | (0xFFFFFFFFull - (uint64_t)bi));
+        atomicMax(&best, ((unsigned long long)max_key(bv) << 32) | (0xFFFFFFFFull - (uint64_t)bi));
     __syncthreads();
     if (threadIdx.x == 0) *idx = best ? 0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFull) : 0u;
 }
@@ -133,7 +133,7 @@ __global__ __launch_bounds__(256) void gen_select_kernel(const float *x, int64_t
         if ((seen[i >> 5] >> (i & 31)) & 1u) v = v < 0.0f ? v * pen : v / pen;
         if (v > bv) { bv = v; bi = i; }
     }
-    unsigned long long key = bv > -INFINITY ? ((unsigned long long)order_key(bv) << 32) | (0xFFFFFFFFull - (uint64_t)bi) : 0ull;
+    unsigned long long key = bv > -INFINITY ? ((unsigned long long)max_key(bv) << 32) | (0xFFFFFFFFull - (uint64_t)bi) : 0ull;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
         const unsigned long long other = __shfl_xor(key, o, WAVE);

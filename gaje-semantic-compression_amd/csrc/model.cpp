@@ -79,6 +79,7 @@ const char *nan_message(int stage) {
         case ST_FFN_OUT: return "NaN in ffn_out";
         case ST_PROJ_FFN: return "NaN in projected_ffn";
         case ST_FINAL: return "NaN after projected_ffn addition";
+        case ST_WAIT: return "attention: an in-kernel wait ran out of its bound (internal error; the step's outputs are invalid)";
         default: return "NaN";
     }
 }
@@ -618,6 +619,7 @@ int enqueue_token(gaje_hip_model *m, hipEvent_t ev_blocks_done) {
         ap.kv_cap = m->cap;
         ap.out = m->attn_out;
         ap.st = m->st;
+        ap.layer = (int32_t)l;
         GAJE_TRY(launch_attention(ap, m->stream));
 
         p = gemv_base(m, Ly.o, m->attn_out);
@@ -707,7 +709,7 @@ int read_state(gaje_hip_model *m, DevState &s) {
 
 int nan_error(const DevState &s) {
     const int stage = (int)(s.nan_code % 8);
-    return set_error(GAJE_ERR_NAN, "%s", nan_message(stage));
+    return set_error(stage == ST_WAIT ? GAJE_ERR_HIP : GAJE_ERR_NAN, "%s", nan_message(stage));
 }
 
 int64_t kwta_k(int64_t n, float ratio) {
@@ -1481,6 +1483,8 @@ int batch_enqueue_step(gaje_hip_batch *b, const uint32_t *ids, int64_t n, int64_
         ap.seq_q_stride = m->q_rows;
         ap.n_seq = (int32_t)b->nseq;
         ap.out_chain_major = 1;
+        ap.seq_nan = b->st.nan_codes;
+        ap.layer = (int32_t)li;
         GAJE_TRY(launch_attention(ap, s));
         BatchGemvParams g = batch_gemv(b, Ly.o, b->ATT, m->q_rows, b->H, E);
         g.mode = MODE_RESIDUAL;
@@ -1531,7 +1535,9 @@ int batch_sync(gaje_hip_batch *b, int32_t *status) {
         if (status) status[q] = halted[q] ? (int32_t)(err[q] % 8) + 1 : 0;
         if (halted[q] && first < 0) first = (int)q;
     }
-    if (first >= 0) return set_error(GAJE_ERR_NAN, "%s", nan_message((int)(err[first] % 8)));
+    if (first >= 0)
+        return set_error((int)(err[first] % 8) == ST_WAIT ? GAJE_ERR_HIP : GAJE_ERR_NAN, "%s",
+                         nan_message((int)(err[first] % 8)));
     return GAJE_OK;
 }
 
@@ -1990,6 +1996,7 @@ extern "C" int gaje_hip_time_stage(gaje_hip_model *m, int stage, int64_t layer, 
                 ap.kv_cap = m->cap;
                 ap.out = m->attn_out;
                 ap.st = m->st;
+                ap.layer = (int32_t)layer;
                 algo = (int64_t)(m->pos + 1) * 2 * m->kv_rows * 4 + 2 * m->q_rows * 4;
                 return launch_attention(ap, m->stream);
             }

@@ -112,7 +112,15 @@ def export_gaje_flat(path: str, tensors, n_embd: int, n_head: int, n_head_kv: in
     """export_gaje_flat over f32 tensors keyed by their GGUF names (token_embd.weight,
     output_norm.weight, lm_head.weight (else the tied token_embd), blk.{i}.attn_norm.weight,
     blk.{i}.ffn_norm.weight, blk.{i}.attn_{q,k,v}.weight (+ .bias), blk.{i}.attn_output.weight,
-    blk.{i}.ffn_{gate,up,down}.weight), each [out][in]."""
+    blk.{i}.ffn_{gate,up,down}.weight), each [out][in].
+
+    body="q4_0" (the default) is the reference exporter's output: Q4_0 blocks and
+    quant_format 1 (scripts/export_gaje_flat.py).  body="lut4" is an extension
+    with no counterpart in that exporter: it writes quant_format 0 and runs
+    genomize_4bit_core over each whole tensor, where the reference's GenomicLayer
+    splits tensors over 100 MB into 10000-row chunks with their own thresholds
+    and anchor buffers; files it writes for such tensors are not what the
+    reference would write."""
     T = {k: _f32(v) for k, v in tensors.items()}
     emb = "q8_0" if quant_embed else "f32"
     w = FlatWriter()

@@ -32,9 +32,13 @@ What pins each part (tests/test_oracle_*.py):
   K-WTA                     brute-force sort
   header / reader           header/tests.rs:7-48 KATs, exporter layout
   whole forward             torch CPU fp32 composition from the dequantised weights
+  sampling branch            its distribution (chi-square against softmax(l / T)), the
+                            near-greedy limit and the penalty before the draw
+  use_genomic_norm           a float64 composition (tests/fp64_model.py) where it fires
 Parity unpinned: the exact bits of glibc expf/powf/sinf/cosf as the Rust build
-would see them (no Rust toolchain here); the multinomial branch of
-generate_native_core (thread_rng upstream, so nothing fixes its draws).
+would see them (no Rust toolchain here); the sampled tokens themselves
+(thread_rng upstream, so nothing fixes its draws; the device's splitmix draws
+are restated by SplitMixDraws).
 """
 from __future__ import annotations
 
@@ -477,9 +481,12 @@ class RustGenomicBlock:
         if np.isnan(ffn_out).any():
             raise ValueError("NaN in ffn_out")
         if self.use_genomic_norm:
-            # block/forward.rs:115-123 (rayon sum: order unspecified upstream)
-            rms = np.float32(np.sqrt(np.float32(np.sum(ffn_out * ffn_out, dtype=np.float32)
-                                                / np.float32(ffn_out.size)) + self.eps))
+            # block/forward.rs:115-123.  Upstream sums with a rayon reduction
+            # whose order is not fixed; here (and on the device) a sequential
+            # float32 sum of the rounded squares, in element order.
+            sq = (ffn_out * ffn_out).astype(np.float32)
+            ss = np.cumsum(sq, dtype=np.float32)[-1] if sq.size else np.float32(0.0)
+            rms = np.float32(np.sqrt(np.float32(np.float32(ss / np.float32(ffn_out.size)) + self.eps)))
             if rms > self.h_scale:
                 ffn_out = (ffn_out * np.float32(self.h_scale / rms)).astype(np.float32)
         proj_ffn = self.w_down.forward_core(ffn_out)
@@ -564,17 +571,10 @@ class GenomicLLM:
                             logits[t] = np.float32(logits[t] * np.float32(repetition_penalty))
                         else:
                             logits[t] = np.float32(logits[t] / np.float32(repetition_penalty))
-            if temperature <= 1e-5:
+            if np.float32(temperature) <= np.float32(1e-5):
                 nxt = argmax_first(logits)
             else:
-                if rng is None:
-                    raise ValueError("sampling needs an rng (upstream uses thread_rng)")
-                m = logits.max()
-                p = np.exp((logits - m) / np.float32(temperature)).astype(np.float32)
-                r = np.float32(rng.random()) * p.sum(dtype=np.float32)
-                c = np.cumsum(p, dtype=np.float32)
-                hit = np.nonzero(r <= c)[0]
-                nxt = int(hit[0]) if hit.size else 0
+                nxt = sample_next(logits, temperature, rng)
             generated.append(int(nxt))
             if nxt in eos_token_ids:
                 break
@@ -645,6 +645,52 @@ def moe_ffn(x: np.ndarray, router: np.ndarray, gate_up, down, ffn: int):
             f.append(dn[e].forward_core(swiglu_balanced(g[:ffn], g[ffn:])))
         y[t] = (w[t, 0] * f[0]).astype(np.float32) + (w[t, 1] * f[1]).astype(np.float32)
     return y, idx, w
+
+
+def sample_next(logits: np.ndarray, temperature: float, rng) -> int:
+    """The multinomial branch of generate_native_core (forward.rs:272-297):
+    max by strict '>', p_i = exp((l_i - max) / T), a sequential float32 sum,
+    r = u * sum with one uniform draw u, then the first i whose running sum
+    reaches r (0 if none)."""
+    if rng is None:
+        raise ValueError("sampling needs an rng (upstream uses thread_rng)")
+    logits = _f32(logits)
+    fin = logits[~np.isnan(logits)]
+    m = fin.max() if fin.size else np.float32(-np.inf)
+    p = expf(((logits - m) / np.float32(temperature)).astype(np.float32))
+    c = np.cumsum(p, dtype=np.float32)
+    r = np.float32(np.float32(_draw(rng)) * c[-1])
+    hit = np.nonzero(r <= c)[0]
+    return int(hit[0]) if hit.size else 0
+
+
+class SplitMixDraws:
+    """The uniform draws of the device library's sampler: a splitmix64 stream,
+    state += 0x9E3779B97F4A7C15, u = (mix(state) >> 40) * 2^-24, a float32 in
+    [0, 1) with 24 random bits (the form of rand's gen::<f32>() that
+    forward.rs:287 draws from thread_rng).  Seeded like gaje_hip_generate."""
+
+    def __init__(self, seed: int):
+        self.state = int(seed) & 0xFFFFFFFFFFFFFFFF
+
+    @staticmethod
+    def mix(z: int) -> int:
+        M = 0xFFFFFFFFFFFFFFFF
+        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & M
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & M
+        return z ^ (z >> 31)
+
+    def __call__(self) -> np.float32:
+        self.state = (self.state + 0x9E3779B97F4A7C15) & 0xFFFFFFFFFFFFFFFF
+        return np.float32((self.mix(self.state) >> 40) * 2.0 ** -24)
+
+
+def _draw(rng) -> np.float32:
+    """One uniform float32 in [0, 1): rng is a callable (SplitMixDraws) or a
+    numpy Generator (24 random bits, as rand's gen::<f32>())."""
+    if callable(rng):
+        return np.float32(rng())
+    return np.float32(int(rng.integers(0, 1 << 24)) * 2.0 ** -24)
 
 
 def argmax_first(logits: np.ndarray) -> int:

@@ -248,6 +248,27 @@ def test_tiny_generate_eos_and_host_path(hip, O, tiny):
     g.close()
 
 
+@pytest.mark.parametrize("temperature,penalty,kwta,seed", [(0.7, 1.0, 0.0, 0), (0.7, 1.3, 0.0, 11),
+                                                            (1.5, 1.1, 0.5, 42), (0.05, 1.0, 0.0, 5)])
+def test_tiny_generate_sampling_matches_oracle(hip, O, tiny, temperature, penalty, kwta, seed):
+    """The multinomial branch (forward.rs:272-297) with the device library's
+    seeded splitmix draws: the oracle, handed the same draw stream, samples the
+    same tokens, since the logits are the same bits and the exponentials, the
+    sequential sum and the running-sum search are the reference's."""
+    prompt = _tokens(6, TINY["vocab_size"], 21)
+    g = hip.load_genomic_auto(tiny)
+    g.set_k_wta_ratio(kwta)
+    r = O.load_genomic(tiny)
+    r.set_k_wta_ratio(kwta)
+    got = g.generate_native_py(prompt, max_new_tokens=40, temperature=temperature,
+                               repetition_penalty=penalty, eos_token_ids=[2], seed=seed)
+    ref = r.generate_native_core(prompt, 40, temperature, penalty, [2], rng=O.SplitMixDraws(seed))
+    print(f"sampling T={temperature} penalty={penalty} kwta={kwta}: {len(got)} tokens, {len(set(got))} distinct")
+    assert got == ref
+    assert g.cache_len() == r.blocks[0].attn.k_cache_len()
+    g.close()
+
+
 def test_tiny_generate_empty_prompt_error(hip, tiny):
     g = hip.load_genomic_auto(tiny)
     with pytest.raises(ValueError, match="Prompt tokens cannot be empty"):
@@ -271,6 +292,15 @@ def test_json_config_interleaved_rope_genomic_norm(hip, O, tmp_models):
     r = O.load_genomic(p)
     assert r.config.config["rope_style"] == "interleaved" and r.blocks[0].use_genomic_norm
     assert _compare_stream(hip, O, p, _tokens(8, TINY["vocab_size"], 8)) <= TOL
+
+
+def test_genomic_norm_branch_fires(hip, O, tmp_models):
+    """use_genomic_norm where its scaling fires (rms > h_scale in most blocks):
+    bit for bit with the oracle, whose branch a float64 composition pins
+    (tests/test_oracle_model.py)."""
+    from conftest import write_genomic_norm_model
+    p = write_genomic_norm_model(str(tmp_models))
+    assert _compare_stream(hip, O, p, _tokens(10, 300, 31)) == 0.0
 
 
 def test_nan_embedding_row_raises(hip, O, tmp_models, tiny):

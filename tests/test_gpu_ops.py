@@ -238,6 +238,18 @@ def test_argmax_first_max(hip, O):
     assert int(idx.read(np.uint32)[0]) == O.argmax_first(x) == 5
 
 
+def test_argmax_signed_zero_tie(hip, O):
+    """-0.0 before +0.0 as the maximum: the reference's strict '>' finds them
+    equal, so the first (the -0.0) wins."""
+    x = -np.abs(hip.synth.normal(72, "amz", 151936)) - 1.0
+    x[7] = -0.0
+    x[100000] = 0.0
+    d = _dev(hip, x)
+    idx = _out(hip, 4)
+    hip.ops.argmax(d, x.size, idx)
+    assert int(idx.read(np.uint32)[0]) == O.argmax_first(x) == 7
+
+
 def test_expf_device_matches_host_libm(hip, O):
     """The device exponential against the host expf on 16.7M inputs spread over
     the whole float range, plus the special values."""

@@ -12,7 +12,14 @@ expected sequence follows from the reference's rules alone:
     last three w-long chunks are equal.
 Each case is chosen so that a plausible slip (penalty sign rule swapped, '>='
 in the argmax, detector bounds off by one, EOS not emitted) changes the
-expected stream.  The multinomial branch (thread_rng upstream) stays unpinned.
+expected stream.
+
+The multinomial branch (:272-297) draws from thread_rng upstream, so no token
+stream is fixed there; what it does fix is pinned instead: the distribution
+(a chi-square test of seeded draws against softmax(l / T) in float64, which a
+temperature applied the wrong way or a dropped 1/T fails), the near-greedy
+limit (T just above 1e-5 with a clear maximum always picks it), and the order
+of the penalty before the draw.
 """
 import numpy as np
 import pytest
@@ -146,3 +153,84 @@ def test_penalty_three_way_cycle():
     # whose last three 2-chunks are first equal at 9 tokens.
     out, _ = _gen(lambda t, n: [3.0, 2.9, 2.8, -1.0], [3], 50, penalty=1.25)
     assert out == [0, 1, 2, 0, 0, 0, 0, 0, 0]
+
+
+# ---- the multinomial branch (forward.rs:272-297) ---------------------------
+
+_LOGITS = np.array([1.2, -0.4, 2.0, 0.3, 1.9, -2.5, 0.0, 1.1, 0.8, -1.0, 2.2, 0.5], np.float32)
+
+
+def _chi2(counts, p):
+    exp = p * counts.sum()
+    return float(((counts - exp) ** 2 / exp).sum())
+
+
+def test_sampler_distribution_chi_square():
+    T, N = 0.7, 20000
+    rng = O.SplitMixDraws(12345)
+    counts = np.bincount([O.sample_next(_LOGITS, T, rng) for _ in range(N)], minlength=_LOGITS.size)
+    l64 = _LOGITS.astype(np.float64)
+    p = np.exp((l64 - l64.max()) / T)
+    p /= p.sum()
+    # 11 degrees of freedom: the 0.999 quantile is 31.26
+    assert _chi2(counts, p) < 31.26
+    # the test tells the distribution apart from plausible slips
+    for wrong in (np.exp((l64 - l64.max()) * T), np.exp(l64 - l64.max())):
+        assert _chi2(counts, wrong / wrong.sum()) > 200.0
+
+
+def test_sampler_numpy_generator_draws():
+    # a numpy Generator stands in for thread_rng with the same 24-bit draws
+    rng = np.random.default_rng(3)
+    counts = np.bincount([O.sample_next(_LOGITS, 1.3, rng) for _ in range(20000)], minlength=_LOGITS.size)
+    l64 = _LOGITS.astype(np.float64)
+    p = np.exp((l64 - l64.max()) / 1.3)
+    assert _chi2(counts, p / p.sum()) < 31.26
+
+
+def test_sampler_draw_stream():
+    # the device library's splitmix stream: state += golden gamma, 24 bits of mix(state)
+    d = O.SplitMixDraws(0)
+    u = [d() for _ in range(3)]
+    st, M = 0, (1 << 64) - 1
+    for k in range(3):
+        st = (st + 0x9E3779B97F4A7C15) & M
+        z = st
+        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & M
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & M
+        z ^= z >> 31
+        assert u[k] == np.float32((z >> 40) / 2.0 ** 24)
+    assert all(0.0 <= v < 1.0 for v in u)
+
+
+def test_sampler_near_greedy_limit():
+    # T just above the greedy threshold: exp((l - max) / T) underflows to 0 for
+    # every logit a clear margin below the maximum, so the maximum is always drawn
+    rng = O.SplitMixDraws(7)
+    picks = {O.sample_next(_LOGITS, 1.1e-5, rng) for _ in range(2000)}
+    assert picks == {int(np.argmax(_LOGITS))}
+    # at T = 1e-5 the loop takes the greedy branch and needs no rng at all
+    out, _ = _gen(lambda t, n: _LOGITS, [1], 3, temperature=1e-5)
+    assert out == [10, 10, 10]
+
+
+def test_sampler_penalty_applies_before_the_draw():
+    # near-greedy sampling with a penalty: 2.2 / 1.5 = 1.467 drops below 2.0,
+    # so the second token is 2; a penalty applied after the draw would give 10
+    # again.  Then 2.0 / 1.5 = 1.333 and 1.467 -> 1.9 (index 4) wins.
+    rng = O.SplitMixDraws(1)
+    stub = _Stub(lambda t, n: _LOGITS)
+    out = O.GenomicLLM.generate_native_core(stub, [0], 3, 2e-5, 1.5, [], rng=rng)
+    assert out == [10, 2, 4]
+
+
+def test_sampler_needs_an_rng():
+    with pytest.raises(ValueError, match="rng"):
+        _gen(lambda t, n: _LOGITS, [1], 2, temperature=0.7)
+
+
+def test_signed_zero_maximum_ties():
+    # -0.0 and +0.0 compare equal under the strict '>', so the first one wins
+    assert O.argmax_first(np.array([-1.0, -0.0, 0.0, -2.0], np.float32)) == 1
+    out, _ = _gen(lambda t, n: [-1.0, -0.0, 0.0, -2.0], [3], 2)
+    assert out == [1, 1]

@@ -13,43 +13,14 @@ benchmark; the genomic norm and the 2-bit paths are not part of HF's model.
 import numpy as np
 import pytest
 
-from conftest import floored_rel_err
+from conftest import GNORM_MODEL, floored_rel_err, write_genomic_norm_model
 
 torch = pytest.importorskip("torch")
 transformers = pytest.importorskip("transformers")
 
 from oracle import oracle as O  # noqa: E402
 from oracle.flat import FlatFile  # noqa: E402
-
-
-def tensor_weights(ff: FlatFile, name: str):
-    """Exact float64 weights [out][in] and bias of a flat tensor."""
-    e = ff.tensors[name]
-    n, k = e["out_features"], e["in_features"]
-    dna = np.asarray(ff.get_slice(e["dna_off"], e["dna_len"]))
-    bias = ff.get_f32_slice(e["bias_off"], e["bias_len"]).astype(np.float64)
-    if e["bit_depth"] == 32:
-        w = np.frombuffer(dna.tobytes(), np.float32)[: n * k].reshape(n, k).astype(np.float64)
-        return w, bias
-    nb = k // 32
-    if e["c_len"] == 0:  # Q4_0 blocks: q * scale + min exactly (f16 scale / min)
-        b = dna[: n * nb * 20].reshape(n * nb, 20)
-        sc = b[:, 0:2].copy().view(np.float16).astype(np.float64)
-        mn = b[:, 2:4].copy().view(np.float16).astype(np.float64)
-        q = np.empty((n * nb, 32))
-        q[:, 0::2], q[:, 1::2] = b[:, 4:] & 15, b[:, 4:] >> 4
-        return (q * sc + mn).reshape(n, k), bias
-    # LUT 4-bit: high nibble = even element; tables expanded as init.rs:109-124
-    t = ff.get_f32_slice(e["c_off"], e["c_len"]).astype(np.float64)
-    if t.size == 16:
-        t = np.tile(t, n * nb)
-    elif t.size == nb * 16:
-        t = np.tile(t, n)
-    t = t[: n * nb * 16].reshape(n * nb, 16)
-    c = dna[: n * nb * 16].reshape(n * nb, 16)
-    idx = np.empty((n * nb, 32), np.int64)
-    idx[:, 0::2], idx[:, 1::2] = c >> 4, c & 15
-    return np.take_along_axis(t, idx, axis=1).reshape(n, k), bias
+from fp64_model import forward_fp64, tensor_weights  # noqa: E402
 
 
 def hf_model(ff: FlatFile, cfg, vocab, ffn, rope_base):
@@ -114,3 +85,46 @@ def test_oracle_forward_matches_hf_qwen2(tmp_path, body_format, fused):
         assert err < 1e-3, (i, err)
     # a wiring slip is not small: the logits of the wrong position are far off
     assert floored_rel_err(r.forward_core(ids[0], True), ref[1]) > 1e-2
+
+
+def test_fp64_composition_matches_hf(tmp_path):
+    """tests/fp64_model.forward_fp64 (the float64 reference for deep-model noise
+    floors) is the same function as HF's Qwen2 in float64.  HF keeps its
+    RMSNorm statistics and rotary tables in float32 even in a float64 model,
+    which leaves ~1e-7 of the largest logit; a wiring slip is O(1)."""
+    import gaje_hip
+    vocab, ffn, base = 300, 192, 10000.0
+    path = str(tmp_path / "m.flat")
+    gaje_hip.synth.write_flat(path, n_embd=128, n_head=4, n_head_kv=2, n_blocks=2, ffn=ffn, vocab_size=vocab,
+                              eps=1e-6, rope_base=base, arch_family=1, qkv_bias=1, tied_embeddings=0, seed=31)
+    ff = FlatFile(path)
+    m = hf_model(ff, ff.model_config(), vocab, ffn, base)
+    ids = [5, 299, 17, 0, 123, 42, 7, 7]
+    with torch.no_grad():
+        ref = m(torch.tensor([ids])).logits[0].numpy()
+    got = forward_fp64(ff, ff.model_config(), ids, logits_for="all")
+    assert np.max(np.abs(got - ref)) < 1e-6 * np.max(np.abs(ref))
+    assert np.allclose(forward_fp64(ff, ff.model_config(), ids), got[-1], rtol=0, atol=1e-12)
+
+
+def test_genomic_norm_branch_fp64(tmp_path):
+    """use_genomic_norm (block/forward.rs:115-123, h_scale 1 from flat_reader.rs:220):
+    where the SwiGLU output's rms exceeds 1 it is scaled to rms 1.  The oracle
+    against the float64 composition, on a model where the branch fires in
+    every block; without the scaling the logits are far off."""
+    path = write_genomic_norm_model(str(tmp_path))
+    r = O.load_genomic(path)
+    r.set_k_wta_ratio(0.0)
+    assert r.blocks[0].use_genomic_norm
+    ids = [5, 299, 17, 0, 123, 42]
+    stats = {}
+    ref = forward_fp64(r.flat, r.config, ids, logits_for="all", stats=stats)
+    assert stats["gnorm_fired"] >= len(ids) * GNORM_MODEL["n_blocks"] // 2
+    for i, t in enumerate(ids):
+        err = floored_rel_err(r.forward_core(t, i == 0), ref[i])
+        assert err < 1e-3, (i, err)
+    import copy
+    cfg = copy.deepcopy(r.config)
+    cfg.config["use_genomic_norm"] = False
+    off = forward_fp64(r.flat, cfg, ids, logits_for="all")
+    assert floored_rel_err(off[-1], ref[-1]) > 1e-2

@@ -48,3 +48,14 @@ def test_noalloc_rejects_beyond_scratch():
     assert hip.ops.q4_0_gemm_mfma_workspace(m, n, k) > (64 << 20)
     with pytest.raises(GajeError, match="scratch"):
         check(lib().gaje_hip_q4_0_gemm_mfma_noalloc(None, None, None, 0, None, m, n, k, None))
+
+
+def test_noalloc_empty_products_match():
+    """m == 0 or n == 0: both entry points return OK without a launch."""
+    import gaje_hip as hip
+    from gaje_hip._lib import check, lib
+    if hip.ops.device_count() < 1:
+        pytest.fail("no HIP device visible")
+    for m, n in ((0, 256), (16, 0), (0, 0)):
+        check(lib().gaje_hip_q4_0_gemm_mfma_noalloc(None, None, None, 0, None, m, n, 512, None))
+        check(lib().gaje_hip_q4_0_gemm_mfma(None, None, None, 0, None, m, n, 512, None, 0, None))
