@@ -75,6 +75,17 @@ __device__ __forceinline__ void lds_dma16_so(const void *base, uint32_t voff, ui
                  : "v"(voff), "s"(bs), "s"(__builtin_amdgcn_readfirstlane(lds))
                  : "memory", "m0");
 }
+// lds_dma16_so as a streaming (non-temporal) read.
+__device__ __forceinline__ void lds_dma16_so_nt(const void *base, uint32_t voff, uint32_t lds) {
+    const uint64_t b = (uint64_t)(uintptr_t)base;
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+    const uint64_t bs = ((uint64_t)hi << 32) | lo;
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt"
+                 :
+                 : "v"(voff), "s"(bs), "s"(__builtin_amdgcn_readfirstlane(lds))
+                 : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 // s_waitcnt for at most n outstanding vector memory operations (gfx9 encoding:

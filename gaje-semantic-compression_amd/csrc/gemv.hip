@@ -1294,6 +1294,19 @@ __device__ __forceinline__ void q4l_copy(const uint8_t *w, int64_t off, int64_t 
     }
 }
 
+// q4l_copy for a tile that lies wholly before the allocation's end: the
+// tile's address is wave-uniform (SGPRs) and each lane adds a loop-invariant
+// offset, v16 = 16 lane for the whole KiBs and vlast for the last one (its
+// bytes, or the tile's first 16 again past the tile's TB bytes), so a copy
+// costs no vector instruction.
+template <int N>
+__device__ __forceinline__ void q4l_copy_full(const uint8_t *w, int64_t off, uint32_t dst, uint32_t v16,
+                                              uint32_t vlast) {
+#pragma unroll
+    for (int i = 0; i < N - 1; ++i) lds_dma16_so_nt(w + off + i * 1024, v16, dst + i * 1024);
+    lds_dma16_so_nt(w + off, vlast, dst + (N - 1) * 1024);
+}
+
 // Copies n bytes (n % 16 == 0) from g to LDS at dst with one wave.
 __device__ __forceinline__ void lds_copy_bytes(const void *g, int64_t n, uint32_t dst, int lane) {
     for (int64_t o = 0; o < n; o += 1024)
@@ -1307,14 +1320,36 @@ __device__ __forceinline__ void lds_copy_bytes(const void *g, int64_t n, uint32_
 template <int G>
 __device__ __forceinline__ void q4l_rows2(const uint8_t *rp0, const uint8_t *rp1, const float4 (&xr)[4 * G], int l,
                                           int base, float &y0, float &y1) {
+    // the two rows' chain steps alternate, so that each step has the other
+    // row's step between it and its predecessor (a dependent fma waits for
+    // its input).  Reading the next group's LDS words a group ahead would
+    // take more registers than the kernel has left (x's registers spill).
     float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-        const vu2 n0 = *(const vu2 *)(rp0 + g * 80 + 8 * l), n1 = *(const vu2 *)(rp1 + g * 80 + 8 * l);
-        const vu4 s0 = *(const vu4 *)(rp0 + g * 80 + 64), s1 = *(const vu4 *)(rp1 + g * 80 + 64);
-        const X4 x{xr[4 * g], xr[4 * g + 1], xr[4 * g + 2], xr[4 * g + 3]};
-        a0 = q4_group(a0, n0, s0, x);
-        a1 = q4_group(a1, n1, s1, x);
+        const vu2 m0 = *(const vu2 *)(rp0 + g * 80 + 8 * l), m1 = *(const vu2 *)(rp1 + g * 80 + 8 * l);
+        const vu4 t0 = *(const vu4 *)(rp0 + g * 80 + 64), t1 = *(const vu4 *)(rp1 + g * 80 + 64);
+        float d0[4][4], d1[4][4];
+        q4_dequant_dw<0>(d0[0], m0.x, t0.x);
+        q4_dequant_dw<1>(d0[1], m0.x, t0.y);
+        q4_dequant_dw<0>(d0[2], m0.y, t0.z);
+        q4_dequant_dw<1>(d0[3], m0.y, t0.w);
+        q4_dequant_dw<0>(d1[0], m1.x, t1.x);
+        q4_dequant_dw<1>(d1[1], m1.x, t1.y);
+        q4_dequant_dw<0>(d1[2], m1.y, t1.z);
+        q4_dequant_dw<1>(d1[3], m1.y, t1.w);
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const float4 x = xr[4 * g + b];
+            a0 = fmaf(d0[b][0], x.x, a0);
+            a1 = fmaf(d1[b][0], x.x, a1);
+            a0 = fmaf(d0[b][1], x.y, a0);
+            a1 = fmaf(d1[b][1], x.y, a1);
+            a0 = fmaf(d0[b][2], x.z, a0);
+            a1 = fmaf(d1[b][2], x.z, a1);
+            a0 = fmaf(d0[b][3], x.w, a0);
+            a1 = fmaf(d1[b][3], x.w, a1);
+        }
     }
     float u = a0 + shfl(a0, base + ((l + 4) & 7)), v = u + shfl(u, base + ((l + 2) & 7));
     y0 = flush_small(v + shfl(v, base + ((l + 1) & 7)));
@@ -1354,12 +1389,17 @@ __global__ __launch_bounds__(WAVES * WAVE) void gemv_q4_lds_kernel(GemvParams p,
     __shared__ float inv_slot;
     __shared__ int or_in[WAVES], or_norm[WAVES];
     DevState *st = p.st;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // the wave index through readfirstlane: the compiler then keeps every
+    // tile and stage address in scalar registers
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l = lane & 7, r = lane >> 3, base = lane - l;
     const int64_t K4 = p.K >> 2;
     const XView xv{smem, xstride};
     uint8_t *raw = (uint8_t *)(smem + 8 * xstride);  // x, then norm_w, then the exponential table
     uint8_t *stages = raw + raw_bytes + (size_t)wave * STAGES * PER * 1024;
+    constexpr int TBI = TROWS * ROW_BYTES;  // bytes of TROWS rows
+    const uint32_t v16 = (uint32_t)lane * 16;
+    const uint32_t vlast = (HALF - 1) * 1024 + v16 + 16 <= (uint32_t)TBI ? (HALF - 1) * 1024 + v16 : 0u;
     const int64_t rows = MODE == MODE_SWIGLU ? p.ffn : p.N;
     const int64_t ntiles = (rows + TROWS - 1) / TROWS;
     const int64_t gw = (int64_t)blockIdx.x * WAVES + wave, nw = (int64_t)gridDim.x * WAVES;
@@ -1369,11 +1409,17 @@ __global__ __launch_bounds__(WAVES * WAVE) void gemv_q4_lds_kernel(GemvParams p,
         constexpr int64_t TB = (int64_t)TROWS * ROW_BYTES;
         if constexpr (MODE == MODE_SWIGLU) {
             const int64_t g0 = t * TB, u0 = (t * TROWS + p.ffn) * ROW_BYTES;
-            q4l_copy<HALF>(p.w, g0, g0 + TB < limit ? g0 + TB : limit, dst, lane);
-            q4l_copy<HALF>(p.w, u0, u0 + TB < limit ? u0 + TB : limit, dst + HALF * 1024, lane);
+            if (u0 + HALF * 1024 <= limit) {
+                q4l_copy_full<HALF>(p.w, g0, dst, v16, vlast);
+                q4l_copy_full<HALF>(p.w, u0, dst + HALF * 1024, v16, vlast);
+            } else {
+                q4l_copy<HALF>(p.w, g0, g0 + TB < limit ? g0 + TB : limit, dst, lane);
+                q4l_copy<HALF>(p.w, u0, u0 + TB < limit ? u0 + TB : limit, dst + HALF * 1024, lane);
+            }
         } else {
             const int64_t o0 = t * TB;
-            q4l_copy<PER>(p.w, o0, o0 + TB < limit ? o0 + TB : limit, dst, lane);
+            if (o0 + PER * 1024 <= limit) q4l_copy_full<PER>(p.w, o0, dst, v16, vlast);
+            else q4l_copy<PER>(p.w, o0, o0 + TB < limit ? o0 + TB : limit, dst, lane);
         }
     };
 

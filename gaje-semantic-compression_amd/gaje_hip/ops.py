@@ -26,11 +26,12 @@ class DeviceBuffer:
         b.write(a)
         return b
 
-    def write(self, a: np.ndarray) -> None:
+    def write(self, a: np.ndarray, offset: int = 0) -> None:
+        """Copy a host array into the buffer at byte `offset`."""
         a = np.ascontiguousarray(a)
-        if a.nbytes > self.nbytes:
-            raise ValueError("array larger than the device buffer")
-        check(lib().gaje_hip_memcpy_h2d(self.ptr, a.ctypes.data, a.nbytes))
+        if offset < 0 or offset + a.nbytes > self.nbytes:
+            raise ValueError("array beyond the device buffer")
+        check(lib().gaje_hip_memcpy_h2d(self.ptr + offset, a.ctypes.data, a.nbytes))
 
     def read(self, dtype, count: int | None = None) -> np.ndarray:
         dtype = np.dtype(dtype)

@@ -122,7 +122,7 @@ def test_model_modes_and_batch_on_subnormal_scales(hip, O, tmp_models):
     hip.synth.write_flat(raw, n_embd=128, n_head=4, n_head_kv=2, n_blocks=2, ffn=256, vocab_size=1000, eps=1e-6,
                          rope_base=1e4, arch_family=1, qkv_bias=1, tied_embeddings=0, seed=19)
     path = _scale_blocks_in_file(raw, str(tmp_models / "edge.flat"))
-    prompts = [[5, 17, 999, 0, 64, 3], [250, 7, 7, 1]]
+    prompts = [[5, 17, 999, 0, 64, 3], [250, 7, 7, 1, 998, 42]]  # equal lengths: the batch returns the last step's logits
     g = hip.load_genomic_auto(path)
     g.set_k_wta_ratio(0.0)
     refs = []
@@ -133,11 +133,8 @@ def test_model_modes_and_batch_on_subnormal_scales(hip, O, tmp_models):
             rl = r.forward_core(t, i == 0)
             assert same_bits(g.forward(t, i == 0), rl), f"decode token {i}"
         refs.append(rl)
-    L = max(len(p) for p in prompts)
-    ids = np.full((2, L), hip.BATCH_INACTIVE, np.uint32)
-    for s, p in enumerate(prompts):
-        ids[s, :len(p)] = p
-    b = hip.GenomicBatch(g, 2, L + 4)
+    ids = np.array(prompts, np.uint32)
+    b = hip.GenomicBatch(g, 2, ids.shape[1] + 4)
     logits = b.feed(ids, want_logits=True)
     for s in range(2):
         assert same_bits(logits[s], refs[s]), f"batched sequence {s}"

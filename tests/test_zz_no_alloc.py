@@ -56,6 +56,11 @@ def test_noalloc_empty_products_match():
     from gaje_hip._lib import check, lib
     if hip.ops.device_count() < 1:
         pytest.fail("no HIP device visible")
+    k = 512
+    W = hip.ops.q4_0_upload(hip.synth.q4_0_tensor(5, "noalloc.empty", 4, k), 4, k)
+    X = hip.ops.DeviceBuffer.from_array(np.zeros(16 * k, np.float32))
+    Y = hip.ops.DeviceBuffer(256)
+    ws = hip.ops.DeviceBuffer(256)
     for m, n in ((0, 256), (16, 0), (0, 0)):
-        check(lib().gaje_hip_q4_0_gemm_mfma_noalloc(None, None, None, 0, None, m, n, 512, None))
-        check(lib().gaje_hip_q4_0_gemm_mfma(None, None, None, 0, None, m, n, 512, None, 0, None))
+        check(lib().gaje_hip_q4_0_gemm_mfma_noalloc(W.ptr, X.ptr, None, 0, Y.ptr, m, n, k, None))
+        check(lib().gaje_hip_q4_0_gemm_mfma(W.ptr, X.ptr, None, 0, Y.ptr, m, n, k, ws.ptr, ws.nbytes, None))
