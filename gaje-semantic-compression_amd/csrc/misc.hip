@@ -59,45 +59,140 @@ __global__ void state_set_kernel(DevState *st, int32_t pos, uint32_t token, int3
 }
 
 // lateral_inhibition_kwta (src/compute/kernels/lut.rs:45-61): the k-th largest
-// value by a 4-pass radix select over orderable keys, then x < thr -> -1e9.
-__global__ __launch_bounds__(1024) void kwta_kernel(float *x, int64_t n, int64_t k, DevState *st) {
+// value by a 4-pass radix select over orderable keys (8 bits a pass, the top
+// byte first), then x < thr -> -1e9.  One workgroup of T threads.
+//  - Each wave counts into its own 256-bin LDS histogram (at most 8 copies:
+//    waves w and w + 8 share one), so waves barely contend; in the first pass (where the keys of similar values share a
+//    top byte) a wave first merges its lanes' equal bins with ballots and
+//    adds each bin's count once.
+//  - The bin holding the rank-th largest key comes from a parallel scan of
+//    the bins in descending order (256 threads, wave scans plus wave totals).
+//  - Rows of at most 4 values per thread keep their keys in registers;
+//    longer ones (the logits) are re-read per pass with 16-byte loads where
+//    aligned.
+//  - Each pass has its own histograms, zeroed once at the start.
+constexpr int KW_REG = 4;  // keys per thread held in registers
+
+// Counts key into the wave's histogram h when `in` (the key matches the
+// prefix selected so far); with ballot_merge every lane of the wave must call it.
+__device__ __forceinline__ void kw_count(uint32_t *h, uint32_t key, bool in, int shift, bool ballot_merge) {
+    const uint32_t bin = (key >> shift) & 255u;
+    if (!ballot_merge) {
+        if (in) atomicAdd(&h[bin], 1u);
+        return;
+    }
+    // merge equal bins of the wave: each round takes the first remaining
+    // lane's bin and counts every remaining lane that shares it
+    unsigned long long left = __ballot(in);
+    const int lane = threadIdx.x & 63;
+    while (left) {
+        const int lead = __ffsll((long long)left) - 1;
+        const uint32_t b = (uint32_t)__shfl((int)bin, lead, 64);
+        const unsigned long long same = __ballot(in && bin == b) & left;
+        if (lane == lead) atomicAdd(&h[b], (uint32_t)__popcll(same));
+        left &= ~same;
+    }
+}
+
+template <int T>
+__global__ __launch_bounds__(T) void kwta_kernel(float *x, int64_t n, int64_t k, DevState *st) {
+    constexpr int W = T / 64, HW = W < 8 ? W : 8;  // waves, histogram copies (waves w and w + 8 share one)
     if (st && st->halted) return;
     if (n <= k || k <= 0) return;
-    __shared__ uint32_t hist[256];
-    __shared__ uint32_t prefix, mask;
-    __shared__ int64_t rank;
-    const int tid = threadIdx.x;
-    if (tid == 0) {
-        prefix = 0;
-        mask = 0;
-        rank = k;
+    __shared__ uint32_t hist[4][HW][256];  // per pass and copy, zeroed once
+    __shared__ uint32_t wsum[4];
+    __shared__ uint32_t sel_prefix;
+    __shared__ int64_t sel_rank;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    {
+        uint32_t *hw = &hist[0][0][0];
+        for (int i = tid; i < 4 * HW * 256; i += T) hw[i] = 0u;
     }
+    const bool inreg = n <= (int64_t)T * KW_REG;
+    uint32_t rk[KW_REG];
+    if (inreg) {
+#pragma unroll
+        for (int j = 0; j < KW_REG; ++j) {
+            const int64_t i = tid + (int64_t)j * T;
+            rk[j] = i < n ? order_key(x[i]) : 0u;
+        }
+    }
+    __syncthreads();
+    const bool vec = ((uintptr_t)x & 15) == 0;
+    uint32_t prefix = 0, mask = 0;
+    int64_t rank = k;
     for (int pass = 0; pass < 4; ++pass) {
         const int shift = 24 - 8 * pass;
-        for (int i = tid; i < 256; i += blockDim.x) hist[i] = 0;
-        __syncthreads();
-        const uint32_t pf = prefix, mk = mask;
-        for (int64_t i = tid; i < n; i += blockDim.x) {
-            const uint32_t key = order_key(x[i]);
-            if ((key & mk) == pf) atomicAdd(&hist[(key >> shift) & 255u], 1u);
-        }
-        __syncthreads();
-        if (tid == 0) {
-            int64_t cum = 0;
-            int b = 255;
-            for (; b > 0; --b) {
-                if (cum + hist[b] >= rank) break;
-                cum += hist[b];
+        uint32_t *h = hist[pass][wave % HW];
+        const bool merge = false;
+        auto match = [&](uint32_t key) { return (key & mask) == prefix; };
+        if (inreg) {
+#pragma unroll
+            for (int j = 0; j < KW_REG; ++j) {
+                const bool ok = tid + (int64_t)j * T < n;
+                kw_count(h, rk[j], ok && match(rk[j]), shift, merge);
             }
-            rank -= cum;
-            prefix |= (uint32_t)b << shift;
-            mask |= 255u << shift;
+        } else if (vec) {
+            const int64_t n4 = n >> 2;
+            for (int64_t q = tid; q < ((n4 + T - 1) / T) * T; q += T) {
+                const bool ok = q < n4;
+                const float4 v = ok ? ((const float4 *)x)[q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                const uint32_t k0 = order_key(v.x), k1 = order_key(v.y), k2 = order_key(v.z), k3 = order_key(v.w);
+                kw_count(h, k0, ok && match(k0), shift, merge);
+                kw_count(h, k1, ok && match(k1), shift, merge);
+                kw_count(h, k2, ok && match(k2), shift, merge);
+                kw_count(h, k3, ok && match(k3), shift, merge);
+            }
+            for (int64_t i = 4 * n4 + tid; i < n; i += T) {
+                const uint32_t kk = order_key(x[i]);
+                kw_count(h, kk, match(kk), shift, false);
+            }
+        } else {
+            for (int64_t i = tid; i < ((n + T - 1) / T) * T; i += T) {
+                const bool ok = i < n;
+                const uint32_t kk = ok ? order_key(x[i]) : 0u;
+                kw_count(h, kk, ok && match(kk), shift, merge);
+            }
         }
         __syncthreads();
+        // bins in descending order: thread t < 256 holds bin 255 - t
+        uint32_t v = 0, incl = 0;
+        if (tid < 256) {
+#pragma unroll
+            for (int w = 0; w < HW; ++w) v += hist[pass][w][255 - tid];
+            incl = v;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const uint32_t u = (uint32_t)__shfl_up((int)incl, o, 64);
+                if (lane >= o) incl += u;
+            }
+            if (lane == 63) wsum[wave] = incl;
+        }
+        __syncthreads();
+        if (tid < 256) {
+            for (int w = 0; w < wave; ++w) incl += wsum[w];
+            const int64_t ex = (int64_t)incl - v;
+            if (ex < rank && (int64_t)incl >= rank) {
+                sel_prefix = prefix | ((uint32_t)(255 - tid) << shift);
+                sel_rank = rank - ex;
+            }
+        }
+        __syncthreads();
+        prefix = sel_prefix;
+        rank = sel_rank;
+        mask |= 255u << shift;
     }
     const float thr = order_key_inv(prefix);
-    for (int64_t i = tid; i < n; i += blockDim.x)
-        if (x[i] < thr) x[i] = -1e9f;
+    if (inreg) {
+#pragma unroll
+        for (int j = 0; j < KW_REG; ++j) {
+            const int64_t i = tid + (int64_t)j * T;
+            if (i < n && order_key_inv(rk[j]) < thr) x[i] = -1e9f;
+        }
+    } else {
+        for (int64_t i = tid; i < n; i += T)
+            if (x[i] < thr) x[i] = -1e9f;
+    }
 }
 
 // First maximum with a strict '>' (llm/forward.rs:262-271).
@@ -297,7 +392,7 @@ int launch_state_set(DevState *st, int32_t pos, uint32_t token, int32_t out_cap,
 int launch_kwta(float *x, int64_t n, int64_t k, DevState *st, hipStream_t s) {
     if (!x || n < 0) return set_error(GAJE_ERR_INVALID_ARG, "kwta: bad arguments");
     if (n <= k || k <= 0) return GAJE_OK;
-    hipLaunchKernelGGL(kwta_kernel, dim3(1), dim3(1024), 0, s, x, n, k, st);
+    hipLaunchKernelGGL(kwta_kernel<1024>, dim3(1), dim3(1024), 0, s, x, n, k, st);
     GAJE_HIP_CHECK(hipGetLastError());
     return GAJE_OK;
 }

@@ -236,6 +236,13 @@ def kwta(scores: DeviceBuffer, n: int, k: int, stream=None):
     check(lib().gaje_hip_kwta(scores.ptr, n, k, stream))
 
 
+def kwta_at(scores: DeviceBuffer, first: int, n: int, k: int, stream=None):
+    """kwta over the n floats that start at float `first` of the buffer."""
+    if first < 0 or (first + n) * 4 > scores.nbytes:
+        raise ValueError("kwta range beyond the buffer")
+    check(lib().gaje_hip_kwta(scores.ptr + 4 * first, n, k, stream))
+
+
 def argmax(x: DeviceBuffer, n: int, idx: DeviceBuffer, stream=None):
     check(lib().gaje_hip_argmax(x.ptr, n, idx.ptr, stream))
 

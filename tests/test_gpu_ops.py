@@ -216,8 +216,11 @@ def test_swiglu(hip, O):
     assert same_bits(got, ref)
 
 
-@pytest.mark.parametrize("n,ratio", [(151936, 0.5), (896, 0.5), (1000, 0.1), (64, 0.99)])
+@pytest.mark.parametrize("n,ratio", [(151936, 0.5), (896, 0.5), (1000, 0.1), (64, 0.99), (4096, 0.5), (4097, 0.3),
+                                     (151937, 0.5), (49152, 0.001), (1536, 0.999)])
 def test_kwta_exact(hip, O, n, ratio):
+    """Keys held in registers (n <= 4096) and streamed (longer rows, with and
+    without a 4-element tail); ties at many positions."""
     x = hip.synth.normal(61, f"k.{n}", n)
     x[::7] = x[3]  # ties at many positions
     k = max(int(np.float32(n) * np.float32(ratio)), 1)
@@ -226,6 +229,32 @@ def test_kwta_exact(hip, O, n, ratio):
     got = d.read(np.float32)
     ref = O.kwta(x, k)
     assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("case", ["logit_like", "signed_zeros", "all_equal", "k1", "unaligned"])
+def test_kwta_edge_cases(hip, O, case):
+    """Logits in a narrow range (most keys share their top byte: the ballot
+    merge), -0/+0 around the threshold, every value equal, k = 1, and a row
+    that does not start on a 16-byte boundary (the scalar path)."""
+    n = 151936
+    x = hip.synth.normal(62, f"ke.{case}", n, 0.0, 0.02)
+    k = n // 2
+    off = 0
+    if case == "signed_zeros":
+        x[::3] = 0.0
+        x[1::3] = -0.0
+    elif case == "all_equal":
+        x[:] = 0.125
+    elif case == "k1":
+        k = 1
+    elif case == "unaligned":
+        off = 1
+    buf = np.concatenate([np.zeros(off, np.float32), x])
+    d = _dev(hip, buf)
+    hip.ops.kwta_at(d, off, n, k) if off else hip.ops.kwta(d, n, k)
+    got = d.read(np.float32)[off:]
+    ref = O.kwta(x, k)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
 
 
 def test_argmax_first_max(hip, O):
