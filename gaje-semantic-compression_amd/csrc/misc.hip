@@ -62,9 +62,9 @@ __global__ void state_set_kernel(DevState *st, int32_t pos, uint32_t token, int3
 // value by a 4-pass radix select over orderable keys (8 bits a pass, the top
 // byte first), then x < thr -> -1e9.  One workgroup of T threads.
 //  - Each wave counts into its own 256-bin LDS histogram (at most 8 copies:
-//    waves w and w + 8 share one), so waves barely contend; in the first pass (where the keys of similar values share a
-//    top byte) a wave first merges its lanes' equal bins with ballots and
-//    adds each bin's count once.
+//    waves w and w + 8 share one), so waves barely contend.  (Merging a
+//    wave's equal bins with ballots before the atomics measured slower on
+//    the blocks' hidden states, whose keys spread over many top bytes.)
 //  - The bin holding the rank-th largest key comes from a parallel scan of
 //    the bins in descending order (256 threads, wave scans plus wave totals).
 //  - Rows of at most 4 values per thread keep their keys in registers;
@@ -74,24 +74,9 @@ __global__ void state_set_kernel(DevState *st, int32_t pos, uint32_t token, int3
 constexpr int KW_REG = 4;  // keys per thread held in registers
 
 // Counts key into the wave's histogram h when `in` (the key matches the
-// prefix selected so far); with ballot_merge every lane of the wave must call it.
-__device__ __forceinline__ void kw_count(uint32_t *h, uint32_t key, bool in, int shift, bool ballot_merge) {
-    const uint32_t bin = (key >> shift) & 255u;
-    if (!ballot_merge) {
-        if (in) atomicAdd(&h[bin], 1u);
-        return;
-    }
-    // merge equal bins of the wave: each round takes the first remaining
-    // lane's bin and counts every remaining lane that shares it
-    unsigned long long left = __ballot(in);
-    const int lane = threadIdx.x & 63;
-    while (left) {
-        const int lead = __ffsll((long long)left) - 1;
-        const uint32_t b = (uint32_t)__shfl((int)bin, lead, 64);
-        const unsigned long long same = __ballot(in && bin == b) & left;
-        if (lane == lead) atomicAdd(&h[b], (uint32_t)__popcll(same));
-        left &= ~same;
-    }
+// prefix selected so far).
+__device__ __forceinline__ void kw_count(uint32_t *h, uint32_t key, bool in, int shift) {
+    if (in) atomicAdd(&h[(key >> shift) & 255u], 1u);
 }
 
 template <int T>
@@ -124,13 +109,12 @@ __global__ __launch_bounds__(T) void kwta_kernel(float *x, int64_t n, int64_t k,
     for (int pass = 0; pass < 4; ++pass) {
         const int shift = 24 - 8 * pass;
         uint32_t *h = hist[pass][wave % HW];
-        const bool merge = false;
         auto match = [&](uint32_t key) { return (key & mask) == prefix; };
         if (inreg) {
 #pragma unroll
             for (int j = 0; j < KW_REG; ++j) {
                 const bool ok = tid + (int64_t)j * T < n;
-                kw_count(h, rk[j], ok && match(rk[j]), shift, merge);
+                kw_count(h, rk[j], ok && match(rk[j]), shift);
             }
         } else if (vec) {
             const int64_t n4 = n >> 2;
@@ -138,20 +122,20 @@ __global__ __launch_bounds__(T) void kwta_kernel(float *x, int64_t n, int64_t k,
                 const bool ok = q < n4;
                 const float4 v = ok ? ((const float4 *)x)[q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                 const uint32_t k0 = order_key(v.x), k1 = order_key(v.y), k2 = order_key(v.z), k3 = order_key(v.w);
-                kw_count(h, k0, ok && match(k0), shift, merge);
-                kw_count(h, k1, ok && match(k1), shift, merge);
-                kw_count(h, k2, ok && match(k2), shift, merge);
-                kw_count(h, k3, ok && match(k3), shift, merge);
+                kw_count(h, k0, ok && match(k0), shift);
+                kw_count(h, k1, ok && match(k1), shift);
+                kw_count(h, k2, ok && match(k2), shift);
+                kw_count(h, k3, ok && match(k3), shift);
             }
             for (int64_t i = 4 * n4 + tid; i < n; i += T) {
                 const uint32_t kk = order_key(x[i]);
-                kw_count(h, kk, match(kk), shift, false);
+                kw_count(h, kk, match(kk), shift);
             }
         } else {
             for (int64_t i = tid; i < ((n + T - 1) / T) * T; i += T) {
                 const bool ok = i < n;
                 const uint32_t kk = ok ? order_key(x[i]) : 0u;
-                kw_count(h, kk, ok && match(kk), shift, merge);
+                kw_count(h, kk, ok && match(kk), shift);
             }
         }
         __syncthreads();
