@@ -1527,6 +1527,105 @@ __global__ __launch_bounds__(WAVES * WAVE) void gemv_q4_lds_kernel(GemvParams p,
     wait_vmcnt<0>();
 }
 
+// LUT-4bit rows stored whole (MODE_STORE, optional bias, no anchors or
+// prologue), LDS-staged: one wave per workgroup takes 16 rows (lane 4 r + c:
+// row r, chain c) and copies, all at once with LDS-direct loads, x, the 16
+// rows' codes (16 B per block, contiguous) and their 16-entry tables (one per
+// row and block, or the one shared table); then each lane walks its chain
+// (elements e of a block with e % 4 == c, blocks in order: genomic.rs:148-204)
+// with its table lookups and x reads from LDS.  Against row_lut4, which waits
+// for each block's table before its lookups, every byte of the tile is in
+// flight from the start.
+constexpr int LUTL_ROWS = 16;
+// Tables in LDS: row q's nb tables at q nb 64 bytes, as the tile lies in
+// memory (one copy per KiB).  For even nb every row's tables then begin on the
+// same LDS bank, so a block's lookups from the 16 rows conflict; padding the
+// rows apart (one copy per row and KiB) measured slower (9.2 against 7.3 us
+// per C0-LUT launch).
+__host__ __device__ constexpr int64_t lut4_trow_bytes(int64_t nb) { return nb * 64; }
+size_t lut4_lds_bytes(int64_t K, int64_t nb, bool shared_table) {
+    const size_t xb = (size_t)K * 4, cb = (size_t)LUTL_ROWS * nb * 16;
+    const size_t tb = shared_table ? 64 : (size_t)LUTL_ROWS * lut4_trow_bytes(nb);
+    return (xb + 1023) / 1024 * 1024 + (cb + 1023) / 1024 * 1024 + (tb + 1023) / 1024 * 1024;
+}
+
+template <bool SHARED>
+__global__ __launch_bounds__(WAVE) void gemv_lut4_lds_kernel(GemvParams p) {
+    extern __shared__ __align__(16) float smem[];
+    const int lane = threadIdx.x, r = lane >> 2, c = lane & 3, base = lane & ~3;
+    const int nb = p.nb;
+    const int64_t K = p.K;
+    const int64_t r0 = (int64_t)blockIdx.x * LUTL_ROWS;
+    float *xs = smem;
+    const int64_t xb = K * 4, cb = (int64_t)LUTL_ROWS * nb * 16;
+    const int64_t trs = lut4_trow_bytes(nb);
+    uint8_t *codes = (uint8_t *)smem + (xb + 1023) / 1024 * 1024;
+    float *tabs = (float *)(codes + (cb + 1023) / 1024 * 1024);
+    // ---- every copy at once: x, the codes, the tables ----
+    lds_copy_bytes(p.x, xb, lds_addr(xs), lane);
+    {
+        // codes of rows r0 .. r0 + 15 (contiguous); lanes past the tensor re-read its start
+        const uint8_t *cw = p.w + r0 * nb * 16;
+        const int64_t cend = (p.N - r0) * nb * 16;
+        for (int64_t o = 0; o < cb; o += 1024) {
+            const int64_t a = o + lane * 16;
+            lds_dma16(cw + (a + 16 <= cend ? a : 0), lds_addr(codes) + (uint32_t)o);
+        }
+    }
+    if constexpr (SHARED) {
+        if (lane < 4) lds_dma16<true>(p.lut + 4 * lane, lds_addr(tabs));
+    } else {
+        // row q's table set (nb 64 bytes) starts at q nb 64 bytes if q < lut_rows_own,
+        // else at 0; rows past the tensor copy row r0's
+        const uint32_t rs = (uint32_t)nb * 64;
+        const uint8_t *lb = (const uint8_t *)p.lut;
+        const int64_t tb = (int64_t)LUTL_ROWS * rs;
+        if (r0 + LUTL_ROWS <= p.lut_rows_own && r0 + LUTL_ROWS <= p.N) {
+            for (int64_t o = 0; o < tb; o += 1024) lds_dma16(lb + r0 * rs + o + lane * 16, lds_addr(tabs) + (uint32_t)o);
+        } else {
+            for (int64_t o = 0; o < tb; o += 1024) {
+                const uint32_t a = (uint32_t)o + lane * 16;
+                int64_t q = r0 + a / rs;
+                q = q < p.N ? q : r0;
+                const int64_t src = (q < p.lut_rows_own ? q * rs : 0) + a % rs;
+                lds_dma16(lb + src, lds_addr(tabs) + (uint32_t)o);
+            }
+        }
+    }
+    if (p.st && s_load_i32(&p.st->halted)) {
+        wait_vmcnt<0>();
+        return;
+    }
+    wait_vmcnt<0>();
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_wave_barrier();
+    // ---- the chain: acc = acc + tbl[code] * x[e], mul then add, blocks in order ----
+    float acc = 0.0f;
+    const uint8_t *crow = codes + (size_t)r * nb * 16;
+    const float *trow = SHARED ? tabs : (const float *)((const uint8_t *)tabs + r * trs);
+    for (int j = 0; j < nb; ++j) {
+        const vu4 cw = *(const vu4 *)(crow + (size_t)j * 16);
+        const float *t = SHARED ? trow : trow + (size_t)j * 16;
+        const float *xj = xs + (size_t)j * 32 + c;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            // element e = 4 u + c; even e is the high nibble of byte e / 2
+            const uint32_t word = (u >> 1) == 0 ? cw.x : (u >> 1) == 1 ? cw.y : (u >> 1) == 2 ? cw.z : cw.w;
+            // byte e / 2 = 2 u + c / 2 of the block: bits 8 ((2u + c/2) & 3) of word u / 2
+            const uint32_t idx = __builtin_amdgcn_ubfe(word, 8 * ((2 * u + (c >> 1)) & 3) + ((c & 1) ? 0 : 4), 4);
+            const float prod = t[idx] * xj[4 * u];
+            acc = acc + prod;
+        }
+    }
+    const float s1 = shfl(acc, base + 1), s2 = shfl(acc, base + 2), s3 = shfl(acc, base + 3);
+    float total = flush_small(((acc + s1) + s2) + s3);  // s0 + s1 + s2 + s3, left to right
+    const int64_t row = r0 + r;
+    if (c == 0 && row < p.N) {
+        if (row < p.bias_len) total = total + p.bias[row];
+        p.y[row] = total;
+    }
+}
+
 template <int MODE, int WAVES, int STAGES, int ROWS>
 void *q4l_kernel(int G) {
     switch (G) {
@@ -2405,6 +2504,21 @@ int launch_gemv(const GemvParams &p, hipStream_t s) {
         hipLaunchKernelGGL(sf, dim3((unsigned)grid), dim3(THREADS), lds, s, p, q4_xstride(p.K));
         GAJE_HIP_CHECK(hipGetLastError());
         return GAJE_OK;
+    }
+    // LUT rows stored whole: the LDS-staged kernel (tables per row and block,
+    // or the one shared table)
+    if (p.fmt == FMT_LUT4 && p.mode == MODE_STORE && !p.gnorm && !p.a_ptr && !p.x_out && !p.norm_w && p.nb > 0 &&
+        p.rows_valid == p.N && p.st_in < 0 && (p.lut_block_stride == 0 || p.lut_block_stride == 16) &&
+        ((uintptr_t)p.x & 15) == 0 && ((uintptr_t)p.lut & 15) == 0 && ((uintptr_t)p.w & 15) == 0) {
+        const bool shared = p.lut_block_stride == 0;
+        const size_t llds = lut4_lds_bytes(p.K, p.nb, shared);
+        if (llds + 1024 <= max_lds_per_block()) {
+            const int64_t grid = (p.N + LUTL_ROWS - 1) / LUTL_ROWS;
+            hipLaunchKernelGGL(shared ? gemv_lut4_lds_kernel<true> : gemv_lut4_lds_kernel<false>, dim3((unsigned)grid),
+                               dim3(WAVE), llds, s, p);
+            GAJE_HIP_CHECK(hipGetLastError());
+            return GAJE_OK;
+        }
     }
     KernelFn fn;
     int lpr;

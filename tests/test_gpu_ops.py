@@ -180,6 +180,24 @@ def test_lut4_gemv(hip, O, n, k, table):
     assert same_bits(got, ref)
 
 
+@pytest.mark.parametrize("n,k,own,bias", [(300, 896, 37, True), (4867, 576, 4867, True), (16, 32, 16, False),
+                                          (33, 1024, 0, True)])
+def test_lut4_gemv_partial_tables_and_bias(hip, O, n, k, own, bias):
+    """Tables for only the first `own` rows (later rows read the first row's
+    set, init.rs:109-124), a bias, partial last tiles, one-block rows."""
+    codes, lut = hip.synth.lut4_tensor(23, f"lutp.{n}.{k}", n, k)
+    nb = k // 32
+    lut = lut[: max(own, 1) * nb * 16].copy()
+    x = hip.synth.normal(24, f"xlp.{k}", k)
+    b = hip.synth.normal(25, f"blp.{n}", n, 0.0, 0.02)
+    y = _out(hip, n * 4)
+    hip.ops.lut4_gemv(_dev(hip, codes), _dev(hip, lut), lut.size, _dev(hip, x), y, n, k,
+                      bias=_dev(hip, b) if bias else None, bias_len=n if bias else 0)
+    got = y.read(np.float32)
+    ref = O.GenomicLinear(codes, b"", lut, n, k, b if bias else None, 4).forward_core(x)
+    assert same_bits(got, ref)
+
+
 @pytest.mark.parametrize("n,k", [(151936, 896), (49152, 576), (1001, 1536), (3, 64), (5, 12), (7, 100)])
 def test_f32_gemv(hip, O, n, k):
     w = hip.synth.normal(31, f"w.{n}.{k}", n * k, 0.0, 0.02)
