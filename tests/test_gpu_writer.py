@@ -33,3 +33,30 @@ def test_exported_model_stream(tmp_models, body, quant_embed, anchors):
     for i, t in enumerate(toks):
         assert same_bits(g.forward(t, i == 0), r.forward_core(t, i == 0)), f"token {i}"
     g.close()
+
+
+@pytest.mark.parametrize("arch", ["llama", "qwen2"])
+def test_imported_gguf_stream(tmp_models, arch):
+    """A GGUF checkpoint (Llama-family Q/K rows interleaved as converters store
+    them) imported to .gaje.flat runs on the device bit for bit like the oracle."""
+    import gaje_hip
+    from gaje_hip import gguf as G
+    from oracle import oracle as O
+    from test_gguf import _md, _tiny_tensors
+    if gaje_hip.ops.device_count() < 1:
+        pytest.fail("no HIP device visible")
+    T = _tiny_tensors(np.random.default_rng(19), E=128, H=4, KV=2, L=2, F=256, V=500, bias=arch == "qwen2")
+    if arch == "llama":
+        for i in range(2):
+            T[f"blk.{i}.attn_q.weight"] = G.permute_qk(T[f"blk.{i}.attn_q.weight"], 4, 32)
+            T[f"blk.{i}.attn_k.weight"] = G.permute_qk(T[f"blk.{i}.attn_k.weight"], 2, 32)
+    src = G.write_gguf(str(tmp_models / f"imp_{arch}.gguf"), _md(arch, E=128), T,
+                       types={k: G.GGML_F16 for k in T if k.startswith("blk.") and T[k].ndim == 2})
+    p = G.import_gguf(src, str(tmp_models / f"imp_{arch}.flat"))
+    g = gaje_hip.load_genomic_auto(p)
+    r = O.load_genomic(p)
+    g.set_k_wta_ratio(0.0)
+    r.set_k_wta_ratio(0.0)
+    for i, t in enumerate([int(v) for v in np.random.default_rng(20).integers(0, 500, 6)]):
+        assert same_bits(g.forward(t, i == 0), r.forward_core(t, i == 0)), f"token {i}"
+    g.close()
