@@ -53,6 +53,11 @@ import numpy as np  # noqa: E402
 HBM_PEAK_GBPS = 8000.0   # MI355X HBM3E, published
 MFMA_F16_TFLOPS = 2500.0  # MI355X dense f16 MFMA, published
 METRIC = "Q4_0 GEMV HBM GB/s (% of peak); decode tok/s, Qwen2-0.5B shape, batch 1"
+# workload legs, in the order they run: the headline decode, the Q4_0 matvecs,
+# the C0-LUT matvec, the decode with K-WTA 0.5, the SmolLM2-135M decode, the
+# Q8_0 embed/lm_head and 2-bit body decodes, Qwen2.5-1.5B prefill + batch-16,
+# the MoE layer, the CPU baseline
+LEGS = ("decode", "gemv", "lut", "kwta", "c1", "q8", "2bit", "c3", "moe", "cpu")
 
 
 def log(*a):
@@ -71,7 +76,7 @@ def model_path(preset: str, seed: int, d: str, quant_embed: int = 0, body_format
     return path
 
 
-def q4_gemv_c0(iters: int = 1024, hot: bool = True, stream: bool = True):
+def q4_gemv_c0(iters: int = 1024, hot: bool = True, stream: bool = True, stream_iters: int = 1024):
     """The C0 matvec: Q4_0 K=896 N=4864, cold (128 copies) and hot (1 copy); the
     launch floors of its grid; and one launch over all 128 copies as a single
     622,592-row matrix (351 MB), the kernel's streaming rate."""
@@ -96,6 +101,22 @@ def q4_gemv_c0(iters: int = 1024, hot: bool = True, stream: bool = True):
     x = ops.DeviceBuffer.from_array(synth.normal(0, "c0.x", k))
     y = ops.DeviceBuffer(n * copies * 4)
     algo = blocks.nbytes + k * 4 + n * 4  # weights + x + y
+    ns = n * copies  # the copies are contiguous: one matrix of 622,592 rows
+    streamable = stream and stride == wbytes
+    stream_out = {}
+    if streamable:
+        # warm-up: the core clock climbs from ~2.1 to ~2.4 GHz over the first
+        # ~20 ms of sustained load, and this matvec's issue rate follows it;
+        # 640 launches (~40 ms) of the stream matvec bring it to steady state,
+        # and the timed launches follow at once
+        ops.bench_gemv(1, w, span, 2, x, y, ns, k, 512)
+        s_ms = ops.bench_gemv(1, w, span, 2, x, y, ns, k, stream_iters)
+        s_algo = ns * (k // 32) * 20 + k * 4 + ns * 4
+        sr_ms = ops.bench_floor(w, ns * (k // 32) * 20, 4096, 256, 64)
+        stream_out = dict(stream_rows=ns, stream_bytes=s_algo, stream_us=s_ms * 1e3,
+                          stream_GBps=s_algo / (s_ms * 1e-3) / 1e9,
+                          stream_frac=s_algo / (s_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
+                          stream_plain_read_GBps=ns * (k // 32) * 20 / (sr_ms * 1e-3) / 1e9)
     cold_ms = ops.bench_gemv(1, w, stride, copies, x, y, n, k, iters)
     hot_ms = ops.bench_gemv(1, w, stride, 1, x, y, n, k, iters) if hot else None
     # floors of a launch: an empty kernel of the C0 matvec's grid (one 64-thread
@@ -113,15 +134,7 @@ def q4_gemv_c0(iters: int = 1024, hot: bool = True, stream: bool = True):
                     "read-only kernel over the same 2,723,840 weight bytes (256 x 256 threads)")
     if hot_ms is not None:
         out.update(hot_us=hot_ms * 1e3, hot_GBps=algo / (hot_ms * 1e-3) / 1e9)
-    if stream and stride == wbytes:
-        ns = n * copies  # the copies are contiguous: one matrix of 622,592 rows
-        s_ms = ops.bench_gemv(1, w, span, 2, x, y, ns, k, 64)
-        s_algo = ns * (k // 32) * 20 + k * 4 + ns * 4
-        sr_ms = ops.bench_floor(w, ns * (k // 32) * 20, 4096, 256, 64)
-        out.update(stream_rows=ns, stream_bytes=s_algo, stream_us=s_ms * 1e3,
-                   stream_GBps=s_algo / (s_ms * 1e-3) / 1e9,
-                   stream_frac=s_algo / (s_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
-                   stream_plain_read_GBps=ns * (k // 32) * 20 / (sr_ms * 1e-3) / 1e9)
+    out.update(stream_out)
     w.close()
     return out
 
@@ -399,6 +412,8 @@ def main():
     ap.add_argument("--no-2bit", action="store_true", help="skip the 2-bit body decode")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the K-WTA-on decode, the SmolLM2-135M decode and the C0-LUT matvec")
+    ap.add_argument("--only", default="",
+                    help="comma-separated legs to run (default: all): " + ", ".join(LEGS))
     ap.add_argument("--gemv-only", action="store_true",
                     help="only the Q4_0 matvecs (C0 cold, the 351 MB stream) and a 256 MiB device copy, for counter runs")
     args = ap.parse_args()
@@ -426,10 +441,22 @@ def main():
         print(json.dumps({"q4_0_gemv": gemv, "copy_bytes": nbytes}), flush=True)
         return
 
+    legs = set(LEGS) if not args.only else {l.strip() for l in args.only.split(",") if l.strip()}
+    unknown = legs - set(LEGS)
+    if unknown:
+        print(f"bench.py: unknown legs {sorted(unknown)} (known: {', '.join(LEGS)})", file=sys.stderr)
+        sys.exit(2)
+    for flag, names in (("no_decode", ("decode", "gemv", "lut", "kwta", "c1", "q8", "2bit")), ("no_extra", ("lut", "kwta", "c1")),
+                        ("no_q8", ("q8",)), ("no_2bit", ("2bit",)), ("no_c3", ("c3",)), ("no_moe", ("moe",)),
+                        ("no_cpu", ("cpu",))):
+        if getattr(args, flag):
+            legs -= set(names)
     d = args.model_dir or tempfile.gettempdir()
-    dec, stages, gemv, lut, roofline, path, prompt = None, {}, None, None, None, None, None
+    dec, stages, gemv, lut, roofline = None, {}, None, None, None
     workloads = {}
-    if not args.no_decode:
+    path = model_path(args.preset, args.seed, d) if ({"decode", "cpu"} & legs) else None
+    prompt = None
+    if "decode" in legs:
         stage_list = None if args.no_stages else ("qkv", "attention", "o", "gate_up", "down", "lm_head", "token")
         dec, path, prompt = decode_workload(d, args.seed, args.preset, args.prompt, args.gen, args.steps,
                                             args.warmup, stages=stage_list)
@@ -438,7 +465,7 @@ def main():
             f"{args.gen}-token step)")
         for s, v in stages.items():
             log(f"[bench] stage {s:9s}: {v['us']:8.2f} us  {v['GBps']:8.1f} GB/s")
-
+    if "gemv" in legs:
         gemv = q4_gemv_c0()
         log(f"[bench] Q4_0 GEMV C0: cold {gemv['cold_us']:.2f} us = {gemv['cold_GBps']:.0f} GB/s "
             f"({100 * gemv['cold_frac']:.1f}% of HBM peak); hot {gemv['hot_us']:.2f} us; launch floors: empty "
@@ -452,46 +479,54 @@ def main():
                         achieved=round(gemv["stream_GBps"], 1), peak=HBM_PEAK_GBPS, unit="GB/s",
                         frac=round(gemv["stream_frac"], 4), traffic=read_traffic(),
                         bytes_per_launch=gemv["stream_bytes"], us_per_launch=round(gemv["stream_us"], 3),
+                        timing="1024 launches alternating two distinct 349 MB matrices, after 128 untimed launches "
+                               "and a 640-launch warm-up; HIP events around a replayed graph",
                         c0_launch=dict(bytes=gemv["algorithmic_bytes"], us=round(gemv["cold_us"], 3),
                                        GBps=round(gemv["cold_GBps"], 1), frac=round(gemv["cold_frac"], 4),
                                        floor_empty_kernel_us=round(gemv["empty_kernel_us"], 3)))
-        if not args.no_extra:
-            lut = lut_gemv_c0()
-            log(f"[bench] C0-LUT GEMV: cold {lut['cold_us']:.2f} us = {lut['cold_GBps']:.0f} GB/s "
-                f"({100 * lut['cold_frac']:.1f}% of HBM peak)")
-            kw, _, _ = decode_workload(d, args.seed, args.preset, args.prompt, args.gen, args.steps, args.warmup,
-                                       kwta=0.5)
-            kw.pop("el")
-            kw["kwta"] = 0.5
-            workloads[f"{args.preset}_decode_kwta_0.5"] = kw
-            log(f"[bench] decode with K-WTA 0.5: {kw['tok_s']:.1f} tok/s")
-            c1, _, _ = decode_workload(d, args.seed, "smollm2-135m", 128, 256, args.steps, args.warmup,
-                                       stages=None if args.no_stages else ("qkv", "attention", "o", "gate_up",
-                                                                           "down", "lm_head"))
-            c1.pop("el")
-            workloads["smollm2-135m_decode_128+256"] = c1
-            log(f"[bench] SmolLM2-135M decode (128 + 256): {c1['tok_s']:.1f} tok/s")
-    if not args.no_q8 and not args.no_decode:
+    if "lut" in legs:
+        lut = lut_gemv_c0()
+        log(f"[bench] C0-LUT GEMV: cold {lut['cold_us']:.2f} us = {lut['cold_GBps']:.0f} GB/s "
+            f"({100 * lut['cold_frac']:.1f}% of HBM peak)")
+    if "kwta" in legs:
+        kw, _, _ = decode_workload(d, args.seed, args.preset, args.prompt, args.gen, args.steps, args.warmup,
+                                   kwta=0.5)
+        kw.pop("el")
+        kw["kwta"] = 0.5
+        workloads[f"{args.preset}_decode_kwta_0.5"] = kw
+        log(f"[bench] decode with K-WTA 0.5: {kw['tok_s']:.1f} tok/s")
+    if "c1" in legs:
+        c1, _, _ = decode_workload(d, args.seed, "smollm2-135m", 128, 256, args.steps, args.warmup,
+                                   stages=None if args.no_stages else ("qkv", "attention", "o", "gate_up",
+                                                                       "down", "lm_head"))
+        c1.pop("el")
+        workloads["smollm2-135m_decode_128+256"] = c1
+        log(f"[bench] SmolLM2-135M decode (128 + 256): {c1['tok_s']:.1f} tok/s")
+    if "q8" in legs:
         q8, _, _ = decode_workload(d, args.seed, args.preset, args.prompt, args.gen, args.steps, args.warmup,
                                    quant_embed=1, stages=None if args.no_stages else ("lm_head",))
         q8.pop("el")
         workloads[f"{args.preset}_q8_0_embed_decode"] = q8
         log(f"[bench] Q8_0 embed/lm_head decode: {q8['tok_s']:.1f} tok/s")
-    if not args.no_2bit and not args.no_decode:
+    if "2bit" in legs:
         b2, _, _ = decode_workload(d, args.seed, args.preset, args.prompt, args.gen, args.steps, args.warmup,
                                    body_format=4, stages=None if args.no_stages else ("qkv", "o", "gate_up", "down"))
         b2.pop("el")
         workloads[f"{args.preset}_2bit_body_decode"] = b2
         log(f"[bench] 2-bit body decode: {b2['tok_s']:.1f} tok/s")
-    if not args.no_c3:
+    if "c3" in legs:
         prefill, decode, _ = c3_workloads(d, args.seed, ctx=args.c3_ctx, gen=args.c3_gen)
         workloads["qwen2.5-1.5b_prefill_512"] = prefill
         workloads["qwen2.5-1.5b_batch16_decode"] = decode
-    if not args.no_moe:
+    if "moe" in legs:
         workloads["moe_ffn_256x1536_8x4096_top2"] = moe_workload(args.seed)
 
     cpu = None
-    if not args.no_cpu and path is not None:
+    if "cpu" in legs:
+        if prompt is None:
+            import gaje_hip as _g
+            vocab = _g.synth.PRESETS[args.preset]["vocab_size"]
+            prompt = np.random.default_rng(args.seed).integers(0, vocab, args.prompt).astype(np.uint32)
         threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
         cpu = cpu_baseline(path, prompt, args.cpu_seconds, threads)
         log(f"[bench] cpu oracle ({cpu['cpu_model']}): {cpu['value']:.2f} tok/s on {cpu['cores']} threads, "
