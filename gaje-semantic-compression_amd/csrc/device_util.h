@@ -538,4 +538,164 @@ __device__ inline void rmsnorm_inplace(float *xs, int64_t n, const float *w, flo
     }
 }
 
+// lateral_inhibition_kwta (compute/kernels/lut.rs:45-61) over the n floats at
+// xs (LDS, 16-byte aligned, n % 4 == 0) by one wave: thr = the k-th largest
+// value, found as kwta_kernel finds it (order_key, 8-bit passes from the top
+// byte, each pass's 256-bin histogram of the keys that match the prefix chosen
+// so far, the bin that holds the rank-th largest key taken from a scan in
+// descending bin order), then x < thr -> -1e9 in place.  Rows of up to
+// 64 * 4 * KW_WQ values keep their keys in registers (read once, with 16-byte
+// reads) and count them without branches; once the chosen bin holds a single
+// key, that key is the threshold and the remaining passes are skipped.
+// Longer rows re-read the keys from LDS each pass.  hist: 4 x 320 words (a
+// histogram per pass, and dummy words).  Returns thr (-inf, masking nothing,
+// when n <= k or k <= 0).  LDS operations of one wave complete in issue order;
+// the explicit waits only keep the compiler from moving them across phases.
+constexpr int KW_WQ = 6;  // quads of keys per lane held in registers (n <= 1536)
+
+// Inclusive prefix sum over the 64 lanes of a wave with DPP: row_shr 1, 2, 4, 8
+// within each row of 16 lanes (lanes with no source add 0), then row_bcast:15
+// (lane 15 of a row into the next row) and row_bcast:31 (lane 31 into rows 2
+// and 3).
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xF, 0xF, true);  // row_shr:1
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xF, 0xF, true);  // row_shr:2
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xF, 0xF, true);  // row_shr:4
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xF, 0xF, true);  // row_shr:8
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x142, 0xA, 0xF, false); // row_bcast:15
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xC, 0xF, false); // row_bcast:31
+    return x;
+}
+
+// wave_kwta for rows past the register budget: the keys re-read from LDS each
+// pass.
+__device__ __forceinline__ float wave_kwta_long(float *xs, int n, int64_t k, uint32_t *hist, int lane) {
+    constexpr int HS = 256 + WAVE;
+    uint32_t prefix = 0u, mask = 0u, rank = (uint32_t)k;
+#pragma unroll
+    for (int z = 0; z < 4; ++z) *(uint4 *)(hist + HS * z + 4 * lane) = make_uint4(0u, 0u, 0u, 0u);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    for (int pass = 0; pass < 4; ++pass) {
+        const int shift = 24 - 8 * pass;
+        uint32_t *h = hist + HS * pass;
+        for (int i = lane; i < n; i += WAVE) {
+            const uint32_t kk = order_key(xs[i]);
+            if ((kk & mask) == prefix) atomicAdd(&h[(kk >> shift) & 255u], 1u);
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        const uint4 hv = *(const uint4 *)(h + 252 - 4 * lane);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        const uint32_t v0 = hv.w, v1 = hv.z, v2 = hv.y, v3 = hv.x;
+        const uint32_t t = v0 + v1 + v2 + v3;
+        const uint32_t incl = wave_incl_scan(t);
+        const uint32_t e0 = incl - t, c0 = e0 + v0, c1 = c0 + v1, c2 = c1 + v2;
+        const int src = __ffsll((long long)__ballot(e0 < rank && incl >= rank)) - 1;
+        const int jl = c0 >= rank ? 0 : c1 >= rank ? 1 : c2 >= rank ? 2 : 3;
+        const uint32_t bl = c0 >= rank ? e0 : c1 >= rank ? c0 : c2 >= rank ? c1 : c2;
+        prefix |= (uint32_t)(255 - (4 * src + __builtin_amdgcn_readlane(jl, src))) << shift;
+        mask |= 255u << shift;
+        rank -= (uint32_t)__builtin_amdgcn_readlane((int)bl, src);
+    }
+    const float thr = order_key_inv(prefix);
+    for (int i = lane; i < n; i += WAVE)
+        if (xs[i] < thr) xs[i] = -1e9f;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    return thr;
+}
+
+__device__ __forceinline__ float wave_kwta(float *xs, int n, int64_t k, uint32_t *hist, int lane) {
+    if ((int64_t)n <= k || k <= 0) return -INFINITY;
+    constexpr int HS = 256 + WAVE;  // a pass's bins, then one dummy word per lane
+    const int n4 = n >> 2;
+    if (n4 > WAVE * KW_WQ) return wave_kwta_long(xs, n, k, hist, lane);
+    const int jn = (n4 + WAVE - 1) / WAVE;  // quads per lane (uniform)
+    uint32_t key[KW_WQ][4];
+    bool ok[KW_WQ];
+#pragma unroll
+    for (int j = 0; j < KW_WQ; ++j) {
+        const int q = lane + WAVE * j;
+        ok[j] = q < n4;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (j < jn) v = *(const float4 *)(xs + 4 * (ok[j] ? q : 0));
+        key[j][0] = order_key(v.x);
+        key[j][1] = order_key(v.y);
+        key[j][2] = order_key(v.z);
+        key[j][3] = order_key(v.w);
+    }
+#pragma unroll
+    for (int z = 0; z < 4; ++z) *(uint4 *)(hist + HS * z + 4 * lane) = make_uint4(0u, 0u, 0u, 0u);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    uint32_t prefix = 0u, mask = 0u, rank = (uint32_t)k;
+    for (int pass = 0; pass < 4; ++pass) {
+        const int shift = 24 - 8 * pass;
+        uint32_t *h = hist + HS * pass;
+        // every key adds once, without branches: a key outside the prefix (or
+        // past n) into its lane's dummy word
+#pragma unroll
+        for (int j = 0; j < KW_WQ; ++j) {
+            if (j < jn) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const bool m = ok[j] && (key[j][c] & mask) == prefix;
+                    atomicAdd(&h[m ? ((key[j][c] >> shift) & 255u) : 256u + lane], 1u);
+                }
+            }
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        // lane L holds bins 255 - 4L .. 252 - 4L, in that (descending) order
+        const uint4 hv = *(const uint4 *)(h + 252 - 4 * lane);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        const uint32_t v0 = hv.w, v1 = hv.z, v2 = hv.y, v3 = hv.x;
+        const uint32_t t = v0 + v1 + v2 + v3;
+        const uint32_t incl = wave_incl_scan(t);
+        const uint32_t e0 = incl - t, c0 = e0 + v0, c1 = c0 + v1, c2 = c1 + v2;
+        // the lane whose bins' range of ranks (e0, incl] holds rank (exactly
+        // one: the counts sum to at least rank), and in it the bin
+        const int src = __ffsll((long long)__ballot(e0 < rank && incl >= rank)) - 1;
+        const int jl = c0 >= rank ? 0 : c1 >= rank ? 1 : c2 >= rank ? 2 : 3;
+        const uint32_t bl = c0 >= rank ? e0 : c1 >= rank ? c0 : c2 >= rank ? c1 : c2;
+        const uint32_t vl = c0 >= rank ? v0 : c1 >= rank ? v1 : c2 >= rank ? v2 : v3;
+        const int jj = __builtin_amdgcn_readlane(jl, src);
+        const uint32_t bb = (uint32_t)__builtin_amdgcn_readlane((int)bl, src);
+        const uint32_t cnt = (uint32_t)__builtin_amdgcn_readlane((int)vl, src);
+        prefix |= (uint32_t)(255 - (4 * src + jj)) << shift;
+        mask |= 255u << shift;
+        rank -= bb;
+        if (cnt == 1u && pass < 3) {
+            // one key has this prefix: it is the k-th largest
+            uint32_t lo = 0u;
+            bool any = false;
+#pragma unroll
+            for (int j = 0; j < KW_WQ; ++j) {
+                if (j < jn) {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        const bool m = ok[j] && (key[j][c] & mask) == prefix;
+                        lo |= m ? key[j][c] : 0u;
+                        any |= m;
+                    }
+                }
+            }
+            prefix = (uint32_t)__builtin_amdgcn_readlane((int)lo, __ffsll((long long)__ballot(any)) - 1);
+            break;
+        }
+    }
+    const float thr = order_key_inv(prefix);
+    // order_key is a bijection on the bit patterns: its inverse gives x back
+#pragma unroll
+    for (int j = 0; j < KW_WQ; ++j) {
+        if (j < jn && ok[j]) {
+            float m4[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const float x = order_key_inv(key[j][c]);
+                m4[c] = x < thr ? -1e9f : x;
+            }
+            *(float4 *)(xs + 4 * (lane + WAVE * j)) = make_float4(m4[0], m4[1], m4[2], m4[3]);
+        }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    return thr;
+}
+
 }  // namespace gaje

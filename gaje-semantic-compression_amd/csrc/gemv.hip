@@ -1954,7 +1954,7 @@ __host__ __device__ constexpr int chain_xstride(int64_t K) { return (int)(16 * (
 __host__ __device__ constexpr int64_t chain_lds_bytes(int64_t K, bool norm) {
     const int64_t G = (K / 32 + 3) / 4, xf = 128 * G, nstage = (G + CH_SQ - 1) / CH_SQ;
     return (2 * CH_LANES * CH_DSTRIDE + xf + (norm ? K : 0) + 8 * (int64_t)chain_xstride(K)) * 4 +
-           nstage * 3 * CH_UNIT;
+           nstage * 3 * CH_UNIT + 4 * 320 * 4;
 }
 
 template <int MODE, bool NORM, int GX>
@@ -1970,6 +1970,7 @@ __global__ __launch_bounds__(THREADS) void gemv_q4_chain_kernel(GemvParams p, in
     float *wn = xs + XF;                             // NORM: the norm weights (K)
     float *xcm = wn + (NORM ? K : 0);                // the chain-major copy: 8 rows of xstride
     uint8_t *tile = (uint8_t *)(xcm + 8 * xstride);  // [stage][producer][CH_UNIT]
+    uint32_t *khist = (uint32_t *)(tile + (size_t)nstage * 3 * CH_UNIT);  // the fused K-WTA's histogram
 
     if (wave > 0) {
         // ---- producers: copy every stage's bytes, then dequantise stage by
@@ -2027,7 +2028,7 @@ __global__ __launch_bounds__(THREADS) void gemv_q4_chain_kernel(GemvParams p, in
     // epilogue operands (they land with them) ----
     const PairRows q = chain_rows<MODE>(p, npairs, lane & (CH_LANES - 1));
     const bool leader = lane < CH_LANES && q.pair_ok && (lane & 15) == 0;
-    float b0 = 0.0f, b1 = 0.0f, old0 = 0.0f, old1 = 0.0f, cs = 0.0f, sn = 0.0f;
+    float b0 = 0.0f, b1 = 0.0f, old0 = 0.0f, old1 = 0.0f, cs = 0.0f, sn = 0.0f, kthr = -INFINITY;
     int pos = 0;
     // longer rows whose producer also wrote the chain-major copy (x_cm, the
     // launcher checks its stride): that copy is this kernel's xcm as it stands
@@ -2045,6 +2046,7 @@ __global__ __launch_bounds__(THREADS) void gemv_q4_chain_kernel(GemvParams p, in
         if constexpr (MODE == MODE_RESIDUAL) {
             old0 = p.y[q.r0];
             if (q.r1 >= 0) old1 = p.y[q.r1];
+            if (p.kwta_k > 0) kthr = *p.kwta_thr;
         } else if constexpr (MODE == MODE_QKV) {
             pos = st->pos;
             const int hh = p.head_dim >> 1;
@@ -2058,6 +2060,15 @@ __global__ __launch_bounds__(THREADS) void gemv_q4_chain_kernel(GemvParams p, in
         return;
     }
     wait_vmcnt<0>();  // this wave's copies have landed (it alone reads them before the barriers)
+    if constexpr (MODE == MODE_QKV) {
+        // the previous block's K-WTA on this workgroup's copy of x (every
+        // workgroup finds the same threshold; workgroup 0 keeps it for the
+        // residual of the attention output)
+        if (p.kwta_k > 0) {
+            const float thr = wave_kwta(xs, (int)K, p.kwta_k, khist, lane);
+            if (blockIdx.x == 0 && lane == 0) *p.kwta_thr = thr;
+        }
+    }
     const int l = lane & 7;
     float4 xq[GX > 0 ? 4 * GX : 1];  // GX > 0: chain l's values c = 4i..4i+3 at xq[i]
     const float *xr = xcm + l * xstride;  // GX == 0: chain l's row of the chain-major copy
@@ -2257,6 +2268,10 @@ __global__ __launch_bounds__(THREADS) void gemv_q4_chain_kernel(GemvParams p, in
         if (r1 >= 0) p.y[r1] = y1;
     } else if constexpr (MODE == MODE_RESIDUAL) {
         if (isnan(y0) || (r1 >= 0 && isnan(y1))) nan_flag(st, p.layer, p.st_a);
+        if (p.kwta_k > 0) {  // the previous block's K-WTA on the residual (the MODE_QKV launch's threshold)
+            old0 = old0 < kthr ? -1e9f : old0;
+            old1 = old1 < kthr ? -1e9f : old1;
+        }
         const float h0 = old0 + y0;
         p.y[r0] = h0;
         bool bad = isnan(h0);
@@ -2361,6 +2376,27 @@ size_t gemv_lds_bytes(int64_t K, int fmt, bool norm) {
     return (size_t)(gemv_x_floats(K, fmt) + (norm ? ((K + 3) & ~(int64_t)3) : 0) + slack) * 4;
 }
 
+// The chain kernel's conditions: latency-bound Q4_0 matvecs (few rows) in the
+// modes it serves, with its stages and LDS within bounds.
+static bool chain_ok(const GemvParams &p, int64_t npairs) {
+    if (!(p.fmt == FMT_Q4_0 && (p.mode == MODE_STORE || p.mode == MODE_RESIDUAL || p.mode == MODE_QKV) && !p.gnorm &&
+          !p.x_out && p.nb > 0 && (npairs + CH_PAIRS - 1) / CH_PAIRS <= 2 * (int64_t)device_cu_count()))
+        return false;
+    const int64_t G = (p.nb + 3) / 4;
+    const size_t clds = (size_t)chain_lds_bytes(p.K, p.norm_w != nullptr);
+    return (G + CH_SQ - 1) / CH_SQ <= CH_MAX_STAGES && G * 80 <= (int64_t)sizeof(kZeroRows) &&
+           clds + 1024 <= max_lds_per_block();
+}
+
+bool gemv_chain_serves(const GemvParams &p) {
+    if (p.N <= 0 || p.K <= 0 || p.nb != (int32_t)(p.K / 32)) return false;
+    int64_t npairs;
+    if (p.mode == MODE_QKV) npairs = (p.q_rows + 2 * p.kv_rows) / 2;
+    else if (p.mode == MODE_STORE || p.mode == MODE_RESIDUAL) npairs = (p.N + 1) / 2;
+    else return false;
+    return npairs > 0 && chain_ok(p, npairs);
+}
+
 int launch_gemv(const GemvParams &p, hipStream_t s) {
     if (p.N < 0 || p.K <= 0 || !p.x || !p.y)
         return set_error(GAJE_ERR_INVALID_ARG, "gemv: invalid shape or null buffer");
@@ -2411,21 +2447,21 @@ int launch_gemv(const GemvParams &p, hipStream_t s) {
             return set_error(GAJE_ERR_INVALID_ARG, "gemv: unknown mode %d", p.mode);
     }
     if (npairs == 0) return GAJE_OK;
+    const bool chain = chain_ok(p, npairs);
+    if (p.kwta_k > 0 && (!chain || (p.mode != MODE_QKV && p.mode != MODE_RESIDUAL) || !p.kwta_thr || p.x_cm ||
+                         (p.mode == MODE_QKV && p.K > INT32_MAX)))
+        return set_error(GAJE_ERR_UNSUPPORTED, "gemv: the fused K-WTA runs only on the chain kernel (QKV / residual)");
     // latency-bound Q4_0 matvecs (few rows): split waves
-    if (p.fmt == FMT_Q4_0 && (p.mode == MODE_STORE || p.mode == MODE_RESIDUAL || p.mode == MODE_QKV) && !p.gnorm &&
-        !p.x_out && p.nb > 0 && (npairs + CH_PAIRS - 1) / CH_PAIRS <= 2 * (int64_t)device_cu_count()) {
+    if (chain) {
         const int64_t G = (p.nb + 3) / 4;
         const size_t clds = (size_t)chain_lds_bytes(p.K, p.norm_w != nullptr);
-        if ((G + CH_SQ - 1) / CH_SQ <= CH_MAX_STAGES && G * 80 <= (int64_t)sizeof(kZeroRows) &&
-            clds + 1024 <= max_lds_per_block()) {
-            const int64_t grid = (npairs + CH_PAIRS - 1) / CH_PAIRS;
-            void (*fn)(GemvParams, int64_t, int) = chain_kernel(p.mode, p.norm_w != nullptr, (int)G);
-            GemvParams pc = p;  // x_cm only in the layout this kernel copies whole
-            if (pc.x_cm && (pc.cm_stride != chain_xstride(p.K) || ((uintptr_t)pc.x_cm & 15))) pc.x_cm = nullptr;
-            hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(THREADS), clds, s, pc, npairs, chain_xstride(p.K));
-            GAJE_HIP_CHECK(hipGetLastError());
-            return GAJE_OK;
-        }
+        const int64_t grid = (npairs + CH_PAIRS - 1) / CH_PAIRS;
+        void (*fn)(GemvParams, int64_t, int) = chain_kernel(p.mode, p.norm_w != nullptr, (int)G);
+        GemvParams pc = p;  // x_cm only in the layout this kernel copies whole
+        if (pc.x_cm && (pc.cm_stride != chain_xstride(p.K) || ((uintptr_t)pc.x_cm & 15))) pc.x_cm = nullptr;
+        hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(THREADS), clds, s, pc, npairs, chain_xstride(p.K));
+        GAJE_HIP_CHECK(hipGetLastError());
+        return GAJE_OK;
     }
     if (p.fmt == FMT_Q4_0 && (p.mode == MODE_STORE || p.mode == MODE_RESIDUAL || p.mode == MODE_QKV) && !p.gnorm &&
         !p.x_out && 2 * npairs <= SPLIT_MAX_ROWS && p.nb > 0 && (!p.norm_w || p.K / 4 <= SPLIT_NORM_MAX_K4)) {

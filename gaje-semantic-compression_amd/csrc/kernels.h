@@ -28,6 +28,7 @@ struct DevState {
     uint32_t nan_code;         // min(layer * 8 + stage) over failed guards
     int32_t out_cap;           // capacity of the greedy output buffer
     unsigned long long argmax_key;  // packed (orderable logit, ~index) maximum
+    float kwta_thr;            // the block K-WTA threshold of the current layer's input
 };
 
 // State of the greedy generate loop kept on the device (generate_native_core,
@@ -113,6 +114,12 @@ struct GemvParams {
     float *y_cm;
     const float *x_cm;
     int32_t cm_stride;
+    // the previous block's lateral_inhibition_kwta, fused (kwta_k > 0; the
+    // chain kernel only): MODE_QKV selects the threshold of x (its k-th largest
+    // value), applies x < thr -> -1e9 to its copy and has workgroup 0 store thr
+    // at kwta_thr; MODE_RESIDUAL applies the same mask to the residual it reads
+    int64_t kwta_k;
+    float *kwta_thr;
     // guards (stage < 0 disables a check)
     DevState *st;
     int32_t layer;
@@ -122,6 +129,9 @@ struct GemvParams {
 // Validates shapes against what the kernels assume and launches; returns a
 // GAJE_* status.
 int launch_gemv(const GemvParams &p, hipStream_t s);
+// Whether launch_gemv runs p on the chain kernel, the one kernel that takes
+// the fused K-WTA fields (launch_gemv rejects kwta_k > 0 elsewhere).
+bool gemv_chain_serves(const GemvParams &p);
 // Row stride (floats) of the chain-major activation layout for in_features K.
 int gemv_chain_stride(int64_t K);
 // Q4_0Block rows (file layout, K % 32 == 0) -> the GEMV's packed row layout.

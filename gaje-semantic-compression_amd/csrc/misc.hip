@@ -179,6 +179,21 @@ __global__ __launch_bounds__(T) void kwta_kernel(float *x, int64_t n, int64_t k,
     }
 }
 
+// The same K-WTA for rows of at most 64 * 4 * KW_WQ values with n % 4 == 0
+// (the blocks' hidden states): one wave, the row copied into LDS, wave_kwta
+// (the fused form the QKV matvec runs), the row written back.
+constexpr int KWW_MAX = WAVE * 4 * KW_WQ;
+__global__ __launch_bounds__(WAVE) void kwta_wave_kernel(float *x, int n, int64_t k, DevState *st) {
+    __shared__ __align__(16) float xs[KWW_MAX];
+    __shared__ __align__(16) uint32_t hist[4 * 320];
+    if (st && st->halted) return;
+    const int lane = threadIdx.x;
+    for (int i = lane; i < n; i += WAVE) xs[i] = x[i];
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    wave_kwta(xs, n, k, hist, lane);
+    for (int i = lane; i < n; i += WAVE) x[i] = xs[i];
+}
+
 // First maximum with a strict '>' (llm/forward.rs:262-271).
 __global__ __launch_bounds__(1024) void argmax_kernel(const float *x, int64_t n, uint32_t *idx) {
     __shared__ unsigned long long best;
@@ -376,7 +391,10 @@ int launch_state_set(DevState *st, int32_t pos, uint32_t token, int32_t out_cap,
 int launch_kwta(float *x, int64_t n, int64_t k, DevState *st, hipStream_t s) {
     if (!x || n < 0) return set_error(GAJE_ERR_INVALID_ARG, "kwta: bad arguments");
     if (n <= k || k <= 0) return GAJE_OK;
-    hipLaunchKernelGGL(kwta_kernel<1024>, dim3(1), dim3(1024), 0, s, x, n, k, st);
+    if (n % 4 == 0 && n <= KWW_MAX)
+        hipLaunchKernelGGL(kwta_wave_kernel, dim3(1), dim3(WAVE), 0, s, x, (int)n, k, st);
+    else
+        hipLaunchKernelGGL(kwta_kernel<1024>, dim3(1), dim3(1024), 0, s, x, n, k, st);
     GAJE_HIP_CHECK(hipGetLastError());
     return GAJE_OK;
 }

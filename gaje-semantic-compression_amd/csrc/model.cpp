@@ -586,7 +586,7 @@ int enqueue_token(gaje_hip_model *m, hipEvent_t ev_blocks_done) {
     GAJE_TRY(launch_embed(ep, m->stream));
 
     const size_t layer_kv = (size_t)m->n_kv * m->cap * m->hd;
-    for (int64_t l = 0; l < m->n_layers; ++l) {
+    auto qkv_params = [&](int64_t l) {
         Layer &Ly = m->layers[l];
         GemvParams p = gemv_base(m, Ly.qkv, m->h);
         p.norm_w = Ly.attn_norm;
@@ -606,6 +606,32 @@ int enqueue_token(gaje_hip_model *m, hipEvent_t ev_blocks_done) {
         p.v_cache = m->v_cache + l * layer_kv;
         p.kv_head_stride = m->cap * m->hd;
         p.kv_cap = m->cap;
+        return p;
+    };
+    auto o_params = [&](int64_t l) {
+        GemvParams p = gemv_base(m, m->layers[l].o, m->attn_out);
+        p.layer = (int32_t)l;
+        p.mode = MODE_RESIDUAL;
+        p.y = m->h;
+        return p;
+    };
+    // The blocks' K-WTA (block/forward.rs:144-148) after block l < L - 1 runs
+    // inside block l + 1's QKV launch (threshold and mask of its copy of h) and
+    // attention-output launch (the same mask on the residual h it adds to),
+    // when both run on the chain kernel; after the last block, and otherwise,
+    // as its own launch.
+    const int64_t bk = block_kwta_k(m);
+    bool fuse = bk > 0;
+    for (int64_t l = 1; fuse && l < m->n_layers; ++l)
+        fuse = gemv_chain_serves(qkv_params(l)) && gemv_chain_serves(o_params(l));
+    for (int64_t l = 0; l < m->n_layers; ++l) {
+        Layer &Ly = m->layers[l];
+        const bool fused_in = fuse && l > 0;
+        GemvParams p = qkv_params(l);
+        if (fused_in) {
+            p.kwta_k = bk;
+            p.kwta_thr = &m->st->kwta_thr;
+        }
         GAJE_TRY(launch_gemv(p, m->stream));
 
         AttnParams ap{};
@@ -622,10 +648,11 @@ int enqueue_token(gaje_hip_model *m, hipEvent_t ev_blocks_done) {
         ap.layer = (int32_t)l;
         GAJE_TRY(launch_attention(ap, m->stream));
 
-        p = gemv_base(m, Ly.o, m->attn_out);
-        p.layer = (int32_t)l;
-        p.mode = MODE_RESIDUAL;
-        p.y = m->h;
+        p = o_params(l);
+        if (fused_in) {
+            p.kwta_k = bk;
+            p.kwta_thr = &m->st->kwta_thr;
+        }
         GAJE_TRY(launch_gemv(p, m->stream));
 
         p = gemv_base(m, Ly.gate_up, m->h);
@@ -651,8 +678,7 @@ int enqueue_token(gaje_hip_model *m, hipEvent_t ev_blocks_done) {
         p.st_b = ST_FINAL;
         GAJE_TRY(launch_gemv(p, m->stream));
 
-        const int64_t bk = block_kwta_k(m);
-        if (bk > 0) GAJE_TRY(launch_kwta(m->h, m->n_embd, bk, m->st, m->stream));
+        if (bk > 0 && (!fuse || l + 1 == m->n_layers)) GAJE_TRY(launch_kwta(m->h, m->n_embd, bk, m->st, m->stream));
     }
     if (ev_blocks_done) GAJE_HIP_CHECK(hipEventRecord(ev_blocks_done, m->stream));
     return enqueue_head(m);

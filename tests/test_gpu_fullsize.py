@@ -58,9 +58,9 @@ def _model(hip, tmp_models, preset):
     return p
 
 
-def _oracle_prefill(O, path, prompt):
+def _oracle_prefill(O, path, prompt, kwta=0.0):
     r = O.load_genomic(path)
-    r.set_k_wta_ratio(0.0)
+    r.set_k_wta_ratio(kwta)
     t = time.perf_counter()
     last = None
     for i, tok in enumerate(prompt):
@@ -69,14 +69,14 @@ def _oracle_prefill(O, path, prompt):
     return r, last
 
 
-def _decode_case(hip, O, path, prompt_len, gen, seed):
+def _decode_case(hip, O, path, prompt_len, gen, seed, kwta=0.0):
     g = hip.load_genomic_auto(path)
-    g.set_k_wta_ratio(0.0)
+    g.set_k_wta_ratio(kwta)
     prompt = np.random.default_rng(seed).integers(0, g.vocab_size, prompt_len).astype(np.uint32)
     g.reserve(prompt_len + gen + 2)
     g.clear_cache_py()
     glast = g.prefill(prompt, want_logits=True)
-    r, rlast = _oracle_prefill(O, path, prompt)
+    r, rlast = _oracle_prefill(O, path, prompt, kwta)
     assert same_bits(glast, rlast), "last prompt logits differ"
     first = O.argmax_first(rlast)
     out = g.decode_greedy(first, gen)
@@ -97,6 +97,15 @@ def _decode_case(hip, O, path, prompt_len, gen, seed):
 @pytest.mark.timeout(900)
 def test_qwen2_0_5b_prompt_512_decode_to_768(hip, O, tmp_models):
     _decode_case(hip, O, _model(hip, tmp_models, "qwen2-0.5b"), 512, 255, 7)
+
+
+@pytest.mark.timeout(600)
+def test_qwen2_0_5b_kwta_decode(hip, O, tmp_models):
+    """K-WTA 0.5 (the flat-load default, flat_reader.rs:234): every block's
+    output filtered (block/forward.rs:144-148; after blocks 0..22 inside the
+    next block's QKV and attention-output launches) and the logits filtered,
+    bit for bit over a 96-token prompt and 64 greedy tokens."""
+    _decode_case(hip, O, _model(hip, tmp_models, "qwen2-0.5b"), 96, 64, 21, kwta=0.5)
 
 
 @pytest.mark.timeout(900)

@@ -249,13 +249,18 @@ def test_kwta_exact(hip, O, n, ratio):
     assert np.array_equal(got, ref)
 
 
-@pytest.mark.parametrize("case", ["logit_like", "signed_zeros", "all_equal", "k1", "unaligned"])
-def test_kwta_edge_cases(hip, O, case):
-    """Logits in a narrow range (most keys share their top byte: the ballot
-    merge), -0/+0 around the threshold, every value equal, k = 1, and a row
-    that does not start on a 16-byte boundary (the scalar path)."""
-    n = 151936
-    x = hip.synth.normal(62, f"ke.{case}", n, 0.0, 0.02)
+@pytest.mark.parametrize("n", [151936, 896])
+@pytest.mark.parametrize("case", ["logit_like", "signed_zeros", "all_equal", "k1", "unaligned", "pairs"])
+def test_kwta_edge_cases(hip, O, case, n):
+    """Values in a narrow range (most keys share their top byte), -0/+0 around
+    the threshold, every value equal, k = 1, a row that does not start on a
+    16-byte boundary (the scalar path of the long rows), and values in equal
+    pairs (no bin ever narrows to one key).  896 values (a hidden state) run
+    the one-wave select that the QKV matvec also runs; 151936 the
+    workgroup-wide one."""
+    x = hip.synth.normal(62, f"ke.{case}.{n}", n, 0.0, 0.02)
+    if case == "pairs":
+        x[1::2] = x[0::2]
     k = n // 2
     off = 0
     if case == "signed_zeros":
