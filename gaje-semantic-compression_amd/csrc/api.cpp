@@ -226,6 +226,13 @@ extern "C" int gaje_hip_q4_0_gemv(const void *packed, const float *x, const floa
     return launch_gemv(plain_gemv(FMT_Q4_0, packed, x, bias, bias_len, y, n, k), as_stream(stream));
 }
 
+extern "C" int gaje_hip_q4_0_gemv_blocks(const void *blocks, const float *x, const float *bias, int64_t bias_len,
+                                         float *y, int64_t n, int64_t k, void *stream) {
+    clear_error();
+    GAJE_TRY(check_dims(n, k));
+    return launch_q4_0_gemv_blocks((const uint8_t *)blocks, x, bias, bias_len, y, n, k, as_stream(stream));
+}
+
 extern "C" int gaje_hip_q4_0_gemm(const void *packed, const float *X, const float *bias, int64_t bias_len, float *Y,
                                   int64_t m, int64_t n, int64_t k, void *stream) {
     GAJE_TRY(check_dims(n, k));

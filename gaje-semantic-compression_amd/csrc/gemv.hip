@@ -2327,6 +2327,83 @@ int launch_pack_q8_0(const uint8_t *src, uint8_t *dst, int64_t N, int64_t K, hip
     return GAJE_OK;
 }
 
+namespace {
+
+// genomic_dot_product_q4_0 on the file's own Q4_0Blocks (20 bytes: f16 scale,
+// f16 min, 16 code bytes, element e in byte e / 2, the low nibble for even e:
+// blocks.rs:18-30), with no packing: lanes 8r..8r+7 of a wave hold row r's
+// eight chains (chain l = element 8c + l of each block's chunk c,
+// genomic.rs:263-336), d = fma(f32(q), scale, min) and acc = fma(d, x, acc)
+// block by block, then the AVX2 reduction ((a0+a4)+(a2+a6)) +
+// ((a1+a5)+(a3+a7)), the flush and the bias.  A lane reads its block's five
+// dwords (the scale/min word and the four code dwords that hold its nibbles)
+// and its four inputs, QB_AHEAD blocks ahead of the arithmetic.
+constexpr int QB_AHEAD = 4;
+__global__ __launch_bounds__(256) void gemv_q4_blocks_kernel(const uint8_t *blocks, const float *x, const float *bias,
+                                                            int64_t bias_len, float *y, int64_t n, int nb) {
+    const int lane = threadIdx.x & 63, l = lane & 7;
+    const int64_t row = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 3;
+    const bool ok = row < n;
+    const uint32_t *rb = (const uint32_t *)(blocks + (size_t)(ok ? row : 0) * nb * 20);
+    const int sh = 8 * (l >> 1) + 4 * (l & 1);  // the nibble of element 8c + l in code dword c
+    float acc = 0.0f;
+    uint32_t w[QB_AHEAD][5];
+    float xv[QB_AHEAD][4];
+    auto load = [&](int j, int s) {
+        const uint32_t *b = rb + 5 * (j < nb ? j : nb - 1);
+#pragma unroll
+        for (int i = 0; i < 5; ++i) w[s][i] = b[i];
+        const float *xb = x + 32 * (int64_t)(j < nb ? j : nb - 1) + l;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) xv[s][c] = xb[8 * c];
+    };
+#pragma unroll
+    for (int s = 0; s < QB_AHEAD; ++s) load(s, s);
+    for (int j0 = 0; j0 < nb; j0 += QB_AHEAD) {
+#pragma unroll
+        for (int s = 0; s < QB_AHEAD; ++s) {
+            const int j = j0 + s;
+            if (j < nb) {
+                const float scale = half_bits((uint16_t)(w[s][0] & 0xFFFFu));
+                const float mn = half_bits((uint16_t)(w[s][0] >> 16));
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const float q = (float)((w[s][1 + c] >> sh) & 15u);
+                    const float d = fmaf(q, scale, mn);
+                    acc = fmaf(d, xv[s][c], acc);
+                }
+            }
+            load(j + QB_AHEAD, s);  // past the row: its last block again, never used
+        }
+    }
+    const int base = lane & ~7;
+    const float u = acc + __shfl(acc, base + ((l + 4) & 7), WAVE);
+    const float vv = u + __shfl(u, base + ((l + 2) & 7), WAVE);
+    float t = flush_small(vv + __shfl(vv, base + ((l + 1) & 7), WAVE));
+    if (ok && l == 0) {
+        if (row < bias_len) t = t + bias[row];
+        y[row] = t;
+    }
+}
+
+}  // namespace
+
+int launch_q4_0_gemv_blocks(const uint8_t *blocks, const float *x, const float *bias, int64_t bias_len, float *y,
+                            int64_t n, int64_t k, hipStream_t s) {
+    if (n < 0 || k <= 0 || k % 32 != 0)
+        return set_error(GAJE_ERR_INVALID_ARG, "q4_0 gemv: in_features must be a positive multiple of 32 (got %lld)",
+                         (long long)k);
+    if (n == 0) return GAJE_OK;
+    if (!blocks || !x || !y || (bias_len > 0 && !bias)) return set_error(GAJE_ERR_INVALID_ARG, "q4_0 gemv: null buffer");
+    if (((uintptr_t)blocks & 3) || ((uintptr_t)x & 3))
+        return set_error(GAJE_ERR_INVALID_ARG, "q4_0 gemv: blocks and x must be 4-byte aligned");
+    const int64_t grid = (n * 8 + 255) / 256;
+    hipLaunchKernelGGL(gemv_q4_blocks_kernel, dim3((unsigned)grid), dim3(256), 0, s, blocks, x, bias, bias_len, y, n,
+                       (int)(k / 32));
+    GAJE_HIP_CHECK(hipGetLastError());
+    return GAJE_OK;
+}
+
 int launch_pack_q4_0(const uint8_t *src, uint8_t *dst, int64_t N, int64_t K, hipStream_t s) {
     if (N < 0 || K <= 0 || K % 32 != 0) return set_error(GAJE_ERR_INVALID_ARG, "pack: K must be a positive multiple of 32");
     if (N == 0) return GAJE_OK;

@@ -139,6 +139,9 @@ int gemv_chain_stride(int64_t K);
 // may read (and never uses); q4_0_packed_bytes includes them.
 constexpr int64_t Q4_TAIL_PAD = 2048;
 int launch_pack_q4_0(const uint8_t *src, uint8_t *dst, int64_t N, int64_t K, hipStream_t s);
+// genomic_dot_product_q4_0 straight from Q4_0Block rows (no packing).
+int launch_q4_0_gemv_blocks(const uint8_t *blocks, const float *x, const float *bias, int64_t bias_len, float *y,
+                            int64_t n, int64_t k, hipStream_t s);
 int64_t q4_0_packed_bytes(int64_t N, int64_t K);
 // Q8_0Block rows (K % 32 == 0) -> tiles of 8 rows: per group of four blocks,
 // the 8 rows' codes (128 bytes each, chain l's at [16l, 16l+16)) and then

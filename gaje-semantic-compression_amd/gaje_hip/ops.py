@@ -105,6 +105,12 @@ def q4_0_gemv(packed: DeviceBuffer, x: DeviceBuffer, y: DeviceBuffer, n: int, k:
     check(lib().gaje_hip_q4_0_gemv(packed.ptr, x.ptr, _p(bias), bias_len, y.ptr, n, k, stream))
 
 
+def q4_0_gemv_blocks(blocks: DeviceBuffer, x: DeviceBuffer, y: DeviceBuffer, n: int, k: int,
+                     bias: DeviceBuffer | None = None, bias_len: int = 0, stream=None) -> None:
+    """The Q4_0 matvec on the file's own Q4_0Block rows (no packing)."""
+    check(lib().gaje_hip_q4_0_gemv_blocks(blocks.ptr, x.ptr, _p(bias), bias_len, y.ptr, n, k, stream))
+
+
 def q4_0_gemm(packed: DeviceBuffer, X: DeviceBuffer, Y: DeviceBuffer, m: int, n: int, k: int,
               bias: DeviceBuffer | None = None, bias_len: int = 0, stream=None) -> None:
     check(lib().gaje_hip_q4_0_gemm(packed.ptr, X.ptr, _p(bias), bias_len, Y.ptr, m, n, k, stream))

@@ -94,6 +94,14 @@ int gaje_hip_q4_0_pack(const void *blocks, void *packed, int64_t n, int64_t k, v
 int gaje_hip_q4_0_gemv(const void *packed, const float *x, const float *bias, int64_t bias_len,
                        float *y, int64_t n, int64_t k, void *stream);
 
+/* The same matvec straight from the file's Q4_0Block rows (20 bytes per
+ * block, n * k/32 blocks, 4-byte aligned), with no packing: the operator as
+ * genomic_dot_product_q4_0(&[Q4_0Block], &[f32]) takes it
+ * (compute/kernels/genomic.rs:210-336), bit for bit like gaje_hip_q4_0_gemv.
+ * The packed entry above is the faster one for weights that are read again. */
+int gaje_hip_q4_0_gemv_blocks(const void *blocks, const float *x, const float *bias, int64_t bias_len, float *y,
+                              int64_t n, int64_t k, void *stream);
+
 /* The same Q4_0 matvec for m activation rows at once (Y[m][n] = X[m][k] W^T):
  * m independent GenomicLinear::forward_core calls sharing one weight read.
  * No reference function batches rows; semantics are per row as above. */

@@ -66,13 +66,17 @@ def edge_blocks(n, k, seed, halves=EDGE):
     return b.reshape(-1)
 
 
-def _run(hip, O, n, k, bias, seed):
+def _run(hip, O, n, k, bias, seed, native=False):
     blocks = edge_blocks(n, k, seed)
     x = hip.synth.normal(seed, f"edge.x.{k}", k)
     b = hip.synth.normal(seed, f"edge.b.{n}", n, 0.0, 0.02) if bias else None
     y = hip.ops.DeviceBuffer(n * 4)
-    hip.ops.q4_0_gemv(hip.ops.q4_0_upload(blocks, n, k), hip.ops.DeviceBuffer.from_array(x), y, n, k,
-                      bias=hip.ops.DeviceBuffer.from_array(b) if bias else None, bias_len=n if bias else 0)
+    kw = dict(bias=hip.ops.DeviceBuffer.from_array(b) if bias else None, bias_len=n if bias else 0)
+    if native:
+        hip.ops.q4_0_gemv_blocks(hip.ops.DeviceBuffer.from_array(blocks), hip.ops.DeviceBuffer.from_array(x), y, n, k,
+                                 **kw)
+    else:
+        hip.ops.q4_0_gemv(hip.ops.q4_0_upload(blocks, n, k), hip.ops.DeviceBuffer.from_array(x), y, n, k, **kw)
     got = y.read(np.float32)
     ref = O.GenomicLinear(blocks, b"", None, n, k, b, 4).forward_core(x)
     return got, ref
@@ -92,6 +96,14 @@ def test_q4_0_gemv_edge_scales(hip, O, n, k, bias, form):
     got, ref = _run(hip, O, n, k, bias, 100 + n % 97)
     assert np.isfinite(ref).all()
     assert same_bits(got, ref), form
+
+
+@pytest.mark.parametrize("n,k", [(896, 576), (300, 4864)])
+def test_q4_0_gemv_blocks_edge_scales(hip, O, n, k):
+    """The same scale/min set through the matvec on unpacked Q4_0Block rows."""
+    got, ref = _run(hip, O, n, k, True, 300 + n % 89, native=True)
+    assert np.isfinite(ref).all()
+    assert same_bits(got, ref)
 
 
 def _scale_blocks_in_file(path, out, every=3):

@@ -144,6 +144,31 @@ def test_q4_0_gemv_no_bias(hip, O, n, k):
     assert same_bits(got, ref)
 
 
+@pytest.mark.parametrize("n,k", [(4864, 896), (963, 576), (5, 32), (129, 4864), (1, 128), (33, 1056), (700, 96)])
+def test_q4_0_gemv_blocks(hip, O, n, k):
+    """genomic_dot_product_q4_0 on the file's own Q4_0Block rows (no packing):
+    bit for bit with the oracle, and so with the packed matvec; a bias shorter
+    than n; K = 576 (18 blocks, the SmolLM2 rows the packed layout pads)."""
+    blocks = hip.synth.q4_0_tensor(18, f"gemvb.{n}.{k}", n, k)
+    x = hip.synth.normal(19, f"xb.{k}", k)
+    bias = hip.synth.normal(20, f"bb.{n}", (n + 1) // 2, 0.0, 0.02)
+    y = _out(hip, n * 4)
+    hip.ops.q4_0_gemv_blocks(_dev(hip, blocks), _dev(hip, x), y, n, k, bias=_dev(hip, bias), bias_len=bias.size)
+    got = y.read(np.float32)
+    ref = _oracle_q4_rows(O, blocks, x, n, k, bias)
+    assert same_bits(got, ref)
+
+
+def test_q4_0_gemv_blocks_errors(hip):
+    """in_features not a multiple of 32, and a misaligned block pointer, are errors."""
+    buf = _out(hip, 4096)
+    y = _out(hip, 64)
+    with pytest.raises(hip.GajeError):
+        hip.ops.q4_0_gemv_blocks(buf, buf, y, 2, 48)
+    rc = hip.lib().gaje_hip_q4_0_gemv_blocks(buf.ptr + 2, buf.ptr, None, 0, y.ptr, 2, 64, None)
+    assert rc != 0 and "aligned" in hip.last_error()
+
+
 def test_q4_0_gemv_flush_rule(hip, O):
     # rows built to cancel exactly: the reference flushes |t| < 1e-6 to 0 before the bias
     k = 64
