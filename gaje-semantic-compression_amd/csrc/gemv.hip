@@ -1313,6 +1313,16 @@ __device__ __forceinline__ void lds_copy_bytes(const void *g, int64_t n, uint32_
         if (o + lane * 16 < n) lds_dma16((const uint8_t *)g + o + lane * 16, dst + (uint32_t)o);
 }
 
+// The AVX2 reduction ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) of the eight chains
+// held by lanes 8r..8r+7 (chain l in lane 8r + l), valid in lane 8r: three DPP
+// row_shl adds (lane i reads lane i + n of its 16-lane row; the lanes whose
+// sums are used read inside their own 8-lane group, and addition commutes).
+__device__ __forceinline__ float red8_dpp(float a) {
+    const float u = a + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, a), 0x104, 0xF, 0xF, false));
+    const float v = u + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, u), 0x102, 0xF, 0xF, false));
+    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x101, 0xF, 0xF, false));
+}
+
 // Chain l of the rows at rp0 and rp1 (LDS), interleaved: groups 0..G-1 in
 // order, then the reduction and the flush (q4_consume's sequence).  xr holds
 // chain l's activations (16 per group), in registers for the whole kernel.
@@ -1351,11 +1361,8 @@ __device__ __forceinline__ void q4l_rows2(const uint8_t *rp0, const uint8_t *rp1
             a1 = fmaf(d1[b][3], x.w, a1);
         }
     }
-    float u = a0 + shfl(a0, base + ((l + 4) & 7)), v = u + shfl(u, base + ((l + 2) & 7));
-    y0 = flush_small(v + shfl(v, base + ((l + 1) & 7)));
-    u = a1 + shfl(a1, base + ((l + 4) & 7));
-    v = u + shfl(u, base + ((l + 2) & 7));
-    y1 = flush_small(v + shfl(v, base + ((l + 1) & 7)));
+    y0 = flush_small(red8_dpp(a0));
+    y1 = flush_small(red8_dpp(a1));
 }
 
 // One chain: q4l_rows2 for the row at rp alone.
@@ -1368,8 +1375,7 @@ __device__ __forceinline__ float q4l_row1(const uint8_t *rp, const float4 (&xr)[
         const vu4 sm = *(const vu4 *)(rp + g * 80 + 64);
         a = q4_group(a, n, sm, X4{xr[4 * g], xr[4 * g + 1], xr[4 * g + 2], xr[4 * g + 3]});
     }
-    const float u = a + shfl(a, base + ((l + 4) & 7)), v = u + shfl(u, base + ((l + 2) & 7));
-    return flush_small(v + shfl(v, base + ((l + 1) & 7)));
+    return flush_small(red8_dpp(a));
 }
 
 // Modes: MODE_STORE (y[r] = row r; a tile is 8 ROWS rows, lane (r, l) walks
