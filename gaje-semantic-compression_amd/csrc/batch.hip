@@ -54,7 +54,7 @@ __global__ __launch_bounds__(NV / VPW * 64) void gemv_batch_q4_kernel(BatchGemvP
     constexpr int UPT = NV * 8 * (RUN / 4) / NTH;     // float4s staged per thread per chunk
     extern __shared__ __align__(16) float xs[];       // [2][NV][8][BQ_CROW]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int l = lane & 7, base = lane & ~7;
+    const int l = lane & 7;
     const int nb = p.nb, G = (nb + 3) >> 2;
     const int64_t K8 = (int64_t)nb * 4;               // column count of a chain row
     const int nch = (int)((K8 + RUN - 1) / RUN);
@@ -160,9 +160,7 @@ __global__ __launch_bounds__(NV / VPW * 64) void gemv_batch_q4_kernel(BatchGemvP
 #pragma unroll
         for (int v = 0; v < VPW; ++v) {
             const float a = acc[j][v];
-            const float u = a + __shfl(a, base + ((l + 4) & 7), WAVE);
-            const float w = u + __shfl(u, base + ((l + 2) & 7), WAVE);
-            const float t = w + __shfl(w, base + ((l + 1) & 7), WAVE);
+            const float t = red8_dpp(a);  // valid in lane 8r
             const int s = vz + v0 + v;
             const int64_t r = row[j];
             if (l != 0 || r >= p.N || s >= p.nv) continue;

@@ -180,6 +180,22 @@ __device__ __forceinline__ float order_key_inv(uint32_t k) {
     return __uint_as_float(u);
 }
 
+// The AVX2 reduction ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) of the eight chains
+// held by lanes 8r..8r+7 (chain l in lane 8r + l), valid in lane 8r: three DPP
+// row_shl adds (lane i reads lane i + n of its 16-lane row; the lanes whose
+// sums are used read inside their own 8-lane group, and addition commutes).
+__device__ __forceinline__ float red8_dpp(float a) {
+    const float u = a + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, a), 0x104, 0xF, 0xF, false));
+    const float v = u + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, u), 0x102, 0xF, 0xF, false));
+    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x101, 0xF, 0xF, false));
+}
+
+// x of lane i + 8 (of its 16-lane row): the second row of a pair whose
+// reductions sit in lanes 16k and 16k + 8.
+__device__ __forceinline__ float dpp_shl8(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x108, 0xF, 0xF, false));
+}
+
 // The reference's |t| < 1e-6 -> 0 flush of the 4-bit dots (genomic.rs:198-203,331-335).
 __device__ __forceinline__ float flush_small(float t) { return fabsf(t) < 1e-6f ? 0.0f : t; }
 

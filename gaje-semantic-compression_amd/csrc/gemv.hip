@@ -265,11 +265,8 @@ __device__ __forceinline__ float q4_consume(const GemvParams &p, const XView &xv
     if (rem == D - 1) acc = q4_tail<D - 1, D>(acc, r, xg, xc, nb - 4 * g);
     else if (rem > D / 2) acc = q4_tail<D, D>(acc, r, xg, xc, nb - 4 * g);
     else if (rem > 0) acc = q4_tail<D / 2, D>(acc, r, xg, xc, nb - 4 * g);
-    // lanes base..base+7 hold chains 0..7
-    const float u = acc + shfl(acc, base + ((l + 4) & 7));  // lane l<4: a_l + a_{l+4}
-    const float v = u + shfl(u, base + ((l + 2) & 7));      // lane 0: u0+u2, lane 1: u1+u3
-    const float total = v + shfl(v, base + ((l + 1) & 7));  // lane 0: (u0+u2) + (u1+u3)
-    return flush_small(total);
+    // lanes base..base+7 hold chains 0..7; the sum is valid in lane base
+    return flush_small(red8_dpp(acc));
 }
 
 // Ring depth of the Q4_0 row walk for rows of nb blocks: a short row's groups
@@ -405,10 +402,7 @@ __device__ __forceinline__ float q8_consume(const GemvParams &p, const XView &xv
     if (rem == D - 1) acc = q8_tail<D - 1, D>(acc, r, xg, xc, nb - 4 * g);
     else if (rem > D / 2) acc = q8_tail<D, D>(acc, r, xg, xc, nb - 4 * g);
     else if (rem > 0) acc = q8_tail<D / 2, D>(acc, r, xg, xc, nb - 4 * g);
-    const float u = acc + shfl(acc, base + ((l + 4) & 7));
-    const float v = u + shfl(u, base + ((l + 2) & 7));
-    const float total = v + shfl(v, base + ((l + 1) & 7));
-    return flush_small(total);
+    return flush_small(red8_dpp(acc));  // valid in lane base
 }
 
 // Q8_0Block rows (file layout, 34 bytes per block) -> the tiled layout; one
@@ -1313,16 +1307,6 @@ __device__ __forceinline__ void lds_copy_bytes(const void *g, int64_t n, uint32_
         if (o + lane * 16 < n) lds_dma16((const uint8_t *)g + o + lane * 16, dst + (uint32_t)o);
 }
 
-// The AVX2 reduction ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) of the eight chains
-// held by lanes 8r..8r+7 (chain l in lane 8r + l), valid in lane 8r: three DPP
-// row_shl adds (lane i reads lane i + n of its 16-lane row; the lanes whose
-// sums are used read inside their own 8-lane group, and addition commutes).
-__device__ __forceinline__ float red8_dpp(float a) {
-    const float u = a + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, a), 0x104, 0xF, 0xF, false));
-    const float v = u + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, u), 0x102, 0xF, 0xF, false));
-    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x101, 0xF, 0xF, false));
-}
-
 // Chain l of the rows at rp0 and rp1 (LDS), interleaved: groups 0..G-1 in
 // order, then the reduction and the flush (q4_consume's sequence).  xr holds
 // chain l's activations (16 per group), in registers for the whole kernel.
@@ -1869,11 +1853,8 @@ __global__ __launch_bounds__(THREADS) void gemv_q4_split_kernel(GemvParams p, in
         }
     }
     // lanes 8r..8r+7 hold a row's chains 0..7: the reduction of q4_consume
-    const int base = lane & ~7;
-    const float u = acc + shfl(acc, base + ((l + 4) & 7));
-    const float vv = u + shfl(u, base + ((l + 2) & 7));
-    const float total = q.row_ok ? flush_small(vv + shfl(vv, base + ((l + 1) & 7))) : 0.0f;
-    const float v1 = shfl(total, (lane & ~15) + 8);  // the pair's second row
+    const float total = q.row_ok ? flush_small(red8_dpp(acc)) : 0.0f;  // valid in lane 8r
+    const float v1 = dpp_shl8(total);  // the pair's second row
     if (!leader) return;
     const int64_t r0 = q.r0, r1 = q.r1;
     const float y0 = finish_row(p, xv, r0, total, b0);
@@ -2248,11 +2229,8 @@ __global__ __launch_bounds__(THREADS) void gemv_q4_chain_kernel(GemvParams p, in
         }
     }
     // lanes 8ρ..8ρ+7 hold a row's chains 0..7: the reduction of q4_consume
-    const int base = lane & ~7;
-    const float u = acc + shfl(acc, base + ((l + 4) & 7));
-    const float vv = u + shfl(u, base + ((l + 2) & 7));
-    const float total = q.row_ok ? flush_small(vv + shfl(vv, base + ((l + 1) & 7))) : 0.0f;
-    const float v1 = shfl(total, (lane & ~15) + 8);  // the pair's second row
+    const float total = q.row_ok ? flush_small(red8_dpp(acc)) : 0.0f;  // valid in lane 8r
+    const float v1 = dpp_shl8(total);  // the pair's second row
     if (!leader) return;
     auto finish = [&](int64_t r, float v, float bias) {  // finish_row over this kernel's copy of x
         if (p.a_ptr) {
@@ -2382,10 +2360,7 @@ __global__ __launch_bounds__(256) void gemv_q4_blocks_kernel(const uint8_t *bloc
             load(j + QB_AHEAD, s);  // past the row: its last block again, never used
         }
     }
-    const int base = lane & ~7;
-    const float u = acc + __shfl(acc, base + ((l + 4) & 7), WAVE);
-    const float vv = u + __shfl(u, base + ((l + 2) & 7), WAVE);
-    float t = flush_small(vv + __shfl(vv, base + ((l + 1) & 7), WAVE));
+    float t = flush_small(red8_dpp(acc));  // valid in lane 8r
     if (ok && l == 0) {
         if (row < bias_len) t = t + bias[row];
         y[row] = t;
