@@ -89,52 +89,50 @@ __global__ __launch_bounds__(64 * MOE_MAX_EXPERTS) void moe_route_kernel(MoePara
 }
 
 // The router with everything staged in LDS (16-byte aligned x rows and router,
-// h % 4 == 0): a workgroup of 256 threads takes TPW tokens (4 with up to 8
-// experts, 2 with up to 16), copies the router and its tokens' activations
-// into LDS with LDS-direct loads (all in flight at once), and then every
-// (token, expert, chain) has its own lane: lane 8e + l of the token's lanes
-// runs chain l of dot_product over the chunks, reading both operands from
-// LDS.  The reduction, the scalar tail and the softmax / top-2 compute
-// moe_route_kernel's values; the exponentials and quotients one lane per
-// expert, with the exponential's table in LDS.  (That kernel, one token per workgroup with the router
-// rows read from global memory eight chunks at a time, waits out 24 memory
-// round trips per logit.)
-template <int CPT>  // lanes per token: 64 (up to 8 experts) or 128 (up to 16)
+// h % 4 == 0): one workgroup of 256 threads per token copies the router and
+// the token's activations into LDS with LDS-direct loads (all in flight at
+// once, spread over the four waves), then lane SL e + l (l < 8, SL = 256 /
+// EMAX lanes per expert slot) runs chain l of dot_product over the chunks for
+// expert e, reading both operands from LDS; two or four experts per wave, so
+// the chains are spread over the four SIMDs.  The reduction, the scalar tail
+// and the softmax / top-2 compute moe_route_kernel's values: wave 0 forms one
+// exponential and one quotient per lane (the exponential's table in LDS) and
+// hands them round with lane shuffles.  (Four tokens per workgroup used a
+// quarter of the CUs and waited longer on their copies: 10 against 7 us for
+// 256 tokens x 8 experts x 1536.)
+template <int EMAX>  // 8 or 16 experts at most
 __global__ __launch_bounds__(256) void moe_route_lds_kernel(MoeParams p) {
-    constexpr int TPW = 256 / CPT;
+    constexpr int SL = 256 / EMAX;
     extern __shared__ __align__(16) float sm[];
-    __shared__ float logit[TPW][MOE_MAX_EXPERTS];
-    __shared__ float prob[TPW][MOE_MAX_EXPERTS];
+    __shared__ float logit[EMAX];
     __shared__ uint64_t tab[32];  // the exponential's table
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     if (tid < 32) tab[tid] = kExp2Tab[tid];
     const int E = p.n_expert;
-    const int64_t h = p.h, t0 = (int64_t)blockIdx.x * TPW;
-    // router rows h + 8 floats apart, so that the 8 experts' reads of one
-    // chunk element fall in different banks
+    const int64_t h = p.h, t = blockIdx.x;
+    // router rows h + 8 floats apart, so that the experts' reads of one chunk
+    // element fall in different banks
     const int64_t rs = h + 8;
     float *rw = sm;            // [E][rs]
-    float *xs = sm + E * rs;   // [TPW][h]
+    float *xs = sm + E * rs;   // [h]
     {
         const int64_t xb = h * 4, nx = (xb + 1023) / 1024;  // bytes and KiB copies of a row
-        const int64_t nt = t0 + TPW <= p.T ? TPW : p.T - t0;
-        for (int64_t q = wave; q < (E + nt) * nx; q += 4) {
+        for (int64_t q = wave; q < (E + 1) * nx; q += 4) {
             const int64_t r = q / nx, c = q % nx;
             if (1024 * c + 16 * lane < xb) {
                 if (r < E)
                     lds_dma16<true>((const uint8_t *)(p.router + r * h) + 1024 * c + 16 * lane,
                                     lds_addr(rw + r * rs) + (uint32_t)(1024 * c));
                 else
-                    lds_dma16((const uint8_t *)(p.x + (t0 + r - E) * p.ldx) + 1024 * c + 16 * lane,
-                              lds_addr(xs + (r - E) * h) + (uint32_t)(1024 * c));
+                    lds_dma16((const uint8_t *)(p.x + t * p.ldx) + 1024 * c + 16 * lane, lds_addr(xs) + (uint32_t)(1024 * c));
             }
         }
         wait_vmcnt<0>();
     }
     __syncthreads();
-    const int tt = tid / CPT, j = tid % CPT, e = j >> 3, l = j & 7;
-    const bool on = e < E && t0 + tt < p.T;
-    const float *x = xs + tt * h, *w = rw + (on ? e : 0) * rs;
+    const int e = tid / SL, l = tid % SL;
+    const bool on = l < 8 && e < E;
+    const float *w = rw + (on ? e : 0) * rs;
     float a = 0.0f;
     const int64_t chunks = h / 8;
     if (on) {
@@ -143,14 +141,15 @@ __global__ __launch_bounds__(256) void moe_route_lds_kernel(MoeParams p) {
             float xv[8], wv[8];
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
-                xv[u] = x[8 * (c + u) + l];
+                xv[u] = xs[8 * (c + u) + l];
                 wv[u] = w[8 * (c + u) + l];
             }
 #pragma unroll
             for (int u = 0; u < 8; ++u) a = fmaf(xv[u], wv[u], a);
         }
-        for (; c < chunks; ++c) a = fmaf(x[8 * c + l], w[8 * c + l], a);
+        for (; c < chunks; ++c) a = fmaf(xs[8 * c + l], w[8 * c + l], a);
     }
+    // lanes SL e .. SL e + 7 are an aligned group of 8
     const float a4 = __shfl(a, (lane + 4) & 7, 8);
     const float u = a + a4;                          // lane l<4: a_l + a_{l+4}
     const float u1 = __shfl(u, (lane + 1) & 7, 8);   // lane 0: u1, lane 2: u3
@@ -159,59 +158,45 @@ __global__ __launch_bounds__(256) void moe_route_lds_kernel(MoeParams p) {
     if (on && l == 0) {
         float sum = v + v2;
         for (int64_t k = chunks * 8; k < h; ++k) {
-            const float prod = x[k] * w[k];
+            const float prod = xs[k] * w[k];
             sum = sum + prod;
         }
-        logit[tt][e] = sum;
+        logit[e] = sum;
     }
     __syncthreads();
-    // softmax over the token's logits (all of them read into registers at once:
-    // the loops below then run on registers, not on dependent LDS reads), one
-    // exponential and one quotient per lane: e_j = expf(l_j - max), the sum in
-    // expert order (every lane forms the same one), p_j = e_j / sum; lane 0 of
-    // the token then takes the top-2 and the weights
-    const bool tok = t0 + tt < p.T;
-    float lg[MOE_MAX_EXPERTS];
+    if (wave != 0) return;
+    // softmax over the token's logits: e_j = expf(l_j - max) in lane j, the sum
+    // in expert order (every lane forms the same one), p_j = e_j / sum; lane 0
+    // then takes the top-2 and the weights
+    float lg[EMAX];
 #pragma unroll
-    for (int i = 0; i < MOE_MAX_EXPERTS; ++i) lg[i] = i < E ? logit[tt][i] : -INFINITY;
-    if (tok && j < E) {
-        float mx = lg[0];
+    for (int i = 0; i < EMAX; ++i) lg[i] = i < E ? logit[i] : -INFINITY;
+    float mx = lg[0];
 #pragma unroll
-        for (int i = 1; i < MOE_MAX_EXPERTS; ++i)
-            if (i < E) mx = lg[i] > mx ? lg[i] : mx;
-        prob[tt][j] = expf_ref_t(lg[j < E ? j : 0] - mx, tab);
-    }
-    __syncthreads();
-    float ex[MOE_MAX_EXPERTS];
+    for (int i = 1; i < EMAX; ++i)
+        if (i < E) mx = lg[i] > mx ? lg[i] : mx;
+    const float ej = expf_ref_t(logit[lane < E ? lane : 0] - mx, tab);
+    float ex[EMAX];
 #pragma unroll
-    for (int i = 0; i < MOE_MAX_EXPERTS; ++i) ex[i] = i < E ? prob[tt][i] : 0.0f;
-    __syncthreads();
-    if (tok && j < E) {
-        float ssum = 0.0f;
+    for (int i = 0; i < EMAX; ++i) ex[i] = __shfl(ej, i, WAVE);
+    float ssum = 0.0f;
 #pragma unroll
-        for (int i = 0; i < MOE_MAX_EXPERTS; ++i)
-            if (i < E) ssum = ssum + ex[i];
-        float mine = ex[0];
+    for (int i = 0; i < EMAX; ++i)
+        if (i < E) ssum = ssum + ex[i];
+    const float pj = ej / ssum;
+    float pr[EMAX];
 #pragma unroll
-        for (int i = 1; i < MOE_MAX_EXPERTS; ++i)
-            if (i == j) mine = ex[i];
-        prob[tt][j] = mine / ssum;
-    }
-    __syncthreads();
-    if (!tok || j != 0) return;
-    const int64_t t = t0 + tt;
-    float pr[MOE_MAX_EXPERTS];
-#pragma unroll
-    for (int i = 0; i < MOE_MAX_EXPERTS; ++i) pr[i] = i < E ? prob[tt][i] : 0.0f;
+    for (int i = 0; i < EMAX; ++i) pr[i] = __shfl(pj, i, WAVE);
+    if (lane != 0) return;
     int ia = 0;
     float pa = pr[0];
 #pragma unroll
-    for (int i = 1; i < MOE_MAX_EXPERTS; ++i)
+    for (int i = 1; i < EMAX; ++i)
         if (i < E && pr[i] > pa) ia = i, pa = pr[i];
     int ib = ia == 0 ? 1 : 0;
     float pb = pr[ib];
 #pragma unroll
-    for (int i = 0; i < MOE_MAX_EXPERTS; ++i)
+    for (int i = 0; i < EMAX; ++i)
         if (i < E && i != ia && pr[i] > pb) ib = i, pb = pr[i];
     const float den = pa + pb;
     p.top_idx[2 * t] = ia;
@@ -302,14 +287,12 @@ int launch_moe_route(const MoeParams &p, hipStream_t s) {
     if (p.T <= 0 || p.T > 65535 || p.n_expert < 2 || p.n_expert > MOE_MAX_EXPERTS || !p.x || !p.router || p.h <= 0)
         return set_error(GAJE_ERR_INVALID_ARG, "moe route: bad arguments");
     if ((size_t)p.h * 4 + 1024 > max_lds_per_block()) return set_error(GAJE_ERR_UNSUPPORTED, "moe route: hidden too large");
-    const int cpt = p.n_expert <= 8 ? 64 : 128, tpw = 256 / cpt;
-    const size_t slds = ((size_t)p.n_expert * (p.h + 8) + (size_t)tpw * p.h) * 4;
+    const size_t slds = ((size_t)p.n_expert * (p.h + 8) + (size_t)p.h) * 4;
     const bool staged = p.h % 4 == 0 && p.ldx % 4 == 0 && (((uintptr_t)p.x | (uintptr_t)p.router) & 15) == 0 &&
                         slds + 1024 <= max_lds_per_block();
     if (staged) {
-        const unsigned grid = (unsigned)((p.T + tpw - 1) / tpw);
-        if (cpt == 64) hipLaunchKernelGGL(moe_route_lds_kernel<64>, dim3(grid), dim3(256), slds, s, p);
-        else hipLaunchKernelGGL(moe_route_lds_kernel<128>, dim3(grid), dim3(256), slds, s, p);
+        if (p.n_expert <= 8) hipLaunchKernelGGL(moe_route_lds_kernel<8>, dim3((unsigned)p.T), dim3(256), slds, s, p);
+        else hipLaunchKernelGGL(moe_route_lds_kernel<16>, dim3((unsigned)p.T), dim3(256), slds, s, p);
     } else {
         hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)p.T), dim3(64 * MOE_MAX_EXPERTS), (size_t)p.h * 4, s, p);
     }
