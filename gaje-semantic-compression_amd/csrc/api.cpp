@@ -883,6 +883,11 @@ template <class F>
 int time_launches(F &&launch_all, int per_pass, int iters, hipStream_t s, float *avg_ms) {
     int rc = launch_all();  // warm-up, eager (validates the arguments)
     const int reps = (iters + per_pass - 1) / per_pass;
+    // untimed passes right before the timed ones, ~640 launches: the core clock
+    // climbs for ~20 ms after the GPU has idled (here: while the graph is
+    // captured and instantiated), and a launch-bound or VALU-bound kernel's
+    // rate follows it
+    const int warm = (640 + per_pass - 1) / per_pass;
     float ms = 0.0f;
     hipEvent_t e0 = nullptr, e1 = nullptr;
     hipGraph_t g = nullptr;
@@ -890,6 +895,7 @@ int time_launches(F &&launch_all, int per_pass, int iters, hipStream_t s, float 
     if (rc == GAJE_OK && (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess))
         rc = set_error(GAJE_ERR_HIP, "event create failed");
     if (rc == GAJE_OK && getenv("GAJE_HIP_PROFILE")) {
+        for (int r = 0; r < warm && rc == GAJE_OK; ++r) rc = launch_all();
         (void)hipEventRecord(e0, s);
         for (int r = 0; r < reps && rc == GAJE_OK; ++r) rc = launch_all();
         (void)hipEventRecord(e1, s);
@@ -904,7 +910,7 @@ int time_launches(F &&launch_all, int per_pass, int iters, hipStream_t s, float 
         if (rc == GAJE_OK && hipGraphInstantiate(&ge, g, nullptr, nullptr, 0) != hipSuccess)
             rc = set_error(GAJE_ERR_HIP, "graph instantiate failed");
         if (rc == GAJE_OK) {
-            (void)hipGraphLaunch(ge, s);  // first replay uploads the graph
+            for (int r = 0; r < warm; ++r) (void)hipGraphLaunch(ge, s);  // (the first uploads the graph)
             (void)hipEventRecord(e0, s);
             for (int r = 0; r < reps; ++r) (void)hipGraphLaunch(ge, s);
             (void)hipEventRecord(e1, s);

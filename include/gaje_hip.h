@@ -383,7 +383,8 @@ int gaje_hip_time_stage(gaje_hip_model *m, int stage, int64_t layer, int iters, 
  * copies laid out `copy_stride` bytes apart (copy i of the LUT tables at
  * lut_base + i * lut_stride), cycling through the copies so that the set can
  * exceed the caches.  The launches are captured once in a HIP graph and
- * replayed until `iters` launches ran; timed with HIP events on a private
+ * replayed until `iters` launches ran, after about 640 untimed launches (the
+ * core clock's climb under load); timed with HIP events on a private
  * stream.  With GAJE_HIP_PROFILE set in the environment the launches are
  * issued one by one instead (no graph), so that a kernel tracer records each;
  * the model's token step is likewise launched kernel by kernel then. */
