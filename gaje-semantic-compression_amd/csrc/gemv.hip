@@ -1517,6 +1517,202 @@ __global__ __launch_bounds__(WAVES * WAVE) void gemv_q4_lds_kernel(GemvParams p,
     wait_vmcnt<0>();
 }
 
+constexpr int Q8L_WAVES = 4, Q8L_STAGES = 2;  // the Q8_0 LDS kernel's shape
+// ------------------------------------- Q8_0 rows through LDS-direct copies ----
+// The Q8_0 lm_head (and other long Q8_0 STORE matrices) with the staging of
+// gemv_q4_lds_kernel: persistent workgroups of WAVES waves, each wave walking
+// super-tiles of two consecutive 8-row tiles (16 rows: one contiguous run of
+// 2 G Q8_TILE_GROUP bytes), copied into its own LDS stages with LDS-direct
+// loads, STAGES ahead.  Lane (r, l) walks chain l of row r of both tiles,
+// their steps alternated.  Values, chain order, reduction and epilogue are
+// q8_consume's and gemv_q8_stream_kernel's, so each row's result is the same
+// bits; rows at or past N (zero in the packed tiles) store into a sink, and
+// the first-maximum key of the walked rows goes to the decode state.
+// Requires rows_valid == N, no bias, anchors or genomic norm (the launcher
+// routes those to the register-ring kernel).  Stores issued after a stage's
+// copies that the wait counts leave out (x_out, a NaN flag) only make the
+// waits stricter.
+template <int G>
+__device__ __forceinline__ void q8l_rows2(const uint8_t *ta, const uint8_t *tb, int r, int l,
+                                          const float4 (&xr)[4 * G], float &y0, float &y1) {
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const vu4 na = *(const vu4 *)(ta + g * Q8_CODES + r * 128 + 16 * l);
+        const vu4 nbv = *(const vu4 *)(tb + g * Q8_CODES + r * 128 + 16 * l);
+        const vu2 sa = *(const vu2 *)(ta + G * Q8_CODES + g * Q8_SCALES + r * 8);
+        const vu2 sb = *(const vu2 *)(tb + G * Q8_CODES + g * Q8_SCALES + r * 8);
+        float da[4][4], db[4][4];
+        q8_dequant(da[0], na.x, half_lo(sa.x));
+        q8_dequant(da[1], na.y, half_hi(sa.x));
+        q8_dequant(da[2], na.z, half_lo(sa.y));
+        q8_dequant(da[3], na.w, half_hi(sa.y));
+        q8_dequant(db[0], nbv.x, half_lo(sb.x));
+        q8_dequant(db[1], nbv.y, half_hi(sb.x));
+        q8_dequant(db[2], nbv.z, half_lo(sb.y));
+        q8_dequant(db[3], nbv.w, half_hi(sb.y));
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const float4 x = xr[4 * g + b];
+            a0 = fmaf(da[b][0], x.x, a0);
+            a1 = fmaf(db[b][0], x.x, a1);
+            a0 = fmaf(da[b][1], x.y, a0);
+            a1 = fmaf(db[b][1], x.y, a1);
+            a0 = fmaf(da[b][2], x.z, a0);
+            a1 = fmaf(db[b][2], x.z, a1);
+            a0 = fmaf(da[b][3], x.w, a0);
+            a1 = fmaf(db[b][3], x.w, a1);
+        }
+    }
+    y0 = flush_small(red8_dpp(a0));
+    y1 = flush_small(red8_dpp(a1));
+}
+
+template <int MODE, int WAVES, int STAGES, int G>
+__global__ __launch_bounds__(WAVES * WAVE) void gemv_q8_lds_kernel(GemvParams p, int xstride, int64_t limit) {
+    constexpr int TB = G * Q8_TILE_GROUP;  // bytes of one 8-row tile
+    constexpr int SB = 2 * TB;             // of a super-tile
+    constexpr int PER = (SB + 1023) / 1024;
+    constexpr int NST = 2;                 // stores per super-tile (the two rows of lane base)
+    extern __shared__ __align__(16) float smem[];
+    __shared__ float inv_slot;
+    __shared__ int or_in[WAVES], or_norm[WAVES];
+    DevState *st = p.st;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l = lane & 7, r = lane >> 3, base = lane - l;
+    const int64_t K4 = p.K >> 2, N = p.N;
+    const XView xv{smem, xstride};
+    uint8_t *raw = (uint8_t *)(smem + 8 * xstride);  // x, then norm_w
+    const int64_t xb = p.K * 4;
+    const int raw_bytes = (int)((p.norm_w ? 2 * xb : xb) + 15) & ~15;
+    uint8_t *stages = raw + raw_bytes + (size_t)wave * STAGES * PER * 1024;
+    const uint32_t v16 = (uint32_t)lane * 16;
+    const uint32_t vlast = (PER - 1) * 1024 + v16 + 16 <= (uint32_t)SB ? (PER - 1) * 1024 + v16 : 0u;
+    const int64_t nsup = (N + 15) / 16;  // super-tiles
+    const int64_t gw = (int64_t)blockIdx.x * WAVES + wave, nw = (int64_t)gridDim.x * WAVES;
+    auto issue = [&](int64_t t, int stage) {
+        const uint32_t dst = lds_addr(stages + stage * PER * 1024);
+        const int64_t o0 = t * SB;
+        if (o0 + PER * 1024 <= limit) q4l_copy_full<PER>(p.w, o0, dst, v16, vlast);
+        else q4l_copy<PER>(p.w, o0, o0 + SB < limit ? o0 + SB : limit, dst, lane);
+    };
+
+    // ---- prologue (gemv_q4_lds_kernel's): wave 0 copies x and the norm
+    // weights, every wave its first super-tiles ----
+    if (wave == 0) {
+        lds_copy_bytes(p.x, xb, lds_addr(raw), lane);
+        if (p.norm_w) lds_copy_bytes(p.norm_w, xb, lds_addr(raw + xb), lane);
+    }
+    int first = 0;
+    for (int i = 0; i < STAGES; ++i)
+        if (gw + i * nw < nsup) {
+            issue(gw + i * nw, i);
+            ++first;
+        }
+    if (st && s_load_i32(&st->halted)) {
+        wait_vmcnt<0>();  // no copy may land after the workgroup's LDS is released
+        return;           // uniform
+    }
+    if (wave == 0) wait_vmcnt_stages<PER, STAGES>(first);  // the shared data has landed
+    lds_barrier();
+    const float *xraw = (const float *)raw, *wraw = (const float *)(raw + xb);
+    constexpr int NT = WAVES * WAVE;
+    int bad_in = 0;
+    for (int64_t m = tid; m < K4; m += NT) {
+        const float4 v = *(const float4 *)(xraw + 4 * m);
+        const float q[4] = {v.x, v.y, v.z, v.w};
+        store_quad<true>(xv, (int)m, q);
+        bad_in |= isnan(v.x) || isnan(v.y) || isnan(v.z) || isnan(v.w);
+    }
+    q4_zero_x_pad(xv, p.nb);
+    if (barrier_or<WAVES>(bad_in, or_in) && p.st_in >= 0 && tid == 0) nan_flag(st, p.layer, p.st_in);
+    if (p.norm_w) {
+        rms_inv_chain_major(xv, p.K, p.eps, &inv_slot);
+        lds_barrier();
+        const float inv = inv_slot;
+        int bad = 0;
+        for (int64_t m = tid; m < K4; m += NT) {
+            const float4 xq = *(const float4 *)(xraw + 4 * m), wq = *(const float4 *)(wraw + 4 * m);
+            float t[4] = {xq.x * inv, xq.y * inv, xq.z * inv, xq.w * inv};
+            const float w[4] = {wq.x, wq.y, wq.z, wq.w};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                t[c] = t[c] * w[c];  // (x * inv) * w, each product rounded
+                bad |= isnan(t[c]);
+            }
+            store_quad<true>(xv, (int)m, t);
+        }
+        if (barrier_or<WAVES>(bad, or_norm) && p.st_norm >= 0 && tid == 0) nan_flag(st, p.layer, p.st_norm);
+    }
+    if (p.x_out && blockIdx.x == 0)
+        for (int64_t k = tid; k < p.K; k += NT) p.x_out[k] = xv.at(k);
+
+    // ---- super-tiles (as gemv_q4_lds_kernel's tiles) ----
+    float4 xr4[4 * G];  // chain l's activations, read once
+    {
+        const float *xg = xv.x + l * xv.stride;
+#pragma unroll
+        for (int i = 0; i < 4 * G; ++i) xr4[i] = *(const float4 *)(xg + 4 * i);
+    }
+    float best_v = -INFINITY;
+    int64_t best_i = 0;
+    int stage = 0, it = 0;
+    int64_t left = gw < nsup ? (nsup - 1 - gw) / nw : 0;
+    for (int64_t t = gw; t < nsup; t += nw, --left, ++it) {
+        wait_vmcnt_ab<NST, PER, STAGES - 1>(it < STAGES - 1 ? it : STAGES - 1,
+                                            (int)(left < STAGES - 1 ? left : STAGES - 1));
+        const uint8_t *s0 = stages + stage * PER * 1024;
+        float y0, y1;
+        q8l_rows2<G>(s0, s0 + TB, r, l, xr4, y0, y1);
+        if (lane == base) {
+            const int64_t ra = t * 16 + r, rb = ra + 8;
+            *(ra < N ? p.y + ra : kSinkOut + lane) = y0;
+            *(rb < N ? p.y + rb : kSinkOut + lane) = y1;
+            if constexpr (MODE == MODE_ARGMAX) {  // rows in increasing order: strict '>' keeps the first
+                const bool b0 = ra < N && y0 > best_v;
+                best_v = b0 ? y0 : best_v;
+                best_i = b0 ? ra : best_i;
+                const bool b1 = rb < N && y1 > best_v;
+                best_v = b1 ? y1 : best_v;
+                best_i = b1 ? rb : best_i;
+            }
+        }
+        if (t + STAGES * nw < nsup) {
+            // the stage's LDS reads have returned: it can be refilled
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+            issue(t + STAGES * nw, stage);
+        }
+        stage = stage + 1 == STAGES ? 0 : stage + 1;
+    }
+    wait_vmcnt<0>();
+    if constexpr (MODE == MODE_ARGMAX) {
+        unsigned long long key =
+            best_v > -INFINITY
+                ? ((unsigned long long)max_key(best_v) << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)best_i)
+                : 0ull;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const unsigned long long other = __shfl_xor(key, o, WAVE);
+            key = other > key ? other : key;
+        }
+        if (lane == 0 && key) atomicMax(&st->argmax_key, key);
+    }
+}
+
+template <int MODE, int WAVES, int STAGES>
+void *q8l_kernel(int G) {
+    switch (G) {
+        case 1: return (void *)gemv_q8_lds_kernel<MODE, WAVES, STAGES, 1>;
+        case 2: return (void *)gemv_q8_lds_kernel<MODE, WAVES, STAGES, 2>;
+        case 3: return (void *)gemv_q8_lds_kernel<MODE, WAVES, STAGES, 3>;
+        case 4: return (void *)gemv_q8_lds_kernel<MODE, WAVES, STAGES, 4>;
+        case 5: return (void *)gemv_q8_lds_kernel<MODE, WAVES, STAGES, 5>;
+        case 6: return (void *)gemv_q8_lds_kernel<MODE, WAVES, STAGES, 6>;
+        case 7: return (void *)gemv_q8_lds_kernel<MODE, WAVES, STAGES, 7>;
+        default: return (void *)gemv_q8_lds_kernel<MODE, WAVES, STAGES, 8>;
+    }
+}
+
 // LUT-4bit rows stored whole (MODE_STORE, optional bias, no anchors or
 // prologue), LDS-staged: one wave per workgroup takes 16 rows (lane 4 r + c:
 // row r, chain c) and copies, all at once with LDS-direct loads, x, the 16
@@ -2585,7 +2781,28 @@ int launch_gemv(const GemvParams &p, hipStream_t s) {
             return GAJE_OK;
         }
     }
-    // Q8_0 rows of at most 8 packed groups (the lm_head): the streamed kernel
+    // Q8_0 rows of at most 8 packed groups: long matrices (the lm_head) through
+    // the LDS-staged kernel, the others on the register-ring stream
+    if (p.fmt == FMT_Q8_0 && (p.mode == MODE_ARGMAX || p.mode == MODE_STORE) && !p.gnorm && !p.a_ptr && p.nb > 0 &&
+        (p.nb + 3) / 4 <= 8 && p.bias_len == 0 && p.rows_valid == p.N &&
+        (p.N + 15) / 16 >= 4 * (int64_t)device_cu_count()) {
+        const int G = (p.nb + 3) / 4;
+        const int xs = q4_xstride(p.K);
+        const int raw = (int)(((p.norm_w ? 2 : 1) * p.K * 4 + 15) & ~15);
+        const size_t per = (size_t)(2 * G * Q8_TILE_GROUP + 1023) / 1024 * 1024;
+        constexpr int W = Q8L_WAVES, S = Q8L_STAGES;
+        const size_t lds = (size_t)8 * xs * 4 + raw + (size_t)W * S * per;
+        if (lds + 1024 <= max_lds_per_block()) {
+            const int64_t nsup = (p.N + 15) / 16;
+            const int64_t grid = std::min<int64_t>((nsup + W - 1) / W, device_cu_count());
+            void (*fn)(GemvParams, int, int64_t) =
+                (void (*)(GemvParams, int, int64_t))(p.mode == MODE_ARGMAX ? q8l_kernel<MODE_ARGMAX, W, S>(G)
+                                                                           : q8l_kernel<MODE_STORE, W, S>(G));
+            hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(W * WAVE), lds, s, p, xs, q8_0_packed_bytes(p.N, p.K));
+            GAJE_HIP_CHECK(hipGetLastError());
+            return GAJE_OK;
+        }
+    }
     if (p.fmt == FMT_Q8_0 && (p.mode == MODE_ARGMAX || p.mode == MODE_STORE) && !p.gnorm && !p.a_ptr && p.nb > 0 &&
         (p.nb + 3) / 4 <= Q8S_D) {
         void (*sf)(GemvParams, int);

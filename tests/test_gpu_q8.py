@@ -81,6 +81,20 @@ def test_q8_0_gemv(hip, O, n, k):
     assert same_bits(got, L.forward_core(x))
 
 
+@pytest.mark.parametrize("n,k", [(151936, 896), (65547, 896), (70001, 1024), (20000, 512), (16400, 128)])
+def test_q8_0_gemv_long_no_bias(hip, O, n, k):
+    """Long Q8_0 matrices without a bias take the LDS-staged kernel (16-row
+    super-tiles): a partial last tile, an odd tile count (the last super-tile
+    half past the rows), K = 1024 (8 groups) and one-group rows; bit for bit."""
+    blocks = _q8_rows(O, n, k, n + 2 * k)
+    x = hip.synth.normal(14, f"x8l.{k}", k)
+    y = hip.ops.DeviceBuffer(n * 4)
+    hip.ops.q8_0_gemv(hip.ops.q8_0_upload(blocks, n, k), hip.ops.DeviceBuffer.from_array(x), y, n, k)
+    got = y.read(np.float32)
+    L = O.GenomicLinear(blocks, b"", None, n, k, None, 8)
+    assert same_bits(got, L.forward_core(x))
+
+
 def test_q8_0_dequant_every_code_and_edge_scale(hip, O):
     codes = np.arange(256, dtype=np.uint8)
     scales = np.array([0x0000, 0x8000, 0x0001, 0x03FF, 0x0400, 0x3C00, 0x7BFF, 0xBC00, 0xFBFF, 0x2E66, 0x7C00, 0xFC00],
@@ -133,7 +147,8 @@ def test_q8_0_embeddings_model_stream(hip, O, tmp_models, tied):
 
 
 def test_q8_0_benchmark_shape(hip, O, tmp_models):
-    """Qwen2-0.5B shape with Q8_0 token_embd / lm_head (151936 x 896), three tokens."""
+    """Qwen2-0.5B shape with Q8_0 token_embd / lm_head (151936 x 896): three tokens' logits, then
+    three greedy tokens through the lm_head's device argmax."""
     p = _write(hip, tmp_models / "qwen2-0.5b_q8.flat", preset="qwen2-0.5b", seed=0, quant_embed=1)
     g = hip.load_genomic_auto(p)
     r = O.load_genomic(p)
@@ -141,4 +156,10 @@ def test_q8_0_benchmark_shape(hip, O, tmp_models):
     r.set_k_wta_ratio(0.0)
     for i, t in enumerate([11, 2024, 151000]):
         assert same_bits(g.forward(t, i == 0), r.forward_core(t, i == 0)), f"token {i}"
+    # the lm_head's device argmax (greedy decode), continuing both caches
+    out = g.decode_greedy(151000, 3)
+    tok = 151000
+    for i in range(3):
+        tok = O.argmax_first(r.forward_core(tok))
+        assert int(out[i]) == tok, f"greedy token {i}"
     g.close()
