@@ -226,6 +226,15 @@ extern "C" int gaje_hip_q4_0_gemv(const void *packed, const float *x, const floa
     return launch_gemv(plain_gemv(FMT_Q4_0, packed, x, bias, bias_len, y, n, k), as_stream(stream));
 }
 
+extern "C" int gaje_hip_q4_0_gemv_tol(const void *packed, const float *x, const float *bias, int64_t bias_len,
+                                      float *y, int64_t n, int64_t k, void *stream) {
+    clear_error();
+    GAJE_TRY(check_dims(n, k));
+    GemvParams p = plain_gemv(FMT_Q4_0, packed, x, bias, bias_len, y, n, k);
+    p.tol = 1;
+    return launch_gemv(p, as_stream(stream));
+}
+
 extern "C" int gaje_hip_q4_0_gemv_blocks(const void *blocks, const float *x, const float *bias, int64_t bias_len,
                                          float *y, int64_t n, int64_t k, void *stream) {
     clear_error();
@@ -939,6 +948,9 @@ extern "C" int gaje_hip_bench_gemv(int format, const void *w_base, size_t copy_s
     GAJE_TRY(check_dims(n, k));
     if (!avg_ms || copies <= 0 || iters <= 0 || !w_base || (format == FMT_LUT4 && !lut_base))
         return set_error(GAJE_ERR_INVALID_ARG, "bad benchmark arguments");
+    // format 3: the Q4_0 matvec in tolerance mode (gaje_hip_q4_0_gemv_tol)
+    const bool tol = format == 3;
+    if (tol) format = FMT_Q4_0;
     if (format != FMT_F32 && format != FMT_Q4_0 && format != FMT_LUT4)
         return set_error(GAJE_ERR_INVALID_ARG, "unknown format %d", format);
     hipStream_t s;
@@ -956,6 +968,7 @@ extern "C" int gaje_hip_bench_gemv(int format, const void *w_base, size_t copy_s
                 p.lut_rows_own = n;
             }
             if (format == FMT_F32) p.nontemporal = 1;
+            p.tol = tol ? 1 : 0;
             GAJE_TRY(launch_gemv(p, s));
         }
         return GAJE_OK;

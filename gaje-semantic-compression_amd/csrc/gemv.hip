@@ -1349,6 +1349,51 @@ __device__ __forceinline__ void q4l_rows2(const uint8_t *rp0, const uint8_t *rp1
     y1 = flush_small(red8_dpp(a1));
 }
 
+// Tolerance mode (gaje_hip_q4_0_gemv_tol): the same rows regrouped by block,
+// sum_k (q_k s + mn) x_k = s (sum_k q_k x_k) + mn (sum_k x_k), as the
+// block-scaled MFMA product regroups them.  Chain l's four codes of a block
+// enter as the f16 subnormals q 2^-24 or q 2^-20 (q4_dequant_dw's masks) and
+// its inputs are held pre-scaled by 2^24 or 2^20 (exact powers of two; the
+// launcher's workgroups fall back to the exact walk when some |x| >= 2^100),
+// so each block costs four v_fma_mix_f32 for the code products, one for
+// s * P with the f16 scale read in place and one for mn * X with the f16 min
+// and the chain's block sum X of the unscaled inputs: 1.5 VALU instructions
+// per weight plus the masks, against 2.875 for the exact walk.  The result
+// differs from the reference's chained fmas by rounding only (the tests hold
+// it to 1e-4 of the row's sum of |w x|); the |t| < 1e-6 flush is kept.
+template <int G>
+__device__ __forceinline__ void q4l_rows2_tol(const uint8_t *rp0, const uint8_t *rp1, const float4 (&xr)[4 * G],
+                                              const float (&xsum)[4 * G], int l, float &y0, float &y1) {
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const vu2 m0 = *(const vu2 *)(rp0 + g * 80 + 8 * l), m1 = *(const vu2 *)(rp1 + g * 80 + 8 * l);
+        const vu4 t0 = *(const vu4 *)(rp0 + g * 80 + 64), t1 = *(const vu4 *)(rp1 + g * 80 + 64);
+        const uint32_t n0[2] = {m0.x, m0.y}, n1[2] = {m1.x, m1.y};
+        const uint32_t s0[4] = {t0.x, t0.y, t0.z, t0.w}, s1[4] = {t1.x, t1.y, t1.z, t1.w};
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const uint32_t M = (b & 1) ? 0x00F000F0u : 0x000F000Fu;
+            const uint32_t e02a = opaque_and(n0[b >> 1], M), e13a = opaque_and(n0[b >> 1] >> 8, M);
+            const uint32_t e02b = opaque_and(n1[b >> 1], M), e13b = opaque_and(n1[b >> 1] >> 8, M);
+            const float4 x = xr[4 * g + b];
+            float pa = fmaf(f16_lo(e02a), x.x, -0.0f), pb = fmaf(f16_lo(e02b), x.x, -0.0f);
+            pa = fmaf(f16_lo(e13a), x.y, pa);
+            pb = fmaf(f16_lo(e13b), x.y, pb);
+            pa = fmaf(f16_hi(e02a), x.z, pa);
+            pb = fmaf(f16_hi(e02b), x.z, pb);
+            pa = fmaf(f16_hi(e13a), x.w, pa);
+            pb = fmaf(f16_hi(e13b), x.w, pb);
+            a0 = fmaf(half_lo(s0[b]), pa, a0);
+            a1 = fmaf(half_lo(s1[b]), pb, a1);
+            a0 = fmaf(half_hi(s0[b]), xsum[4 * g + b], a0);
+            a1 = fmaf(half_hi(s1[b]), xsum[4 * g + b], a1);
+        }
+    }
+    y0 = flush_small(red8_dpp(a0));
+    y1 = flush_small(red8_dpp(a1));
+}
+
 // One chain: q4l_rows2 for the row at rp alone.
 template <int G>
 __device__ __forceinline__ float q4l_row1(const uint8_t *rp, const float4 (&xr)[4 * G], int l, int base) {
@@ -1368,9 +1413,10 @@ __device__ __forceinline__ float q4l_row1(const uint8_t *rp, const float4 (&xr)[
 // up rows, lane (r, l) walks gate row r and its up row).  No bias, anchors or
 // genomic norm (the launcher routes those elsewhere).  G = packed groups per
 // row.
-template <int MODE, int WAVES, int STAGES, int G, int ROWS>
+template <int MODE, int WAVES, int STAGES, int G, int ROWS, bool TOL = false>
 __global__ __launch_bounds__(WAVES * WAVE) void gemv_q4_lds_kernel(GemvParams p, int xstride, int64_t limit, int raw_bytes) {
     static_assert(ROWS == 2 || (ROWS == 1 && MODE == MODE_STORE), "one or two rows per lane");
+    static_assert(!TOL || (MODE == MODE_STORE && ROWS == 2), "the regrouped walk: STORE streams");
     constexpr int ROW_BYTES = G * 80;
     constexpr int TROWS = MODE == MODE_SWIGLU ? 4 * ROWS : 8 * ROWS;  // output rows per tile
     constexpr int HALF = (TROWS * ROW_BYTES + 1023) / 1024;           // copies per TROWS rows
@@ -1478,6 +1524,29 @@ __global__ __launch_bounds__(WAVES * WAVE) void gemv_q4_lds_kernel(GemvParams p,
 #pragma unroll
         for (int i = 0; i < 4 * G; ++i) xr4[i] = *(const float4 *)(xg + 4 * i);
     }
+    // TOL: the chain's block sums of x, then x scaled by 2^24 (low-nibble
+    // blocks) or 2^20 (high-nibble blocks) unless some |x| >= 2^100 in the
+    // wave's chains (which cover all of x): then this wave walks exactly
+    float xsum[TOL ? 4 * G : 1];
+    bool exact = !TOL;
+    if constexpr (TOL) {
+        int big = 0;
+#pragma unroll
+        for (int i = 0; i < 4 * G; ++i) {
+            const float4 v = xr4[i];
+            xsum[i] = (v.x + v.y) + (v.z + v.w);
+            big |= !(fabsf(v.x) < 0x1p100f) | !(fabsf(v.y) < 0x1p100f) | !(fabsf(v.z) < 0x1p100f) |
+                   !(fabsf(v.w) < 0x1p100f);
+        }
+        exact = __any(big);
+        if (!exact) {
+#pragma unroll
+            for (int i = 0; i < 4 * G; ++i) {
+                const float sc = (i & 1) ? 0x1p20f : 0x1p24f;  // block i % 4: low (even) or high (odd) nibbles
+                xr4[i] = make_float4(xr4[i].x * sc, xr4[i].y * sc, xr4[i].z * sc, xr4[i].w * sc);
+            }
+        }
+    }
     int stage = 0, it = 0;
     int64_t left = gw < ntiles ? (ntiles - 1 - gw) / nw : 0;  // this wave's tiles after t
     for (int64_t t = gw; t < ntiles; t += nw, --left, ++it) {
@@ -1488,7 +1557,11 @@ __global__ __launch_bounds__(WAVES * WAVE) void gemv_q4_lds_kernel(GemvParams p,
         if constexpr (MODE == MODE_SWIGLU) {
             q4l_rows2<G>(st0 + r * ROW_BYTES, st0 + HALF * 1024 + r * ROW_BYTES, xr4, l, base, y0, y1);
         } else if constexpr (ROWS == 2) {
-            q4l_rows2<G>(st0 + r * ROW_BYTES, st0 + (r + 8) * ROW_BYTES, xr4, l, base, y0, y1);
+            if (!exact) {
+                if constexpr (TOL) q4l_rows2_tol<G>(st0 + r * ROW_BYTES, st0 + (r + 8) * ROW_BYTES, xr4, xsum, l, y0, y1);
+            } else {
+                q4l_rows2<G>(st0 + r * ROW_BYTES, st0 + (r + 8) * ROW_BYTES, xr4, l, base, y0, y1);
+            }
         } else {
             y0 = q4l_row1<G>(st0 + r * ROW_BYTES, xr4, l, base);
         }
@@ -1812,17 +1885,17 @@ __global__ __launch_bounds__(WAVE) void gemv_lut4_lds_kernel(GemvParams p) {
     }
 }
 
-template <int MODE, int WAVES, int STAGES, int ROWS>
+template <int MODE, int WAVES, int STAGES, int ROWS, bool TOL = false>
 void *q4l_kernel(int G) {
     switch (G) {
-        case 1: return (void *)gemv_q4_lds_kernel<MODE, WAVES, STAGES, 1, ROWS>;
-        case 2: return (void *)gemv_q4_lds_kernel<MODE, WAVES, STAGES, 2, ROWS>;
-        case 3: return (void *)gemv_q4_lds_kernel<MODE, WAVES, STAGES, 3, ROWS>;
-        case 4: return (void *)gemv_q4_lds_kernel<MODE, WAVES, STAGES, 4, ROWS>;
-        case 5: return (void *)gemv_q4_lds_kernel<MODE, WAVES, STAGES, 5, ROWS>;
-        case 6: return (void *)gemv_q4_lds_kernel<MODE, WAVES, STAGES, 6, ROWS>;
-        case 7: return (void *)gemv_q4_lds_kernel<MODE, WAVES, STAGES, 7, ROWS>;
-        default: return (void *)gemv_q4_lds_kernel<MODE, WAVES, STAGES, 8, ROWS>;
+        case 1: return (void *)gemv_q4_lds_kernel<MODE, WAVES, STAGES, 1, ROWS, TOL>;
+        case 2: return (void *)gemv_q4_lds_kernel<MODE, WAVES, STAGES, 2, ROWS, TOL>;
+        case 3: return (void *)gemv_q4_lds_kernel<MODE, WAVES, STAGES, 3, ROWS, TOL>;
+        case 4: return (void *)gemv_q4_lds_kernel<MODE, WAVES, STAGES, 4, ROWS, TOL>;
+        case 5: return (void *)gemv_q4_lds_kernel<MODE, WAVES, STAGES, 5, ROWS, TOL>;
+        case 6: return (void *)gemv_q4_lds_kernel<MODE, WAVES, STAGES, 6, ROWS, TOL>;
+        case 7: return (void *)gemv_q4_lds_kernel<MODE, WAVES, STAGES, 7, ROWS, TOL>;
+        default: return (void *)gemv_q4_lds_kernel<MODE, WAVES, STAGES, 8, ROWS, TOL>;
     }
 }
 
@@ -2770,6 +2843,7 @@ int launch_gemv(const GemvParams &p, hipStream_t s) {
             const int64_t ntiles = (rows + 2 * trows1 - 1) / (2 * trows1);
             grid = std::min<int64_t>((ntiles + waves - 1) / waves, device_cu_count());
             if (swiglu) fn = two ? q4l_kernel<MODE_SWIGLU, 8, 2, 2>(G) : q4l_kernel<MODE_SWIGLU, 4, 3, 2>(G);
+            else if (p.tol) fn = two ? q4l_kernel<MODE_STORE, 8, 2, 2, true>(G) : q4l_kernel<MODE_STORE, 4, 3, 2, true>(G);
             else fn = two ? q4l_kernel<MODE_STORE, 8, 2, 2>(G) : q4l_kernel<MODE_STORE, 4, 3, 2>(G);
         }
         const size_t lds = fixed - 1024 + (size_t)waves * nst * stage;

@@ -73,6 +73,7 @@ struct GemvParams {
     int32_t fmt;
     int32_t f32_tiled;       // FMT_F32 weights in the tiled layout (K % 8 == 0)
     int32_t nontemporal;     // stream the weights past the caches (read-once tensors)
+    int32_t tol;             // Q4_0 STORE streams: the regrouped walk, held to 1e-4 of each row's mass
     const float *lut;        // FMT_LUT4 tables / FMT_G2 centroids (T = 16 or 4 floats per block)
     int64_t lut_rows_own;    // rows r < lut_rows_own use the tables from r*nb*T, others from 0
     int32_t lut_block_stride;// T = one table per block, 0 = one shared table

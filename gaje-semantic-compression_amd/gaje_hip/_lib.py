@@ -120,6 +120,7 @@ SIGNATURES = [
     ("gaje_hip_q4_0_pack", ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, c_vp]),
     ("gaje_hip_q4_0_gemv", ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_vp]),
     ("gaje_hip_q4_0_gemv_blocks", ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_vp]),
+    ("gaje_hip_q4_0_gemv_tol", ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_vp]),
     ("gaje_hip_q4_0_gemm", ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_vp]),
     ("gaje_hip_q4_0_gemm_mfma_workspace", c_i64, [c_i64, c_i64, c_i64]),
     ("gaje_hip_q4_0_gemm_mfma", ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_vp,

@@ -105,6 +105,13 @@ def q4_0_gemv(packed: DeviceBuffer, x: DeviceBuffer, y: DeviceBuffer, n: int, k:
     check(lib().gaje_hip_q4_0_gemv(packed.ptr, x.ptr, _p(bias), bias_len, y.ptr, n, k, stream))
 
 
+def q4_0_gemv_tol(packed: DeviceBuffer, x: DeviceBuffer, y: DeviceBuffer, n: int, k: int,
+                  bias: DeviceBuffer | None = None, bias_len: int = 0, stream=None) -> None:
+    """q4_0_gemv in tolerance mode: within 1e-4 of each row's sum of |w x|
+    (regrouped by block on the long streams), not bit for bit."""
+    check(lib().gaje_hip_q4_0_gemv_tol(packed.ptr, x.ptr, _p(bias), bias_len, y.ptr, n, k, stream))
+
+
 def q4_0_gemv_blocks(blocks: DeviceBuffer, x: DeviceBuffer, y: DeviceBuffer, n: int, k: int,
                      bias: DeviceBuffer | None = None, bias_len: int = 0, stream=None) -> None:
     """The Q4_0 matvec on the file's own Q4_0Block rows (no packing)."""

@@ -94,6 +94,18 @@ int gaje_hip_q4_0_pack(const void *blocks, void *packed, int64_t n, int64_t k, v
 int gaje_hip_q4_0_gemv(const void *packed, const float *x, const float *bias, int64_t bias_len,
                        float *y, int64_t n, int64_t k, void *stream);
 
+/* The same matvec in tolerance mode, for callers that accept the 1e-4 bound
+ * of the GEMV rather than the reference's bits: each row regrouped by block
+ * as scale * sum(q x) + min * sum(x) (genomic_dot_product_q4_0's value,
+ * compute/kernels/genomic.rs:210-336, in another summation order, then the
+ * same |t| < 1e-6 flush and bias add), held to 1e-4 of the row's sum of
+ * |w x|.  No reference function has this form: it replaces
+ * genomic_dot_product_q4_0 where that bound is the contract.  Long matrices
+ * (the streaming kernel's shapes, no bias) run the regrouped walk; other
+ * shapes and inputs with some |x| >= 2^100 run the exact one. */
+int gaje_hip_q4_0_gemv_tol(const void *packed, const float *x, const float *bias, int64_t bias_len, float *y,
+                           int64_t n, int64_t k, void *stream);
+
 /* The same matvec straight from the file's Q4_0Block rows (20 bytes per
  * block, n * k/32 blocks, 4-byte aligned), with no packing: the operator as
  * genomic_dot_product_q4_0(&[Q4_0Block], &[f32]) takes it
@@ -379,7 +391,8 @@ int gaje_hip_time_stage(gaje_hip_model *m, int stage, int64_t layer, int iters, 
                         int64_t *bytes);
 
 /* Average device time per launch of the operator matvec for `format`
- * (1 = Q4_0, 2 = LUT-4bit with per-row tables, 0 = f32) over `copies` weight
+ * (1 = Q4_0, 3 = Q4_0 in tolerance mode, 2 = LUT-4bit with per-row tables,
+ * 0 = f32) over `copies` weight
  * copies laid out `copy_stride` bytes apart (copy i of the LUT tables at
  * lut_base + i * lut_stride), cycling through the copies so that the set can
  * exceed the caches.  The launches are captured once in a HIP graph and

@@ -144,6 +144,51 @@ def test_q4_0_gemv_no_bias(hip, O, n, k):
     assert same_bits(got, ref)
 
 
+def _q4_mass(O, blocks, x, n, k):
+    """float64 W x and sum |W x| per row, from the exactly dequantised weights."""
+    W = O.q4_0_dequant(blocks).astype(np.float64).reshape(n, k)
+    x64 = x.astype(np.float64)
+    return W @ x64, np.abs(W) @ np.abs(x64)
+
+
+@pytest.mark.parametrize("n,k,seed", [(622592, 896, 30), (65536, 896, 31), (70007, 1024, 32), (40000, 512, 33),
+                                      (20011, 128, 34)])
+def test_q4_0_gemv_tol_streams(hip, O, n, k, seed):
+    """Tolerance mode on the streaming shapes (the regrouped walk): every row
+    within 1e-4 of its sum of |w x| of the reference's value (the oracle, bit
+    for bit the reference's fp32 order), and as close to the float64 product;
+    the 622,592 x 896 matrix is the bench's stream; partial last tiles."""
+    blocks = hip.synth.q4_0_tensor(seed, f"gemvtol.{n}.{k}", n, k)
+    x = hip.synth.normal(seed + 100, f"xtol.{k}", k)
+    y = _out(hip, n * 4)
+    hip.ops.q4_0_gemv_tol(hip.ops.q4_0_upload(blocks, n, k), _dev(hip, x), y, n, k)
+    got = y.read(np.float32).astype(np.float64)
+    ref = _oracle_q4_rows(O, blocks, x, n, k).astype(np.float64)
+    exact, mass = _q4_mass(O, blocks, x, n, k)
+    err_ref = np.max(np.abs(got - ref) / mass)
+    err_exact = np.max(np.abs(got - exact) / mass)
+    print(f"q4_0 gemv tol n={n} k={k}: max |got - ref| / mass {err_ref:.2e}, vs float64 {err_exact:.2e}, "
+          f"rows differing from the exact bits {np.mean(got != ref):.3f}")
+    assert err_ref <= 1e-4 and err_exact <= 1e-4
+    # the regrouped walk ran: the bits differ from the exact walk's on most rows
+    assert np.mean(got != ref) > 0.5
+
+
+def test_q4_0_gemv_tol_exact_where_it_falls_back(hip, O):
+    """Shapes off the streaming path, a bias, and inputs with some |x| >= 2^100
+    run the exact walk: bit for bit with the oracle."""
+    for n, k, big, with_bias in [(4864, 896, False, False), (70000, 896, True, False), (65536, 896, False, True)]:
+        blocks = hip.synth.q4_0_tensor(35, f"gemvtolx.{n}.{k}", n, k)
+        x = hip.synth.normal(36, f"xtolx.{k}", k)
+        if big:
+            x[123] = np.float32(2.0 ** 101)
+        bias = hip.synth.normal(37, f"btolx.{n}", n, 0.0, 0.02) if with_bias else None
+        y = _out(hip, n * 4)
+        hip.ops.q4_0_gemv_tol(hip.ops.q4_0_upload(blocks, n, k), _dev(hip, x), y, n, k,
+                              bias=_dev(hip, bias) if with_bias else None, bias_len=n if with_bias else 0)
+        assert same_bits(y.read(np.float32), _oracle_q4_rows(O, blocks, x, n, k, bias)), (n, k, big, with_bias)
+
+
 @pytest.mark.parametrize("n,k", [(4864, 896), (963, 576), (5, 32), (129, 4864), (1, 128), (33, 1056), (700, 96)])
 def test_q4_0_gemv_blocks(hip, O, n, k):
     """genomic_dot_product_q4_0 on the file's own Q4_0Block rows (no packing):
