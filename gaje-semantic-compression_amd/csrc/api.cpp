@@ -740,6 +740,7 @@ extern "C" int gaje_hip_moe_ffn_prepared(const float *x, int64_t T, int64_t h, c
         p.g_wf_stride = pw.wf_stride[i];
         p.g_wsc_stride = pw.wsc_stride[i];
         p.g_mins_stride = pw.mins_stride[i];
+        p.defer_reduce = i == 1 && pl.splits > 1;  // down: the combine sums its partials
         return launch_gemm_q4_bs(p, pl, s);
     };
     GAJE_TRY(gemm(0, w.pgu, 2 * ffn, h, w.GU));
@@ -760,7 +761,10 @@ extern "C" int gaje_hip_moe_ffn_prepared(const float *x, int64_t T, int64_t h, c
     sp.st_a = sp.st_b = -1;
     GAJE_TRY(launch_split_rows(sp, s));
     GAJE_TRY(gemm(1, w.pdn, h, ffn, w.Y));
-    GAJE_TRY(launch_moe_combine(mp, w.Y, s));
+    if (w.pdn.splits > 1)
+        GAJE_TRY(launch_moe_combine_split(mp, w.part, w.pdn.splits, R, s));
+    else
+        GAJE_TRY(launch_moe_combine(mp, w.Y, s));
     if (top_idx) GAJE_HIP_CHECK(hipMemcpyAsync(top_idx, w.top_idx, (size_t)R * 4, hipMemcpyDeviceToDevice, s));
     if (top_w) GAJE_HIP_CHECK(hipMemcpyAsync(top_w, w.top_w, (size_t)R * 4, hipMemcpyDeviceToDevice, s));
     return GAJE_OK;

@@ -494,6 +494,9 @@ struct MoeParams {
 };
 int launch_moe_route(const MoeParams &p, hipStream_t s);
 int launch_moe_combine(const MoeParams &p, const float *Y, hipStream_t s);
+// The combine over the S = nsplit split-K partials [S][R][h] of the down
+// product (its reduce deferred): sums them as gemm_reduce_kernel would.
+int launch_moe_combine_split(const MoeParams &p, const float *part, int nsplit, int64_t R, hipStream_t s);
 
 int launch_finalize(DevState *st, uint32_t *out_tokens, hipStream_t s);
 int launch_kwta(float *x, int64_t n, int64_t k, DevState *st, hipStream_t s);

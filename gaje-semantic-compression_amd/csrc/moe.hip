@@ -281,6 +281,28 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeParams p, const flo
     p.y[t * p.ldy + j] = ya + yb;
 }
 
+// The combine with the down product's split-K reduce folded in: expert row r's
+// output is formed from the S partials part[z][r][.] (R rows each) as
+// gemm_reduce_kernel forms it (summed in split order, then flush_small; the
+// expert products carry no bias or residual), then weighted as above.
+__global__ __launch_bounds__(256) void moe_combine_split_kernel(MoeParams p, const float *part, int S, int64_t R) {
+    const int64_t t = blockIdx.y;
+    const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (j >= p.h) return;
+    const int ra = p.slot[2 * t], rb = p.slot[2 * t + 1];
+    const float wa = p.top_w[2 * t], wb = p.top_w[2 * t + 1];
+    const int64_t plane = R * p.h;
+    const float *pa = part + (int64_t)ra * p.h + j, *pb = part + (int64_t)rb * p.h + j;
+    float va = pa[0], vb = pb[0];
+    for (int z = 1; z < S; ++z) {
+        va = va + pa[z * plane];
+        vb = vb + pb[z * plane];
+    }
+    const float ya = wa * flush_small(va);
+    const float yb = wb * flush_small(vb);
+    p.y[t * p.ldy + j] = ya + yb;
+}
+
 }  // namespace
 
 int launch_moe_route(const MoeParams &p, hipStream_t s) {
@@ -304,6 +326,14 @@ int launch_moe_route(const MoeParams &p, hipStream_t s) {
 
 int launch_moe_combine(const MoeParams &p, const float *Y, hipStream_t s) {
     hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((p.h + 255) / 256), (unsigned)p.T), dim3(256), 0, s, p, Y);
+    GAJE_HIP_CHECK(hipGetLastError());
+    return GAJE_OK;
+}
+
+int launch_moe_combine_split(const MoeParams &p, const float *part, int nsplit, int64_t R, hipStream_t s) {
+    if (!part || nsplit < 1 || R < 2 * p.T) return set_error(GAJE_ERR_INVALID_ARG, "moe combine: bad partials");
+    hipLaunchKernelGGL(moe_combine_split_kernel, dim3((unsigned)((p.h + 255) / 256), (unsigned)p.T), dim3(256), 0, s, p,
+                       part, nsplit, R);
     GAJE_HIP_CHECK(hipGetLastError());
     return GAJE_OK;
 }
