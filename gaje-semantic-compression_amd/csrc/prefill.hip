@@ -140,6 +140,21 @@ __global__ __launch_bounds__(1024) void prefill_rope_kernel(PrefillRopeParams p)
     const int nt = (int)min((int64_t)32, p.P - t0);
     const int64_t col0 = (int64_t)head * hd;
     const int64_t q_rows = (int64_t)p.n_head * hd;
+    const bool is_q = head < p.n_head, is_v = head >= p.n_head + p.n_kv;
+    // this thread's rotation angles (pairs tid, tid + 1024 of the tile: 32 x half
+    // <= 2048), read with the tile's loads rather than after them
+    float rc[2] = {0.0f, 0.0f}, rsn[2] = {0.0f, 0.0f};
+    if (!is_v) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int kk = tid + 1024 * u, r = kk & 31, i = kk >> 5;
+            if (kk < 32 * half && r < nt) {
+                const int64_t pos = p.pos0 + t0 + r;
+                rc[u] = p.rope_cos[pos * half + i];
+                rsn[u] = p.rope_sin[pos * half + i];
+            }
+        }
+    }
     // ---- the tile: 32 x hd values, one float4 per thread (hd <= 128), all nine
     // partial loads of a thread issued before any sum ----
     const int k = tid;
@@ -185,17 +200,18 @@ __global__ __launch_bounds__(1024) void prefill_rope_kernel(PrefillRopeParams p)
         tile[r][4 * c4 + 3] = v.w;
     }
     __syncthreads();
-    const bool is_q = head < p.n_head, is_v = head >= p.n_head + p.n_kv;
     // ---- rotation of q and k heads, in place: pair (r, i), tokens fastest ----
     if (!is_v) {
-        for (int k = tid; k < 32 * half; k += 1024) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int k = tid + 1024 * u;
+            if (k >= 32 * half) break;
             const int r = k & 31, i = k >> 5;
             if (r >= nt) continue;
-            const int64_t pos = p.pos0 + t0 + r;
             const int d0 = p.rope_split ? i : 2 * i;
             const int d1 = p.rope_split ? i + half : 2 * i + 1;
             const float y0 = tile[r][d0], y1 = tile[r][d1];
-            const float cs = p.rope_cos[pos * half + i], sn = p.rope_sin[pos * half + i];
+            const float cs = rc[u], sn = rsn[u];
             const float a0 = y0 * cs, a1 = y1 * sn, a2 = y0 * sn, a3 = y1 * cs;
             tile[r][d0] = a0 - a1;
             tile[r][d1] = a2 + a3;
